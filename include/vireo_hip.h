@@ -1,0 +1,154 @@
+/* vireo-hip: MI355X (gfx950) kernels for vireo's quantized MoE-FFN path.
+ *
+ * A drop-in for the compute interface that the reference's GGUF runner uses:
+ *   gguf_matmul      (src/gguf_compute.h:10)  -> qmatvec / qmatvec_async
+ *   gguf_dequant_row (src/gguf_compute.h:9)   -> qdequant_rows
+ *   moe_ffn          (src/gguf_run.c:185-214, static in the reference)
+ *                                              -> moe_ffn_forward
+ *   expert_store_*   (src/expert_store.h)     -> vireo_expert_store.h (HBM pool)
+ *   rmsnorm / argmax (src/gguf_run.c:161-165, :254) -> vireo_rmsnorm / vireo_argmax
+ *
+ * Conventions
+ *   - Every pointer to tensor data, activations or outputs is a device pointer;
+ *     structs (gguf_tensor, vireo_moe_model, ...) live in host memory.
+ *   - Every entry point returns 0 or a negative errno value (-EINVAL for bad
+ *     arguments or an unsupported ggml type, -ENOMEM, -EIO for a HIP runtime
+ *     failure). The reference returns void and silently skips unknown types;
+ *     for valid inputs the outputs have the reference's meaning.
+ *   - `stream` is a hipStream_t passed as void*. With stream == NULL the call
+ *     runs on the default stream and returns after the work has finished (the
+ *     reference is synchronous); with a stream the call only enqueues.
+ *   - Tensor data must be 4-byte aligned at its start (hipMalloc gives 256);
+ *     every row in these formats is a whole number of 2-byte units.
+ *   - Calls on one device are not thread-safe with respect to each other: the
+ *     library keeps one workspace per device, like the reference's single
+ *     Model buffers (src/gguf_run.c:346-350).
+ */
+#ifndef VIREO_HIP_H
+#define VIREO_HIP_H
+
+#include <stdint.h>
+#include "vireo_gguf.h"
+#include "vireo_expert_store.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library ---------------------------------------------------------------- */
+
+/* Select the device the library works on (default: the current HIP device). */
+int vireo_hip_init(int device);
+/* Text for an error code returned by this library. */
+const char *vireo_hip_strerror(int err);
+/* Block geometry of a ggml type: src/gguf.c:27-38 (F32, F16, Q8_0, Q5_0, Q4_K,
+ * Q6_K are supported by the kernels; Q4_0 is sized but, as in the reference,
+ * not computable). Returns 0 or -EINVAL. */
+int vireo_type_block(uint32_t ggml_type, int *block_elems, int *block_bytes);
+
+/* ---- quantized compute (src/gguf_compute.h) ---------------------------------- */
+
+/* gguf_matmul (src/gguf_compute.c:159-214): y[o] = sum_i W[o][i] * x[i] for
+ * o < d, with W = w->data holding d rows of n elements of type w->ggml_type.
+ * y, x, w->data are device pointers; y must not alias x. Synchronous. */
+int qmatvec(float *y, const float *x, const gguf_tensor *w, int n, int d);
+/* The same, enqueued on `stream`. */
+int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int n, int d, void *stream);
+
+/* gguf_dequant_row (src/gguf_compute.c:105-124) applied to `rows` consecutive
+ * rows of n elements: dst[r*n + i] = dequant(src row r)[i]. Bit-identical to
+ * the reference (every dequantized value has at most one rounding). */
+int qdequant_rows(uint32_t ggml_type, const void *src, float *dst, int n, int rows, void *stream);
+
+/* ---- model glue used by the MoE stack --------------------------------------- */
+
+/* rmsnorm (src/gguf_run.c:161-165) on `rows` rows of n floats:
+ * o = x * (1/sqrt(mean(x^2) + eps)) * w. w: device [n] F32 weight. o may
+ * equal x. */
+int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream);
+/* argmax (src/gguf_run.c:254): first index of the maximum of v[0..n). */
+int vireo_argmax(const float *v, int n, int32_t *out, void *stream);
+
+/* ---- MoE FFN (src/gguf_run.c:185-214) ---------------------------------------- */
+
+/* The MoE layer tensors moe_ffn reads from Layer (src/gguf_run.c:144). */
+typedef struct {
+    const gguf_tensor *router;     /* F32 [n_experts x dim]; data: device */
+    const gguf_tensor *gate_exps;  /* only ggml_type is read: expert bytes  */
+    const gguf_tensor *up_exps;    /*   come from the ExpertStore, as in    */
+    const gguf_tensor *down_exps;  /*   src/gguf_run.c:201-204              */
+    /* Optional device [n_experts] F32 bias added to the router logits before
+     * the softmax; NULL = none. No counterpart in the reference (its router has
+     * no bias); used to skew routing for prefill workloads. */
+    const float *logit_bias;
+} vireo_moe_layer;
+
+/* The fields moe_ffn reads from Model (src/gguf_run.c:146-157). */
+typedef struct {
+    int dim;          /* d */
+    int n_experts;    /* E */
+    int n_used;       /* k (top-k), 1 <= k <= min(E, 64) */
+    int ffn_exp;      /* expert intermediate size fe */
+    int topk_renorm;  /* renormalise the k weights (src/gguf_run.c:292-293) */
+    int n_layers;
+    const vireo_moe_layer *layers;   /* host array [n_layers] */
+    ExpertStore *es;
+} vireo_moe_model;
+
+/* Routing flags, one word per token (moe_route `flags`). */
+#define VIREO_ROUTE_EXACT_FALLBACK 1u  /* the fast fp64 router could not certify
+                                          the order; exact fp32 sums were used */
+#define VIREO_ROUTE_NEAR_TIE       2u  /* a selection boundary had an exact logit
+                                          gap below 1e-6 (reported exception)  */
+
+/* Stage 1 of moe_ffn_forward: router logits (F32 matvec), softmax, top-k with
+ * lowest-index tie-break, optional renorm (src/gguf_run.c:187-192), for
+ * n_tokens tokens. hb: device [n_tokens x dim]. idx [n_tokens x k] (int32) and
+ * w [n_tokens x k] receive the chosen experts in selection order and their
+ * weights; flags [n_tokens] (optional) receives VIREO_ROUTE_* bits; probs
+ * [n_tokens x E] (optional) receives the softmax probabilities. The expert
+ * ids equal the reference's bit for bit except where flags report a near tie. */
+int moe_route(const vireo_moe_model *m, int layer, const float *hb, int n_tokens,
+              int32_t *idx, float *w, uint32_t *flags, float *probs, void *stream);
+
+/* Stage 2: bucket the n_tokens*k (token, slot) pairs by expert. counts [E],
+ * offs [E+1] (exclusive prefix sum, offs[E] = n_tokens*k) and perm
+ * [n_tokens*k], where perm lists pair ids t*k + j sorted by (expert, t). No
+ * counterpart in the reference (it runs tokens one at a time). */
+int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts,
+                 int32_t *counts, int32_t *offs, int32_t *perm, void *stream);
+
+/* moe_ffn for n_tokens independent tokens: x[t] += sum_j w_tj * down_e(
+ * silu(gate_e hb[t]) * up_e hb[t]) over the k routed experts e = idx[t][j],
+ * combined in selection order without atomics. x, hb: device
+ * [n_tokens x dim]; idx_out / w_out (optional) receive the routing.
+ * Expert slices come from m->es; on the first call for a layer every expert
+ * of that layer is looked up once and its lease held (the resident set is
+ * the whole layer), as there is no host round trip per token. An expert that
+ * is not registered contributes nothing, as in the reference. */
+int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
+                    int32_t *idx_out, float *w_out, void *stream);
+
+/* Execution plan for moe_ffn_forward (a tuning and testing knob; no
+ * counterpart in the reference): 0 = automatic (default), 1 = the one-token
+ * decode plan whenever it applies, 2 = always the grouped plan. */
+int vireo_hip_set_path(int path);
+
+/* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
+
+/* A store whose backing "file" is already in device memory (dev_base, size
+ * bytes), for weights generated or uploaded on the GPU: slices registered
+ * with offsets into dev_base become resident without a copy. */
+ExpertStore *expert_store_create_device(const void *dev_base, uint64_t size, uint64_t capacity_bytes,
+                                        int n_layers, int n_experts);
+/* Look up every registered expert of `layer` once and hold the leases, and
+ * return a device table [n_experts x 3] of {gate, up, down} pointers (NULL for
+ * unregistered experts). Later calls return the same table. */
+int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_table);
+/* Release the leases taken by expert_store_pin_layer for `layer`. */
+int expert_store_unpin_layer(ExpertStore *s, int layer);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,128 @@
+"""ctypes bindings for libvireo_hip.so (the C-ABI declared in include/*.h).
+
+The library is built in-tree by vireo_amd.build; loading fails loudly when it
+is missing, because there is no CPU fallback for any of these entry points.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvireo_hip.so")
+
+c_vp = C.c_void_p
+c_i32p = C.POINTER(C.c_int32)
+
+
+class GGUFStr(C.Structure):
+    _fields_ = [("ptr", C.c_char_p), ("len", C.c_uint64)]
+
+
+class GGUFTensor(C.Structure):
+    """gguf_tensor (src/gguf.h:36-45); only data and ggml_type are read."""
+    _fields_ = [
+        ("name", GGUFStr),
+        ("n_dims", C.c_uint32),
+        ("dims", C.c_uint64 * 4),
+        ("ggml_type", C.c_uint32),
+        ("offset", C.c_uint64),
+        ("data", c_vp),
+        ("n_elems", C.c_uint64),
+        ("nbytes", C.c_uint64),
+    ]
+
+
+class ExpertStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "requests", "hits", "misses", "bytes_read", "resident_bytes", "capacity_bytes", "experts_resident")]
+
+
+class ExpertSlices(C.Structure):
+    _fields_ = [
+        ("gate_off", C.c_uint64), ("up_off", C.c_uint64), ("down_off", C.c_uint64),
+        ("gate_bytes", C.c_uint32), ("up_bytes", C.c_uint32), ("down_bytes", C.c_uint32),
+    ]
+
+
+class ExpertView(C.Structure):
+    _fields_ = [("gate", c_vp), ("up", c_vp), ("down", c_vp), ("slot", c_vp)]
+
+
+class MoELayer(C.Structure):
+    _fields_ = [
+        ("router", C.POINTER(GGUFTensor)),
+        ("gate_exps", C.POINTER(GGUFTensor)),
+        ("up_exps", C.POINTER(GGUFTensor)),
+        ("down_exps", C.POINTER(GGUFTensor)),
+        ("logit_bias", c_vp),
+    ]
+
+
+class MoEModel(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int), ("n_experts", C.c_int), ("n_used", C.c_int), ("ffn_exp", C.c_int),
+        ("topk_renorm", C.c_int), ("n_layers", C.c_int),
+        ("layers", C.POINTER(MoELayer)),
+        ("es", c_vp),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "vireo_hip_init": (C.c_int, [C.c_int]),
+    "vireo_hip_strerror": (C.c_char_p, [C.c_int]),
+    "vireo_type_block": (C.c_int, [C.c_uint32, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "qmatvec": (C.c_int, [c_vp, c_vp, C.POINTER(GGUFTensor), C.c_int, C.c_int]),
+    "qmatvec_async": (C.c_int, [c_vp, c_vp, C.POINTER(GGUFTensor), C.c_int, C.c_int, c_vp]),
+    "qdequant_rows": (C.c_int, [C.c_uint32, c_vp, c_vp, C.c_int, C.c_int, c_vp]),
+    "vireo_rmsnorm": (C.c_int, [c_vp, c_vp, c_vp, C.c_int, C.c_int, C.c_float, c_vp]),
+    "vireo_argmax": (C.c_int, [c_vp, C.c_int, c_vp, c_vp]),
+    "moe_route": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "moe_dispatch": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
+    "vireo_hip_set_path": (C.c_int, [C.c_int]),
+    "moe_ffn_forward": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp]),
+    "expert_store_create": (c_vp, [C.c_int, C.c_uint64, C.c_int, C.c_int]),
+    "expert_store_create_device": (c_vp, [c_vp, C.c_uint64, C.c_uint64, C.c_int, C.c_int]),
+    "expert_store_register": (None, [c_vp, C.c_int, C.c_int, C.POINTER(ExpertSlices)]),
+    "expert_store_lookup": (C.c_int, [c_vp, C.c_int, C.c_int, C.POINTER(ExpertView)]),
+    "expert_store_release": (None, [c_vp, C.POINTER(ExpertView)]),
+    "expert_store_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
+    "expert_store_destroy": (None, [c_vp]),
+    "expert_store_pin_layer": (C.c_int, [c_vp, C.c_int, C.POINTER(c_vp)]),
+    "expert_store_unpin_layer": (C.c_int, [c_vp, C.c_int]),
+    "vireo_synth_normal": (C.c_int, [c_vp, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float]),
+    "vireo_quantize": (C.c_int, [C.c_uint32, c_vp, c_vp, C.c_int, C.c_int64]),
+    "vireo_synth_matrix": (C.c_int, [C.c_uint32, c_vp, C.c_int, C.c_int64, C.c_int64, C.c_uint64, C.c_uint64,
+                                     C.c_float]),
+    "vireo_synth_matrix_dev": (C.c_int, [C.c_uint32, c_vp, C.c_int, C.c_int64, C.c_int64, C.c_uint64, C.c_uint64,
+                                         C.c_float, c_vp]),
+    "vireo_synth_hidden": (C.c_int, [c_vp, c_vp, C.c_int, C.c_int64, C.c_uint64, C.c_uint64, C.c_float]),
+    "vireo_row_bytes": (C.c_int64, [C.c_uint32, C.c_int]),
+}
+
+_lib = None
+
+
+class VireoError(RuntimeError):
+    pass
+
+
+def load():
+    """Load libvireo_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VireoError(f"{LIB_PATH} is missing: run `python -m vireo_amd.build` (no CPU fallback exists)")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc, what="vireo-hip call"):
+    if rc != 0:
+        msg = load().vireo_hip_strerror(rc)
+        raise VireoError(f"{what} failed: {rc} ({msg.decode() if msg else '?'})")
+    return rc

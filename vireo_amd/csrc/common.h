@@ -1,0 +1,96 @@
+// Shared device helpers for the vireo-hip kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <errno.h>
+#include <stdint.h>
+
+#define VH_DEV __device__ __forceinline__
+
+enum { VT_F32 = 0, VT_F16 = 1, VT_Q4_0 = 2, VT_Q5_0 = 6, VT_Q8_0 = 8, VT_Q4_K = 12, VT_Q6_K = 14 };
+
+// ---- host-side helpers ------------------------------------------------------
+int vh_check(hipError_t e);            // hipSuccess -> 0, else records the error and returns -EIO
+int vh_finish(hipStream_t s, int rc);  // synchronise when the caller passed no stream
+int vh_device_workspace(size_t bytes, void **out);  // per-device scratch, grown on demand
+int vh_counters(int n, unsigned **out);              // per-device zeroed counters (self-resetting use)
+int vh_num_cus();
+
+// ---- loads ------------------------------------------------------------------
+// All quantized rows used here are made of 2-byte units and start 4-byte
+// aligned, so any field starts at an address that is 0 or 2 mod 4. Fields are
+// read with naturally aligned dword loads of a window that never leaves the
+// field's own block, then shifted into place with v_alignbyte_b32.
+VH_DEV uint32_t ld_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+VH_DEV uint32_t ld_u16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+VH_DEV uint32_t ld_u8(const uint8_t *p) { return *p; }
+VH_DEV uint32_t align2(uint32_t hi, uint32_t lo, uint32_t bytes) { return __builtin_amdgcn_alignbyte(hi, lo, bytes); }
+
+// ---- binary16 -> binary32 (exact; v_cvt_f32_f16) --------------------------------
+VH_DEV float h2f(uint32_t h) {
+    _Float16 v;
+    uint16_t b = uint16_t(h);
+    __builtin_memcpy(&v, &b, 2);
+    return float(v);
+}
+
+// 12 bytes at byte offset off (even) of a 4-aligned base, as three dwords:
+// one aligned dwordx3 load of [off&~3, (off&~3)+12), shifted into place. The
+// first two words hold bytes [off, off+8); callers keep the window in bounds.
+VH_DEV void ld12_even(const uint8_t *base, int off, uint32_t &w0, uint32_t &w1) {
+    const uint32_t s = uint32_t(off) & 3u;
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    const u32x3 v = *reinterpret_cast<const u32x3 *>(base + (off - int(s)));
+    w0 = align2(v.y, v.x, s);
+    w1 = align2(v.z, v.y, s);
+}
+
+// ---- wave reductions (DPP, fixed order) --------------------------------------------
+// dpp_ctrl values (GFX9 DPP): quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] =
+// 0x4E, row_half_mirror = 0x141, row_mirror = 0x140, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf>
+VH_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+VH_DEV uint32_t dpp_u(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, ROW_MASK, 0xf, false));
+}
+// Sum over aligned groups of L lanes (L a power of two <= 64). The total is in
+// the last lane of each group (lane % L == L-1); for L <= 16 every lane of the
+// group holds it. Must be called with all 64 lanes active.
+template <int L>
+VH_DEV float group_sum(float v) {
+    if constexpr (L >= 2) v += dpp_f<0xB1>(v);
+    if constexpr (L >= 4) v += dpp_f<0x4E>(v);
+    if constexpr (L >= 8) v += dpp_f<0x141>(v);
+    if constexpr (L >= 16) v += dpp_f<0x140>(v);
+    if constexpr (L >= 32) v += dpp_f<0x142, 0xA>(v);
+    if constexpr (L >= 64) v += dpp_f<0x143, 0xC>(v);
+    return v;
+}
+// Wave-wide sum / unsigned max, returned on every lane (readlane of lane 63).
+VH_DEV float wave_sum_f(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum<64>(v)), 63)); }
+VH_DEV uint32_t wave_max_u(uint32_t v) {
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x140>(v));
+    v = max(v, dpp_u<0x142, 0xA>(v));
+    v = max(v, dpp_u<0x143, 0xC>(v));
+    return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+VH_DEV double readlane_d(double v, int lane) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), lane));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), lane));
+    return __longlong_as_double(int64_t((uint64_t(hi) << 32) | lo));
+}
+VH_DEV double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---- SwiGLU gate: silu(g) * u, as src/gguf_run.c:207 -----------------------------
+VH_DEV float swiglu(float g, float u) { return (g / (1.0f + expf(-g))) * u; }

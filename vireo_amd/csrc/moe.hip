@@ -1,0 +1,152 @@
+// moe_route / moe_dispatch / moe_ffn_forward: host orchestration of the MoE
+// kernels (route.hip, moe_decode.hip, moe_grouped.hip).
+//
+// Reference: moe_ffn, src/gguf_run.c:185-214. Two execution plans produce its
+// result for a batch of independent tokens:
+//   decode (one token):  router parts -> fused top-k + gate/up SwiGLU ->
+//                        down + combine + residual               (3 kernels)
+//   grouped (any count): router -> top-k -> dispatch -> grouped gate/up ->
+//                        grouped down -> combine + residual      (6 kernels)
+// The grouped plan reads each routed expert's weights once per call however
+// many tokens chose it.
+#include <hip/hip_runtime.h>
+#include <string.h>
+#include "common.h"
+#include "route_kernels.h"
+#include "vireo_hip.h"
+
+namespace {
+
+int g_path = 0;                        // 0 auto, 1 decode plan when possible, 2 grouped plan
+constexpr int kExactRouteTokens = 64;  // from this many tokens on, exact sequential logits
+
+bool type_ok(uint32_t t, int n) {
+    switch (t) {
+    case VT_Q8_0: case VT_Q5_0: return n % 32 == 0;
+    case VT_Q4_K: case VT_Q6_K: return n % 256 == 0;
+    default: return false;
+    }
+}
+
+int check_model(const vireo_moe_model *m, int layer) {
+    if (!m || layer < 0 || layer >= m->n_layers || !m->layers) return -EINVAL;
+    const vireo_moe_layer &L = m->layers[layer];
+    if (m->dim <= 0 || m->ffn_exp <= 0 || m->n_experts <= 0 || m->n_experts > kMaxExperts) return -EINVAL;
+    if (m->n_used < 1 || m->n_used > 64 || m->n_used > m->n_experts) return -EINVAL;
+    if (!L.router || L.router->ggml_type != VT_F32 || !L.router->data) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(L.router->data) & 3u) return -EINVAL;
+    return 0;
+}
+
+size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct Ws {
+    RoutePart *parts;
+    int32_t *idx, *counts, *offs, *perm, *active;
+    float *w, *h, *ybuf;
+    uint32_t *flags;
+};
+
+int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws) {
+    const size_t P = size_t(T) * k;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
+    const size_t o_parts = take(size_t(T) * E * sizeof(RoutePart));
+    const size_t o_idx = take(P * 4), o_w = take(P * 4), o_flags = take(size_t(T) * 4);
+    const size_t o_counts = take(size_t(E) * 4), o_offs = take(size_t(E + 1) * 4), o_perm = take(P * 4),
+                 o_active = take(size_t(E + 1) * 4);
+    const size_t o_h = experts ? take(P * fe * 4) : 0;
+    const size_t o_y = (experts && grouped) ? take(P * d * 4) : 0;
+    void *base;
+    if (int rc = vh_device_workspace(off, &base)) return rc;
+    char *b = static_cast<char *>(base);
+    ws->parts = reinterpret_cast<RoutePart *>(b + o_parts);
+    ws->idx = reinterpret_cast<int32_t *>(b + o_idx);
+    ws->w = reinterpret_cast<float *>(b + o_w);
+    ws->flags = reinterpret_cast<uint32_t *>(b + o_flags);
+    ws->counts = reinterpret_cast<int32_t *>(b + o_counts);
+    ws->offs = reinterpret_cast<int32_t *>(b + o_offs);
+    ws->perm = reinterpret_cast<int32_t *>(b + o_perm);
+    ws->active = reinterpret_cast<int32_t *>(b + o_active);
+    ws->h = experts ? reinterpret_cast<float *>(b + o_h) : nullptr;
+    ws->ybuf = (experts && grouped) ? reinterpret_cast<float *>(b + o_y) : nullptr;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int vireo_hip_set_path(int path) {
+    if (path < 0 || path > 2) return -EINVAL;
+    g_path = path;
+    return 0;
+}
+
+extern "C" int moe_route(const vireo_moe_model *m, int layer, const float *hb, int n_tokens, int32_t *idx, float *w,
+                         uint32_t *flags, float *probs, void *stream) {
+    if (int rc = check_model(m, layer)) return rc;
+    if (n_tokens < 0 || (n_tokens && (!hb || !idx || !w))) return -EINVAL;
+    if (n_tokens == 0) return 0;
+    if (n_tokens > 65535) return -E2BIG;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const vireo_moe_layer &L = m->layers[layer];
+    const float *R = static_cast<const float *>(L.router->data);
+    Ws ws;
+    if (int rc = get_ws(n_tokens, m->n_experts, m->n_used, m->dim, m->ffn_exp, false, false, &ws)) return rc;
+    const bool exact = n_tokens >= kExactRouteTokens;
+    int rc = vh_route_parts(R, hb, L.logit_bias, m->dim, m->n_experts, n_tokens, exact, ws.parts, s);
+    if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, m->dim, m->n_experts, m->n_used, m->topk_renorm,
+                                  exact, n_tokens, idx, w, flags, probs, s);
+    return vh_finish(s, rc);
+}
+
+extern "C" int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts, int32_t *counts, int32_t *offs,
+                            int32_t *perm, void *stream) {
+    if (n_tokens < 0 || k < 1 || n_experts < 1 || n_experts > kMaxExperts) return -EINVAL;
+    if (!counts || !offs || (n_tokens && (!idx || !perm))) return -EINVAL;
+    const int64_t P = int64_t(n_tokens) * k;
+    if (P > (int64_t(1) << 30)) return -E2BIG;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, vh_dispatch(idx, int(P), n_experts, counts, offs, perm, nullptr, s));
+}
+
+extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
+                               int32_t *idx_out, float *w_out, void *stream) {
+    if (int rc = check_model(m, layer)) return rc;
+    if (n_tokens < 0 || (n_tokens && (!x || !hb))) return -EINVAL;
+    if (n_tokens == 0) return 0;
+    const vireo_moe_layer &L = m->layers[layer];
+    if (!L.gate_exps || !L.up_exps || !L.down_exps || !m->es) return -EINVAL;
+    const uint32_t tg = L.gate_exps->ggml_type, tu = L.up_exps->ggml_type, td = L.down_exps->ggml_type;
+    const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
+    if (tg != tu || !type_ok(tg, d) || !type_ok(td, fe) || fe % 4) return -EINVAL;
+    if (int64_t(n_tokens) * k > 65535 || n_tokens > 65535) return -E2BIG;
+    const void *const *table = nullptr;
+    if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const float *R = static_cast<const float *>(L.router->data);
+
+    const bool decode = n_tokens == 1 && g_path != 2 && vh_decode_gateup_supported(tg, d, fe) &&
+                        vh_down_combine_supported(td, d, fe, k);
+    Ws ws;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws)) return rc;
+    int32_t *idx = idx_out ? idx_out : ws.idx;
+    float *w = w_out ? w_out : ws.w;
+    int rc;
+    if (decode) {
+        rc = vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, ws.parts, s);
+        if (!rc) rc = vh_decode_gateup(tg, ws.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, ws.h,
+                                       idx, w, ws.flags, s);
+        if (!rc) rc = vh_down_combine(td, idx, w, table, ws.h, d, fe, k, 1, x, s);
+        return vh_finish(s, rc);
+    }
+    const bool exact = n_tokens >= kExactRouteTokens;
+    const int P = n_tokens * k, slots = P < E ? P : E;
+    rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
+    if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
+                                  ws.flags, nullptr, s);
+    if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
+    if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
+    return vh_finish(s, rc);
+}

@@ -1,0 +1,190 @@
+// qmatvec (gguf_matmul on the GPU) and qdequant_rows (gguf_dequant_row).
+//
+// qmatvec: each output row is split over L lanes of a wave (L chosen per shape
+// so no lane idles), every lane decodes whole 32-weight items straight from
+// the GGUF bytes with aligned loads, and the L partial sums are folded with a
+// shuffle tree. Rows are streamed once; the kernel is HBM-bound.
+#include <hip/hip_runtime.h>
+#include "common.h"
+#include "qdecode.h"
+#include "vireo_hip.h"
+
+namespace {
+
+template <int T, bool PAIRED, int L>
+__global__ void __launch_bounds__(256) qmatvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                      const uint8_t *__restrict__ w, int n, int d, int64_t row_bytes) {
+    using F = Fmt<T, PAIRED>;
+    constexpr int RPW = 64 / L;
+    const int lane = threadIdx.x & 63, sub = lane / L, li = lane % L;
+    const int items = F::items(n);
+    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t nwaves = int64_t(gridDim.x) * 4;
+    for (int64_t r0 = wave * RPW; r0 < d; r0 += nwaves * RPW) {
+        const int64_t row = r0 + sub;
+        float acc = 0.0f;
+        if (row < d) {
+            const int64_t ro = row * row_bytes;
+            for (int it = li; it < items; it += L) acc += F::dot(w, ro, it, n, x);
+        }
+        acc = group_sum<L>(acc);
+        if (li == L - 1 && row < d) y[row] = acc;
+    }
+}
+
+template <int T, bool PAIRED>
+int launch_L(int L, float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, hipStream_t s) {
+    const int rpw = 64 / L;
+    int64_t waves = (int64_t(d) + rpw - 1) / rpw;
+    int64_t blocks = (waves + 3) / 4;
+    const int64_t cap = int64_t(vh_num_cus()) * 16;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    dim3 g(static_cast<unsigned>(blocks)), b(256);
+    switch (L) {
+    case 64: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 64>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 32: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 32>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 16: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 16>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 8: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 8>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 4: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 4>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 2: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 2>), g, b, 0, s, y, x, w, n, d, rb); break;
+    default: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 1>), g, b, 0, s, y, x, w, n, d, rb); break;
+    }
+    return vh_check(hipGetLastError());
+}
+
+// Lanes per row: the power of two (<= 64) that leaves the fewest idle item
+// slots, preferring more lanes on a tie.
+int pick_lanes(int items) {
+    int best = 64, waste_best = 1 << 30;
+    for (int L = 64; L >= 1; L >>= 1) {
+        int waste = L * ((items + L - 1) / L) - items;
+        if (waste < waste_best) { waste_best = waste; best = L; }
+    }
+    return best;
+}
+
+// ---- dequant ----
+template <int T>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict__ src, float *__restrict__ dst, int n,
+                                                      int rows, int64_t row_bytes, int items) {
+#pragma clang fp contract(off)
+    const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= int64_t(rows) * items) return;
+    const int64_t row = gid / items;
+    const int it = int(gid % items);
+    const uint8_t *r = src + row * row_bytes;
+    float *o = dst + row * int64_t(n);
+    if constexpr (T == VT_Q8_0) {
+        const uint8_t *b = r + 34 * it;
+        const float d = h2f(ld_u16(b));
+        for (int i = 0; i < 32; i++) o[32 * it + i] = __fmul_rn(float(int8_t(ld_u8(b + 2 + i))), d);
+    } else if constexpr (T == VT_Q4_K) {
+        // one 32-element sub-block j per thread (items = n/32): y = (d*sc)*q - dmin*m
+        const int sbi = it >> 3, j = it & 7;
+        const uint8_t *sb = r + 144 * sbi;
+        const float d = h2f(ld_u16(sb)), dmin = h2f(ld_u16(sb + 2));
+        const uint32_t s0 = ld_u32(sb + 4), s1 = ld_u32(sb + 8), s2 = ld_u32(sb + 12);
+        int sc, m;
+        q4k_scale_min(j, s0, s1, s2, sc, m);
+        const float d1 = __fmul_rn(d, float(sc)), m1 = __fmul_rn(dmin, float(m));
+        const uint8_t *q = sb + 16 + 32 * (j >> 1);
+        const int sh = (j & 1) ? 4 : 0;
+        for (int l = 0; l < 32; l++) o[256 * sbi + 32 * j + l] = __fsub_rn(__fmul_rn(d1, float((ld_u8(q + l) >> sh) & 15u)), m1);
+    } else if constexpr (T == VT_Q6_K) {
+        // 16 elements sharing one scale per thread (items = n/16)
+        const int sbi = it >> 4, s = it & 15;
+        const uint8_t *sb = r + 210 * sbi;
+        const float d = h2f(ld_u16(sb + 208));
+        const float ds = __fmul_rn(d, float(int8_t(ld_u8(sb + 192 + s))));
+        const int hh = s >> 3, g = (s >> 1) & 3, half = s & 1;
+        for (int i = 0; i < 16; i++) {
+            const int l = 16 * half + i;
+            const uint32_t qlb = ld_u8(sb + 64 * hh + l + 32 * (g & 1));
+            const uint32_t lo4 = g >= 2 ? (qlb >> 4) : (qlb & 15u);
+            const uint32_t hi2 = (ld_u8(sb + 128 + 32 * hh + l) >> (2 * g)) & 3u;
+            o[256 * sbi + 128 * hh + 32 * g + l] = __fmul_rn(ds, float(int(lo4 | (hi2 << 4)) - 32));
+        }
+    } else if constexpr (T == VT_Q5_0) {
+        const uint8_t *b = r + 22 * it;
+        const float d = h2f(ld_u16(b));
+        const uint32_t qh = ld_u16(b + 2) | (ld_u16(b + 4) << 16);
+        for (int j = 0; j < 16; j++) {
+            const uint32_t qs = ld_u8(b + 6 + j);
+            o[32 * it + j] = __fmul_rn(float(int((qs & 15u) | (((qh >> j) & 1u) << 4)) - 16), d);
+            o[32 * it + j + 16] = __fmul_rn(float(int((qs >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16), d);
+        }
+    } else if constexpr (T == VT_F16) {
+        for (int i = 32 * it; i < n && i < 32 * it + 32; i++) o[i] = h2f(ld_u16(r + 2 * i));
+    } else {
+        const float *rf = reinterpret_cast<const float *>(r);
+        for (int i = 32 * it; i < n && i < 32 * it + 32; i++) o[i] = rf[i];
+    }
+}
+
+}  // namespace
+
+// Host-side shape checks shared by the matvec entry points.
+static int check_weights(uint32_t type, const void *data, int n, int d, int64_t *row_bytes) {
+    int be, bb;
+    if (vireo_type_block(type, &be, &bb) || type == VT_Q4_0) return -EINVAL;
+    if (n <= 0 || d < 0 || n % be) return -EINVAL;
+    if (!data && d) return -EINVAL;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(data);
+    if (a & 3u) return -EINVAL;
+    if (type == VT_Q4_K && (a & 15u)) return -EINVAL;
+    *row_bytes = int64_t(n / be) * bb;
+    return 0;
+}
+
+extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int n, int d, void *stream) {
+    if (!w || (!y && d) || (!x && d)) return -EINVAL;
+    int64_t rb;
+    if (int rc = check_weights(w->ggml_type, w->data, n, d, &rb)) return rc;
+    if (d == 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *wd = static_cast<const uint8_t *>(w->data);
+    switch (w->ggml_type) {
+    case VT_Q8_0:
+        if (n % 64 == 0) return launch_L<VT_Q8_0, true>(pick_lanes(n / 64), y, x, wd, n, d, rb, s);
+        return launch_L<VT_Q8_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
+    case VT_Q4_K: return launch_L<VT_Q4_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
+    case VT_Q6_K: return launch_L<VT_Q6_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
+    case VT_Q5_0: return launch_L<VT_Q5_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
+    case VT_F16: return launch_L<VT_F16, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, s);
+    case VT_F32: return launch_L<VT_F32, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, s);
+    default: return -EINVAL;
+    }
+}
+
+extern "C" int qmatvec(float *y, const float *x, const gguf_tensor *w, int n, int d) {
+    return vh_finish(nullptr, qmatvec_async(y, x, w, n, d, nullptr));
+}
+
+extern "C" int qdequant_rows(uint32_t type, const void *src, float *dst, int n, int rows, void *stream) {
+    int64_t rb;
+    if (rows < 0 || (!dst && rows)) return -EINVAL;
+    if (int rc = check_weights(type, src, n, rows, &rb)) return rc;
+    if (rows == 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *sp = static_cast<const uint8_t *>(src);
+    int items;
+    switch (type) {
+    case VT_Q6_K: items = n / 16; break;
+    case VT_F16: case VT_F32: items = (n + 31) / 32; break;
+    default: items = n / 32; break;
+    }
+    const int64_t total = int64_t(rows) * items;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffff) return -E2BIG;
+    dim3 g(static_cast<unsigned>(blocks)), b(256);
+    switch (type) {
+    case VT_Q8_0: hipLaunchKernelGGL(dequant_kernel<VT_Q8_0>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    case VT_Q4_K: hipLaunchKernelGGL(dequant_kernel<VT_Q4_K>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    case VT_Q6_K: hipLaunchKernelGGL(dequant_kernel<VT_Q6_K>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    case VT_Q5_0: hipLaunchKernelGGL(dequant_kernel<VT_Q5_0>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    case VT_F16: hipLaunchKernelGGL(dequant_kernel<VT_F16>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    default: hipLaunchKernelGGL(dequant_kernel<VT_F32>, g, b, 0, s, sp, dst, n, rows, rb, items); break;
+    }
+    return vh_finish(s, vh_check(hipGetLastError()));
+}

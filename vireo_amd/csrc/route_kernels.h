@@ -1,0 +1,36 @@
+// Host-side launchers shared between the routing, decode and grouped kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include "route.h"
+
+// Router logits of T tokens into parts[T x E] (fast bounded, or exact).
+int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
+                   RoutePart *parts, hipStream_t s);
+// Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
+int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
+                    int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
+                    hipStream_t s);
+
+// Decode path (one token): gate/up with the top-k fused in, then down + combine.
+int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
+                     int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
+                     uint32_t *flags, hipStream_t s);
+bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
+// Down projection + weighted combine + residual for T tokens (each token's
+// k experts in selection order): x[t] += sum_j w[t][j] * down_{idx[t][j]} h[t*k+j].
+int vh_down_combine(uint32_t type, const int32_t *idx, const float *w, const void *const *table, const float *h,
+                    int d, int fe, int k, int T, float *x, hipStream_t s);
+bool vh_down_combine_supported(uint32_t type, int d, int fe, int k);
+
+// Grouped path (any number of tokens): dispatch, grouped gate/up, grouped
+// down, combine.
+int vh_dispatch(const int32_t *idx, int P, int E, int32_t *counts, int32_t *offs, int32_t *perm, int32_t *active,
+                hipStream_t s);
+int vh_grouped_gateup(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
+                      const int32_t *active, const void *const *table, const float *hb, int d, int fe, int k, int E,
+                      int max_slots, float *h, hipStream_t s);
+int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
+                    const int32_t *active, const void *const *table, const float *h, int d, int fe, int E,
+                    int max_slots, float *ybuf, hipStream_t s);
+int vh_combine(const int32_t *idx, const float *w, const void *const *table, const float *ybuf, int d, int k, int T,
+               float *x, hipStream_t s);
