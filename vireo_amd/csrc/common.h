@@ -69,6 +69,20 @@ VH_DEV float group_sum(float v) {
     if constexpr (L >= 64) v += dpp_f<0x143, 0xC>(v);
     return v;
 }
+template <int CTRL, int ROW_MASK = 0xf>
+VH_DEV float dpp_keep(float v) {  // rows outside ROW_MASK read their own value
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+// Wave-wide max of floats, returned on every lane.
+VH_DEV float wave_max_f(float v) {
+    v = fmaxf(v, dpp_keep<0xB1>(v));
+    v = fmaxf(v, dpp_keep<0x4E>(v));
+    v = fmaxf(v, dpp_keep<0x141>(v));
+    v = fmaxf(v, dpp_keep<0x140>(v));
+    v = fmaxf(v, dpp_keep<0x142, 0xA>(v));
+    v = fmaxf(v, dpp_keep<0x143, 0xC>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 // Wave-wide sum / unsigned max, returned on every lane (readlane of lane 63).
 VH_DEV float wave_sum_f(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum<64>(v)), 63)); }
 VH_DEV uint32_t wave_max_u(uint32_t v) {
@@ -86,9 +100,34 @@ VH_DEV double readlane_d(double v, int lane) {
     const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), lane));
     return __longlong_as_double(int64_t((uint64_t(hi) << 32) | lo));
 }
+// DPP move of a double (two 32-bit halves); lanes without a source read 0.
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = false>
+VH_DEV double dpp_d(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(b)), CTRL, ROW_MASK, 0xf, BOUND_ZERO));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(b >> 32)), CTRL, ROW_MASK, 0xf, BOUND_ZERO));
+    return __longlong_as_double(int64_t((uint64_t(hi) << 32) | lo));
+}
+// Wave-wide fp64 sum (fixed tree), returned on every lane.
 VH_DEV double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    v += dpp_d<0x142, 0xA>(v);
+    v += dpp_d<0x143, 0xC>(v);
+    return readlane_d(v, 63);
+}
+// Inclusive fp64 prefix sum over the 64 lanes (Hillis-Steele inside each
+// 16-lane row with row_shr 1/2/4/8, then the row totals carried forward with
+// row_bcast 15/31).
+VH_DEV double wave_incl_scan_d(double v) {
+    v += dpp_d<0x111, 0xf, true>(v);
+    v += dpp_d<0x112, 0xf, true>(v);
+    v += dpp_d<0x114, 0xf, true>(v);
+    v += dpp_d<0x118, 0xf, true>(v);
+    v += dpp_d<0x142, 0xA>(v);
+    v += dpp_d<0x143, 0xC>(v);
     return v;
 }
 

@@ -45,6 +45,7 @@ struct Ws {
     int32_t *idx, *counts, *offs, *perm, *active;
     float *w, *h, *ybuf;
     uint32_t *flags;
+    DecodePlan *plan;
 };
 
 int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws) {
@@ -53,6 +54,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
     const size_t o_parts = take(size_t(T) * E * sizeof(RoutePart));
     const size_t o_idx = take(P * 4), o_w = take(P * 4), o_flags = take(size_t(T) * 4);
+    const size_t o_plan = take(sizeof(DecodePlan));
     const size_t o_counts = take(size_t(E) * 4), o_offs = take(size_t(E + 1) * 4), o_perm = take(P * 4),
                  o_active = take(size_t(E + 1) * 4);
     const size_t o_h = experts ? take(P * fe * 4) : 0;
@@ -64,6 +66,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->idx = reinterpret_cast<int32_t *>(b + o_idx);
     ws->w = reinterpret_cast<float *>(b + o_w);
     ws->flags = reinterpret_cast<uint32_t *>(b + o_flags);
+    ws->plan = reinterpret_cast<DecodePlan *>(b + o_plan);
     ws->counts = reinterpret_cast<int32_t *>(b + o_counts);
     ws->offs = reinterpret_cast<int32_t *>(b + o_offs);
     ws->perm = reinterpret_cast<int32_t *>(b + o_perm);
@@ -135,8 +138,8 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (decode) {
         rc = vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, ws.parts, s);
         if (!rc) rc = vh_decode_gateup(tg, ws.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, ws.h,
-                                       idx, w, ws.flags, s);
-        if (!rc) rc = vh_down_combine(td, idx, w, table, ws.h, d, fe, k, 1, x, s);
+                                       idx, w, ws.flags, ws.plan, s);
+        if (!rc) rc = vh_down_combine(td, ws.plan, ws.h, d, fe, k, x, s);
         return vh_finish(s, rc);
     }
     const bool exact = n_tokens >= kExactRouteTokens;

@@ -49,14 +49,15 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(const RoutePart *__r
                                                             int fe, int renorm, const void *const *__restrict__ table,
                                                             int64_t row_bytes, float *__restrict__ h,
                                                             int32_t *__restrict__ idx_out, float *__restrict__ w_out,
-                                                            uint32_t *__restrict__ flags_out) {
+                                                            uint32_t *__restrict__ flags_out,
+                                                            DecodePlan *__restrict__ plan) {
     using S = Split<T>;
     constexpr int NW = S::NW, SUB = 64 / L;
-    __shared__ int s_sel[64];
+    __shared__ TopKSmem sm;
     __shared__ const void *s_tab[3 * kMaxExperts];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, sub = lane / L, li = lane % L;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / L, li = lane % L;
     const int j = blockIdx.y;
-    for (int i = threadIdx.x; i < 3 * E; i += 256) s_tab[i] = table[i];
+    for (int i = tid; i < 3 * E; i += 256) s_tab[i] = table[i];
     // the lane's inputs, in the item's own order
     float xr[NW];
     {
@@ -69,16 +70,17 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(const RoutePart *__r
 #pragma unroll
         for (int i = 0; i < 16; i++) { sl += xr[i]; sh += xr[16 + i]; }
     }
-    if (wv == 0) {
-        const TopK tk = route_topk(parts, R, hb, bias, d, E, k, renorm, false, nullptr);
-        if (lane < k) s_sel[lane] = tk.sel;
-        if (blockIdx.x == 0 && blockIdx.y == 0) {
-            if (lane < k) { idx_out[lane] = tk.sel; w_out[lane] = tk.w; }
-            if (lane == 0 && flags_out) flags_out[0] = tk.flag;
+    route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (tid < k) {
+            idx_out[tid] = sm.sel[tid];
+            w_out[tid] = sm.sel_w[tid];
+            plan->down[tid] = s_tab[3 * sm.sel[tid] + 2];
+            plan->w[tid] = sm.sel_w[tid];
         }
+        if (tid == 0 && flags_out) flags_out[0] = sm.flag;
     }
-    __syncthreads();
-    const int e = s_sel[j];
+    const int e = sm.sel[j];
     const uint8_t *G = static_cast<const uint8_t *>(s_tab[3 * e]);
     const uint8_t *U = static_cast<const uint8_t *>(s_tab[3 * e + 1]);
     const int o0 = (blockIdx.x * 4 + wv) * RPW * SUB + sub;
@@ -118,32 +120,31 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(const RoutePart *__r
 template <int T, int L, int RPW>
 int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E,
                          int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx,
-                         float *w, uint32_t *flags, hipStream_t s) {
+                         float *w, uint32_t *flags, DecodePlan *plan, hipStream_t s) {
     constexpr int rows_per_block = 4 * RPW * (64 / L);
     dim3 g((fe + rows_per_block - 1) / rows_per_block, k);
     hipLaunchKernelGGL((decode_gateup_kernel<T, L, RPW>), g, dim3(256), 0, s, parts, R, hb, bias, d, E, k, fe,
-                       renorm, table, rb, h, idx, w, flags);
+                       renorm, table, rb, h, idx, w, flags, plan);
     return vh_check(hipGetLastError());
 }
 
 // ------------------------------------------------------------------ down + combine
-// grid (d / R, T), 256 threads, R = 256 / (Q * k): unit (r, j) = output row
-// o0 + r of expert j, handled by Q consecutive lanes; a lane takes items
-// qi, qi + Q, ... (at most IPL of them).
+// grid (d / R), 256 threads, R = 256 / (Q * k): unit (r, j) = output row o0 + r
+// of expert j, handled by Q consecutive lanes; a lane takes items qi, qi + Q,
+// ... (at most IPL of them). The k activations sit in LDS with one pad float
+// per 32 and a stride that spreads a wave's simultaneous reads over the banks.
 template <int T, int Q, int IPL>
-__global__ void __launch_bounds__(256) down_combine_kernel(const int32_t *__restrict__ idx, const float *__restrict__ w,
-                                                           const void *const *__restrict__ table,
+__global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__restrict__ plan,
                                                            const float *__restrict__ h, int d, int fe, int k, int R,
-                                                           int64_t row_bytes, float *__restrict__ x) {
+                                                           int64_t row_bytes, int hstride, float *__restrict__ x) {
     using S = Split<T>;
-    extern __shared__ float hs[];  // [k][fe], then ys [R][k]
-    float *ys = hs + size_t(k) * fe;
-    const int t = blockIdx.y, o0 = blockIdx.x * R, tid = threadIdx.x;
+    extern __shared__ float hs[];  // k padded rows of stride hstride, then ys [R][k]
+    float *ys = hs + size_t(k) * hstride;
+    const int o0 = blockIdx.x * R, tid = threadIdx.x;
     const int u = tid / Q, qi = tid % Q, r = u / k, jj = u % k;
     const int items = T == VT_Q8_0 ? fe / 64 : fe / 32;
-    // this lane's expert and its rows' items, loaded before anything else
-    const int e = idx[size_t(t) * k + jj];
-    const uint8_t *D = e >= 0 ? static_cast<const uint8_t *>(table[3 * e + 2]) : nullptr;
+    // this lane's rows' items, loaded before anything else
+    const uint8_t *D = static_cast<const uint8_t *>(plan->down[jj]);
     typename S::Raw raw[IPL];
     const int64_t row = int64_t(o0 + r) * row_bytes;
     if (D) {
@@ -153,16 +154,22 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const int32_t *__rest
             if (it < items) raw[m] = S::fetch(D, row, it);
         }
     }
-    const float *ht = h + size_t(t) * k * fe;
-    for (int i = tid; i < k * fe / 4; i += 256) reinterpret_cast<float4 *>(hs)[i] = reinterpret_cast<const float4 *>(ht)[i];
+    // activations: float4 chunks never straddle a 32-float group
+    const int fe4 = fe >> 2;
+    for (int i = tid; i < k * fe4; i += 256) {
+        const int j2 = i / fe4, c = 4 * (i - j2 * fe4);
+        const float4 v = reinterpret_cast<const float4 *>(h)[i];
+        float *dst = hs + j2 * hstride + c + (c >> 5);
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
     __syncthreads();
     float acc = 0.0f;
     if (D) {
-        const float *hx = hs + size_t(jj) * fe;
+        const float *hx = hs + size_t(jj) * hstride;
 #pragma unroll
         for (int m = 0; m < IPL; m++) {
             const int it = qi + Q * m;
-            if (it < items) acc += S::compute(raw[m], it, S::xrow(hx, it));
+            if (it < items) acc += S::compute(raw[m], it, XPadded<T>{hx, it});
         }
     }
     acc = group_sum<Q>(acc);
@@ -171,38 +178,46 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const int32_t *__rest
     if (tid < R) {
         float a = 0.0f;
         for (int j2 = 0; j2 < k; j2++) {
-            const int e2 = idx[size_t(t) * k + j2];
-            if (e2 < 0 || !table[3 * e2 + 2]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-            a = __fadd_rn(a, __fmul_rn(w[size_t(t) * k + j2], ys[tid * k + j2]));
+            if (!plan->down[j2]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
+            a = __fadd_rn(a, __fmul_rn(plan->w[j2], ys[tid * k + j2]));
         }
-        const size_t o = size_t(t) * d + o0 + tid;
-        x[o] = __fadd_rn(x[o], a);
+        x[o0 + tid] = __fadd_rn(x[o0 + tid], a);
     }
 }
 
 constexpr int kDownQ = 4;
 
+// LDS stride between the k padded activation rows, chosen mod 64 banks so the
+// items that the 64 lanes of a wave read together (4 lanes per (row, expert),
+// 8 experts) fall in distinct banks: experts step the bank by 8 for Q8_0 (items
+// are 66 padded floats apart, 2 banks), by 1 for Q6_K (items 8 apart) and by 5
+// for Q4_K (items at 0/16/66/82).
+int down_hstride(uint32_t type, int fe) {
+    const int base = fe + (fe >> 5);
+    const int target = type == VT_Q8_0 ? 8 : type == VT_Q6_K ? 1 : 5;
+    return base + ((target - base % 64) + 64) % 64;
+}
+
 int items_of(uint32_t type, int fe) { return type == VT_Q8_0 ? fe / 64 : fe / 32; }
 
 template <int T, int IPL>
-int launch_down(const int32_t *idx, const float *w, const void *const *table, const float *h, int d, int fe, int k,
-                int T_, float *x, hipStream_t s) {
+int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, hipStream_t s) {
     const int R = 256 / (kDownQ * k);
     const int64_t rb = row_bytes_of(T, fe);
-    const size_t lds = size_t(k) * fe * 4 + size_t(R) * k * 4;
-    dim3 g(d / R, T_);
-    hipLaunchKernelGGL((down_combine_kernel<T, kDownQ, IPL>), g, dim3(256), lds, s, idx, w, table, h, d, fe, k, R, rb, x);
+    const int hstride = down_hstride(T, fe);
+    const size_t lds = size_t(k) * hstride * 4 + size_t(R) * k * 4;
+    hipLaunchKernelGGL((down_combine_kernel<T, kDownQ, IPL>), dim3(d / R), dim3(256), lds, s, plan, h, d, fe, k, R,
+                       rb, hstride, x);
     return vh_check(hipGetLastError());
 }
 
 template <int T>
-int launch_down_ipl(int ipl, const int32_t *idx, const float *w, const void *const *table, const float *h, int d,
-                    int fe, int k, int T_, float *x, hipStream_t s) {
-    if (ipl <= 2) return launch_down<T, 2>(idx, w, table, h, d, fe, k, T_, x, s);
-    if (ipl <= 3) return launch_down<T, 3>(idx, w, table, h, d, fe, k, T_, x, s);
-    if (ipl <= 4) return launch_down<T, 4>(idx, w, table, h, d, fe, k, T_, x, s);
-    if (ipl <= 6) return launch_down<T, 6>(idx, w, table, h, d, fe, k, T_, x, s);
-    if (ipl <= 8) return launch_down<T, 8>(idx, w, table, h, d, fe, k, T_, x, s);
+int launch_down_ipl(int ipl, const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, hipStream_t s) {
+    if (ipl <= 2) return launch_down<T, 2>(plan, h, d, fe, k, x, s);
+    if (ipl <= 3) return launch_down<T, 3>(plan, h, d, fe, k, x, s);
+    if (ipl <= 4) return launch_down<T, 4>(plan, h, d, fe, k, x, s);
+    if (ipl <= 6) return launch_down<T, 6>(plan, h, d, fe, k, x, s);
+    if (ipl <= 8) return launch_down<T, 8>(plan, h, d, fe, k, x, s);
     return -EINVAL;
 }
 
@@ -215,12 +230,12 @@ bool vh_decode_gateup_supported(uint32_t type, int d, int fe) {
 
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
-                     uint32_t *flags, hipStream_t s) {
+                     uint32_t *flags, DecodePlan *plan, hipStream_t s) {
     const int64_t rb = row_bytes_of(type, d);
     switch (type) {
-    case VT_Q4_K: return launch_decode_gateup<VT_Q4_K, 64, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, s);
-    case VT_Q8_0: return launch_decode_gateup<VT_Q8_0, 32, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, s);
-    case VT_Q6_K: return launch_decode_gateup<VT_Q6_K, 64, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, s);
+    case VT_Q4_K: return launch_decode_gateup<VT_Q4_K, 64, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
+    case VT_Q8_0: return launch_decode_gateup<VT_Q8_0, 32, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
+    case VT_Q6_K: return launch_decode_gateup<VT_Q6_K, 64, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
     default: return -EINVAL;
     }
 }
@@ -228,22 +243,22 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
 bool vh_down_combine_supported(uint32_t type, int d, int fe, int k) {
     if (!(type == VT_Q4_K || type == VT_Q8_0 || type == VT_Q6_K)) return false;
     if (type == VT_Q8_0 && fe % 64) return false;
-    if (k < 1 || 256 % (kDownQ * k)) return false;
+    if (k < 1 || k > 64 || 256 % (kDownQ * k)) return false;
     const int R = 256 / (kDownQ * k);
     if (d % R) return false;
     const int ipl = (items_of(type, fe) + kDownQ - 1) / kDownQ;
     if (ipl > 8) return false;
-    return size_t(k) * fe * 4 + size_t(R) * k * 4 <= 64 * 1024;
+    return size_t(k) * down_hstride(type, fe) * 4 + size_t(R) * k * 4 <= 64 * 1024;
 }
 
-int vh_down_combine(uint32_t type, const int32_t *idx, const float *w, const void *const *table, const float *h,
-                    int d, int fe, int k, int T, float *x, hipStream_t s) {
+int vh_down_combine(uint32_t type, const DecodePlan *plan, const float *h, int d, int fe, int k, float *x,
+                    hipStream_t s) {
     if (!vh_down_combine_supported(type, d, fe, k)) return -EINVAL;
     const int ipl = (items_of(type, fe) + kDownQ - 1) / kDownQ;
     switch (type) {
-    case VT_Q4_K: return launch_down_ipl<VT_Q4_K>(ipl, idx, w, table, h, d, fe, k, T, x, s);
-    case VT_Q8_0: return launch_down_ipl<VT_Q8_0>(ipl, idx, w, table, h, d, fe, k, T, x, s);
-    case VT_Q6_K: return launch_down_ipl<VT_Q6_K>(ipl, idx, w, table, h, d, fe, k, T, x, s);
+    case VT_Q4_K: return launch_down_ipl<VT_Q4_K>(ipl, plan, h, d, fe, k, x, s);
+    case VT_Q8_0: return launch_down_ipl<VT_Q8_0>(ipl, plan, h, d, fe, k, x, s);
+    case VT_Q6_K: return launch_down_ipl<VT_Q6_K>(ipl, plan, h, d, fe, k, x, s);
     default: return -EINVAL;
     }
 }

@@ -285,6 +285,7 @@ struct Split<VT_Q8_0> {  // paired blocks, 4-aligned
         VH_DEV float operator[](int i) const { return p[i]; }
     };
     static VH_DEV XRow xrow(const float *x, int it) { return XRow{x + 64 * it}; }
+    static VH_DEV int col(int it, int i) { return 64 * it + i; }
 };
 
 template <>
@@ -333,6 +334,7 @@ struct Split<VT_Q4_K> {  // 16-aligned super-blocks
         VH_DEV float operator[](int i) const { return p[i < 16 ? i : i + 16]; }
     };
     static VH_DEV XRow xrow(const float *x, int it) { return XRow{x + col0(it)}; }
+    static VH_DEV int col(int it, int i) { return col0(it) + (i < 16 ? i : i + 16); }
 };
 
 template <>
@@ -351,4 +353,19 @@ struct Split<VT_Q6_K> {  // even-offset super-blocks
         VH_DEV float operator[](int i) const { return p[32 * (i >> 3) + (i & 7)]; }
     };
     static VH_DEV XRow xrow(const float *x, int it) { return XRow{x + col0(it)}; }
+    static VH_DEV int col(int it, int i) { return col0(it) + 32 * (i >> 3) + (i & 7); }
 };
+
+// Inputs from a row held in LDS with one pad float after every 32 (element c
+// at c + c/32), which spreads the items that a wave reads at once over
+// different banks.
+template <int T>
+struct XPadded {
+    const float *p;
+    int it;
+    VH_DEV float operator[](int i) const {
+        const int c = Split<T>::col(it, i);
+        return p[c + (c >> 5)];
+    }
+};
+VH_DEV int padded_len(int n) { return n + (n >> 5); }

@@ -78,21 +78,22 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     }
 }
 
-// one wave per token
-__global__ void __launch_bounds__(64) route_finish_kernel(const RoutePart *__restrict__ parts,
-                                                          const float *__restrict__ R, const float *__restrict__ hb,
-                                                          const float *__restrict__ bias, int d, int E, int k,
-                                                          int renorm, int exact, int32_t *__restrict__ idx,
-                                                          float *__restrict__ w, uint32_t *__restrict__ flags,
-                                                          float *__restrict__ probs) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const TopK tk = route_topk(parts + size_t(t) * E, R, hb + size_t(t) * d, bias, d, E, k, renorm, exact != 0,
-                               probs ? probs + size_t(t) * E : nullptr);
-    if (lane < k) {
-        idx[size_t(t) * k + lane] = tk.sel;
-        w[size_t(t) * k + lane] = tk.w;
+// one 256-thread workgroup per token
+__global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__restrict__ parts,
+                                                           const float *__restrict__ R, const float *__restrict__ hb,
+                                                           const float *__restrict__ bias, int d, int E, int k,
+                                                           int renorm, int exact, int32_t *__restrict__ idx,
+                                                           float *__restrict__ w, uint32_t *__restrict__ flags,
+                                                           float *__restrict__ probs) {
+    __shared__ TopKSmem sm;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    route_topk_block(sm, parts + size_t(t) * E, R, hb + size_t(t) * d, bias, d, E, k, renorm, exact != 0,
+                     probs ? probs + size_t(t) * E : nullptr);
+    if (tid < k) {
+        idx[size_t(t) * k + tid] = sm.sel[tid];
+        w[size_t(t) * k + tid] = sm.sel_w[tid];
     }
-    if (lane == 0 && flags) flags[t] = tk.flag;
+    if (tid == 0 && flags) flags[t] = sm.flag;
 }
 
 }  // namespace
@@ -115,7 +116,7 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
                     hipStream_t s) {
-    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(64), 0, s, parts, R, hb, bias, d, E, k, renorm,
+    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(256), 0, s, parts, R, hb, bias, d, E, k, renorm,
                        exact ? 1 : 0, idx, w, flags, probs);
     return vh_check(hipGetLastError());
 }

@@ -11,15 +11,22 @@ int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, con
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
                     hipStream_t s);
 
+// What the decode gate/up kernel hands to the down kernel: the chosen experts'
+// down matrices (NULL for an unregistered expert) and weights, in selection order.
+struct DecodePlan {
+    const void *down[64];
+    float w[64];
+};
+
 // Decode path (one token): gate/up with the top-k fused in, then down + combine.
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
-                     uint32_t *flags, hipStream_t s);
+                     uint32_t *flags, DecodePlan *plan, hipStream_t s);
 bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
-// Down projection + weighted combine + residual for T tokens (each token's
-// k experts in selection order): x[t] += sum_j w[t][j] * down_{idx[t][j]} h[t*k+j].
-int vh_down_combine(uint32_t type, const int32_t *idx, const float *w, const void *const *table, const float *h,
-                    int d, int fe, int k, int T, float *x, hipStream_t s);
+// Down projection + weighted combine + residual for one token:
+// x += sum_j plan.w[j] * down_j h[j], in selection order.
+int vh_down_combine(uint32_t type, const DecodePlan *plan, const float *h, int d, int fe, int k, float *x,
+                    hipStream_t s);
 bool vh_down_combine_supported(uint32_t type, int d, int fe, int k);
 
 // Grouped path (any number of tokens): dispatch, grouped gate/up, grouped
