@@ -1,0 +1,88 @@
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch  # noqa: F401  first, so the library binds to the same HIP runtime as torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HERE = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, HERE):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+GOLDEN = os.path.join(HERE, "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "slow: full-size parity cases")
+
+
+def _ensure_built():
+    """Build what the tests load when it is absent (a fresh checkout): the
+    oracle with make, the HIP library with vireo_amd.build. Where the built
+    files are present (the usual case, and always on a GPU machine) nothing
+    is rebuilt here."""
+    if not os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle"), "oracle"], check=True,
+                       stdout=subprocess.DEVNULL)
+    if not os.path.exists(os.path.join(ROOT, "vireo_amd", "libvireo_hip.so")):
+        from vireo_amd import build
+        build.build()
+
+
+_ensure_built()
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle.oracle import Oracle
+    return Oracle()
+
+
+@pytest.fixture(scope="session")
+def lib():
+    from vireo_amd import _lib
+    return _lib.load()
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def gpu_available():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+@pytest.fixture(scope="session")
+def cuda():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    from vireo_amd import _lib
+    _lib.check(_lib.load().vireo_hip_init(0), "vireo_hip_init")
+    return torch.device("cuda:0")
+
+
+def d2h(ptr, nbytes):
+    """Copy nbytes at a raw device address to a host uint8 array."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    out = np.empty(nbytes, np.uint8)
+    rc = hip.hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr), C.c_size_t(nbytes), 2)
+    assert rc == 0, f"hipMemcpy failed: {rc}"
+    return out
+
+
+def expert_lists(shape, g, u, d):
+    """Split stacked expert tensors into per-expert byte arrays."""
+    gs, us, ds = shape.slice_bytes()
+    E = shape.E
+    return ([g[e * gs:(e + 1) * gs] for e in range(E)], [u[e * us:(e + 1) * us] for e in range(E)],
+            [d[e * ds:(e + 1) * ds] for e in range(E)])

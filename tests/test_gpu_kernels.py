@@ -1,0 +1,79 @@
+"""qmatvec / qdequant_rows / rmsnorm / argmax on the GPU against the oracle,
+the golden vectors and the rigorous error bound of an fp32 dot product."""
+import numpy as np
+import pytest
+import torch
+
+import qformats as Q
+from conftest import golden
+from vireo_amd import moe as M
+from vireo_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+U24 = 2.0 ** -24
+
+CASES = [(W.Q8_0, 2048, 768), (W.Q8_0, 96, 33), (W.Q4_K, 2048, 768), (W.Q6_K, 768, 2048), (W.Q6_K, 1024, 37),
+         (W.Q5_0, 1024, 64), (W.F16, 300, 16), (W.F32, 2048, 128), (W.Q4_K, 256, 1)]
+
+
+def _weights(typ, n, d, seed):
+    if typ == W.F32:
+        return W.host_normal(n * d, seed, 3, sigma=0.02).view(np.uint8)
+    if typ == W.F16:
+        return W.host_normal(n * d, seed, 3).astype(np.float16).view(np.uint8)
+    return W.host_matrix(typ, n, 0, d, seed, 3)
+
+
+@pytest.mark.parametrize("typ,n,d", CASES)
+def test_qmatvec(cuda, oracle, typ, n, d):
+    w = _weights(typ, n, d, seed=n + d)
+    x = W.host_normal(n, 5, 6)
+    wt = torch.from_numpy(w).to(cuda)
+    y = torch.empty(d, dtype=torch.float32, device=cuda)
+    M.qmatvec(y, torch.from_numpy(x).to(cuda), wt, typ, n, d)
+    yg = y.cpu().numpy().astype(np.float64)
+    wd = Q.decode(typ, w, n).astype(np.float64)
+    exact = wd @ x.astype(np.float64)
+    bound = (n + 2) * U24 * (np.abs(wd) @ np.abs(x.astype(np.float64))) + 1e-30
+    assert np.all(np.abs(yg - exact) <= bound)
+    yo = oracle.matmul(typ, w if typ != W.F32 else w.view(np.float32), x, n, d)
+    assert np.abs(yg - yo).max() <= 2e-3 * np.abs(yo).max()
+
+
+@pytest.mark.parametrize("typ,n,rows", [(W.Q8_0, 2048, 16), (W.Q4_K, 2048, 16), (W.Q6_K, 768, 16), (W.Q5_0, 512, 8),
+                                        (W.F16, 300, 4), (W.F32, 64, 4)])
+def test_dequant_bit_exact(cuda, oracle, typ, n, rows):
+    w = _weights(typ, n, rows, seed=11)
+    out = M.dequant_rows(typ, torch.from_numpy(w).to(cuda), n, rows).cpu().numpy()
+    rb = w.size // rows
+    want = np.stack([oracle.dequant_row(typ, w[i * rb:(i + 1) * rb], n) for i in range(rows)])
+    np.testing.assert_array_equal(out, want)
+
+
+def test_golden_kernels_on_gpu(cuda):
+    g = golden("kernels.npz")
+    for tag in ("Q8_0_512x16", "Q8_0_96x5", "Q4_K_512x16", "Q6_K_512x16", "Q6_K_768x6", "Q5_0_512x16"):
+        tname, dims = tag.rsplit("_", 1)
+        n, d = map(int, dims.split("x"))
+        typ = {"Q8_0": W.Q8_0, "Q4_K": W.Q4_K, "Q6_K": W.Q6_K, "Q5_0": W.Q5_0}[tname]
+        wt = torch.from_numpy(g[f"{tag}_w"].view(np.uint8)).to(cuda)
+        np.testing.assert_array_equal(M.dequant_rows(typ, wt, n, d).cpu().numpy(), g[f"{tag}_deq"])
+        y = torch.empty(d, dtype=torch.float32, device=cuda)
+        M.qmatvec(y, torch.from_numpy(g[f"{tag}_x"]).to(cuda), wt, typ, n, d)
+        want = g[f"{tag}_y"]
+        assert np.abs(y.cpu().numpy() - want).max() <= 2e-3 * np.abs(want).max()
+
+
+def test_rmsnorm(cuda, oracle):
+    x = W.host_normal(4 * 2048, 1, 1).reshape(4, 2048) * np.float32(3)
+    w = W.host_normal(2048, 2, 2)
+    out = M.rmsnorm(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), 1e-6).cpu().numpy()
+    for r in range(4):
+        np.testing.assert_allclose(out[r], oracle.rmsnorm(x[r], w, 1e-6), rtol=2e-5, atol=1e-6)
+
+
+def test_argmax_first_max(cuda, oracle):
+    v = W.host_normal(151936, 3, 3)
+    v[100000] = v[7] = v.max() + 1  # tie: the first index wins, as in the reference's strict '>' scan
+    got = int(M.argmax(torch.from_numpy(v).to(cuda)).cpu()[0])
+    assert got == 7 == oracle.argmax(v)

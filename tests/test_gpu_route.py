@@ -1,0 +1,98 @@
+"""moe_route and moe_dispatch on the GPU: the chosen experts bit-exact with
+the oracle (the reference picks by its own fp32 logits with a strict '>'
+scan, src/gguf_run.c:189-191), including exactly tied experts, Zipf-biased
+routers and the prefill path; dispatch against a stable sort."""
+import numpy as np
+import pytest
+import torch
+
+from vireo_amd import moe as M
+from vireo_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+FALLBACK, NEAR_TIE = 1, 2
+
+
+def oracle_route(oracle, shape, router, hb, bias=None):
+    """Per-token (idx, w, probs) as moe_ffn computes them."""
+    T = hb.shape[0]
+    idx = np.empty((T, shape.k), np.int32)
+    w = np.empty((T, shape.k), np.float32)
+    probs = np.empty((T, shape.E), np.float32)
+    for t in range(T):
+        lg = oracle.matmul(W.F32, router, hb[t], shape.d, shape.E)
+        if bias is not None:
+            lg = (lg + bias).astype(np.float32)
+        p = oracle.softmax(lg)
+        probs[t] = p
+        idx[t], w[t] = oracle.topk(p, shape.k, shape.renorm)
+    return idx, w, probs
+
+
+@pytest.mark.parametrize("name,T", [("qwen3-30b-a3b-q4_k_m", 1), ("qwen3-30b-a3b-q4_k_m", 37),
+                                    ("olmoe-q8_0", 1), ("olmoe-q8_0", 16), ("qwen3-30b-a3b-q8_0", 64),
+                                    ("olmoe-q4_k_m", 130)])
+def test_route_matches_oracle(cuda, oracle, name, T):
+    shape = W.SHAPES[name]
+    m = M.DeviceMoE(shape, 1, seed=41)
+    x, hb = W.host_hidden(shape.d, T, 41)
+    idx, w, flags, probs = m.route(0, torch.from_numpy(hb).to(cuda), want_probs=True)
+    oi, ow, op = oracle_route(oracle, shape, m.host_router(0), hb)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(probs.cpu().numpy(), op, rtol=1e-5, atol=1e-8)
+    fl = flags.cpu().numpy()
+    assert not np.any(fl & NEAR_TIE)
+    if T >= 64:  # prefill: exact sequential logits, never a fallback
+        assert not np.any(fl & FALLBACK)
+    m.close()
+
+
+def test_route_exact_ties(cuda, oracle):
+    """Experts with identical router rows tie exactly; the lowest index wins."""
+    shape = W.SHAPES["olmoe-q8_0"]
+    m = M.DeviceMoE(shape, 1, seed=43)
+    r = m.routers[0]
+    for a, b in ((5, 9), (9, 40), (12, 13), (60, 2)):
+        r[b].copy_(r[a])
+    x, hb = W.host_hidden(shape.d, 24, 43)
+    router = m.host_router(0)
+    # make the tied rows win for some tokens: align a token with expert 5's row
+    hb[0] = router[5] / np.linalg.norm(router[5]) * np.sqrt(shape.d)
+    hb[1] = router[12] / np.linalg.norm(router[12]) * np.sqrt(shape.d)
+    for T in (1, 24, 64):
+        h = np.concatenate([hb] * 3)[:T] if T > 24 else hb[:T]
+        idx, w, flags, _ = m.route(0, torch.from_numpy(np.ascontiguousarray(h)).to(cuda))
+        oi, ow, _ = oracle_route(oracle, shape, router, h)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+        np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5)
+        assert flags.cpu().numpy()[0] & NEAR_TIE  # a tie inside or at the edge of the top-k is reported
+    got = idx.cpu().numpy()
+    assert 5 in got[0] and 9 in got[0]
+    m.close()
+
+
+def test_route_zipf_bias(cuda, oracle):
+    shape = W.SHAPES["qwen3-30b-a3b-q8_0"]
+    bias = W.zipf_bias(shape.E, 1.1, seed=3)
+    m = M.DeviceMoE(shape, 1, seed=44, logit_bias=bias)
+    x, hb = W.host_hidden(shape.d, 200, 44)
+    idx, w, flags, _ = m.route(0, torch.from_numpy(hb).to(cuda))
+    oi, ow, _ = oracle_route(oracle, shape, m.host_router(0), hb, bias)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5)
+    counts = np.bincount(oi.reshape(-1), minlength=shape.E)
+    assert counts.max() > 4 * np.median(counts)  # the bias skews the load
+    m.close()
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (7, 8, 64), (2048, 8, 128), (300, 1, 256), (33, 4, 8)])
+def test_dispatch_is_a_stable_sort(cuda, T, k, E):
+    rng = np.random.default_rng(T * k + E)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    counts, offs, perm = M.dispatch(torch.from_numpy(idx).to(cuda), E)
+    flat = idx.reshape(-1)
+    np.testing.assert_array_equal(counts.cpu().numpy(), np.bincount(flat, minlength=E))
+    np.testing.assert_array_equal(offs.cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]))
+    np.testing.assert_array_equal(perm.cpu().numpy(), np.argsort(flat, kind="stable"))

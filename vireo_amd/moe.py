@@ -34,7 +34,8 @@ class DeviceMoE:
     without a copy, and moe_ffn_forward pins each layer's leases on first use.
     """
 
-    def __init__(self, shape, n_layers=1, seed=1234, logit_bias=None, device="cuda", layer_seeds=None):
+    def __init__(self, shape, n_layers=1, seed=1234, logit_bias=None, device="cuda", layer_seeds=None,
+                 unregistered=()):
         self.lib = _lib.load()
         self.shape, self.n_layers, self.seed = shape, n_layers, seed
         self.layer_seeds = layer_seeds or [(seed, l) for l in range(n_layers)]
@@ -68,6 +69,8 @@ class DeviceMoE:
         for l in range(n_layers):
             off = l * self.layer_bytes
             for e in range(E):
+                if (l, e) in unregistered:  # its lookups fail, as for an expert missing from the file
+                    continue
                 sl = _lib.ExpertSlices(off + e * gs, off + E * gs + e * us, off + E * (gs + us) + e * ds, gs, us, ds)
                 self.lib.expert_store_register(self.es, l, e, C.byref(sl))
         # tensors and the model struct the C-ABI reads
