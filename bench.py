@@ -1,0 +1,259 @@
+#!/usr/bin/env python3
+"""Throughput of the quantized MoE-FFN layer on one MI355X.
+
+Default workload: a Qwen3-30B-A3B-shaped MoE layer (d=2048, 128 experts,
+top-8 renormalised, expert intermediate 768, gate/up Q4_K, down Q6_K, F32
+router) at decode batch 1. A step is one moe_ffn_forward call on one token.
+Steps rotate over --layers distinct layers (different routers and experts,
+all resident in HBM through the ExpertStore) and every step has its own
+token, so the routed weights stream from HBM rather than from the 256 MB
+last-level cache. The K timed steps are one HIP-graph replay bracketed by
+events on the launch stream.
+
+The roofline object is for the dominant kernel, the decode plan's fused
+top-k + gate/up SwiGLU (stage 1 of moe_decode_stage): the same kernel is
+launched alone over per-(layer, token) states in a second graph, and its
+average duration is that graph's event time / launches.
+
+cpu_baseline times the reference's own moe_ffn (compiled from its sources
+into oracle/_ref) on a bounded sample of the same workload on the host
+cores, or the oracle's restatement where that library is absent.
+
+Other workloads (--workload) print the same JSON schema: OLMoE shapes,
+batched decode and 2048-token prefill.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer decode tok/s + achieved HBM GB/s (% of peak); prefill tok/s"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (shape, tokens per step, layers rotated, router logit bias)
+    "qwen3-q4km-decode-b1": ("qwen3-30b-a3b-q4_k_m", 1, 32, False),
+    "qwen3-q4km-decode-b32": ("qwen3-30b-a3b-q4_k_m", 32, 8, False),
+    "olmoe-q8_0-decode-b1": ("olmoe-q8_0", 1, 24, False),
+    "olmoe-q4km-decode-b1": ("olmoe-q4_k_m", 1, 32, False),
+    "olmoe-q4km-decode-b4": ("olmoe-q4_k_m", 4, 16, False),
+    "olmoe-q4km-decode-b16": ("olmoe-q4_k_m", 16, 8, False),
+    "qwen3-q8_0-prefill-2048": ("qwen3-30b-a3b-q8_0", 2048, 2, True),
+}
+DEFAULT = "qwen3-q4km-decode-b1"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def alg_bytes_layer(shape, idx, B):
+    """Router + distinct routed experts' slices + activations (x in/out, hb)."""
+    distinct = len(np.unique(idx.reshape(-1)))
+    return shape.E * shape.d * 4 + distinct * shape.expert_bytes() + 3 * B * shape.d * 4, distinct
+
+
+def alg_bytes_gateup(shape):
+    """Stage 1 for one token: k experts' gate and up slices, hb, the router
+    parts and expert table it reads, the k x fe activations it writes."""
+    gs, us, _ = shape.slice_bytes()
+    return shape.k * (gs + us) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + shape.k * shape.fe * 4
+
+
+def cpu_baseline(shape, B, seed, seconds):
+    """The reference's moe_ffn on the host: tokens one at a time, as the
+    reference runs them (it has no batched path)."""
+    from vireo_amd import workloads as W
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    g, u, d = W.host_layer(shape, 0, seed)
+    router = W.host_router(shape, 0, seed)
+    warm, n_max = 48, 4096
+    x, hb = W.host_hidden(shape.d, warm + n_max, seed, stream=W.stream_id(0, W.KIND_HIDDEN) + 7)
+    from oracle.oracle import Reference, RefMoE, Oracle
+    if Reference.available():
+        rm = RefMoE(Reference(), shape, [router], [g], [u], [d])
+        run = lambda t: rm.run(0, x[t:t + 1], hb[t:t + 1])  # noqa: E731
+        kind = "reference"
+    else:
+        o = Oracle()
+        gs, us, ds = shape.slice_bytes()
+        G = [g[e * gs:(e + 1) * gs] for e in range(shape.E)]
+        U = [u[e * us:(e + 1) * us] for e in range(shape.E)]
+        D = [d[e * ds:(e + 1) * ds] for e in range(shape.E)]
+        run = lambda t: o.moe_ffn(shape, router, G, U, D, x[t:t + 1], hb[t:t + 1])  # noqa: E731
+        rm = None
+        kind = "port"
+    for t in range(warm):  # page every expert the sample will touch into RAM
+        run(t)
+    n, t0 = 0, time.perf_counter()
+    while n < n_max and (time.perf_counter() - t0 < seconds or n < 5):
+        run(warm + n)
+        n += 1
+    dt = time.perf_counter() - t0
+    if rm is not None:
+        rm.close()
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{n} single-token {shape.name} MoE-layer calls (one layer, weights warm in RAM after "
+                      f"{warm} untimed tokens), {dt:.1f} s, OpenMP threads={threads}",
+            "us_per_layer": round(dt / n * 1e6, 1)}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the MoE path here is built and timed on a single MI355X "
+              f"(no collectives, no sharding); --gpus {args.gpus} / WORLD_SIZE {world} is not supported.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vireo_amd import _lib
+    from vireo_amd import moe as M
+    from vireo_amd import workloads as W
+
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    dev = torch.device("cuda:0")
+    shape_name, B, L, biased = WORKLOADS[args.workload]
+    L = args.layers or L
+    shape = W.SHAPES[shape_name]
+    K = args.steps or (48 * L if B < 64 else 8 * L)
+    Wm = args.warmup if args.warmup is not None else L
+    bias = W.zipf_bias(shape.E, 1.1, seed=args.seed) if biased else None
+    print(f"[bench] {args.workload}: building {L} layers of {shape.name} on the GPU", file=sys.stderr, flush=True)
+    m = M.DeviceMoE(shape, L, seed=args.seed, logit_bias=bias)
+
+    n_tok = K if B == 1 else min(K, 4 * L) * B  # a distinct token per step for decode
+    x0, hb0 = W.host_hidden(shape.d, min(n_tok, 4096), args.seed, stream=W.stream_id(0, W.KIND_HIDDEN) + 1)
+    reps = (n_tok + x0.shape[0] - 1) // x0.shape[0]
+    hb_all = torch.from_numpy(np.tile(hb0, (reps, 1))[:n_tok]).to(dev)
+    x_all = torch.from_numpy(np.tile(x0, (reps, 1))[:n_tok]).to(dev)
+    steps_tok = n_tok // B
+
+    def step(i, x=x_all, hb=hb_all):
+        j = i % steps_tok
+        m.forward(i % L, x[j * B:(j + 1) * B], hb[j * B:(j + 1) * B])
+
+    for l in range(L):  # pin every layer and size the workspace outside the timed graph
+        step(l)
+    for i in range(Wm):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(K):
+            step(i)
+    torch.cuda.synchronize()
+    g.replay()  # untimed replay: first-launch costs of the graph
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    ms_per_step = ms / K
+    value = K * B / (ms / 1e3)
+
+    # routing of one pass, for the algorithmic byte count
+    idx, _ = m.forward(0, x_all[:B].clone(), hb_all[:B], return_routing=True)
+    lb, distinct = alg_bytes_layer(shape, idx.cpu().numpy(), B)
+    layer_gbs = lb / (ms_per_step / 1e3) / 1e9
+
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{shape.name} MoE layer, {'prefill' if B > 64 else 'decode'} batch {B}",
+                   "d": shape.d, "experts": shape.E, "top_k": shape.k, "ffn_exp": shape.fe,
+                   "renorm": shape.renorm, "types": [W.TYPE_NAMES[t] for t in (shape.gate_type, shape.up_type,
+                                                                                shape.down_type)],
+                   "tokens_per_step": B, "layers_rotated": L, "router_bias": "log Zipf(1.1)" if biased else None},
+        "us_per_layer": round(ms_per_step * 1e3, 3),
+        "layer_alg_bytes": int(lb), "distinct_experts": int(distinct),
+        "layer_GBps": round(layer_gbs, 1), "layer_frac_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
+    }
+
+    if B == 1 and lib.moe_decode_state_bytes(M.C.byref(m.model)) > 0:
+        result.update(decode_stage_roofline(m, shape, L, x_all, hb_all, dev))
+    else:
+        result["roofline"] = {"kernel": "moe_ffn_forward (all kernels of the layer)", "bound": "hbm",
+                              "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": None}
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(shape, B, args.seed, args.cpu_seconds)
+    m.close()
+    print(json.dumps(result), flush=True)
+
+
+def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
+    """Time each decode stage alone over NS distinct (layer, token) states and
+    price the dominant one (stage 1) against HBM."""
+    import torch
+    NS = 8 * L
+    states = [m.decode_state() for _ in range(NS)]
+    idx = torch.empty((NS, shape.k), dtype=torch.int32, device=dev)
+    w = torch.empty((NS, shape.k), dtype=torch.float32, device=dev)
+    x = x_all[:NS].clone()
+    hb = hb_all[:NS]
+
+    def launch(stage, j):
+        m.decode_stage(j % L, stage, x[j], hb[j], states[j], idx[j], w[j])
+
+    times = {}
+    for stage in (0, 1, 2):
+        for j in range(NS):  # eager pass: fills every state for the next stage
+            launch(stage, j)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for j in range(NS):
+                launch(stage, j)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times[stage] = e0.elapsed_time(e1) * 1e3 / NS  # us per launch
+    nb = alg_bytes_gateup(shape)
+    gbs = nb / (times[1] * 1e-6) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"traffic_decode_gateup_{shape.name}.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {
+        "roofline": {"kernel": "decode_gateup_kernel (top-k + gate/up SwiGLU, stage 1)", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "alg_bytes_per_launch": nb,
+                     "avg_launch_us": round(times[1], 3), "launches": NS},
+        "stages_us": {"route": round(times[0], 3), "topk_gateup": round(times[1], 3),
+                      "down_combine": round(times[2], 3)},
+    }
+
+
+if __name__ == "__main__":
+    main()

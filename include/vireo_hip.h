@@ -134,6 +134,23 @@ int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *
  * decode plan whenever it applies, 2 = always the grouped plan. */
 int vireo_hip_set_path(int path);
 
+/* The one-token decode plan of moe_ffn_forward as three separate launches
+ * over a caller-owned device `state` buffer of moe_decode_state_bytes(m)
+ * bytes (no counterpart in the reference, whose moe_ffn is one function):
+ *   stage 0  router logits of hb into state
+ *   stage 1  top-k, then the chosen experts' gate/up SwiGLU into state;
+ *            idx_out / w_out (optional, k entries) receive the routing
+ *   stage 2  down projections, weighted combine in selection order, x += ...
+ * Running 0, 1, 2 in order gives moe_ffn_forward's result for one token bit
+ * for bit. Stages 1 and 2 read only what the previous stage left in state, so
+ * one state per (layer, token) lets a caller (a profiler, a scheduler that
+ * interleaves other work) launch and time each stage on its own.
+ * moe_decode_state_bytes returns -EINVAL when the model's shapes or types
+ * have no decode plan (moe_ffn_forward then always uses the grouped plan). */
+int64_t moe_decode_state_bytes(const vireo_moe_model *m);
+int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, float *x, const float *hb, void *state,
+                     int32_t *idx_out, float *w_out, void *stream);
+
 /* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
 
 /* A store whose backing "file" is already in device memory (dev_base, size

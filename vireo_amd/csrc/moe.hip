@@ -76,7 +76,79 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     return 0;
 }
 
+bool decode_supported(const vireo_moe_model *m, int layer) {
+    const vireo_moe_layer &L = m->layers[layer];
+    if (!L.gate_exps || !L.up_exps || !L.down_exps) return false;
+    const uint32_t tg = L.gate_exps->ggml_type, tu = L.up_exps->ggml_type, td = L.down_exps->ggml_type;
+    return tg == tu && vh_decode_gateup_supported(tg, m->dim, m->ffn_exp) &&
+           vh_down_combine_supported(td, m->dim, m->ffn_exp, m->n_used);
+}
+
+// Where the decode stages keep what they hand to each other.
+struct DecodeState {
+    RoutePart *parts;  // [E]
+    DecodePlan *plan;
+    float *h;          // [k x fe]
+    uint32_t *flags;   // [1]
+};
+
+size_t decode_state_layout(const vireo_moe_model *m, size_t off[4]) {
+    size_t o = 0;
+    off[0] = o; o += al256(size_t(m->n_experts) * sizeof(RoutePart));
+    off[1] = o; o += al256(sizeof(DecodePlan));
+    off[2] = o; o += al256(size_t(m->n_used) * m->ffn_exp * sizeof(float));
+    off[3] = o; o += al256(sizeof(uint32_t));
+    return o;
+}
+
+int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *const *table, float *x,
+                 const float *hb, const DecodeState &st, int32_t *idx, float *w, hipStream_t s) {
+    const vireo_moe_layer &L = m->layers[layer];
+    const float *R = static_cast<const float *>(L.router->data);
+    const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
+    switch (stage) {
+    case 0: return vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, st.parts, s);
+    case 1:
+        return vh_decode_gateup(L.gate_exps->ggml_type, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm,
+                                table, st.h, idx, w, st.flags, st.plan, s);
+    case 2: return vh_down_combine(L.down_exps->ggml_type, st.plan, st.h, d, fe, k, x, s);
+    default: return -EINVAL;
+    }
+}
+
 }  // namespace
+
+extern "C" int64_t moe_decode_state_bytes(const vireo_moe_model *m) {
+    if (check_model(m, 0) || !decode_supported(m, 0)) return -EINVAL;
+    size_t off[4];
+    return int64_t(decode_state_layout(m, off));
+}
+
+extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, float *x, const float *hb, void *state,
+                                int32_t *idx_out, float *w_out, void *stream) {
+    if (int rc = check_model(m, layer)) return rc;
+    if (!decode_supported(m, layer) || !state || !hb || stage < 0 || stage > 2) return -EINVAL;
+    if (stage == 2 && !x) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
+    if (!m->es) return -EINVAL;
+    const void *const *table = nullptr;
+    if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
+    size_t off[4];
+    decode_state_layout(m, off);
+    char *b = static_cast<char *>(state);
+    const DecodeState st{reinterpret_cast<RoutePart *>(b + off[0]), reinterpret_cast<DecodePlan *>(b + off[1]),
+                         reinterpret_cast<float *>(b + off[2]), reinterpret_cast<uint32_t *>(b + off[3])};
+    int32_t *idx = idx_out;
+    float *w = w_out;
+    Ws ws;
+    if (stage == 1 && (!idx || !w)) {  // the kernel always writes the routing somewhere
+        if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, false, false, &ws)) return rc;
+        if (!idx) idx = ws.idx;
+        if (!w) w = ws.w;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, decode_stage(m, layer, stage, table, x, hb, st, idx, w, s));
+}
 
 extern "C" int vireo_hip_set_path(int path) {
     if (path < 0 || path > 2) return -EINVAL;
@@ -128,18 +200,17 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     hipStream_t s = static_cast<hipStream_t>(stream);
     const float *R = static_cast<const float *>(L.router->data);
 
-    const bool decode = n_tokens == 1 && g_path != 2 && vh_decode_gateup_supported(tg, d, fe) &&
-                        vh_down_combine_supported(td, d, fe, k);
+    const bool decode = n_tokens == 1 && g_path != 2 && decode_supported(m, layer);
     Ws ws;
     if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
     if (decode) {
-        rc = vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, ws.parts, s);
-        if (!rc) rc = vh_decode_gateup(tg, ws.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, ws.h,
-                                       idx, w, ws.flags, ws.plan, s);
-        if (!rc) rc = vh_down_combine(td, ws.plan, ws.h, d, fe, k, x, s);
+        const DecodeState st{ws.parts, ws.plan, ws.h, ws.flags};
+        rc = 0;
+        for (int stage = 0; stage < 3 && !rc; stage++)
+            rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s);
         return vh_finish(s, rc);
     }
     const bool exact = n_tokens >= kExactRouteTokens;

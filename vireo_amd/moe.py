@@ -114,6 +114,19 @@ class DeviceMoE:
                                             _stream_handle(stream)), "moe_ffn_forward")
         return (idx, w) if return_routing else None
 
+    def decode_state(self):
+        """A device buffer for moe_decode_stage (one layer, one token)."""
+        nb = self.lib.moe_decode_state_bytes(C.byref(self.model))
+        if nb < 0:
+            raise _lib.VireoError(f"no decode plan for {self.shape.name}")
+        return torch.empty(int(nb), dtype=torch.uint8, device=self.buf.device)
+
+    def decode_stage(self, layer, stage, x, hb, state, idx=None, w=None, stream=None):
+        """One stage (0 route, 1 top-k + gate/up, 2 down + combine) of the
+        one-token decode plan over `state`."""
+        _lib.check(self.lib.moe_decode_stage(C.byref(self.model), layer, stage, _ptr(x), _ptr(hb), _ptr(state),
+                                             _ptr(idx), _ptr(w), _stream_handle(stream)), "moe_decode_stage")
+
     def stats(self):
         st = _lib.ExpertStats()
         self.lib.expert_store_stats(self.es, C.byref(st))
