@@ -162,3 +162,26 @@ def test_prefill_2048_zipf(cuda, oracle):
     xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
     check("prefill sample", x[sample], xt.cpu().numpy()[sample], xo, ig[sample], io)
     m.close()
+
+
+@pytest.mark.parametrize("name", ["qwen3-30b-a3b-q4_k_m", "olmoe-q8_0", "olmoe-q4_k_m"])
+def test_decode_stages_equal_forward(cuda, name):
+    """moe_decode_stage 0, 1, 2 over a caller-owned state gives
+    moe_ffn_forward's single-token result bit for bit."""
+    shape = W.SHAPES[name]
+    m = M.DeviceMoE(shape, 2, seed=57)
+    x, hb = W.host_hidden(shape.d, 1, 57)
+    hbt = torch.from_numpy(hb).to(cuda)
+    for layer in (1, 0):
+        xa = torch.from_numpy(x).to(cuda)
+        ia, wa = m.forward(layer, xa, hbt, return_routing=True)
+        xb = torch.from_numpy(x).to(cuda)
+        state = m.decode_state()
+        ib = torch.empty_like(ia)
+        wb = torch.empty_like(wa)
+        for stage in range(3):
+            m.decode_stage(layer, stage, xb[0], hbt[0], state, ib, wb)
+        np.testing.assert_array_equal(xb.cpu().numpy(), xa.cpu().numpy())
+        np.testing.assert_array_equal(ib.cpu().numpy(), ia.cpu().numpy())
+        np.testing.assert_array_equal(wb.cpu().numpy(), wa.cpu().numpy())
+    m.close()
