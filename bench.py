@@ -12,8 +12,9 @@ events on the launch stream.
 
 The roofline object is for the dominant kernel, the decode plan's fused
 top-k + gate/up SwiGLU (stage 1 of moe_decode_stage): the same kernel is
-launched alone over per-(layer, token) states in a second graph, and its
-average duration is that graph's event time / launches.
+launched alone over 8 x layers distinct (layer, token) states, and each
+launch's duration comes from HIP events that the dispatch itself records
+(moe_decode_stage_timed); the average of those durations prices it.
 
 cpu_baseline times the reference's own moe_ffn (compiled from its sources
 into oracle/_ref) on a bounded sample of the same workload on the host
@@ -54,7 +55,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS) + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -113,8 +114,38 @@ def cpu_baseline(shape, B, seed, seconds):
             "us_per_layer": round(dt / n * 1e6, 1)}
 
 
+def copy_calibration(args):
+    """A plain device-to-device copy of 512 MiB, the reference kernel whose
+    HBM counters (FETCH_SIZE, WRITE_SIZE) calibrate the traffic of the MoE
+    kernels, and a measure of the bandwidth a streaming kernel reaches."""
+    import torch
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    reps = args.steps or 20
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = 2 * n / (ms / 1e3) / 1e9
+    print(json.dumps({"metric": "device copy GB/s (read + write)", "value": round(gbs, 1), "unit": "GB/s",
+                      "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(ms, 4),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+                      "data": "synthetic", "config": {"workload": "copy 512 MiB", "bytes_read": n, "bytes_written": n},
+                      "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def main():
     args = parse()
+    if args.workload == "copy-512MiB":
+        return copy_calibration(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: the MoE path here is built and timed on a single MI355X "
@@ -139,7 +170,9 @@ def main():
     print(f"[bench] {args.workload}: building {L} layers of {shape.name} on the GPU", file=sys.stderr, flush=True)
     m = M.DeviceMoE(shape, L, seed=args.seed, logit_bias=bias)
 
-    n_tok = K if B == 1 else min(K, 4 * L) * B  # a distinct token per step for decode
+    # a distinct token per step for decode, and at least the 8 x layers tokens
+    # that the per-stage timing of the decode plan launches over
+    n_tok = max(K, 8 * L) if B == 1 else min(K, 4 * L) * B
     x0, hb0 = W.host_hidden(shape.d, min(n_tok, 4096), args.seed, stream=W.stream_id(0, W.KIND_HIDDEN) + 1)
     reps = (n_tok + x0.shape[0] - 1) // x0.shape[0]
     hb_all = torch.from_numpy(np.tile(hb0, (reps, 1))[:n_tok]).to(dev)
@@ -206,40 +239,28 @@ def main():
 
 
 def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
-    """Time each decode stage alone over NS distinct (layer, token) states and
-    price the dominant one (stage 1) against HBM."""
+    """Time each decode stage alone over NS distinct (layer, token) states:
+    moe_decode_stage_timed launches the stage back to back and reads every
+    launch's begin and end from HIP events recorded by the dispatch itself
+    (hipExtLaunchKernelGGL), the same timestamps a kernel trace reports.
+    The dominant kernel (stage 1, top-k + gate/up) is priced against HBM."""
     import torch
     NS = 8 * L
-    states = [m.decode_state() for _ in range(NS)]
+    if x_all.shape[0] < NS or hb_all.shape[0] < NS:
+        raise ValueError(f"stage timing needs {NS} token rows, have {x_all.shape[0]}")
+    states = m.decode_states(NS)
     idx = torch.empty((NS, shape.k), dtype=torch.int32, device=dev)
     w = torch.empty((NS, shape.k), dtype=torch.float32, device=dev)
     x = x_all[:NS].clone()
     hb = hb_all[:NS]
-
-    def launch(stage, j):
-        m.decode_stage(j % L, stage, x[j], hb[j], states[j], idx[j], w[j])
-
+    layers = [j % L for j in range(NS)]
     times = {}
     for stage in (0, 1, 2):
-        for j in range(NS):  # eager pass: fills every state for the next stage
-            launch(stage, j)
-        torch.cuda.synchronize()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            for j in range(NS):
-                launch(stage, j)
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        times[stage] = e0.elapsed_time(e1) * 1e3 / NS  # us per launch
+        us = m.decode_stage_timed(stage, layers, x, hb, states, idx, w)
+        times[stage] = (float(us.mean()), float(np.median(us)))
     nb = alg_bytes_gateup(shape)
-    gbs = nb / (times[1] * 1e-6) / 1e9
+    avg = times[1][0]
+    gbs = nb / (avg * 1e-6) / 1e9
     traffic = None
     tf = os.path.join(ROOT, "profiles", f"traffic_decode_gateup_{shape.name}.json")
     if os.path.exists(tf):
@@ -249,9 +270,9 @@ def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
         "roofline": {"kernel": "decode_gateup_kernel (top-k + gate/up SwiGLU, stage 1)", "bound": "hbm",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "alg_bytes_per_launch": nb,
-                     "avg_launch_us": round(times[1], 3), "launches": NS},
-        "stages_us": {"route": round(times[0], 3), "topk_gateup": round(times[1], 3),
-                      "down_combine": round(times[2], 3)},
+                     "avg_launch_us": round(avg, 3), "median_launch_us": round(times[1][1], 3), "launches": NS},
+        "stages_us": {"route": round(times[0][0], 3), "topk_gateup": round(times[1][0], 3),
+                      "down_combine": round(times[2][0], 3)},
     }
 
 

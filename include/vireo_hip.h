@@ -150,6 +150,16 @@ int vireo_hip_set_path(int path);
 int64_t moe_decode_state_bytes(const vireo_moe_model *m);
 int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, float *x, const float *hb, void *state,
                      int32_t *idx_out, float *w_out, void *stream);
+/* Profiling form of moe_decode_stage: launches `stage` n times back to back,
+ * launch i on layer layers[i] (host array) with token row i of x / hb
+ * (device [n x dim]), state i at states + i * state_stride (256-aligned,
+ * at least moe_decode_state_bytes) and routing row i of idx / w
+ * (device [n x n_used]). Each launch records its own begin and end on HIP
+ * events (hipExtLaunchKernelGGL, the dispatch's timestamps); the call waits
+ * for the last one and writes the n kernel durations in microseconds to
+ * us_out (host). Results are those of n moe_decode_stage calls. */
+int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n, const int *layers, float *x, const float *hb,
+                           void *states, int64_t state_stride, int32_t *idx, float *w, float *us_out, void *stream);
 
 /* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
 

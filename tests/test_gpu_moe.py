@@ -185,3 +185,32 @@ def test_decode_stages_equal_forward(cuda, name):
         np.testing.assert_array_equal(ib.cpu().numpy(), ia.cpu().numpy())
         np.testing.assert_array_equal(wb.cpu().numpy(), wa.cpu().numpy())
     m.close()
+
+
+@pytest.mark.parametrize("name", ["olmoe-q8_0", "qwen3-30b-a3b-q4_k_m"])
+def test_decode_plan_ties_take_the_exact_path(cuda, oracle, path, name):
+    """Exactly tied router rows inside and at the edge of the top-k: the
+    decode kernel's one-wave ranking cannot certify the order and the whole
+    workgroup re-ranks on exact logits; experts and output match the oracle."""
+    path(1)
+    shape = W.SHAPES[name]
+    m = M.DeviceMoE(shape, 1, seed=58)
+    r = m.routers[0]
+    x, hb = W.host_hidden(shape.d, 1, 58)
+    order = np.argsort(-(m.host_router(0) @ hb[0]), kind="stable")
+    for a, b in ((order[0], order[1]), (order[7], order[8]), (order[3], order[20])):
+        r[b].copy_(r[a])  # b now ties a exactly
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"{name} decode ties", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    np.testing.assert_allclose(w.cpu().numpy(), wo, rtol=1e-5)
+    state = m.decode_state()
+    ib, wb = torch.empty_like(idx), torch.empty_like(w)
+    xs = torch.from_numpy(x).to(cuda)
+    hbt = torch.from_numpy(hb).to(cuda)
+    for stage in range(3):
+        m.decode_stage(0, stage, xs[0], hbt[0], state, ib, wb)
+    flags = state[-256:].view(torch.int32)  # the flag word is the state's last 256-byte slot
+    assert int(flags[0].cpu()) & 2, "near tie not reported"
+    m.close()

@@ -1,10 +1,21 @@
 // Shared device helpers for the vireo-hip kernels (gfx950, wave64).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <errno.h>
 #include <stdint.h>
 
 #define VH_DEV __device__ __forceinline__
+
+// Events on which the next launch records its own begin and end (taken from
+// the dispatch itself by hipExtLaunchKernelGGL). Both are null except while
+// moe_decode_stage_timed times a launch.
+struct VhLaunchTiming {
+    hipEvent_t start, stop;
+};
+extern VhLaunchTiming g_vh_timing;
+#define VH_LAUNCH(K, G, B, SH, ST, ...) \
+    hipExtLaunchKernelGGL(K, G, B, SH, ST, g_vh_timing.start, g_vh_timing.stop, 0, __VA_ARGS__)
 
 enum { VT_F32 = 0, VT_F16 = 1, VT_Q4_0 = 2, VT_Q5_0 = 6, VT_Q8_0 = 8, VT_Q4_K = 12, VT_Q6_K = 14 };
 

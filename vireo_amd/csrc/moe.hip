@@ -10,6 +10,7 @@
 // The grouped plan reads each routed expert's weights once per call however
 // many tokens chose it.
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 #include <string.h>
 #include "common.h"
 #include "route_kernels.h"
@@ -128,6 +129,7 @@ extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, 
                                 int32_t *idx_out, float *w_out, void *stream) {
     if (int rc = check_model(m, layer)) return rc;
     if (!decode_supported(m, layer) || !state || !hb || stage < 0 || stage > 2) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(hb) & 15u) return -EINVAL;  // the decode kernels read hb in 16-byte units
     if (stage == 2 && !x) return -EINVAL;
     if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
     if (!m->es) return -EINVAL;
@@ -148,6 +150,51 @@ extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, 
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     return vh_finish(s, decode_stage(m, layer, stage, table, x, hb, st, idx, w, s));
+}
+
+extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n, const int *layers, float *x,
+                                      const float *hb, void *states, int64_t state_stride, int32_t *idx, float *w,
+                                      float *us_out, void *stream) {
+    if (int rc = check_model(m, 0)) return rc;
+    if (n <= 0 || !layers || !hb || !states || !idx || !w || !us_out || stage < 0 || stage > 2) return -EINVAL;
+    if (stage == 2 && !x) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(hb) & 15u || (m->dim * 4) & 15) return -EINVAL;
+    size_t off[4];
+    if (!decode_supported(m, 0) || state_stride < int64_t(decode_state_layout(m, off)) || (state_stride & 255) ||
+        (reinterpret_cast<uintptr_t>(states) & 255u))
+        return -EINVAL;
+    static hipEvent_t *ev = nullptr;
+    static int nev = 0;
+    if (2 * n > nev) {
+        hipEvent_t *ne = static_cast<hipEvent_t *>(realloc(ev, sizeof(hipEvent_t) * 2 * n));
+        if (!ne) return -ENOMEM;
+        ev = ne;
+        for (; nev < 2 * n; nev++)
+            if (int rc = vh_check(hipEventCreate(&ev[nev]))) return rc;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int d = m->dim, k = m->n_used;
+    int rc = 0;
+    for (int i = 0; i < n && !rc; i++) {
+        const int layer = layers[i];
+        if (layer < 0 || layer >= m->n_layers || !decode_supported(m, layer)) { rc = -EINVAL; break; }
+        const void *const *table = nullptr;
+        if ((rc = expert_store_pin_layer(m->es, layer, &table))) break;
+        char *b = static_cast<char *>(states) + i * state_stride;
+        const DecodeState st{reinterpret_cast<RoutePart *>(b + off[0]), reinterpret_cast<DecodePlan *>(b + off[1]),
+                             reinterpret_cast<float *>(b + off[2]), reinterpret_cast<uint32_t *>(b + off[3])};
+        g_vh_timing = {ev[2 * i], ev[2 * i + 1]};
+        rc = decode_stage(m, layer, stage, table, x ? x + size_t(i) * d : nullptr, hb + size_t(i) * d, st,
+                          idx + size_t(i) * k, w + size_t(i) * k, s);
+        g_vh_timing = {nullptr, nullptr};
+    }
+    if (!rc) rc = vh_check(hipEventSynchronize(ev[2 * n - 1]));
+    for (int i = 0; i < n && !rc; i++) {
+        float ms = 0.0f;
+        rc = vh_check(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+        us_out[i] = ms * 1000.0f;
+    }
+    return rc;
 }
 
 extern "C" int vireo_hip_set_path(int path) {
@@ -200,7 +247,8 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     hipStream_t s = static_cast<hipStream_t>(stream);
     const float *R = static_cast<const float *>(L.router->data);
 
-    const bool decode = n_tokens == 1 && g_path != 2 && decode_supported(m, layer);
+    const bool decode = n_tokens == 1 && g_path != 2 && decode_supported(m, layer) &&
+                        (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
     Ws ws;
     if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;

@@ -313,7 +313,11 @@ struct Split<VT_Q4_K> {  // 16-aligned super-blocks
         float dl = 0.0f, dh = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t lo = qw[i] & 0x0f0f0f0fu, hi = (qw[i] >> 4) & 0x0f0f0f0fu;
+            uint32_t lo = qw[i] & 0x0f0f0f0fu, hi = (qw[i] >> 4) & 0x0f0f0f0fu;
+            // keep the masked words as they are, so each byte below converts with
+            // one v_cvt_f32_ubyte{0..3} (otherwise the masks fold into bitfield
+            // extracts and every quant costs an extra instruction)
+            asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 dl = fmaf(float((lo >> (8 * k)) & 0xffu), x[4 * i + k], dl);
@@ -369,3 +373,133 @@ struct XPadded {
     }
 };
 VH_DEV int padded_len(int n) { return n + (n >> 5); }
+
+// ---------------------------------------------------------------- register-resident inputs
+// Decoders for kernels that keep an item's 32 inputs in registers (x[32], in the
+// item's own order as above) together with sums of runs of those inputs, so
+// per-run constants (Q4_K mins, the Q6_K offset of 32) are applied once per run
+// instead of once per weight:
+//   Q4_K  sums[0] = x[0..15], sums[1] = x[16..31] (the low- and high-nibble runs)
+//   Q6_K  sums[g] = x[8g .. 8g+7]
+//   Q8_0  no sums (an unpaired 34-byte block at an even offset)
+template <int T>
+struct Reg;
+
+// float4 loads of an item's inputs from a row vector; runs of R columns, RS apart.
+template <int RUNS, int R, int RS>
+VH_DEV void load_runs(const float *__restrict__ p, float (&x)[32]) {
+#pragma unroll
+    for (int g = 0; g < RUNS; g++)
+#pragma unroll
+        for (int i = 0; i < R / 4; i++) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + g * RS + 4 * i);
+            x[g * R + 4 * i + 0] = v.x;
+            x[g * R + 4 * i + 1] = v.y;
+            x[g * R + 4 * i + 2] = v.z;
+            x[g * R + 4 * i + 3] = v.w;
+        }
+}
+
+template <>
+struct Reg<VT_Q4_K> {
+    static constexpr int NS = 2;
+    using Raw = Split<VT_Q4_K>::Raw;
+    static __host__ __device__ int items(int n) { return n / 32; }
+    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) { return Split<VT_Q4_K>::fetch(base, row, it); }
+    static VH_DEV void load_x(const float *row, int it, float (&x)[32]) {
+        load_runs<2, 16, 32>(row + Split<VT_Q4_K>::col0(it), x);
+    }
+    static VH_DEV void sums(const float (&x)[32], float (&s)[NS]) {
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) { a += x[i]; b += x[16 + i]; }
+        s[0] = a;
+        s[1] = b;
+    }
+    static VH_DEV float compute(const Raw &r, int it, const float (&x)[32], const float (&s)[NS]) {
+        return Split<VT_Q4_K>::compute(r, it, x, s[0], s[1]);
+    }
+};
+
+// Q6_K: the four runs' 6-bit quants are assembled four to a word (one per byte)
+// and converted with v_cvt_f32_ubyte*; sum_i (q_i - 32) x_i is formed as
+// sum_i q_i x_i - 32 sum_i x_i.
+VH_DEV float q6k_compute_s(const Q6Raw &r, const float (&x)[32], const float (&sx)[4]) {
+    uint32_t t[4][2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t A = h ? r.a1 : r.a0, B = h ? r.b1 : r.b0, H = h ? r.h1 : r.h0;
+        t[0][h] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+        t[1][h] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+        t[2][h] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+        t[3][h] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+    }
+    asm volatile("" : "+v"(t[0][0]), "+v"(t[0][1]), "+v"(t[1][0]), "+v"(t[1][1]), "+v"(t[2][0]), "+v"(t[2][1]),
+                 "+v"(t[3][0]), "+v"(t[3][1]));
+    float s = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = fmaf(float((t[g][i >> 2] >> (8 * (i & 3))) & 0xffu), x[8 * g + i], acc);
+        s = fmaf(float(int(int8_t(r.sc >> (8 * g)))), fmaf(-32.0f, sx[g], acc), s);
+    }
+    return h2f(r.d) * s;
+}
+
+template <>
+struct Reg<VT_Q6_K> {
+    static constexpr int NS = 4;
+    using Raw = Q6Raw;
+    static __host__ __device__ int items(int n) { return n / 32; }
+    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) { return Split<VT_Q6_K>::fetch(base, row, it); }
+    static VH_DEV void load_x(const float *row, int it, float (&x)[32]) {
+        load_runs<4, 8, 32>(row + Split<VT_Q6_K>::col0(it), x);
+    }
+    static VH_DEV void sums(const float (&x)[32], float (&s)[NS]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) a += x[8 * g + i];
+            s[g] = a;
+        }
+    }
+    static VH_DEV float compute(const Raw &r, int, const float (&x)[32], const float (&s)[NS]) {
+        return q6k_compute_s(r, x, s);
+    }
+};
+
+template <>
+struct Reg<VT_Q8_0> {
+    static constexpr int NS = 1;
+    struct Raw { uint32_t w[9], s; };
+    static __host__ __device__ int items(int n) { return n / 32; }
+    // block it of the row at byte offset row (even): the aligned window from
+    // the dword holding its first byte; the last word is completed with a
+    // 16-bit load when the block starts 2 mod 4, so nothing past the block is read
+    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) {
+        const int64_t b = row + 34 * int64_t(it);
+        Raw r;
+        r.s = uint32_t(b) & 3u;
+        const uint8_t *a = base + (b - int64_t(r.s));
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.w[i] = ld_u32(a + 4 * i);
+        r.w[8] = ld_u16(a + 32) | (r.s ? (ld_u16(a + 34) << 16) : 0u);
+        return r;
+    }
+    static VH_DEV void load_x(const float *row, int it, float (&x)[32]) { load_runs<1, 32, 32>(row + 32 * it, x); }
+    static VH_DEV void sums(const float (&)[32], float (&s)[NS]) { s[0] = 0.0f; }
+    static VH_DEV float compute(const Raw &r, int, const float (&x)[32], const float (&)[NS]) {
+        const float d = h2f((r.w[0] >> (8 * r.s)) & 0xffffu);
+        const uint32_t sh = 16 + 8 * r.s;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = uint32_t(((uint64_t(r.w[i + 1]) << 32) | r.w[i]) >> sh);
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc = fmaf(float(int(int8_t(q >> (8 * k)))), x[4 * i + k], acc);
+        }
+        return acc * d;
+    }
+};

@@ -66,9 +66,33 @@ VH_DEV RoutePart route_row_part(const float *__restrict__ r, const float *__rest
 }
 
 // The reference logit exactly: a = 0; a += r[i]*x[i] for i in order, every
-// product and sum rounded to fp32.
+// product and sum rounded to fp32. The chain is sequential, so its speed is
+// set by keeping the operands in registers ahead of it: with 16-byte aligned
+// rows and d a multiple of 64, chunks of 64 elements are loaded one chunk
+// ahead of the chunk being summed.
 VH_DEV float exact_logit(const float *__restrict__ r, const float *__restrict__ x, int d) {
     float a = 0.0f;
+    if (((reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0 && d % 64 == 0) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(r), *x4 = reinterpret_cast<const float4 *>(x);
+        float4 rc[16], xc[16], rn[16], xn[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) { rc[i] = r4[i]; xc[i] = x4[i]; }
+        for (int c = 0; c < d / 64; c++) {
+            const int nxt = c + 1 < d / 64 ? c + 1 : c;
+#pragma unroll
+            for (int i = 0; i < 16; i++) { rn[i] = r4[16 * nxt + i]; xn[i] = x4[16 * nxt + i]; }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                a = __fadd_rn(a, __fmul_rn(rc[i].x, xc[i].x));
+                a = __fadd_rn(a, __fmul_rn(rc[i].y, xc[i].y));
+                a = __fadd_rn(a, __fmul_rn(rc[i].z, xc[i].z));
+                a = __fadd_rn(a, __fmul_rn(rc[i].w, xc[i].w));
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) { rc[i] = rn[i]; xc[i] = xn[i]; }
+        }
+        return a;
+    }
     for (int i = 0; i < d; i++) a = __fadd_rn(a, __fmul_rn(r[i], x[i]));
     return a;
 }
@@ -86,14 +110,14 @@ struct TopKSmem {
     int sel[64];                     // chosen experts in order
     float sel_w[64];                 // their weights
     double sel_lo[65], sel_hi[64];   // their intervals; sel_lo[64]: best remaining
-    float red[2][4];                 // per-wave partials
+    float red[2][8];                 // per-wave partials (up to 8 waves)
     float m;                         // max logit
     uint32_t flag;
     int uncertain;
 };
 
-// Top-k of one token by a 256-thread workgroup (all threads call it; E <= 256,
-// k <= 64). Thread e owns expert e. Its rank is the number of experts with a
+// Top-k of one token by a workgroup of 256 to 512 threads (all threads call
+// it; E <= 256, k <= 64). Thread e owns expert e. Its rank is the number of experts with a
 // larger key, so the k chosen experts and their order come out of one parallel
 // pass. The ranking is certified with the fp64 intervals; when any gap that
 // decides the set or its order is not wider than both bounds plus
@@ -120,7 +144,7 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     // keys): values that close can never be certified, so a wrong truncated
     // order always reaches the full-precision re-ranking below.
     const uint32_t key = mine ? ((ordered_u32(lg) & 0xffffff00u) | uint32_t(255 - tid)) : 0u;
-    sm.key[tid] = key;
+    if (tid < kMaxExperts) sm.key[tid] = key;
     if (tid == 0) { sm.uncertain = 0; sm.flag = 0; }
     __syncthreads();
     int rank = 1 << 30;
@@ -137,12 +161,14 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     }
     // the largest upper bound outside the chosen k, rounded up to fp32 (an
     // upper bound is all the certification needs)
+    const int nwaves = int(blockDim.x) >> 6;
     const float rest = (mine && rank >= k) ? __double2float_ru(hi) : -INFINITY;
     const float rw = wave_max_f(rest);
     if (lane == 0) sm.red[0][wv] = rw;
     __syncthreads();
     if (tid < k) {
-        const float rh = fmaxf(fmaxf(sm.red[0][0], sm.red[0][1]), fmaxf(sm.red[0][2], sm.red[0][3]));
+        float rh = sm.red[0][0];
+        for (int i = 1; i < nwaves; i++) rh = fmaxf(rh, sm.red[0][i]);
         const double next_hi = tid + 1 < k ? sm.sel_hi[tid + 1] : (k < E ? double(rh) : -INFINITY);
         if (!(sm.sel_lo[tid] - next_hi > (exact_parts ? 0.0 : kRouteMargin))) atomicOr(&sm.uncertain, 1);
         if (exact_parts && sm.sel_lo[tid] - next_hi < double(kNearTie)) atomicOr(&sm.flag, VIREO_ROUTE_NEAR_TIE);
@@ -159,7 +185,7 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
             if (bias) a = __fadd_rn(a, bias[tid]);
             lg = a;
         }
-        sm.key64[tid] = cand ? ((uint64_t(ordered_u32(lg)) << 8) | uint64_t(255 - tid)) : 0ull;
+        if (tid < kMaxExperts) sm.key64[tid] = cand ? ((uint64_t(ordered_u32(lg)) << 8) | uint64_t(255 - tid)) : 0ull;
         if (tid == 0) {
             // the near-tie verdict is taken again on the full-precision ranking
             sm.flag = exact_parts ? 0u : VIREO_ROUTE_EXACT_FALLBACK;
@@ -188,7 +214,8 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     const float part_sum = wave_sum_f(ex);
     if (lane == 0) sm.red[1][wv] = part_sum;
     __syncthreads();
-    const float s = (sm.red[1][0] + sm.red[1][1]) + (sm.red[1][2] + sm.red[1][3]);
+    float s = sm.red[1][0];
+    for (int i = 1; i < nwaves; i++) s += sm.red[1][i];
     if (mine) {
         if (probs) probs[tid] = ex / s;
         if (rank < k) sm.sel_w[rank] = ex / s;
@@ -201,4 +228,84 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
             for (int t = 0; t < k; t++) sm.sel_w[t] = sm.sel_w[t] / wsum;
     }
     __syncthreads();
+}
+
+// Top-k of one token by one wave (all 64 lanes active), for the fused decode
+// kernel: lane l holds the parts of experts l, l+64, l+128, l+192 (E <= 256).
+// k rounds of a wave-wide max over the 32-bit keys of route_topk_block (the
+// ordered fp32 image of the midpoint, low 8 bits 255 - e, so the lower id wins
+// a tie) give the chosen experts in order; each round's winner interval is
+// read from its owner lane and the order is certified on the fly: every chosen
+// lower bound must exceed the next upper bound (or, for the last, the best
+// upper bound left out) by kRouteMargin. Certified gaps exceed kNearTie, so
+// the flag is 0. Returns whether the order was certified (the same on every
+// lane); only then are sm.sel, sm.sel_w and sm.flag written, and the caller
+// must fall back to route_topk_block otherwise.
+VH_DEV bool route_topk_wave(TopKSmem &sm, const RoutePart (&p)[4], int E, int k, int renorm) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[4];
+    float lg[4];
+    int rank[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int e = lane + 64 * q;
+        const bool mine = e < E;
+        lg[q] = mine ? float(p[q].c) : -INFINITY;
+        key[q] = mine ? ((ordered_u32(lg[q]) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
+        rank[q] = -1;
+    }
+    bool ok = true;
+    double prev_lo = 0.0;
+    float m = 0.0f;
+    for (int t = 0; t < k; t++) {
+        uint32_t best = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (rank[q] < 0 && key[q] > best) best = key[q];
+        const uint32_t wb = wave_max_u(best);
+        const int e = 255 - int(wb & 0xffu), qw = e >> 6, owner = e & 63;
+        double c = 0.0, b = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (q == qw) {
+                c = p[q].c;
+                b = p[q].beta;
+                if (lane == owner) rank[q] = t;
+            }
+        }
+        c = readlane_d(c, owner);
+        b = readlane_d(b, owner);
+        if (t == 0) m = float(c);
+        else ok = ok && (prev_lo - (c + b) > kRouteMargin);
+        prev_lo = c - b;
+        if (lane == 0) sm.sel[t] = e;
+    }
+    float rest = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (rank[q] < 0 && key[q] != 0u) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
+    rest = wave_max_f(rest);
+    if (k < E) ok = ok && (prev_lo - double(rest) > kRouteMargin);
+    if (!ok) return false;
+    // softmax over all experts (src/gguf_run.c:181-182); m is the largest logit
+    float ex[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) ex[q] = key[q] != 0u ? expf(lg[q] - m) : 0.0f;
+    const float s = wave_sum_f((ex[0] + ex[1]) + (ex[2] + ex[3]));
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (rank[q] >= 0) sm.sel_w[rank[q]] = ex[q] / s;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+        sm.flag = 0u;
+        if (renorm) {
+            float wsum = 0.0f;
+            for (int t = 0; t < k; t++) wsum += sm.sel_w[t];  // in selection order (src/gguf_run.c:192)
+            if (wsum > 0.0f)
+                for (int t = 0; t < k; t++) sm.sel_w[t] = sm.sel_w[t] / wsum;
+        }
+    }
+    return true;
 }

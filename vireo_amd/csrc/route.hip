@@ -107,8 +107,8 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
         const bool fast = d == 2048 && (reinterpret_cast<uintptr_t>(R) & 15u) == 0 &&
                           (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
         dim3 g(E, T);
-        if (fast) hipLaunchKernelGGL(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
-        else hipLaunchKernelGGL(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
+        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
+        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
     }
     return vh_check(hipGetLastError());
 }

@@ -26,6 +26,8 @@ int cur_dev() {
 }
 }  // namespace
 
+VhLaunchTiming g_vh_timing = {nullptr, nullptr};
+
 int vh_check(hipError_t e) {
     if (e == hipSuccess) return 0;
     snprintf(g_err, sizeof g_err, "HIP error %d: %s", int(e), hipGetErrorString(e));

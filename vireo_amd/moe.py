@@ -25,6 +25,14 @@ def _ptr(t):
     return C.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _need(name, t, rows, cols, dtype=torch.float32):
+    """The library takes raw device pointers: check sizes on the host."""
+    if t is None or t.dtype != dtype or not t.is_cuda or not t.is_contiguous() or t.numel() < rows * cols or \
+            (t.dim() >= 1 and t.shape[-1] != cols and t.dim() > 1):
+        raise ValueError(f"{name}: need a contiguous {dtype} device tensor of at least [{rows} x {cols}], "
+                         f"got {None if t is None else (tuple(t.shape), t.dtype, t.device)}")
+
+
 class DeviceMoE:
     """n_layers MoE layers of `shape`, all experts resident in HBM.
 
@@ -95,6 +103,7 @@ class DeviceMoE:
     def route(self, layer, hb, stream=None, want_probs=False):
         T = hb.shape[0]
         k = self.shape.k
+        _need("hb", hb, T, self.shape.d)
         idx = torch.empty((T, k), dtype=torch.int32, device=hb.device)
         w = torch.empty((T, k), dtype=torch.float32, device=hb.device)
         flags = torch.empty(T, dtype=torch.int32, device=hb.device)
@@ -106,6 +115,8 @@ class DeviceMoE:
     def forward(self, layer, x, hb, stream=None, return_routing=False):
         """x[t] += moe(hb[t]) in place for every token t (moe_ffn_forward)."""
         T = hb.shape[0]
+        _need("hb", hb, T, self.shape.d)
+        _need("x", x, T, self.shape.d)
         idx = w = None
         if return_routing:
             idx = torch.empty((T, self.shape.k), dtype=torch.int32, device=hb.device)
@@ -124,8 +135,49 @@ class DeviceMoE:
     def decode_stage(self, layer, stage, x, hb, state, idx=None, w=None, stream=None):
         """One stage (0 route, 1 top-k + gate/up, 2 down + combine) of the
         one-token decode plan over `state`."""
+        d, k = self.shape.d, self.shape.k
+        _need("hb", hb, 1, d)
+        if stage == 2:
+            _need("x", x, 1, d)
+        for name, t, dt in (("idx", idx, torch.int32), ("w", w, torch.float32)):
+            if t is not None:
+                _need(name, t, 1, k, dt)
+        nb = self.lib.moe_decode_state_bytes(C.byref(self.model))
+        if state.numel() < nb or state.dtype != torch.uint8:
+            raise ValueError(f"state: need {nb} bytes")
         _lib.check(self.lib.moe_decode_stage(C.byref(self.model), layer, stage, _ptr(x), _ptr(hb), _ptr(state),
                                              _ptr(idx), _ptr(w), _stream_handle(stream)), "moe_decode_stage")
+
+    def decode_stage_timed(self, stage, layers, x, hb, states, idx, w, stream=None):
+        """Launch `stage` once per entry of `layers` (token row i of x/hb,
+        state i of the [n x stride] uint8 tensor `states`) back to back and
+        return each launch's kernel duration in microseconds."""
+        n = len(layers)
+        d, k = self.shape.d, self.shape.k
+        # the library sees raw pointers: every buffer must hold n rows
+        for name, t, cols in (("x", x, d), ("hb", hb, d), ("idx", idx, k), ("w", w, k)):
+            if t is None or t.dim() != 2 or t.shape[0] < n or t.shape[1] != cols or not t.is_contiguous():
+                raise ValueError(f"decode_stage_timed: {name} must be a contiguous [>= {n} x {cols}] tensor")
+        if states.dim() != 2 or states.shape[0] < n:
+            raise ValueError(f"decode_stage_timed: states must hold {n} states")
+        if any(not 0 <= l < self.n_layers for l in layers):
+            raise ValueError("decode_stage_timed: layer out of range")
+        lay = (C.c_int * n)(*layers)
+        us = (C.c_float * n)()
+        _lib.check(self.lib.moe_decode_stage_timed(C.byref(self.model), stage, n, lay, _ptr(x), _ptr(hb),
+                                                   _ptr(states), states.stride(0), _ptr(idx), _ptr(w), us,
+                                                   _stream_handle(stream)), "moe_decode_stage_timed")
+        return np.array(us[:], dtype=np.float64)
+
+    def decode_states(self, n):
+        """n decode states, one per row of a [n x stride] uint8 tensor."""
+        nb = self.lib.moe_decode_state_bytes(C.byref(self.model))
+        if nb < 0:
+            raise _lib.VireoError(f"no decode plan for {self.shape.name}")
+        stride = (int(nb) + 255) // 256 * 256
+        buf = torch.empty(n * stride + 256, dtype=torch.uint8, device=self.buf.device)
+        off = (-buf.data_ptr()) % 256
+        return buf[off:off + n * stride].view(n, stride)
 
     def stats(self):
         st = _lib.ExpertStats()
