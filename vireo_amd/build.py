@@ -21,6 +21,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-command-line-argument",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first kernel arguments arrive in SGPRs at wave launch instead of
+    # through a scalar load (gfx950 kernarg preloading)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", INCLUDE, "-I", CSRC,
 ]
 C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-I", INCLUDE, "-I", os.path.join(ROCM, "include")]

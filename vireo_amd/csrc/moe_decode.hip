@@ -38,65 +38,93 @@ int64_t row_bytes_of(uint32_t t, int n) {
 // ------------------------------------------------------------------ fused top-k + gate/up
 constexpr int kGuWaves = 8;
 
-// grid (ceil(fe / (kGuWaves * RPW)), k), 512 threads. A row has 64 * IPL items
-// (d = 2048 * IPL); lane l owns items l, l + 64, ...
-template <int T, int IPL, int RPW>
+// Entry idx of a table spread over the wave's registers (lane l holds entries
+// [TPL*l, TPL*l + TPL)); idx is the same on every lane.
+template <int TPL>
+VH_DEV const uint8_t *table_entry(const void *const (&tab)[TPL], int idx) {
+    const int src = idx / TPL, slot = idx - src * TPL;
+    uint64_t v = 0;
+#pragma unroll
+    for (int s = 0; s < TPL; s++)
+        if (s == slot) v = reinterpret_cast<uint64_t>(tab[s]);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), src));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), src));
+    return reinterpret_cast<const uint8_t *>((uint64_t(hi) << 32) | lo);
+}
+
+// grid (ceil(fe / (kGuWaves * RPW)), k), 512 threads, d = 2048 (lane l owns
+// item l of a row), E <= 64 * Q. The arguments the prologue needs come first:
+// they are the ones preloaded into SGPRs at launch.
+template <int T, int Q, int RPW>
 __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__restrict__ parts,
-                                                            const float *__restrict__ R,
                                                             const float *__restrict__ hb,
-                                                            const float *__restrict__ bias, int d, int E, int k,
-                                                            int fe, int renorm, const void *const *__restrict__ table,
-                                                            int64_t row_bytes, float *__restrict__ h,
+                                                            const void *const *__restrict__ table, int E, int k,
+                                                            int fe, int d, int renorm, int64_t row_bytes,
+                                                            const float *__restrict__ R,
+                                                            const float *__restrict__ bias, float *__restrict__ h,
                                                             int32_t *__restrict__ idx_out, float *__restrict__ w_out,
                                                             uint32_t *__restrict__ flags_out,
                                                             DecodePlan *__restrict__ plan) {
     using F = Reg<T>;
-    constexpr int NS = F::NS;
-    __shared__ TopKSmem sm;
-    __shared__ const void *s_tab[3 * kMaxExperts];
-    __shared__ int s_ok;
+    constexpr int NS = F::NS, TPL = 3 * Q;
+    __shared__ TopKSmem sm;         // the exact fallback's workspace
+    __shared__ float2 stage[64];    // the weights, in the workgroup that writes the plan
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int j = blockIdx.y;
 
-    // 1. every load of the prologue, issued before any of them is used
-    RoutePart p[4];
-    if (wv == 0) {
+    // 1. every load of the prologue, issued before any of them is used: the
+    //    router parts, the layer's expert table (spread over the lanes) and
+    //    this lane's item of the input
+    RoutePart p[Q];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int e = lane + 64 * q;
-            if (e < E) p[q] = parts[e];
-            else p[q] = RoutePart{0.0, 0.0};
-        }
-    } else {
-        for (int i = tid - 64; i < 3 * E; i += int(blockDim.x) - 64) s_tab[i] = table[i];
+    for (int q = 0; q < Q; q++) {
+        const int e = lane + 64 * q;
+        if (e < E) p[q] = parts[e];
+        else p[q] = RoutePart{0.0, 0.0};
     }
-    float xr[IPL][32], xs[IPL][NS];
+    const void *tab[TPL];
 #pragma unroll
-    for (int m = 0; m < IPL; m++) F::load_x(hb, lane + 64 * m, xr[m]);
-#pragma unroll
-    for (int m = 0; m < IPL; m++) F::sums(xr[m], xs[m]);
+    for (int s = 0; s < TPL; s++) {
+        const int i = TPL * lane + s;
+        tab[s] = i < 3 * E ? table[i] : nullptr;
+    }
+    float xr[32], xs[NS];
+    F::load_x(hb, lane, xr);
+    F::sums(xr, xs);
 
-    // 2. the top-k: one wave, or the whole workgroup when not certified
-    if (wv == 0) {
-        const bool ok = route_topk_wave(sm, p, E, k, renorm);
-        if (lane == 0) s_ok = ok;
-    }
-    __syncthreads();
-    if (!s_ok) route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-        if (tid < k) {
-            idx_out[tid] = sm.sel[tid];
-            w_out[tid] = sm.sel_w[tid];
-            plan->down[tid] = s_tab[3 * sm.sel[tid] + 2];
-            plan->w[tid] = sm.sel_w[tid];
+    // 2. every wave selects on its own (no LDS, no barrier); a token whose
+    //    order is not certified (the same verdict in every wave) is ranked
+    //    again by the whole workgroup on exact logits
+    int e_j, rank[Q];
+    const bool ok = route_select_wave<Q>(p, E, k, j, e_j, rank);
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+    if (!ok) {
+        route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);
+        e_j = sm.sel[j];
+        if (writer && wv == 0 && lane < k) {
+            const int e = sm.sel[lane];
+            idx_out[lane] = e;
+            w_out[lane] = sm.sel_w[lane];
+            plan->w[lane] = sm.sel_w[lane];
+            plan->down[lane] = table[3 * e + 2];
         }
-        if (tid == 0 && flags_out) flags_out[0] = sm.flag;
+        if (writer && tid == 0 && flags_out) flags_out[0] = sm.flag;
+    } else if (writer && wv == 0) {
+        int e;
+        float w;
+        route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
+        if (lane < k) {
+            idx_out[lane] = e;
+            w_out[lane] = w;
+            plan->w[lane] = w;
+            plan->down[lane] = table[3 * e + 2];
+        }
+        if (lane == 0 && flags_out) flags_out[0] = 0u;
     }
 
     // 3. RPW rows of gate and up of the chosen expert j
-    const int e = sm.sel[j];
-    const uint8_t *G = static_cast<const uint8_t *>(s_tab[3 * e]);
-    const uint8_t *U = static_cast<const uint8_t *>(s_tab[3 * e + 1]);
+    const uint8_t *G = table_entry<TPL>(tab, 3 * e_j);
+    const uint8_t *U = table_entry<TPL>(tab, 3 * e_j + 1);
     const int o0 = (blockIdx.x * kGuWaves + wv) * RPW;
     if (!G || !U) {  // unregistered expert: contributes nothing (src/gguf_run.c:201)
 #pragma unroll
@@ -104,38 +132,31 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = 0.0f;
         return;
     }
-    typename F::Raw rg[RPW][IPL], ru[RPW][IPL];
+    typename F::Raw rg[RPW], ru[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
         const int64_t o = min(o0 + r, fe - 1);
-#pragma unroll
-        for (int m = 0; m < IPL; m++) {
-            rg[r][m] = F::fetch(G, o * row_bytes, lane + 64 * m);
-            ru[r][m] = F::fetch(U, o * row_bytes, lane + 64 * m);
-        }
+        rg[r] = F::fetch(G, o * row_bytes, lane);
+        ru[r] = F::fetch(U, o * row_bytes, lane);
     }
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-        float g = 0.0f, u = 0.0f;
-#pragma unroll
-        for (int m = 0; m < IPL; m++) {
-            g += F::compute(rg[r][m], lane + 64 * m, xr[m], xs[m]);
-            u += F::compute(ru[r][m], lane + 64 * m, xr[m], xs[m]);
-        }
+        float g = F::compute(rg[r], lane, xr, xs);
+        float u = F::compute(ru[r], lane, xr, xs);
         g = group_sum<64>(g);
         u = group_sum<64>(u);
         if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = swiglu(g, u);
     }
 }
 
-template <int T, int IPL, int RPW>
+template <int T, int Q, int RPW>
 int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E,
                          int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx,
                          float *w, uint32_t *flags, DecodePlan *plan, hipStream_t s) {
     constexpr int rows_per_block = kGuWaves * RPW;
     dim3 g((fe + rows_per_block - 1) / rows_per_block, k);
-    VH_LAUNCH((decode_gateup_kernel<T, IPL, RPW>), g, dim3(64 * kGuWaves), 0, s, parts, R, hb, bias, d, E, k, fe,
-              renorm, table, rb, h, idx, w, flags, plan);
+    VH_LAUNCH((decode_gateup_kernel<T, Q, RPW>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe, d, renorm,
+              rb, R, bias, h, idx, w, flags, plan);
     return vh_check(hipGetLastError());
 }
 
@@ -145,18 +166,31 @@ int gateup_rpw(int fe, int k) {
     return want <= 2 ? 2 : want <= 3 ? 3 : 4;
 }
 
-template <int T, int IPL>
+template <int T, int Q>
 int launch_gateup_rpw(int rpw, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                       int E, int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx,
                       float *w, uint32_t *flags, DecodePlan *plan, hipStream_t s) {
     if (rpw == 2)
-        return launch_decode_gateup<T, IPL, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                               plan, s);
+        return launch_decode_gateup<T, Q, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
+                                             plan, s);
     if (rpw == 3)
-        return launch_decode_gateup<T, IPL, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                               plan, s);
-    return launch_decode_gateup<T, IPL, 4>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan,
-                                           s);
+        return launch_decode_gateup<T, Q, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
+                                             plan, s);
+    return launch_decode_gateup<T, Q, 4>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan,
+                                         s);
+}
+
+template <int T>
+int launch_gateup_t(int rpw, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E,
+                    int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
+                    uint32_t *flags, DecodePlan *plan, hipStream_t s) {
+    if (E <= 64)
+        return launch_gateup_rpw<T, 1>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
+                                       plan, s);
+    if (E <= 128)
+        return launch_gateup_rpw<T, 2>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
+                                       plan, s);
+    return launch_gateup_rpw<T, 4>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
 }
 
 // ------------------------------------------------------------------ down + combine
@@ -176,7 +210,17 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     const int j = g % k, rstep = NG / k, rf = g / k;
     const int o0 = blockIdx.x * R;
     const int items = F::items(fe);
+    const int lane = tid & 63;
     const uint8_t *D = static_cast<const uint8_t *>(plan->down[j]);
+    // what the combine needs, loaded now: lane j2 < k of wave 0 holds expert
+    // j2's weight and whether its lookup succeeded, thread tid < R its output
+    float wj2 = 0.0f, xo = 0.0f;
+    int pres = 0;
+    if (tid < 64 && lane < k) {
+        pres = plan->down[lane] != nullptr;
+        wj2 = plan->w[lane];
+    }
+    if (tid < R) xo = x[o0 + tid];
     // activations of expert j for this lane's items (independent of the plan)
     float xv[IPL][32], xs[IPL][NS];
 #pragma unroll
@@ -215,13 +259,15 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
         if (li == L - 1) ys[j * R + rf + rr * rstep] = acc;
     }
     __syncthreads();
-    if (tid < R) {
+    if (tid < 64) {  // R <= 64: the combining threads are in wave 0
         float a = 0.0f;
         for (int j2 = 0; j2 < k; j2++) {
-            if (!plan->down[j2]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-            a = __fadd_rn(a, __fmul_rn(plan->w[j2], ys[j2 * R + tid]));
+            const int present = __builtin_amdgcn_readlane(pres, j2);
+            const float wv2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj2), j2));
+            if (!present) continue;  // failed lookup: skipped (src/gguf_run.c:201)
+            if (tid < R) a = __fadd_rn(a, __fmul_rn(wv2, ys[j2 * R + tid]));
         }
-        x[o0 + tid] = __fadd_rn(x[o0 + tid], a);
+        if (tid < R) x[o0 + tid] = __fadd_rn(xo, a);
     }
 }
 
@@ -258,7 +304,7 @@ int launch_down_t(const DecodePlan *plan, const float *h, int d, int fe, int k, 
 }  // namespace
 
 bool vh_decode_gateup_supported(uint32_t type, int d, int fe) {
-    return (d == 2048 || d == 4096) && fe >= 1 && (type == VT_Q4_K || type == VT_Q8_0 || type == VT_Q6_K);
+    return d == 2048 && fe >= 1 && (type == VT_Q4_K || type == VT_Q8_0 || type == VT_Q6_K);
 }
 
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
@@ -267,23 +313,10 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
     if (!vh_decode_gateup_supported(type, d, fe) || E > kMaxExperts || k > 64) return -EINVAL;
     const int64_t rb = row_bytes_of(type, d);
     const int rpw = gateup_rpw(fe, k);
-    const bool two = d == 4096;
     switch (type) {
-    case VT_Q4_K:
-        return two ? launch_gateup_rpw<VT_Q4_K, 2>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s)
-                   : launch_gateup_rpw<VT_Q4_K, 1>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s);
-    case VT_Q8_0:
-        return two ? launch_gateup_rpw<VT_Q8_0, 2>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s)
-                   : launch_gateup_rpw<VT_Q8_0, 1>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s);
-    case VT_Q6_K:
-        return two ? launch_gateup_rpw<VT_Q6_K, 2>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s)
-                   : launch_gateup_rpw<VT_Q6_K, 1>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w,
-                                                   flags, plan, s);
+    case VT_Q4_K: return launch_gateup_t<VT_Q4_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
+    case VT_Q8_0: return launch_gateup_t<VT_Q8_0>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
+    case VT_Q6_K: return launch_gateup_t<VT_Q6_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, s);
     default: return -EINVAL;
     }
 }

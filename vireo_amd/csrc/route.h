@@ -309,3 +309,94 @@ VH_DEV bool route_topk_wave(TopKSmem &sm, const RoutePart (&p)[4], int E, int k,
     }
     return true;
 }
+
+// The chosen experts of one token by one wave, in registers only (no LDS, no
+// barrier), so that every wave of a workgroup can select on its own: Q parts
+// per lane (expert lane + 64q, E <= 64Q), k rounds of a wave-wide max over the
+// 32-bit keys (lower id wins a tie), the order certified as in
+// route_topk_block. Returns whether it was certified (the same on every lane
+// and in every wave given the same parts). e_want receives the expert chosen
+// in round `want`; rank[q] receives the round in which this lane's slot q was
+// chosen (-1 if not chosen).
+template <int Q>
+VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, int &e_want, int (&rank)[Q]) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? ((ordered_u32(float(p[q].c)) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
+        rank[q] = -1;
+    }
+    bool ok = true;
+    double prev_lo = 0.0;
+    e_want = 0;
+    for (int t = 0; t < k; t++) {
+        uint32_t best = 0u;
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (rank[q] < 0 && key[q] > best) best = key[q];
+        const uint32_t wb = wave_max_u(best);
+        const int e = 255 - int(wb & 0xffu), qw = e >> 6, owner = e & 63;
+        double c = 0.0, b = 0.0;
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            if (q == qw) {
+                c = p[q].c;
+                b = p[q].beta;
+                if (lane == owner) rank[q] = t;
+            }
+        }
+        c = readlane_d(c, owner);
+        b = readlane_d(b, owner);
+        if (t > 0) ok = ok && (prev_lo - (c + b) > kRouteMargin);
+        prev_lo = c - b;
+        if (t == want) e_want = e;
+    }
+    float rest = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < Q; q++)
+        if (rank[q] < 0 && key[q] != 0u) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
+    rest = wave_max_f(rest);
+    if (k < E) ok = ok && (prev_lo - double(rest) > kRouteMargin);
+    return ok;
+}
+
+// Softmax weights of the experts chosen by route_select_wave (src/gguf_run.c:
+// 181-192), by one wave: lane t < k returns the expert of round t in e_out and
+// its weight (renormalised over the k in selection order when renorm).
+// `stage` is a 64-entry LDS scratch owned by this wave.
+template <int Q>
+VH_DEV void route_weights_wave(const RoutePart (&p)[Q], const int (&rank)[Q], int E, int k, int renorm,
+                               float2 *stage, int &e_out, float &w_out) {
+    const int lane = threadIdx.x & 63;
+    float lg[Q], mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        lg[q] = lane + 64 * q < E ? float(p[q].c) : -INFINITY;
+        mx = fmaxf(mx, lg[q]);
+    }
+    const float m = wave_max_f(mx);
+    float ex[Q], part = 0.0f;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        ex[q] = lane + 64 * q < E ? expf(lg[q] - m) : 0.0f;
+        part += ex[q];
+    }
+    const float s = wave_sum_f(part);
+#pragma unroll
+    for (int q = 0; q < Q; q++)
+        if (rank[q] >= 0) stage[rank[q]] = make_float2(ex[q] / s, __int_as_float(lane + 64 * q));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float2 v = stage[lane < k ? lane : 0];
+    float w = v.x;
+    if (renorm) {
+        float wsum = 0.0f;
+        for (int t = 0; t < k; t++) wsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
+        if (wsum > 0.0f) w = w / wsum;
+    }
+    e_out = __float_as_int(v.y);
+    w_out = w;
+}
