@@ -69,6 +69,15 @@ def alg_bytes_layer(shape, idx, B):
     return shape.E * shape.d * 4 + distinct * shape.expert_bytes() + 3 * B * shape.d * 4, distinct
 
 
+def alg_bytes_experts(shape):
+    """Fused stage 1 for one token: the k experts' gate, up and down slices,
+    hb, the router parts and expert table it reads, h written and read back,
+    x read and written."""
+    gs, us, ds = shape.slice_bytes()
+    return (shape.k * (gs + us + ds) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + 2 * shape.k * shape.fe * 4
+            + 2 * shape.d * 4)
+
+
 def alg_bytes_gateup(shape):
     """Stage 1 for one token: k experts' gate and up slices, hb, the router
     parts and expert table it reads, the k x fe activations it writes."""
@@ -258,20 +267,23 @@ def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
     for stage in (0, 1, 2):
         us = m.decode_stage_timed(stage, layers, x, hb, states, idx, w)
         times[stage] = (float(us.mean()), float(np.median(us)))
-    nb = alg_bytes_gateup(shape)
+    fused = times[2][0] == 0.0  # stage 1 was the fused kernel: gate/up, down and combine in one launch
+    nb = alg_bytes_experts(shape) if fused else alg_bytes_gateup(shape)
+    kname = ("decode_experts_kernel (top-k, gate/up, down, combine; stage 1)" if fused
+             else "decode_gateup_kernel (top-k + gate/up SwiGLU, stage 1)")
     avg = times[1][0]
     gbs = nb / (avg * 1e-6) / 1e9
     traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_decode_gateup_{shape.name}.json")
+    tf = os.path.join(ROOT, "profiles", f"traffic_{'decode_experts' if fused else 'decode_gateup'}_{shape.name}.json")
     if os.path.exists(tf):
         with open(tf) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     return {
-        "roofline": {"kernel": "decode_gateup_kernel (top-k + gate/up SwiGLU, stage 1)", "bound": "hbm",
+        "roofline": {"kernel": kname, "bound": "hbm",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "alg_bytes_per_launch": nb,
                      "avg_launch_us": round(avg, 3), "median_launch_us": round(times[1][1], 3), "launches": NS},
-        "stages_us": {"route": round(times[0][0], 3), "topk_gateup": round(times[1][0], 3),
+        "stages_us": {"route": round(times[0][0], 3), "experts" if fused else "topk_gateup": round(times[1][0], 3),
                       "down_combine": round(times[2][0], 3)},
     }
 

@@ -131,20 +131,31 @@ int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *
 
 /* Execution plan for moe_ffn_forward (a tuning and testing knob; no
  * counterpart in the reference): 0 = automatic (default), 1 = the one-token
- * decode plan whenever it applies, 2 = always the grouped plan. */
+ * decode plan whenever it applies, 2 = always the grouped plan, 3 = the
+ * one-token decode plan with its experts fused into one kernel where that
+ * kernel is built for the shapes (see moe_decode_stage). */
 int vireo_hip_set_path(int path);
 
-/* The one-token decode plan of moe_ffn_forward as three separate launches
- * over a caller-owned device `state` buffer of moe_decode_state_bytes(m)
- * bytes (no counterpart in the reference, whose moe_ffn is one function):
+/* The one-token decode plan of moe_ffn_forward as separate launches over a
+ * caller-owned device `state` buffer of moe_decode_state_bytes(m) bytes (no
+ * counterpart in the reference, whose moe_ffn is one function):
  *   stage 0  router logits of hb into state
- *   stage 1  top-k, then the chosen experts' gate/up SwiGLU into state;
- *            idx_out / w_out (optional, k entries) receive the routing
- *   stage 2  down projections, weighted combine in selection order, x += ...
+ *   stage 1  top-k and the gate/up SwiGLU into state; idx_out / w_out
+ *            (optional, k entries) receive the routing. Under plan 3
+ *            (vireo_hip_set_path) and for the shapes the fused kernel is
+ *            built for (d = 2048, k = 8, 256 CUs; Qwen3-30B-A3B and OLMoE
+ *            layers with Q4_K/Q6_K or Q8_0 experts) one launch computes
+ *            gate/up, down and the combine and updates x
+ *   stage 2  down projections and the combine, x += ... (nothing to do when
+ *            stage 1 was the fused kernel)
  * Running 0, 1, 2 in order gives moe_ffn_forward's result for one token bit
- * for bit. Stages 1 and 2 read only what the previous stage left in state, so
- * one state per (layer, token) lets a caller (a profiler, a scheduler that
- * interleaves other work) launch and time each stage on its own.
+ * for bit. Each stage reads only what the previous one left in state (stage
+ * 1 needs stage 0 of the same state right before it: stage 0 also clears the
+ * fused kernel's flags), so one state per (layer, token) lets a caller (a
+ * profiler, a scheduler that interleaves other work) launch and time each
+ * stage on its own. The token's flag word (VIREO_ROUTE_* bits, and 4 if a
+ * fused launch waited too long for its workgroups, which makes its result
+ * invalid) is the last word written by stage 1.
  * moe_decode_state_bytes returns -EINVAL when the model's shapes or types
  * have no decode plan (moe_ffn_forward then always uses the grouped plan). */
 int64_t moe_decode_state_bytes(const vireo_moe_model *m);

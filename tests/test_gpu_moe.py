@@ -51,8 +51,10 @@ CONFIGS = [("olmoe-q8_0", 1), ("olmoe-q4_k_m", 1), ("olmoe-q4_k_m", 4), ("olmoe-
 
 
 @pytest.mark.parametrize("name,T", CONFIGS)
-@pytest.mark.parametrize("plan", [0, 2])
+@pytest.mark.parametrize("plan", [0, 2, 3])
 def test_moe_ffn_matches_oracle(cuda, oracle, path, name, T, plan):
+    if plan == 3 and T > 1:
+        pytest.skip("plan 3 (fused experts kernel) is a one-token decode plan")
     path(plan)
     shape = W.SHAPES[name]
     m = M.DeviceMoE(shape, 1, seed=51)
@@ -164,10 +166,12 @@ def test_prefill_2048_zipf(cuda, oracle):
     m.close()
 
 
+@pytest.mark.parametrize("plan", [0, 3])
 @pytest.mark.parametrize("name", ["qwen3-30b-a3b-q4_k_m", "olmoe-q8_0", "olmoe-q4_k_m"])
-def test_decode_stages_equal_forward(cuda, name):
+def test_decode_stages_equal_forward(cuda, path, name, plan):
     """moe_decode_stage 0, 1, 2 over a caller-owned state gives
-    moe_ffn_forward's single-token result bit for bit."""
+    moe_ffn_forward's single-token result bit for bit (three-kernel and fused)."""
+    path(plan)
     shape = W.SHAPES[name]
     m = M.DeviceMoE(shape, 2, seed=57)
     x, hb = W.host_hidden(shape.d, 1, 57)
@@ -187,12 +191,13 @@ def test_decode_stages_equal_forward(cuda, name):
     m.close()
 
 
+@pytest.mark.parametrize("plan", [1, 3])
 @pytest.mark.parametrize("name", ["olmoe-q8_0", "qwen3-30b-a3b-q4_k_m"])
-def test_decode_plan_ties_take_the_exact_path(cuda, oracle, path, name):
+def test_decode_plan_ties_take_the_exact_path(cuda, oracle, path, name, plan):
     """Exactly tied router rows inside and at the edge of the top-k: the
     decode kernel's one-wave ranking cannot certify the order and the whole
     workgroup re-ranks on exact logits; experts and output match the oracle."""
-    path(1)
+    path(plan)
     shape = W.SHAPES[name]
     m = M.DeviceMoE(shape, 1, seed=58)
     r = m.routers[0]

@@ -18,7 +18,7 @@
 
 namespace {
 
-int g_path = 0;                        // 0 auto, 1 decode plan when possible, 2 grouped plan
+int g_path = 0;  // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the fused experts kernel
 constexpr int kExactRouteTokens = 64;  // from this many tokens on, exact sequential logits
 
 bool type_ok(uint32_t t, int n) {
@@ -46,6 +46,7 @@ struct Ws {
     int32_t *idx, *counts, *offs, *perm, *active;
     float *w, *h, *ybuf;
     uint32_t *flags;
+    uint32_t *bar;  // decode plan: kFusedBlocks barrier flags, then the token's flag word
     DecodePlan *plan;
 };
 
@@ -56,6 +57,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_parts = take(size_t(T) * E * sizeof(RoutePart));
     const size_t o_idx = take(P * 4), o_w = take(P * 4), o_flags = take(size_t(T) * 4);
     const size_t o_plan = take(sizeof(DecodePlan));
+    const size_t o_bar = take((kFusedBlocks + 1) * 4);
     const size_t o_counts = take(size_t(E) * 4), o_offs = take(size_t(E + 1) * 4), o_perm = take(P * 4),
                  o_active = take(size_t(E + 1) * 4);
     const size_t o_h = experts ? take(P * fe * 4) : 0;
@@ -68,6 +70,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->w = reinterpret_cast<float *>(b + o_w);
     ws->flags = reinterpret_cast<uint32_t *>(b + o_flags);
     ws->plan = reinterpret_cast<DecodePlan *>(b + o_plan);
+    ws->bar = reinterpret_cast<uint32_t *>(b + o_bar);
     ws->counts = reinterpret_cast<int32_t *>(b + o_counts);
     ws->offs = reinterpret_cast<int32_t *>(b + o_offs);
     ws->perm = reinterpret_cast<int32_t *>(b + o_perm);
@@ -90,7 +93,8 @@ struct DecodeState {
     RoutePart *parts;  // [E]
     DecodePlan *plan;
     float *h;          // [k x fe]
-    uint32_t *flags;   // [1]
+    uint32_t *bar;     // [kFusedBlocks] barrier flags of the fused kernel, then the token's flag word
+    uint32_t *flags() const { return bar + kFusedBlocks; }
 };
 
 size_t decode_state_layout(const vireo_moe_model *m, size_t off[4]) {
@@ -98,21 +102,38 @@ size_t decode_state_layout(const vireo_moe_model *m, size_t off[4]) {
     off[0] = o; o += al256(size_t(m->n_experts) * sizeof(RoutePart));
     off[1] = o; o += al256(sizeof(DecodePlan));
     off[2] = o; o += al256(size_t(m->n_used) * m->ffn_exp * sizeof(float));
-    off[3] = o; o += al256(sizeof(uint32_t));
+    off[3] = o; o += al256((kFusedBlocks + 1) * sizeof(uint32_t));
     return o;
 }
 
+bool fused(const vireo_moe_model *m, int layer) {
+    if (g_path != 3) return false;
+    const vireo_moe_layer &L = m->layers[layer];
+    return vh_fused_blocks(L.gate_exps->ggml_type, L.down_exps->ggml_type, m->dim, m->n_experts, m->n_used,
+                           m->ffn_exp) > 0;
+}
+
+// Stage 0: router logits (and the barrier flags cleared). Stage 1: the fused
+// experts kernel where it is built for the shapes (x is updated there and
+// stage 2 has nothing left to do), else top-k + gate/up. Stage 2: down +
+// combine.
 int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *const *table, float *x,
                  const float *hb, const DecodeState &st, int32_t *idx, float *w, hipStream_t s) {
     const vireo_moe_layer &L = m->layers[layer];
     const float *R = static_cast<const float *>(L.router->data);
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
+    const uint32_t tg = L.gate_exps->ggml_type, td = L.down_exps->ggml_type;
     switch (stage) {
-    case 0: return vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, st.parts, s);
+    case 0: return vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, st.parts, s, st.bar, kFusedBlocks + 1);
     case 1:
-        return vh_decode_gateup(L.gate_exps->ggml_type, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm,
-                                table, st.h, idx, w, st.flags, st.plan, s);
-    case 2: return vh_down_combine(L.down_exps->ggml_type, st.plan, st.h, d, fe, k, x, s);
+        if (fused(m, layer))
+            return vh_decode_experts(tg, td, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h,
+                                     st.bar, x, idx, w, s);
+        return vh_decode_gateup(tg, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h, idx, w,
+                                st.flags(), st.plan, s);
+    case 2:
+        if (fused(m, layer)) return 0;
+        return vh_down_combine(td, st.plan, st.h, d, fe, k, x, s);
     default: return -EINVAL;
     }
 }
@@ -140,6 +161,7 @@ extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, 
     char *b = static_cast<char *>(state);
     const DecodeState st{reinterpret_cast<RoutePart *>(b + off[0]), reinterpret_cast<DecodePlan *>(b + off[1]),
                          reinterpret_cast<float *>(b + off[2]), reinterpret_cast<uint32_t *>(b + off[3])};
+    if (stage == 1 && !x && fused(m, layer)) return -EINVAL;  // the fused stage 1 updates x
     int32_t *idx = idx_out;
     float *w = w_out;
     Ws ws;
@@ -157,7 +179,7 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
                                       float *us_out, void *stream) {
     if (int rc = check_model(m, 0)) return rc;
     if (n <= 0 || !layers || !hb || !states || !idx || !w || !us_out || stage < 0 || stage > 2) return -EINVAL;
-    if (stage == 2 && !x) return -EINVAL;
+    if (stage > 0 && !x) return -EINVAL;
     if (reinterpret_cast<uintptr_t>(hb) & 15u || (m->dim * 4) & 15) return -EINVAL;
     size_t off[4];
     if (!decode_supported(m, 0) || state_stride < int64_t(decode_state_layout(m, off)) || (state_stride & 255) ||
@@ -183,13 +205,18 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
         char *b = static_cast<char *>(states) + i * state_stride;
         const DecodeState st{reinterpret_cast<RoutePart *>(b + off[0]), reinterpret_cast<DecodePlan *>(b + off[1]),
                              reinterpret_cast<float *>(b + off[2]), reinterpret_cast<uint32_t *>(b + off[3])};
+        us_out[i] = (stage == 2 && fused(m, layer)) ? -1.0f : 0.0f;  // -1: no kernel to time (done in stage 1)
         g_vh_timing = {ev[2 * i], ev[2 * i + 1]};
         rc = decode_stage(m, layer, stage, table, x ? x + size_t(i) * d : nullptr, hb + size_t(i) * d, st,
                           idx + size_t(i) * k, w + size_t(i) * k, s);
         g_vh_timing = {nullptr, nullptr};
     }
-    if (!rc) rc = vh_check(hipEventSynchronize(ev[2 * n - 1]));
+    if (!rc) rc = vh_check(hipStreamSynchronize(s));
     for (int i = 0; i < n && !rc; i++) {
+        if (us_out[i] < 0.0f) {
+            us_out[i] = 0.0f;
+            continue;
+        }
         float ms = 0.0f;
         rc = vh_check(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
         us_out[i] = ms * 1000.0f;
@@ -198,7 +225,7 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
 }
 
 extern "C" int vireo_hip_set_path(int path) {
-    if (path < 0 || path > 2) return -EINVAL;
+    if (path < 0 || path > 3) return -EINVAL;
     g_path = path;
     return 0;
 }
@@ -255,7 +282,7 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     float *w = w_out ? w_out : ws.w;
     int rc;
     if (decode) {
-        const DecodeState st{ws.parts, ws.plan, ws.h, ws.flags};
+        const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
         rc = 0;
         for (int stage = 0; stage < 3 && !rc; stage++)
             rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s);

@@ -38,20 +38,6 @@ int64_t row_bytes_of(uint32_t t, int n) {
 // ------------------------------------------------------------------ fused top-k + gate/up
 constexpr int kGuWaves = 8;
 
-// Entry idx of a table spread over the wave's registers (lane l holds entries
-// [TPL*l, TPL*l + TPL)); idx is the same on every lane.
-template <int TPL>
-VH_DEV const uint8_t *table_entry(const void *const (&tab)[TPL], int idx) {
-    const int src = idx / TPL, slot = idx - src * TPL;
-    uint64_t v = 0;
-#pragma unroll
-    for (int s = 0; s < TPL; s++)
-        if (s == slot) v = reinterpret_cast<uint64_t>(tab[s]);
-    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), src));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), src));
-    return reinterpret_cast<const uint8_t *>((uint64_t(hi) << 32) | lo);
-}
-
 // grid (ceil(fe / (kGuWaves * RPW)), k), 512 threads, d = 2048 (lane l owns
 // item l of a row), E <= 64 * Q. The arguments the prologue needs come first:
 // they are the ones preloaded into SGPRs at launch.
@@ -69,6 +55,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     constexpr int NS = F::NS, TPL = 3 * Q;
     __shared__ TopKSmem sm;         // the exact fallback's workspace
     __shared__ float2 stage[64];    // the weights, in the workgroup that writes the plan
+    __shared__ double2 cert[kGuWaves][64];  // per wave: the chosen experts' intervals
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int j = blockIdx.y;
 
@@ -95,8 +82,8 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     // 2. every wave selects on its own (no LDS, no barrier); a token whose
     //    order is not certified (the same verdict in every wave) is ranked
     //    again by the whole workgroup on exact logits
-    int e_j, rank[Q];
-    const bool ok = route_select_wave<Q>(p, E, k, j, e_j, rank);
+    int e_j, e_unused, rank[Q];
+    const bool ok = route_select_wave<Q>(p, E, k, j, e_j, j, e_unused, rank, cert[wv]);
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
     if (!ok) {
         route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);

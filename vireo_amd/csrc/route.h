@@ -230,96 +230,19 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     __syncthreads();
 }
 
-// Top-k of one token by one wave (all 64 lanes active), for the fused decode
-// kernel: lane l holds the parts of experts l, l+64, l+128, l+192 (E <= 256).
-// k rounds of a wave-wide max over the 32-bit keys of route_topk_block (the
-// ordered fp32 image of the midpoint, low 8 bits 255 - e, so the lower id wins
-// a tie) give the chosen experts in order; each round's winner interval is
-// read from its owner lane and the order is certified on the fly: every chosen
-// lower bound must exceed the next upper bound (or, for the last, the best
-// upper bound left out) by kRouteMargin. Certified gaps exceed kNearTie, so
-// the flag is 0. Returns whether the order was certified (the same on every
-// lane); only then are sm.sel, sm.sel_w and sm.flag written, and the caller
-// must fall back to route_topk_block otherwise.
-VH_DEV bool route_topk_wave(TopKSmem &sm, const RoutePart (&p)[4], int E, int k, int renorm) {
-    const int lane = threadIdx.x & 63;
-    uint32_t key[4];
-    float lg[4];
-    int rank[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int e = lane + 64 * q;
-        const bool mine = e < E;
-        lg[q] = mine ? float(p[q].c) : -INFINITY;
-        key[q] = mine ? ((ordered_u32(lg[q]) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
-        rank[q] = -1;
-    }
-    bool ok = true;
-    double prev_lo = 0.0;
-    float m = 0.0f;
-    for (int t = 0; t < k; t++) {
-        uint32_t best = 0u;
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (rank[q] < 0 && key[q] > best) best = key[q];
-        const uint32_t wb = wave_max_u(best);
-        const int e = 255 - int(wb & 0xffu), qw = e >> 6, owner = e & 63;
-        double c = 0.0, b = 0.0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (q == qw) {
-                c = p[q].c;
-                b = p[q].beta;
-                if (lane == owner) rank[q] = t;
-            }
-        }
-        c = readlane_d(c, owner);
-        b = readlane_d(b, owner);
-        if (t == 0) m = float(c);
-        else ok = ok && (prev_lo - (c + b) > kRouteMargin);
-        prev_lo = c - b;
-        if (lane == 0) sm.sel[t] = e;
-    }
-    float rest = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-        if (rank[q] < 0 && key[q] != 0u) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
-    rest = wave_max_f(rest);
-    if (k < E) ok = ok && (prev_lo - double(rest) > kRouteMargin);
-    if (!ok) return false;
-    // softmax over all experts (src/gguf_run.c:181-182); m is the largest logit
-    float ex[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) ex[q] = key[q] != 0u ? expf(lg[q] - m) : 0.0f;
-    const float s = wave_sum_f((ex[0] + ex[1]) + (ex[2] + ex[3]));
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-        if (rank[q] >= 0) sm.sel_w[rank[q]] = ex[q] / s;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-        sm.flag = 0u;
-        if (renorm) {
-            float wsum = 0.0f;
-            for (int t = 0; t < k; t++) wsum += sm.sel_w[t];  // in selection order (src/gguf_run.c:192)
-            if (wsum > 0.0f)
-                for (int t = 0; t < k; t++) sm.sel_w[t] = sm.sel_w[t] / wsum;
-        }
-    }
-    return true;
-}
-
-// The chosen experts of one token by one wave, in registers only (no LDS, no
-// barrier), so that every wave of a workgroup can select on its own: Q parts
-// per lane (expert lane + 64q, E <= 64Q), k rounds of a wave-wide max over the
-// 32-bit keys (lower id wins a tie), the order certified as in
-// route_topk_block. Returns whether it was certified (the same on every lane
-// and in every wave given the same parts). e_want receives the expert chosen
-// in round `want`; rank[q] receives the round in which this lane's slot q was
-// chosen (-1 if not chosen).
+// The chosen experts of one token by one wave, without a workgroup barrier,
+// so that every wave of a workgroup can select on its own: Q parts per lane
+// (expert lane + 64q, E <= 64Q); k rounds of a wave-wide max over the 32-bit
+// keys (lower id wins a tie) find the winners, then the order is certified in
+// one step as in route_topk_block: each winner's owner writes its interval to
+// `cert` (64 entries of this wave's LDS) and lane t checks round t against
+// round t+1 (the last round against the best upper bound left out). Returns
+// whether it was certified (the same on every lane, and in every wave given
+// the same parts). e_want / e_want2 receive the experts chosen in rounds want
+// / want2; rank[q] the round in which this lane's slot q was chosen (-1 if not).
 template <int Q>
-VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, int &e_want, int (&rank)[Q]) {
+VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, int &e_want, int want2, int &e_want2,
+                              int (&rank)[Q], double2 *cert) {
     const int lane = threadIdx.x & 63;
     uint32_t key[Q];
 #pragma unroll
@@ -328,38 +251,37 @@ VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, i
         key[q] = e < E ? ((ordered_u32(float(p[q].c)) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
         rank[q] = -1;
     }
-    bool ok = true;
-    double prev_lo = 0.0;
     e_want = 0;
+    e_want2 = 0;
     for (int t = 0; t < k; t++) {
         uint32_t best = 0u;
 #pragma unroll
         for (int q = 0; q < Q; q++)
             if (rank[q] < 0 && key[q] > best) best = key[q];
         const uint32_t wb = wave_max_u(best);
-        const int e = 255 - int(wb & 0xffu), qw = e >> 6, owner = e & 63;
-        double c = 0.0, b = 0.0;
 #pragma unroll
-        for (int q = 0; q < Q; q++) {
-            if (q == qw) {
-                c = p[q].c;
-                b = p[q].beta;
-                if (lane == owner) rank[q] = t;
-            }
-        }
-        c = readlane_d(c, owner);
-        b = readlane_d(b, owner);
-        if (t > 0) ok = ok && (prev_lo - (c + b) > kRouteMargin);
-        prev_lo = c - b;
-        if (t == want) e_want = e;
+        for (int q = 0; q < Q; q++)
+            if (key[q] == wb) rank[q] = t;  // keys are distinct: one slot of one lane
+        if (t == want) e_want = 255 - int(wb & 0xffu);
+        if (t == want2) e_want2 = 255 - int(wb & 0xffu);
     }
     float rest = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < Q; q++)
-        if (rank[q] < 0 && key[q] != 0u) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
+    for (int q = 0; q < Q; q++) {
+        if (rank[q] >= 0) cert[rank[q]] = make_double2(p[q].c - p[q].beta, p[q].c + p[q].beta);
+        else if (key[q] != 0u) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
+    }
     rest = wave_max_f(rest);
-    if (k < E) ok = ok && (prev_lo - double(rest) > kRouteMargin);
-    return ok;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool good = true;
+    if (lane < k) {
+        const double lo = cert[lane].x;
+        if (lane + 1 < k) good = lo - cert[lane + 1].y > kRouteMargin;
+        else if (k < E) good = lo - double(rest) > kRouteMargin;
+    }
+    return __builtin_amdgcn_read_exec() == __ballot(good);
 }
 
 // Softmax weights of the experts chosen by route_select_wave (src/gguf_run.c:
@@ -399,4 +321,18 @@ VH_DEV void route_weights_wave(const RoutePart (&p)[Q], const int (&rank)[Q], in
     }
     e_out = __float_as_int(v.y);
     w_out = w;
+}
+
+// Entry idx of a table spread over a wave's registers (lane l holds entries
+// [TPL*l, TPL*l + TPL)); idx must be the same on every lane.
+template <int TPL>
+VH_DEV const uint8_t *table_entry(const void *const (&tab)[TPL], int idx) {
+    const int src = idx / TPL, slot = idx - src * TPL;
+    uint64_t v = 0;
+#pragma unroll
+    for (int s = 0; s < TPL; s++)
+        if (s == slot) v = reinterpret_cast<uint64_t>(tab[s]);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), src));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), src));
+    return reinterpret_cast<const uint8_t *>((uint64_t(hi) << 32) | lo);
 }

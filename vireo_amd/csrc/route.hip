@@ -22,8 +22,11 @@ namespace {
 template <int C>
 __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict__ R, const float *__restrict__ hb,
                                                          const float *__restrict__ bias, int d, int E,
-                                                         RoutePart *__restrict__ parts) {
+                                                         RoutePart *__restrict__ parts, uint32_t *__restrict__ zero,
+                                                         int nzero) {
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
+    if (gid < nzero) zero[gid] = 0u;
     RoutePart p = route_row_part<C>(R + size_t(e) * d, hb + size_t(t) * d, d, lane);
     if (lane == 0) {
         if (bias) p.c += double(bias[e]);
@@ -99,16 +102,18 @@ __global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__re
 }  // namespace
 
 int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
-                   RoutePart *parts, hipStream_t s) {
+                   RoutePart *parts, hipStream_t s, uint32_t *zero, int nzero) {
+    if (nzero > E * T * 64) return -EINVAL;
     if (exact) {
+        if (nzero) return -EINVAL;
         dim3 g((T + kExTok - 1) / kExTok, (E + kExExp - 1) / kExExp);
         hipLaunchKernelGGL(route_exact_kernel, g, dim3(256), 0, s, R, hb, bias, d, E, T, parts);
     } else {
         const bool fast = d == 2048 && (reinterpret_cast<uintptr_t>(R) & 15u) == 0 &&
                           (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
         dim3 g(E, T);
-        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
-        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts);
+        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero);
+        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero);
     }
     return vh_check(hipGetLastError());
 }

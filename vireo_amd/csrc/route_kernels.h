@@ -3,9 +3,10 @@
 #include <hip/hip_runtime.h>
 #include "route.h"
 
-// Router logits of T tokens into parts[T x E] (fast bounded, or exact).
+// Router logits of T tokens into parts[T x E] (fast bounded, or exact); the
+// launch also sets zero[0 .. nzero) to 0 (the fused decode kernel's flags).
 int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
-                   RoutePart *parts, hipStream_t s);
+                   RoutePart *parts, hipStream_t s, uint32_t *zero = nullptr, int nzero = 0);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
@@ -41,3 +42,14 @@ int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, c
                     int max_slots, float *ybuf, hipStream_t s);
 int vh_combine(const int32_t *idx, const float *w, const void *const *table, const float *ybuf, int d, int k, int T,
                float *x, hipStream_t s);
+
+// Fused one-token experts kernel (moe_fused.hip): top-k, gate/up, down and
+// combine in one launch of kFusedBlocks workgroups that meet once through
+// bar[0 .. kFusedBlocks) (zeroed by vh_route_parts); bar[kFusedBlocks] is the
+// token's flag word (VIREO_ROUTE_* bits, VIREO_DECODE_TIMEOUT).
+constexpr int kFusedBlocks = 256;
+constexpr uint32_t VIREO_DECODE_TIMEOUT = 4u;
+int vh_fused_blocks(uint32_t tg, uint32_t td, int d, int E, int k, int fe);  // kFusedBlocks, or 0 if not built for it
+int vh_decode_experts(uint32_t tg, uint32_t td, const RoutePart *parts, const float *R, const float *hb,
+                      const float *bias, int d, int E, int k, int fe, int renorm, const void *const *table, float *h,
+                      uint32_t *bar, float *x, int32_t *idx, float *w, hipStream_t s);
