@@ -22,8 +22,8 @@ int g_path = 0;  // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decod
 constexpr int kExactRouteTokens = 64;  // from this many tokens on, exact sequential logits
 
 bool type_ok(uint32_t t, int n) {
-    switch (t) {
-    case VT_Q8_0: case VT_Q5_0: return n % 32 == 0;
+    switch (t) {  // the expert formats of the MoE models: Q8_0, Q4_K (gate/up), Q6_K (down)
+    case VT_Q8_0: return n % 32 == 0;
     case VT_Q4_K: case VT_Q6_K: return n % 256 == 0;
     default: return false;
     }

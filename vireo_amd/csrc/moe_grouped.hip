@@ -5,9 +5,9 @@
 //            at least one token. The reference has no counterpart: it runs
 //            tokens one at a time (src/gguf_run.c:367-368).
 // gateup     one workgroup per (active expert, row block): each weight item is
-//            decoded once into registers and applied to every token of the
-//            expert (token rows staged in LDS), so expert weights are read once
-//            per call instead of once per token.
+//            read once into registers, dequantized once per chunk of tokens
+//            and applied to every token of the expert (token rows staged in
+//            LDS), so expert weights are read once per call, not per token.
 // down       the same for the down projection; writes y[pair][o].
 // combine    x[t][o] += sum_j w[t][j] * y[t*k+j][o] in selection order
 //            (src/gguf_run.c:209,213); one writer per element, no atomics.
@@ -36,17 +36,39 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(const int32_t *__restric
         if (e >= 0 && e < E) atomicAdd(&hist[e][wv], 1);  // counts only: order-free
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0, na = 0;
-        for (int e = 0; e < E; e++) {
-            tot[e] = run;
-            int ce = 0;
-            for (int s = 0; s < kDispWaves; s++) { const int c = hist[e][s]; hist[e][s] = run + ce; ce += c; }
-            run += ce;
-            if (active && ce > 0) active[na++] = e;
+    // exclusive scan in (expert, segment) order: thread e < E turns its row of
+    // segment counts into prefixes, then a block scan over the expert totals
+    // (and over "has tokens", for the list of active experts) adds the offsets
+    __shared__ int wsum[kDispWaves][2];
+    const int t = threadIdx.x;
+    int ce = 0;
+    if (t < E) {
+        for (int s = 0; s < kDispWaves; s++) {
+            const int c = hist[t][s];
+            hist[t][s] = ce;
+            ce += c;
         }
-        tot[E] = run;
-        if (active) active[E] = na;  // number of active experts
+    }
+    const int a = (t < E && ce > 0) ? 1 : 0;
+    int ic = ce, ia = a;  // inclusive wave scans (row_shr steps, then across rows)
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+        const int oc = __shfl_up(ic, sh, 64), oa = __shfl_up(ia, sh, 64);
+        if (lane >= sh) { ic += oc; ia += oa; }
+    }
+    if (lane == 63) { wsum[wv][0] = ic; wsum[wv][1] = ia; }
+    __syncthreads();
+    int bc = 0, ba = 0;
+    for (int w2 = 0; w2 < wv; w2++) { bc += wsum[w2][0]; ba += wsum[w2][1]; }
+    const int ex_c = bc + ic - ce, ex_a = ba + ia - a;
+    if (t < E) {
+        tot[t] = ex_c;
+        for (int s = 0; s < kDispWaves; s++) hist[t][s] += ex_c;
+        if (active && a) active[ex_a] = t;
+    }
+    if (t == E - 1) {
+        tot[E] = ex_c + ce;
+        if (active) active[E] = ex_a + a;  // number of active experts
     }
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
@@ -72,109 +94,6 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(const int32_t *__restric
     }
 }
 
-// ------------------------------------------------------------ item dequant
-// An item of a row dequantized to NW floats in natural column order; col0 is
-// the column of the first one. Q4_K and Q6_K items cover two / four runs of
-// columns (see qdecode.h); they are split into 16- / 8-column segments.
-template <int T, bool PAIRED>
-struct Items {
-    static constexpr int NW = (T == VT_Q8_0 && PAIRED) ? 64 : 32;
-    static constexpr int SEG = T == VT_Q4_K ? 16 : T == VT_Q6_K ? 8 : NW;  // columns per contiguous run
-    static constexpr int STRIDE = T == VT_Q4_K ? 32 : T == VT_Q6_K ? 32 : 0;  // column step between runs
-    static __host__ __device__ int items(int n) { return T == VT_Q8_0 && PAIRED ? n / 64 : n / 32; }
-    static VH_DEV int col0(int it) {
-        if constexpr (T == VT_Q4_K) { const int sb = it >> 3, r = it & 7; return 256 * sb + 64 * (r >> 1) + 16 * (r & 1); }
-        else if constexpr (T == VT_Q6_K) { const int sb = it >> 3, r = it & 7; return 256 * sb + 128 * (r >> 2) + 8 * (r & 3); }
-        else return NW * it;
-    }
-    // item `it` of the row at byte offset `row` of the 4-aligned tensor `base`
-    static VH_DEV void deq(const uint8_t *base, int64_t row, int it, float *wv) {
-        if constexpr (T == VT_Q8_0 && PAIRED) {
-            const uint8_t *p = base + row + 68 * it;
-            uint32_t w[17];
-#pragma unroll
-            for (int i = 0; i < 17; i++) w[i] = ld_u32(p + 4 * i);
-            const float d0 = h2f(w[0] & 0xffffu), d1 = h2f(w[8] >> 16);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t q0 = align2(w[i + 1], w[i], 2), q1 = w[9 + i];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    wv[4 * i + k] = float(int(int8_t(q0 >> (8 * k)))) * d0;
-                    wv[32 + 4 * i + k] = float(int(int8_t(q1 >> (8 * k)))) * d1;
-                }
-            }
-        } else if constexpr (T == VT_Q8_0) {
-            const uint8_t *b = base + row + 34 * it;  // even address
-            const float d = h2f(ld_u16(b));
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t two = ld_u16(b + 2 + 2 * i);
-                wv[2 * i] = float(int(int8_t(two))) * d;
-                wv[2 * i + 1] = float(int(int8_t(two >> 8))) * d;
-            }
-        } else if constexpr (T == VT_Q4_K) {
-            const int sbi = it >> 3, r = it & 7, c = r >> 1, h = r & 1;
-            const uint8_t *sb = base + row + 144 * sbi;
-            const uint4 hdr = *reinterpret_cast<const uint4 *>(sb);
-            const uint4 q = *reinterpret_cast<const uint4 *>(sb + 16 + 32 * c + 16 * h);
-            const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
-            int sc0, m0, sc1, m1;
-            q4k_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
-            q4k_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
-            const float d1 = d * float(sc0), mm1 = dmin * float(m0), d2 = d * float(sc1), mm2 = dmin * float(m1);
-            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t b = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-                wv[i] = d1 * float(b & 15u) - mm1;
-                wv[16 + i] = d2 * float(b >> 4) - mm2;
-            }
-        } else if constexpr (T == VT_Q6_K) {
-            const int sbi = it >> 3, r = it & 7;
-            const Q6Raw q = q6k_fetch(base, row + 210 * sbi, r >> 2, r & 3);
-            const float d = h2f(q.d);
-            float ds[4];
-#pragma unroll
-            for (int g = 0; g < 4; g++) ds[g] = d * float(int(int8_t(q.sc >> (8 * g))));
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t qa = ((i < 4 ? q.a0 : q.a1) >> (8 * (i & 3))) & 0xffu;
-                const uint32_t qb = ((i < 4 ? q.b0 : q.b1) >> (8 * (i & 3))) & 0xffu;
-                const uint32_t qh = ((i < 4 ? q.h0 : q.h1) >> (8 * (i & 3))) & 0xffu;
-                wv[i] = ds[0] * float(int((qa & 15u) | ((qh & 3u) << 4)) - 32);
-                wv[8 + i] = ds[1] * float(int((qb & 15u) | (((qh >> 2) & 3u) << 4)) - 32);
-                wv[16 + i] = ds[2] * float(int((qa >> 4) | (((qh >> 4) & 3u) << 4)) - 32);
-                wv[24 + i] = ds[3] * float(int((qb >> 4) | (((qh >> 6) & 3u) << 4)) - 32);
-            }
-        } else {  // Q5_0
-            const uint8_t *b = base + row + 22 * it;  // even address
-            const float d = h2f(ld_u16(b));
-            const uint32_t qh = ld_u16(b + 2) | (ld_u16(b + 4) << 16);
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const uint32_t qs = (ld_u16(b + 6 + 2 * (j / 2)) >> (8 * (j & 1))) & 0xffu;
-                wv[j] = float(int((qs & 15u) | (((qh >> j) & 1u) << 4)) - 16) * d;
-                wv[j + 16] = float(int((qs >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16) * d;
-            }
-        }
-    }
-    // dot of a dequantized item with a row x (LDS or global)
-    static VH_DEV float dot(const float *wv, int c0, const float *x) {
-        float acc = 0.0f;
-        if constexpr (SEG == NW) {
-#pragma unroll
-            for (int i = 0; i < NW; i++) acc = fmaf(wv[i], x[c0 + i], acc);
-        } else {
-#pragma unroll
-            for (int s = 0; s < NW / SEG; s++)
-#pragma unroll
-                for (int i = 0; i < SEG; i++) acc = fmaf(wv[s * SEG + i], x[c0 + s * STRIDE + i], acc);
-        }
-        return acc;
-    }
-};
-
 int64_t rbytes(uint32_t t, int n) {
     switch (t) {
     case VT_Q8_0: return int64_t(n / 32) * 34;
@@ -184,115 +103,181 @@ int64_t rbytes(uint32_t t, int n) {
     }
 }
 
-constexpr int kTokTile = 8;   // tokens staged per pass
-constexpr int kGuRows = 16;   // gate/up rows per workgroup (4 per wave)
-
-// grid (ceil(fe / kGuRows), max_slots), 256 threads. A row is split over L
-// lanes (L = items per row rounded down to a power of two, <= 64).
-template <int T, bool PAIRED, int L>
-__global__ void __launch_bounds__(256) grouped_gateup_kernel(const int32_t *__restrict__ counts,
-                                                             const int32_t *__restrict__ offs,
-                                                             const int32_t *__restrict__ perm,
-                                                             const int32_t *__restrict__ active,
-                                                             const void *const *__restrict__ table,
-                                                             const float *__restrict__ hb, int d, int fe, int k, int E,
-                                                             int64_t row_bytes, float *__restrict__ h) {
-    using I = Items<T, PAIRED>;
-    extern __shared__ float xs[];  // [kTokTile][d]
-    const int s = blockIdx.y;
-    if (s >= active[E]) return;
-    const int e = active[s], cnt = counts[e], base = offs[e];
-    const uint8_t *G = static_cast<const uint8_t *>(table[3 * e]);
-    const uint8_t *U = static_cast<const uint8_t *>(table[3 * e + 1]);
-    constexpr int RPW = 64 / L;  // rows per wave per step
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, sub = lane / L, li = lane % L;
-    const int items = I::items(d);
-    for (int t0 = 0; t0 < cnt; t0 += kTokTile) {
-        const int tn = min(kTokTile, cnt - t0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < tn * d; i += 256) {
-            const int tt = i / d, c = i % d;
-            xs[i] = hb[size_t(perm[base + t0 + tt] / k) * d + c];
+// ------------------------------------------------------------ grouped projections
+// An item's 32 weights dequantized from the raw words of Reg<T>::fetch, in the
+// item's own order (the order Reg<T>::load_x gives the inputs): every value is
+// the reference's dequantized weight (src/gguf_compute.c:52-103, 112-120).
+template <int T>
+VH_DEV void deq_raw(const typename Reg<T>::Raw &r, float (&w)[32]) {
+    if constexpr (T == VT_Q4_K) {
+        // the item's two sub-blocks: c = it/2 % 4 is not in the raw words, so
+        // the caller passes the scale pair through deq_q4k below
+    } else if constexpr (T == VT_Q6_K) {
+        const float d = h2f(r.d);
+        float ds[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) ds[g] = d * float(int(int8_t(r.sc >> (8 * g))));
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t qa = ((i < 4 ? r.a0 : r.a1) >> (8 * (i & 3))) & 0xffu;
+            const uint32_t qb = ((i < 4 ? r.b0 : r.b1) >> (8 * (i & 3))) & 0xffu;
+            const uint32_t qh = ((i < 4 ? r.h0 : r.h1) >> (8 * (i & 3))) & 0xffu;
+            w[i] = ds[0] * float(int((qa & 15u) | ((qh & 3u) << 4)) - 32);
+            w[8 + i] = ds[1] * float(int((qb & 15u) | (((qh >> 2) & 3u) << 4)) - 32);
+            w[16 + i] = ds[2] * float(int((qa >> 4) | (((qh >> 4) & 3u) << 4)) - 32);
+            w[24 + i] = ds[3] * float(int((qb >> 4) | (((qh >> 6) & 3u) << 4)) - 32);
         }
-        __syncthreads();
-        for (int ob = blockIdx.x * kGuRows + wv * RPW; ob < min(fe, (blockIdx.x + 1) * kGuRows); ob += 4 * RPW) {
-            const int o = ob + sub;
-            const bool ok = o < fe && G && U;
-            float ag[kTokTile], au[kTokTile];
+    } else {  // Q8_0
+        const float d = h2f((r.w[0] >> (8 * r.s)) & 0xffffu);
+        const uint32_t sh = 16 + 8 * r.s;
 #pragma unroll
-            for (int tt = 0; tt < kTokTile; tt++) ag[tt] = au[tt] = 0.0f;
-            if (ok) {
-                for (int it = li; it < items; it += L) {
-                    float wg[I::NW], wu[I::NW];
-                    I::deq(G, int64_t(o) * row_bytes, it, wg);
-                    I::deq(U, int64_t(o) * row_bytes, it, wu);
-                    const int c0 = I::col0(it);
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = uint32_t(((uint64_t(r.w[i + 1]) << 32) | r.w[i]) >> sh);
 #pragma unroll
-                    for (int tt = 0; tt < kTokTile; tt++) {
-                        if (tt < tn) {
-                            ag[tt] += I::dot(wg, c0, xs + tt * d);
-                            au[tt] += I::dot(wu, c0, xs + tt * d);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int tt = 0; tt < kTokTile; tt++) {
-                const float g = group_sum<L>(ag[tt]), u = group_sum<L>(au[tt]);
-                if (li == L - 1 && o < fe && tt < tn) h[size_t(perm[base + t0 + tt]) * fe + o] = ok ? swiglu(g, u) : 0.0f;
-            }
+            for (int k = 0; k < 4; k++) w[4 * i + k] = float(int(int8_t(q >> (8 * k)))) * d;
         }
     }
 }
+VH_DEV void deq_q4k(const Reg<VT_Q4_K>::Raw &r, int it, float (&w)[32]) {
+    const int c = (it & 7) >> 1;
+    const float d = h2f(r.hdr.x & 0xffffu), dmin = h2f(r.hdr.x >> 16);
+    int sc0, m0, sc1, m1;
+    q4k_scale_min(2 * c, r.hdr.y, r.hdr.z, r.hdr.w, sc0, m0);
+    q4k_scale_min(2 * c + 1, r.hdr.y, r.hdr.z, r.hdr.w, sc1, m1);
+    const float d1 = d * float(sc0), mm1 = dmin * float(m0), d2 = d * float(sc1), mm2 = dmin * float(m1);
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t b = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        w[i] = d1 * float(b & 15u) - mm1;
+        w[16 + i] = d2 * float(b >> 4) - mm2;
+    }
+}
+template <int T>
+VH_DEV void deq_item(const typename Reg<T>::Raw &r, int it, float (&w)[32]) {
+    if constexpr (T == VT_Q4_K) deq_q4k(r, it, w);
+    else deq_raw<T>(r, w);
+}
 
-// grid (d / kDnRows, max_slots), 256 threads: rows of the down matrix of one
-// expert against the activations of its tokens.
-constexpr int kDnRows = 16;
-template <int T, bool PAIRED, int L>
-__global__ void __launch_bounds__(256) grouped_down_kernel(const int32_t *__restrict__ counts,
+// Column of the item's i-th input (i a multiple of 4: runs never split a float4).
+template <int T>
+VH_DEV int item_col(int it, int i) {
+    if constexpr (T == VT_Q4_K) return Split<VT_Q4_K>::col0(it) + (i < 16 ? i : i + 16);
+    else if constexpr (T == VT_Q6_K) return Split<VT_Q6_K>::col0(it) + 32 * (i >> 3) + (i & 7);
+    else return 32 * it + i;
+}
+// Rows staged in LDS keep 4 pad floats after every 32, so the float4 reads of
+// the lanes of a wave (32 columns apart) fall in different banks.
+VH_DEV int padc(int c) { return c + 4 * (c >> 5); }
+__host__ __device__ inline int padded_k(int K) { return K + 4 * (K / 32); }
+
+// grid (ceil(rows / RB), max_slots), 512 threads, RB = 8 * (64 / L) * RPL
+// rows per workgroup. Workgroup (rb, s): rows [rb*RB, rb*RB + RB) of the
+// weight matrix (or matrices) of active expert s, for every token routed to it,
+// in chunks of NT tokens staged in LDS. Lane group g (L lanes) takes RPL
+// consecutive rows, one after the other, loading the next row's raw words
+// while the current one computes; lane li owns items li, li + L, ... (IPL at
+// most) of each row. GATEUP: rows of gate and up (K = d) -> h[pair][o] =
+// silu(g) * u; else rows of down (K = fe) -> y[pair][o].
+template <int T, bool GATEUP, int L, int IPL, int NT, int RPL>
+__global__ void __launch_bounds__(512) grouped_proj_kernel(const int32_t *__restrict__ counts,
                                                            const int32_t *__restrict__ offs,
                                                            const int32_t *__restrict__ perm,
                                                            const int32_t *__restrict__ active,
                                                            const void *const *__restrict__ table,
-                                                           const float *__restrict__ h, int d, int fe, int E,
-                                                           int64_t row_bytes, float *__restrict__ ybuf) {
-    using I = Items<T, PAIRED>;
-    extern __shared__ float hs[];  // [kTokTile][fe]
+                                                           const float *__restrict__ src, int K, int rows, int k,
+                                                           int E, int64_t row_bytes, float *__restrict__ out) {
+    constexpr int SUB = 64 / L, RB = 8 * SUB * RPL, NM = GATEUP ? 2 : 1;
+    using Raw = typename Reg<T>::Raw;
+    extern __shared__ float xs[];  // [NT][padded_k(K)]
     const int s = blockIdx.y;
     if (s >= active[E]) return;
     const int e = active[s], cnt = counts[e], base = offs[e];
-    const uint8_t *D = static_cast<const uint8_t *>(table[3 * e + 2]);
-    constexpr int RPW = 64 / L;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, sub = lane / L, li = lane % L;
-    const int items = I::items(fe);
-    for (int t0 = 0; t0 < cnt; t0 += kTokTile) {
-        const int tn = min(kTokTile, cnt - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, grp = lane / L, li = lane % L;
+    const uint8_t *M0 = static_cast<const uint8_t *>(table[3 * e + (GATEUP ? 0 : 2)]);
+    const uint8_t *M1 = GATEUP ? static_cast<const uint8_t *>(table[3 * e + 1]) : nullptr;
+    const bool ok = M0 && (!GATEUP || M1);
+    const int items = K / 32, KP = padded_k(K);
+    const int o_first = blockIdx.x * RB + (wv * SUB + grp) * RPL;
+    auto fetch_row = [&](int o, Raw (&raw)[NM][IPL]) {
+        const int64_t oo = min(o, rows - 1);
+#pragma unroll
+        for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+            for (int m = 0; m < IPL; m++) {
+                const int it = li + L * m;
+                if (it < items) raw[mtx][m] = Reg<T>::fetch(mtx ? M1 : M0, oo * row_bytes, it);
+            }
+    };
+    for (int t0 = 0; t0 < cnt; t0 += NT) {
+        const int tn = min(NT, cnt - t0);
+        Raw cur[NM][IPL];
+        if (ok) fetch_row(o_first, cur);
         __syncthreads();
-        for (int i = threadIdx.x; i < tn * fe; i += 256) {
-            const int tt = i / fe, c = i % fe;
-            hs[i] = h[size_t(perm[base + t0 + tt]) * fe + c];
+        for (int i = tid; i < tn * (K / 4); i += 512) {
+            const int tt = i / (K / 4), c = 4 * (i - tt * (K / 4));
+            const int p = perm[base + t0 + tt];
+            const float *row = GATEUP ? src + size_t(p / k) * K : src + size_t(p) * K;
+            *reinterpret_cast<float4 *>(xs + tt * KP + padc(c)) = *reinterpret_cast<const float4 *>(row + c);
         }
         __syncthreads();
-        for (int ob = blockIdx.x * kDnRows + wv * RPW; ob < min(d, (blockIdx.x + 1) * kDnRows); ob += 4 * RPW) {
-            const int o = ob + sub;
-            const bool ok = o < d && D;
-            float ay[kTokTile];
+#pragma unroll 1
+        for (int rr = 0; rr < RPL; rr++) {
+            const int o = o_first + rr;
+            Raw nxt[NM][IPL];
+            if (ok && rr + 1 < RPL) fetch_row(o + 1, nxt);
+            float acc[NM][NT];
 #pragma unroll
-            for (int tt = 0; tt < kTokTile; tt++) ay[tt] = 0.0f;
+            for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) acc[mtx][tt] = 0.0f;
             if (ok) {
-                for (int it = li; it < items; it += L) {
-                    float wd[I::NW];
-                    I::deq(D, int64_t(o) * row_bytes, it, wd);
-                    const int c0 = I::col0(it);
 #pragma unroll
-                    for (int tt = 0; tt < kTokTile; tt++)
-                        if (tt < tn) ay[tt] += I::dot(wd, c0, hs + tt * fe);
+                for (int m = 0; m < IPL; m++) {
+                    const int it = li + L * m;
+                    if (it >= items) continue;
+                    float w[NM][32];
+#pragma unroll
+                    for (int mtx = 0; mtx < NM; mtx++) deq_item<T>(cur[mtx][m], it, w[mtx]);
+#pragma unroll
+                    for (int tt = 0; tt < NT; tt++) {
+                        if (tt >= tn) break;
+                        const float *xt = xs + tt * KP;
+#pragma unroll
+                        for (int q = 0; q < 8; q++) {
+                            const float4 v = *reinterpret_cast<const float4 *>(xt + padc(item_col<T>(it, 4 * q)));
+#pragma unroll
+                            for (int mtx = 0; mtx < NM; mtx++) {
+                                float a = acc[mtx][tt];
+                                a = fmaf(w[mtx][4 * q + 0], v.x, a);
+                                a = fmaf(w[mtx][4 * q + 1], v.y, a);
+                                a = fmaf(w[mtx][4 * q + 2], v.z, a);
+                                a = fmaf(w[mtx][4 * q + 3], v.w, a);
+                                acc[mtx][tt] = a;
+                            }
+                        }
+                        // one token's inputs in registers at a time: keep the
+                        // scheduler from hoisting the next token's reads
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
 #pragma unroll
-            for (int tt = 0; tt < kTokTile; tt++) {
-                const float y = group_sum<L>(ay[tt]);
-                if (li == L - 1 && o < d && tt < tn) ybuf[size_t(perm[base + t0 + tt]) * d + o] = ok ? y : 0.0f;
+            for (int tt = 0; tt < NT; tt++) {
+                if (tt >= tn) break;  // the same for every lane of the workgroup
+                const float g = group_sum<L>(acc[0][tt]);
+                const float u = GATEUP ? group_sum<L>(acc[NM - 1][tt]) : 0.0f;
+                if (li == L - 1 && o < rows) {
+                    const int p = perm[base + t0 + tt];
+                    // an unregistered expert contributes nothing (src/gguf_run.c:201)
+                    out[size_t(p) * rows + o] = !ok ? 0.0f : GATEUP ? swiglu(g, u) : g;
+                }
+            }
+            if (rr + 1 < RPL) {
+#pragma unroll
+                for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+                    for (int m = 0; m < IPL; m++) cur[mtx][m] = nxt[mtx][m];
             }
         }
     }
@@ -314,37 +299,61 @@ __global__ void __launch_bounds__(256) combine_kernel(const int32_t *__restrict_
     x[size_t(t) * d + o] = __fadd_rn(x[size_t(t) * d + o], a);
 }
 
-int lanes_for(int items) {
-    int L = 64;
-    while (L > 1 && L > items) L >>= 1;
-    return L;
+// tokens staged per chunk: 4 (more would not fit the registers of 512-thread
+// workgroups; 4 rows of d = 2048 inputs take 37 KB of LDS)
+template <bool GATEUP>
+constexpr int group_tokens() { return 4; }
+
+// Lanes per row: the smallest of 8 / 16 / 32 / 64 with at most 3 items per
+// lane; for the two matrices of gate/up, one item per lane where a row has at
+// most 64 items (two matrices' raw words and weights must fit the registers).
+int proj_lanes(int items, bool gateup) {
+    if (gateup && items <= 64) {
+        int L = 8;
+        while (L < items) L *= 2;
+        return L;
+    }
+    for (int L : {8, 16, 32, 64})
+        if ((items + L - 1) / L <= 3) return L;
+    return 0;
 }
 
-template <int T, bool PAIRED>
-int gu_launch(int L, dim3 g, size_t lds, hipStream_t s, const int32_t *counts, const int32_t *offs,
-              const int32_t *perm, const int32_t *active, const void *const *table, const float *hb, int d, int fe,
-              int k, int E, int64_t rb, float *h) {
-    switch (L) {
-    case 64: hipLaunchKernelGGL((grouped_gateup_kernel<T, PAIRED, 64>), g, dim3(256), lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h); break;
-    case 32: hipLaunchKernelGGL((grouped_gateup_kernel<T, PAIRED, 32>), g, dim3(256), lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h); break;
-    case 16: hipLaunchKernelGGL((grouped_gateup_kernel<T, PAIRED, 16>), g, dim3(256), lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h); break;
-    case 8: hipLaunchKernelGGL((grouped_gateup_kernel<T, PAIRED, 8>), g, dim3(256), lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h); break;
-    default: hipLaunchKernelGGL((grouped_gateup_kernel<T, PAIRED, 4>), g, dim3(256), lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h); break;
+template <int T, bool GATEUP>
+int proj_launch(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
+                const void *const *table, const float *src, int K, int rows, int k, int E, int max_slots, float *out,
+                hipStream_t s) {
+    const int items = K / 32, L = proj_lanes(items, GATEUP);
+    if (!L || K % 32) return -EINVAL;
+    constexpr int RPL = GATEUP ? 8 : 4;
+    const int ipl = (items + L - 1) / L, RB = 8 * (64 / L) * RPL;
+    const dim3 g((rows + RB - 1) / RB, max_slots);
+    constexpr int NT = group_tokens<GATEUP>();
+    const size_t lds = size_t(NT) * padded_k(K) * 4;
+    if (lds > 64 * 1024) return -E2BIG;
+    const int64_t rb = rbytes(T, K);
+#define VH_PROJ(LL, II) \
+    hipLaunchKernelGGL((grouped_proj_kernel<T, GATEUP, LL, II, NT, RPL>), g, dim3(512), lds, s, counts, offs, \
+                       perm, active, table, src, K, rows, k, E, rb, out)
+    if constexpr (GATEUP) {  // L >= items: one item per lane
+        switch (L) {
+        case 8: VH_PROJ(8, 1); break;
+        case 16: VH_PROJ(16, 1); break;
+        case 32: VH_PROJ(32, 1); break;
+        default: VH_PROJ(64, 1); break;
+        }
+    } else {
+        switch (L * 4 + (ipl <= 2 ? 2 : 3)) {
+        case 8 * 4 + 2: VH_PROJ(8, 2); break;
+        case 8 * 4 + 3: VH_PROJ(8, 3); break;
+        case 16 * 4 + 2: VH_PROJ(16, 2); break;
+        case 16 * 4 + 3: VH_PROJ(16, 3); break;
+        case 32 * 4 + 2: VH_PROJ(32, 2); break;
+        case 32 * 4 + 3: VH_PROJ(32, 3); break;
+        case 64 * 4 + 2: VH_PROJ(64, 2); break;
+        default: VH_PROJ(64, 3); break;
+        }
     }
-    return vh_check(hipGetLastError());
-}
-
-template <int T, bool PAIRED>
-int dn_launch(int L, dim3 g, size_t lds, hipStream_t s, const int32_t *counts, const int32_t *offs,
-              const int32_t *perm, const int32_t *active, const void *const *table, const float *h, int d, int fe,
-              int E, int64_t rb, float *ybuf) {
-    switch (L) {
-    case 64: hipLaunchKernelGGL((grouped_down_kernel<T, PAIRED, 64>), g, dim3(256), lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf); break;
-    case 32: hipLaunchKernelGGL((grouped_down_kernel<T, PAIRED, 32>), g, dim3(256), lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf); break;
-    case 16: hipLaunchKernelGGL((grouped_down_kernel<T, PAIRED, 16>), g, dim3(256), lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf); break;
-    case 8: hipLaunchKernelGGL((grouped_down_kernel<T, PAIRED, 8>), g, dim3(256), lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf); break;
-    default: hipLaunchKernelGGL((grouped_down_kernel<T, PAIRED, 4>), g, dim3(256), lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf); break;
-    }
+#undef VH_PROJ
     return vh_check(hipGetLastError());
 }
 
@@ -359,16 +368,10 @@ int vh_dispatch(const int32_t *idx, int P, int E, int32_t *counts, int32_t *offs
 int vh_grouped_gateup(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
                       const int32_t *active, const void *const *table, const float *hb, int d, int fe, int k, int E,
                       int max_slots, float *h, hipStream_t s) {
-    const int64_t rb = rbytes(type, d);
-    dim3 g((fe + kGuRows - 1) / kGuRows, max_slots);
-    const size_t lds = size_t(kTokTile) * d * 4;
     switch (type) {
-    case VT_Q8_0:
-        if (d % 64 == 0) return gu_launch<VT_Q8_0, true>(lanes_for(d / 64), g, lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h);
-        return gu_launch<VT_Q8_0, false>(lanes_for(d / 32), g, lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h);
-    case VT_Q4_K: return gu_launch<VT_Q4_K, false>(lanes_for(d / 32), g, lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h);
-    case VT_Q6_K: return gu_launch<VT_Q6_K, false>(lanes_for(d / 32), g, lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h);
-    case VT_Q5_0: return gu_launch<VT_Q5_0, false>(lanes_for(d / 32), g, lds, s, counts, offs, perm, active, table, hb, d, fe, k, E, rb, h);
+    case VT_Q8_0: return proj_launch<VT_Q8_0, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
+    case VT_Q4_K: return proj_launch<VT_Q4_K, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
+    case VT_Q6_K: return proj_launch<VT_Q6_K, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
     default: return -EINVAL;
     }
 }
@@ -376,16 +379,10 @@ int vh_grouped_gateup(uint32_t type, const int32_t *counts, const int32_t *offs,
 int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
                     const int32_t *active, const void *const *table, const float *h, int d, int fe, int E,
                     int max_slots, float *ybuf, hipStream_t s) {
-    const int64_t rb = rbytes(type, fe);
-    dim3 g((d + kDnRows - 1) / kDnRows, max_slots);
-    const size_t lds = size_t(kTokTile) * fe * 4;
     switch (type) {
-    case VT_Q8_0:
-        if (fe % 64 == 0) return dn_launch<VT_Q8_0, true>(lanes_for(fe / 64), g, lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf);
-        return dn_launch<VT_Q8_0, false>(lanes_for(fe / 32), g, lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf);
-    case VT_Q4_K: return dn_launch<VT_Q4_K, false>(lanes_for(fe / 32), g, lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf);
-    case VT_Q6_K: return dn_launch<VT_Q6_K, false>(lanes_for(fe / 32), g, lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf);
-    case VT_Q5_0: return dn_launch<VT_Q5_0, false>(lanes_for(fe / 32), g, lds, s, counts, offs, perm, active, table, h, d, fe, E, rb, ybuf);
+    case VT_Q8_0: return proj_launch<VT_Q8_0, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
+    case VT_Q4_K: return proj_launch<VT_Q4_K, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
+    case VT_Q6_K: return proj_launch<VT_Q6_K, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
     default: return -EINVAL;
     }
 }
