@@ -3,7 +3,8 @@ src/gguf_run.c:185-214, restated) and against the golden vectors the
 reference itself wrote, on both execution plans.
 
 Bar: the routed experts bit-exact; the layer's contribution (x_out - x)
-within 2e-3 of its largest magnitude; the mean absolute error is printed.
+within 2e-3 of its largest magnitude (1e-2 where groups run as bf16
+matrix-core GEMMs); the mean absolute error is printed.
 """
 import numpy as np
 import pytest
@@ -16,6 +17,7 @@ from vireo_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+TOL_BF16 = 1e-2  # groups of >= 16 tokens in calls of >= 64 tokens: bf16 GEMMs
 
 
 @pytest.fixture
@@ -36,13 +38,13 @@ def oracle_layer(oracle, m, layer, x, hb, tokens=None):
     return oracle.moe_ffn(shape, m.host_router(layer), G, U, D, x[sel], hb[sel], bias=bias)
 
 
-def check(name, x, xg, xo, idx_g, idx_o):
+def check(name, x, xg, xo, idx_g, idx_o, tol=TOL):
     np.testing.assert_array_equal(idx_g, idx_o)
     dg, do = xg - x, xo - x
     err = np.abs(dg - do)
     rel = err.max() / np.abs(do).max()
     print(f"{name}: max rel {rel:.2e}  mean abs {err.mean():.2e}")
-    assert rel <= TOL
+    assert rel <= tol
 
 
 CONFIGS = [("olmoe-q8_0", 1), ("olmoe-q4_k_m", 1), ("olmoe-q4_k_m", 4), ("olmoe-q4_k_m", 16),
@@ -162,7 +164,79 @@ def test_prefill_2048_zipf(cuda, oracle):
     np.testing.assert_array_equal(ig, oi)
     sample = np.array([0, 1, 777, 1500, 2047])
     xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
-    check("prefill sample", x[sample], xt.cpu().numpy()[sample], xo, ig[sample], io)
+    check("prefill sample", x[sample], xt.cpu().numpy()[sample], xo, ig[sample], io, tol=TOL_BF16)
+    m.close()
+
+
+def oracle_routing(oracle, m, hb, bias=None):
+    shape = m.shape
+    router = m.host_router(0)
+    out = np.empty((len(hb), shape.k), dtype=np.int32)
+    for t in range(len(hb)):
+        lg = oracle.matmul(W.F32, router, hb[t], shape.d, shape.E)
+        if bias is not None:
+            lg = (lg + bias).astype(np.float32)
+        out[t] = oracle.topk(oracle.softmax(lg), shape.k, shape.renorm)[0]
+    return out
+
+
+# (model, tokens, Zipf router bias): groups of >= 16 tokens (several 128-row
+# tiles, ragged last tiles under the bias) next to smaller groups
+MFMA_CASES = [("qwen3-30b-a3b-q8_0", 512, True), ("olmoe-q4_k_m", 128, False), ("qwen3-30b-a3b-q4_k_m", 128, False)]
+
+
+@pytest.mark.parametrize("name,T,zipf", MFMA_CASES)
+@pytest.mark.parametrize("plan", [0, 4])
+def test_grouped_plan_large_groups(cuda, oracle, path, name, T, zipf, plan):
+    """Calls with groups of >= 16 tokens: under plan 0 those groups run as
+    bf16 matrix-core GEMMs and the rest on the fp32 kernels; plan 4 runs all
+    of them on the fp32 kernels. Every token's experts bit-exact; a sample of
+    tokens against the oracle; the same call twice gives the same bits."""
+    path(plan)
+    shape = W.SHAPES[name]
+    bias = W.zipf_bias(shape.E, 1.1, seed=8) if zipf else None
+    m = M.DeviceMoE(shape, 1, seed=59, logit_bias=bias)
+    x, hb = W.host_hidden(shape.d, T, 59)
+    hbt = torch.from_numpy(hb).to(cuda)
+    outs = []
+    for _ in range(2):
+        xt = torch.from_numpy(x).to(cuda)
+        idx, _ = m.forward(0, xt, hbt, return_routing=True)
+        outs.append(xt.cpu().numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ig = idx.cpu().numpy()
+    np.testing.assert_array_equal(ig, oracle_routing(oracle, m, hb, bias))
+    counts = np.bincount(ig.ravel(), minlength=shape.E)
+    assert counts.max() >= 16 and ((counts > 0) & (counts < 16)).any(), counts
+    if zipf:
+        assert counts.max() > 128, counts.max()
+    sample = np.unique(np.concatenate([np.arange(0, T, T // 10), [T - 1]]))
+    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
+    check(f"{name} T={T} plan={plan}", x[sample], outs[0][sample], xo, ig[sample], io,
+          tol=TOL_BF16 if plan == 0 else TOL)
+    m.close()
+
+
+def test_grouped_plan_large_groups_unregistered(cuda, oracle, path):
+    """Unregistered experts among the matrix-core groups contribute nothing."""
+    path(0)
+    shape = W.SHAPES["olmoe-q4_k_m"]
+    T = 256
+    x, hb = W.host_hidden(shape.d, T, 60)
+    probe = M.DeviceMoE(shape, 1, seed=60)
+    ig = probe.route(0, torch.from_numpy(hb).to(cuda))[0].cpu().numpy()
+    probe.close()
+    counts = np.bincount(ig.ravel(), minlength=shape.E)
+    big = np.argsort(-counts, kind="stable")
+    drop = {(0, int(big[0])), (0, int(big[5]))}
+    m = M.DeviceMoE(shape, 1, seed=60, unregistered=drop)
+    m._unregistered = drop
+    xt = torch.from_numpy(x).to(cuda)
+    idx, _ = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    sample = np.flatnonzero((ig == big[0]).any(axis=1))[:6]
+    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
+    check("unregistered large groups", x[sample], xt.cpu().numpy()[sample], xo, idx.cpu().numpy()[sample], io,
+          tol=TOL_BF16)
     m.close()
 
 

@@ -25,6 +25,17 @@ int vh_finish(hipStream_t s, int rc);  // synchronise when the caller passed no 
 int vh_device_workspace(size_t bytes, void **out);  // per-device scratch, grown on demand
 int vh_counters(int n, unsigned **out);              // per-device zeroed counters (self-resetting use)
 int vh_num_cus();
+// bytes of a row of n weights of ggml type t (src/gguf.c:27-38; F32 otherwise)
+inline int64_t vh_row_bytes(uint32_t t, int n) {
+    switch (t) {
+    case VT_Q8_0: return int64_t(n / 32) * 34;
+    case VT_Q4_K: return int64_t(n / 256) * 144;
+    case VT_Q6_K: return int64_t(n / 256) * 210;
+    case VT_Q5_0: return int64_t(n / 32) * 22;
+    case VT_F16: return int64_t(n) * 2;
+    default: return int64_t(n) * 4;
+    }
+}
 
 // ---- loads ------------------------------------------------------------------
 // All quantized rows used here are made of 2-byte units and start 4-byte

@@ -1,5 +1,5 @@
 // moe_route / moe_dispatch / moe_ffn_forward: host orchestration of the MoE
-// kernels (route.hip, moe_decode.hip, moe_grouped.hip).
+// kernels (route.hip, moe_decode.hip, moe_grouped.hip, moe_mfma.hip).
 //
 // Reference: moe_ffn, src/gguf_run.c:185-214. Two execution plans produce its
 // result for a batch of independent tokens:
@@ -8,7 +8,9 @@
 //   grouped (any count): router -> top-k -> dispatch -> grouped gate/up ->
 //                        grouped down -> combine + residual      (6 kernels)
 // The grouped plan reads each routed expert's weights once per call however
-// many tokens chose it.
+// many tokens chose it. In calls of at least kMfmaMinCall tokens, groups of at
+// least kMfmaMinTokens tokens run as bf16 matrix-core GEMMs (moe_mfma.hip;
+// 3 more kernels) and only the smaller groups on the fp32 grouped kernels.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -18,7 +20,9 @@
 
 namespace {
 
-int g_path = 0;  // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the fused experts kernel
+// 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the
+// fused experts kernel, 4 grouped plan without the matrix-core GEMMs
+int g_path = 0;
 constexpr int kExactRouteTokens = 64;  // from this many tokens on, exact sequential logits
 
 bool type_ok(uint32_t t, int n) {
@@ -48,9 +52,11 @@ struct Ws {
     uint32_t *flags;
     uint32_t *bar;  // decode plan: kFusedBlocks barrier flags, then the token's flag word
     DecodePlan *plan;
+    int32_t *tiles, *small;  // matrix-core plan: token tiles, the other groups
+    void *hs;                // matrix-core plan: bf16 h rows in dispatch order
 };
 
-int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws) {
+int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false) {
     const size_t P = size_t(T) * k;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
@@ -62,6 +68,9 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
                  o_active = take(size_t(E + 1) * 4);
     const size_t o_h = experts ? take(P * fe * 4) : 0;
     const size_t o_y = (experts && grouped) ? take(P * d * 4) : 0;
+    const size_t o_tiles = mfma ? take((1 + 2 * size_t(vh_mfma_max_tiles(int(P), E))) * 4) : 0;
+    const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
+    const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     void *base;
     if (int rc = vh_device_workspace(off, &base)) return rc;
     char *b = static_cast<char *>(base);
@@ -77,6 +86,9 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->active = reinterpret_cast<int32_t *>(b + o_active);
     ws->h = experts ? reinterpret_cast<float *>(b + o_h) : nullptr;
     ws->ybuf = (experts && grouped) ? reinterpret_cast<float *>(b + o_y) : nullptr;
+    ws->tiles = mfma ? reinterpret_cast<int32_t *>(b + o_tiles) : nullptr;
+    ws->small = mfma ? reinterpret_cast<int32_t *>(b + o_small) : nullptr;
+    ws->hs = mfma ? b + o_hs : nullptr;
     return 0;
 }
 
@@ -225,7 +237,7 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
 }
 
 extern "C" int vireo_hip_set_path(int path) {
-    if (path < 0 || path > 3) return -EINVAL;
+    if (path < 0 || path > 4) return -EINVAL;
     g_path = path;
     return 0;
 }
@@ -274,10 +286,12 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     hipStream_t s = static_cast<hipStream_t>(stream);
     const float *R = static_cast<const float *>(L.router->data);
 
-    const bool decode = n_tokens == 1 && g_path != 2 && decode_supported(m, layer) &&
+    const bool decode = n_tokens == 1 && g_path != 2 && g_path != 4 && decode_supported(m, layer) &&
                         (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
+    const bool mfma = !decode && g_path != 4 && n_tokens >= kMfmaMinCall && vh_mfma_supported(tg, td, d, fe, E) &&
+                      (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
     Ws ws;
-    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws)) return rc;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws, mfma)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
@@ -294,8 +308,18 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
-    if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
-    if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    // groups of at least kMfmaMinTokens tokens on the matrix cores, the rest
+    // (listed in ws.small) on the fp32 kernels
+    const int32_t *act = ws.active;
+    if (mfma) {
+        const int mt = vh_mfma_max_tiles(P, E);
+        if (!rc) rc = vh_mfma_plan(ws.counts, E, kMfmaMinTokens, ws.tiles, ws.small, s);
+        if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, hb, d, fe, k, ws.hs, s);
+        if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
+        act = ws.small;
+    }
+    if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
+    if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
     return vh_finish(s, rc);
 }

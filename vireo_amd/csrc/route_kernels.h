@@ -43,6 +43,24 @@ int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, c
 int vh_combine(const int32_t *idx, const float *w, const void *const *table, const float *ybuf, int d, int k, int T,
                float *x, hipStream_t s);
 
+// Matrix-core grouped GEMMs (moe_mfma.hip) for groups of at least
+// kMfmaMinTokens tokens, in calls of at least kMfmaMinCall tokens (below that
+// no group is expected to reach the size). vh_mfma_plan lists their token
+// tiles in tiles[0 .. 1 + 2 * vh_mfma_max_tiles) and the other non-empty groups
+// in small[E + 1] (the `active` format); gate/up writes bf16 h rows in dispatch
+// order into hs [P x fe]; down writes ybuf rows like vh_grouped_down.
+constexpr int kMfmaMinTokens = 16;
+constexpr int kMfmaMinCall = 64;
+bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E);
+int vh_mfma_max_tiles(int P, int E);
+int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, int32_t *small, hipStream_t s);
+int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
+                   const int32_t *perm, const void *const *table, const float *hb, int d, int fe, int k, void *hs,
+                   hipStream_t s);
+int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
+                 const int32_t *perm, const void *const *table, const void *hs, int d, int fe, float *ybuf,
+                 hipStream_t s);
+
 // Fused one-token experts kernel (moe_fused.hip): top-k, gate/up, down and
 // combine in one launch of kFusedBlocks workgroups that meet once through
 // bar[0 .. kFusedBlocks) (zeroed by vh_route_parts); bar[kFusedBlocks] is the
