@@ -87,10 +87,18 @@ def test_route_zipf_bias(cuda, oracle):
     m.close()
 
 
-@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (7, 8, 64), (2048, 8, 128), (300, 1, 256), (33, 4, 8)])
-def test_dispatch_is_a_stable_sort(cuda, T, k, E):
+@pytest.mark.parametrize("T,k,E,skew", [(1, 8, 128, 0), (7, 8, 64, 0), (2048, 8, 128, 0), (300, 1, 256, 0),
+                                         (33, 4, 8, 0), (256, 8, 64, 0), (257, 8, 64, 0), (4096, 8, 128, 1.1),
+                                         (1000, 3, 256, 1.1)])
+def test_dispatch_is_a_stable_sort(cuda, T, k, E, skew):
+    """One-workgroup form up to 2048 pairs, per-expert form above (256 x 8 and
+    257 x 8 straddle the switch); skew draws experts with Zipf weights."""
     rng = np.random.default_rng(T * k + E)
-    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    p = None
+    if skew:
+        p = 1.0 / np.arange(1, E + 1) ** skew
+        p /= p.sum()
+    idx = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
     counts, offs, perm = M.dispatch(torch.from_numpy(idx).to(cuda), E)
     flat = idx.reshape(-1)
     np.testing.assert_array_equal(counts.cpu().numpy(), np.bincount(flat, minlength=E))

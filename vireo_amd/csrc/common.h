@@ -45,6 +45,28 @@ inline int64_t vh_row_bytes(uint32_t t, int n) {
 VH_DEV uint32_t ld_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 VH_DEV uint32_t ld_u16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
 VH_DEV uint32_t ld_u8(const uint8_t *p) { return *p; }
+
+// Global-memory views of pointers the compiler cannot trace to a kernel
+// argument (expert tables hold generic pointers): loads through them are
+// global_load, not flat_load, which would also count against the LDS wait
+// counter and make every LDS wait drain the weight prefetches.
+typedef const __attribute__((address_space(1))) uint8_t gbyte;
+VH_DEV gbyte *gmem(const void *p) { return (gbyte *)p; }
+template <class V>
+VH_DEV V ldg(gbyte *p) { return *(const __attribute__((address_space(1))) V *)p; }  // scalar or ext_vector V
+VH_DEV uint32_t ld_u32(gbyte *p) { return ldg<uint32_t>(p); }
+VH_DEV uint32_t ld_u16(gbyte *p) { return ldg<uint16_t>(p); }
+VH_DEV uint32_t ld_u8(gbyte *p) { return *p; }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+VH_DEV uint2 ld_u64(gbyte *p) {
+    const u32x2 v = ldg<u32x2>(p);
+    return make_uint2(v.x, v.y);
+}
+VH_DEV uint4 ld_u128(gbyte *p) {
+    const u32x4 v = ldg<u32x4>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 VH_DEV uint32_t align2(uint32_t hi, uint32_t lo, uint32_t bytes) { return __builtin_amdgcn_alignbyte(hi, lo, bytes); }
 
 // ---- binary16 -> binary32 (exact; v_cvt_f32_f16) --------------------------------

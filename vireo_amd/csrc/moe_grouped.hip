@@ -19,6 +19,9 @@
 namespace {
 
 constexpr int kDispWaves = 16;
+// up to this many pairs one workgroup dispatches (one launch, shorter); above,
+// the two-kernel form with a workgroup per expert
+constexpr int kDispatchOneBlock = 2048;
 
 // One workgroup of 16 waves (see moe_dispatch in include/vireo_hip.h).
 __global__ void __launch_bounds__(1024) dispatch_kernel(const int32_t *__restrict__ idx, int P, int E,
@@ -100,6 +103,87 @@ int64_t rbytes(uint32_t t, int n) {
     case VT_Q4_K: return int64_t(n / 256) * 144;
     case VT_Q6_K: return int64_t(n / 256) * 210;
     default: return int64_t(n / 32) * 22;  // Q5_0
+    }
+}
+
+// Large calls: one workgroup per expert, twice. dispatch_count_kernel counts
+// the pairs of expert blockIdx.x; dispatch_place_kernel sums the counts of the
+// experts before it (its bucket offset and its rank among the non-empty
+// experts) and writes its pairs in pair order: blocks of 16 consecutive pairs
+// per thread, a block scan of the per-thread matches giving each its slot.
+constexpr int kPlacePer = 16;
+
+VH_DEV int block_excl_scan(int v, int &total, int (&wsum)[4]) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+        const int o = __shfl_up(inc, sh, 64);
+        if (lane >= sh) inc += o;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        before += w < wv ? wsum[w] : 0;
+        total += wsum[w];
+    }
+    __syncthreads();  // wsum is reused by the next call
+    return before + inc - v;
+}
+
+__global__ void __launch_bounds__(256) dispatch_count_kernel(const int32_t *__restrict__ idx, int P,
+                                                             int32_t *__restrict__ counts) {
+    __shared__ int wsum[4];
+    const int e = blockIdx.x;
+    int c = 0;
+    for (int p = threadIdx.x; p < P; p += 256) c += idx[p] == e ? 1 : 0;
+    int total;
+    block_excl_scan(c, total, wsum);
+    if (threadIdx.x == 0) counts[e] = total;
+}
+
+__global__ void __launch_bounds__(256) dispatch_place_kernel(const int32_t *__restrict__ idx, int P, int E,
+                                                             const int32_t *__restrict__ counts,
+                                                             int32_t *__restrict__ offs, int32_t *__restrict__ perm,
+                                                             int32_t *__restrict__ active) {
+    __shared__ int wsum[4];
+    const int e = blockIdx.x, tid = threadIdx.x;
+    int o = 0, a = 0;
+    for (int i = tid; i < e; i += 256) {
+        const int c = counts[i];
+        o += c;
+        a += c > 0 ? 1 : 0;
+    }
+    int base, rank;
+    block_excl_scan(o, base, wsum);
+    block_excl_scan(a, rank, wsum);
+    const int mine = counts[e];
+    if (tid == 0) {
+        offs[e] = base;
+        if (active && mine > 0) active[rank] = e;
+        if (e == E - 1) {
+            offs[E] = base + mine;
+            if (active) active[E] = rank + (mine > 0 ? 1 : 0);
+        }
+    }
+    int run = base;
+    for (int p0 = 0; p0 < P; p0 += 256 * kPlacePer) {
+        const int q0 = p0 + kPlacePer * tid;
+        uint32_t hit = 0;
+#pragma unroll
+        for (int j = 0; j < kPlacePer; j++)
+            if (q0 + j < P && idx[q0 + j] == e) hit |= 1u << j;
+        int total;
+        int pos = run + block_excl_scan(__popc(hit), total, wsum);
+        while (hit) {
+            const int j = __ffs(hit) - 1;
+            perm[pos++] = q0 + j;
+            hit &= hit - 1u;
+        }
+        run += total;
     }
 }
 
@@ -361,7 +445,12 @@ int proj_launch(const int32_t *counts, const int32_t *offs, const int32_t *perm,
 
 int vh_dispatch(const int32_t *idx, int P, int E, int32_t *counts, int32_t *offs, int32_t *perm, int32_t *active,
                 hipStream_t s) {
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, idx, P, E, counts, offs, perm, active);
+    if (P <= kDispatchOneBlock) {
+        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, idx, P, E, counts, offs, perm, active);
+    } else {
+        hipLaunchKernelGGL(dispatch_count_kernel, dim3(E), dim3(256), 0, s, idx, P, counts);
+        hipLaunchKernelGGL(dispatch_place_kernel, dim3(E), dim3(256), 0, s, idx, P, E, counts, offs, perm, active);
+    }
     return vh_check(hipGetLastError());
 }
 

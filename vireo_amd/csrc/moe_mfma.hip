@@ -36,15 +36,22 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBM = 128, kBK = 64, kBRows = 128, kThreads = 256;
 constexpr int kChunks = kBK / 8;  // 16-byte chunks per row and K step
 
-// 8 bytes at even byte offset c of a 4-aligned tensor, read from aligned
-// words that never leave [c - 2, c + 8)
-VH_DEV uint2 ld8_even(const uint8_t *base, int64_t c) {
-    const uint32_t sh = uint32_t(c) & 3u;
-    const uint8_t *a = base + (c - int64_t(sh));
-    const uint32_t w0 = ld_u32(a), w1 = ld_u32(a + 4);
-    const uint32_t w2 = sh ? ld_u16(a + 8) : 0u;
-    return make_uint2(align2(w1, w0, sh), align2(w2, w1, sh));
-}
+// 8 bytes at even byte offset c of a 4-aligned tensor, from aligned words
+// that never leave [c - 2, c + 8): fetched into (w0, w1, w2) at load time,
+// shifted into place (sh = c & 3 bytes) only when the values are needed, so
+// the loads stay in flight across the MFMAs.
+struct Even8 {
+    uint32_t w0, w1, w2, sh;
+    VH_DEV void load(gbyte *base, int64_t c) {
+        sh = uint32_t(c) & 3u;
+        gbyte *a = base + (c - int64_t(sh));
+        w0 = ld_u32(a);
+        w1 = ld_u32(a + 4);
+        w2 = ld_u16(a + (sh ? 8 : 6));  // bytes c+6, c+7 (unused when sh == 0)
+    }
+    VH_DEV uint32_t lo() const { return align2(w1, w0, sh); }
+    VH_DEV uint32_t hi() const { return align2(w2, w1, sh); }
+};
 
 // The raw bytes of 8 consecutive weights (columns c .. c+7, c a multiple of 8)
 // of the row at byte offset ro of the 4-aligned tensor m, and their
@@ -55,17 +62,18 @@ struct Chunk;
 
 template <>
 struct Chunk<VT_Q8_0> {  // src/gguf_compute.c:112-120: y = qs * d, exact
-    uint2 q;
+    Even8 q;
     uint32_t d;
-    VH_DEV void load(const uint8_t *m, int64_t ro, int c) {
+    VH_DEV void load(gbyte *m, int64_t ro, int c) {
         const int64_t b = ro + 34 * int64_t(c >> 5);
         d = ld_u16(m + b);
-        q = ld8_even(m, b + 2 + (c & 31));
+        q.load(m, b + 2 + (c & 31));
     }
     VH_DEV void values(float (&v)[8]) const {
         const float s = h2f(d);
+        const uint32_t w[2] = {q.lo(), q.hi()};
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = float(int(int8_t(((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xffu))) * s;
+        for (int i = 0; i < 8; i++) v[i] = float(int(int8_t((w[i >> 2] >> (8 * (i & 3))) & 0xffu))) * s;
     }
 };
 
@@ -74,12 +82,12 @@ struct Chunk<VT_Q4_K> {  // src/gguf_compute.c:52-66: y = (d*sc)*q - dmin*m
     uint4 hdr;
     uint2 q;
     int c;
-    VH_DEV void load(const uint8_t *m, int64_t ro, int col) {
-        const uint8_t *sb = m + ro + 144 * int64_t(col >> 8);
+    VH_DEV void load(gbyte *m, int64_t ro, int col) {
+        gbyte *sb = m + ro + 144 * int64_t(col >> 8);
         const int cc = col & 255;
         c = cc;
-        hdr = *reinterpret_cast<const uint4 *>(sb);
-        q = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * (cc >> 6) + (cc & 31));
+        hdr = ld_u128(sb);
+        q = ld_u64(sb + 16 + 32 * (cc >> 6) + (cc & 31));
     }
     VH_DEV void values(float (&v)[8]) const {
         const int j = 2 * (c >> 6) + ((c >> 5) & 1);  // sub-block; odd ones take the high nibbles
@@ -97,15 +105,15 @@ struct Chunk<VT_Q4_K> {  // src/gguf_compute.c:52-66: y = (d*sc)*q - dmin*m
 
 template <>
 struct Chunk<VT_Q6_K> {  // src/gguf_compute.c:83-103: y = (d*sc)*(q - 32)
-    uint2 ql, qh;
+    Even8 ql, qh;
     uint32_t d, sc;
     int c;
-    VH_DEV void load(const uint8_t *m, int64_t ro, int col) {
+    VH_DEV void load(gbyte *m, int64_t ro, int col) {
         const int64_t sbo = ro + 210 * int64_t(col >> 8);
         const int i = col & 255, h = i >> 7, g = (i >> 5) & 3, l = i & 31;
         c = i;
-        ql = ld8_even(m, sbo + 64 * h + 32 * (g & 1) + l);
-        qh = ld8_even(m, sbo + 128 + 32 * h + l);
+        ql.load(m, sbo + 64 * h + 32 * (g & 1) + l);
+        qh.load(m, sbo + 128 + 32 * h + l);
         sc = ld_u8(m + sbo + 192 + 8 * h + (l >> 4) + 2 * g);
         d = ld_u16(m + sbo + 208);
     }
@@ -113,10 +121,11 @@ struct Chunk<VT_Q6_K> {  // src/gguf_compute.c:83-103: y = (d*sc)*(q - 32)
         const int g = (c >> 5) & 3;
         const float s = h2f(d) * float(int(int8_t(sc)));
         const uint32_t lsh = g >= 2 ? 4u : 0u, hsh = 2u * uint32_t(g);
+        const uint32_t l2[2] = {ql.lo(), ql.hi()}, h2[2] = {qh.lo(), qh.hi()};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const uint32_t lo = (((i < 4 ? ql.x : ql.y) >> (8 * (i & 3))) >> lsh) & 15u;
-            const uint32_t hi = (((i < 4 ? qh.x : qh.y) >> (8 * (i & 3))) >> hsh) & 3u;
+            const uint32_t lo = ((l2[i >> 2] >> (8 * (i & 3))) >> lsh) & 15u;
+            const uint32_t hi = ((h2[i >> 2] >> (8 * (i & 3))) >> hsh) & 3u;
             v[i] = s * float(int(lo | (hi << 4)) - 32);
         }
     }
@@ -152,8 +161,8 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv >> 1, wn = wv & 1;
     const int n0 = blockIdx.x * (GATEUP ? 64 : 128);
 
-    const uint8_t *M0 = static_cast<const uint8_t *>(table[3 * e + (GATEUP ? 0 : 2)]);
-    const uint8_t *M1 = GATEUP ? static_cast<const uint8_t *>(table[3 * e + 1]) : M0;
+    gbyte *M0 = gmem(table[3 * e + (GATEUP ? 0 : 2)]);
+    gbyte *M1 = GATEUP ? gmem(table[3 * e + 1]) : M0;
     if (!M0 || !M1) {
         // an unregistered expert contributes nothing (src/gguf_run.c:201): its
         // h rows are zero, and the combine skips its y rows
@@ -169,7 +178,7 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
     // (rows past the group read its last row and stage zeros)
     const uint8_t *arow[4];
     bool aval[4];
-    const uint8_t *bmat[4];
+    gbyte *bmat[4];
     int64_t boff[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {

@@ -36,31 +36,72 @@ __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict
 
 constexpr int kExTok = 64, kExExp = 16, kExChunk = 64;
 
-// grid (ceil(T/64), ceil(E/16)), 256 threads: thread (token tid%64, experts
-// 4*(tid/64) .. +3 of the tile). Router and token chunks go through LDS.
+// grid (ceil(T/64), ceil(E/16)), 256 threads: lane = token t0 + lane, wave g
+// = experts e0 + 4g .. +3 (four independent in-order chains per lane). Each
+// 64-column chunk of the tokens' inputs (transposed, xs[column][token], padded
+// so that both the staging writes and the per-column reads are conflict-free)
+// and of the 16 router rows (read four columns at a time, one address for the
+// whole wave) goes through LDS; the next chunk is loaded into registers while
+// the current one is summed.
 __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restrict__ R, const float *__restrict__ hb,
                                                           const float *__restrict__ bias, int d, int E, int T,
                                                           RoutePart *__restrict__ parts) {
-    __shared__ float xs[kExTok][kExChunk + 1];
-    __shared__ float rs[kExExp][kExChunk];
+    __shared__ float xs[kExChunk][kExTok + 1];
+    __shared__ float4 rs[kExExp][kExChunk / 4];
     const int tid = threadIdx.x, tl = tid & 63, g = tid >> 6;
     const int t0 = blockIdx.x * kExTok, e0 = blockIdx.y * kExExp;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c0 = 0; c0 < d; c0 += kExChunk) {
-        const int cn = min(kExChunk, d - c0);
-        for (int i = tid; i < kExTok * kExChunk; i += 256) {
-            const int tt = i / kExChunk, cc = i % kExChunk;
-            xs[tt][cc] = (t0 + tt < T && cc < cn) ? hb[size_t(t0 + tt) * d + c0 + cc] : 0.0f;
-        }
-        for (int i = tid; i < kExExp * kExChunk; i += 256) {
-            const int ee = i / kExChunk, cc = i % kExChunk;
-            rs[ee][cc] = (e0 + ee < E && cc < cn) ? R[size_t(e0 + ee) * d + c0 + cc] : 0.0f;
-        }
-        __syncthreads();
-        for (int i = 0; i < cn; i++) {
-            const float xv = xs[tl][i];
+    // staging: thread tid loads column tid & 63 of token rows (tid >> 6) + 4j
+    // (j < 16) and of router rows (tid >> 6) + 4j (j < 4)
+    const int cc = tid & 63, r0 = tid >> 6;
+    float xr[16], rr[4];
+    auto load = [&](int c0) {
+        const bool in = c0 + cc < d;
 #pragma unroll
-            for (int q = 0; q < 4; q++) acc[q] = __fadd_rn(acc[q], __fmul_rn(rs[4 * g + q][i], xv));
+        for (int j = 0; j < 16; j++) {
+            const int tt = r0 + 4 * j;
+            xr[j] = (in && t0 + tt < T) ? hb[size_t(t0 + tt) * d + c0 + cc] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int ee = r0 + 4 * j;
+            rr[j] = (in && e0 + ee < E) ? R[size_t(e0 + ee) * d + c0 + cc] : 0.0f;
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < 16; j++) xs[cc][r0 + 4 * j] = xr[j];
+#pragma unroll
+        for (int j = 0; j < 4; j++) reinterpret_cast<float *>(&rs[r0 + 4 * j][0])[cc] = rr[j];
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    for (int c0 = 0; c0 < d; c0 += kExChunk) {
+        store();
+        __syncthreads();
+        if (c0 + kExChunk < d) load(c0 + kExChunk);
+        if (d - c0 >= kExChunk) {
+#pragma unroll
+            for (int i4 = 0; i4 < kExChunk / 4; i4++) {
+                float4 r[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) r[q] = rs[4 * g + q][i4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float xv = xs[4 * i4 + u][tl];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float rv = u == 0 ? r[q].x : u == 1 ? r[q].y : u == 2 ? r[q].z : r[q].w;
+                        acc[q] = __fadd_rn(acc[q], __fmul_rn(rv, xv));
+                    }
+                }
+            }
+        } else {  // the last, partial chunk: only its d - c0 columns
+            for (int i = 0; i < d - c0; i++) {
+                const float xv = xs[i][tl];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    acc[q] = __fadd_rn(acc[q], __fmul_rn(reinterpret_cast<const float *>(&rs[4 * g + q][0])[i], xv));
+            }
         }
         __syncthreads();
     }
