@@ -10,7 +10,7 @@
 // The grouped plan reads each routed expert's weights once per call however
 // many tokens chose it. In calls of at least kMfmaMinCall tokens, groups of at
 // least kMfmaMinTokens tokens run as bf16 matrix-core GEMMs (moe_mfma.hip;
-// 3 more kernels) and only the smaller groups on the fp32 grouped kernels.
+// 4 more kernels) and only the smaller groups on the fp32 grouped kernels.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -54,6 +54,7 @@ struct Ws {
     DecodePlan *plan;
     int32_t *tiles, *small;  // matrix-core plan: token tiles, the other groups
     void *hs;                // matrix-core plan: bf16 h rows in dispatch order
+    void *xb;                // matrix-core plan: bf16 copy of hb
 };
 
 int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false) {
@@ -71,6 +72,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_tiles = mfma ? take((1 + 2 * size_t(vh_mfma_max_tiles(int(P), E))) * 4) : 0;
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
+    const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
     void *base;
     if (int rc = vh_device_workspace(off, &base)) return rc;
     char *b = static_cast<char *>(base);
@@ -89,6 +91,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->tiles = mfma ? reinterpret_cast<int32_t *>(b + o_tiles) : nullptr;
     ws->small = mfma ? reinterpret_cast<int32_t *>(b + o_small) : nullptr;
     ws->hs = mfma ? b + o_hs : nullptr;
+    ws->xb = mfma ? b + o_xb : nullptr;
     return 0;
 }
 
@@ -314,7 +317,8 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (mfma) {
         const int mt = vh_mfma_max_tiles(P, E);
         if (!rc) rc = vh_mfma_plan(ws.counts, E, kMfmaMinTokens, ws.tiles, ws.small, s);
-        if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, hb, d, fe, k, ws.hs, s);
+        if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
+        if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
         act = ws.small;
     }

@@ -5,24 +5,30 @@
 // and its projections become GEMMs: H_e = silu(X_e G_e^T) * (X_e U_e^T) and
 // Y_e = H_e D_e^T, with X_e the group's rows of hb gathered through the
 // dispatch permutation. Groups of at least kMfmaMinTokens tokens run here on
-// v_mfma_f32_16x16x32_bf16: the inputs are rounded to bf16, the weights are
+// v_mfma_f32_32x32x16_bf16: the inputs are rounded to bf16, the weights are
 // dequantized exactly (src/gguf_compute.c:52-120) and then rounded to bf16
 // while they are staged, and products are accumulated in fp32. Smaller groups
 // stay on the fp32 kernels of moe_grouped.hip.
 //
-// Tiles: a workgroup (256 threads, 4 waves in 2 x 2) owns kBM = 128 rows of
-// one group (token tile) and 128 weight rows (gate/up: 64 rows of gate and the
-// same 64 rows of up; down: 128 rows), and steps over K in kBK = 64 columns.
-// Each step stages both operands in LDS, as 16-byte chunks of 8 consecutive
-// K values laid out [K/8][row], so a 16-lane group's MFMA operand read is one
-// contiguous 256-byte run. Global loads for step s + 1 are issued before the
-// MFMAs of step s and written to the other LDS buffer after them; one barrier
-// per step. The fp32 accumulators of a wave cover 64 rows x 64 columns.
+// Tiles: a workgroup (512 threads) owns kBM = 128 rows of one group (a token
+// tile) and kBRows = 256 weight rows (gate/up: 128 rows of gate and the same
+// 128 rows of up; down: 256 rows), and steps over K in kBK = 64 columns. Each
+// step stages both operands in LDS as 16-byte chunks of 8 consecutive K
+// values laid out [K/8][row] (row index XOR-swizzled by the chunk), so a
+// 32-lane group's operand read is one contiguous 512-byte run. Four waves
+// multiply and four stage (see mfma_proj_kernel).
+//
+// Order: the workgroups are numbered so that each XCD (hardware dispatch sends
+// workgroup b to XCD b mod 8) takes a contiguous run of (token tile, column
+// tile) pairs, column tiles fastest: the workgroups sharing a token tile, and
+// the consecutive token tiles of one expert that share its weight tiles, meet
+// in the same L2.
 //
 // Outputs: gate/up writes h as bf16 rows in dispatch order (hs[offs[e] + i]),
 // so the down GEMM reads its A operand contiguously; down writes the fp32 row
 // y[pair] that the combine kernel reads, as on the fp32 plan.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include "common.h"
 #include "qdecode.h"
 #include "route_kernels.h"
@@ -32,19 +38,97 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBK = 64, kBRows = 128, kThreads = 256;
+constexpr int kBM = 128, kBK = 64, kBRows = 256, kThreads = 512, kXcds = 8;
 constexpr int kChunks = kBK / 8;  // 16-byte chunks per row and K step
 
-// 8 bytes at even byte offset c of a 4-aligned tensor, from aligned words
-// that never leave [c - 2, c + 8): fetched into (w0, w1, w2) at load time,
-// shifted into place (sh = c & 3 bytes) only when the values are needed, so
-// the loads stay in flight across the MFMAs.
+// The raw bytes of 8 consecutive weights of one row - K chunk kc (columns
+// 64 s + 8 kc .. + 7) of K step s - and their dequantization to fp32 with the
+// reference's arithmetic (every value is that of gguf_dequant_row). Pos holds
+// what does not change with s (setup() takes the row's byte offset ro in the
+// 4-aligned tensor, under 4 GiB); Raw holds one step's words (load()); the
+// step enters the addresses only through uniform base pointers.
+template <int T>
+struct Chunk;
+
+template <>
+struct Chunk<VT_Q8_0> {  // src/gguf_compute.c:112-120: y = qs * d, exact
+    // block (2 s + kc / 4) starts at ob + 68 s and the thread's 8 quant bytes
+    // at oq + 68 s, an even offset: one 8-byte load (global memory accepts any
+    // alignment), one 16-bit load of the scale
+    struct Pos {
+        uint32_t ob, oq;
+    };
+    struct Raw {
+        uint32_t d;
+        uint2 q;
+    };
+    static VH_DEV void setup(Pos &p, uint32_t ro, int kc) {
+        p.ob = ro + 34u * uint32_t(kc >> 2);
+        p.oq = p.ob + 2u + 8u * uint32_t(kc & 3);
+    }
+    static VH_DEV void load(const Pos &p, Raw &r, gbyte *m, int s) {
+        gbyte *ms = m + 68 * s;
+        r.d = ld_u16(ms + p.ob);
+        r.q = ld_u64(ms + p.oq);
+    }
+    static VH_DEV void values(const Pos &, const Raw &r, int, float (&v)[8]) {
+        // q + 128 as an unsigned byte, converted with v_cvt_f32_ubyte*; then
+        // (q + 128) * s - 128 * s is q * s exactly (at most 19 significant bits)
+        const float sc = h2f(r.d), off = -128.0f * sc;
+        uint32_t u0 = r.q.x ^ 0x80808080u, u1 = r.q.y ^ 0x80808080u;
+        asm volatile("" : "+v"(u0), "+v"(u1));
+        const uint32_t w[2] = {u0, u1};
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = fmaf(float((w[i >> 2] >> (8 * (i & 3))) & 0xffu), sc, off);
+    }
+};
+
+template <>
+struct Chunk<VT_Q4_K> {  // src/gguf_compute.c:52-66: y = (d*sc)*q - dmin*m
+    // step s lies in super-block s / 4 and its chunk pair s % 4 (both
+    // uniform); the thread's 8 nibbles are bytes 8 (kc % 4) .. + 7 of the
+    // pair's 32: low nibbles (sub-block 2 (s % 4)) for kc < 4, else high
+    struct Pos {
+        uint32_t ro, oq, hi;
+    };
+    struct Raw {
+        uint4 hdr;
+        uint2 q;
+    };
+    static VH_DEV void setup(Pos &p, uint32_t ro, int kc) {
+        p.ro = ro;
+        p.oq = ro + 16u + 8u * uint32_t(kc & 3);
+        p.hi = uint32_t(kc >> 2);
+    }
+    static VH_DEV void load(const Pos &p, Raw &r, gbyte *m, int s) {
+        gbyte *ms = m + 144 * (s >> 2);
+        r.hdr = ld_u128(ms + p.ro);
+        r.q = ld_u64(ms + 32 * (s & 3) + p.oq);
+    }
+    static VH_DEV void values(const Pos &p, const Raw &r, int s, float (&v)[8]) {
+        int sc, mn;
+        q4k_scale_min(2 * (s & 3) + int(p.hi), r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+        const float d1 = h2f(r.hdr.x & 0xffffu) * float(sc), m1 = h2f(r.hdr.x >> 16) * float(mn);
+        const uint32_t sh = 4u * p.hi;
+        uint32_t w0 = (r.q.x >> sh) & 0x0f0f0f0fu, w1 = (r.q.y >> sh) & 0x0f0f0f0fu;
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        const uint32_t w[2] = {w0, w1};
+#pragma unroll
+        for (int i = 0; i < 8; i++)  // d1 * q is exact: one rounding, as in the reference
+            v[i] = fmaf(d1, float((w[i >> 2] >> (8 * (i & 3))) & 0xffu), -m1);
+    }
+};
+
+// 8 bytes at even byte offset c of a 4-aligned tensor, read as aligned words
+// that stay in [c - 2, c + 8) and shifted into place (by sh = c & 3 bytes)
+// when used. p points at c.
 struct Even8 {
     uint32_t w0, w1, w2, sh;
-    VH_DEV void load(gbyte *base, int64_t c) {
-        sh = uint32_t(c) & 3u;
-        gbyte *a = base + (c - int64_t(sh));
+    VH_DEV void load(gbyte *p, uint32_t shift) {
+        sh = shift;
+        gbyte *a = p - sh;
         w0 = ld_u32(a);
         w1 = ld_u32(a + 4);
         w2 = ld_u16(a + (sh ? 8 : 6));  // bytes c+6, c+7 (unused when sh == 0)
@@ -53,81 +137,50 @@ struct Even8 {
     VH_DEV uint32_t hi() const { return align2(w2, w1, sh); }
 };
 
-// The raw bytes of 8 consecutive weights (columns c .. c+7, c a multiple of 8)
-// of the row at byte offset ro of the 4-aligned tensor m, and their
-// dequantization to fp32 with the reference's arithmetic (every value is that
-// of gguf_dequant_row).
-template <int T>
-struct Chunk;
-
-template <>
-struct Chunk<VT_Q8_0> {  // src/gguf_compute.c:112-120: y = qs * d, exact
-    Even8 q;
-    uint32_t d;
-    VH_DEV void load(gbyte *m, int64_t ro, int c) {
-        const int64_t b = ro + 34 * int64_t(c >> 5);
-        d = ld_u16(m + b);
-        q.load(m, b + 2 + (c & 31));
-    }
-    VH_DEV void values(float (&v)[8]) const {
-        const float s = h2f(d);
-        const uint32_t w[2] = {q.lo(), q.hi()};
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = float(int(int8_t((w[i >> 2] >> (8 * (i & 3))) & 0xffu))) * s;
-    }
-};
-
-template <>
-struct Chunk<VT_Q4_K> {  // src/gguf_compute.c:52-66: y = (d*sc)*q - dmin*m
-    uint4 hdr;
-    uint2 q;
-    int c;
-    VH_DEV void load(gbyte *m, int64_t ro, int col) {
-        gbyte *sb = m + ro + 144 * int64_t(col >> 8);
-        const int cc = col & 255;
-        c = cc;
-        hdr = ld_u128(sb);
-        q = ld_u64(sb + 16 + 32 * (cc >> 6) + (cc & 31));
-    }
-    VH_DEV void values(float (&v)[8]) const {
-        const int j = 2 * (c >> 6) + ((c >> 5) & 1);  // sub-block; odd ones take the high nibbles
-        int sc, mn;
-        q4k_scale_min(j, hdr.y, hdr.z, hdr.w, sc, mn);
-        const float d1 = h2f(hdr.x & 0xffffu) * float(sc), m1 = h2f(hdr.x >> 16) * float(mn);
-        const uint32_t sh = (j & 1) ? 4u : 0u;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t qi = (((i < 4 ? q.x : q.y) >> (8 * (i & 3))) >> sh) & 15u;
-            v[i] = d1 * float(qi) - m1;  // d1 * q is exact: one rounding, as in the reference
-        }
-    }
-};
-
 template <>
 struct Chunk<VT_Q6_K> {  // src/gguf_compute.c:83-103: y = (d*sc)*(q - 32)
-    Even8 ql, qh;
-    uint32_t d, sc;
-    int c;
-    VH_DEV void load(gbyte *m, int64_t ro, int col) {
-        const int64_t sbo = ro + 210 * int64_t(col >> 8);
-        const int i = col & 255, h = i >> 7, g = (i >> 5) & 3, l = i & 31;
-        c = i;
-        ql.load(m, sbo + 64 * h + 32 * (g & 1) + l);
-        qh.load(m, sbo + 128 + 32 * h + l);
-        sc = ld_u8(m + sbo + 192 + 8 * h + (l >> 4) + 2 * g);
-        d = ld_u16(m + sbo + 208);
+    // step s: super-block b = s / 4 at byte U = 210 b of the row, half
+    // h = (s % 4) / 2, both uniform. The thread's 8 elements are l = 8 (kc % 4)
+    // .. + 7 of group g = 2 (s % 2) + kc / 4: the low (g < 2) or high nibbles
+    // of ql[64 h + 32 (g % 2) + l], bits 2g of qh[32 h + l], scale
+    // [8 h + l / 16 + 2 g]. U is even, so a field's alignment is that of its
+    // offset within the row's first super-block plus 2 (b % 2).
+    struct Pos {
+        uint32_t oql, oqh, osc, od, gl;
+    };
+    struct Raw {
+        Even8 ql, qh;
+        uint32_t d, sc;
+    };
+    static VH_DEV void setup(Pos &p, uint32_t ro, int kc) {
+        const uint32_t l = 8u * uint32_t(kc & 3);
+        p.oql = ro + 32u * uint32_t(kc >> 2) + l;
+        p.oqh = ro + 128u + l;
+        p.osc = ro + 192u + (l >> 4) + 2u * uint32_t(kc >> 2);
+        p.od = ro + 208u;
+        p.gl = uint32_t(kc >> 2);
     }
-    VH_DEV void values(float (&v)[8]) const {
-        const int g = (c >> 5) & 3;
-        const float s = h2f(d) * float(int(int8_t(sc)));
-        const uint32_t lsh = g >= 2 ? 4u : 0u, hsh = 2u * uint32_t(g);
-        const uint32_t l2[2] = {ql.lo(), ql.hi()}, h2[2] = {qh.lo(), qh.hi()};
+    static VH_DEV void load(const Pos &p, Raw &r, gbyte *m, int s) {
+        const int b = s >> 2, h = (s & 3) >> 1;
+        gbyte *ms = m + 210 * b;
+        const uint32_t odd = 2u * uint32_t(b & 1);
+        r.ql.load(ms + 64 * h + p.oql, (p.oql + odd) & 3u);
+        r.qh.load(ms + 32 * h + p.oqh, (p.oqh + odd) & 3u);
+        r.sc = ld_u8(ms + 8 * h + 4 * (s & 1) + p.osc);
+        r.d = ld_u16(ms + p.od);
+    }
+    static VH_DEV void values(const Pos &p, const Raw &r, int s, float (&v)[8]) {
+        const uint32_t g = 2u * uint32_t(s & 1) + p.gl;
+        const float sc = h2f(r.d) * float(int(int8_t(r.sc)));
+        const uint32_t lsh = g >= 2 ? 4u : 0u, hsh = 2u * g;
+        uint32_t w0 = ((r.ql.lo() >> lsh) & 0x0f0f0f0fu) | (((r.qh.lo() >> hsh) & 0x03030303u) << 4);
+        uint32_t w1 = ((r.ql.hi() >> lsh) & 0x0f0f0f0fu) | (((r.qh.hi() >> hsh) & 0x03030303u) << 4);
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        const uint32_t w[2] = {w0, w1};
+        // sc * q - 32 sc is sc * (q - 32) exactly before its one rounding, as
+        // in the reference's (d * sc) * (q - 32)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t lo = ((l2[i >> 2] >> (8 * (i & 3))) >> lsh) & 15u;
-            const uint32_t hi = ((h2[i >> 2] >> (8 * (i & 3))) >> hsh) & 3u;
-            v[i] = s * float(int(lo | (hi << 4)) - 32);
-        }
+        for (int i = 0; i < 8; i++) v[i] = fmaf(sc, float((w[i >> 2] >> (8 * (i & 3))) & 0xffu), -32.0f * sc);
     }
 };
 
@@ -138,28 +191,40 @@ VH_DEV bf16x8 to_bf16(const float (&v)[8]) {
     return __builtin_convertvector(f, bf16x8);
 }
 
-// grid (rows_out / (GATEUP ? 64 : 128), max_tiles), 256 threads. Tile t of
-// the plan is (expert e, first row m0 of its group). GATEUP: A = hb (fp32
-// [T x K], row perm[i] / k), B = gate and up rows, out = hs (bf16 [P x rows],
-// row i); else A = hs (bf16 [P x K], row i), B = down rows, out = y (fp32
-// [P x rows], row perm[i]). i runs over offs[e] + m0 .. + kBM - 1 within the
-// group.
+// 1-D grid of at least (column tiles) x (tile-plan capacity) workgroups, a
+// multiple of kXcds; 512 threads. Tile t of the plan is (expert e, first row
+// m0 of its group). A is bf16: GATEUP: xb [T x K], row perm[i] / k; else hs
+// [P x K], row i. GATEUP: B = gate and up rows, out = hs (bf16 [P x rows],
+// row i); else B = down rows, out = y (fp32 [P x rows], row perm[i]). i runs
+// over offs[e] + m0 .. + kBM - 1 within the group.
+//
+// Waves 0-3 only multiply: wave c owns rows 64 (c / 2) .. + 63 of the tile
+// and 128 of its weight rows (gate/up: 64 columns of gate and the same 64 of
+// up), eight 32 x 32 accumulator fragments. Waves 4-7 only stage: their global loads run
+// two K steps ahead in two register sets, and each step they dequantize the
+// set that arrived a step ago into the LDS buffer the multiplying waves will
+// read next. Every SIMD holds one wave of each kind, so the matrix cores and
+// the vector ALUs work at the same time; one barrier per K step.
 template <int T, bool GATEUP>
 __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__restrict__ tiles,
                                                              const int32_t *__restrict__ counts,
                                                              const int32_t *__restrict__ offs,
                                                              const int32_t *__restrict__ perm,
                                                              const void *const *__restrict__ table,
-                                                             const void *__restrict__ src, int K, int rows, int k,
+                                                             const __bf16 *__restrict__ src, int K, int rows, int k,
                                                              int64_t row_bytes, void *__restrict__ out) {
+    constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;  // output columns per workgroup
     __shared__ bf16x8 As[2][kChunks][kBM];
     __shared__ bf16x8 Bs[2][kChunks][kBRows];
-    const int t = blockIdx.y;
-    if (t >= tiles[0]) return;
+    // XCD-contiguous numbering of the live (token tile, column tile) pairs
+    const int nct = rows / NCOL, live = tiles[0] * nct, per = (live + kXcds - 1) / kXcds;
+    const int slot = blockIdx.x / kXcds, L = (blockIdx.x % kXcds) * per + slot;
+    if (slot >= per || L >= live) return;
+    const int t = L / nct, n0 = (L % nct) * NCOL;
     const int e = tiles[1 + 2 * t], m0 = tiles[2 + 2 * t];
     const int base = offs[e], mcnt = min(kBM, counts[e] - m0);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv >> 1, wn = wv & 1;
-    const int n0 = blockIdx.x * (GATEUP ? 64 : 128);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool mult = wv < 4;
 
     gbyte *M0 = gmem(table[3 * e + (GATEUP ? 0 : 2)]);
     gbyte *M1 = GATEUP ? gmem(table[3 * e + 1]) : M0;
@@ -167,121 +232,142 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         // an unregistered expert contributes nothing (src/gguf_run.c:201): its
         // h rows are zero, and the combine skips its y rows
         if (GATEUP)
-            for (int i = tid; i < mcnt * 64; i += kThreads)
-                static_cast<__bf16 *>(out)[size_t(base + m0 + i / 64) * rows + n0 + i % 64] = __bf16(0.0f);
+            for (int i = tid; i < mcnt * NCOL; i += kThreads)
+                static_cast<__bf16 *>(out)[size_t(base + m0 + i / NCOL) * rows + n0 + i % NCOL] = __bf16(0.0f);
+        return;
+    }
+    const int nk = K / kBK;
+
+    if (!mult) {
+        // ---- staging waves: thread p stages K chunk kc = p & 7 of A rows
+        // (p >> 3) + 32 q (q < 4; rows past the group repeat its last row,
+        // whose results are not stored) and of B rows (p >> 3) + 32 q (q < 8).
+        // In LDS, chunk kc of row r sits at [kc][r ^ kc]: the 8 lanes of a row
+        // write 8 different bank groups, and a 32-lane operand read stays
+        // conflict-free. The K step enters the global addresses only through
+        // uniform base pointers.
+        const int p = tid - 256, kc = p & 7, rx = (p >> 3) ^ kc;
+        gbyte *abase = gmem(src);
+        uint32_t aoff[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int i = base + m0 + min((p >> 3) + 32 * q, mcnt - 1);
+            aoff[q] = uint32_t((GATEUP ? size_t(perm[i] / k) : size_t(i)) * K * 2) + 16u * uint32_t(kc);
+        }
+        // B rows (p >> 3) + 32 q lie 32 q rows (gate/up: 32 (q % 4) rows of
+        // gate or up) past row p >> 3: one set of offsets, and per q a uniform
+        // base pointer (32 rows are a multiple of 4 bytes, so alignments agree)
+        using C = Chunk<T>;
+        typename C::Pos bp;
+        C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
+        gbyte *bm[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) bm[q] = (GATEUP && q >= 4 ? M1 : M0) + (GATEUP ? q & 3 : q) * 32 * row_bytes;
+
+        struct Stage {
+            uint4 ah[4];
+            typename C::Raw bw[8];
+        } st0, st1;
+        auto load = [&](Stage &g, int step) {
+            gbyte *as = abase + 128 * step;
+#pragma unroll
+            for (int q = 0; q < 4; q++) g.ah[q] = ld_u128(as + aoff[q]);
+#pragma unroll
+            for (int q = 0; q < 8; q++) C::load(bp, g.bw[q], bm[q], step);
+        };
+        auto store = [&](const Stage &g, int buf, int step) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) As[buf][kc][rx + 32 * q] = __builtin_bit_cast(bf16x8, g.ah[q]);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                float w[8];
+                C::values(bp, g.bw[q], step, w);
+                Bs[buf][kc][rx + 32 * q] = to_bf16(w);
+            }
+        };
+        load(st0, 0);
+        if (nk > 1) load(st1, 1);
+        store(st0, 0, 0);
+        __syncthreads();
+        for (int s = 0; s < nk; s += 2) {
+            // step s: the multiplying waves read buffer 0
+            if (s + 2 < nk) load(st0, s + 2);
+            if (s + 1 < nk) store(st1, 1, s + 1);
+            __syncthreads();
+            if (s + 1 >= nk) break;
+            // step s + 1: they read buffer 1
+            if (s + 3 < nk) load(st1, s + 3);
+            if (s + 2 < nk) store(st0, 0, s + 2);
+            __syncthreads();
+        }
         return;
     }
 
-    // this thread's staging slots: chunk tid + 256 q (q < 4) of each operand,
-    // row (tid >> 3) + 32 q, K chunk tid & 7
-    const int kc = tid & 7;
-    // (rows past the group read its last row and stage zeros)
-    const uint8_t *arow[4];
-    bool aval[4];
-    gbyte *bmat[4];
-    int64_t boff[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int r = (tid >> 3) + 32 * q;
-        aval[q] = r < mcnt;
-        const int i = base + m0 + min(r, mcnt - 1);
-        arow[q] = GATEUP ? static_cast<const uint8_t *>(src) + size_t(perm[i] / k) * K * 4
-                         : static_cast<const uint8_t *>(src) + size_t(i) * K * 2;
-        bmat[q] = GATEUP ? (r < 64 ? M0 : M1) : M0;
-        boff[q] = int64_t(GATEUP ? n0 + (r & 63) : n0 + r) * row_bytes;
-    }
-
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // staged registers for one K step
-    float4 ax[4][2];
-    uint4 ah[4];
-    Chunk<T> bw[4];
-    auto load = [&](int k0) {
-        const int c = k0 + 8 * kc;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (GATEUP) {
-                ax[q][0] = *reinterpret_cast<const float4 *>(arow[q] + 4 * c);
-                ax[q][1] = *reinterpret_cast<const float4 *>(arow[q] + 4 * c + 16);
-            } else {
-                ah[q] = *reinterpret_cast<const uint4 *>(arow[q] + 2 * c);
-            }
-            bw[q].load(bmat[q], boff[q], c);
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int r = (tid >> 3) + 32 * q;
-            if (GATEUP) {
-                f32x8 f;
-                f[0] = ax[q][0].x; f[1] = ax[q][0].y; f[2] = ax[q][0].z; f[3] = ax[q][0].w;
-                f[4] = ax[q][1].x; f[5] = ax[q][1].y; f[6] = ax[q][1].z; f[7] = ax[q][1].w;
-                As[buf][kc][r] = __builtin_convertvector(aval[q] ? f : f32x8{}, bf16x8);
-            } else {
-                As[buf][kc][r] = __builtin_bit_cast(bf16x8, aval[q] ? ah[q] : make_uint4(0u, 0u, 0u, 0u));
-            }
-            float w[8];
-            bw[q].values(w);
-            Bs[buf][kc][r] = to_bf16(w);
-        }
-    };
-
-    // B rows of the wave's four 16-column fragments
+    // ---- multiplying waves: v_mfma_f32_32x32x16_bf16 (lane l supplies row
+    // l % 32, K values 8 (l / 32) .. + 7 of each operand; it holds column
+    // l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 of the 32 x 32 result)
+    const int wm = wv >> 1, wn = wv & 1;
+    // B rows of the wave's four 32-column fragments (gate/up: two of gate,
+    // the same two of up)
     int bfr[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) bfr[j] = GATEUP ? (j < 2 ? 0 : 64) + 32 * wn + 16 * (j & 1) : 64 * wn + 16 * j;
-
-    const int nk = K / kBK;
-    load(0);
-    store(0);
-    __syncthreads();
+    for (int j = 0; j < 4; j++) bfr[j] = GATEUP ? (j < 2 ? 0 : NCOL) + 64 * wn + 32 * (j & 1) : 128 * wn + 32 * j;
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    __syncthreads();  // buffer 0 staged
     for (int s = 0; s < nk; s++) {
         const int buf = s & 1;
-        if (s + 1 < nk) load((s + 1) * kBK);
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const int kg = 4 * ks + (lane >> 4);
-            bf16x8 a[4], b[4];
+        for (int ks = 0; ks < 4; ks++) {
+            const int kg = 2 * ks + (lane >> 5), lx = (lane & 31) ^ kg;
+            bf16x8 a[2], b[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) a[i] = As[buf][kg][64 * wm + 16 * i + (lane & 15)];
+            for (int i = 0; i < 2; i++) a[i] = As[buf][kg][lx + 64 * wm + 32 * i];
 #pragma unroll
-            for (int j = 0; j < 4; j++) b[j] = Bs[buf][kg][bfr[j] + (lane & 15)];
+            for (int j = 0; j < 4; j++) b[j] = Bs[buf][kg][lx + bfr[j]];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < nk) store(buf ^ 1);
         __syncthreads();
     }
 
-    // epilogue: lane holds rows 4 (lane >> 4) + r, column lane & 15 of each
-    // 16 x 16 fragment
+    // epilogue
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = 64 * wm + 16 * i + 4 * (lane >> 4) + r;
+        for (int r = 0; r < 16; r++) {
+            const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (row >= mcnt) continue;
             const int pos = base + m0 + row;
             if (GATEUP) {
                 __bf16 *hs = static_cast<__bf16 *>(out) + size_t(pos) * rows;
 #pragma unroll
-                for (int jj = 0; jj < 2; jj++) {
-                    hs[n0 + 32 * wn + 16 * jj + (lane & 15)] = __bf16(swiglu(acc[i][jj][r], acc[i][2 + jj][r]));
-                }
+                for (int jj = 0; jj < 2; jj++)
+                    hs[n0 + 64 * wn + 32 * jj + (lane & 31)] = __bf16(swiglu(acc[i][jj][r], acc[i][2 + jj][r]));
             } else {
                 float *y = static_cast<float *>(out) + size_t(perm[pos]) * rows;
 #pragma unroll
-                for (int j = 0; j < 4; j++) y[n0 + 64 * wn + 16 * j + (lane & 15)] = acc[i][j][r];
+                for (int j = 0; j < 4; j++) y[n0 + 128 * wn + 32 * j + (lane & 31)] = acc[i][j][r];
             }
         }
+}
+
+// bf16 copy of n fp32 values (n a multiple of 4, both 16-byte aligned)
+__global__ void __launch_bounds__(256) to_bf16_kernel(const float4 *__restrict__ x, uint2 *__restrict__ y, int64_t n4) {
+    for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+        const float4 v = x[i];
+        typedef float f32x4_ __attribute__((ext_vector_type(4)));
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const bf16x4 b = __builtin_convertvector(f32x4_{v.x, v.y, v.z, v.w}, bf16x4);
+        y[i] = __builtin_bit_cast(uint2, b);
+    }
 }
 
 // One workgroup: tiles = {n, (e, m0) x n} for the groups of at least
@@ -319,9 +405,10 @@ __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restric
 
 template <bool GATEUP>
 int mfma_launch(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                const int32_t *perm, const void *const *table, const void *src, int K, int rows, int k,
+                const int32_t *perm, const void *const *table, const __bf16 *src, int K, int rows, int k,
                 void *out, hipStream_t s) {
-    const dim3 g(rows / (GATEUP ? 64 : 128), max_tiles);
+    const int64_t nwg = int64_t(rows / (GATEUP ? kBRows / 2 : kBRows)) * max_tiles;
+    const dim3 g(unsigned((nwg + kXcds - 1) / kXcds * kXcds));
     switch (type) {
     case VT_Q8_0:
         hipLaunchKernelGGL((mfma_proj_kernel<VT_Q8_0, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs, perm,
@@ -345,8 +432,8 @@ int mfma_launch(uint32_t type, const int32_t *tiles, int max_tiles, const int32_
 bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E) {
     auto ok = [](uint32_t t) { return t == VT_Q8_0 || t == VT_Q4_K || t == VT_Q6_K; };
     auto kq = [](uint32_t t, int n) { return t == VT_Q8_0 ? n % 32 == 0 : n % 256 == 0; };
-    return ok(tg) && ok(td) && kq(tg, d) && kq(td, fe) && d % kBK == 0 && fe % kBK == 0 && fe % 64 == 0 &&
-           d % 128 == 0 && E <= 256;
+    return ok(tg) && ok(td) && kq(tg, d) && kq(td, fe) && d % kBRows == 0 && fe % (kBRows / 2) == 0 &&
+           d % kBK == 0 && fe % kBK == 0 && E <= 256;
 }
 
 int vh_mfma_max_tiles(int P, int E) { return P / kBM + E; }
@@ -357,14 +444,25 @@ int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, i
     return vh_check(hipGetLastError());
 }
 
+int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s) {
+    if (n % 4 || (reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u)) return -EINVAL;
+    const int64_t n4 = n / 4;
+    const unsigned blocks = unsigned(std::min<int64_t>((n4 + 255) / 256, 4096));
+    hipLaunchKernelGGL(to_bf16_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const float4 *>(x),
+                       static_cast<uint2 *>(y), n4);
+    return vh_check(hipGetLastError());
+}
+
 int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                   const int32_t *perm, const void *const *table, const float *hb, int d, int fe, int k, void *hs,
+                   const int32_t *perm, const void *const *table, const void *xb, int d, int fe, int k, void *hs,
                    hipStream_t s) {
-    return mfma_launch<true>(type, tiles, max_tiles, counts, offs, perm, table, hb, d, fe, k, hs, s);
+    return mfma_launch<true>(type, tiles, max_tiles, counts, offs, perm, table, static_cast<const __bf16 *>(xb), d,
+                             fe, k, hs, s);
 }
 
 int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
                  const int32_t *perm, const void *const *table, const void *hs, int d, int fe, float *ybuf,
                  hipStream_t s) {
-    return mfma_launch<false>(type, tiles, max_tiles, counts, offs, perm, table, hs, fe, d, 1, ybuf, s);
+    return mfma_launch<false>(type, tiles, max_tiles, counts, offs, perm, table, static_cast<const __bf16 *>(hs), fe,
+                              d, 1, ybuf, s);
 }

@@ -54,8 +54,10 @@ constexpr int kMfmaMinCall = 64;
 bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E);
 int vh_mfma_max_tiles(int P, int E);
 int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, int32_t *small, hipStream_t s);
+// xb: the bf16 copy of hb (vh_to_bf16)
+int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s);
 int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                   const int32_t *perm, const void *const *table, const float *hb, int d, int fe, int k, void *hs,
+                   const int32_t *perm, const void *const *table, const void *xb, int d, int fe, int k, void *hs,
                    hipStream_t s);
 int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
                  const int32_t *perm, const void *const *table, const void *hs, int d, int fe, float *ybuf,
