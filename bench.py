@@ -48,6 +48,8 @@ WORKLOADS = {
     "qwen3-q8_0-prefill-2048": ("qwen3-30b-a3b-q8_0", 2048, 2, True),
 }
 DEFAULT = "qwen3-q4km-decode-b1"
+# name: (shape, layers, vocab): greedy decode of a whole MoE stack + Q8_0 LM head
+STACKS = {"qwen3-q4km-stack48": ("qwen3-30b-a3b-q4_k_m", 48, 151936)}
 
 
 def parse():
@@ -55,7 +57,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS) + ["copy-512MiB"])
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS) + sorted(STACKS) + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -123,6 +125,95 @@ def cpu_baseline(shape, B, seed, seconds):
             "us_per_layer": round(dt / n * 1e6, 1)}
 
 
+def cpu_baseline_stack(shape, L, vocab, seed, seconds):
+    """Host time per token of the stack: L x the reference's moe_ffn on one
+    layer (cpu_baseline) plus its gguf_matmul of the Q8_0 LM head, timed on
+    a slice of the head's rows and scaled to the vocabulary (the matmul is
+    row-parallel)."""
+    from vireo_amd import workloads as W
+    from oracle.oracle import Reference, Oracle
+    layer = cpu_baseline(shape, 1, seed, seconds)
+    rows = 16384
+    head = W.host_matrix(W.Q8_0, shape.d, 0, rows, seed, W.stream_id(0, W.KIND_LM_HEAD))
+    x = W.host_normal(shape.d, seed, 99)
+    lib = Reference() if Reference.available() else Oracle()
+    lib.matmul(W.Q8_0, head, x, shape.d, rows)
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < 1.0:
+        lib.matmul(W.Q8_0, head, x, shape.d, rows)
+        n += 1
+    head_s = (time.perf_counter() - t0) / n * vocab / rows
+    tok_s = 1.0 / (L * layer["us_per_layer"] * 1e-6 + head_s)
+    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": layer["cores"], "kind": layer["kind"],
+            "sample": f"{layer['sample']}; times {L} layers, plus the LM head matmul timed on {rows} of its "
+                      f"{vocab} rows ({head_s * 1e3:.1f} ms scaled)",
+            "us_per_layer": layer["us_per_layer"], "lm_head_ms": round(head_s * 1e3, 2)}
+
+
+def bench_stack(args):
+    """Greedy decode through moe_stack_step: embedding row (the tied LM head),
+    RMSNorm + MoE layer x L, RMSNorm, Q8_0 LM head, argmax; K steps captured
+    in one HIP graph, each step reading the token the previous one wrote."""
+    import torch
+    from vireo_amd import _lib
+    from vireo_amd import stack as S
+    from vireo_amd import workloads as W
+
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    shape_name, L, vocab = STACKS[args.workload]
+    L = args.layers or L
+    shape = W.SHAPES[shape_name]
+    K = args.steps or 128
+    Wm = args.warmup if args.warmup is not None else 2
+    print(f"[bench] {args.workload}: building {L} layers of {shape.name} and a [{vocab} x {shape.d}] Q8_0 LM head",
+          file=sys.stderr, flush=True)
+    st = S.DeviceStack(shape, L, vocab=vocab, seed=args.seed)
+    token = torch.full((1,), 17, dtype=torch.int32, device="cuda")
+    for _ in range(max(1, Wm)):  # the first step pins every layer's leases
+        st.step(token)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(K):
+            st.step(token, stream=s)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    ms_per_step = ms / K
+    # algorithmic bytes of one token: per layer the router, the k selected
+    # experts and the activations; the LM head; the embedding row
+    layer_b = shape.E * shape.d * 4 + shape.k * shape.expert_bytes() + 2 * shape.d * 4
+    tok_b = L * layer_b + vocab * W.row_bytes(W.Q8_0, shape.d) + W.row_bytes(W.Q8_0, shape.d) + vocab * 4
+    gbs = tok_b / (ms_per_step / 1e3) / 1e9
+    result = {
+        "metric": METRIC, "value": round(K / (ms / 1e3), 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{L}-layer {shape.name} MoE stack (attention omitted) + Q8_0 LM head "
+                               f"[{vocab} x {shape.d}], greedy decode batch 1",
+                   "layers": L, "d": shape.d, "experts": shape.E, "top_k": shape.k, "ffn_exp": shape.fe,
+                   "vocab": vocab, "tied_embedding": True},
+        "us_per_layer": round(ms_per_step * 1e3 / L, 3),
+        "token_alg_bytes": int(tok_b), "step_GBps": round(gbs, 1),
+        "roofline": {"kernel": "moe_stack_step (all kernels of a step)", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline_stack(shape, L, vocab, args.seed, args.cpu_seconds)
+    st.close()
+    print(json.dumps(result), flush=True)
+
+
 def copy_calibration(args):
     """A plain device-to-device copy of 512 MiB, the reference kernel whose
     HBM counters (FETCH_SIZE, WRITE_SIZE) calibrate the traffic of the MoE
@@ -161,6 +252,8 @@ def main():
               f"(no collectives, no sharding); --gpus {args.gpus} / WORLD_SIZE {world} is not supported.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload in STACKS:
+        return bench_stack(args)
 
     import torch
     from vireo_amd import _lib

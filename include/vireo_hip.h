@@ -63,11 +63,18 @@ int qdequant_rows(uint32_t ggml_type, const void *src, float *dst, int n, int ro
 /* ---- model glue used by the MoE stack --------------------------------------- */
 
 /* rmsnorm (src/gguf_run.c:161-165) on `rows` rows of n floats:
- * o = x * (1/sqrt(mean(x^2) + eps)) * w. w: device [n] F32 weight. o may
- * equal x. */
+ * o = x * (1/sqrt(mean(x^2) + eps)) * w. w: device [n] F32 weight, or NULL
+ * for a unit weight. o may equal x. */
 int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream);
 /* argmax (src/gguf_run.c:254): first index of the maximum of v[0..n). */
 int vireo_argmax(const float *v, int n, int32_t *out, void *stream);
+/* Embedding lookup (src/gguf_run.c:218, gguf_dequant_row of a tok_embd row):
+ * dst[i*n + j] = dequant(row tokens[i] of table)[j] for i < count. table:
+ * device [n_rows x n] of type Q8_0, F16 or F32; tokens: device int32 (an
+ * argmax output, so a decode loop needs no host round trip); a token outside
+ * [0, n_rows) gives a zero row. */
+int vireo_embed(uint32_t type, const void *table, int n, int n_rows, const int32_t *tokens, int count, float *dst,
+                void *stream);
 
 /* ---- MoE FFN (src/gguf_run.c:185-214) ---------------------------------------- */
 
@@ -177,6 +184,30 @@ int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, float *x, c
  * us_out (host). Results are those of n moe_decode_stage calls. */
 int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n, const int *layers, float *x, const float *hb,
                            void *states, int64_t state_stride, int32_t *idx, float *w, float *us_out, void *stream);
+
+/* ---- MoE stack decode step (src/gguf_run.c:216-254) --------------------------- */
+
+/* An attention-free stack of MoE layers with an LM head. */
+typedef struct {
+    const vireo_moe_model *moe;    /* the n_layers MoE layers */
+    const float *const *ffn_norm;  /* host array [n_layers] of device [dim] F32 RMSNorm weights (an
+                                      entry or the array NULL: unit weight) */
+    const float *out_norm;         /* device [dim] F32, or NULL (unit weight) */
+    const gguf_tensor *lm_head;    /* [vocab x dim], data on the device; also the token embedding
+                                      (a tied model, src/gguf_run.c:297) */
+    int vocab;
+    float eps;
+} vireo_moe_stack;
+
+/* One greedy decode step, forward() (src/gguf_run.c:216-251) with attention
+ * omitted, then argmax (:254): x = embed(token[0]); for each layer l,
+ * xb = rmsnorm(x, ffn_norm[l]) and moe_ffn_forward(l) adds to x; then
+ * logits = lm_head * rmsnorm(x, out_norm) and token[0] = argmax(logits).
+ * token (int32 [1]), x, xb ([dim]) and logits ([vocab]) are caller-owned
+ * device buffers; with a stream every launch is only enqueued there, so a
+ * caller can capture a loop of steps in a graph (after one uncaptured step:
+ * the first call on a layer pins its expert leases). */
+int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits, void *stream);
 
 /* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
 

@@ -66,6 +66,17 @@ class MoEModel(C.Structure):
     ]
 
 
+class MoEStack(C.Structure):
+    _fields_ = [
+        ("moe", C.POINTER(MoEModel)),
+        ("ffn_norm", c_vp),
+        ("out_norm", c_vp),
+        ("lm_head", C.POINTER(GGUFTensor)),
+        ("vocab", C.c_int),
+        ("eps", C.c_float),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "vireo_hip_init": (C.c_int, [C.c_int]),
@@ -76,6 +87,8 @@ SIGNATURES = {
     "qdequant_rows": (C.c_int, [C.c_uint32, c_vp, c_vp, C.c_int, C.c_int, c_vp]),
     "vireo_rmsnorm": (C.c_int, [c_vp, c_vp, c_vp, C.c_int, C.c_int, C.c_float, c_vp]),
     "vireo_argmax": (C.c_int, [c_vp, C.c_int, c_vp, c_vp]),
+    "vireo_embed": (C.c_int, [C.c_uint32, c_vp, C.c_int, C.c_int, c_vp, C.c_int, c_vp, c_vp]),
+    "moe_stack_step": (C.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_route": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_dispatch": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
     "vireo_hip_set_path": (C.c_int, [C.c_int]),

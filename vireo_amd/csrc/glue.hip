@@ -1,7 +1,9 @@
-// Model glue around the MoE layers: rmsnorm (src/gguf_run.c:161-165) and
-// argmax (src/gguf_run.c:254).
+// Model glue around the MoE layers: rmsnorm (src/gguf_run.c:161-165), argmax
+// (src/gguf_run.c:254), the embedding lookup (src/gguf_run.c:218) and the
+// decode step of an MoE stack (src/gguf_run.c:216-251 without attention).
 #include <hip/hip_runtime.h>
 #include "common.h"
+#include "qdecode.h"
 #include "vireo_hip.h"
 
 namespace {
@@ -25,7 +27,8 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(float *o, const float *x,
     __syncthreads();
     const float ss = float((part[0] + part[1]) + (part[2] + part[3]));
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(n)), eps)));
-    for (int i = threadIdx.x; i < n; i += 256) orow[i] = __fmul_rn(__fmul_rn(xr[i], r), w[i]);
+    // w == nullptr: unit weight (x * r * 1.0f is x * r)
+    for (int i = threadIdx.x; i < n; i += 256) orow[i] = w ? __fmul_rn(__fmul_rn(xr[i], r), w[i]) : __fmul_rn(xr[i], r);
 }
 
 __global__ void __launch_bounds__(1024) argmax_kernel(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
@@ -53,10 +56,71 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float *__restrict__ 
     }
 }
 
+// dst[i] = gguf_dequant_row(table row tokens[i]) for i < count, one
+// workgroup per row (Q8_0: thread j of 256 writes elements j, j + 256, ...;
+// the block scale of element c is that of block c / 32). A token outside
+// [0, n_rows) gives a zero row.
+template <int T>
+__global__ void __launch_bounds__(256) embed_kernel(const uint8_t *__restrict__ table, int64_t row_bytes, int n,
+                                                    int n_rows, const int32_t *__restrict__ tokens,
+                                                    float *__restrict__ dst) {
+    const int tok = tokens[blockIdx.x];
+    float *o = dst + size_t(blockIdx.x) * n;
+    if (tok < 0 || tok >= n_rows) {
+        for (int c = threadIdx.x; c < n; c += 256) o[c] = 0.0f;
+        return;
+    }
+    const uint8_t *r = table + int64_t(tok) * row_bytes;
+    for (int c = threadIdx.x; c < n; c += 256) {
+        if constexpr (T == VT_Q8_0) {  // src/gguf_compute.c:112-120: qs * d, exact
+            const uint8_t *b = r + 34 * (c >> 5);
+            o[c] = __fmul_rn(float(int8_t(ld_u8(b + 2 + (c & 31)))), h2f(ld_u16(b)));
+        } else if constexpr (T == VT_F16) {
+            o[c] = h2f(ld_u16(r + 2 * c));
+        } else {
+            o[c] = reinterpret_cast<const float *>(r)[c];
+        }
+    }
+}
+
 }  // namespace
 
+extern "C" int vireo_embed(uint32_t type, const void *table, int n, int n_rows, const int32_t *tokens, int count,
+                           float *dst, void *stream) {
+    if (n <= 0 || n_rows <= 0 || count < 0 || (count && (!table || !tokens || !dst))) return -EINVAL;
+    if ((type == VT_Q8_0 && n % 32) || (type != VT_Q8_0 && type != VT_F16 && type != VT_F32)) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(table) & 3u) return -EINVAL;
+    if (count == 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t *t = static_cast<const uint8_t *>(table);
+    const int64_t rb = vh_row_bytes(type, n);
+    switch (type) {
+    case VT_Q8_0: hipLaunchKernelGGL(embed_kernel<VT_Q8_0>, dim3(count), dim3(256), 0, s, t, rb, n, n_rows, tokens, dst); break;
+    case VT_F16: hipLaunchKernelGGL(embed_kernel<VT_F16>, dim3(count), dim3(256), 0, s, t, rb, n, n_rows, tokens, dst); break;
+    default: hipLaunchKernelGGL(embed_kernel<VT_F32>, dim3(count), dim3(256), 0, s, t, rb, n, n_rows, tokens, dst); break;
+    }
+    return vh_finish(s, vh_check(hipGetLastError()));
+}
+
+extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits,
+                              void *stream) {
+    if (!st || !st->moe || !st->lm_head || !token || !x || !xb || !logits || st->vocab <= 0) return -EINVAL;
+    const vireo_moe_model *m = st->moe;
+    const int d = m->dim;
+    void *s = stream;
+    int rc = vireo_embed(st->lm_head->ggml_type, st->lm_head->data, d, st->vocab, token, 1, x, s);
+    for (int l = 0; l < m->n_layers && !rc; l++) {
+        rc = vireo_rmsnorm(xb, x, st->ffn_norm ? st->ffn_norm[l] : nullptr, d, 1, st->eps, s);
+        if (!rc) rc = moe_ffn_forward(m, l, x, xb, 1, nullptr, nullptr, s);
+    }
+    if (!rc) rc = vireo_rmsnorm(xb, x, st->out_norm, d, 1, st->eps, s);
+    if (!rc) rc = qmatvec_async(logits, xb, st->lm_head, d, st->vocab, s);
+    if (!rc) rc = vireo_argmax(logits, st->vocab, token, s);
+    return vh_finish(static_cast<hipStream_t>(s), rc);
+}
+
 extern "C" int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream) {
-    if (n <= 0 || rows < 0 || (rows && (!o || !x || !w))) return -EINVAL;
+    if (n <= 0 || rows < 0 || (rows && (!o || !x))) return -EINVAL;
     if (rows == 0) return 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, o, x, w, n, eps);
