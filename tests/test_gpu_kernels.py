@@ -72,8 +72,30 @@ def test_rmsnorm(cuda, oracle):
         np.testing.assert_allclose(out[r], oracle.rmsnorm(x[r], w, 1e-6), rtol=2e-5, atol=1e-6)
 
 
-def test_argmax_first_max(cuda, oracle):
-    v = W.host_normal(151936, 3, 3)
-    v[100000] = v[7] = v.max() + 1  # tie: the first index wins, as in the reference's strict '>' scan
+@pytest.mark.parametrize("n,ties", [(151936, (7, 100000)), (151936, (4096 * 3 - 1, 4096 * 3, 151935)),
+                                    (151936, (151935,)), (5, (0, 4)), (1, (0,)), (4097, (4096,))])
+def test_argmax_first_max(cuda, oracle, n, ties):
+    """The first index of the maximum, as the reference's strict '>' scan:
+    ties inside a chunk, across the two-launch reduction's chunk boundaries,
+    at the last element, and a single element."""
+    v = W.host_normal(n, 3, 3)
+    top = v.max() + 1
+    for t in ties:
+        v[t] = top
     got = int(M.argmax(torch.from_numpy(v).to(cuda)).cpu()[0])
-    assert got == 7 == oracle.argmax(v)
+    assert got == min(ties) == oracle.argmax(v)
+
+
+@pytest.mark.parametrize("typ,n,d", [(W.Q8_0, 2048, 8197), (W.Q4_K, 2048, 4096), (W.Q6_K, 2048, 4100),
+                                     (W.Q8_0, 4096, 4099), (W.Q8_0, 1056, 5000), (W.Q6_K, 3072, 4096)])
+def test_qmatvec_many_rows(cuda, oracle, typ, n, d):
+    """Matrices with many rows (the LM head's path: inputs kept in registers,
+    8 rows fetched per wave at a time): one or two items per lane, row
+    counts that leave a partial last batch, item counts that leave lanes
+    idle; against the oracle's gguf_matmul within 2e-3 of the largest output."""
+    w = W.host_matrix(typ, n, 0, d, 71, W.stream_id(0, W.KIND_LM_HEAD))
+    x = W.host_normal(n, 72, 1)
+    y = torch.empty(d, dtype=torch.float32, device=cuda)
+    M.qmatvec(y, torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), typ, n, d)
+    want = oracle.matmul(typ, w, x, n, d)
+    assert np.abs(y.cpu().numpy() - want).max() <= 2e-3 * np.abs(want).max()

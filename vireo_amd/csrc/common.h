@@ -24,6 +24,7 @@ int vh_check(hipError_t e);            // hipSuccess -> 0, else records the erro
 int vh_finish(hipStream_t s, int rc);  // synchronise when the caller passed no stream
 int vh_device_workspace(size_t bytes, void **out);  // per-device scratch, grown on demand
 int vh_counters(int n, unsigned **out);              // per-device zeroed counters (self-resetting use)
+int vh_reduce_scratch(size_t bytes, void **out);     // per-device scratch for reduction partials
 int vh_num_cus();
 // bytes of a row of n weights of ggml type t (src/gguf.c:27-38; F32 otherwise)
 inline int64_t vh_row_bytes(uint32_t t, int n) {

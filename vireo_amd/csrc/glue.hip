@@ -31,29 +31,56 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(float *o, const float *x,
     for (int i = threadIdx.x; i < n; i += 256) orow[i] = w ? __fmul_rn(__fmul_rn(xr[i], r), w[i]) : __fmul_rn(xr[i], r);
 }
 
-__global__ void __launch_bounds__(1024) argmax_kernel(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
-    __shared__ float bvs[16];
-    __shared__ int bis[16];
-    float bv = v[0];
-    int bi = 0;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float c = v[i];
-        if (c > bv || (c == bv && i < bi)) { bv = c; bi = i; }
+// argmax in two launches: workgroup g of argmax_part_kernel reduces the
+// chunk [g * chunk, (g + 1) * chunk) to its first maximum (value, index);
+// argmax_final_kernel reduces the partials in chunk order. A later index
+// replaces the running best only when strictly greater, an earlier one also
+// when equal, so the result is the first index of the maximum, as the
+// reference's upward scan with a strict '>' from v[0] (src/gguf_run.c:254).
+struct ArgBest {
+    float v;
+    int i;
+};
+VH_DEV void arg_merge(float &bv, int &bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
     }
+}
+VH_DEV void arg_block(float &bv, int &bi, float (&sv)[4], int (&si)[4]) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    for (int off = 32; off > 0; off >>= 1) arg_merge(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
     }
-    if ((threadIdx.x & 63) == 0) { bvs[threadIdx.x >> 6] = bv; bis[threadIdx.x >> 6] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int wv = 1; wv < 16; wv++)
-            if (bvs[wv] > bv || (bvs[wv] == bv && bis[wv] < bi)) { bv = bvs[wv]; bi = bis[wv]; }
-        // the reference scans upward with a strict '>' from v[0]: the first maximum
-        *out = bi;
-    }
+    bv = sv[0];
+    bi = si[0];
+    for (int w = 1; w < 4; w++) arg_merge(bv, bi, sv[w], si[w]);
+}
+
+__global__ void __launch_bounds__(256) argmax_part_kernel(const float *__restrict__ v, int n, int chunk,
+                                                          ArgBest *__restrict__ part) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
+    float bv = v[lo];
+    int bi = lo;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) arg_merge(bv, bi, v[i], i);
+    arg_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) part[blockIdx.x] = ArgBest{bv, bi};
+}
+
+__global__ void __launch_bounds__(256) argmax_final_kernel(const ArgBest *__restrict__ part, int np,
+                                                           int32_t *__restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    float bv = part[0].v;
+    int bi = part[0].i;
+    for (int g = threadIdx.x; g < np; g += 256) arg_merge(bv, bi, part[g].v, part[g].i);
+    arg_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) *out = bi;
 }
 
 // dst[i] = gguf_dequant_row(table row tokens[i]) for i < count, one
@@ -130,6 +157,15 @@ extern "C" int vireo_rmsnorm(float *o, const float *x, const float *w, int n, in
 extern "C" int vireo_argmax(const float *v, int n, int32_t *out, void *stream) {
     if (n <= 0 || !v || !out) return -EINVAL;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
+    // about 4 K values per workgroup, at most 1 024 workgroups
+    int np = (n + 4095) / 4096;
+    if (np > 1024) np = 1024;
+    const int chunk = (n + np - 1) / np;
+    np = (n + chunk - 1) / chunk;
+    void *part;
+    if (int rc = vh_reduce_scratch(sizeof(ArgBest) * size_t(np), &part)) return rc;
+    ArgBest *p = static_cast<ArgBest *>(part);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(np), dim3(256), 0, s, v, n, chunk, p);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, p, np, out);
     return vh_finish(s, vh_check(hipGetLastError()));
 }

@@ -3,7 +3,9 @@
 // qmatvec: each output row is split over L lanes of a wave (L chosen per shape
 // so no lane idles), every lane decodes whole 32-weight items straight from
 // the GGUF bytes with aligned loads, and the L partial sums are folded with a
-// shuffle tree. Rows are streamed once; the kernel is HBM-bound.
+// shuffle tree. Rows are streamed once; the kernel is HBM-bound. Matrices with
+// many rows of 32..128 items (the LM head) take qmatvec_reg_kernel, which
+// keeps each lane's inputs in registers across rows.
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
@@ -62,6 +64,77 @@ int pick_lanes(int items) {
         if (waste < waste_best) { waste_best = waste; best = L; }
     }
     return best;
+}
+
+// Large matrices (the LM head): lane l of every wave owns items l, l + 64, ...
+// (IPL of them, 32 weights each) of every row, so it loads its inputs (and
+// their run sums) once and keeps them in registers for all the rows its wave
+// computes; the wave fetches the raw words of RB rows at a time, then
+// computes and reduces them (one full-wave DPP tree per row).
+template <int T, int IPL, int RB>
+__global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                          const uint8_t *__restrict__ w, int n, int d,
+                                                          int64_t row_bytes) {
+    using F = Reg<T>;
+    constexpr int NS = F::NS;
+    const int lane = threadIdx.x & 63;
+    const int items = F::items(n);
+    float xr[IPL][32], xs[IPL][NS];
+#pragma unroll
+    for (int m = 0; m < IPL; m++) {
+        const int it = lane + 64 * m;
+        if (it < items) {
+            F::load_x(x, it, xr[m]);
+            F::sums(xr[m], xs[m]);
+        }
+    }
+    const int64_t nw = int64_t(gridDim.x) * 4;
+    for (int64_t r0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RB; r0 < d; r0 += nw * RB) {
+        typename F::Raw raw[RB][IPL];
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            const int64_t row = r0 + rr < d ? r0 + rr : d - 1;
+#pragma unroll
+            for (int m = 0; m < IPL; m++) {
+                const int it = lane + 64 * m;
+                if (it < items) raw[rr][m] = F::fetch(w, row * row_bytes, it);
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < IPL; m++) {
+                const int it = lane + 64 * m;
+                if (it < items) acc += F::compute(raw[rr][m], it, xr[m], xs[m]);
+            }
+            acc = group_sum<64>(acc);
+            if (lane == 63 && r0 + rr < d) y[r0 + rr] = acc;
+        }
+    }
+}
+
+template <int T>
+int launch_reg(float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, hipStream_t s) {
+    constexpr int RB = 8;
+    const int items = n / 32;
+    int64_t blocks = (int64_t(d) + 4 * RB - 1) / (4 * RB);
+    const int64_t cap = int64_t(vh_num_cus()) * 8;
+    if (blocks > cap) blocks = cap;
+    dim3 g(static_cast<unsigned>(blocks)), b(256);
+    if (items <= 64)
+        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 1, RB>), g, b, 0, s, y, x, w, n, d, rb);
+    else
+        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 2, RB>), g, b, 0, s, y, x, w, n, d, rb);
+    return vh_check(hipGetLastError());
+}
+
+// the register-input kernel applies to Q8_0 / Q4_K / Q6_K rows of 32..128
+// items with many rows and a 16-byte aligned input
+bool reg_path(uint32_t type, const float *x, int n, int d) {
+    if (type != VT_Q8_0 && type != VT_Q4_K && type != VT_Q6_K) return false;
+    const int items = n / 32;
+    return n % 32 == 0 && items >= 32 && items <= 128 && d >= 4096 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 // ---- dequant ----
@@ -144,6 +217,13 @@ extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int
     if (d == 0) return 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t *wd = static_cast<const uint8_t *>(w->data);
+    if (reg_path(w->ggml_type, x, n, d)) {
+        switch (w->ggml_type) {
+        case VT_Q8_0: return launch_reg<VT_Q8_0>(y, x, wd, n, d, rb, s);
+        case VT_Q4_K: return launch_reg<VT_Q4_K>(y, x, wd, n, d, rb, s);
+        default: return launch_reg<VT_Q6_K>(y, x, wd, n, d, rb, s);
+        }
+    }
     switch (w->ggml_type) {
     case VT_Q8_0:
         if (n % 64 == 0) return launch_L<VT_Q8_0, true>(pick_lanes(n / 64), y, x, wd, n, d, rb, s);

@@ -26,6 +26,35 @@ constexpr int kMaxExperts = 256;
 
 // One wave: router row r (d floats) against x. Lane l owns elements
 // [l*C, l*C + C) so prefix sums follow element order. Returns the part on all lanes.
+// The same part from the lane's C inputs already in registers (columns
+// lane*C .. lane*C + C - 1; d == 64*C).
+template <int C>
+VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&xv)[C], int lane) {
+    float p[C];
+    const float4 *r4 = reinterpret_cast<const float4 *>(r + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 4; i++) {
+        const float4 a = r4[i];
+        p[4 * i + 0] = __fmul_rn(a.x, xv[4 * i + 0]);
+        p[4 * i + 1] = __fmul_rn(a.y, xv[4 * i + 1]);
+        p[4 * i + 2] = __fmul_rn(a.z, xv[4 * i + 2]);
+        p[4 * i + 3] = __fmul_rn(a.w, xv[4 * i + 3]);
+    }
+    double tot = 0.0, absum = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; i++) tot += double(p[i]);
+    double run = wave_incl_scan_d(tot) - tot;
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        run += double(p[i]);
+        absum += fabs(run);
+    }
+    RoutePart out;
+    out.c = wave_sum_d(tot);
+    out.beta = 1.001 * 5.9604644775390625e-08 * wave_sum_d(absum) + 1e-30;
+    return out;
+}
+
 template <int C>
 VH_DEV RoutePart route_row_part(const float *__restrict__ r, const float *__restrict__ x, int d, int lane) {
     double tot = 0.0, run, absum = 0.0;

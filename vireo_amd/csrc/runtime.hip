@@ -14,6 +14,8 @@ struct DevState {
     size_t ws_bytes = 0;
     unsigned *ctr = nullptr;
     int ctr_n = 0;
+    void *red = nullptr;
+    size_t red_bytes = 0;
     int cus = 0;
 };
 DevState g_dev[kMaxDev];
@@ -95,6 +97,27 @@ int vh_counters(int n, unsigned **out) {
         st.ctr_n = nn;
     }
     *out = st.ctr;
+    return 0;
+}
+
+// Grow-only scratch for the partial results of multi-workgroup reductions
+// (argmax), separate from the MoE workspace.
+int vh_reduce_scratch(size_t bytes, void **out) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (bytes > st.red_bytes) {
+        const size_t nb = (bytes + 0xffff) & ~size_t(0xffff);
+        if (st.red) {
+            if (int rc = vh_check(hipDeviceSynchronize())) return rc;
+            if (int rc = vh_check(hipFree(st.red))) return rc;
+            st.red = nullptr;
+            st.red_bytes = 0;
+        }
+        if (int rc = vh_check(hipMalloc(&st.red, nb))) return rc;
+        st.red_bytes = nb;
+    }
+    *out = st.red;
     return 0;
 }
 
