@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
+#include "route_kernels.h"
 #include "vireo_hip.h"
 
 namespace {
@@ -136,10 +137,9 @@ extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *
     const int d = m->dim;
     void *s = stream;
     int rc = vireo_embed(st->lm_head->ggml_type, st->lm_head->data, d, st->vocab, token, 1, x, s);
-    for (int l = 0; l < m->n_layers && !rc; l++) {
-        rc = vireo_rmsnorm(xb, x, st->ffn_norm ? st->ffn_norm[l] : nullptr, d, 1, st->eps, s);
-        if (!rc) rc = moe_ffn_forward(m, l, x, xb, 1, nullptr, nullptr, s);
-    }
+    for (int l = 0; l < m->n_layers && !rc; l++)
+        rc = vh_moe_layer_normed(m, l, x, st->ffn_norm ? st->ffn_norm[l] : nullptr, st->eps, xb,
+                                 static_cast<hipStream_t>(s));
     if (!rc) rc = vireo_rmsnorm(xb, x, st->out_norm, d, 1, st->eps, s);
     if (!rc) rc = qmatvec_async(logits, xb, st->lm_head, d, st->vocab, s);
     if (!rc) rc = vireo_argmax(logits, st->vocab, token, s);

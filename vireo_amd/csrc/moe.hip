@@ -155,6 +155,29 @@ int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *con
 
 }  // namespace
 
+int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
+                        hipStream_t s) {
+    if (int rc = check_model(m, layer)) return rc;
+    if (!x || !xb || !m->es) return -EINVAL;
+    const bool decode = g_path != 2 && g_path != 4 && decode_supported(m, layer) && m->dim == 2048 &&
+                        !((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xb)) & 15u) &&
+                        !(reinterpret_cast<uintptr_t>(m->layers[layer].router->data) & 15u);
+    if (!decode) {
+        if (int rc = vireo_rmsnorm(xb, x, nw, m->dim, 1, eps, s)) return rc;
+        return moe_ffn_forward(m, layer, x, xb, 1, nullptr, nullptr, s);
+    }
+    const vireo_moe_layer &L = m->layers[layer];
+    const void *const *table = nullptr;
+    if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
+    Ws ws;
+    if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, true, false, &ws)) return rc;
+    const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
+    int rc = vh_route_parts_norm(static_cast<const float *>(L.router->data), x, nw, eps, xb, L.logit_bias, m->dim,
+                                 m->n_experts, 1, st.parts, s, st.bar, kFusedBlocks + 1);
+    for (int stage = 1; stage < 3 && !rc; stage++) rc = decode_stage(m, layer, stage, table, x, xb, st, ws.idx, ws.w, s);
+    return rc;
+}
+
 extern "C" int64_t moe_decode_state_bytes(const vireo_moe_model *m) {
     if (check_model(m, 0) || !decode_supported(m, 0)) return -EINVAL;
     size_t off[4];

@@ -34,6 +34,49 @@ __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict
     }
 }
 
+// route_parts_kernel on the RMSNorm of x (src/gguf_run.c:161-165) instead of a
+// given hb: every wave reduces the sum of squares of its token's x in fp64
+// (the same operations in every wave, so the same r), forms
+// hb = (x * r) * w in registers and uses it for its row's part; the wave of
+// expert 0 also writes hb for the later stages. d == 64 * C.
+template <int C>
+__global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__restrict__ R, const float *__restrict__ x,
+                                                              const float *__restrict__ nw, float eps,
+                                                              float *__restrict__ hb_out, const float *__restrict__ bias,
+                                                              int d, int E, RoutePart *__restrict__ parts,
+                                                              uint32_t *__restrict__ zero, int nzero) {
+    const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
+    if (gid < nzero) zero[gid] = 0u;
+    float xv[C];
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + size_t(t) * d + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 4; i++) {
+        const float4 v = x4[i];
+        xv[4 * i + 0] = v.x;
+        xv[4 * i + 1] = v.y;
+        xv[4 * i + 2] = v.z;
+        xv[4 * i + 3] = v.w;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; i++) ss += double(__fmul_rn(xv[i], xv[i]));
+    ss = wave_sum_d(ss);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(float(ss), float(d)), eps)));
+#pragma unroll
+    for (int i = 0; i < C; i++) xv[i] = nw ? __fmul_rn(__fmul_rn(xv[i], r), nw[lane * C + i]) : __fmul_rn(xv[i], r);
+    if (e == 0) {
+        float4 *h4 = reinterpret_cast<float4 *>(hb_out + size_t(t) * d + lane * C);
+#pragma unroll
+        for (int i = 0; i < C / 4; i++) h4[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+    }
+    RoutePart p = route_row_part_regs<C>(R + size_t(e) * d, xv, lane);
+    if (lane == 0) {
+        if (bias) p.c += double(bias[e]);
+        parts[size_t(t) * E + e] = p;
+    }
+}
+
 constexpr int kExTok = 64, kExExp = 16, kExChunk = 64;
 
 // grid (ceil(T/64), ceil(E/16)), 256 threads: lane = token t0 + lane, wave g
@@ -141,6 +184,16 @@ __global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__re
 }
 
 }  // namespace
+
+int vh_route_parts_norm(const float *R, const float *x, const float *nw, float eps, float *hb_out, const float *bias,
+                        int d, int E, int T, RoutePart *parts, hipStream_t s, uint32_t *zero, int nzero) {
+    if (d != 2048 || (reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(hb_out) & 15u) ||
+        (reinterpret_cast<uintptr_t>(R) & 15u) || nzero > E * T * 64)
+        return -EINVAL;
+    VH_LAUNCH(route_parts_norm_kernel<32>, dim3(E, T), dim3(64), 0, s, R, x, nw, eps, hb_out, bias, d, E, parts, zero,
+              nzero);
+    return vh_check(hipGetLastError());
+}
 
 int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
                    RoutePart *parts, hipStream_t s, uint32_t *zero, int nzero) {

@@ -2,11 +2,22 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include "route.h"
+#include "vireo_hip.h"
 
 // Router logits of T tokens into parts[T x E] (fast bounded, or exact); the
 // launch also sets zero[0 .. nzero) to 0 (the fused decode kernel's flags).
 int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
                    RoutePart *parts, hipStream_t s, uint32_t *zero = nullptr, int nzero = 0);
+// The same parts of the RMSNorm of x (weight nw, NULL = unit): the launch also
+// writes hb_out = rmsnorm(x) for the later stages. d == 2048, x and hb_out
+// 16-byte aligned, else -EINVAL.
+int vh_route_parts_norm(const float *R, const float *x, const float *nw, float eps, float *hb_out, const float *bias,
+                        int d, int E, int T, RoutePart *parts, hipStream_t s, uint32_t *zero = nullptr, int nzero = 0);
+// One MoE layer of a stack for one token: xb = rmsnorm(x, nw); x += moe(xb).
+// The one-token decode plan folds the RMSNorm into its router launch; other
+// shapes run vireo_rmsnorm and moe_ffn_forward.
+int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
+                        hipStream_t s);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
