@@ -60,6 +60,11 @@ VH_DEV uint32_t ld_u16(gbyte *p) { return ldg<uint16_t>(p); }
 VH_DEV uint32_t ld_u8(gbyte *p) { return *p; }
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+VH_DEV u32x3 ld_u96(gbyte *p) { return ldg<u32x3>(p); }
+// the same loads through generic pointers (tensors in LDS or traced to an argument)
+VH_DEV uint4 ld_u128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+VH_DEV u32x3 ld_u96(const uint8_t *p) { return *reinterpret_cast<const u32x3 *>(p); }
 VH_DEV uint2 ld_u64(gbyte *p) {
     const u32x2 v = ldg<u32x2>(p);
     return make_uint2(v.x, v.y);
@@ -81,10 +86,10 @@ VH_DEV float h2f(uint32_t h) {
 // 12 bytes at byte offset off (even) of a 4-aligned base, as three dwords:
 // one aligned dwordx3 load of [off&~3, (off&~3)+12), shifted into place. The
 // first two words hold bytes [off, off+8); callers keep the window in bounds.
-VH_DEV void ld12_even(const uint8_t *base, int off, uint32_t &w0, uint32_t &w1) {
+template <class P>
+VH_DEV void ld12_even(P base, int off, uint32_t &w0, uint32_t &w1) {
     const uint32_t s = uint32_t(off) & 3u;
-    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-    const u32x3 v = *reinterpret_cast<const u32x3 *>(base + (off - int(s)));
+    const u32x3 v = ld_u96(base + (off - int(s)));
     w0 = align2(v.y, v.x, s);
     w1 = align2(v.z, v.y, s);
 }

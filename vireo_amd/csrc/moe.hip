@@ -11,6 +11,8 @@
 // many tokens chose it. In calls of at least kMfmaMinCall tokens, groups of at
 // least kMfmaMinTokens tokens run as bf16 matrix-core GEMMs (moe_mfma.hip;
 // 4 more kernels) and only the smaller groups on the fp32 grouped kernels.
+// Calls of fewer tokens run their groups on moe_gdec.hip's kernels, which keep
+// a group's inputs in registers and stream each weight row once.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -345,8 +347,15 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
         act = ws.small;
     }
-    if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
-    if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    // calls of a decode batch's size (a few tokens per group) on the kernels
+    // that hold a group's inputs in registers; larger groups on the tiled ones
+    if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
+        if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
+        if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    } else {
+        if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
+        if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    }
     if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
     return vh_finish(s, rc);
 }

@@ -119,18 +119,19 @@ struct Q6Raw {
 // 8 bytes at even offset `off` of 4-aligned `base`, from the 12-byte aligned
 // window that ends at the first multiple of 4 at or after off + 8 (so the window
 // never reaches past off + 10).
-VH_DEV void ld8_end(const uint8_t *base, int off, uint32_t &w0, uint32_t &w1) {
-    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+template <class P>
+VH_DEV void ld8_end(P base, int off, uint32_t &w0, uint32_t &w1) {
     const int end = (off + 8 + 3) & ~3;
-    const u32x3 v = *reinterpret_cast<const u32x3 *>(base + end - 12);
+    const u32x3 v = ld_u96(base + end - 12);
     const bool four = ((off & 3) == 0);  // bytes [off, off+8) start 4 into the window, else 2
     w0 = four ? v.y : align2(v.y, v.x, 2);
     w1 = four ? v.z : align2(v.z, v.y, 2);
 }
-VH_DEV Q6Raw q6k_fetch(const uint8_t *base, int64_t sbo, int hh, int q) {
+template <class P>
+VH_DEV Q6Raw q6k_fetch(P base, int64_t sbo, int hh, int q) {
     Q6Raw r;
     const int o = int(sbo & 3);
-    const uint8_t *sb = base + (sbo - o);  // 4-aligned; offsets below are relative to it
+    P sb = base + (sbo - o);  // 4-aligned; offsets below are relative to it
     // windows [start, start+12) with start >= field - 2 >= -2 and end <= 196
     ld12_even(sb, o + 64 * hh + 8 * q, r.a0, r.a1);
     ld12_even(sb, o + 64 * hh + 32 + 8 * q, r.b0, r.b1);
@@ -258,9 +259,10 @@ struct Split<VT_Q8_0> {  // paired blocks, 4-aligned
     static constexpr int NW = 64;
     struct Raw { uint32_t w[17]; };
     static VH_DEV int col0(int it) { return 64 * it; }
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) {
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
         Raw r;
-        const uint8_t *p = base + row + 68 * it;
+        P p = base + row + 68 * it;
 #pragma unroll
         for (int i = 0; i < 17; i++) r.w[i] = ld_u32(p + 4 * i);
         return r;
@@ -293,12 +295,13 @@ struct Split<VT_Q4_K> {  // 16-aligned super-blocks
     static constexpr int NW = 32;
     struct Raw { uint4 hdr, q; };
     static VH_DEV int col0(int it) { const int sb = it >> 3, r = it & 7; return 256 * sb + 64 * (r >> 1) + 16 * (r & 1); }
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) {
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
         const int sb = it >> 3, r = it & 7;
-        const uint8_t *p = base + row + 144 * sb;
+        P p = base + row + 144 * sb;
         Raw w;
-        w.hdr = *reinterpret_cast<const uint4 *>(p);
-        w.q = *reinterpret_cast<const uint4 *>(p + 16 + 32 * (r >> 1) + 16 * (r & 1));
+        w.hdr = ld_u128(p);
+        w.q = ld_u128(p + 16 + 32 * (r >> 1) + 16 * (r & 1));
         return w;
     }
     // sl, sh: sums of the low-run and high-run inputs
@@ -346,7 +349,8 @@ struct Split<VT_Q6_K> {  // even-offset super-blocks
     static constexpr int NW = 32;
     using Raw = Q6Raw;
     static VH_DEV int col0(int it) { const int sb = it >> 3, r = it & 7; return 256 * sb + 128 * (r >> 2) + 8 * (r & 3); }
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) {
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
         const int sb = it >> 3, r = it & 7;
         return q6k_fetch(base, row + 210 * sb, r >> 2, r & 3);
     }
@@ -405,7 +409,8 @@ struct Reg<VT_Q4_K> {
     static constexpr int NS = 2;
     using Raw = Split<VT_Q4_K>::Raw;
     static __host__ __device__ int items(int n) { return n / 32; }
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) { return Split<VT_Q4_K>::fetch(base, row, it); }
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) { return Split<VT_Q4_K>::fetch(base, row, it); }
     static VH_DEV void load_x(const float *row, int it, float (&x)[32]) {
         load_runs<2, 16, 32>(row + Split<VT_Q4_K>::col0(it), x);
     }
@@ -452,7 +457,8 @@ struct Reg<VT_Q6_K> {
     static constexpr int NS = 4;
     using Raw = Q6Raw;
     static __host__ __device__ int items(int n) { return n / 32; }
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) { return Split<VT_Q6_K>::fetch(base, row, it); }
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) { return Split<VT_Q6_K>::fetch(base, row, it); }
     static VH_DEV void load_x(const float *row, int it, float (&x)[32]) {
         load_runs<4, 8, 32>(row + Split<VT_Q6_K>::col0(it), x);
     }
@@ -478,11 +484,12 @@ struct Reg<VT_Q8_0> {
     // block it of the row at byte offset row (even): the aligned window from
     // the dword holding its first byte; the last word is completed with a
     // 16-bit load when the block starts 2 mod 4, so nothing past the block is read
-    static VH_DEV Raw fetch(const uint8_t *base, int64_t row, int it) {
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
         const int64_t b = row + 34 * int64_t(it);
         Raw r;
         r.s = uint32_t(b) & 3u;
-        const uint8_t *a = base + (b - int64_t(r.s));
+        P a = base + (b - int64_t(r.s));
 #pragma unroll
         for (int i = 0; i < 8; i++) r.w[i] = ld_u32(a + 4 * i);
         r.w[8] = ld_u16(a + 32) | (r.s ? (ld_u16(a + 34) << 16) : 0u);

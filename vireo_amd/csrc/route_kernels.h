@@ -54,6 +54,17 @@ int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, c
 int vh_combine(const int32_t *idx, const float *w, const void *const *table, const float *ybuf, int d, int k, int T,
                float *x, hipStream_t s);
 
+// Decode-style grouped projections (moe_gdec.hip): the same inputs and outputs
+// as vh_grouped_gateup / vh_grouped_down; Q8_0 / Q4_K / Q6_K rows of at most
+// 2048 weights and a 16-byte aligned hb.
+bool vh_gdec_supported(uint32_t tg, uint32_t td, int d, int fe, const float *hb);
+int vh_gdec_gateup(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
+                   const int32_t *active, const void *const *table, const float *hb, int d, int fe, int k, int E,
+                   int max_slots, float *h, hipStream_t s);
+int vh_gdec_down(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
+                 const int32_t *active, const void *const *table, const float *h, int d, int fe, int E, int max_slots,
+                 float *ybuf, hipStream_t s);
+
 // Matrix-core grouped GEMMs (moe_mfma.hip) for groups of at least
 // kMfmaMinTokens tokens, in calls of at least kMfmaMinCall tokens (below that
 // no group is expected to reach the size). vh_mfma_plan lists their token
