@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--plan", type=int, default=0,
+                    help="execution plan (vireo_hip_set_path): 0 automatic, 1 decode, 2 grouped, 3 fused, 4 fp32")
     return ap.parse_args()
 
 
@@ -161,6 +163,7 @@ def bench_stack(args):
 
     lib = _lib.load()
     _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    _lib.check(lib.vireo_hip_set_path(args.plan), "vireo_hip_set_path")
     shape_name, L, vocab = STACKS[args.workload]
     L = args.layers or L
     shape = W.SHAPES[shape_name]
@@ -262,6 +265,7 @@ def main():
 
     lib = _lib.load()
     _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    _lib.check(lib.vireo_hip_set_path(args.plan), "vireo_hip_set_path")
     dev = torch.device("cuda:0")
     shape_name, B, L, biased = WORKLOADS[args.workload]
     L = args.layers or L
@@ -321,7 +325,7 @@ def main():
                    "d": shape.d, "experts": shape.E, "top_k": shape.k, "ffn_exp": shape.fe,
                    "renorm": shape.renorm, "types": [W.TYPE_NAMES[t] for t in (shape.gate_type, shape.up_type,
                                                                                 shape.down_type)],
-                   "tokens_per_step": B, "layers_rotated": L, "router_bias": "log Zipf(1.1)" if biased else None},
+                   "tokens_per_step": B, "layers_rotated": L, "plan": args.plan, "router_bias": "log Zipf(1.1)" if biased else None},
         "us_per_layer": round(ms_per_step * 1e3, 3),
         "layer_alg_bytes": int(lb), "distinct_experts": int(distinct),
         "layer_GBps": round(layer_gbs, 1), "layer_frac_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),

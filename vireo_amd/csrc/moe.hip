@@ -147,7 +147,7 @@ int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *con
             return vh_decode_experts(tg, td, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h,
                                      st.bar, x, idx, w, s);
         return vh_decode_gateup(tg, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h, idx, w,
-                                st.flags(), st.plan, s);
+                                st.flags(), st.plan, td, s);
     case 2:
         if (fused(m, layer)) return 0;
         return vh_down_combine(td, st.plan, st.h, d, fe, k, x, s);

@@ -33,7 +33,7 @@ struct DecodePlan {
 // Decode path (one token): gate/up with the top-k fused in, then down + combine.
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
-                     uint32_t *flags, DecodePlan *plan, hipStream_t s);
+                     uint32_t *flags, DecodePlan *plan, uint32_t down_type, hipStream_t s);
 bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
 // Down projection + weighted combine + residual for one token:
 // x += sum_j plan.w[j] * down_j h[j], in selection order.
