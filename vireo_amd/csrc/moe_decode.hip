@@ -244,34 +244,27 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     const uint8_t *D = static_cast<const uint8_t *>(plan->down[j]);
     // what the combine needs, loaded now: lane j2 < k of wave 0 holds expert
     // j2's weight and whether its lookup succeeded, thread tid < R its output
-    float wj2 = 0.0f, xo = 0.0f;
-    int pres = 0;
-    if (tid < 64 && lane < k) {
-        pres = plan->down[lane] != nullptr;
-        wj2 = plan->w[lane];
-    }
-    if (tid < R) xo = x[o0 + tid];
-    // activations of expert j for this lane's items (independent of the plan)
+    // (unconditional loads: DecodePlan has 64 entries and lanes past k are not
+    // read; the pointer is tested only in the combine, so nothing waits for it
+    // earlier)
+    const void *dj2 = plan->down[lane];
+    const float wj2 = plan->w[lane];
+    const float xo = x[o0 + min(tid, R - 1)];
+    // activations of expert j for this lane's items (independent of the plan;
+    // items past the row repeat its last one, and their products are skipped)
     float xv[IPL][32], xs[IPL][NS];
 #pragma unroll
-    for (int m = 0; m < IPL; m++) {
-        const int it = li + L * m;
-        if (it < items) {
-            F::load_x(h + size_t(j) * fe, it, xv[m]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; i++) xv[m][i] = 0.0f;
-        }
-    }
+    for (int m = 0; m < IPL; m++) F::load_x(h + size_t(j) * fe, min(li + L * m, items - 1), xv[m]);
+    // every lane loads (items past the row repeat its last one and are not
+    // used), through a global-address-space pointer, with no branch: all the
+    // loads are in flight before the first is used
     typename F::Raw raw[kDnRpg][IPL];
     if (D) {
 #pragma unroll
         for (int rr = 0; rr < kDnRpg; rr++)
 #pragma unroll
-            for (int m = 0; m < IPL; m++) {
-                const int it = li + L * m;
-                if (it < items) raw[rr][m] = F::fetch(D, int64_t(o0 + rf + rr * rstep) * row_bytes, it);
-            }
+            for (int m = 0; m < IPL; m++)
+                raw[rr][m] = F::fetch(gmem(D), int64_t(o0 + rf + rr * rstep) * row_bytes, min(li + L * m, items - 1));
     }
 #pragma unroll
     for (int m = 0; m < IPL; m++) F::sums(xv[m], xs[m]);
@@ -290,6 +283,7 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     }
     __syncthreads();
     if (tid < 64) {  // R <= 64: the combining threads are in wave 0
+        const int pres = dj2 != nullptr;
         float a = 0.0f;
         for (int j2 = 0; j2 < k; j2++) {
             const int present = __builtin_amdgcn_readlane(pres, j2);

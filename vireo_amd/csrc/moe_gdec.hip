@@ -33,7 +33,7 @@ template <>
 struct Prep<VT_Q4_K> {  // d1·Σq·x − m1·Σx over the low and the high nibbles
     uint4 q;
     float d1, m1, d2, m2;
-    VH_DEV void set(const Reg<VT_Q4_K>::Raw &r, int it) {
+    VH_DEV void set(const Reg<VT_Q4_K>::Words &r, int it) {
         const int c = (it & 7) >> 1;
         const float d = h2f(r.hdr.x & 0xffffu), dmin = h2f(r.hdr.x >> 16);
         int sc0, mn0, sc1, mn1;
@@ -98,7 +98,7 @@ template <>
 struct Prep<VT_Q8_0> {  // d·Σq·x over the block's 32 signed bytes
     uint32_t q[8];
     float d;
-    VH_DEV void set(const Reg<VT_Q8_0>::Raw &r, int) {
+    VH_DEV void set(const Reg<VT_Q8_0>::Words &r, int) {
         d = h2f((r.w[0] >> (8 * r.s)) & 0xffffu);
         const uint32_t sh = 16 + 8 * r.s;
 #pragma unroll
@@ -186,8 +186,8 @@ __global__ void __launch_bounds__(512) gdec_gateup_kernel(const int32_t *__restr
                 for (int m = 0; m < IPL; m++) {
                     const int it = lane + 64 * m;
                     if (it < items) {
-                        pg[m].set(rg[r][m], it);
-                        pu[m].set(ru[r][m], it);
+                        pg[m].set(F::resolve(rg[r][m], it), it);
+                        pu[m].set(F::resolve(ru[r][m], it), it);
                     }
                 }
 #pragma unroll
@@ -283,7 +283,7 @@ __global__ void __launch_bounds__(512) gdec_down_kernel(const int32_t *__restric
 #pragma unroll
                 for (int m = 0; m < IPL; m++) {
                     const int it = li + L * m;
-                    if (it < items) pw[m].set(raw[r][m], it);
+                    if (it < items) pw[m].set(F::resolve(raw[r][m], it), it);
                 }
 #pragma unroll
                 for (int j = 0; j < NT; j++) {

@@ -188,11 +188,11 @@ __global__ void __launch_bounds__(256) dispatch_place_kernel(const int32_t *__re
 }
 
 // ------------------------------------------------------------ grouped projections
-// An item's 32 weights dequantized from the raw words of Reg<T>::fetch, in the
+// An item's 32 weights dequantized from the resolved words of Reg<T>::fetch, in the
 // item's own order (the order Reg<T>::load_x gives the inputs): every value is
 // the reference's dequantized weight (src/gguf_compute.c:52-103, 112-120).
 template <int T>
-VH_DEV void deq_raw(const typename Reg<T>::Raw &r, float (&w)[32]) {
+VH_DEV void deq_raw(const typename Reg<T>::Words &r, float (&w)[32]) {
     if constexpr (T == VT_Q4_K) {
         // the item's two sub-blocks: c = it/2 % 4 is not in the raw words, so
         // the caller passes the scale pair through deq_q4k below
@@ -238,7 +238,8 @@ VH_DEV void deq_q4k(const Reg<VT_Q4_K>::Raw &r, int it, float (&w)[32]) {
     }
 }
 template <int T>
-VH_DEV void deq_item(const typename Reg<T>::Raw &r, int it, float (&w)[32]) {
+VH_DEV void deq_item(const typename Reg<T>::Raw &raw, int it, float (&w)[32]) {
+    const typename Reg<T>::Words &r = Reg<T>::resolve(raw, it);
     if constexpr (T == VT_Q4_K) deq_q4k(r, it, w);
     else deq_raw<T>(r, w);
 }

@@ -145,6 +145,44 @@ VH_DEV Q6Raw q6k_fetch(P base, int64_t sbo, int hh, int q) {
     r.d = ld_u16(sb + o + 208);
     return r;
 }
+// The same item as the aligned windows the loads return, before any
+// arithmetic on them: a kernel that issues many items' loads before using any
+// keeps them all in flight (arithmetic on a loaded word waits for the load).
+struct Q6Win {
+    u32x3 a, b, h, s;  // 12-byte windows holding ql[.. +8q], ql[.. +32 +8q], qh[.. +8q], scales[8hh ..]
+    uint32_t d;        // f16 bits
+    uint32_t o;        // sbo & 3 (0 or 2): where each field starts in its window
+};
+template <class P>
+VH_DEV Q6Win q6k_fetch_raw(P base, int64_t sbo, int hh, int q) {
+    Q6Win r;
+    r.o = uint32_t(sbo & 3);
+    P sb = base + (sbo - int64_t(r.o));
+    // the windows of ld12_even (fields at offsets o + 8m, o even) and ld8_end
+    r.a = ld_u96(sb + 64 * hh + 8 * q);
+    r.b = ld_u96(sb + 64 * hh + 32 + 8 * q);
+    r.h = ld_u96(sb + 128 + 32 * hh + 8 * q);
+    r.s = ld_u96(sb + ((int(r.o) + 192 + 8 * hh + 8 + 3) & ~3) - 12);
+    r.d = ld_u16(sb + r.o + 208);
+    return r;
+}
+// q6k_fetch's words from the windows (q = item index mod 4)
+VH_DEV Q6Raw q6k_resolve(const Q6Win &w, int q) {
+    Q6Raw r;
+    r.a0 = align2(w.a.y, w.a.x, w.o);
+    r.a1 = align2(w.a.z, w.a.y, w.o);
+    r.b0 = align2(w.b.y, w.b.x, w.o);
+    r.b1 = align2(w.b.z, w.b.y, w.o);
+    r.h0 = align2(w.h.y, w.h.x, w.o);
+    r.h1 = align2(w.h.z, w.h.y, w.o);
+    const bool four = w.o == 0u;  // as ld8_end
+    const uint32_t s0 = four ? w.s.y : align2(w.s.y, w.s.x, 2), s1 = four ? w.s.z : align2(w.s.z, w.s.y, 2);
+    const uint32_t sh = 8u * uint32_t(q >> 1);
+    const uint32_t t0 = (s0 >> sh) & 0x00ff00ffu, t1 = (s1 >> sh) & 0x00ff00ffu;
+    r.sc = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+    r.d = w.d;
+    return r;
+}
 // xv: the item's 32 inputs, g-major (xv[8g + i] = x[128hh + 32g + 8q + i])
 template <class XV>
 VH_DEV float q6k_compute(const Q6Raw &r, const XV &xv) {
@@ -407,7 +445,9 @@ VH_DEV void load_runs(const float *__restrict__ p, float (&x)[32]) {
 template <>
 struct Reg<VT_Q4_K> {
     static constexpr int NS = 2;
-    using Raw = Split<VT_Q4_K>::Raw;
+    using Raw = Split<VT_Q4_K>::Raw;  // two 16-byte loads: nothing to resolve
+    using Words = Raw;
+    static VH_DEV const Words &resolve(const Raw &r, int) { return r; }
     static __host__ __device__ int items(int n) { return n / 32; }
     template <class P>
     static VH_DEV Raw fetch(P base, int64_t row, int it) { return Split<VT_Q4_K>::fetch(base, row, it); }
@@ -455,10 +495,15 @@ VH_DEV float q6k_compute_s(const Q6Raw &r, const float (&x)[32], const float (&s
 template <>
 struct Reg<VT_Q6_K> {
     static constexpr int NS = 4;
-    using Raw = Q6Raw;
+    using Raw = Q6Win;
+    using Words = Q6Raw;
     static __host__ __device__ int items(int n) { return n / 32; }
     template <class P>
-    static VH_DEV Raw fetch(P base, int64_t row, int it) { return Split<VT_Q6_K>::fetch(base, row, it); }
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
+        const int sb = it >> 3, r = it & 7;
+        return q6k_fetch_raw(base, row + 210 * sb, r >> 2, r & 3);
+    }
+    static VH_DEV Words resolve(const Raw &r, int it) { return q6k_resolve(r, it & 3); }
     static VH_DEV void load_x(const float *row, int it, float (&x)[32]) {
         load_runs<4, 8, 32>(row + Split<VT_Q6_K>::col0(it), x);
     }
@@ -471,19 +516,21 @@ struct Reg<VT_Q6_K> {
             s[g] = a;
         }
     }
-    static VH_DEV float compute(const Raw &r, int, const float (&x)[32], const float (&s)[NS]) {
-        return q6k_compute_s(r, x, s);
+    static VH_DEV float compute(const Raw &r, int it, const float (&x)[32], const float (&s)[NS]) {
+        return q6k_compute_s(resolve(r, it), x, s);
     }
 };
 
 template <>
 struct Reg<VT_Q8_0> {
     static constexpr int NS = 1;
-    struct Raw { uint32_t w[9], s; };
+    struct Raw { uint32_t w[8], lo, hi, s; };
+    struct Words { uint32_t w[9], s; };
     static __host__ __device__ int items(int n) { return n / 32; }
     // block it of the row at byte offset row (even): the aligned window from
-    // the dword holding its first byte; the last word is completed with a
-    // 16-bit load when the block starts 2 mod 4, so nothing past the block is read
+    // the dword holding its first byte. Its last word is two 16-bit loads, at
+    // a + 32 and at a + 32 + s (the same halfword when the block starts 4-aligned),
+    // so nothing past the block is read and no load depends on another.
     template <class P>
     static VH_DEV Raw fetch(P base, int64_t row, int it) {
         const int64_t b = row + 34 * int64_t(it);
@@ -492,12 +539,22 @@ struct Reg<VT_Q8_0> {
         P a = base + (b - int64_t(r.s));
 #pragma unroll
         for (int i = 0; i < 8; i++) r.w[i] = ld_u32(a + 4 * i);
-        r.w[8] = ld_u16(a + 32) | (r.s ? (ld_u16(a + 34) << 16) : 0u);
+        r.lo = ld_u16(a + 32);
+        r.hi = ld_u16(a + 32 + r.s);
         return r;
+    }
+    static VH_DEV Words resolve(const Raw &r, int) {
+        Words v;
+#pragma unroll
+        for (int i = 0; i < 8; i++) v.w[i] = r.w[i];
+        v.w[8] = r.lo | (r.hi << 16);  // the high half is not read when s == 0
+        v.s = r.s;
+        return v;
     }
     static VH_DEV void load_x(const float *row, int it, float (&x)[32]) { load_runs<1, 32, 32>(row + 32 * it, x); }
     static VH_DEV void sums(const float (&)[32], float (&s)[NS]) { s[0] = 0.0f; }
-    static VH_DEV float compute(const Raw &r, int, const float (&x)[32], const float (&)[NS]) {
+    static VH_DEV float compute(const Raw &raw, int it, const float (&x)[32], const float (&)[NS]) {
+        const Words r = resolve(raw, it);
         const float d = h2f((r.w[0] >> (8 * r.s)) & 0xffffu);
         const uint32_t sh = 16 + 8 * r.s;
         float acc = 0.0f;
