@@ -83,10 +83,12 @@ def alg_bytes_experts(shape):
 
 
 def alg_bytes_gateup(shape):
-    """Stage 1 for one token: k experts' gate and up slices, hb, the router
+    """Stage 1 for one token: k experts' gate and up slices, and their down
+    slices too (the kernel loads every 64-byte line of the down rows ahead of
+    the down kernel, so these bytes leave HBM in this kernel), hb, the router
     parts and expert table it reads, the k x fe activations it writes."""
-    gs, us, _ = shape.slice_bytes()
-    return shape.k * (gs + us) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + shape.k * shape.fe * 4
+    gs, us, ds = shape.slice_bytes()
+    return shape.k * (gs + us + ds) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + shape.k * shape.fe * 4
 
 
 def cpu_baseline(shape, B, seed, seconds):
@@ -367,7 +369,7 @@ def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
     fused = times[2][0] == 0.0  # stage 1 was the fused kernel: gate/up, down and combine in one launch
     nb = alg_bytes_experts(shape) if fused else alg_bytes_gateup(shape)
     kname = ("decode_experts_kernel (top-k, gate/up, down, combine; stage 1)" if fused
-             else "decode_gateup_kernel (top-k + gate/up SwiGLU, stage 1)")
+             else "decode_gateup_kernel (top-k + gate/up SwiGLU + down rows warmed, stage 1)")
     avg = times[1][0]
     gbs = nb / (avg * 1e-6) / 1e9
     traffic = None

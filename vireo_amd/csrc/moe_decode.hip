@@ -41,14 +41,17 @@ constexpr int kGuWaves = 8;
 // grid (ceil(fe / (kGuWaves * RPW)), k), 512 threads, d = 2048 (lane l owns
 // item l of a row), E <= 64 * Q. The arguments the prologue needs come first:
 // they are the ones preloaded into SGPRs at launch.
-// L2 warm-up of the down rows (pf_rows > 0): workgroup L runs on XCD L % 8,
+// Warm-up of the down rows (pf_rows > 0): workgroup L runs on XCD L % 8,
 // and so does the down kernel's workgroup b (rows [pf_rows b, pf_rows (b + 1))
 // of every chosen expert) for b = L % 8 (mod 8). With gridDim.x and the down
 // grid nbd both multiples of 8, the gridDim.x / 8 gate/up workgroups of expert
 // slot j on XCD x share the nbd / 8 down workgroups b = x + 8 i of that XCD
 // (i = q mod gridDim.x / 8 for the workgroup with blockIdx.x = x' + 8 q) and
 // load one word of every 64-byte line of those rows of expert j's down
-// matrix, so the down kernel reads them from this XCD's L2.
+// matrix. Measured on MI355X: the down kernel's L2 miss bytes (FETCH_SIZE)
+// are the same with or without it, so its reads are served from beyond the L2
+// (the memory-side Infinity Cache), and this XCD-matched split is faster than
+// a contiguous split of each matrix (18.3 against 18.65 us per Qwen3 layer).
 constexpr int kPfPerThread = 3;  // warm-up lines per thread: at most 1536 per workgroup
 
 template <int T, int Q, int RPW>
@@ -137,7 +140,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
         rg[r] = F::fetch(gmem(G), o * row_bytes, lane);
         ru[r] = F::fetch(gmem(U), o * row_bytes, lane);
     }
-    // the down rows' L2 warm-up, issued after this workgroup's own loads.
+    // the down rows' warm-up, issued after this workgroup's own loads.
     // Unconditional loads (threads past the last line repeat it) whose values
     // are used only by the asm statement at the end, so no wait for them, or
     // for the weights issued before them, comes earlier.
@@ -167,7 +170,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     for (int u = 0; u < kPfPerThread; u++) asm volatile("" ::"v"(pf[u]));  // keeps the warm-up loads
 }
 
-// The down kernel's row blocks, for the L2 warm-up (0 rows: none).
+// The down kernel's row blocks, for the warm-up (0 rows: none).
 struct DownPrefetch {
     int rows, nbd;
     int64_t rb;
