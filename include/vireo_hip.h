@@ -193,10 +193,11 @@ typedef struct {
     const float *const *ffn_norm;  /* host array [n_layers] of device [dim] F32 RMSNorm weights (an
                                       entry or the array NULL: unit weight) */
     const float *out_norm;         /* device [dim] F32, or NULL (unit weight) */
-    const gguf_tensor *lm_head;    /* [vocab x dim], data on the device; also the token embedding
-                                      (a tied model, src/gguf_run.c:297) */
+    const gguf_tensor *lm_head;    /* [vocab x dim], data on the device */
     int vocab;
     float eps;
+    const gguf_tensor *tok_embd;   /* [vocab x dim] token embedding (Q8_0, F16 or F32), data on the
+                                      device; NULL: lm_head (a tied model, src/gguf_run.c:297) */
 } vireo_moe_stack;
 
 /* One greedy decode step, forward() (src/gguf_run.c:216-251) with attention
@@ -208,6 +209,40 @@ typedef struct {
  * caller can capture a loop of steps in a graph (after one uncaptured step:
  * the first call on a layer pins its expert leases). */
 int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits, void *stream);
+
+/* ---- MoE models from GGUF files (src/gguf_run.c:266-333) ---------------------- */
+
+/* A MoE model read from a GGUF file: the metadata and MoE tensors bound as the
+ * reference's loader binds them, the routers, FFN norms, output norm and LM head
+ * copied to the device, and every expert's gate/up/down slice registered with
+ * an ExpertStore that pages them from the open file into HBM. */
+typedef struct {
+    gguf_ctx *gguf;          /* the parsed file (host mapping), from vireo_gguf_open */
+    char arch[64];           /* general.architecture ("qwen2" if absent, as the reference) */
+    vireo_moe_model model;   /* ready for moe_ffn_forward */
+    vireo_moe_stack stack;   /* ready for moe_stack_step when lm_head != NULL */
+    int vocab;               /* token_embd.weight dims[1]; 0 without that tensor */
+    float eps;               /* <arch>.attention.layer_norm_rms_epsilon (0 if absent, as the reference) */
+    void *priv;              /* the library's allocations */
+} vireo_gguf_moe;
+
+/* Read an MoE GGUF file (general.architecture, <arch>.block_count,
+ * embedding_length, feed_forward_length, expert_count, expert_used_count
+ * (default 8), expert_feed_forward_length (default feed_forward_length),
+ * expert_weights_norm (default: renormalise unless the architecture is
+ * "olmoe"), as src/gguf_run.c:276-292), bind blk.<l>.ffn_gate_inp / ffn_gate_exps
+ * / ffn_up_exps / ffn_down_exps / ffn_norm (:315-318), and register expert e of
+ * layer l at tensor offset + e * (nbytes / n_experts) (:320-333) with an
+ * ExpertStore of expert_capacity_bytes (0 = unbounded) over the file. With
+ * load_head, output_norm.weight and the LM head (output.weight, else
+ * token_embd.weight, :297-299) and token_embd.weight go to the device too.
+ * Returns 0, -EINVAL for a file that is not such a model (the message names
+ * what is missing or inconsistent: vireo_gguf_moe_error), or -errno. */
+int vireo_gguf_moe_load(const char *path, uint64_t expert_capacity_bytes, int load_head, vireo_gguf_moe **out);
+/* Why the last vireo_gguf_moe_load on this thread failed ("" after a success). */
+const char *vireo_gguf_moe_error(void);
+/* Destroy the store, free the device copies and close the file. */
+void vireo_gguf_moe_free(vireo_gguf_moe *m);
 
 /* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
 

@@ -1,0 +1,110 @@
+"""MoE models read from GGUF files (vireo_gguf_moe_load) on the GPU, against
+the oracle on the arrays that were written into the file.
+
+* Layers: the loader binds every layer's router and expert tensors and
+  registers expert e at offset + e * slice (src/gguf_run.c:320-333); each
+  layer's moe_ffn_forward over a few tokens then matches the oracle's moe_ffn
+  on the written router and expert bytes (routing exact, outputs within 2e-3
+  of the layer's largest contribution). Shapes: Qwen3 Q4_K/Q6_K layers with
+  16 experts (the one-token decode plan for single tokens) and d=256 layers
+  of every expert type (the grouped plan). The metadata read back (top-k,
+  widths, renormalisation rule by architecture, eps) is what was written.
+* The store pages the experts from the file: after a layer's first call its
+  resident bytes are the layer's expert bytes, read once.
+* Stack: moe_stack_step on the file's ffn norms, output norm, LM head and
+  token embedding (untied and tied) against the oracle's decode skeleton
+  (src/gguf_run.c:216-254 with attention omitted), as in test_gpu_stack.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import expert_lists
+from vireo_amd import gguf as G
+from vireo_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+SHAPES = {
+    "qwen3-16e": W.SHAPES["qwen3-30b-a3b-q4_k_m"].with_(name="qwen3-16e", E=16),
+    "tiny-k": W.MoEShape("tiny-k", 256, 8, 2, 256, True, W.Q4_K, W.Q4_K, W.Q6_K),
+    "tiny-q8": W.MoEShape("tiny-q8", 256, 8, 3, 256, False, W.Q8_0, W.Q8_0, W.Q8_0),
+}
+
+
+def check(name, x, xg, xo, idx_g, idx_o):
+    np.testing.assert_array_equal(idx_g, idx_o)
+    dg, do = xg - x, xo - x
+    rel = np.abs(dg - do).max() / np.abs(do).max()
+    print(f"{name}: max rel {rel:.2e}")
+    assert rel <= TOL
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_gguf_layers_match_oracle(cuda, oracle, tmp_path, name):
+    shape, L = SHAPES[name], 2
+    path = tmp_path / f"{name}.gguf"
+    arr = G.write_moe_gguf(str(path), shape, L, seed=29)
+    m = G.GGUFModel(path, load_head=False)
+    assert (m.arch, m.n_layers, m.d, m.E, m.k, m.fe, m.renorm) == (G.moe_arch(shape), L, shape.d, shape.E,
+                                                                    shape.k, shape.fe, shape.renorm)
+    assert m.eps == np.float32(W.EPS)
+    gs, us, ds = shape.slice_bytes()
+    for layer in range(L):
+        Gl, Ul, Dl = expert_lists(shape, *arr["experts"][layer])
+        for T in (1, 5):
+            x, hb = W.host_hidden(shape.d, T, seed=layer * 7 + T)
+            xg, hg = torch.from_numpy(x).to(cuda), torch.from_numpy(hb).to(cuda)
+            idx, _ = m.forward(layer, xg, hg, return_routing=True)
+            xo, io, _, _ = oracle.moe_ffn(shape, arr["routers"][layer], Gl, Ul, Dl, x, hb)
+            check(f"{name} layer {layer} T={T}", x, xg.cpu().numpy(), xo, idx.cpu().numpy(), io)
+        st = m.stats()
+        assert st["resident_bytes"] == (layer + 1) * shape.E * (gs + us + ds)
+        assert st["bytes_read"] == st["resident_bytes"]
+    m.close()
+
+
+def oracle_stack(oracle, shape, arr, L, vocab):
+    d = shape.d
+    rb = W.row_bytes(W.Q8_0, d)
+    emb, head = arr["token_embd"], arr["output"]
+    layers = [expert_lists(shape, *arr["experts"][l]) for l in range(L)]
+
+    def step(tok):
+        x = oracle.dequant_row(W.Q8_0, emb[tok * rb:(tok + 1) * rb], d)
+        for l in range(L):
+            xb = oracle.rmsnorm(x, arr["ffn_norm"][l], W.EPS)
+            x = oracle.moe_ffn(shape, arr["routers"][l], *layers[l], x, xb)[0][0]
+        logits = oracle.matmul(W.Q8_0, head, oracle.rmsnorm(x, arr["out_norm"], W.EPS), d, vocab)
+        return x, logits, oracle.argmax(logits)
+    return step
+
+
+@pytest.mark.parametrize("name,untied", [("tiny-k", True), ("tiny-k", False), ("qwen3-16e", True)])
+def test_gguf_stack_matches_oracle(cuda, oracle, tmp_path, name, untied):
+    """qwen3-16e runs the one-token decode plan, whose router launch applies
+    the file's RMSNorm weights itself; tiny-k the grouped plan."""
+    shape, L, vocab = SHAPES[name], 3, 700
+    path = tmp_path / "stack.gguf"
+    arr = G.write_moe_gguf(str(path), shape, L, seed=37, vocab=vocab, untied=untied)
+    m = G.GGUFModel(path)
+    assert m.vocab == vocab
+    ref = oracle_stack(oracle, shape, arr, L, vocab)
+    x = torch.empty(shape.d, dtype=torch.float32, device=cuda)
+    xb = torch.empty_like(x)
+    logits = torch.empty(vocab, dtype=torch.float32, device=cuda)
+    token = torch.empty(1, dtype=torch.int32, device=cuda)
+    for i, tok in enumerate((5, vocab - 1, vocab // 2, 0)):
+        token.fill_(tok)
+        m.step(token, x, xb, logits)
+        xo, lo, to = ref(tok)
+        xg, lg, tg = x.cpu().numpy(), logits.cpu().numpy(), int(token.cpu()[0])
+        rx = np.abs(xg - xo).max() / np.abs(xo).max()
+        rl = np.abs(lg - lo).max() / np.abs(lo).max()
+        print(f"{name} untied={untied} step {i}: token {tok} -> {tg} (oracle {to}); x {rx:.2e}, logits {rl:.2e}")
+        assert rx <= TOL and rl <= TOL
+        top2 = np.sort(lo)[-2:]
+        if top2[1] - top2[0] > TOL * np.abs(lo).max():
+            assert tg == to
+    m.close()

@@ -14,7 +14,11 @@ c_i32p = C.POINTER(C.c_int32)
 
 
 class GGUFStr(C.Structure):
-    _fields_ = [("ptr", C.c_char_p), ("len", C.c_uint64)]
+    """gguf_str: `len` bytes at `ptr` (inside a file mapping: not NUL-terminated)."""
+    _fields_ = [("ptr", c_vp), ("len", C.c_uint64)]
+
+    def text(self):
+        return C.string_at(self.ptr, self.len).decode("utf-8", "replace") if self.len else ""
 
 
 class GGUFTensor(C.Structure):
@@ -74,6 +78,46 @@ class MoEStack(C.Structure):
         ("lm_head", C.POINTER(GGUFTensor)),
         ("vocab", C.c_int),
         ("eps", C.c_float),
+        ("tok_embd", C.POINTER(GGUFTensor)),
+    ]
+
+
+class GGUFKV(C.Structure):
+    """gguf_kv (src/gguf.h:27-34); `val` is the union's 8 bytes."""
+    _fields_ = [
+        ("key", GGUFStr),
+        ("type", C.c_uint32),
+        ("val", C.c_uint64),
+        ("str", GGUFStr),
+        ("arr_type", C.c_uint32),
+        ("arr_len", C.c_uint64),
+        ("arr_data", c_vp),
+    ]
+
+
+class GGUFCtx(C.Structure):
+    """gguf_ctx (src/gguf.h:47-55)."""
+    _fields_ = [
+        ("fd", C.c_int), ("map", c_vp), ("size", C.c_size_t),
+        ("version", C.c_uint32),
+        ("n_tensors", C.c_uint64), ("n_kv", C.c_uint64),
+        ("kv", C.POINTER(GGUFKV)),
+        ("tensors", C.POINTER(GGUFTensor)),
+        ("data", c_vp),
+        ("alignment", C.c_uint64),
+    ]
+
+
+class GGUFMoE(C.Structure):
+    """vireo_gguf_moe (include/vireo_hip.h)."""
+    _fields_ = [
+        ("gguf", C.POINTER(GGUFCtx)),
+        ("arch", C.c_char * 64),
+        ("model", MoEModel),
+        ("stack", MoEStack),
+        ("vocab", C.c_int),
+        ("eps", C.c_float),
+        ("priv", c_vp),
     ]
 
 
@@ -114,6 +158,16 @@ SIGNATURES = {
                                          C.c_float, c_vp]),
     "vireo_synth_hidden": (C.c_int, [c_vp, c_vp, C.c_int, C.c_int64, C.c_uint64, C.c_uint64, C.c_float]),
     "vireo_row_bytes": (C.c_int64, [C.c_uint32, C.c_int]),
+    "vireo_gguf_open": (C.POINTER(GGUFCtx), [C.c_char_p]),
+    "vireo_gguf_close": (None, [C.POINTER(GGUFCtx)]),
+    "vireo_gguf_find": (C.POINTER(GGUFKV), [C.POINTER(GGUFCtx), C.c_char_p]),
+    "vireo_gguf_get_u64": (C.c_int, [C.POINTER(GGUFCtx), C.c_char_p, C.POINTER(C.c_uint64)]),
+    "vireo_gguf_get_f32": (C.c_int, [C.POINTER(GGUFCtx), C.c_char_p, C.POINTER(C.c_float)]),
+    "vireo_gguf_get_str": (c_vp, [C.POINTER(GGUFCtx), C.c_char_p, C.POINTER(C.c_uint64)]),
+    "vireo_gguf_tensor_by_name": (C.POINTER(GGUFTensor), [C.POINTER(GGUFCtx), C.c_char_p]),
+    "vireo_gguf_moe_load": (C.c_int, [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.POINTER(GGUFMoE))]),
+    "vireo_gguf_moe_error": (C.c_char_p, []),
+    "vireo_gguf_moe_free": (None, [C.POINTER(GGUFMoE)]),
 }
 
 _lib = None

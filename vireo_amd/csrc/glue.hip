@@ -136,7 +136,8 @@ extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *
     const vireo_moe_model *m = st->moe;
     const int d = m->dim;
     void *s = stream;
-    int rc = vireo_embed(st->lm_head->ggml_type, st->lm_head->data, d, st->vocab, token, 1, x, s);
+    const gguf_tensor *emb = st->tok_embd ? st->tok_embd : st->lm_head;
+    int rc = vireo_embed(emb->ggml_type, emb->data, d, st->vocab, token, 1, x, s);
     for (int l = 0; l < m->n_layers && !rc; l++)
         rc = vh_moe_layer_normed(m, l, x, st->ffn_norm ? st->ffn_norm[l] : nullptr, st->eps, xb,
                                  static_cast<hipStream_t>(s));

@@ -1,0 +1,196 @@
+"""GGUF files for the MoE path.
+
+* GGUFWriter: writes GGUF v3 files (metadata of every scalar type, strings,
+  arrays, tensors at the file's alignment).
+* write_moe_gguf: a synthetic MoE model file with the tensor names and
+  metadata keys of a real MoE GGUF (src/gguf_run.c:276-318): per layer
+  blk.<l>.ffn_gate_inp (F32 router), ffn_gate_exps / ffn_up_exps /
+  ffn_down_exps (stacked experts, expert-major) and ffn_norm, plus
+  token_embd, output_norm and optionally an untied output head; weights are
+  the deterministic synthetic weights of vireo_amd.workloads.
+* GGUFModel: the device model that vireo_gguf_moe_load builds from a file
+  (routers, norms and head in HBM, experts paged by the ExpertStore).
+"""
+import ctypes as C
+import struct
+
+import numpy as np
+
+from . import _lib
+from . import workloads as W
+
+# metadata value types (src/gguf.h:16-18)
+U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
+_FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?", U64: "<Q",
+        I64: "<q", F64: "<d"}
+
+
+def _str(s):
+    b = s.encode() if isinstance(s, str) else bytes(s)
+    return struct.pack("<Q", len(b)) + b
+
+
+def _value(vtype, value, arr_type=None):
+    """Encoded value; for an ARRAY, arr_type is the item type, or a tuple
+    (ARRAY, item type of the inner arrays) for an array of arrays."""
+    if vtype == STRING:
+        return _str(value)
+    if vtype == ARRAY:
+        item, inner = arr_type if isinstance(arr_type, tuple) else (arr_type, None)
+        out = struct.pack("<IQ", item, len(value))
+        return out + b"".join(_value(item, v, inner) for v in value)
+    return struct.pack(_FMT[vtype], value)
+
+
+class GGUFWriter:
+    """Collects metadata and tensors, then writes one GGUF v3 file."""
+
+    def __init__(self, alignment=32):
+        self.alignment = alignment
+        self.kv = []
+        self.tensors = []
+        if alignment != 32:
+            self.add("general.alignment", U32, alignment)
+
+    def add(self, key, vtype, value, arr_type=None):
+        self.kv.append((key, vtype, value, arr_type))
+
+    def add_tensor(self, name, dims, ggml_type, data):
+        """dims in GGUF order: dims[0] is the row length."""
+        self.tensors.append((name, list(dims), ggml_type, np.ascontiguousarray(data).view(np.uint8).reshape(-1)))
+
+    def write(self, path):
+        a = self.alignment
+        head = [b"GGUF", struct.pack("<IQQ", 3, len(self.tensors), len(self.kv))]
+        for key, vtype, value, arr_type in self.kv:
+            head.append(_str(key) + struct.pack("<I", vtype) + _value(vtype, value, arr_type))
+        offsets, off = [], 0
+        for _, _, _, data in self.tensors:
+            offsets.append(off)
+            off += (len(data) + a - 1) // a * a
+        for (name, dims, typ, _), o in zip(self.tensors, offsets):
+            head.append(_str(name) + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims) +
+                        struct.pack("<IQ", typ, o))
+        blob = b"".join(head)
+        with open(path, "wb") as f:
+            f.write(blob)
+            f.write(b"\0" * ((a - len(blob) % a) % a))
+            for (_, _, _, data), o in zip(self.tensors, offsets):
+                f.write(data.tobytes())
+                f.write(b"\0" * ((a - len(data) % a) % a))
+
+
+def moe_arch(shape):
+    """Architecture name whose loader rule gives the shape's renormalisation
+    (src/gguf_run.c:292: every architecture but "olmoe" renormalises)."""
+    return "qwen3moe" if shape.renorm else "olmoe"
+
+
+def write_moe_gguf(path, shape, n_layers, seed, vocab=0, untied=False, norms=True, alignment=32, arch=None,
+                   lm_type=W.Q8_0):
+    """Write a synthetic MoE GGUF file; returns the host arrays written, for
+    checking (routers [L][E x d], experts [L] (gate_all, up_all, down_all),
+    ffn_norm [L][d] or None, and with vocab: out_norm, token_embd, output)."""
+    d, E, fe = shape.d, shape.E, shape.fe
+    arch = arch or moe_arch(shape)
+    w = GGUFWriter(alignment)
+    w.add("general.architecture", STRING, arch)
+    w.add("general.name", STRING, f"synthetic {shape.name}")
+    w.add(f"{arch}.block_count", U32, n_layers)
+    w.add(f"{arch}.embedding_length", U32, d)
+    w.add(f"{arch}.feed_forward_length", U32, 4 * d)
+    w.add(f"{arch}.expert_feed_forward_length", U32, fe)
+    w.add(f"{arch}.expert_count", U32, E)
+    w.add(f"{arch}.expert_used_count", U32, shape.k)
+    w.add(f"{arch}.attention.layer_norm_rms_epsilon", F32, W.EPS)
+    if vocab:
+        w.add("tokenizer.ggml.tokens", ARRAY, [f"<t{i}>" for i in range(vocab)], STRING)
+        w.add("tokenizer.ggml.scores", ARRAY, [float(-i) for i in range(vocab)], F32)
+    out = {"routers": [], "experts": [], "ffn_norm": [] if norms else None}
+    for l in range(n_layers):
+        r = W.host_router(shape, l, seed)
+        g, u, dn = W.host_layer(shape, l, seed)
+        w.add_tensor(f"blk.{l}.ffn_gate_inp.weight", [d, E], W.F32, r)
+        w.add_tensor(f"blk.{l}.ffn_gate_exps.weight", [d, fe, E], shape.gate_type, g)
+        w.add_tensor(f"blk.{l}.ffn_up_exps.weight", [d, fe, E], shape.up_type, u)
+        w.add_tensor(f"blk.{l}.ffn_down_exps.weight", [fe, d, E], shape.down_type, dn)
+        out["routers"].append(r)
+        out["experts"].append((g, u, dn))
+        if norms:
+            nw = (1.0 + 0.25 * W.host_normal(d, seed, W.stream_id(l, 15))).astype(np.float32)
+            w.add_tensor(f"blk.{l}.ffn_norm.weight", [d], W.F32, nw)
+            out["ffn_norm"].append(nw)
+    if vocab:
+        emb = W.host_matrix(lm_type, d, 0, vocab, seed, W.stream_id(0, W.KIND_LM_HEAD))
+        on = (1.0 + 0.25 * W.host_normal(d, seed, W.stream_id(n_layers, 15))).astype(np.float32)
+        w.add_tensor("token_embd.weight", [d, vocab], lm_type, emb)
+        w.add_tensor("output_norm.weight", [d], W.F32, on)
+        out["token_embd"], out["out_norm"], out["output"] = emb, on, emb
+        if untied:
+            head = W.host_matrix(lm_type, d, 0, vocab, seed + 1, W.stream_id(0, W.KIND_LM_HEAD))
+            w.add_tensor("output.weight", [d, vocab], lm_type, head)
+            out["output"] = head
+    w.write(path)
+    return out
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class GGUFModel:
+    """vireo_gguf_moe_load: an MoE GGUF file on the device."""
+
+    def __init__(self, path, expert_capacity=0, load_head=True):
+        self.lib = _lib.load()
+        p = C.POINTER(_lib.GGUFMoE)()
+        rc = self.lib.vireo_gguf_moe_load(str(path).encode(), expert_capacity, int(load_head), C.byref(p))
+        if rc:
+            why = self.lib.vireo_gguf_moe_error()
+            raise _lib.VireoError(f"vireo_gguf_moe_load({path}) failed: {rc} ({why.decode() if why else '?'})")
+        self.p = p
+        m = p.contents
+        self.arch = m.arch.decode()
+        self.vocab, self.eps = m.vocab, m.eps
+        md = m.model
+        self.d, self.E, self.k, self.fe = md.dim, md.n_experts, md.n_used, md.ffn_exp
+        self.renorm, self.n_layers = bool(md.topk_renorm), md.n_layers
+
+    def forward(self, layer, x, hb, stream=None, return_routing=False):
+        """x[t] += moe(hb[t]) in place (moe_ffn_forward)."""
+        import torch
+        T = hb.shape[0]
+        idx = w = None
+        if return_routing:
+            idx = torch.empty((T, self.k), dtype=torch.int32, device=hb.device)
+            w = torch.empty((T, self.k), dtype=torch.float32, device=hb.device)
+        _lib.check(self.lib.moe_ffn_forward(C.byref(self.p.contents.model), layer, _ptr(x), _ptr(hb), T, _ptr(idx),
+                                            _ptr(w), _stream(stream)), "moe_ffn_forward")
+        return (idx, w) if return_routing else None
+
+    def step(self, token, x, xb, logits, stream=None):
+        """moe_stack_step on the file's norms and head."""
+        _lib.check(self.lib.moe_stack_step(C.byref(self.p.contents.stack), _ptr(token), _ptr(x), _ptr(xb),
+                                           _ptr(logits), _stream(stream)), "moe_stack_step")
+
+    def stats(self):
+        st = _lib.ExpertStats()
+        self.lib.expert_store_stats(self.p.contents.model.es, C.byref(st))
+        return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
+
+    def close(self):
+        if getattr(self, "p", None):
+            self.lib.vireo_gguf_moe_free(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
