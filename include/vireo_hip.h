@@ -131,8 +131,13 @@ int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts,
  * [n_tokens x dim]; idx_out / w_out (optional) receive the routing.
  * Expert slices come from m->es; on the first call for a layer every expert
  * of that layer is looked up once and its lease held (the resident set is
- * the whole layer), as there is no host round trip per token. An expert that
- * is not registered contributes nothing, as in the reference. */
+ * the whole layer), as there is no host round trip per token. When the
+ * store's capacity is below one layer's experts, every call instead copies
+ * the per-expert token counts to the host and looks the routed experts up in
+ * batches that fit (misses paged in from the store's file, least recently
+ * used unleased experts evicted), releasing each batch after its kernels; such
+ * a call synchronizes the stream and cannot be captured in a graph. An expert
+ * that is not registered contributes nothing, as in the reference. */
 int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
                     int32_t *idx_out, float *w_out, void *stream);
 
@@ -253,7 +258,9 @@ ExpertStore *expert_store_create_device(const void *dev_base, uint64_t size, uin
                                         int n_layers, int n_experts);
 /* Look up every registered expert of `layer` once and hold the leases, and
  * return a device table [n_experts x 3] of {gate, up, down} pointers (NULL for
- * unregistered experts). Later calls return the same table. */
+ * unregistered experts). Later calls return the same table. -ENOSPC (nothing
+ * evicted) when the layer's experts exceed the capacity, or when the leased
+ * experts of other layers leave no room for them. */
 int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_table);
 /* Release the leases taken by expert_store_pin_layer for `layer`. */
 int expert_store_unpin_layer(ExpertStore *s, int layer);

@@ -14,6 +14,11 @@ the oracle on the arrays that were written into the file.
 * Stack: moe_stack_step on the file's ffn norms, output norm, LM head and
   token embedding (untied and tied) against the oracle's decode skeleton
   (src/gguf_run.c:216-254 with attention omitted), as in test_gpu_stack.
+* A store smaller than a layer (the reference's laptop case): every call
+  pages its routed experts in batches that fit; outputs match the oracle, and
+  equal the fully resident model's bit for bit where both run the grouped
+  kernels (more than one token); the pool never exceeds its capacity, every
+  call looks up each routed expert once, and the stack decodes through it.
 """
 import numpy as np
 import pytest
@@ -81,14 +86,16 @@ def oracle_stack(oracle, shape, arr, L, vocab):
     return step
 
 
-@pytest.mark.parametrize("name,untied", [("tiny-k", True), ("tiny-k", False), ("qwen3-16e", True)])
-def test_gguf_stack_matches_oracle(cuda, oracle, tmp_path, name, untied):
+@pytest.mark.parametrize("name,untied,cap_experts", [("tiny-k", True, 0), ("tiny-k", False, 0), ("qwen3-16e", True, 0),
+                                                     ("qwen3-16e", True, 5)])
+def test_gguf_stack_matches_oracle(cuda, oracle, tmp_path, name, untied, cap_experts):
     """qwen3-16e runs the one-token decode plan, whose router launch applies
-    the file's RMSNorm weights itself; tiny-k the grouped plan."""
+    the file's RMSNorm weights itself, or, with a store of 5 experts, the
+    paged plan; tiny-k the grouped plan."""
     shape, L, vocab = SHAPES[name], 3, 700
     path = tmp_path / "stack.gguf"
     arr = G.write_moe_gguf(str(path), shape, L, seed=37, vocab=vocab, untied=untied)
-    m = G.GGUFModel(path)
+    m = G.GGUFModel(path, expert_capacity=cap_experts * shape.expert_bytes())
     assert m.vocab == vocab
     ref = oracle_stack(oracle, shape, arr, L, vocab)
     x = torch.empty(shape.d, dtype=torch.float32, device=cuda)
@@ -108,3 +115,34 @@ def test_gguf_stack_matches_oracle(cuda, oracle, tmp_path, name, untied):
         if top2[1] - top2[0] > TOL * np.abs(lo).max():
             assert tg == to
     m.close()
+
+
+@pytest.mark.parametrize("name,cap_experts,T", [("tiny-k", 3, 5), ("tiny-q8", 1, 3), ("qwen3-16e", 4, 1),
+                                               ("qwen3-16e", 5, 6)])
+def test_gguf_paged_store(cuda, oracle, tmp_path, name, cap_experts, T):
+    shape, L = SHAPES[name], 2
+    path = tmp_path / f"{name}.gguf"
+    arr = G.write_moe_gguf(str(path), shape, L, seed=41)
+    cap = cap_experts * shape.expert_bytes()
+    paged = G.GGUFModel(path, expert_capacity=cap, load_head=False)
+    full = G.GGUFModel(path, load_head=False)
+    lookups = 0
+    for call in range(6):
+        layer = call % L
+        Gl, Ul, Dl = expert_lists(shape, *arr["experts"][layer])
+        x, hb = W.host_hidden(shape.d, T, seed=100 + call)
+        xp, hp = torch.from_numpy(x).to(cuda), torch.from_numpy(hb).to(cuda)
+        xf = xp.clone()
+        idx, _ = paged.forward(layer, xp, hp, return_routing=True)
+        full.forward(layer, xf, hp)
+        xo, io, _, _ = oracle.moe_ffn(shape, arr["routers"][layer], Gl, Ul, Dl, x, hb)
+        check(f"{name} paged call {call} layer {layer}", x, xp.cpu().numpy(), xo, idx.cpu().numpy(), io)
+        if T > 1:  # both on the grouped kernels: the same rows, the same combine
+            assert torch.equal(xp, xf)
+        lookups += len(np.unique(io))
+        st = paged.stats()
+        assert st["resident_bytes"] <= cap
+        assert st["requests"] == lookups and st["hits"] + st["misses"] == lookups
+    print(f"{name}: {paged.stats()}")
+    paged.close()
+    full.close()

@@ -248,11 +248,14 @@ int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_ta
     if (!s || !dev_table || layer < 0 || layer >= s->n_layers) return -EINVAL;
     if (s->tables[layer]) { *dev_table = (const void *const *)s->tables[layer]; return 0; }
     const int E = s->n_experts;
-    uint64_t need = 0;
+    uint64_t need = 0, all = 0;
     for (int e = 0; e < E; e++) {
         Slot *sl = slot_at(s, layer, e);
         if (sl->registered && !sl->resident) need += sl->bytes;
+        if (sl->registered) all += sl->bytes;
     }
+    /* a layer larger than the store never fits: say so before evicting anything */
+    if (s->capacity_bytes && all > s->capacity_bytes) return -ENOSPC;
     if (s->capacity_bytes && s->resident_bytes + need > s->capacity_bytes) {
         /* evict what can go; the layer must then fit entirely */
         make_room(s, need);
@@ -315,3 +318,13 @@ void expert_store_destroy(ExpertStore *s) {
     free(s->slots);
     free(s);
 }
+
+/* Bytes an expert takes in the pool (0 if unregistered), and the pool's
+ * capacity (0 = unbounded), for callers that page experts in batches. */
+uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert) {
+    const Slot *sl = (s && layer >= 0 && layer < s->n_layers && expert >= 0 && expert < s->n_experts)
+                         ? &s->slots[(size_t)layer * (size_t)s->n_experts + (size_t)expert]
+                         : NULL;
+    return sl && sl->registered ? sl->bytes : 0;
+}
+uint64_t vh_store_capacity(const ExpertStore *s) { return s ? s->capacity_bytes : 0; }

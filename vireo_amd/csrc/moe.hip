@@ -57,6 +57,8 @@ struct Ws {
     int32_t *tiles, *small;  // matrix-core plan: token tiles, the other groups
     void *hs;                // matrix-core plan: bf16 h rows in dispatch order
     void *xb;                // matrix-core plan: bf16 copy of hb
+    const void **tab;        // paged plan: [3 E] expert table of the current batch
+    int32_t *act;            // paged plan: [E + 1] active list of the current batch
 };
 
 int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false) {
@@ -75,6 +77,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
+    const size_t o_tab = take(size_t(3) * E * sizeof(void *)), o_act = take(size_t(E + 1) * 4);
     void *base;
     if (int rc = vh_device_workspace(off, &base)) return rc;
     char *b = static_cast<char *>(base);
@@ -94,6 +97,8 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->small = mfma ? reinterpret_cast<int32_t *>(b + o_small) : nullptr;
     ws->hs = mfma ? b + o_hs : nullptr;
     ws->xb = mfma ? b + o_xb : nullptr;
+    ws->tab = reinterpret_cast<const void **>(b + o_tab);
+    ws->act = reinterpret_cast<int32_t *>(b + o_act);
     return 0;
 }
 
@@ -170,7 +175,11 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
     }
     const vireo_moe_layer &L = m->layers[layer];
     const void *const *table = nullptr;
-    if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
+    if (int rc = expert_store_pin_layer(m->es, layer, &table)) {
+        if (rc != -ENOSPC) return rc;
+        if ((rc = vireo_rmsnorm(xb, x, nw, m->dim, 1, eps, s))) return rc;
+        return moe_ffn_forward(m, layer, x, xb, 1, nullptr, nullptr, s);  // pages the routed experts
+    }
     Ws ws;
     if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, true, false, &ws)) return rc;
     const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
@@ -298,6 +307,95 @@ extern "C" int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_exper
     return vh_finish(s, vh_dispatch(idx, int(P), n_experts, counts, offs, perm, nullptr, s));
 }
 
+// moe_ffn_forward when the ExpertStore cannot hold the layer. The reference
+// looks each routed expert up in turn and releases it after use
+// (src/gguf_run.c:193-213), so a store of any size serves it; here the
+// routing and the dispatch run on the device, the per-expert counts come back
+// to the host, and the routed experts are taken in batches that fit the
+// store's capacity: look the batch up (the store pages misses in from its file
+// and evicts the least recently used unleased experts), run the grouped
+// projections on that batch alone, wait for them, release the leases. The
+// combine runs once all batches have written their rows. The stream is
+// synchronized (the host needs the routing), so such a call cannot be
+// captured in a graph.
+int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
+                  float *w_out, hipStream_t s) {
+    const vireo_moe_layer &L = m->layers[layer];
+    const uint32_t tg = L.gate_exps->ggml_type, td = L.down_exps->ggml_type;
+    const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
+    const int P = n_tokens * k, slots = P < E ? P : E;
+    Ws ws;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, true, &ws)) return rc;
+    int32_t *idx = idx_out ? idx_out : ws.idx;
+    float *w = w_out ? w_out : ws.w;
+    const float *R = static_cast<const float *>(L.router->data);
+    const bool exact = n_tokens >= kExactRouteTokens;
+    int rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
+    if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
+                                  ws.flags, nullptr, s);
+    if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    int32_t counts[kMaxExperts];
+    if (!rc) rc = vh_check(hipStreamSynchronize(s));
+    if (!rc) rc = vh_check(hipMemcpy(counts, ws.counts, size_t(E) * 4, hipMemcpyDeviceToHost));
+    if (rc) return rc;
+    const uint64_t cap = vh_store_capacity(m->es);
+    const bool gdec = n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
+    const void *tab[3 * kMaxExperts], *present[3 * kMaxExperts];
+    ExpertView views[kMaxExperts];
+    int32_t act[kMaxExperts + 1];
+    memset(present, 0, sizeof(void *) * 3 * size_t(E));
+    int e0 = 0;
+    while (!rc) {
+        while (e0 < E && counts[e0] == 0) e0++;
+        if (e0 == E) break;
+        // the next batch: routed experts in id order while their bytes fit (at least one)
+        int n = 0;
+        uint64_t bytes = 0;
+        int e1 = e0;
+        for (; e1 < E; e1++) {
+            if (counts[e1] == 0) continue;
+            const uint64_t b = vh_store_expert_bytes(m->es, layer, e1);
+            if (n && cap && bytes + b > cap) break;
+            bytes += b;
+            act[n++] = e1;
+        }
+        memset(tab, 0, sizeof(void *) * 3 * size_t(E));
+        int got = 0;
+        for (int i = 0; i < n && !rc; i++) {
+            const int e = act[i];
+            const int lr = expert_store_lookup(m->es, layer, e, &views[e]);
+            if (lr == -1) continue;  // unregistered: skipped (src/gguf_run.c:201)
+            if (lr) { rc = lr; break; }
+            tab[3 * e] = views[e].gate;
+            tab[3 * e + 1] = views[e].up;
+            tab[3 * e + 2] = views[e].down;
+            present[3 * e + 2] = views[e].down;
+            act[got++] = e;
+        }
+        act[E] = got;
+        if (!rc && got) {
+            rc = vh_check(hipMemcpy(ws.tab, tab, sizeof(void *) * 3 * size_t(E), hipMemcpyHostToDevice));
+            if (!rc) rc = vh_check(hipMemcpy(ws.act, act, size_t(E + 1) * 4, hipMemcpyHostToDevice));
+            const void *const *dt = ws.tab;
+            if (gdec) {
+                if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, ws.h, s);
+                if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
+            } else {
+                if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, ws.h, s);
+                if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
+            }
+            const int sr = vh_check(hipStreamSynchronize(s));  // the batch's kernels are done with its experts
+            if (!rc) rc = sr;
+        }
+        for (int i = 0; i < got; i++) expert_store_release(m->es, &views[act[i]]);
+        e0 = e1;
+    }
+    // the combine reads only whether each expert was found
+    if (!rc) rc = vh_check(hipMemcpy(ws.tab, present, sizeof(void *) * 3 * size_t(E), hipMemcpyHostToDevice));
+    if (!rc) rc = vh_combine(idx, w, ws.tab, ws.ybuf, d, k, n_tokens, x, s);
+    return rc;
+}
+
 extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
                                int32_t *idx_out, float *w_out, void *stream) {
     if (int rc = check_model(m, layer)) return rc;
@@ -310,8 +408,12 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (tg != tu || !type_ok(tg, d) || !type_ok(td, fe) || fe % 4) return -EINVAL;
     if (int64_t(n_tokens) * k > 65535 || n_tokens > 65535) return -E2BIG;
     const void *const *table = nullptr;
-    if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = expert_store_pin_layer(m->es, layer, &table)) {
+        if (rc != -ENOSPC) return rc;
+        // the layer does not fit the store: page its routed experts per call
+        return vh_finish(s, paged_forward(m, layer, x, hb, n_tokens, idx_out, w_out, s));
+    }
     const float *R = static_cast<const float *>(L.router->data);
 
     const bool decode = n_tokens == 1 && g_path != 2 && g_path != 4 && decode_supported(m, layer) &&

@@ -16,6 +16,11 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
 // One MoE layer of a stack for one token: xb = rmsnorm(x, nw); x += moe(xb).
 // The one-token decode plan folds the RMSNorm into its router launch; other
 // shapes run vireo_rmsnorm and moe_ffn_forward.
+// Bytes of a registered expert in the store's pool (0 if unregistered) and
+// the pool's capacity (0 = unbounded) (expert_store.c).
+extern "C" uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert);
+extern "C" uint64_t vh_store_capacity(const ExpertStore *s);
+
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
                         hipStream_t s);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
