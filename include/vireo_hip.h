@@ -147,8 +147,8 @@ int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *
  * one-token decode plan with its experts fused into one kernel where that
  * kernel is built for the shapes (see moe_decode_stage), 4 = always the
  * grouped plan, with every group on the fp32 kernels.
- * Under plans 0 and 2, calls of at least 64 tokens run the groups of at least
- * 16 tokens as bf16 matrix-core GEMMs (inputs and dequantized weights rounded
+ * Under plans 0 and 2, calls of at least 64 tokens run every group as bf16
+ * matrix-core GEMMs (inputs and dequantized weights rounded
  * to bf16, fp32 accumulation; the layer's contribution then agrees with the
  * reference to about 1e-2 of its largest magnitude instead of 2e-3); the
  * routing is unaffected. */

@@ -17,7 +17,7 @@ from vireo_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
-TOL_BF16 = 1e-2  # groups of >= 16 tokens in calls of >= 64 tokens: bf16 GEMMs
+TOL_BF16 = 1e-2  # calls of >= 64 tokens: every group as bf16 GEMMs
 
 
 @pytest.fixture
@@ -64,7 +64,9 @@ def test_moe_ffn_matches_oracle(cuda, oracle, path, name, T, plan):
     xt = torch.from_numpy(x).to(cuda)
     idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
     xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
-    check(f"{name} T={T} plan={plan}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    # calls of >= 64 tokens run every group as bf16 matrix-core GEMMs under plans 0 and 2
+    tol = TOL_BF16 if T >= 64 and plan in (0, 2) else TOL
+    check(f"{name} T={T} plan={plan}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io, tol=tol)
     np.testing.assert_allclose(w.cpu().numpy(), wo, rtol=1e-5)
     m.close()
 
@@ -188,10 +190,11 @@ MFMA_CASES = [("qwen3-30b-a3b-q8_0", 512, True), ("olmoe-q4_k_m", 128, False), (
 @pytest.mark.parametrize("name,T,zipf", MFMA_CASES)
 @pytest.mark.parametrize("plan", [0, 4])
 def test_grouped_plan_large_groups(cuda, oracle, path, name, T, zipf, plan):
-    """Calls with groups of >= 16 tokens: under plan 0 those groups run as
-    bf16 matrix-core GEMMs and the rest on the fp32 kernels; plan 4 runs all
-    of them on the fp32 kernels. Every token's experts bit-exact; a sample of
-    tokens against the oracle; the same call twice gives the same bits."""
+    """Calls of >= 64 tokens with groups of every size (1-15 tokens, and 16 to
+    over 128): under plan 0 every group runs as bf16 matrix-core GEMMs, one
+    tile or several, ragged or not; plan 4 runs all of them on the fp32
+    kernels. Every token's experts bit-exact; a sample of tokens against the
+    oracle; the same call twice gives the same bits."""
     path(plan)
     shape = W.SHAPES[name]
     bias = W.zipf_bias(shape.E, 1.1, seed=8) if zipf else None

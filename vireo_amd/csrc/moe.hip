@@ -8,11 +8,11 @@
 //   grouped (any count): router -> top-k -> dispatch -> grouped gate/up ->
 //                        grouped down -> combine + residual      (6 kernels)
 // The grouped plan reads each routed expert's weights once per call however
-// many tokens chose it. In calls of at least kMfmaMinCall tokens, groups of at
-// least kMfmaMinTokens tokens run as bf16 matrix-core GEMMs (moe_mfma.hip;
-// 4 more kernels) and only the smaller groups on the fp32 grouped kernels.
-// Calls of fewer tokens run their groups on moe_gdec.hip's kernels, which keep
-// a group's inputs in registers and stream each weight row once.
+// many tokens chose it. In calls of at least kMfmaMinCall tokens every group
+// runs as bf16 matrix-core GEMMs (moe_mfma.hip; 4 more kernels); calls of
+// fewer tokens run their groups on moe_gdec.hip's kernels, which keep a
+// group's inputs in registers and stream each weight row once, and plan 4
+// runs every call on the fp32 grouped kernels (moe_grouped.hip).
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -438,25 +438,19 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
-    // groups of at least kMfmaMinTokens tokens on the matrix cores, the rest
-    // (listed in ws.small) on the fp32 kernels
-    const int32_t *act = ws.active;
-    if (mfma) {
+    if (mfma) {  // every group on the matrix cores (its small list stays empty)
         const int mt = vh_mfma_max_tiles(P, E);
-        if (!rc) rc = vh_mfma_plan(ws.counts, E, kMfmaMinTokens, ws.tiles, ws.small, s);
+        if (!rc) rc = vh_mfma_plan(ws.counts, E, 1, ws.tiles, ws.small, s);
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
-        act = ws.small;
-    }
-    // calls of a decode batch's size (a few tokens per group) on the kernels
-    // that hold a group's inputs in registers; larger groups on the tiled ones
-    if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
-        if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
-        if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+    } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
+        // calls of a decode batch's size (a few tokens per group): inputs in registers
+        if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
+        if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     } else {
-        if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, act, table, hb, d, fe, k, E, slots, ws.h, s);
-        if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, act, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+        if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
+        if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     }
     if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
     return vh_finish(s, rc);

@@ -1,14 +1,15 @@
-// bf16 matrix-core (MFMA) grouped GEMMs for the grouped plan's large groups.
+// bf16 matrix-core (MFMA) grouped GEMMs for the groups of large calls.
 //
 // moe_ffn (src/gguf_run.c:193-213) runs every (token, expert) pair as two
 // matvecs; when a call carries many tokens, an expert's tokens form a group
 // and its projections become GEMMs: H_e = silu(X_e G_e^T) * (X_e U_e^T) and
 // Y_e = H_e D_e^T, with X_e the group's rows of hb gathered through the
-// dispatch permutation. Groups of at least kMfmaMinTokens tokens run here on
-// v_mfma_f32_32x32x16_bf16: the inputs are rounded to bf16, the weights are
+// dispatch permutation. Every group of a call of at least kMfmaMinCall
+// tokens runs here on v_mfma_f32_32x32x16_bf16 (a group smaller than a token
+// tile leaves the tile's other rows unused; the tile's cost is staging its
+// weights either way): the inputs are rounded to bf16, the weights are
 // dequantized exactly (src/gguf_compute.c:52-120) and then rounded to bf16
-// while they are staged, and products are accumulated in fp32. Smaller groups
-// stay on the fp32 kernels of moe_grouped.hip.
+// while they are staged, and products are accumulated in fp32.
 //
 // Tiles: a workgroup (512 threads) owns kBM = 128 rows of one group (a token
 // tile) and kBRows = 256 weight rows (gate/up: 128 rows of gate and the same

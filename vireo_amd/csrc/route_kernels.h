@@ -70,13 +70,16 @@ int vh_gdec_down(uint32_t type, const int32_t *counts, const int32_t *offs, cons
                  const int32_t *active, const void *const *table, const float *h, int d, int fe, int E, int max_slots,
                  float *ybuf, hipStream_t s);
 
-// Matrix-core grouped GEMMs (moe_mfma.hip) for groups of at least
-// kMfmaMinTokens tokens, in calls of at least kMfmaMinCall tokens (below that
-// no group is expected to reach the size). vh_mfma_plan lists their token
-// tiles in tiles[0 .. 1 + 2 * vh_mfma_max_tiles) and the other non-empty groups
-// in small[E + 1] (the `active` format); gate/up writes bf16 h rows in dispatch
-// order into hs [P x fe]; down writes ybuf rows like vh_grouped_down.
-constexpr int kMfmaMinTokens = 16;
+// Matrix-core grouped GEMMs (moe_mfma.hip) for the groups of calls of at
+// least kMfmaMinCall tokens. vh_mfma_plan lists the token tiles of groups of
+// at least min_tokens tokens in tiles[0 .. 1 + 2 * vh_mfma_max_tiles) and the
+// other non-empty groups in small[E + 1] (the `active` format); gate/up writes
+// bf16 h rows in dispatch order into hs [P x fe]; down writes ybuf rows like
+// vh_grouped_down. The forward pass sends every group of such a call to the
+// matrix cores (min_tokens 1): a tile's cost is its weight staging, so even a
+// one-token group is cheaper there than on the fp32 kernels (a 2048-token
+// Qwen3 Q8_0 prefill: 646 us per layer with every group on the matrix cores,
+// 666 / 678 / 727 us with groups below 4 / 8 / 16 tokens on the fp32 kernels).
 constexpr int kMfmaMinCall = 64;
 bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E);
 int vh_mfma_max_tiles(int P, int E);
