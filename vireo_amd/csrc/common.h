@@ -73,6 +73,7 @@ VH_DEV uint4 ld_u128(gbyte *p) {
     const u32x4 v = ldg<u32x4>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// bytes [b, b + 4) of the 8-byte value hi:lo, b in 0..3 (v_alignbyte takes b mod 4)
 VH_DEV uint32_t align2(uint32_t hi, uint32_t lo, uint32_t bytes) { return __builtin_amdgcn_alignbyte(hi, lo, bytes); }
 
 // ---- binary16 -> binary32 (exact; v_cvt_f32_f16) --------------------------------
