@@ -280,3 +280,86 @@ class RefMoE:
             self.close()
         except Exception:
             pass
+
+
+class _KVConfig(C.Structure):  # src/kvstore.h:26-33
+    _fields_ = [("n_layers", C.c_int), ("kv_dim", C.c_int), ("block_tokens", C.c_int), ("sink_tokens", C.c_int),
+                ("window_tokens", C.c_int), ("capacity_bytes", C.c_uint64)]
+
+
+class _KVStats(C.Structure):  # src/kvstore.h:35-44
+    _fields_ = [(n, C.c_uint64) for n in ("requests", "hits", "misses", "prefetched", "bytes_read", "bytes_spilled",
+                                          "resident_bytes", "capacity_bytes")]
+
+
+_KV_APPEND = C.CFUNCTYPE(None, _vp, C.c_int, C.c_int, _vp, _vp)
+_KV_ATTEND = C.CFUNCTYPE(None, _vp, C.c_int, _vp, _vp)
+_KV_STATS = C.CFUNCTYPE(None, _vp, _vp)
+_KV_DESTROY = C.CFUNCTYPE(None, _vp)
+
+
+class _KVOps(C.Structure):  # src/kvstore.h:47-52
+    _fields_ = [("append", _KV_APPEND), ("attend", _KV_ATTEND), ("stats", _KV_STATS), ("destroy", _KV_DESTROY)]
+
+
+class _KVStore(C.Structure):  # src/kvstore.h:54-58
+    _fields_ = [("ops", C.POINTER(_KVOps)), ("cfg", _KVConfig), ("state", _vp)]
+
+
+class _SelectStrategy(C.Structure):  # src/select/select.h:38-44
+    _fields_ = [("name", C.c_char_p), ("select", _vp), ("budget", C.c_int)]
+
+
+class RefKV:
+    """The reference's own KV stores (src/kvstore_dense.c, src/kvstore_ooc.c
+    with src/select/*), compiled into oracle/_ref: strategy "all", "recent"
+    or "topk" (with budget) for the out-of-core store, None for the dense one.
+    append/attend take numpy float32 vectors."""
+
+    def __init__(self, ref, n_layers, kv_dim, block_tokens, sink_tokens=0, window_tokens=0, capacity_bytes=0,
+                 strategy=None, budget=0, workdir=None):
+        L = self.lib = ref.lib
+        L.kvstore_dense_create.restype = C.POINTER(_KVStore)
+        L.kvstore_dense_create.argtypes = [_KVConfig]
+        L.kvstore_ooc_create.restype = C.POINTER(_KVStore)
+        L.kvstore_ooc_create.argtypes = [_KVConfig, _vp, C.c_char_p]
+        L.vireo_select_topk.restype = _vp
+        L.vireo_select_topk.argtypes = [C.c_int]
+        cfg = _KVConfig(n_layers, kv_dim, block_tokens, sink_tokens, window_tokens, capacity_bytes)
+        if strategy is None:
+            self.s = L.kvstore_dense_create(cfg)
+        else:
+            if strategy == "topk":
+                st = L.vireo_select_topk(budget)
+            else:
+                st = C.addressof(_SelectStrategy.in_dll(L, {"all": "VIREO_SELECT_ALL",
+                                                            "recent": "VIREO_SELECT_RECENT"}[strategy]))
+            self.s = L.kvstore_ooc_create(cfg, st, (workdir or os.environ.get("TMPDIR", "/tmp")).encode())
+        self.ops = self.s.contents.ops.contents
+        self.kv_dim = kv_dim
+
+    def append(self, layer, pos, k, v):
+        k, v = _f32(k), _f32(v)
+        self.ops.append(C.cast(self.s, _vp), layer, pos, _ptr(k), _ptr(v))
+
+    def attend(self, layer, q):
+        q = _f32(q)
+        out = np.empty(self.kv_dim, np.float32)
+        self.ops.attend(C.cast(self.s, _vp), layer, _ptr(q), _ptr(out))
+        return out
+
+    def stats(self):
+        st = _KVStats()
+        self.ops.stats(C.cast(self.s, _vp), C.cast(C.pointer(st), _vp))
+        return {n: getattr(st, n) for n, _ in _KVStats._fields_}
+
+    def close(self):
+        if getattr(self, "s", None):
+            self.ops.destroy(C.cast(self.s, _vp))
+            self.s = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -121,6 +121,18 @@ class GGUFMoE(C.Structure):
     ]
 
 
+class KVConfig(C.Structure):
+    """KVConfig (src/kvstore.h:26-33)."""
+    _fields_ = [("n_layers", C.c_int), ("kv_dim", C.c_int), ("block_tokens", C.c_int), ("sink_tokens", C.c_int),
+                ("window_tokens", C.c_int), ("capacity_bytes", C.c_uint64)]
+
+
+class KVStats(C.Structure):
+    """KVStats (src/kvstore.h:35-44)."""
+    _fields_ = [(n, C.c_uint64) for n in ("requests", "hits", "misses", "prefetched", "bytes_read", "bytes_spilled",
+                                          "resident_bytes", "capacity_bytes")]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "vireo_hip_init": (C.c_int, [C.c_int]),
@@ -168,6 +180,14 @@ SIGNATURES = {
     "vireo_gguf_moe_load": (C.c_int, [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.POINTER(GGUFMoE))]),
     "vireo_gguf_moe_error": (C.c_char_p, []),
     "vireo_gguf_moe_free": (None, [C.POINTER(GGUFMoE)]),
+    "vireo_kv_create_dense": (c_vp, [KVConfig]),
+    "vireo_kv_create_paged": (c_vp, [KVConfig, C.c_int, C.c_int]),
+    "vireo_kv_append": (C.c_int, [c_vp, C.c_int, C.c_int, c_vp, c_vp, c_vp]),
+    "vireo_kv_append_n": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp]),
+    "vireo_kv_attend": (C.c_int, [c_vp, C.c_int, c_vp, c_vp, c_vp]),
+    "vireo_kv_attend_gqa": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp]),
+    "vireo_kv_stats": (None, [c_vp, C.POINTER(KVStats)]),
+    "vireo_kv_destroy": (None, [c_vp]),
 }
 
 _lib = None

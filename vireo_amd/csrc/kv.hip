@@ -1,0 +1,627 @@
+// KV cache on the GPU (API: include/vireo_kv.h): the reference's KVStore
+// (src/kvstore.h, src/kvstore_dense.c, src/kvstore_ooc.c, src/select/*) with
+// its blocks in HBM.
+//
+// Host side: per layer a list of blocks (device copy, host copy once
+// spilled, token count, lease, recency) and the pager of kvstore_ooc: blocks
+// start resident, the least recently used unpinned unleased block is spilled
+// (a device-to-host copy into pinned memory) when a new one would exceed the
+// capacity, and a query pages its selected blocks back (host to device),
+// counting requests, hits, misses and bytes as the reference does. Device
+// memory comes from slabs of kSlabBlocks blocks; a block is K (G x d) then V.
+//
+// Device side:
+//   kv_append_kernel   copies n (k, v) rows into their blocks and updates each
+//                      block's running mean key with the reference's fp32
+//                      operations (src/kvstore_ooc.c:139-141), so the TOPK
+//                      scores below are the reference's bits;
+//   kv_score_kernel    q . mean key per candidate block, the reference's
+//                      in-order fp32 sum (kv_dot, src/kvstore.h:75-79);
+//   kv_attend_kernel   grid (chunks, heads), 256 threads: wave w of chunk c
+//                      takes list entries c CB + w, c CB + w + 4, ... and runs
+//                      an online softmax over their tokens (lane = token for
+//                      the scores, lane = output dimension for the weighted
+//                      sum), then the four waves merge in order into the
+//                      chunk's partial (m, l, acc);
+//   kv_merge_kernel    per head, the chunks' partials in order: out = acc / l.
+// The work split depends only on the selected token sequence, so a block
+// gives the same bits resident, spilled or paged back.
+#include <hip/hip_runtime.h>
+#include <errno.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <new>
+#include <vector>
+#include "common.h"
+#include "vireo_kv.h"
+
+namespace {
+
+constexpr int kSlabBlocks = 64;   // blocks per device allocation
+constexpr int kMaxAppend = 16;    // rows per vireo_kv_append_n launch
+constexpr int kChunkBlocks = 8;   // list entries per attention workgroup
+
+struct KvBlock {
+    float *dev = nullptr;   // K (G d) then V (G d), while resident
+    float *host = nullptr;  // pinned copy, made at the first spill
+    int ntok = 0;
+    int resident = 0;
+    int lease = 0;
+    uint64_t last_used = 0;
+};
+
+struct KvLayer {
+    std::vector<KvBlock> blocks;
+    float *ksum = nullptr;  // device [cap x d]: running mean key per block
+    int cap = 0;
+};
+
+struct KvDesc {
+    const float *blk;
+    int ntok;
+    int pad;
+};
+
+struct AppendArgs {
+    float *dst[kMaxAppend];  // the token's K row in its block (V at + G d)
+    float *ks[kMaxAppend];   // the block's mean key
+    float inv[kMaxAppend];   // 1 / (tokens in the block after this one)
+};
+
+// grid n, 64 * DPL threads... (any multiple of 64): row i of k and v into its block
+__global__ void __launch_bounds__(256) kv_append_kernel(AppendArgs a, const float *__restrict__ k,
+                                                        const float *__restrict__ v, int d, int gd) {
+    const int i = blockIdx.x;
+    const float *ki = k + size_t(i) * d, *vi = v + size_t(i) * d;
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+        const float kj = ki[j];
+        a.dst[i][j] = kj;
+        a.dst[i][gd + j] = vi[j];
+        // ks += (k - ks) * inv, three roundings as in the reference
+        const float ks = a.ks[i][j];
+        a.ks[i][j] = __fadd_rn(ks, __fmul_rn(__fsub_rn(kj, ks), a.inv[i]));
+    }
+}
+
+// scores[h * stride + c] = q_h . ksum[cand[h] + c] for c < ncand[h]
+__global__ void __launch_bounds__(256) kv_score_kernel(const float *const *__restrict__ ksum,
+                                                       const int *__restrict__ lo, const int *__restrict__ ncand,
+                                                       const float *__restrict__ q, int d, int stride,
+                                                       float *__restrict__ scores) {
+    const int h = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= ncand[h]) return;
+    const float *a = q + size_t(h) * d, *b = ksum[h] + size_t(lo[h] + c) * d;
+    float s = 0.0f;
+    for (int i = 0; i < d; i++) s = __fadd_rn(s, __fmul_rn(a[i], b[i]));
+    scores[size_t(h) * stride + c] = s;
+}
+
+// partial of chunk c of head h: part[(h * nchunk + c) * (2 + d)] = {m, l, acc[d]}
+template <int DPL>
+__global__ void __launch_bounds__(256) kv_attend_kernel(const KvDesc *__restrict__ desc, const int *__restrict__ off,
+                                                        const int *__restrict__ cnt, const float *__restrict__ q,
+                                                        int G, float scale, int nchunk, float *__restrict__ part) {
+    constexpr int D = 64 * DPL;
+    __shared__ float qs[D];
+    __shared__ float wm[4], wl[4], wacc[4][D];
+    const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = cnt[h], e0 = c * kChunkBlocks, e1 = min(n, e0 + kChunkBlocks);
+    float *pout = part + (size_t(h) * nchunk + c) * (2 + D);
+    if (e0 >= n) {  // an empty chunk (heads with fewer entries than others)
+        if (tid == 0) { pout[0] = -INFINITY; pout[1] = 0.0f; }
+        return;
+    }
+    for (int j = tid; j < D; j += 256) qs[j] = q[size_t(h) * D + j];
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; i++) acc[i] = 0.0f;
+    const KvDesc *dl = desc + off[h];
+    for (int e = e0 + wv; e < e1; e += 4) {
+        // the entry is the same for the whole wave
+        const int ntok = __builtin_amdgcn_readfirstlane(dl[e].ntok);
+        const uint64_t bp = reinterpret_cast<uint64_t>(dl[e].blk);
+        const float *K = reinterpret_cast<const float *>(
+            (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(bp >> 32)))) << 32) |
+            uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(bp)))));
+        const float *V = K + size_t(G) * D;
+        // scores: lane t < ntok takes token t
+        float s = -INFINITY;
+        if (lane < ntok) {
+            const float4 *kr = reinterpret_cast<const float4 *>(K + size_t(lane) * D);
+            const float4 *qv = reinterpret_cast<const float4 *>(qs);
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll 8
+            for (int j = 0; j < D / 4; j++) {
+                const float4 kk = kr[j], qq = qv[j];
+                a0 = fmaf(qq.x, kk.x, a0);
+                a1 = fmaf(qq.y, kk.y, a1);
+                a2 = fmaf(qq.z, kk.z, a2);
+                a3 = fmaf(qq.w, kk.w, a3);
+            }
+            s = ((a0 + a1) + (a2 + a3)) * scale;
+        }
+        const float bm = wave_max_f(s);
+        const float mn = fmaxf(m, bm);
+        const float cr = expf(m - mn);  // 0 while m is -inf
+        const float p = lane < ntok ? expf(s - mn) : 0.0f;
+        l = l * cr + wave_sum_f(p);
+#pragma unroll
+        for (int i = 0; i < DPL; i++) acc[i] *= cr;
+        for (int t = 0; t < ntok; t++) {
+            const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), t));
+            const float *vr = V + size_t(t) * D;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) acc[i] = fmaf(pt, vr[lane + 64 * i], acc[i]);
+        }
+        m = mn;
+    }
+    if (lane == 0) { wm[wv] = m; wl[wv] = l; }
+#pragma unroll
+    for (int i = 0; i < DPL; i++) wacc[wv][lane + 64 * i] = acc[i];
+    __syncthreads();
+    if (wv == 0) {  // the four waves' partials, in wave order
+        float M = -INFINITY;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w]);
+        float L = 0.0f, A[DPL];
+#pragma unroll
+        for (int i = 0; i < DPL; i++) A[i] = 0.0f;
+        for (int w = 0; w < 4; w++) {
+            if (wl[w] == 0.0f) continue;  // a wave without tokens
+            const float f = expf(wm[w] - M);
+            L += wl[w] * f;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) A[i] = fmaf(wacc[w][lane + 64 * i], f, A[i]);
+        }
+        if (lane == 0) { pout[0] = M; pout[1] = L; }
+#pragma unroll
+        for (int i = 0; i < DPL; i++) pout[2 + lane + 64 * i] = A[i];
+    }
+}
+
+// out[h] = (sum_c acc_c e^(m_c - M)) / (sum_c l_c e^(m_c - M)), chunks in order
+template <int DPL>
+__global__ void __launch_bounds__(64) kv_merge_kernel(const float *__restrict__ part, const int *__restrict__ cnt,
+                                                      int nchunk, float *__restrict__ out) {
+    constexpr int D = 64 * DPL;
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int nc = (cnt[h] + kChunkBlocks - 1) / kChunkBlocks;
+    const float *p = part + size_t(h) * nchunk * (2 + D);
+    float M = -INFINITY;
+    for (int c = 0; c < nc; c++) M = fmaxf(M, p[size_t(c) * (2 + D)]);
+    float L = 0.0f, A[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; i++) A[i] = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const float *pc = p + size_t(c) * (2 + D);
+        if (pc[1] == 0.0f) continue;
+        const float f = expf(pc[0] - M);
+        L += pc[1] * f;
+#pragma unroll
+        for (int i = 0; i < DPL; i++) A[i] = fmaf(pc[2 + lane + 64 * i], f, A[i]);
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int i = 0; i < DPL; i++) out[size_t(h) * D + lane + 64 * i] = A[i] * inv;
+}
+
+int blocks_for(int tokens, int g) { return tokens > 0 ? (tokens + g - 1) / g : 0; }
+
+int by_score_desc(const void *a, const void *b);
+
+}  // namespace
+
+struct VireoKV {
+    KVConfig cfg{};
+    bool dense = false;  // kvstore_dense semantics for the statistics
+    int strategy = VIREO_KV_SELECT_ALL, budget = 0;  // budget: the strategy's (0 = unbounded)
+    int sink_blocks = 0, window_blocks = 0, d = 0, G = 0;
+    uint64_t block_bytes = 0, resident_bytes = 0, tick = 0;
+    KVStats st{};
+    std::vector<KvLayer> layers;
+    std::vector<void *> slabs;
+    std::vector<float *> free_blocks;
+    // device scratch and its pinned staging
+    void *dscratch = nullptr;
+    size_t dscratch_bytes = 0;
+    void *hstage = nullptr;
+    size_t hstage_bytes = 0;
+    hipEvent_t staged = nullptr;  // the last upload from hstage has been read
+    float *part = nullptr;
+    size_t part_bytes = 0;
+    std::vector<float> hscores;
+};
+
+namespace {
+
+struct Scored {
+    int id;
+    float score;
+};
+// src/select/select_topk.c: descending score (the same comparator, for qsort)
+int by_score_desc(const void *a, const void *b) {
+    const float d = static_cast<const Scored *>(b)->score - static_cast<const Scored *>(a)->score;
+    return (d > 0) - (d < 0);
+}
+
+bool is_pinned(const VireoKV *S, const KvLayer &L, int i) {
+    const int nb = int(L.blocks.size());
+    return i < S->sink_blocks || i >= nb - S->window_blocks || i == nb - 1;
+}
+
+int take_block(VireoKV *S, float **out) {
+    if (S->free_blocks.empty()) {
+        void *p = nullptr;
+        if (hipMalloc(&p, S->block_bytes * kSlabBlocks) != hipSuccess) return -ENOMEM;
+        S->slabs.push_back(p);
+        for (int i = kSlabBlocks - 1; i >= 0; i--)
+            S->free_blocks.push_back(reinterpret_cast<float *>(static_cast<char *>(p) + size_t(i) * S->block_bytes));
+    }
+    *out = S->free_blocks.back();
+    S->free_blocks.pop_back();
+    return 0;
+}
+
+// src/kvstore_ooc.c:63-72 (a copy in pinned host memory instead of a file)
+int spill(VireoKV *S, KvBlock &b, hipStream_t s) {
+    if (!b.host && hipHostMalloc(reinterpret_cast<void **>(&b.host), S->block_bytes, 0) != hipSuccess) {
+        b.host = nullptr;
+        return -ENOMEM;
+    }
+    if (hipMemcpyAsync(b.host, b.dev, S->block_bytes, hipMemcpyDeviceToHost, s) != hipSuccess) return -EIO;
+    S->st.bytes_spilled += S->block_bytes;
+    S->free_blocks.push_back(b.dev);  // reused only by work enqueued after this copy
+    b.dev = nullptr;
+    b.resident = 0;
+    S->resident_bytes -= S->block_bytes;
+    return 0;
+}
+
+// src/kvstore_ooc.c:74-91
+int evict_until_room(VireoKV *S, hipStream_t s) {
+    if (!S->cfg.capacity_bytes) return 0;
+    while (S->resident_bytes + S->block_bytes > S->cfg.capacity_bytes) {
+        KvBlock *victim = nullptr;
+        uint64_t best = UINT64_MAX;
+        for (auto &L : S->layers)
+            for (int i = 0; i < int(L.blocks.size()); i++) {
+                KvBlock &b = L.blocks[i];
+                if (b.resident && !b.lease && !is_pinned(S, L, i) && b.last_used < best) {
+                    best = b.last_used;
+                    victim = &b;
+                }
+            }
+        if (!victim) break;  // nothing evictable now: stay over budget
+        if (int rc = spill(S, *victim, s)) return rc;
+    }
+    return 0;
+}
+
+// src/kvstore_ooc.c:93-110 (a lease is taken on the block)
+int ensure_resident(VireoKV *S, KvBlock &b, hipStream_t s) {
+    S->st.requests++;
+    if (b.resident) {
+        S->st.hits++;
+        b.last_used = ++S->tick;
+        b.lease++;
+        return 0;
+    }
+    S->st.misses++;
+    if (int rc = evict_until_room(S, s)) return rc;
+    if (int rc = take_block(S, &b.dev)) return rc;
+    if (hipMemcpyAsync(b.dev, b.host, S->block_bytes, hipMemcpyHostToDevice, s) != hipSuccess) return -EIO;
+    b.resident = 1;
+    S->resident_bytes += S->block_bytes;
+    S->st.bytes_read += S->block_bytes;
+    b.last_used = ++S->tick;
+    b.lease++;
+    return 0;
+}
+
+// src/kvstore_ooc.c:113-132
+int start_block(VireoKV *S, KvLayer &L, hipStream_t s) {
+    const int nb = int(L.blocks.size());
+    if (nb >= L.cap) {
+        const int cap = L.cap ? 2 * L.cap : 64;
+        float *ks = nullptr;
+        if (hipMalloc(&ks, size_t(cap) * S->d * sizeof(float)) != hipSuccess) return -ENOMEM;
+        if (L.ksum) {
+            if (hipMemcpyAsync(ks, L.ksum, size_t(nb) * S->d * sizeof(float), hipMemcpyDeviceToDevice, s) !=
+                    hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return -EIO;
+            (void)hipFree(L.ksum);
+        }
+        L.ksum = ks;
+        L.cap = cap;
+    }
+    KvBlock b;
+    if (int rc = take_block(S, &b.dev)) return rc;
+    b.resident = 1;
+    b.last_used = ++S->tick;
+    if (hipMemsetAsync(L.ksum + size_t(nb) * S->d, 0, size_t(S->d) * sizeof(float), s) != hipSuccess) return -EIO;
+    L.blocks.push_back(b);
+    S->resident_bytes += S->block_bytes;
+    return evict_until_room(S, s);
+}
+
+// device scratch of at least `bytes` (grown; the stream is idle when it grows)
+int scratch(VireoKV *S, size_t bytes, hipStream_t s, void **out) {
+    if (bytes > S->dscratch_bytes) {
+        if (hipStreamSynchronize(s) != hipSuccess) return -EIO;
+        if (S->dscratch) (void)hipFree(S->dscratch);
+        S->dscratch = nullptr;
+        const size_t nb = bytes < (size_t(1) << 16) ? (size_t(1) << 16) : 2 * bytes;
+        if (hipMalloc(&S->dscratch, nb) != hipSuccess) { S->dscratch_bytes = 0; return -ENOMEM; }
+        S->dscratch_bytes = nb;
+    }
+    *out = S->dscratch;
+    return 0;
+}
+
+// pinned staging of at least `bytes`, once the previous upload from it is done
+int staging(VireoKV *S, size_t bytes, void **out) {
+    if (S->staged && hipEventSynchronize(S->staged) != hipSuccess) return -EIO;
+    if (bytes > S->hstage_bytes) {
+        if (S->hstage) (void)hipHostFree(S->hstage);
+        S->hstage = nullptr;
+        const size_t nb = bytes < (size_t(1) << 16) ? (size_t(1) << 16) : 2 * bytes;
+        if (hipHostMalloc(&S->hstage, nb, 0) != hipSuccess) { S->hstage_bytes = 0; return -ENOMEM; }
+        S->hstage_bytes = nb;
+    }
+    *out = S->hstage;
+    return 0;
+}
+
+int append_n(VireoKV *S, int layer0, int n, const float *k, const float *v, hipStream_t s) {
+    AppendArgs a;
+    for (int i = 0; i < n; i++) {
+        KvLayer &L = S->layers[layer0 + i];
+        if (L.blocks.empty() || L.blocks.back().ntok == S->G)
+            if (int rc = start_block(S, L, s)) return rc;
+        const int bi = int(L.blocks.size()) - 1;
+        KvBlock &b = L.blocks[bi];
+        a.dst[i] = b.dev + size_t(b.ntok) * S->d;
+        a.ks[i] = L.ksum + size_t(bi) * S->d;
+        b.ntok++;
+        a.inv[i] = 1.0f / float(b.ntok);
+        b.last_used = ++S->tick;
+    }
+    hipLaunchKernelGGL(kv_append_kernel, dim3(n), dim3(S->d < 256 ? S->d : 256), 0, s, a, k, v, S->d, S->G * S->d);
+    return vh_check(hipGetLastError());
+}
+
+// The blocks head h attends to (src/kvstore_ooc.c:163-176), as ids into
+// seen[]; for TOPK the candidates' scores are in scores[0 .. ncand).
+void select_blocks(const VireoKV *S, int nb, const float *scores, std::vector<unsigned char> &seen) {
+    seen.assign(size_t(nb), 0);
+    int budget = S->budget > 0 ? S->budget : nb;
+    if (budget > nb) budget = nb;
+    if (S->strategy == VIREO_KV_SELECT_ALL) {
+        for (int i = 0; i < budget; i++) seen[i] = 1;
+    } else if (S->strategy == VIREO_KV_SELECT_TOPK) {
+        const int lo = S->sink_blocks, hi = nb - S->window_blocks;
+        if (nb > 0 && hi > lo) {  // src/select/select_topk.c:19-40
+            const int ncand = hi - lo;
+            std::vector<Scored> sc(static_cast<size_t>(ncand));
+            for (int i = 0; i < ncand; i++) sc[i] = Scored{lo + i, scores[i]};
+            qsort(sc.data(), size_t(ncand), sizeof(Scored), by_score_desc);
+            int take = S->budget < ncand ? S->budget : ncand;
+            if (take > budget) take = budget;
+            for (int i = 0; i < take; i++) seen[sc[i].id] = 1;
+        }
+    }
+    for (int i = 0; i < S->sink_blocks && i < nb; i++) seen[i] = 1;
+    for (int i = nb - S->window_blocks; i < nb; i++)
+        if (i >= 0) seen[i] = 1;
+}
+
+template <int DPL>
+void launch_attend(const KvDesc *desc, const int *off, const int *cnt, const float *q, int G, float scale,
+                   int nchunk, int heads, float *part, float *out, hipStream_t s) {
+    hipLaunchKernelGGL((kv_attend_kernel<DPL>), dim3(nchunk, heads), dim3(256), 0, s, desc, off, cnt, q, G, scale,
+                       nchunk, part);
+    hipLaunchKernelGGL((kv_merge_kernel<DPL>), dim3(heads), dim3(64), 0, s, part, cnt, nchunk, out);
+}
+
+// heads h < n_heads attend layer layer0 + h / kv_mul with q_h
+int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, float *out, hipStream_t s) {
+    const int d = S->d;
+    std::vector<std::vector<unsigned char>> seen(static_cast<size_t>(n_heads));
+    // TOPK: every head's candidate scores in one launch, then on the host
+    if (S->strategy == VIREO_KV_SELECT_TOPK) {
+        int maxc = 0;
+        std::vector<int> lo(static_cast<size_t>(n_heads)), nc(static_cast<size_t>(n_heads));
+        std::vector<const float *> ks(static_cast<size_t>(n_heads));
+        for (int h = 0; h < n_heads; h++) {
+            const KvLayer &L = S->layers[layer0 + h / kv_mul];
+            const int nb = int(L.blocks.size()), hi = nb - S->window_blocks;
+            lo[h] = S->sink_blocks;
+            nc[h] = hi > lo[h] ? hi - lo[h] : 0;
+            ks[h] = L.ksum;
+            maxc = nc[h] > maxc ? nc[h] : maxc;
+        }
+        if (maxc > 0) {
+            const size_t tb = size_t(n_heads) * (sizeof(void *) + 2 * sizeof(int));
+            const size_t sb = size_t(n_heads) * maxc * sizeof(float);
+            void *dv, *hv;
+            if (int rc = scratch(S, tb + sb, s, &dv)) return rc;
+            if (int rc = staging(S, tb, &hv)) return rc;
+            char *hc = static_cast<char *>(hv);
+            memcpy(hc, ks.data(), size_t(n_heads) * sizeof(void *));
+            memcpy(hc + size_t(n_heads) * sizeof(void *), lo.data(), size_t(n_heads) * sizeof(int));
+            memcpy(hc + size_t(n_heads) * (sizeof(void *) + sizeof(int)), nc.data(), size_t(n_heads) * sizeof(int));
+            char *dc = static_cast<char *>(dv);
+            if (hipMemcpyAsync(dc, hc, tb, hipMemcpyHostToDevice, s) != hipSuccess) return -EIO;
+            float *dsc = reinterpret_cast<float *>(dc + tb);
+            hipLaunchKernelGGL(kv_score_kernel, dim3((maxc + 255) / 256, n_heads), dim3(256), 0, s,
+                               reinterpret_cast<const float *const *>(dc),
+                               reinterpret_cast<const int *>(dc + size_t(n_heads) * sizeof(void *)),
+                               reinterpret_cast<const int *>(dc + size_t(n_heads) * (sizeof(void *) + sizeof(int))), q,
+                               d, maxc, dsc);
+            if (int rc = vh_check(hipGetLastError())) return rc;
+            S->hscores.resize(size_t(n_heads) * maxc);
+            if (hipMemcpyAsync(S->hscores.data(), dsc, sb, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return -EIO;
+        }
+        for (int h = 0; h < n_heads; h++)
+            select_blocks(S, int(S->layers[layer0 + h / kv_mul].blocks.size()),
+                          maxc > 0 ? S->hscores.data() + size_t(h) * maxc : nullptr, seen[h]);
+    } else {
+        for (int h = 0; h < n_heads; h++) select_blocks(S, int(S->layers[layer0 + h / kv_mul].blocks.size()), nullptr, seen[h]);
+    }
+    // page the selected blocks in, head by head and in ascending order, and
+    // list them; every lease is held until the kernels are enqueued
+    std::vector<KvDesc> desc;
+    std::vector<int> off(static_cast<size_t>(n_heads)), cnt(static_cast<size_t>(n_heads));
+    std::vector<KvBlock *> leased;
+    int rc = 0, nchunk = 1;
+    for (int h = 0; h < n_heads && !rc; h++) {
+        KvLayer &L = S->layers[layer0 + h / kv_mul];
+        off[h] = int(desc.size());
+        for (int i = 0; i < int(L.blocks.size()) && !rc; i++) {
+            if (!seen[h][i]) continue;
+            KvBlock &b = L.blocks[i];
+            if ((rc = ensure_resident(S, b, s))) break;
+            leased.push_back(&b);
+            desc.push_back(KvDesc{b.dev, b.ntok, 0});
+        }
+        cnt[h] = int(desc.size()) - off[h];
+        const int nc = (cnt[h] + kChunkBlocks - 1) / kChunkBlocks;
+        nchunk = nc > nchunk ? nc : nchunk;
+    }
+    if (!rc) {
+        const size_t db = desc.size() * sizeof(KvDesc), ib = 2 * size_t(n_heads) * sizeof(int);
+        const size_t pb = size_t(n_heads) * nchunk * (2 + d) * sizeof(float);
+        void *dv = nullptr, *hv = nullptr;
+        rc = scratch(S, db + ib + 256, s, &dv);
+        if (!rc && pb > S->part_bytes) {
+            if (hipStreamSynchronize(s) != hipSuccess) rc = -EIO;
+            if (S->part) (void)hipFree(S->part);
+            S->part = nullptr;
+            S->part_bytes = 0;
+            if (!rc && hipMalloc(reinterpret_cast<void **>(&S->part), 2 * pb) != hipSuccess) rc = -ENOMEM;
+            if (!rc) S->part_bytes = 2 * pb;
+        }
+        if (!rc) rc = staging(S, db + ib + 256, &hv);
+        if (!rc) {
+            char *hc = static_cast<char *>(hv), *dc = static_cast<char *>(dv);
+            const size_t io = (db + 255) & ~size_t(255);
+            if (db) memcpy(hc, desc.data(), db);
+            memcpy(hc + io, off.data(), size_t(n_heads) * sizeof(int));
+            memcpy(hc + io + size_t(n_heads) * sizeof(int), cnt.data(), size_t(n_heads) * sizeof(int));
+            if (hipMemcpyAsync(dc, hc, io + ib, hipMemcpyHostToDevice, s) != hipSuccess ||
+                hipEventRecord(S->staged, s) != hipSuccess)
+                rc = -EIO;
+            const KvDesc *dd = reinterpret_cast<const KvDesc *>(dc);
+            const int *doff = reinterpret_cast<const int *>(dc + io), *dcnt = doff + n_heads;
+            const float scale = 1.0f / sqrtf(float(d));
+            if (!rc) {
+                if (d == 64) launch_attend<1>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
+                else if (d == 128) launch_attend<2>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
+                else launch_attend<4>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
+                rc = vh_check(hipGetLastError());
+            }
+        }
+    }
+    // src/kvstore_ooc.c:182: released once read (the kernels are enqueued
+    // before any copy that could reuse these blocks' memory)
+    for (KvBlock *b : leased)
+        if (b->lease > 0) b->lease--;
+    return rc;
+}
+
+VireoKV *create(KVConfig cfg, int strategy, int budget) {
+    if (cfg.n_layers <= 0 || (cfg.kv_dim != 64 && cfg.kv_dim != 128 && cfg.kv_dim != 256) ||
+        cfg.block_tokens < 1 || cfg.block_tokens > 64 || cfg.sink_tokens < 0 || cfg.window_tokens < 0)
+        return nullptr;
+    if (strategy < VIREO_KV_SELECT_ALL || strategy > VIREO_KV_SELECT_TOPK) return nullptr;
+    VireoKV *S = new (std::nothrow) VireoKV;
+    if (!S) return nullptr;
+    S->cfg = cfg;
+    S->strategy = strategy;
+    S->budget = strategy == VIREO_KV_SELECT_TOPK ? (budget > 0 ? budget : 8) : 0;
+    S->d = cfg.kv_dim;
+    S->G = cfg.block_tokens;
+    S->sink_blocks = blocks_for(cfg.sink_tokens, cfg.block_tokens);
+    S->window_blocks = blocks_for(cfg.window_tokens, cfg.block_tokens);
+    S->block_bytes = 2ull * uint64_t(cfg.block_tokens) * uint64_t(cfg.kv_dim) * sizeof(float);
+    S->layers.resize(size_t(cfg.n_layers));
+    if (hipEventCreateWithFlags(&S->staged, hipEventDisableTiming) != hipSuccess) {
+        S->staged = nullptr;
+        vireo_kv_destroy(S);
+        return nullptr;
+    }
+    return S;
+}
+
+}  // namespace
+
+extern "C" VireoKV *vireo_kv_create_dense(KVConfig cfg) {
+    cfg.capacity_bytes = 0;
+    cfg.sink_tokens = 0;
+    cfg.window_tokens = 0;
+    VireoKV *S = create(cfg, VIREO_KV_SELECT_ALL, 0);
+    if (S) S->dense = true;
+    return S;
+}
+
+extern "C" VireoKV *vireo_kv_create_paged(KVConfig cfg, int strategy, int topk_budget) {
+    return create(cfg, strategy, topk_budget);
+}
+
+extern "C" int vireo_kv_append_n(VireoKV *S, int layer0, int n, int pos, const float *k, const float *v,
+                                 void *stream) {
+    (void)pos;  // tokens are appended in order, as in the reference
+    if (!S || n < 1 || n > kMaxAppend || layer0 < 0 || layer0 + n > S->cfg.n_layers || !k || !v) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, append_n(S, layer0, n, k, v, s));
+}
+
+extern "C" int vireo_kv_append(VireoKV *S, int layer, int pos, const float *k, const float *v, void *stream) {
+    return vireo_kv_append_n(S, layer, 1, pos, k, v, stream);
+}
+
+extern "C" int vireo_kv_attend_gqa(VireoKV *S, int layer0, int n_heads, int n_kv_heads, const float *q, float *out,
+                                   void *stream) {
+    if (!S || !q || !out || n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads || layer0 < 0 ||
+        layer0 + n_kv_heads > S->cfg.n_layers)
+        return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, attend(S, layer0, n_heads, n_heads / n_kv_heads, q, out, s));
+}
+
+extern "C" int vireo_kv_attend(VireoKV *S, int layer, const float *q, float *out, void *stream) {
+    return vireo_kv_attend_gqa(S, layer, 1, 1, q, out, stream);
+}
+
+extern "C" void vireo_kv_stats(const VireoKV *S, KVStats *out) {
+    if (!S || !out) return;
+    if (S->dense) {  // src/kvstore_dense.c:56-63: no counters; the appended tokens' bytes
+        memset(out, 0, sizeof *out);
+        for (const auto &L : S->layers)
+            for (const auto &b : L.blocks) out->resident_bytes += uint64_t(b.ntok) * uint64_t(S->d) * 2 * sizeof(float);
+        return;
+    }
+    *out = S->st;
+    out->resident_bytes = S->resident_bytes;
+    out->capacity_bytes = S->cfg.capacity_bytes;
+}
+
+extern "C" void vireo_kv_destroy(VireoKV *S) {
+    if (!S) return;
+    (void)hipDeviceSynchronize();
+    for (auto &L : S->layers) {
+        for (auto &b : L.blocks)
+            if (b.host) (void)hipHostFree(b.host);
+        if (L.ksum) (void)hipFree(L.ksum);
+    }
+    for (void *p : S->slabs) (void)hipFree(p);
+    if (S->dscratch) (void)hipFree(S->dscratch);
+    if (S->part) (void)hipFree(S->part);
+    if (S->hstage) (void)hipHostFree(S->hstage);
+    if (S->staged) (void)hipEventDestroy(S->staged);
+    delete S;
+}
