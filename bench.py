@@ -50,6 +50,9 @@ WORKLOADS = {
 DEFAULT = "qwen3-q4km-decode-b1"
 # name: (shape, layers, vocab): greedy decode of a whole MoE stack + Q8_0 LM head
 STACKS = {"qwen3-q4km-stack48": ("qwen3-30b-a3b-q4_k_m", 48, 151936)}
+# name: (transformer layers, query heads, kv heads, head dim, context tokens, block tokens):
+# decode attention over the GPU KV store (dense, every block attended)
+ATTN = {"qwen3-attn-ctx4096": (48, 32, 4, 128, 4096, 32)}
 
 
 def parse():
@@ -57,7 +60,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS) + sorted(STACKS) + ["copy-512MiB"])
+    ap.add_argument("--workload", default=DEFAULT,
+                    choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(ATTN) + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -247,6 +251,101 @@ def copy_calibration(args):
                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+def cpu_baseline_attn(L, H, KVH, hd, ctx, G, seed, seconds):
+    """The reference's dense KV store (src/kvstore_dense.c, from oracle/_ref)
+    attending one layer's query heads at the same context on the host,
+    scaled to the whole model's layers."""
+    from oracle.oracle import Reference, RefKV
+    if not Reference.available():
+        return None
+    ref = Reference()
+    rng = np.random.default_rng(seed)
+    kv = RefKV(ref, KVH, hd, G)
+    for t in range(ctx):
+        k = rng.standard_normal((KVH, hd)).astype(np.float32)
+        v = rng.standard_normal((KVH, hd)).astype(np.float32)
+        for h in range(KVH):
+            kv.append(h, t, k[h], v[h])
+    q = rng.standard_normal((H, hd)).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for h in range(H):
+            kv.attend(h // (H // KVH), q[h])
+        n += 1
+    dt = time.perf_counter() - t0
+    kv.close()
+    us_layer = dt / n * 1e6
+    return {"value": round(1e6 / (us_layer * L), 3), "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"{n} layers of {H}-head attention at context {ctx} through the reference's dense store "
+                      f"(one host thread), {dt:.1f} s, scaled to {L} layers",
+            "us_per_layer": round(us_layer, 1)}
+
+
+def bench_attn(args):
+    """Decode attention of a Qwen3-30B-A3B-shaped model over the GPU KV store:
+    a step appends one token's keys and values to every layer's kv heads
+    (vireo_kv_append_n per layer) and attends its query heads over the whole
+    context (vireo_kv_attend_gqa per layer). Algorithmic bytes per step are the
+    keys and values of the context, read once per kv head."""
+    import torch
+    from vireo_amd import _lib
+    from vireo_amd import kv as KV
+    _lib.check(_lib.load().vireo_hip_init(0), "vireo_hip_init")
+    L, H, KVH, hd, ctx, G = ATTN[args.workload]
+    K = args.steps or 64
+    Wm = args.warmup if args.warmup is not None else 8
+    dev = torch.device("cuda:0")
+    print(f"[bench] {args.workload}: filling {ctx} tokens of {L} x {KVH} kv heads", file=sys.stderr, flush=True)
+    kv = KV.DeviceKV(L * KVH, hd, G, dense=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    kbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
+    vbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
+    s = torch.cuda.current_stream()
+    for t in range(ctx - Wm - K):  # the context before the measured steps
+        for l in range(L):
+            kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
+    q = torch.randn((H, hd), generator=gen, device=dev)
+    out = torch.empty((H, hd), device=dev)
+
+    def step(t):
+        for l in range(L):
+            kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
+            kv.attend_gqa(l * KVH, H, KVH, q, out, stream=s)
+    t = ctx - Wm - K
+    for _ in range(Wm):
+        step(t)
+        t += 1
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K):
+        step(t)
+        t += 1
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    ms_step = ms / K
+    kv_bytes = L * KVH * (ctx - K // 2) * hd * 2 * 4  # the mean context of the timed steps
+    gbs = kv_bytes / (ms_step / 1e3) / 1e9
+    result = {
+        "metric": "decode attention tok/s over the GPU KV store (context 4096)", "value": round(K / (ms / 1e3), 2),
+        "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm, "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{L}-layer attention, {H} query heads over {KVH} kv heads of {hd}, context {ctx}, "
+                               f"blocks of {G} tokens, dense store",
+                   "layers": L, "heads": H, "kv_heads": KVH, "head_dim": hd, "context": ctx, "block_tokens": G},
+        "us_per_layer": round(ms_step * 1e3 / L, 3), "kv_bytes_per_step": kv_bytes,
+        "roofline": {"kernel": "every kernel of a step (append, attention, merge)", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    kv.close()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_attn(L, H, KVH, hd, ctx, G, args.seed, args.cpu_seconds)
+    print(json.dumps(result))
+
+
 def main():
     args = parse()
     if args.workload == "copy-512MiB":
@@ -259,6 +358,8 @@ def main():
         sys.exit(2)
     if args.workload in STACKS:
         return bench_stack(args)
+    if args.workload in ATTN:
+        return bench_attn(args)
 
     import torch
     from vireo_amd import _lib
