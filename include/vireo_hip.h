@@ -249,6 +249,84 @@ const char *vireo_gguf_moe_error(void);
 /* Destroy the store, free the device copies and close the file. */
 void vireo_gguf_moe_free(vireo_gguf_moe *m);
 
+/* ---- Whole-model decode (src/gguf_run.c:216-251) ---------------------------- */
+
+/* One transformer block's tensors (the reference's Layer, src/gguf_run.c:141-145),
+ * data on the device. Matrices may be of any type qmatvec takes; norms and
+ * biases are F32 vectors. */
+typedef struct {
+    const float *attn_norm;              /* [dim], NULL: unit weight */
+    const gguf_tensor *wq, *wk, *wv;     /* [n_heads*hs x dim], [n_kv_heads*hs x dim] x 2 */
+    const float *bq, *bk, *bv;           /* biases (add_bias, :166), NULL: none */
+    const float *q_norm, *k_norm;        /* QK-norm weights, NULL: none (:226-229) */
+    int q_norm_len, k_norm_len;          /* == head_size: per head (rmsnorm_heads, :177-179);
+                                            otherwise one norm over the whole vector */
+    const gguf_tensor *wo;               /* [dim x n_heads*hs] */
+    const float *ffn_norm;               /* [dim], NULL: unit weight */
+    const gguf_tensor *wg, *wu, *wd;     /* dense SwiGLU FFN [ffn x dim] x 2, [dim x ffn]; unused when
+                                            the model's FFNs are MoE layers */
+} vireo_block;
+
+/* The reference's Model (src/gguf_run.c:146-157) as the decode step reads it. */
+typedef struct {
+    int n_layers, dim, n_heads, n_kv_heads, head_size, ffn, vocab;
+    float eps, rope_base;
+    const vireo_block *blocks;           /* host array [n_layers] */
+    const vireo_moe_model *moe;          /* the MoE FFNs (same n_layers and dim), NULL: dense FFNs */
+    const gguf_tensor *tok_embd;         /* [vocab x dim] Q8_0, F16 or F32 */
+    const float *out_norm;               /* [dim], NULL: unit weight */
+    const gguf_tensor *lm_head;          /* [vocab x dim] */
+    const float *rope;                   /* device [max_pos x head_size] from vireo_rope_table */
+    int max_pos;
+} vireo_model;
+
+/* NEOX RoPE angles (rope_neox, src/gguf_run.c:169-174) for positions 0 ..
+ * max_pos - 1: row p of dev_out [max_pos x head_size] holds cosf(a_j) for
+ * j < head_size / 2, then sinf(a_j), with a_j = p * powf(base, -2j / hs) in the
+ * reference's float expression order, computed on the host with the C library
+ * (the same values the reference computes per call). */
+int vireo_rope_table(float base, int head_size, int max_pos, float *dev_out);
+/* Bytes of the caller-owned device state a vireo_model_step needs (activation
+ * buffers: xb, q, k, v, attention output, FFN intermediates). */
+int64_t vireo_model_state_bytes(const vireo_model *m);
+/* One token through the whole model: forward() (src/gguf_run.c:216-251).
+ * x = embed(token[0]); per block: xb = rmsnorm(x, attn_norm); q, k, v = wq, wk,
+ * wv . xb (+ biases); QK-norms; RoPE at `pos`; k, v appended to kv as token pos
+ * of layers l * n_kv_heads + h; each query head attends (grouped: head hh reads
+ * kv head hh / (n_heads / n_kv_heads)); x += wo . attention; then
+ * xb = rmsnorm(x, ffn_norm) and x += moe_ffn(xb) or the dense SwiGLU FFN. With
+ * want_logits: logits = lm_head . rmsnorm(x, out_norm) and token[0] =
+ * argmax(logits) (:254). kv: n_layers * n_kv_heads layers of head_size.
+ * token (int32 [1]), x ([dim]), logits ([vocab], may be NULL without
+ * want_logits) and state (vireo_model_state_bytes, 256-aligned) are device
+ * buffers; 0 <= pos < max_pos. Every launch goes to `stream`. */
+int vireo_model_step(const vireo_model *m, struct VireoKV *kv, int32_t *token, int pos, int want_logits, float *x,
+                     float *logits, void *state, void *stream);
+
+/* A whole model read from a GGUF file: every tensor forward() reads bound as
+ * the reference's loader binds it (src/gguf_run.c:276-318) and moved to the
+ * device, MoE experts registered with an ExpertStore over the file. */
+typedef struct {
+    gguf_ctx *gguf;
+    char arch[64];
+    vireo_model model;                   /* ready for vireo_model_step */
+    vireo_moe_model moe;                 /* model.moe points here for MoE files */
+    void *priv;
+} vireo_gguf_model;
+
+/* Read a GGUF model (metadata src/gguf_run.c:276-293: block_count,
+ * embedding_length, feed_forward_length, attention.head_count,
+ * head_count_kv, layer_norm_rms_epsilon, rope.freq_base (default 10000),
+ * attention.key_length (default dim / heads), and the MoE keys of
+ * vireo_gguf_moe_load when expert_count is present); bind blk.<l>.attn_norm,
+ * attn_q/k/v (+ .bias), attn_q_norm / attn_k_norm, attn_output, ffn_norm and
+ * either the MoE tensors or ffn_gate / ffn_up / ffn_down (:300-318), and
+ * token_embd, output_norm, output (else token_embd). Norms and biases of any
+ * dequantizable type become F32 on the device. max_pos sizes the RoPE table.
+ * Returns 0, -EINVAL (vireo_gguf_moe_error says why) or -errno. */
+int vireo_gguf_model_load(const char *path, uint64_t expert_capacity_bytes, int max_pos, vireo_gguf_model **out);
+void vireo_gguf_model_free(vireo_gguf_model *m);
+
 /* ---- ExpertStore extensions (HBM pool) -------------------------------------- */
 
 /* A store whose backing "file" is already in device memory (dev_base, size

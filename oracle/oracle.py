@@ -363,3 +363,42 @@ class RefKV:
             self.close()
         except Exception:
             pass
+
+
+class RefModel:
+    """The reference's forward() (src/gguf_run.c:216-251) on a GGUF file
+    (oracle/_ref: the shim binds the reference's Model with its own reader,
+    ExpertStore and out-of-core KV store with the "all" strategy)."""
+
+    def __init__(self, ref, path, block_tokens=32):
+        L = self.lib = ref.lib
+        L.ref_model_open.restype = _vp
+        L.ref_model_open.argtypes = [C.c_char_p, C.c_int]
+        L.ref_model_shape.argtypes = [_vp, _vp]
+        L.ref_model_forward.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
+        L.ref_model_close.argtypes = [_vp]
+        self.h = L.ref_model_open(str(path).encode(), block_tokens)
+        if not self.h:
+            raise RuntimeError(f"the reference cannot bind {path}")
+        sh = np.zeros(7, np.int32)
+        L.ref_model_shape(self.h, _ptr(sh))
+        self.dim, self.vocab, self.n_layers, self.n_heads, self.n_kv_heads, self.head_size, self.is_moe = map(int, sh)
+
+    def forward(self, token, pos, want_logits=True):
+        """(x after the last block, logits or None)."""
+        x = np.empty(self.dim, np.float32)
+        lg = np.empty(self.vocab, np.float32) if want_logits else None
+        self.lib.ref_model_forward(self.h, int(token), int(pos), int(want_logits), _ptr(x),
+                                   _ptr(lg) if want_logits else None)
+        return x, lg
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.ref_model_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -221,3 +221,29 @@ def test_loader_metadata_errors(vl, tmp_path):
         assert why in vl.vireo_gguf_moe_error().decode()
     out = C.POINTER(_lib.GGUFMoE)()
     assert vl.vireo_gguf_moe_load(str(tmp_path / "absent.gguf").encode(), 0, 0, C.byref(out)) == -errno.ENOENT
+
+
+def test_whole_model_file_binds_in_the_reference(tmp_path):
+    """write_model_gguf writes what the reference's forward() runs on: the
+    reference binds the file (shape as written) and two fresh instances give the
+    same bits for the same token sequence (the KV store starts empty)."""
+    from oracle.oracle import Reference, RefModel
+    if not Reference.available():
+        pytest.skip("oracle/_ref not built")
+    ref = Reference()
+    path = tmp_path / "m.gguf"
+    moe = W.MoEShape("m", 256, 8, 2, 256, True, W.Q4_K, W.Q4_K, W.Q6_K)
+    G.write_model_gguf(str(path), "qwen3moe", 2, 256, 8, 2, 64, 300, 3, moe=moe, untied=True)
+    runs = []
+    for _ in range(2):
+        r = RefModel(ref, path, block_tokens=4)
+        assert (r.dim, r.vocab, r.n_layers, r.n_heads, r.n_kv_heads, r.head_size, r.is_moe) == (256, 300, 2, 8, 2,
+                                                                                             64, 1)
+        out = [r.forward(t, p, p >= 2) for p, t in enumerate([5, 6, 7, 8, 9])]
+        runs.append(out)
+        r.close()
+    for (xa, la), (xb, lb) in zip(*runs):
+        np.testing.assert_array_equal(xa, xb)
+        if la is not None:
+            assert np.isfinite(la).all()
+            np.testing.assert_array_equal(la, lb)

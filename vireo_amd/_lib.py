@@ -133,6 +133,47 @@ class KVStats(C.Structure):
                                           "resident_bytes", "capacity_bytes")]
 
 
+class Block(C.Structure):
+    """vireo_block (include/vireo_hip.h): one transformer block's device tensors."""
+    _fields_ = [
+        ("attn_norm", c_vp),
+        ("wq", C.POINTER(GGUFTensor)), ("wk", C.POINTER(GGUFTensor)), ("wv", C.POINTER(GGUFTensor)),
+        ("bq", c_vp), ("bk", c_vp), ("bv", c_vp),
+        ("q_norm", c_vp), ("k_norm", c_vp),
+        ("q_norm_len", C.c_int), ("k_norm_len", C.c_int),
+        ("wo", C.POINTER(GGUFTensor)),
+        ("ffn_norm", c_vp),
+        ("wg", C.POINTER(GGUFTensor)), ("wu", C.POINTER(GGUFTensor)), ("wd", C.POINTER(GGUFTensor)),
+    ]
+
+
+class Model(C.Structure):
+    """vireo_model (include/vireo_hip.h)."""
+    _fields_ = [
+        ("n_layers", C.c_int), ("dim", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_size", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
+        ("eps", C.c_float), ("rope_base", C.c_float),
+        ("blocks", C.POINTER(Block)),
+        ("moe", C.POINTER(MoEModel)),
+        ("tok_embd", C.POINTER(GGUFTensor)),
+        ("out_norm", c_vp),
+        ("lm_head", C.POINTER(GGUFTensor)),
+        ("rope", c_vp),
+        ("max_pos", C.c_int),
+    ]
+
+
+class GGUFModelC(C.Structure):
+    """vireo_gguf_model (include/vireo_hip.h)."""
+    _fields_ = [
+        ("gguf", C.POINTER(GGUFCtx)),
+        ("arch", C.c_char * 64),
+        ("model", Model),
+        ("moe", MoEModel),
+        ("priv", c_vp),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "vireo_hip_init": (C.c_int, [C.c_int]),
@@ -180,6 +221,11 @@ SIGNATURES = {
     "vireo_gguf_moe_load": (C.c_int, [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.POINTER(GGUFMoE))]),
     "vireo_gguf_moe_error": (C.c_char_p, []),
     "vireo_gguf_moe_free": (None, [C.POINTER(GGUFMoE)]),
+    "vireo_rope_table": (C.c_int, [C.c_float, C.c_int, C.c_int, c_vp]),
+    "vireo_model_state_bytes": (C.c_int64, [C.POINTER(Model)]),
+    "vireo_model_step": (C.c_int, [C.POINTER(Model), c_vp, c_vp, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
+    "vireo_gguf_model_load": (C.c_int, [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.POINTER(GGUFModelC))]),
+    "vireo_gguf_model_free": (None, [C.POINTER(GGUFModelC)]),
     "vireo_kv_create_dense": (c_vp, [KVConfig]),
     "vireo_kv_create_paged": (c_vp, [KVConfig, C.c_int, C.c_int]),
     "vireo_kv_append": (C.c_int, [c_vp, C.c_int, C.c_int, c_vp, c_vp, c_vp]),

@@ -1,0 +1,167 @@
+// Whole-model decode: forward() of the reference's GGUF runner
+// (src/gguf_run.c:216-251) on the device, one launch sequence per token:
+// embedding, per block RMSNorm -> q/k/v matvecs (+ biases) -> QK-norms ->
+// NEOX RoPE -> KV append -> grouped-query attention over the KV store ->
+// output projection -> residual -> RMSNorm -> MoE layer or dense SwiGLU FFN
+// -> residual, then the output norm, LM head and argmax. The matvecs are
+// qmatvec, the attention is the KV store's kernel, the MoE layer is the decode
+// plan of moe_ffn_forward; this file adds the small element-wise kernels.
+#include <hip/hip_runtime.h>
+#include "common.h"
+#include "vireo_hip.h"
+#include "route_kernels.h"
+#include "vireo_kv.h"
+
+namespace {
+
+// NEOX rotation of q (nq heads) and k (nk heads) in place at one position
+// (rope_neox, src/gguf_run.c:169-174): pair (j, j + hs/2) of every head turns
+// by angle a_j; tab = [cos a_0 .. cos a_{hs/2-1}, sin a_0 ..]. Each product
+// and sum is rounded on its own, as the reference's C (no contraction).
+__global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, int nq, float *__restrict__ k, int nk, int hs,
+                                                   const float *__restrict__ tab) {
+    const int half = hs / 2;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= (nq + nk) * half) return;
+    const int h = i / half, j = i % half;
+    float *p = h < nq ? q + size_t(h) * hs : k + size_t(h - nq) * hs;
+    const float c = tab[j], s = tab[half + j];
+    const float x0 = p[j], x1 = p[j + half];
+    p[j] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    p[j + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+// y_i += b_i for up to three (y, b, n) vectors (add_bias, src/gguf_run.c:166,
+// and the residual adds x += xb, :237 / :248); a null b is skipped
+struct AddJob {
+    float *y;
+    const float *b;
+    int n;
+};
+__global__ void __launch_bounds__(256) add_kernel(AddJob j0, AddJob j1, AddJob j2) {
+    const AddJob &j = blockIdx.y == 0 ? j0 : blockIdx.y == 1 ? j1 : j2;
+    if (!j.b) return;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < j.n; i += gridDim.x * 256) j.y[i] = __fadd_rn(j.y[i], j.b[i]);
+}
+
+// h1_i = silu(h1_i) * h2_i (src/gguf_run.c:246)
+__global__ void __launch_bounds__(256) swiglu_kernel(float *__restrict__ h1, const float *__restrict__ h2, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h1[i] = swiglu(h1[i], h2[i]);
+}
+
+int add3(AddJob a, AddJob b, AddJob c, hipStream_t s) {
+    const int n = max(a.n, max(b.n, c.n));
+    const unsigned gx = unsigned(min((n + 255) / 256, 64));
+    hipLaunchKernelGGL(add_kernel, dim3(gx, 3), dim3(256), 0, s, a, b, c);
+    return vh_check(hipGetLastError());
+}
+
+int64_t pad64(int64_t n) { return (n + 63) / 64 * 64; }
+
+// the state's buffers, each 256-byte aligned
+struct Bufs {
+    float *xb, *q, *k, *v, *att, *h1, *h2;
+};
+
+Bufs carve(const vireo_model *m, void *state) {
+    const int64_t nq = int64_t(m->n_heads) * m->head_size, nk = int64_t(m->n_kv_heads) * m->head_size;
+    const int64_t nf = m->moe ? 0 : m->ffn;
+    float *p = static_cast<float *>(state);
+    Bufs b;
+    b.xb = p, p += pad64(m->dim);
+    b.q = p, p += pad64(nq);
+    b.k = p, p += pad64(nk);
+    b.v = p, p += pad64(nk);
+    b.att = p, p += pad64(nq);
+    b.h1 = p, p += pad64(nf);
+    b.h2 = p;
+    return b;
+}
+
+int check_model(const vireo_model *m) {
+    if (!m || !m->blocks || !m->tok_embd || m->n_layers <= 0 || m->dim <= 0 || m->n_heads <= 0 ||
+        m->n_kv_heads <= 0 || m->n_heads % m->n_kv_heads || m->head_size <= 0 || m->head_size % 2 || m->vocab <= 0 ||
+        !m->rope || m->max_pos <= 0)
+        return -EINVAL;
+    if (m->moe ? (m->moe->n_layers != m->n_layers || m->moe->dim != m->dim) : m->ffn <= 0) return -EINVAL;
+    for (int l = 0; l < m->n_layers; l++) {
+        const vireo_block &b = m->blocks[l];
+        if (!b.wq || !b.wk || !b.wv || !b.wo) return -EINVAL;
+        if (!m->moe && (!b.wg || !b.wu || !b.wd)) return -EINVAL;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int64_t vireo_model_state_bytes(const vireo_model *m) {
+    if (int rc = check_model(m)) return rc;
+    const int64_t nq = int64_t(m->n_heads) * m->head_size, nk = int64_t(m->n_kv_heads) * m->head_size;
+    const int64_t nf = m->moe ? 0 : m->ffn;
+    return 4 * (pad64(m->dim) + 2 * pad64(nq) + 2 * pad64(nk) + 2 * pad64(nf));
+}
+
+extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int want_logits,
+                                float *x, float *logits, void *state, void *stream) {
+    if (int rc = check_model(m)) return rc;
+    if (!kv || !token || !x || !state || (want_logits && (!logits || !m->lm_head)) || pos < 0 || pos >= m->max_pos)
+        return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const Bufs b = carve(m, state);
+    const int d = m->dim, hs = m->head_size, nh = m->n_heads, nkh = m->n_kv_heads;
+    const int nq = nh * hs, nk = nkh * hs;
+    const float eps = m->eps;
+    const float *tab = m->rope + size_t(pos) * hs;
+    const AddJob none{nullptr, nullptr, 0};
+
+    int rc = vireo_embed(m->tok_embd->ggml_type, m->tok_embd->data, d, m->vocab, token, 1, x, s);
+    for (int l = 0; l < m->n_layers && !rc; l++) {
+        const vireo_block &B = m->blocks[l];
+        // attention (src/gguf_run.c:221-237)
+        rc = vireo_rmsnorm(b.xb, x, B.attn_norm, d, 1, eps, s);
+        if (!rc) rc = qmatvec_async(b.q, b.xb, B.wq, d, nq, s);
+        if (!rc) rc = qmatvec_async(b.k, b.xb, B.wk, d, nk, s);
+        if (!rc) rc = qmatvec_async(b.v, b.xb, B.wv, d, nk, s);
+        if (!rc && (B.bq || B.bk || B.bv))
+            rc = add3(AddJob{b.q, B.bq, nq}, AddJob{b.k, B.bk, nk}, AddJob{b.v, B.bv, nk}, s);
+        if (!rc && B.q_norm)
+            rc = B.q_norm_len == hs ? vireo_rmsnorm(b.q, b.q, B.q_norm, hs, nh, eps, s)
+                                    : vireo_rmsnorm(b.q, b.q, B.q_norm, nq, 1, eps, s);
+        if (!rc && B.k_norm)
+            rc = B.k_norm_len == hs ? vireo_rmsnorm(b.k, b.k, B.k_norm, hs, nkh, eps, s)
+                                    : vireo_rmsnorm(b.k, b.k, B.k_norm, nk, 1, eps, s);
+        if (!rc) {
+            const int pairs = (nh + nkh) * (hs / 2);
+            hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, b.q, nh, b.k, nkh, hs, tab);
+            rc = vh_check(hipGetLastError());
+        }
+        if (!rc) rc = vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
+        if (!rc) rc = vireo_kv_attend_gqa(kv, l * nkh, nh, nkh, b.q, b.att, s);
+        if (!rc) rc = qmatvec_async(b.xb, b.att, B.wo, nq, d, s);
+        if (!rc) rc = add3(AddJob{x, b.xb, d}, none, none, s);
+        // FFN (src/gguf_run.c:238-249)
+        if (rc) break;
+        if (m->moe) {
+            rc = vh_moe_layer_normed(m->moe, l, x, B.ffn_norm, eps, b.xb, s);
+        } else {
+            const int f = m->ffn;
+            rc = vireo_rmsnorm(b.xb, x, B.ffn_norm, d, 1, eps, s);
+            if (!rc) rc = qmatvec_async(b.h1, b.xb, B.wg, d, f, s);
+            if (!rc) rc = qmatvec_async(b.h2, b.xb, B.wu, d, f, s);
+            if (!rc) {
+                hipLaunchKernelGGL(swiglu_kernel, dim3((f + 255) / 256), dim3(256), 0, s, b.h1, b.h2, f);
+                rc = vh_check(hipGetLastError());
+            }
+            if (!rc) rc = qmatvec_async(b.xb, b.h1, B.wd, f, d, s);
+            if (!rc) rc = add3(AddJob{x, b.xb, d}, none, none, s);
+        }
+    }
+    if (want_logits && !rc) {  // src/gguf_run.c:251-252, argmax :254
+        rc = vireo_rmsnorm(b.xb, x, m->out_norm, d, 1, eps, s);
+        if (!rc) rc = qmatvec_async(logits, b.xb, m->lm_head, d, m->vocab, s);
+        if (!rc) rc = vireo_argmax(logits, m->vocab, token, s);
+    }
+    return vh_finish(s, rc);
+}

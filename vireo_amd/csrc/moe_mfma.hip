@@ -43,6 +43,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 128, kBK = 64, kBRows = 256, kThreads = 512, kXcds = 8;
 constexpr int kChunks = kBK / 8;  // 16-byte chunks per row and K step
+#ifndef VH_MFMA_SETS
+#define VH_MFMA_SETS 3
+#endif
+// register sets of the staging waves: a step's global loads are issued
+// sets<T>() - 1 K steps before its words are dequantized into LDS (a Q4_K
+// set holds 64 registers, a Q6_K set 96: two fit)
+template <int T>
+constexpr int sets() { return T == VT_Q8_0 ? VH_MFMA_SETS : 2; }
 
 // The raw bytes of 8 consecutive weights of one row - K chunk kc (columns
 // 64 s + 8 kc .. + 7) of K step s - and their dequantization to fp32 with the
@@ -259,6 +267,7 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         // gate or up) past row p >> 3: one set of offsets, and per q a uniform
         // base pointer (32 rows are a multiple of 4 bytes, so alignments agree)
         using C = Chunk<T>;
+        constexpr int kSets = sets<T>();
         typename C::Pos bp;
         C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
         gbyte *bm[8];
@@ -268,7 +277,7 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         struct Stage {
             uint4 ah[4];
             typename C::Raw bw[8];
-        } st0, st1;
+        } st[kSets];
         auto load = [&](Stage &g, int step) {
             gbyte *as = abase + 128 * step;
 #pragma unroll
@@ -286,20 +295,23 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
                 Bs[buf][kc][rx + 32 * q] = to_bf16(w);
             }
         };
-        load(st0, 0);
-        if (nk > 1) load(st1, 1);
-        store(st0, 0, 0);
+        // step t's words live in register set t % kSets: issued at step
+        // t - kSets, dequantized into LDS at step t - 1
+#pragma unroll
+        for (int j = 0; j < kSets; j++)
+            if (j < nk) load(st[j], j);
+        store(st[0], 0, 0);
         __syncthreads();
-        for (int s = 0; s < nk; s += 2) {
-            // step s: the multiplying waves read buffer 0
-            if (s + 2 < nk) load(st0, s + 2);
-            if (s + 1 < nk) store(st1, 1, s + 1);
-            __syncthreads();
-            if (s + 1 >= nk) break;
-            // step s + 1: they read buffer 1
-            if (s + 3 < nk) load(st1, s + 3);
-            if (s + 2 < nk) store(st0, 0, s + 2);
-            __syncthreads();
+        for (int s0 = 0; s0 < nk; s0 += kSets) {
+#pragma unroll
+            for (int j = 0; j < kSets; j++) {
+                // step s: the multiplying waves read buffer s & 1
+                const int s = s0 + j;
+                if (s >= nk) break;
+                if (s + kSets < nk) load(st[j], s + kSets);
+                if (s + 1 < nk) store(st[(j + 1) % kSets], (s + 1) & 1, s + 1);
+                __syncthreads();
+            }
         }
         return;
     }

@@ -194,3 +194,86 @@ class GGUFModel:
             self.close()
         except Exception:
             pass
+
+
+# stream kinds of the attention and dense-FFN tensors (after the MoE kinds
+# of vireo_amd.workloads; 15 is the norms')
+KIND_WQ, KIND_WK, KIND_WV, KIND_WO, KIND_FG, KIND_FU, KIND_FD, KIND_VEC = range(7, 15)
+
+
+def write_model_gguf(path, arch, n_layers, d, n_heads, n_kv_heads, head_size, vocab, seed, attn_type=W.Q8_0,
+                     moe=None, ffn=0, ffn_types=(W.Q4_K, W.Q4_K, W.Q6_K), bias=False, qk_norm="head",
+                     norm_type=W.F32, untied=False, rope_base=1000000.0, lm_type=W.Q8_0, explicit_head=True):
+    """Write a synthetic whole-model GGUF file with the tensor names and
+    metadata keys the reference's loader reads (src/gguf_run.c:276-318):
+    per block attn_norm, attn_q/k/v (+ .bias with `bias`), attn_q_norm /
+    attn_k_norm (qk_norm "head": [head_size], "full": [heads * head_size],
+    None: absent), attn_output, ffn_norm, and either the MoE tensors of
+    `moe` (a workloads.MoEShape with d == moe.d) or a dense SwiGLU FFN of
+    width ffn with types ffn_types; token_embd, output_norm and, with
+    untied, output. Norm weights are 1 + 0.25 N(0, 1) stored as norm_type,
+    biases N(0, 0.1). Returns the file's expert shape (or None)."""
+    w = GGUFWriter()
+    w.add("general.architecture", STRING, arch)
+    w.add("general.name", STRING, "synthetic whole model")
+    w.add(f"{arch}.block_count", U32, n_layers)
+    w.add(f"{arch}.embedding_length", U32, d)
+    w.add(f"{arch}.feed_forward_length", U32, ffn if ffn else 4 * d)
+    w.add(f"{arch}.attention.head_count", U32, n_heads)
+    w.add(f"{arch}.attention.head_count_kv", U32, n_kv_heads)
+    if explicit_head:
+        w.add(f"{arch}.attention.key_length", U32, head_size)
+    else:
+        assert head_size == d // n_heads
+    w.add(f"{arch}.attention.layer_norm_rms_epsilon", F32, W.EPS)
+    w.add(f"{arch}.rope.freq_base", F32, rope_base)
+    if moe is not None:
+        assert moe.d == d
+        w.add(f"{arch}.expert_feed_forward_length", U32, moe.fe)
+        w.add(f"{arch}.expert_count", U32, moe.E)
+        w.add(f"{arch}.expert_used_count", U32, moe.k)
+        w.add(f"{arch}.expert_weights_norm", U32, int(moe.renorm))
+    nq, nk = n_heads * head_size, n_kv_heads * head_size
+
+    def vec(n, l, slot, base, sigma):
+        v = (base + sigma * W.host_normal(n, seed, W.stream_id(l, KIND_VEC), first=slot * 65536)).astype(np.float32)
+        if norm_type == W.F16:
+            return [n], W.F16, v.astype(np.float16)
+        return [n], W.F32, v
+
+    def mat(name, typ, cols, rows, l, kind, sigma=W.WEIGHT_SIGMA):
+        w.add_tensor(name, [cols, rows], typ, W.host_matrix(typ, cols, 0, rows, seed, W.stream_id(l, kind), sigma))
+
+    for l in range(n_layers):
+        w.add_tensor(f"blk.{l}.attn_norm.weight", *vec(d, l, 0, 1.0, 0.25))
+        mat(f"blk.{l}.attn_q.weight", attn_type, d, nq, l, KIND_WQ, 0.05)
+        mat(f"blk.{l}.attn_k.weight", attn_type, d, nk, l, KIND_WK, 0.05)
+        mat(f"blk.{l}.attn_v.weight", attn_type, d, nk, l, KIND_WV, 0.05)
+        mat(f"blk.{l}.attn_output.weight", attn_type, nq, d, l, KIND_WO, 0.05)
+        if bias:
+            w.add_tensor(f"blk.{l}.attn_q.bias", *vec(nq, l, 1, 0.0, 0.1))
+            w.add_tensor(f"blk.{l}.attn_k.bias", *vec(nk, l, 2, 0.0, 0.1))
+            w.add_tensor(f"blk.{l}.attn_v.bias", *vec(nk, l, 3, 0.0, 0.1))
+        if qk_norm:
+            w.add_tensor(f"blk.{l}.attn_q_norm.weight", *vec(head_size if qk_norm == "head" else nq, l, 4, 1.0, 0.25))
+            w.add_tensor(f"blk.{l}.attn_k_norm.weight", *vec(head_size if qk_norm == "head" else nk, l, 5, 1.0, 0.25))
+        w.add_tensor(f"blk.{l}.ffn_norm.weight", *vec(d, l, 6, 1.0, 0.25))
+        if moe is not None:
+            E, fe = moe.E, moe.fe
+            g, u, dn = W.host_layer(moe, l, seed)
+            w.add_tensor(f"blk.{l}.ffn_gate_inp.weight", [d, E], W.F32, W.host_router(moe, l, seed))
+            w.add_tensor(f"blk.{l}.ffn_gate_exps.weight", [d, fe, E], moe.gate_type, g)
+            w.add_tensor(f"blk.{l}.ffn_up_exps.weight", [d, fe, E], moe.up_type, u)
+            w.add_tensor(f"blk.{l}.ffn_down_exps.weight", [fe, d, E], moe.down_type, dn)
+        else:
+            mat(f"blk.{l}.ffn_gate.weight", ffn_types[0], d, ffn, l, KIND_FG)
+            mat(f"blk.{l}.ffn_up.weight", ffn_types[1], d, ffn, l, KIND_FU)
+            mat(f"blk.{l}.ffn_down.weight", ffn_types[2], ffn, d, l, KIND_FD)
+    emb = W.host_matrix(lm_type, d, 0, vocab, seed, W.stream_id(0, W.KIND_LM_HEAD), 0.5)
+    w.add_tensor("token_embd.weight", [d, vocab], lm_type, emb)
+    w.add_tensor("output_norm.weight", *vec(d, n_layers, 7, 1.0, 0.25))
+    if untied:
+        w.add_tensor("output.weight", [d, vocab], lm_type,
+                     W.host_matrix(lm_type, d, 0, vocab, seed + 1, W.stream_id(0, W.KIND_LM_HEAD)))
+    w.write(path)
+    return moe
