@@ -53,6 +53,9 @@ STACKS = {"qwen3-q4km-stack48": ("qwen3-30b-a3b-q4_k_m", 48, 151936)}
 # name: (transformer layers, query heads, kv heads, head dim, context tokens, block tokens):
 # decode attention over the GPU KV store (dense, every block attended)
 ATTN = {"qwen3-attn-ctx4096": (48, 32, 4, 128, 4096, 32)}
+# name: (shape, layers, query heads, kv heads, head dim, context tokens, block tokens, vocab): greedy decode of a
+# whole model (attention over the KV store + MoE FFN per block, tied Q8_0 head) through vireo_model_step
+MODELS = {"qwen3-model-ctx1024": ("qwen3-30b-a3b-q4_k_m", 48, 32, 4, 128, 1024, 32, 151936)}
 
 
 def parse():
@@ -61,7 +64,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=DEFAULT,
-                    choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(ATTN) + ["copy-512MiB"])
+                    choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(ATTN) + sorted(MODELS) + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -346,6 +349,125 @@ def bench_attn(args):
     print(json.dumps(result))
 
 
+def cpu_baseline_model(shape, L, H, KVH, hd, ctx, G, vocab, attn_types, seed, seconds):
+    """Host time per token of the whole model: the MoE stack's (cpu_baseline_stack)
+    plus, per block, the reference's gguf_matmul of the four attention matrices
+    and its dense KV store attending every query head at the context, each timed
+    on one block and scaled to L blocks."""
+    from vireo_amd import workloads as W
+    from oracle.oracle import Reference, RefKV
+    if not Reference.available():
+        return None
+    ref = Reference()
+    stack = cpu_baseline_stack(shape, L, vocab, seed, seconds)
+    d, nq, nk = shape.d, H * hd, KVH * hd
+    mats = [(t, n, r, W.host_matrix(t, n, 0, r, seed, 200 + i))
+            for i, (t, (n, r)) in enumerate(zip(attn_types, [(d, nq), (d, nk), (d, nk), (nq, d)]))]
+    xs = {n: W.host_normal(n, seed, 99) for n in (d, nq)}
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < 1.0:
+        for t, cols, rows, w in mats:
+            ref.matmul(t, w, xs[cols], cols, rows)
+        n += 1
+    mat_s = (time.perf_counter() - t0) / n
+    rng = np.random.default_rng(seed)
+    kv = RefKV(ref, KVH, hd, G)
+    for t in range(ctx):
+        for h in range(KVH):
+            kv.append(h, t, rng.standard_normal(hd).astype(np.float32), rng.standard_normal(hd).astype(np.float32))
+    q = rng.standard_normal((H, hd)).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while n < 2 or time.perf_counter() - t0 < 1.0:
+        for h in range(H):
+            kv.attend(h // (H // KVH), q[h])
+        n += 1
+    att_s = (time.perf_counter() - t0) / n
+    kv.close()
+    tok_s = 1.0 / (1.0 / stack["value"] + L * (mat_s + att_s))
+    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": stack["cores"], "kind": "reference",
+            "sample": f"{stack['sample']}; plus per block the attention matmuls ({mat_s * 1e3:.2f} ms) and "
+                      f"{H}-head attention at context {ctx} through the dense store ({att_s * 1e3:.2f} ms, one "
+                      f"thread), each timed on one block and scaled to {L}"}
+
+
+def bench_model(args):
+    """Greedy decode of a whole Qwen3-30B-A3B-shaped model through
+    vireo_model_step: per block RMSNorm, q/k/v matvecs, per-head QK-norm, RoPE,
+    KV append, grouped-query attention over the context, output matvec, then
+    the MoE FFN; final norm, Q8_0 LM head (tied embedding), argmax. The KV
+    store is first filled to the context with synthetic keys and values; the K
+    timed steps continue from there, launched in order on one stream (the KV
+    store's host-side block tables change with the position, so steps are not
+    captured in a graph)."""
+    import torch
+    from vireo_amd import _lib
+    from vireo_amd import model as MD
+    from vireo_amd import workloads as W
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    shape_name, L, H, KVH, hd, ctx, G, vocab = MODELS[args.workload]
+    L = args.layers or L
+    shape = W.SHAPES[shape_name]
+    K = args.steps or 32
+    Wm = args.warmup if args.warmup is not None else 4
+    attn_types = (W.Q4_K, W.Q4_K, W.Q6_K, W.Q4_K)
+    print(f"[bench] {args.workload}: building {L} blocks (attention {H}/{KVH} x {hd} + {shape.name} MoE) and "
+          f"the LM head; filling {ctx - Wm} tokens of context", file=sys.stderr, flush=True)
+    m = MD.DeviceModel(shape, L, H, KVH, hd, vocab=vocab, max_pos=ctx + K + 8, seed=args.seed,
+                       attn_types=attn_types, block_tokens=G)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    kbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
+    vbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
+    s = torch.cuda.current_stream()
+    p0 = ctx - Wm
+    for t in range(p0):
+        for l in range(L):
+            m.kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
+    pos = p0
+    for _ in range(Wm):
+        m.step(pos)
+        pos += 1
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K):
+        m.step(pos)
+        pos += 1
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    ms_step = ms / K
+    # algorithmic bytes of one token: per block the attention matrices, the
+    # keys and values of the context, and the MoE layer (router, k experts,
+    # activations); the LM head and the embedding row
+    layer_b = (m.attn_bytes + KVH * (ctx + K // 2) * hd * 2 * 4 + shape.E * shape.d * 4 +
+               shape.k * shape.expert_bytes() + 2 * shape.d * 4)
+    tok_b = L * layer_b + vocab * W.row_bytes(W.Q8_0, shape.d) + W.row_bytes(W.Q8_0, shape.d) + vocab * 4
+    gbs = tok_b / (ms_step / 1e3) / 1e9
+    result = {
+        "metric": "whole-model decode tok/s (attention over the KV store + MoE FFN, batch 1)",
+        "value": round(K / (ms / 1e3), 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(ms_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{L}-block {shape.name}-shaped model: attention {H} query / {KVH} kv heads of {hd} "
+                               f"(wq, wk Q4_K, wv Q6_K, wo Q4_K), context {ctx}, MoE FFN, Q8_0 LM head "
+                               f"[{vocab} x {shape.d}] tied, greedy decode batch 1",
+                   "layers": L, "heads": H, "kv_heads": KVH, "head_dim": hd, "context": ctx, "block_tokens": G,
+                   "vocab": vocab},
+        "us_per_layer": round(ms_step * 1e3 / L, 3), "token_alg_bytes": int(tok_b),
+        "roofline": {"kernel": "vireo_model_step (all kernels of a step)", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    m.close()
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline_model(shape, L, H, KVH, hd, ctx, G, vocab, attn_types, args.seed,
+                                                    args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.workload == "copy-512MiB":
@@ -360,6 +482,8 @@ def main():
         return bench_stack(args)
     if args.workload in ATTN:
         return bench_attn(args)
+    if args.workload in MODELS:
+        return bench_model(args)
 
     import torch
     from vireo_amd import _lib
