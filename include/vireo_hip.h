@@ -251,6 +251,8 @@ void vireo_gguf_moe_free(vireo_gguf_moe *m);
 
 /* ---- Whole-model decode (src/gguf_run.c:216-251) ---------------------------- */
 
+struct VireoKV; /* the GPU KV store, include/vireo_kv.h */
+
 /* One transformer block's tensors (the reference's Layer, src/gguf_run.c:141-145),
  * data on the device. Matrices may be of any type qmatvec takes; norms and
  * biases are F32 vectors. */

@@ -71,6 +71,29 @@ def test_moe_ffn_matches_oracle(cuda, oracle, path, name, T, plan):
     m.close()
 
 
+WIDE_TYPES = {"q6k-q6k-q8": (W.Q6_K, W.Q6_K, W.Q8_0), "q8-q8-q4k": (W.Q8_0, W.Q8_0, W.Q4_K),
+              "q4k-q4k-q6k": (W.Q4_K, W.Q4_K, W.Q6_K)}
+
+
+@pytest.mark.parametrize("types", list(WIDE_TYPES))
+@pytest.mark.parametrize("T", [3, 24])
+def test_decode_batch_every_type(cuda, oracle, types, T):
+    """Calls of a few tokens on d = 2048 layers of every gate/up and down type;
+    with 24 tokens over 16 experts most groups hold more tokens than one pass of
+    the decode-batch kernels takes, and a few hold one."""
+    shape = W.MoEShape("wide-" + types, 2048, 16, 4, 512, True, *WIDE_TYPES[types])
+    m = M.DeviceMoE(shape, 1, seed=53)
+    x, hb = W.host_hidden(shape.d, T, 53)
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"{shape.name} T={T}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    counts = np.bincount(io.reshape(-1), minlength=shape.E)
+    if T == 24:
+        assert counts.max() > 4 and (counts == 1).any() or counts.max() > 4
+    m.close()
+
+
 @pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
 def test_golden_moe_on_gpu(cuda, case):
     g = golden(f"moe_{case}.npz")

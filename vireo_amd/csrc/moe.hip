@@ -378,8 +378,8 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
             if (!rc) rc = vh_check(hipMemcpy(ws.act, act, size_t(E + 1) * 4, hipMemcpyHostToDevice));
             const void *const *dt = ws.tab;
             if (gdec) {
-                if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, ws.h, s);
-                if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
+                if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
+                if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
             } else {
                 if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, ws.h, s);
                 if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
@@ -446,8 +446,8 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
     } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
         // calls of a decode batch's size (a few tokens per group): inputs in registers
-        if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
-        if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
+        if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
+        if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
     } else {
         if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
         if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);

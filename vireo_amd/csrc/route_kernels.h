@@ -65,10 +65,10 @@ int vh_combine(const int32_t *idx, const float *w, const void *const *table, con
 bool vh_gdec_supported(uint32_t tg, uint32_t td, int d, int fe, const float *hb);
 int vh_gdec_gateup(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
                    const int32_t *active, const void *const *table, const float *hb, int d, int fe, int k, int E,
-                   int max_slots, float *h, hipStream_t s);
+                   int max_slots, int max_count, float *h, hipStream_t s);
 int vh_gdec_down(uint32_t type, const int32_t *counts, const int32_t *offs, const int32_t *perm,
                  const int32_t *active, const void *const *table, const float *h, int d, int fe, int E, int max_slots,
-                 float *ybuf, hipStream_t s);
+                 int max_count, float *ybuf, hipStream_t s);
 
 // Matrix-core grouped GEMMs (moe_mfma.hip) for the groups of calls of at
 // least kMfmaMinCall tokens. vh_mfma_plan lists the token tiles of groups of
