@@ -41,6 +41,7 @@ namespace {
 constexpr int kSlabBlocks = 64;   // blocks per device allocation
 constexpr int kMaxAppend = 16;    // rows per vireo_kv_append_n launch
 constexpr int kChunkBlocks = 8;   // list entries per attention workgroup
+constexpr int kStageRing = 8;     // pinned staging buffers in turn
 
 struct KvBlock {
     float *dev = nullptr;   // K (G d) then V (G d), while resident
@@ -68,6 +69,13 @@ struct AppendArgs {
     float *ks[kMaxAppend];   // the block's mean key
     float inv[kMaxAppend];   // 1 / (tokens in the block after this one)
 };
+
+// sum of v over the 64 lanes in lane order (the same on every lane)
+VH_DEV float wave_sum_ordered(float v) {
+    float s = 0.0f;
+    for (int u = 0; u < 64; u++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), u));
+    return s;
+}
 
 // grid n, 64 * DPL threads... (any multiple of 64): row i of k and v into its block
 __global__ void __launch_bounds__(256) kv_append_kernel(AppendArgs a, const float *__restrict__ k,
@@ -180,30 +188,207 @@ __global__ void __launch_bounds__(256) kv_attend_kernel(const KvDesc *__restrict
     }
 }
 
-// out[h] = (sum_c acc_c e^(m_c - M)) / (sum_c l_c e^(m_c - M)), chunks in order
+// out[h] = (sum_c acc_c e^(m_c - M)) / (sum_c l_c e^(m_c - M)), chunks in
+// order: lane c takes chunk c's (m, l) for the maximum and the weights
+// e^(m_c - M) (64 chunks at a time), then every lane adds its columns'
+// accumulators over the chunks in order
 template <int DPL>
 __global__ void __launch_bounds__(64) kv_merge_kernel(const float *__restrict__ part, const int *__restrict__ cnt,
-                                                      int nchunk, float *__restrict__ out) {
+                                                      int nchunk, int cb, float *__restrict__ out) {
     constexpr int D = 64 * DPL;
+    __shared__ float fs[64];
     const int h = blockIdx.x, lane = threadIdx.x;
-    const int nc = (cnt[h] + kChunkBlocks - 1) / kChunkBlocks;
+    const int nc = (cnt[h] + cb - 1) / cb;
     const float *p = part + size_t(h) * nchunk * (2 + D);
     float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, p[size_t(c) * (2 + D)]);
+    for (int c = lane; c < nc; c += 64) M = fmaxf(M, p[size_t(c) * (2 + D)]);
+    M = wave_max_f(M);
     float L = 0.0f, A[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; i++) A[i] = 0.0f;
-    for (int c = 0; c < nc; c++) {
-        const float *pc = p + size_t(c) * (2 + D);
-        if (pc[1] == 0.0f) continue;
-        const float f = expf(pc[0] - M);
-        L += pc[1] * f;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int c = c0 + lane;
+        float f = 0.0f, lw = 0.0f;
+        if (c < nc) {
+            const float lc = p[size_t(c) * (2 + D) + 1];
+            if (lc != 0.0f) {  // an empty chunk adds nothing
+                f = expf(p[size_t(c) * (2 + D)] - M);
+                lw = lc * f;
+            }
+        }
+        fs[lane] = f;
+        // l summed in chunk order: lane 0 adds the 64 weights in turn
+        __syncthreads();
+        const float lsum = wave_sum_ordered(lw);
+        L += lsum;
+        const int n = min(64, nc - c0);
+#pragma unroll 4
+        for (int u = 0; u < n; u++) {
+            const float fu = fs[u];
+            const float *pc = p + size_t(c0 + u) * (2 + D) + 2;
 #pragma unroll
-        for (int i = 0; i < DPL; i++) A[i] = fmaf(pc[2 + lane + 64 * i], f, A[i]);
+            for (int i = 0; i < DPL; i++) A[i] = fmaf(pc[lane + 64 * i], fu, A[i]);
+        }
+        __syncthreads();
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
     for (int i = 0; i < DPL; i++) out[size_t(h) * D + lane + 64 * i] = A[i] * inv;
+}
+
+constexpr int kGroupBlocks = 2;  // list entries per workgroup of the grouped-query kernel
+
+// Grouped-query attention when every query head of a group attends the same
+// blocks (selections that do not depend on the query): grid (chunks, kv
+// heads), 256 threads. Chunk c of kv head g covers entries c CB .. c CB + CB - 1
+// of g's list; its keys and values are read once for the HPG query heads
+// g HPG .. g HPG + HPG - 1, whose partials {m, l, acc} it writes as
+// kv_attend_kernel does (chunk size CB). Phases: the scores of every token
+// and head (a quad of lanes per token, a quarter of the dimensions each), the
+// per-head softmax over the chunk (a wave per head), then the weighted sum of
+// the values (a thread per column of 4 dimensions and group of tokens),
+// reduced over the token groups in order.
+template <int D, int HPG>
+__global__ void __launch_bounds__(256) kv_attend_group_kernel(const KvDesc *__restrict__ desc,
+                                                              const int *__restrict__ off, const int *__restrict__ cnt,
+                                                              const float *__restrict__ q, int G, float scale,
+                                                              int nchunk, float *__restrict__ part) {
+    constexpr int CB = kGroupBlocks, TMAX = CB * 64, QD = D / 4, NDQ = D / 4, NTG = 256 / NDQ;
+    __shared__ float4 qs[HPG][D / 4];
+    __shared__ float ps[HPG][TMAX];
+    __shared__ float hm[HPG], hl[HPG];
+    __shared__ float4 red[NTG][HPG][NDQ];
+    const int g = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = cnt[g], e0 = c * CB, e1 = min(n, e0 + CB);
+    if (e0 >= n) {  // an empty chunk: its heads' partials are empty
+        if (tid < HPG) {
+            float *po = part + (size_t(g * HPG + tid) * nchunk + c) * (2 + D);
+            po[0] = -INFINITY;
+            po[1] = 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < HPG * (D / 4); i += 256)
+        qs[i / (D / 4)][i % (D / 4)] = reinterpret_cast<const float4 *>(q + size_t(g) * HPG * D)[i];
+    const KvDesc *dl = desc + off[g];
+    const float *B0 = dl[e0].blk, *B1 = e0 + 1 < e1 ? dl[e0 + 1].blk : B0;
+    const int n0 = dl[e0].ntok, T = n0 + (e0 + 1 < e1 ? dl[e0 + 1].ntok : 0);
+    auto krow = [&](int t) { return t < n0 ? B0 + size_t(t) * D : B1 + size_t(t - n0) * D; };  // V at + G D
+    // the values this thread weighs in the last phase, loaded before the scores
+    // are formed (D <= 128: at most 16 float4 per thread)
+    const int dq = tid % NDQ, tg = tid / NDQ;
+    constexpr int MT = D <= 128 ? TMAX / NTG : 1;
+    float4 vv[MT];
+    if constexpr (D <= 128) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            const int t = tg + NTG * m;
+            vv[m] = t < T ? reinterpret_cast<const float4 *>(krow(t) + size_t(G) * D)[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    __syncthreads();
+    // scores: lanes 4m .. 4m + 3 take token t = tid / 4 (+ 64 j), quarter tid % 4
+    const int qd = tid & 3;
+#pragma unroll
+    for (int t0 = 0; t0 < TMAX; t0 += 64) {
+        const int t = t0 + (tid >> 2);
+        float sc[HPG];
+#pragma unroll
+        for (int i = 0; i < HPG; i++) sc[i] = 0.0f;
+        if (t < T) {
+            const float4 *kr = reinterpret_cast<const float4 *>(krow(t) + qd * QD);
+#pragma unroll
+            for (int j = 0; j < QD / 4; j++) {
+                const float4 kk = kr[j];
+#pragma unroll
+                for (int i = 0; i < HPG; i++) {
+                    const float4 qq = qs[i][qd * (QD / 4) + j];
+                    sc[i] = fmaf(qq.x, kk.x, fmaf(qq.y, kk.y, fmaf(qq.z, kk.z, fmaf(qq.w, kk.w, sc[i]))));
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < HPG; i++) {
+            sc[i] += dpp_f<0xB1>(sc[i]);
+            sc[i] += dpp_f<0x4E>(sc[i]);
+        }
+        if (qd == 0 && t < T)
+#pragma unroll
+            for (int i = 0; i < HPG; i++) ps[i][t] = sc[i] * scale;
+    }
+    __syncthreads();
+    // softmax of each head over the chunk's tokens: wave w takes heads w, w + 4, ...
+    for (int i = wv; i < HPG; i += 4) {
+        const float a = lane < T ? ps[i][lane] : -INFINITY, b = lane + 64 < T ? ps[i][lane + 64] : -INFINITY;
+        const float mx = wave_max_f(fmaxf(a, b));
+        const float pa = lane < T ? expf(a - mx) : 0.0f, pb = lane + 64 < T ? expf(b - mx) : 0.0f;
+        const float l = wave_sum_f(pa + pb);
+        if (lane < T) ps[i][lane] = pa;
+        if (lane + 64 < T) ps[i][lane + 64] = pb;
+        if (lane == 0) {
+            hm[i] = mx;
+            hl[i] = l;
+        }
+    }
+    __syncthreads();
+    // weighted values: thread (token group tg, column dq) sums tokens tg, tg + NTG, ...
+    float4 acc[HPG];
+#pragma unroll
+    for (int i = 0; i < HPG; i++) acc[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto weigh = [&](const float4 &v, int t) {
+#pragma unroll
+        for (int i = 0; i < HPG; i++) {
+            const float pt = ps[i][t];
+            acc[i].x = fmaf(pt, v.x, acc[i].x);
+            acc[i].y = fmaf(pt, v.y, acc[i].y);
+            acc[i].z = fmaf(pt, v.z, acc[i].z);
+            acc[i].w = fmaf(pt, v.w, acc[i].w);
+        }
+    };
+    if constexpr (D <= 128) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+            if (tg + NTG * m < T) weigh(vv[m], tg + NTG * m);
+    } else {
+        for (int t = tg; t < T; t += NTG) weigh(reinterpret_cast<const float4 *>(krow(t) + size_t(G) * D)[dq], t);
+    }
+#pragma unroll
+    for (int i = 0; i < HPG; i++) red[tg][i][dq] = acc[i];
+    __syncthreads();
+    for (int x = tid; x < HPG * NDQ; x += 256) {
+        const int i = x / NDQ, col = x % NDQ;
+        float4 a = red[0][i][col];
+        for (int u = 1; u < NTG; u++) {
+            const float4 b = red[u][i][col];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        float *po = part + (size_t(g * HPG + i) * nchunk + c) * (2 + D);
+        po[2 + 4 * col] = a.x;
+        po[3 + 4 * col] = a.y;
+        po[4 + 4 * col] = a.z;
+        po[5 + 4 * col] = a.w;
+        if (col == 0) {
+            po[0] = hm[i];
+            po[1] = hl[i];
+        }
+    }
+}
+
+template <int D>
+int launch_group(int hpg, const KvDesc *desc, const int *off, const int *cnt_kv, const int *cnt_q, const float *q,
+                 int G, float scale, int nchunk, int n_kv, int n_heads, float *part, float *out, hipStream_t s) {
+    const dim3 g(nchunk, n_kv);
+    switch (hpg) {
+    case 1: hipLaunchKernelGGL((kv_attend_group_kernel<D, 1>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
+    case 2: hipLaunchKernelGGL((kv_attend_group_kernel<D, 2>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
+    case 4: hipLaunchKernelGGL((kv_attend_group_kernel<D, 4>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
+    default: hipLaunchKernelGGL((kv_attend_group_kernel<D, 8>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
+    }
+    hipLaunchKernelGGL((kv_merge_kernel<D / 64>), dim3(n_heads), dim3(64), 0, s, part, cnt_q, nchunk, kGroupBlocks, out);
+    return vh_check(hipGetLastError());
 }
 
 int blocks_for(int tokens, int g) { return tokens > 0 ? (tokens + g - 1) / g : 0; }
@@ -225,9 +410,12 @@ struct VireoKV {
     // device scratch and its pinned staging
     void *dscratch = nullptr;
     size_t dscratch_bytes = 0;
-    void *hstage = nullptr;
-    size_t hstage_bytes = 0;
-    hipEvent_t staged = nullptr;  // the last upload from hstage has been read
+    // pinned staging for uploads, a ring: slot i is reused once its last
+    // upload has been read (staged[i]), so the host may run calls ahead
+    void *hstage[kStageRing] = {};
+    size_t hstage_bytes[kStageRing] = {};
+    hipEvent_t staged[kStageRing] = {};
+    int stage_next = 0;
     float *part = nullptr;
     size_t part_bytes = 0;
     std::vector<float> hscores;
@@ -360,17 +548,21 @@ int scratch(VireoKV *S, size_t bytes, hipStream_t s, void **out) {
     return 0;
 }
 
-// pinned staging of at least `bytes`, once the previous upload from it is done
-int staging(VireoKV *S, size_t bytes, void **out) {
-    if (S->staged && hipEventSynchronize(S->staged) != hipSuccess) return -EIO;
-    if (bytes > S->hstage_bytes) {
-        if (S->hstage) (void)hipHostFree(S->hstage);
-        S->hstage = nullptr;
+// the next pinned staging buffer of the ring, of at least `bytes`, once its
+// previous upload is done; record staged[*slot] after the upload from it
+int staging(VireoKV *S, size_t bytes, void **out, int *slot) {
+    const int i = S->stage_next;
+    S->stage_next = (i + 1) % kStageRing;
+    if (S->staged[i] && hipEventSynchronize(S->staged[i]) != hipSuccess) return -EIO;
+    if (bytes > S->hstage_bytes[i]) {
+        if (S->hstage[i]) (void)hipHostFree(S->hstage[i]);
+        S->hstage[i] = nullptr;
         const size_t nb = bytes < (size_t(1) << 16) ? (size_t(1) << 16) : 2 * bytes;
-        if (hipHostMalloc(&S->hstage, nb, 0) != hipSuccess) { S->hstage_bytes = 0; return -ENOMEM; }
-        S->hstage_bytes = nb;
+        if (hipHostMalloc(&S->hstage[i], nb, 0) != hipSuccess) { S->hstage_bytes[i] = 0; return -ENOMEM; }
+        S->hstage_bytes[i] = nb;
     }
-    *out = S->hstage;
+    *out = S->hstage[i];
+    *slot = i;
     return 0;
 }
 
@@ -422,7 +614,7 @@ void launch_attend(const KvDesc *desc, const int *off, const int *cnt, const flo
                    int nchunk, int heads, float *part, float *out, hipStream_t s) {
     hipLaunchKernelGGL((kv_attend_kernel<DPL>), dim3(nchunk, heads), dim3(256), 0, s, desc, off, cnt, q, G, scale,
                        nchunk, part);
-    hipLaunchKernelGGL((kv_merge_kernel<DPL>), dim3(heads), dim3(64), 0, s, part, cnt, nchunk, out);
+    hipLaunchKernelGGL((kv_merge_kernel<DPL>), dim3(heads), dim3(64), 0, s, part, cnt, nchunk, kChunkBlocks, out);
 }
 
 // heads h < n_heads attend layer layer0 + h / kv_mul with q_h
@@ -447,13 +639,16 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
             const size_t sb = size_t(n_heads) * maxc * sizeof(float);
             void *dv, *hv;
             if (int rc = scratch(S, tb + sb, s, &dv)) return rc;
-            if (int rc = staging(S, tb, &hv)) return rc;
+            int slot;
+            if (int rc = staging(S, tb, &hv, &slot)) return rc;
             char *hc = static_cast<char *>(hv);
             memcpy(hc, ks.data(), size_t(n_heads) * sizeof(void *));
             memcpy(hc + size_t(n_heads) * sizeof(void *), lo.data(), size_t(n_heads) * sizeof(int));
             memcpy(hc + size_t(n_heads) * (sizeof(void *) + sizeof(int)), nc.data(), size_t(n_heads) * sizeof(int));
             char *dc = static_cast<char *>(dv);
-            if (hipMemcpyAsync(dc, hc, tb, hipMemcpyHostToDevice, s) != hipSuccess) return -EIO;
+            if (hipMemcpyAsync(dc, hc, tb, hipMemcpyHostToDevice, s) != hipSuccess ||
+                hipEventRecord(S->staged[slot], s) != hipSuccess)
+                return -EIO;
             float *dsc = reinterpret_cast<float *>(dc + tb);
             hipLaunchKernelGGL(kv_score_kernel, dim3((maxc + 255) / 256, n_heads), dim3(256), 0, s,
                                reinterpret_cast<const float *const *>(dc),
@@ -473,29 +668,46 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
         for (int h = 0; h < n_heads; h++) select_blocks(S, int(S->layers[layer0 + h / kv_mul].blocks.size()), nullptr, seen[h]);
     }
     // page the selected blocks in, head by head and in ascending order, and
-    // list them; every lease is held until the kernels are enqueued
+    // list them; every lease is held until the kernels are enqueued. When the
+    // selection does not depend on the query and the group size has a
+    // grouped-query kernel, the list is kept once per kv head (the heads of a
+    // group select the same blocks) and the blocks are read once per group.
+    const bool grouped = S->strategy != VIREO_KV_SELECT_TOPK &&
+                         (kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 8) &&
+                         !(reinterpret_cast<uintptr_t>(q) & 15u);
+    const int n_lists = grouped ? n_heads / kv_mul : n_heads, cb = grouped ? kGroupBlocks : kChunkBlocks;
     std::vector<KvDesc> desc;
-    std::vector<int> off(static_cast<size_t>(n_heads)), cnt(static_cast<size_t>(n_heads));
+    std::vector<int> off(static_cast<size_t>(n_lists)), cnt(static_cast<size_t>(n_heads));
     std::vector<KvBlock *> leased;
     int rc = 0, nchunk = 1;
     for (int h = 0; h < n_heads && !rc; h++) {
         KvLayer &L = S->layers[layer0 + h / kv_mul];
-        off[h] = int(desc.size());
+        const bool lists = !grouped || h % kv_mul == 0;
+        const int d0 = int(desc.size());
+        if (lists) off[grouped ? h / kv_mul : h] = d0;
+        int got = 0;
         for (int i = 0; i < int(L.blocks.size()) && !rc; i++) {
             if (!seen[h][i]) continue;
             KvBlock &b = L.blocks[i];
             if ((rc = ensure_resident(S, b, s))) break;
             leased.push_back(&b);
-            desc.push_back(KvDesc{b.dev, b.ntok, 0});
+            if (lists) desc.push_back(KvDesc{b.dev, b.ntok, 0});
+            got++;
         }
-        cnt[h] = int(desc.size()) - off[h];
-        const int nc = (cnt[h] + kChunkBlocks - 1) / kChunkBlocks;
+        cnt[h] = got;
+        const int nc = (got + cb - 1) / cb;
         nchunk = nc > nchunk ? nc : nchunk;
     }
     if (!rc) {
-        const size_t db = desc.size() * sizeof(KvDesc), ib = 2 * size_t(n_heads) * sizeof(int);
+        // device: desc, then off [n_lists], then (grouped) the per-list counts, then the per-head counts
+        std::vector<int> cnt_list;
+        if (grouped)
+            for (int g = 0; g < n_lists; g++) cnt_list.push_back(cnt[size_t(g) * kv_mul]);
+        const size_t db = desc.size() * sizeof(KvDesc);
+        const size_t ib = (size_t(n_lists) * (grouped ? 2 : 1) + size_t(n_heads)) * sizeof(int);
         const size_t pb = size_t(n_heads) * nchunk * (2 + d) * sizeof(float);
         void *dv = nullptr, *hv = nullptr;
+        int slot = 0;
         rc = scratch(S, db + ib + 256, s, &dv);
         if (!rc && pb > S->part_bytes) {
             if (hipStreamSynchronize(s) != hipSuccess) rc = -EIO;
@@ -505,20 +717,27 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
             if (!rc && hipMalloc(reinterpret_cast<void **>(&S->part), 2 * pb) != hipSuccess) rc = -ENOMEM;
             if (!rc) S->part_bytes = 2 * pb;
         }
-        if (!rc) rc = staging(S, db + ib + 256, &hv);
+        if (!rc) rc = staging(S, db + ib + 256, &hv, &slot);
         if (!rc) {
             char *hc = static_cast<char *>(hv), *dc = static_cast<char *>(dv);
             const size_t io = (db + 255) & ~size_t(255);
             if (db) memcpy(hc, desc.data(), db);
-            memcpy(hc + io, off.data(), size_t(n_heads) * sizeof(int));
-            memcpy(hc + io + size_t(n_heads) * sizeof(int), cnt.data(), size_t(n_heads) * sizeof(int));
+            int *hi = reinterpret_cast<int *>(hc + io);
+            memcpy(hi, off.data(), size_t(n_lists) * sizeof(int));
+            if (grouped) memcpy(hi + n_lists, cnt_list.data(), size_t(n_lists) * sizeof(int));
+            memcpy(hi + n_lists * (grouped ? 2 : 1), cnt.data(), size_t(n_heads) * sizeof(int));
             if (hipMemcpyAsync(dc, hc, io + ib, hipMemcpyHostToDevice, s) != hipSuccess ||
-                hipEventRecord(S->staged, s) != hipSuccess)
+                hipEventRecord(S->staged[slot], s) != hipSuccess)
                 rc = -EIO;
             const KvDesc *dd = reinterpret_cast<const KvDesc *>(dc);
-            const int *doff = reinterpret_cast<const int *>(dc + io), *dcnt = doff + n_heads;
+            const int *doff = reinterpret_cast<const int *>(dc + io);
+            const int *dcnt_list = doff + n_lists, *dcnt = doff + n_lists * (grouped ? 2 : 1);
             const float scale = 1.0f / sqrtf(float(d));
-            if (!rc) {
+            if (!rc && grouped) {
+                if (d == 64) rc = launch_group<64>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else if (d == 128) rc = launch_group<128>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else rc = launch_group<256>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+            } else if (!rc) {
                 if (d == 64) launch_attend<1>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
                 else if (d == 128) launch_attend<2>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
                 else launch_attend<4>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
@@ -549,11 +768,12 @@ VireoKV *create(KVConfig cfg, int strategy, int budget) {
     S->window_blocks = blocks_for(cfg.window_tokens, cfg.block_tokens);
     S->block_bytes = 2ull * uint64_t(cfg.block_tokens) * uint64_t(cfg.kv_dim) * sizeof(float);
     S->layers.resize(size_t(cfg.n_layers));
-    if (hipEventCreateWithFlags(&S->staged, hipEventDisableTiming) != hipSuccess) {
-        S->staged = nullptr;
-        vireo_kv_destroy(S);
-        return nullptr;
-    }
+    for (int i = 0; i < kStageRing; i++)
+        if (hipEventCreateWithFlags(&S->staged[i], hipEventDisableTiming) != hipSuccess) {
+            S->staged[i] = nullptr;
+            vireo_kv_destroy(S);
+            return nullptr;
+        }
     return S;
 }
 
@@ -621,7 +841,9 @@ extern "C" void vireo_kv_destroy(VireoKV *S) {
     for (void *p : S->slabs) (void)hipFree(p);
     if (S->dscratch) (void)hipFree(S->dscratch);
     if (S->part) (void)hipFree(S->part);
-    if (S->hstage) (void)hipHostFree(S->hstage);
-    if (S->staged) (void)hipEventDestroy(S->staged);
+    for (int i = 0; i < kStageRing; i++) {
+        if (S->hstage[i]) (void)hipHostFree(S->hstage[i]);
+        if (S->staged[i]) (void)hipEventDestroy(S->staged[i]);
+    }
     delete S;
 }
