@@ -392,13 +392,13 @@ def cpu_baseline_model(shape, L, H, KVH, hd, ctx, G, vocab, attn_types, seed, se
 
 def bench_model(args):
     """Greedy decode of a whole Qwen3-30B-A3B-shaped model through
-    vireo_model_step: per block RMSNorm, q/k/v matvecs, per-head QK-norm, RoPE,
-    KV append, grouped-query attention over the context, output matvec, then
-    the MoE FFN; final norm, Q8_0 LM head (tied embedding), argmax. The KV
-    store is first filled to the context with synthetic keys and values; the K
-    timed steps continue from there, launched in order on one stream (the KV
-    store's host-side block tables change with the position, so steps are not
-    captured in a graph)."""
+    vireo_model_step_pos: per block RMSNorm, q/k/v matvecs, per-head QK-norm,
+    RoPE, KV append, grouped-query attention over the context, output matvec,
+    then the MoE FFN; final norm, Q8_0 LM head (tied embedding), argmax. The
+    contiguous KV store is first filled to the context with synthetic keys and
+    values; the position and the token live on the device, so the K timed
+    steps are one HIP-graph replay (each step reads the token and position
+    the previous one wrote)."""
     import torch
     from vireo_amd import _lib
     from vireo_amd import model as MD
@@ -409,12 +409,12 @@ def bench_model(args):
     L = args.layers or L
     shape = W.SHAPES[shape_name]
     K = args.steps or 32
-    Wm = args.warmup if args.warmup is not None else 4
+    Wm = args.warmup if args.warmup is not None else 2
     attn_types = (W.Q4_K, W.Q4_K, W.Q6_K, W.Q4_K)
     print(f"[bench] {args.workload}: building {L} blocks (attention {H}/{KVH} x {hd} + {shape.name} MoE) and "
           f"the LM head; filling {ctx - Wm} tokens of context", file=sys.stderr, flush=True)
     m = MD.DeviceModel(shape, L, H, KVH, hd, vocab=vocab, max_pos=ctx + K + 8, seed=args.seed,
-                       attn_types=attn_types, block_tokens=G)
+                       attn_types=attn_types, block_tokens=G, contiguous=True)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
@@ -425,18 +425,34 @@ def bench_model(args):
     for t in range(p0):
         for l in range(L):
             m.kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
-    pos = p0
-    for _ in range(Wm):
-        m.step(pos)
-        pos += 1
+    m.pos.fill_(p0)
+    for _ in range(Wm):  # uncaptured: first calls pin expert leases and size buffers
+        m.step_pos()
+    torch.cuda.synchronize()
+    tok0 = int(m.token.item())
+    gs = torch.cuda.Stream()
+    gs.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gs):
+        for _ in range(K):
+            m.step_pos(stream=gs)
+    torch.cuda.synchronize()
+
+    def replay():
+        m.pos.fill_(ctx)
+        m.token.fill_(tok0)
+        graph.replay()
+    replay()  # untimed: the same positions and tokens as the timed replay
+    torch.cuda.synchronize()
+    m.pos.fill_(ctx)
+    m.token.fill_(tok0)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(K):
-        m.step(pos)
-        pos += 1
+    graph.replay()
     e1.record()
     torch.cuda.synchronize()
+    assert int(m.pos.item()) == ctx + K
     ms = e0.elapsed_time(e1)
     ms_step = ms / K
     # algorithmic bytes of one token: per block the attention matrices, the
@@ -453,7 +469,7 @@ def bench_model(args):
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{L}-block {shape.name}-shaped model: attention {H} query / {KVH} kv heads of {hd} "
                                f"(wq, wk Q4_K, wv Q6_K, wo Q4_K), context {ctx}, MoE FFN, Q8_0 LM head "
-                               f"[{vocab} x {shape.d}] tied, greedy decode batch 1",
+                               f"[{vocab} x {shape.d}] tied, greedy decode batch 1, steps in one HIP graph",
                    "layers": L, "heads": H, "kv_heads": KVH, "head_dim": hd, "context": ctx, "block_tokens": G,
                    "vocab": vocab},
         "us_per_layer": round(ms_step * 1e3 / L, 3), "token_alg_bytes": int(tok_b),

@@ -304,6 +304,15 @@ int64_t vireo_model_state_bytes(const vireo_model *m);
  * buffers; 0 <= pos < max_pos. Every launch goes to `stream`. */
 int vireo_model_step(const vireo_model *m, struct VireoKV *kv, int32_t *token, int pos, int want_logits, float *x,
                      float *logits, void *state, void *stream);
+/* vireo_model_step at the position *pos (device int32), which the call then
+ * advances by one; kv must be a contiguous store (vireo_kv_create_contiguous)
+ * driven by device positions. Every launch reads the position from device
+ * memory, so a loop of steps can be captured in one HIP graph (after one
+ * uncaptured step: first calls size buffers and pin expert leases). A
+ * position outside [0, max_pos) or past the store's tokens makes the step's
+ * RoPE and KV writes no-ops. No counterpart in the reference. */
+int vireo_model_step_pos(const vireo_model *m, struct VireoKV *kv, int32_t *token, int32_t *pos, int want_logits,
+                         float *x, float *logits, void *state, void *stream);
 
 /* A whole model read from a GGUF file: every tensor forward() reads bound as
  * the reference's loader binds it (src/gguf_run.c:276-318) and moved to the

@@ -100,6 +100,26 @@ int vireo_kv_attend(VireoKV *s, int layer, const float *q, float *out, void *str
  * reference's forward does (src/gguf_run.c:233-235). One launch for all heads. */
 int vireo_kv_attend_gqa(VireoKV *s, int layer0, int n_heads, int n_kv_heads, const float *q, float *out,
                         void *stream);
+/* A dense store whose blocks for up to max_tokens tokens per layer are
+ * allocated at once, every layer's blocks consecutive, so a block's address
+ * follows from the position: besides the calls above (host positions) it
+ * takes the two calls below, which read the position from device memory and
+ * so can be captured in a HIP graph with a device-side position counter.
+ * Results equal vireo_kv_create_dense's bit for bit. Once a device-position
+ * append has been made, a store takes only device-position calls (the host
+ * does not track those tokens; vireo_kv_stats counts the host-position ones).
+ * NULL on failure. No counterpart in the reference (its stores grow by host
+ * calls). */
+VireoKV *vireo_kv_create_contiguous(KVConfig cfg, int max_tokens);
+/* vireo_kv_append_n at the position *pos (device int32); nothing is written
+ * for a position outside [0, max_tokens). */
+int vireo_kv_append_pos(VireoKV *s, int layer0, int n, const int32_t *pos, const float *k, const float *v,
+                        void *stream);
+/* vireo_kv_attend_gqa over tokens 0 .. *pos of each kv head (n_heads /
+ * n_kv_heads in {1, 2, 4, 8}; q 16-byte aligned). The first call on a store
+ * sizes its buffers (synchronizing the stream): capture after one call. */
+int vireo_kv_attend_gqa_pos(VireoKV *s, int layer0, int n_heads, int n_kv_heads, const int32_t *pos, const float *q,
+                            float *out, void *stream);
 /* kv_stats (src/kvstore.h:65) */
 void vireo_kv_stats(const VireoKV *s, KVStats *out);
 /* kv_destroy (src/kvstore.h:66-68); waits for the store's work first */

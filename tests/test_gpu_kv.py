@@ -149,3 +149,45 @@ def test_empty_layer_attends_to_zero(cuda, ref):
     g.attend(1, q, out)
     assert torch.count_nonzero(out).item() == 0
     g.close()
+
+
+@pytest.mark.parametrize("d,G", [(128, 32), (64, 16)])
+def test_contiguous_store_equals_dense(cuda, d, G):
+    """A contiguous store (blocks allocated up front) gives the dense store's
+    grouped-query results bit for bit, driven by host positions and, in a third
+    store, by device positions (vireo_kv_append_pos / vireo_kv_attend_gqa_pos,
+    the calls a captured decode loop makes), across block boundaries."""
+    n_tl, n_kv, n_heads, T = 2, 2, 8, 3 * G + 5
+    L = n_tl * n_kv
+    dense = KV.DeviceKV(L, d, G, dense=True)
+    cont = KV.DeviceKV(L, d, G, dense=True, max_tokens=T)
+    devp = KV.DeviceKV(L, d, G, dense=True, max_tokens=T)
+    pos = torch.zeros(1, dtype=torch.int32, device=cuda)
+    rng = np.random.default_rng(5)
+    outs = [torch.empty((n_heads, d), dtype=torch.float32, device=cuda) for _ in range(3)]
+    for t in range(T):
+        K = torch.from_numpy(rng.standard_normal((L, d)).astype(np.float32)).to(cuda)
+        V = torch.from_numpy(rng.standard_normal((L, d)).astype(np.float32)).to(cuda)
+        dense.append(0, t, K, V)
+        cont.append(0, t, K, V)
+        pos.fill_(t)
+        devp.append_pos(0, pos, K, V)
+        if t % 7 == 6 or t == T - 1:
+            for tl in range(n_tl):
+                q = torch.from_numpy(rng.standard_normal((n_heads, d)).astype(np.float32)).to(cuda)
+                dense.attend_gqa(tl * n_kv, n_heads, n_kv, q, outs[0])
+                cont.attend_gqa(tl * n_kv, n_heads, n_kv, q, outs[1])
+                devp.attend_gqa_pos(tl * n_kv, n_heads, n_kv, pos, q, outs[2])
+                assert torch.equal(outs[0], outs[1]), (t, tl)
+                assert torch.equal(outs[0], outs[2]), (t, tl)
+    # a position past the store's tokens writes nothing
+    pos.fill_(T)
+    before = outs[2].clone()
+    devp.append_pos(0, pos, K, V)
+    pos.fill_(T - 1)
+    devp.attend_gqa_pos(0, n_heads, n_kv, pos, q, outs[2])
+    dense.attend_gqa(0, n_heads, n_kv, q, outs[0])
+    assert torch.equal(outs[0], outs[2])
+    del before
+    for s in (dense, cont, devp):
+        s.close()

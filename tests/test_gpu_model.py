@@ -143,3 +143,53 @@ def test_model_load_names_what_is_missing(cuda, tmp_path):
     w.write(str(path))
     with pytest.raises(_lib.VireoError, match="attn_q"):
         GGUFDecoder(path, max_pos=8)
+
+
+@pytest.mark.parametrize("name", ["qwen3moe", "qwen2-dense"])
+def test_device_position_steps_and_graph(cuda, tmp_path, name):
+    """vireo_model_step_pos (position on the device, contiguous KV store) gives
+    vireo_model_step's results bit for bit; and a greedy continuation captured
+    in one HIP graph (the device position advancing inside) replays to the same
+    tokens and logits as the same steps run eagerly."""
+    from vireo_amd.model import GGUFDecoder
+    path = tmp_path / f"{name}.gguf"
+    G.write_model_gguf(str(path), seed=43, **CASES[name])
+    host = GGUFDecoder(path, max_pos=64, block_tokens=BLOCK)
+    devp = GGUFDecoder(path, max_pos=64, block_tokens=BLOCK, contiguous=True)
+    tok = PROMPT[0]
+    for pos in range(12):  # prompt, then greedy
+        want = pos >= len(PROMPT) - 1
+        nt = host.step(tok, pos, want)
+        devp.token.fill_(tok)
+        devp.step_pos(want)
+        torch.cuda.synchronize()
+        assert torch.equal(host.x, devp.x), pos
+        if want:
+            assert torch.equal(host.logits, devp.logits), pos
+            assert int(devp.token.item()) == nt
+        tok = nt if want else PROMPT[pos + 1]
+    assert int(devp.pos.item()) == 12
+    # eager reference continuation on the host-position decoder
+    start, eager = tok, []
+    for pos in range(12, 20):
+        tok = host.step(tok, pos, True)
+        eager.append((tok, host.logits.clone()))
+    # the same 8 steps captured once (nothing runs while capturing) and replayed
+    assert int(devp.token.item()) == start
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    logits = []
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(8):
+            devp.step_pos(True, stream=s)
+            logits.append(devp.logits.clone())
+    torch.cuda.synchronize()
+    assert int(devp.pos.item()) == 12
+    g.replay()
+    torch.cuda.synchronize()
+    for i, (t, lg) in enumerate(eager):
+        assert torch.equal(logits[i], lg), i
+    assert int(devp.token.item()) == eager[-1][0] and int(devp.pos.item()) == 20
+    host.close()
+    devp.close()

@@ -224,6 +224,10 @@ SIGNATURES = {
     "vireo_rope_table": (C.c_int, [C.c_float, C.c_int, C.c_int, c_vp]),
     "vireo_model_state_bytes": (C.c_int64, [C.POINTER(Model)]),
     "vireo_model_step": (C.c_int, [C.POINTER(Model), c_vp, c_vp, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
+    "vireo_model_step_pos": (C.c_int, [C.POINTER(Model), c_vp, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp, c_vp]),
+    "vireo_kv_create_contiguous": (c_vp, [KVConfig, C.c_int]),
+    "vireo_kv_append_pos": (C.c_int, [c_vp, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
+    "vireo_kv_attend_gqa_pos": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
     "vireo_gguf_model_load": (C.c_int, [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.POINTER(GGUFModelC))]),
     "vireo_gguf_model_free": (None, [C.POINTER(GGUFModelC)]),
     "vireo_kv_create_dense": (c_vp, [KVConfig]),

@@ -248,18 +248,41 @@ constexpr int kGroupBlocks = 2;  // list entries per workgroup of the grouped-qu
 // per-head softmax over the chunk (a wave per head), then the weighted sum of
 // the values (a thread per column of 4 dimensions and group of tokens),
 // reduced over the token groups in order.
-template <int D, int HPG>
-__global__ void __launch_bounds__(256) kv_attend_group_kernel(const KvDesc *__restrict__ desc,
-                                                              const int *__restrict__ off, const int *__restrict__ cnt,
-                                                              const float *__restrict__ q, int G, float scale,
-                                                              int nchunk, float *__restrict__ part) {
+// The blocks of kv head g's list: count(g), and entry(g, e) = (block, tokens).
+struct ListedBlocks {  // lists uploaded by the host
+    const KvDesc *desc;
+    const int *off, *cnt;
+    VH_DEV int count(int g) const { return cnt[g]; }
+    VH_DEV KvDesc entry(int g, int e) const { return desc[off[g] + e]; }
+};
+struct ContiguousBlocks {  // a contiguous store at the position *pos (every block attended)
+    const float *base;  // block b of layer l at base + (l * max_blocks + b) * 2 G D
+    const int *pos;
+    int layer0, max_blocks, G, D;
+    VH_DEV int count(int) const {
+        const int p = *pos;
+        return p < 0 ? 0 : min(p / G + 1, max_blocks);
+    }
+    VH_DEV KvDesc entry(int g, int e) const {
+        const int p = *pos, last = p / G;
+        KvDesc k;
+        k.blk = base + (size_t(layer0 + g) * max_blocks + e) * size_t(2 * G * D);
+        k.ntok = e < last ? G : p % G + 1;
+        k.pad = 0;
+        return k;
+    }
+};
+
+template <int D, int HPG, class Lists>
+__global__ void __launch_bounds__(256) kv_attend_group_kernel(Lists lists, const float *__restrict__ q, int G,
+                                                              float scale, int nchunk, float *__restrict__ part) {
     constexpr int CB = kGroupBlocks, TMAX = CB * 64, QD = D / 4, NDQ = D / 4, NTG = 256 / NDQ;
     __shared__ float4 qs[HPG][D / 4];
     __shared__ float ps[HPG][TMAX];
     __shared__ float hm[HPG], hl[HPG];
     __shared__ float4 red[NTG][HPG][NDQ];
     const int g = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int n = cnt[g], e0 = c * CB, e1 = min(n, e0 + CB);
+    const int n = lists.count(g), e0 = c * CB, e1 = min(n, e0 + CB);
     if (e0 >= n) {  // an empty chunk: its heads' partials are empty
         if (tid < HPG) {
             float *po = part + (size_t(g * HPG + tid) * nchunk + c) * (2 + D);
@@ -270,9 +293,9 @@ __global__ void __launch_bounds__(256) kv_attend_group_kernel(const KvDesc *__re
     }
     for (int i = tid; i < HPG * (D / 4); i += 256)
         qs[i / (D / 4)][i % (D / 4)] = reinterpret_cast<const float4 *>(q + size_t(g) * HPG * D)[i];
-    const KvDesc *dl = desc + off[g];
-    const float *B0 = dl[e0].blk, *B1 = e0 + 1 < e1 ? dl[e0 + 1].blk : B0;
-    const int n0 = dl[e0].ntok, T = n0 + (e0 + 1 < e1 ? dl[e0 + 1].ntok : 0);
+    const KvDesc d0 = lists.entry(g, e0), d1 = e0 + 1 < e1 ? lists.entry(g, e0 + 1) : KvDesc{d0.blk, 0, 0};
+    const float *B0 = d0.blk, *B1 = d1.blk;
+    const int n0 = d0.ntok, T = n0 + d1.ntok;
     auto krow = [&](int t) { return t < n0 ? B0 + size_t(t) * D : B1 + size_t(t - n0) * D; };  // V at + G D
     // the values this thread weighs in the last phase, loaded before the scores
     // are formed (D <= 128: at most 16 float4 per thread)
@@ -377,18 +400,47 @@ __global__ void __launch_bounds__(256) kv_attend_group_kernel(const KvDesc *__re
     }
 }
 
-template <int D>
-int launch_group(int hpg, const KvDesc *desc, const int *off, const int *cnt_kv, const int *cnt_q, const float *q,
-                 int G, float scale, int nchunk, int n_kv, int n_heads, float *part, float *out, hipStream_t s) {
+template <int D, class Lists>
+int launch_group(int hpg, Lists lists, const int *cnt_q, const float *q, int G, float scale, int nchunk, int n_kv,
+                 int n_heads, float *part, float *out, hipStream_t s) {
     const dim3 g(nchunk, n_kv);
     switch (hpg) {
-    case 1: hipLaunchKernelGGL((kv_attend_group_kernel<D, 1>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
-    case 2: hipLaunchKernelGGL((kv_attend_group_kernel<D, 2>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
-    case 4: hipLaunchKernelGGL((kv_attend_group_kernel<D, 4>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
-    default: hipLaunchKernelGGL((kv_attend_group_kernel<D, 8>), g, dim3(256), 0, s, desc, off, cnt_kv, q, G, scale, nchunk, part); break;
+    case 1: hipLaunchKernelGGL((kv_attend_group_kernel<D, 1, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
+    case 2: hipLaunchKernelGGL((kv_attend_group_kernel<D, 2, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
+    case 4: hipLaunchKernelGGL((kv_attend_group_kernel<D, 4, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
+    default: hipLaunchKernelGGL((kv_attend_group_kernel<D, 8, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
     }
     hipLaunchKernelGGL((kv_merge_kernel<D / 64>), dim3(n_heads), dim3(64), 0, s, part, cnt_q, nchunk, kGroupBlocks, out);
     return vh_check(hipGetLastError());
+}
+
+// contiguous stores: k and v rows for layers layer0 .. layer0 + n - 1 at the
+// position *pos (no effect outside [0, max_tokens)), as kv_append_kernel
+__global__ void __launch_bounds__(256) kv_append_pos_kernel(float *__restrict__ base, float *__restrict__ ksum,
+                                                            int layer0, int max_blocks, int max_tokens,
+                                                            const int *__restrict__ pos_p, const float *__restrict__ k,
+                                                            const float *__restrict__ v, int d, int G) {
+    const int pos = *pos_p;
+    if (pos < 0 || pos >= max_tokens) return;
+    const int i = blockIdx.x, b = pos / G, slot = pos % G;
+    const size_t li = size_t(layer0 + i) * max_blocks + b;
+    float *blk = base + li * size_t(2 * G * d);
+    float *ks = ksum + li * size_t(d);
+    const float inv = 1.0f / float(slot + 1);
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+        const float kj = k[size_t(i) * d + j];
+        blk[size_t(slot) * d + j] = kj;
+        blk[size_t(G + slot) * d + j] = v[size_t(i) * d + j];
+        const float old = slot == 0 ? 0.0f : ks[j];  // a new block's mean starts at zero
+        ks[j] = __fadd_rn(old, __fmul_rn(__fsub_rn(kj, old), inv));
+    }
+}
+
+// per-head block counts of a contiguous store at *pos, for the merge
+__global__ void __launch_bounds__(64) kv_count_pos_kernel(const int *__restrict__ pos_p, int G, int max_blocks,
+                                                          int n_heads, int *__restrict__ cnt) {
+    const int p = *pos_p, n = p < 0 ? 0 : min(p / G + 1, max_blocks);
+    for (int h = threadIdx.x; h < n_heads; h += 64) cnt[h] = n;
 }
 
 int blocks_for(int tokens, int g) { return tokens > 0 ? (tokens + g - 1) / g : 0; }
@@ -419,6 +471,14 @@ struct VireoKV {
     float *part = nullptr;
     size_t part_bytes = 0;
     std::vector<float> hscores;
+    // contiguous stores (vireo_kv_create_contiguous): every layer's blocks in
+    // one region, block b of layer l at cbase + (l * max_blocks + b) * 2 G d,
+    // mean keys at cksum + (l * max_blocks + b) * d
+    bool contig = false;
+    int max_blocks = 0;
+    float *cbase = nullptr, *cksum = nullptr;
+    int *cnt_dev = nullptr;  // per-head counts for device-position calls
+    int cnt_heads = 0;
 };
 
 namespace {
@@ -510,6 +570,19 @@ int ensure_resident(VireoKV *S, KvBlock &b, hipStream_t s) {
 // src/kvstore_ooc.c:113-132
 int start_block(VireoKV *S, KvLayer &L, hipStream_t s) {
     const int nb = int(L.blocks.size());
+    if (S->contig) {
+        if (nb >= S->max_blocks) return -ENOSPC;
+        const size_t li = size_t(&L - S->layers.data()) * S->max_blocks + nb;
+        KvBlock b;
+        b.dev = S->cbase + li * size_t(2 * S->G * S->d);
+        b.resident = 1;
+        b.last_used = ++S->tick;
+        L.blocks.push_back(b);
+        S->resident_bytes += S->block_bytes;
+        // the mean key starts at zero (the region is cleared at creation; the
+        // row is cleared again in case a device-position call wrote it)
+        return hipMemsetAsync(S->cksum + li * S->d, 0, size_t(S->d) * sizeof(float), s) == hipSuccess ? 0 : -EIO;
+    }
     if (nb >= L.cap) {
         const int cap = L.cap ? 2 * L.cap : 64;
         float *ks = nullptr;
@@ -734,9 +807,10 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
             const int *dcnt_list = doff + n_lists, *dcnt = doff + n_lists * (grouped ? 2 : 1);
             const float scale = 1.0f / sqrtf(float(d));
             if (!rc && grouped) {
-                if (d == 64) rc = launch_group<64>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
-                else if (d == 128) rc = launch_group<128>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
-                else rc = launch_group<256>(kv_mul, dd, doff, dcnt_list, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                const ListedBlocks lb{dd, doff, dcnt_list};
+                if (d == 64) rc = launch_group<64>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else if (d == 128) rc = launch_group<128>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else rc = launch_group<256>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
             } else if (!rc) {
                 if (d == 64) launch_attend<1>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
                 else if (d == 128) launch_attend<2>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
@@ -792,6 +866,77 @@ extern "C" VireoKV *vireo_kv_create_paged(KVConfig cfg, int strategy, int topk_b
     return create(cfg, strategy, topk_budget);
 }
 
+extern "C" VireoKV *vireo_kv_create_contiguous(KVConfig cfg, int max_tokens) {
+    cfg.capacity_bytes = 0;
+    cfg.sink_tokens = 0;
+    cfg.window_tokens = 0;
+    if (max_tokens < 1) return nullptr;
+    VireoKV *S = create(cfg, VIREO_KV_SELECT_ALL, 0);
+    if (!S) return nullptr;
+    S->dense = true;
+    S->contig = true;
+    S->max_blocks = blocks_for(max_tokens, S->G);
+    const size_t nblk = size_t(cfg.n_layers) * S->max_blocks;
+    if (hipMalloc(reinterpret_cast<void **>(&S->cbase), nblk * S->block_bytes) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void **>(&S->cksum), nblk * S->d * sizeof(float)) != hipSuccess ||
+        hipMemset(S->cksum, 0, nblk * S->d * sizeof(float)) != hipSuccess) {
+        vireo_kv_destroy(S);
+        return nullptr;
+    }
+    for (size_t l = 0; l < S->layers.size(); l++) {
+        S->layers[l].ksum = S->cksum + l * S->max_blocks * S->d;
+        S->layers[l].cap = S->max_blocks;
+    }
+    return S;
+}
+
+extern "C" int vireo_kv_append_pos(VireoKV *S, int layer0, int n, const int32_t *pos, const float *k, const float *v,
+                                   void *stream) {
+    if (!S || !S->contig || !pos || n < 1 || layer0 < 0 || layer0 + n > S->cfg.n_layers || !k || !v) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(kv_append_pos_kernel, dim3(n), dim3(S->d < 256 ? S->d : 256), 0, s, S->cbase, S->cksum, layer0,
+                       S->max_blocks, S->max_blocks * S->G, pos, k, v, S->d, S->G);
+    return vh_finish(s, vh_check(hipGetLastError()));
+}
+
+extern "C" int vireo_kv_attend_gqa_pos(VireoKV *S, int layer0, int n_heads, int n_kv_heads, const int32_t *pos,
+                                       const float *q, float *out, void *stream) {
+    if (!S || !S->contig || !pos || !q || !out || n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads ||
+        layer0 < 0 || layer0 + n_kv_heads > S->cfg.n_layers || (reinterpret_cast<uintptr_t>(q) & 15u))
+        return -EINVAL;
+    const int kv_mul = n_heads / n_kv_heads, d = S->d;
+    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 4 && kv_mul != 8) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int nchunk = (S->max_blocks + kGroupBlocks - 1) / kGroupBlocks;
+    const size_t pb = size_t(n_heads) * nchunk * (2 + d) * sizeof(float);
+    if (pb > S->part_bytes || n_heads > S->cnt_heads) {  // the first call sizes the buffers
+        if (hipStreamSynchronize(s) != hipSuccess) return -EIO;
+        if (pb > S->part_bytes) {
+            if (S->part) (void)hipFree(S->part);
+            S->part = nullptr;
+            S->part_bytes = 0;
+            if (hipMalloc(reinterpret_cast<void **>(&S->part), pb) != hipSuccess) return -ENOMEM;
+            S->part_bytes = pb;
+        }
+        if (n_heads > S->cnt_heads) {
+            if (S->cnt_dev) (void)hipFree(S->cnt_dev);
+            S->cnt_dev = nullptr;
+            S->cnt_heads = 0;
+            if (hipMalloc(reinterpret_cast<void **>(&S->cnt_dev), size_t(n_heads) * sizeof(int)) != hipSuccess)
+                return -ENOMEM;
+            S->cnt_heads = n_heads;
+        }
+    }
+    hipLaunchKernelGGL(kv_count_pos_kernel, dim3(1), dim3(64), 0, s, pos, S->G, S->max_blocks, n_heads, S->cnt_dev);
+    const ContiguousBlocks cb{S->cbase, pos, layer0, S->max_blocks, S->G, d};
+    const float scale = 1.0f / sqrtf(float(d));
+    int rc;
+    if (d == 64) rc = launch_group<64>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    else if (d == 128) rc = launch_group<128>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    else rc = launch_group<256>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    return vh_finish(s, rc);
+}
+
 extern "C" int vireo_kv_append_n(VireoKV *S, int layer0, int n, int pos, const float *k, const float *v,
                                  void *stream) {
     (void)pos;  // tokens are appended in order, as in the reference
@@ -836,8 +981,11 @@ extern "C" void vireo_kv_destroy(VireoKV *S) {
     for (auto &L : S->layers) {
         for (auto &b : L.blocks)
             if (b.host) (void)hipHostFree(b.host);
-        if (L.ksum) (void)hipFree(L.ksum);
+        if (L.ksum && !S->contig) (void)hipFree(L.ksum);
     }
+    if (S->cbase) (void)hipFree(S->cbase);
+    if (S->cksum) (void)hipFree(S->cksum);
+    if (S->cnt_dev) (void)hipFree(S->cnt_dev);
     for (void *p : S->slabs) (void)hipFree(p);
     if (S->dscratch) (void)hipFree(S->dscratch);
     if (S->part) (void)hipFree(S->part);

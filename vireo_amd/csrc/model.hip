@@ -18,11 +18,16 @@ namespace {
 // (rope_neox, src/gguf_run.c:169-174): pair (j, j + hs/2) of every head turns
 // by angle a_j; tab = [cos a_0 .. cos a_{hs/2-1}, sin a_0 ..]. Each product
 // and sum is rounded on its own, as the reference's C (no contraction).
+// The table row is that of position pos_dev ? *pos_dev : pos; a device
+// position outside [0, max_pos) rotates nothing.
 __global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, int nq, float *__restrict__ k, int nk, int hs,
-                                                   const float *__restrict__ tab) {
+                                                   const float *__restrict__ rope, int pos,
+                                                   const int32_t *__restrict__ pos_dev, int max_pos) {
     const int half = hs / 2;
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= (nq + nk) * half) return;
+    if (pos_dev) pos = *pos_dev;
+    if (i >= (nq + nk) * half || pos < 0 || pos >= max_pos) return;
+    const float *tab = rope + size_t(pos) * hs;
     const int h = i / half, j = i % half;
     float *p = h < nq ? q + size_t(h) * hs : k + size_t(h - nq) * hs;
     const float c = tab[j], s = tab[half + j];
@@ -43,6 +48,9 @@ __global__ void __launch_bounds__(256) add_kernel(AddJob j0, AddJob j1, AddJob j
     if (!j.b) return;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < j.n; i += gridDim.x * 256) j.y[i] = __fadd_rn(j.y[i], j.b[i]);
 }
+
+// *pos += 1 (the device position of a captured decode loop)
+__global__ void advance_kernel(int32_t *pos) { *pos += 1; }
 
 // h1_i = silu(h1_i) * h2_i (src/gguf_run.c:246)
 __global__ void __launch_bounds__(256) swiglu_kernel(float *__restrict__ h1, const float *__restrict__ h2, int n) {
@@ -102,18 +110,15 @@ extern "C" int64_t vireo_model_state_bytes(const vireo_model *m) {
     return 4 * (pad64(m->dim) + 2 * pad64(nq) + 2 * pad64(nk) + 2 * pad64(nf));
 }
 
-extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int want_logits,
-                                float *x, float *logits, void *state, void *stream) {
-    if (int rc = check_model(m)) return rc;
-    if (!kv || !token || !x || !state || (want_logits && (!logits || !m->lm_head)) || pos < 0 || pos >= m->max_pos)
-        return -EINVAL;
-    if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+namespace {
+
+// one token through the model at position pos (host) or *pos_dev (device)
+int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32_t *pos_dev, int want_logits,
+               float *x, float *logits, void *state, hipStream_t s) {
     const Bufs b = carve(m, state);
     const int d = m->dim, hs = m->head_size, nh = m->n_heads, nkh = m->n_kv_heads;
     const int nq = nh * hs, nk = nkh * hs;
     const float eps = m->eps;
-    const float *tab = m->rope + size_t(pos) * hs;
     const AddJob none{nullptr, nullptr, 0};
 
     int rc = vireo_embed(m->tok_embd->ggml_type, m->tok_embd->data, d, m->vocab, token, 1, x, s);
@@ -134,11 +139,14 @@ extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *toke
                                     : vireo_rmsnorm(b.k, b.k, B.k_norm, nk, 1, eps, s);
         if (!rc) {
             const int pairs = (nh + nkh) * (hs / 2);
-            hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, b.q, nh, b.k, nkh, hs, tab);
+            hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, b.q, nh, b.k, nkh, hs, m->rope,
+                               pos, pos_dev, m->max_pos);
             rc = vh_check(hipGetLastError());
         }
-        if (!rc) rc = vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
-        if (!rc) rc = vireo_kv_attend_gqa(kv, l * nkh, nh, nkh, b.q, b.att, s);
+        if (!rc) rc = pos_dev ? vireo_kv_append_pos(kv, l * nkh, nkh, pos_dev, b.k, b.v, s)
+                              : vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
+        if (!rc) rc = pos_dev ? vireo_kv_attend_gqa_pos(kv, l * nkh, nh, nkh, pos_dev, b.q, b.att, s)
+                              : vireo_kv_attend_gqa(kv, l * nkh, nh, nkh, b.q, b.att, s);
         if (!rc) rc = qmatvec_async(b.xb, b.att, B.wo, nq, d, s);
         if (!rc) rc = add3(AddJob{x, b.xb, d}, none, none, s);
         // FFN (src/gguf_run.c:238-249)
@@ -162,6 +170,32 @@ extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *toke
         rc = vireo_rmsnorm(b.xb, x, m->out_norm, d, 1, eps, s);
         if (!rc) rc = qmatvec_async(logits, b.xb, m->lm_head, d, m->vocab, s);
         if (!rc) rc = vireo_argmax(logits, m->vocab, token, s);
+    }
+    return rc;
+}
+
+}  // namespace
+
+extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int want_logits,
+                                float *x, float *logits, void *state, void *stream) {
+    if (int rc = check_model(m)) return rc;
+    if (!kv || !token || !x || !state || (want_logits && (!logits || !m->lm_head)) || pos < 0 || pos >= m->max_pos)
+        return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, model_step(m, kv, token, pos, nullptr, want_logits, x, logits, state, s));
+}
+
+extern "C" int vireo_model_step_pos(const vireo_model *m, VireoKV *kv, int32_t *token, int32_t *pos,
+                                    int want_logits, float *x, float *logits, void *state, void *stream) {
+    if (int rc = check_model(m)) return rc;
+    if (!kv || !token || !pos || !x || !state || (want_logits && (!logits || !m->lm_head))) return -EINVAL;
+    if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = model_step(m, kv, token, 0, pos, want_logits, x, logits, state, s);
+    if (!rc) {
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pos);
+        rc = vh_check(hipGetLastError());
     }
     return vh_finish(s, rc);
 }

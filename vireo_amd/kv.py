@@ -24,11 +24,16 @@ class DeviceKV:
     `strategy` (ALL, RECENT, TOPK with topk_budget) over capacity_bytes of HBM."""
 
     def __init__(self, n_layers, kv_dim, block_tokens, sink_tokens=0, window_tokens=0, capacity_bytes=0,
-                 dense=False, strategy=ALL, topk_budget=0):
+                 dense=False, strategy=ALL, topk_budget=0, max_tokens=0):
+        """max_tokens > 0: a contiguous dense store (vireo_kv_create_contiguous)
+        that also takes device positions (append_pos / attend_gqa_pos)."""
         self.lib = _lib.load()
         cfg = _lib.KVConfig(n_layers, kv_dim, block_tokens, sink_tokens, window_tokens, capacity_bytes)
-        self.h = (self.lib.vireo_kv_create_dense(cfg) if dense
-                  else self.lib.vireo_kv_create_paged(cfg, strategy, topk_budget))
+        if max_tokens > 0:
+            self.h = self.lib.vireo_kv_create_contiguous(cfg, max_tokens)
+        else:
+            self.h = (self.lib.vireo_kv_create_dense(cfg) if dense
+                      else self.lib.vireo_kv_create_paged(cfg, strategy, topk_budget))
         if not self.h:
             raise _lib.VireoError("vireo_kv_create failed (check kv_dim in {64, 128, 256}, block_tokens <= 64)")
         self.kv_dim = kv_dim
@@ -38,6 +43,16 @@ class DeviceKV:
         n = 1 if k.dim() == 1 else k.shape[0]
         _lib.check(self.lib.vireo_kv_append_n(self.h, layer, n, pos, _ptr(k), _ptr(v), _stream(stream)),
                    "vireo_kv_append_n")
+
+    def append_pos(self, layer, pos, k, v, stream=None):
+        """append at the device position pos (int32 tensor [1])."""
+        n = 1 if k.dim() == 1 else k.shape[0]
+        _lib.check(self.lib.vireo_kv_append_pos(self.h, layer, n, _ptr(pos), _ptr(k), _ptr(v), _stream(stream)),
+                   "vireo_kv_append_pos")
+
+    def attend_gqa_pos(self, layer0, n_heads, n_kv_heads, pos, q, out, stream=None):
+        _lib.check(self.lib.vireo_kv_attend_gqa_pos(self.h, layer0, n_heads, n_kv_heads, _ptr(pos), _ptr(q), _ptr(out),
+                                                    _stream(stream)), "vireo_kv_attend_gqa_pos")
 
     def attend(self, layer, q, out, stream=None):
         _lib.check(self.lib.vireo_kv_attend(self.h, layer, _ptr(q), _ptr(out), _stream(stream)), "vireo_kv_attend")

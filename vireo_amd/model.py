@@ -22,7 +22,7 @@ class GGUFDecoder:
     the reference runner's default sink and window): step(token, pos) runs
     one forward() and, with want_logits, returns the greedy next token."""
 
-    def __init__(self, path, max_pos=256, expert_capacity=0, block_tokens=32, device="cuda"):
+    def __init__(self, path, max_pos=256, expert_capacity=0, block_tokens=32, device="cuda", contiguous=False):
         import torch
         self.lib = _lib.load()
         p = C.POINTER(_lib.GGUFModelC)()
@@ -36,7 +36,9 @@ class GGUFDecoder:
         self.dim, self.vocab, self.n_layers = m.dim, m.vocab, m.n_layers
         self.n_heads, self.n_kv_heads, self.head_size = m.n_heads, m.n_kv_heads, m.head_size
         self.is_moe = bool(m.moe)
-        self.kv = DeviceKV(self.n_layers * self.n_kv_heads, self.head_size, block_tokens, 32, 256, dense=True)
+        self.kv = DeviceKV(self.n_layers * self.n_kv_heads, self.head_size, block_tokens, 32, 256, dense=True,
+                           max_tokens=max_pos if contiguous else 0)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
         nbytes = self.lib.vireo_model_state_bytes(C.byref(m))
         if nbytes < 0:
             raise _lib.VireoError(f"vireo_model_state_bytes failed: {nbytes}")
@@ -53,6 +55,14 @@ class GGUFDecoder:
                                              _ptr(self.logits) if want_logits else None, _ptr(self.state),
                                              _stream(stream)), "vireo_model_step")
         return int(self.token.item()) if want_logits else None
+
+    def step_pos(self, want_logits=True, stream=None):
+        """vireo_model_step_pos: forward(self.token, self.pos) with both on the
+        device; self.token receives the greedy token, self.pos advances."""
+        _lib.check(self.lib.vireo_model_step_pos(C.byref(self.p.contents.model), C.c_void_p(self.kv.h),
+                                                 _ptr(self.token), _ptr(self.pos), int(want_logits), _ptr(self.x),
+                                                 _ptr(self.logits) if want_logits else None, _ptr(self.state),
+                                                 _stream(stream)), "vireo_model_step_pos")
 
     def close(self):
         if getattr(self, "kv", None):
@@ -77,7 +87,7 @@ class DeviceModel:
     norm weights are unit weights. KV store: dense, block_tokens per block."""
 
     def __init__(self, shape, n_layers, n_heads=32, n_kv_heads=4, head_size=128, vocab=None, max_pos=8192,
-                 seed=1234, attn_types=None, block_tokens=32, rope_base=1000000.0, device="cuda"):
+                 seed=1234, attn_types=None, block_tokens=32, rope_base=1000000.0, device="cuda", contiguous=False):
         import torch
         from . import stack as S
         from . import workloads as W
@@ -118,7 +128,9 @@ class DeviceModel:
         self.model = _lib.Model(n_layers, d, n_heads, n_kv_heads, head_size, 0, vocab, W.EPS, rope_base,
                                 self._blocks, C.pointer(self.stack.moe.model), lm, None, lm,
                                 self.rope.data_ptr(), max_pos)
-        self.kv = DeviceKV(n_layers * n_kv_heads, head_size, block_tokens, 32, 256, dense=True)
+        self.kv = DeviceKV(n_layers * n_kv_heads, head_size, block_tokens, 32, 256, dense=True,
+                           max_tokens=max_pos if contiguous else 0)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
         nbytes = self.lib.vireo_model_state_bytes(C.byref(self.model))
         if nbytes < 0:
             raise _lib.VireoError(f"vireo_model_state_bytes failed: {nbytes}")
@@ -135,6 +147,12 @@ class DeviceModel:
         _lib.check(self.lib.vireo_model_step(C.byref(self.model), C.c_void_p(self.kv.h), _ptr(self.token), pos, 1,
                                              _ptr(self.x), _ptr(self.logits), _ptr(self.state), _stream(stream)),
                    "vireo_model_step")
+
+    def step_pos(self, stream=None):
+        """vireo_model_step_pos at self.pos (device), which advances."""
+        _lib.check(self.lib.vireo_model_step_pos(C.byref(self.model), C.c_void_p(self.kv.h), _ptr(self.token),
+                                                 _ptr(self.pos), 1, _ptr(self.x), _ptr(self.logits), _ptr(self.state),
+                                                 _stream(stream)), "vireo_model_step_pos")
 
     def close(self):
         if getattr(self, "kv", None):
