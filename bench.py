@@ -286,57 +286,72 @@ def cpu_baseline_attn(L, H, KVH, hd, ctx, G, seed, seconds):
 
 def bench_attn(args):
     """Decode attention of a Qwen3-30B-A3B-shaped model over the GPU KV store:
-    a step appends one token's keys and values to every layer's kv heads
-    (vireo_kv_append_n per layer) and attends its query heads over the whole
-    context (vireo_kv_attend_gqa per layer). Algorithmic bytes per step are the
-    keys and values of the context, read once per kv head."""
+    a step appends one token's keys and values to every layer's kv heads and
+    attends its query heads over the whole context. The store is contiguous
+    and the position lives on the device (vireo_kv_append_pos /
+    vireo_kv_attend_gqa_pos), so the K timed steps are one HIP-graph replay.
+    Algorithmic bytes per step are the keys and values of the context, read
+    once per kv head."""
     import torch
     from vireo_amd import _lib
     from vireo_amd import kv as KV
     _lib.check(_lib.load().vireo_hip_init(0), "vireo_hip_init")
     L, H, KVH, hd, ctx, G = ATTN[args.workload]
     K = args.steps or 64
-    Wm = args.warmup if args.warmup is not None else 8
+    Wm = args.warmup if args.warmup is not None else 2
     dev = torch.device("cuda:0")
     print(f"[bench] {args.workload}: filling {ctx} tokens of {L} x {KVH} kv heads", file=sys.stderr, flush=True)
-    kv = KV.DeviceKV(L * KVH, hd, G, dense=True)
+    kv = KV.DeviceKV(L * KVH, hd, G, dense=True, max_tokens=ctx + K)
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     kbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
     vbuf = torch.randn((64, KVH, hd), generator=gen, device=dev)
     s = torch.cuda.current_stream()
-    for t in range(ctx - Wm - K):  # the context before the measured steps
+    p0 = ctx - K // 2  # the timed steps cover positions p0 .. p0 + K - 1 (mean context ctx)
+    for t in range(p0):  # the context before the measured steps
         for l in range(L):
             kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
     q = torch.randn((H, hd), generator=gen, device=dev)
     out = torch.empty((H, hd), device=dev)
+    pos = torch.full((1,), p0, dtype=torch.int32, device=dev)
+    one = torch.ones(1, dtype=torch.int32, device=dev)
 
-    def step(t):
+    def step(st):
         for l in range(L):
-            kv.append(l * KVH, t, kbuf[(t + l) % 64], vbuf[(t + 7 * l) % 64], stream=s)
-            kv.attend_gqa(l * KVH, H, KVH, q, out, stream=s)
-    t = ctx - Wm - K
-    for _ in range(Wm):
-        step(t)
-        t += 1
+            kv.append_pos(l * KVH, pos, kbuf[l % 64], vbuf[(7 * l) % 64], stream=st)
+            kv.attend_gqa_pos(l * KVH, H, KVH, pos, q, out, stream=st)
+        pos.add_(one)
+    for _ in range(Wm):  # uncaptured: the first attention call sizes the store's buffers
+        step(s)
+    torch.cuda.synchronize()
+    gs = torch.cuda.Stream()
+    gs.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gs):
+        for _ in range(K):
+            step(gs)
+    torch.cuda.synchronize()
+    pos.fill_(p0)
+    graph.replay()  # untimed: the same positions as the timed replay
+    torch.cuda.synchronize()
+    pos.fill_(p0)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(K):
-        step(t)
-        t += 1
+    graph.replay()
     e1.record()
     torch.cuda.synchronize()
+    assert int(pos.item()) == p0 + K
     ms = e0.elapsed_time(e1)
     ms_step = ms / K
-    kv_bytes = L * KVH * (ctx - K // 2) * hd * 2 * 4  # the mean context of the timed steps
+    kv_bytes = L * KVH * ctx * hd * 2 * 4  # the mean context of the timed steps
     gbs = kv_bytes / (ms_step / 1e3) / 1e9
     result = {
         "metric": "decode attention tok/s over the GPU KV store (context 4096)", "value": round(K / (ms / 1e3), 2),
         "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm, "ms_per_step": round(ms_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{L}-layer attention, {H} query heads over {KVH} kv heads of {hd}, context {ctx}, "
-                               f"blocks of {G} tokens, dense store",
+                               f"blocks of {G} tokens, contiguous dense store, steps in one HIP graph",
                    "layers": L, "heads": H, "kv_heads": KVH, "head_dim": hd, "context": ctx, "block_tokens": G},
         "us_per_layer": round(ms_step * 1e3 / L, 3), "kv_bytes_per_step": kv_bytes,
         "roofline": {"kernel": "every kernel of a step (append, attention, merge)", "bound": "hbm",
