@@ -44,7 +44,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBM = 128, kBK = 64, kBRows = 256, kThreads = 512, kXcds = 8;
 constexpr int kChunks = kBK / 8;  // 16-byte chunks per row and K step
 #ifndef VH_MFMA_SETS
-#define VH_MFMA_SETS 3
+#define VH_MFMA_SETS 2
 #endif
 // register sets of the staging waves: a step's global loads are issued
 // sets<T>() - 1 K steps before its words are dequantized into LDS (a Q4_K
