@@ -632,11 +632,13 @@ int wide_rpw(int rows, int slots) {
 }
 
 // register sets of rows in flight (a Q6_K row's words are 13 registers per
-// item, Q4_K 8, Q8_0 11)
+// item, Q4_K 8, Q8_0 11): two keep every kernel at 4 waves per SIMD except
+// the Q6_K gate/up (3); the Q6_K down kernel measured 104 -> 78 us at Qwen3
+// B=32 going from 3 sets (3 waves per SIMD) to 2 (4 waves)
 template <int T>
-constexpr int wide_pd_gu() { return T == VT_Q4_K ? 3 : 2; }
+constexpr int wide_pd_gu() { return 2; }
 template <int T>
-constexpr int wide_pd_down() { return T == VT_Q6_K ? 3 : 4; }
+constexpr int wide_pd_down() { return T == VT_Q6_K ? 2 : 4; }
 
 constexpr int kGdecRPW = 2;
 // down rows per lane group and batch: Q6_K's decoder needs more registers
