@@ -192,13 +192,18 @@ __global__ void __launch_bounds__(256) kv_attend_kernel(const KvDesc *__restrict
 // order: lane c takes chunk c's (m, l) for the maximum and the weights
 // e^(m_c - M) (64 chunks at a time), then every lane adds its columns'
 // accumulators over the chunks in order
-template <int DPL>
-__global__ void __launch_bounds__(64) kv_merge_kernel(const float *__restrict__ part, const int *__restrict__ cnt,
-                                                      int nchunk, int cb, float *__restrict__ out) {
+// counts.count(h): the blocks query head h attended
+struct HeadCounts {
+    const int *cnt;
+    VH_DEV int count(int h) const { return cnt[h]; }
+};
+template <int DPL, class Counts>
+__global__ void __launch_bounds__(64) kv_merge_kernel(const float *__restrict__ part, Counts counts, int nchunk, int cb,
+                                                      float *__restrict__ out) {
     constexpr int D = 64 * DPL;
     __shared__ float fs[64];
     const int h = blockIdx.x, lane = threadIdx.x;
-    const int nc = (cnt[h] + cb - 1) / cb;
+    const int nc = (counts.count(h) + cb - 1) / cb;
     const float *p = part + size_t(h) * nchunk * (2 + D);
     float M = -INFINITY;
     for (int c = lane; c < nc; c += 64) M = fmaxf(M, p[size_t(c) * (2 + D)]);
@@ -271,6 +276,15 @@ struct ContiguousBlocks {  // a contiguous store at the position *pos (every blo
         k.pad = 0;
         return k;
     }
+};
+
+// a query head's count is its kv head's list's (the heads of a group attend
+// the same blocks)
+template <class Lists>
+struct GroupCounts {
+    Lists lists;
+    int hpg;
+    VH_DEV int count(int h) const { return lists.count(h / hpg); }
 };
 
 template <int D, int HPG, class Lists>
@@ -401,8 +415,8 @@ __global__ void __launch_bounds__(256) kv_attend_group_kernel(Lists lists, const
 }
 
 template <int D, class Lists>
-int launch_group(int hpg, Lists lists, const int *cnt_q, const float *q, int G, float scale, int nchunk, int n_kv,
-                 int n_heads, float *part, float *out, hipStream_t s) {
+int launch_group(int hpg, Lists lists, const float *q, int G, float scale, int nchunk, int n_kv, int n_heads,
+                 float *part, float *out, hipStream_t s) {
     const dim3 g(nchunk, n_kv);
     switch (hpg) {
     case 1: hipLaunchKernelGGL((kv_attend_group_kernel<D, 1, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
@@ -410,7 +424,8 @@ int launch_group(int hpg, Lists lists, const int *cnt_q, const float *q, int G, 
     case 4: hipLaunchKernelGGL((kv_attend_group_kernel<D, 4, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
     default: hipLaunchKernelGGL((kv_attend_group_kernel<D, 8, Lists>), g, dim3(256), 0, s, lists, q, G, scale, nchunk, part); break;
     }
-    hipLaunchKernelGGL((kv_merge_kernel<D / 64>), dim3(n_heads), dim3(64), 0, s, part, cnt_q, nchunk, kGroupBlocks, out);
+    hipLaunchKernelGGL((kv_merge_kernel<D / 64, GroupCounts<Lists>>), dim3(n_heads), dim3(64), 0, s, part,
+                       GroupCounts<Lists>{lists, hpg}, nchunk, kGroupBlocks, out);
     return vh_check(hipGetLastError());
 }
 
@@ -434,13 +449,6 @@ __global__ void __launch_bounds__(256) kv_append_pos_kernel(float *__restrict__ 
         const float old = slot == 0 ? 0.0f : ks[j];  // a new block's mean starts at zero
         ks[j] = __fadd_rn(old, __fmul_rn(__fsub_rn(kj, old), inv));
     }
-}
-
-// per-head block counts of a contiguous store at *pos, for the merge
-__global__ void __launch_bounds__(64) kv_count_pos_kernel(const int *__restrict__ pos_p, int G, int max_blocks,
-                                                          int n_heads, int *__restrict__ cnt) {
-    const int p = *pos_p, n = p < 0 ? 0 : min(p / G + 1, max_blocks);
-    for (int h = threadIdx.x; h < n_heads; h += 64) cnt[h] = n;
 }
 
 int blocks_for(int tokens, int g) { return tokens > 0 ? (tokens + g - 1) / g : 0; }
@@ -477,8 +485,6 @@ struct VireoKV {
     bool contig = false;
     int max_blocks = 0;
     float *cbase = nullptr, *cksum = nullptr;
-    int *cnt_dev = nullptr;  // per-head counts for device-position calls
-    int cnt_heads = 0;
 };
 
 namespace {
@@ -687,7 +693,8 @@ void launch_attend(const KvDesc *desc, const int *off, const int *cnt, const flo
                    int nchunk, int heads, float *part, float *out, hipStream_t s) {
     hipLaunchKernelGGL((kv_attend_kernel<DPL>), dim3(nchunk, heads), dim3(256), 0, s, desc, off, cnt, q, G, scale,
                        nchunk, part);
-    hipLaunchKernelGGL((kv_merge_kernel<DPL>), dim3(heads), dim3(64), 0, s, part, cnt, nchunk, kChunkBlocks, out);
+    hipLaunchKernelGGL((kv_merge_kernel<DPL, HeadCounts>), dim3(heads), dim3(64), 0, s, part, HeadCounts{cnt}, nchunk,
+                       kChunkBlocks, out);
 }
 
 // heads h < n_heads attend layer layer0 + h / kv_mul with q_h
@@ -808,9 +815,9 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
             const float scale = 1.0f / sqrtf(float(d));
             if (!rc && grouped) {
                 const ListedBlocks lb{dd, doff, dcnt_list};
-                if (d == 64) rc = launch_group<64>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
-                else if (d == 128) rc = launch_group<128>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
-                else rc = launch_group<256>(kv_mul, lb, dcnt, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                if (d == 64) rc = launch_group<64>(kv_mul, lb, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else if (d == 128) rc = launch_group<128>(kv_mul, lb, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
+                else rc = launch_group<256>(kv_mul, lb, q, S->G, scale, nchunk, n_lists, n_heads, S->part, out, s);
             } else if (!rc) {
                 if (d == 64) launch_attend<1>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
                 else if (d == 128) launch_attend<2>(dd, doff, dcnt, q, S->G, scale, nchunk, n_heads, S->part, out, s);
@@ -909,31 +916,20 @@ extern "C" int vireo_kv_attend_gqa_pos(VireoKV *S, int layer0, int n_heads, int 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int nchunk = (S->max_blocks + kGroupBlocks - 1) / kGroupBlocks;
     const size_t pb = size_t(n_heads) * nchunk * (2 + d) * sizeof(float);
-    if (pb > S->part_bytes || n_heads > S->cnt_heads) {  // the first call sizes the buffers
+    if (pb > S->part_bytes) {  // the first call sizes the partials
         if (hipStreamSynchronize(s) != hipSuccess) return -EIO;
-        if (pb > S->part_bytes) {
-            if (S->part) (void)hipFree(S->part);
-            S->part = nullptr;
-            S->part_bytes = 0;
-            if (hipMalloc(reinterpret_cast<void **>(&S->part), pb) != hipSuccess) return -ENOMEM;
-            S->part_bytes = pb;
-        }
-        if (n_heads > S->cnt_heads) {
-            if (S->cnt_dev) (void)hipFree(S->cnt_dev);
-            S->cnt_dev = nullptr;
-            S->cnt_heads = 0;
-            if (hipMalloc(reinterpret_cast<void **>(&S->cnt_dev), size_t(n_heads) * sizeof(int)) != hipSuccess)
-                return -ENOMEM;
-            S->cnt_heads = n_heads;
-        }
+        if (S->part) (void)hipFree(S->part);
+        S->part = nullptr;
+        S->part_bytes = 0;
+        if (hipMalloc(reinterpret_cast<void **>(&S->part), pb) != hipSuccess) return -ENOMEM;
+        S->part_bytes = pb;
     }
-    hipLaunchKernelGGL(kv_count_pos_kernel, dim3(1), dim3(64), 0, s, pos, S->G, S->max_blocks, n_heads, S->cnt_dev);
     const ContiguousBlocks cb{S->cbase, pos, layer0, S->max_blocks, S->G, d};
     const float scale = 1.0f / sqrtf(float(d));
     int rc;
-    if (d == 64) rc = launch_group<64>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
-    else if (d == 128) rc = launch_group<128>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
-    else rc = launch_group<256>(kv_mul, cb, S->cnt_dev, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    if (d == 64) rc = launch_group<64>(kv_mul, cb, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    else if (d == 128) rc = launch_group<128>(kv_mul, cb, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
+    else rc = launch_group<256>(kv_mul, cb, q, S->G, scale, nchunk, n_kv_heads, n_heads, S->part, out, s);
     return vh_finish(s, rc);
 }
 
@@ -985,7 +981,6 @@ extern "C" void vireo_kv_destroy(VireoKV *S) {
     }
     if (S->cbase) (void)hipFree(S->cbase);
     if (S->cksum) (void)hipFree(S->cksum);
-    if (S->cnt_dev) (void)hipFree(S->cnt_dev);
     for (void *p : S->slabs) (void)hipFree(p);
     if (S->dscratch) (void)hipFree(S->dscratch);
     if (S->part) (void)hipFree(S->part);

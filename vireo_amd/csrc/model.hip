@@ -4,8 +4,10 @@
 // NEOX RoPE -> KV append -> grouped-query attention over the KV store ->
 // output projection -> residual -> RMSNorm -> MoE layer or dense SwiGLU FFN
 // -> residual, then the output norm, LM head and argmax. The matvecs are
-// qmatvec, the attention is the KV store's kernel, the MoE layer is the decode
-// plan of moe_ffn_forward; this file adds the small element-wise kernels.
+// qmatvec (the output and down projections add into the residual stream
+// themselves), the attention is the KV store's kernel, the MoE layer is the
+// decode plan of moe_ffn_forward; this file adds the small element-wise
+// kernels (biases, per-head QK-norms and RoPE in one launch).
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "vireo_hip.h"
@@ -34,6 +36,70 @@ __global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, int nq
     const float x0 = p[j], x1 = p[j + half];
     p[j] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     p[j + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+// The attention inputs of one token in one launch: workgroup h (one wave)
+// takes query head h, then the key heads, then the value heads (value heads
+// only when they have a bias). A head gets its bias (as add_kernel), its
+// RMSNorm over the head (as rmsnorm_kernel over a row of hs <= 256 values:
+// lane l squares values l + 64 c, each group c of 64 is summed by one wave
+// reduction and the groups' sums are added as ((s0 + s1) + (s2 + s3)), so
+// the result is that kernel's bit for bit) and then, for queries and keys,
+// the rotation of rope_kernel. hs is a multiple of 64.
+struct HeadJob {
+    float *p;           // heads x hs values, updated in place
+    const float *bias;  // heads x hs values, or null
+    const float *norm;  // hs RMSNorm weights shared by the heads, or null: no norm
+    int heads;
+};
+__global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k, HeadJob v, int hs, float eps,
+                                                           const float *__restrict__ rope, int pos,
+                                                           const int32_t *__restrict__ pos_dev, int max_pos) {
+    __shared__ float row[256];
+    int h = blockIdx.x;
+    bool rotate = true;
+    HeadJob j = q;
+    if (h >= q.heads) {
+        h -= q.heads, j = k;
+        if (h >= k.heads) h -= k.heads, j = v, rotate = false;
+    }
+    const int l = threadIdx.x, ng = hs >> 6;
+    float *p = j.p + size_t(h) * hs;
+    float val[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        if (c < ng) {
+            val[c] = p[64 * c + l];
+            if (j.bias) val[c] = __fadd_rn(val[c], j.bias[size_t(h) * hs + 64 * c + l]);
+        }
+    if (j.norm) {
+        double part[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) part[c] = c < ng ? wave_sum_d(double(__fmul_rn(val[c], val[c]))) : 0.0;
+        const float ss = float((part[0] + part[1]) + (part[2] + part[3]));
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(hs)), eps)));
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if (c < ng) val[c] = __fmul_rn(__fmul_rn(val[c], r), j.norm[64 * c + l]);
+    }
+    if (rotate && pos_dev) pos = *pos_dev;
+    if (rotate && pos >= 0 && pos < max_pos) {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if (c < ng) row[64 * c + l] = val[c];
+        __syncthreads();
+        const int half = hs / 2;
+        const float *tab = rope + size_t(pos) * hs;
+        for (int i = l; i < half; i += 64) {
+            const float cs = tab[i], sn = tab[half + i], x0 = row[i], x1 = row[i + half];
+            p[i] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+            p[i + half] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+        }
+        return;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        if (c < ng) p[64 * c + l] = val[c];
 }
 
 // y_i += b_i for up to three (y, b, n) vectors (add_bias, src/gguf_run.c:166,
@@ -119,7 +185,6 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
     const int d = m->dim, hs = m->head_size, nh = m->n_heads, nkh = m->n_kv_heads;
     const int nq = nh * hs, nk = nkh * hs;
     const float eps = m->eps;
-    const AddJob none{nullptr, nullptr, 0};
 
     int rc = vireo_embed(m->tok_embd->ggml_type, m->tok_embd->data, d, m->vocab, token, 1, x, s);
     for (int l = 0; l < m->n_layers && !rc; l++) {
@@ -129,26 +194,36 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
         if (!rc) rc = qmatvec_async(b.q, b.xb, B.wq, d, nq, s);
         if (!rc) rc = qmatvec_async(b.k, b.xb, B.wk, d, nk, s);
         if (!rc) rc = qmatvec_async(b.v, b.xb, B.wv, d, nk, s);
-        if (!rc && (B.bq || B.bk || B.bv))
-            rc = add3(AddJob{b.q, B.bq, nq}, AddJob{b.k, B.bk, nk}, AddJob{b.v, B.bv, nk}, s);
-        if (!rc && B.q_norm)
-            rc = B.q_norm_len == hs ? vireo_rmsnorm(b.q, b.q, B.q_norm, hs, nh, eps, s)
-                                    : vireo_rmsnorm(b.q, b.q, B.q_norm, nq, 1, eps, s);
-        if (!rc && B.k_norm)
-            rc = B.k_norm_len == hs ? vireo_rmsnorm(b.k, b.k, B.k_norm, hs, nkh, eps, s)
-                                    : vireo_rmsnorm(b.k, b.k, B.k_norm, nk, 1, eps, s);
-        if (!rc) {
-            const int pairs = (nh + nkh) * (hs / 2);
-            hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, b.q, nh, b.k, nkh, hs, m->rope,
+        if (!rc && hs % 64 == 0 && hs <= 256 && (!B.q_norm || B.q_norm_len == hs) &&
+            (!B.k_norm || B.k_norm_len == hs)) {
+            // per-head QK-norms (or none): biases, norms and RoPE in one launch
+            const unsigned heads = unsigned(nh + nkh + (B.bv ? nkh : 0));
+            hipLaunchKernelGGL(head_prologue_kernel, dim3(heads), dim3(64), 0, s, HeadJob{b.q, B.bq, B.q_norm, nh},
+                               HeadJob{b.k, B.bk, B.k_norm, nkh}, HeadJob{b.v, B.bv, nullptr, nkh}, hs, eps, m->rope,
                                pos, pos_dev, m->max_pos);
             rc = vh_check(hipGetLastError());
+        } else if (!rc) {
+            // a norm over the whole q or k vector: separate launches
+            if (B.bq || B.bk || B.bv)
+                rc = add3(AddJob{b.q, B.bq, nq}, AddJob{b.k, B.bk, nk}, AddJob{b.v, B.bv, nk}, s);
+            if (!rc && B.q_norm)
+                rc = B.q_norm_len == hs ? vireo_rmsnorm(b.q, b.q, B.q_norm, hs, nh, eps, s)
+                                        : vireo_rmsnorm(b.q, b.q, B.q_norm, nq, 1, eps, s);
+            if (!rc && B.k_norm)
+                rc = B.k_norm_len == hs ? vireo_rmsnorm(b.k, b.k, B.k_norm, hs, nkh, eps, s)
+                                        : vireo_rmsnorm(b.k, b.k, B.k_norm, nk, 1, eps, s);
+            if (!rc) {
+                const int pairs = (nh + nkh) * (hs / 2);
+                hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, b.q, nh, b.k, nkh, hs,
+                                   m->rope, pos, pos_dev, m->max_pos);
+                rc = vh_check(hipGetLastError());
+            }
         }
         if (!rc) rc = pos_dev ? vireo_kv_append_pos(kv, l * nkh, nkh, pos_dev, b.k, b.v, s)
                               : vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
         if (!rc) rc = pos_dev ? vireo_kv_attend_gqa_pos(kv, l * nkh, nh, nkh, pos_dev, b.q, b.att, s)
                               : vireo_kv_attend_gqa(kv, l * nkh, nh, nkh, b.q, b.att, s);
-        if (!rc) rc = qmatvec_async(b.xb, b.att, B.wo, nq, d, s);
-        if (!rc) rc = add3(AddJob{x, b.xb, d}, none, none, s);
+        if (!rc) rc = vh_qmatvec_acc(x, b.att, B.wo, nq, d, s);  // x += wo att
         // FFN (src/gguf_run.c:238-249)
         if (rc) break;
         if (m->moe) {
@@ -162,8 +237,7 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
                 hipLaunchKernelGGL(swiglu_kernel, dim3((f + 255) / 256), dim3(256), 0, s, b.h1, b.h2, f);
                 rc = vh_check(hipGetLastError());
             }
-            if (!rc) rc = qmatvec_async(b.xb, b.h1, B.wd, f, d, s);
-            if (!rc) rc = add3(AddJob{x, b.xb, d}, none, none, s);
+            if (!rc) rc = vh_qmatvec_acc(x, b.h1, B.wd, f, d, s);  // x += wd h
         }
     }
     if (want_logits && !rc) {  // src/gguf_run.c:251-252, argmax :254

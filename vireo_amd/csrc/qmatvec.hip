@@ -5,17 +5,21 @@
 // the GGUF bytes with aligned loads, and the L partial sums are folded with a
 // shuffle tree. Rows are streamed once; the kernel is HBM-bound. Matrices with
 // many rows of 32..128 items (the LM head) take qmatvec_reg_kernel, which
-// keeps each lane's inputs in registers across rows.
+// keeps each lane's inputs in registers across rows. With `accumulate` the
+// kernels add their result to y (y_r + sum, one rounding, as a separate
+// residual add of the stored result would give).
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
+#include "route_kernels.h"
 #include "vireo_hip.h"
 
 namespace {
 
 template <int T, bool PAIRED, int L>
 __global__ void __launch_bounds__(256) qmatvec_kernel(float *__restrict__ y, const float *__restrict__ x,
-                                                      const uint8_t *__restrict__ w, int n, int d, int64_t row_bytes) {
+                                                      const uint8_t *__restrict__ w, int n, int d, int64_t row_bytes,
+                                                      int accumulate) {
     using F = Fmt<T, PAIRED>;
     constexpr int RPW = 64 / L;
     const int lane = threadIdx.x & 63, sub = lane / L, li = lane % L;
@@ -30,12 +34,12 @@ __global__ void __launch_bounds__(256) qmatvec_kernel(float *__restrict__ y, con
             for (int it = li; it < items; it += L) acc += F::dot(w, ro, it, n, x);
         }
         acc = group_sum<L>(acc);
-        if (li == L - 1 && row < d) y[row] = acc;
+        if (li == L - 1 && row < d) y[row] = accumulate ? __fadd_rn(y[row], acc) : acc;
     }
 }
 
 template <int T, bool PAIRED>
-int launch_L(int L, float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, hipStream_t s) {
+int launch_L(int L, float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, int acc, hipStream_t s) {
     const int rpw = 64 / L;
     int64_t waves = (int64_t(d) + rpw - 1) / rpw;
     int64_t blocks = (waves + 3) / 4;
@@ -44,13 +48,13 @@ int launch_L(int L, float *y, const float *x, const uint8_t *w, int n, int d, in
     if (blocks < 1) blocks = 1;
     dim3 g(static_cast<unsigned>(blocks)), b(256);
     switch (L) {
-    case 64: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 64>), g, b, 0, s, y, x, w, n, d, rb); break;
-    case 32: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 32>), g, b, 0, s, y, x, w, n, d, rb); break;
-    case 16: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 16>), g, b, 0, s, y, x, w, n, d, rb); break;
-    case 8: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 8>), g, b, 0, s, y, x, w, n, d, rb); break;
-    case 4: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 4>), g, b, 0, s, y, x, w, n, d, rb); break;
-    case 2: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 2>), g, b, 0, s, y, x, w, n, d, rb); break;
-    default: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 1>), g, b, 0, s, y, x, w, n, d, rb); break;
+    case 64: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 64>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    case 32: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 32>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    case 16: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 16>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    case 8: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 8>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    case 4: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 4>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    case 2: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 2>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
+    default: hipLaunchKernelGGL((qmatvec_kernel<T, PAIRED, 1>), g, b, 0, s, y, x, w, n, d, rb, acc); break;
     }
     return vh_check(hipGetLastError());
 }
@@ -74,7 +78,7 @@ int pick_lanes(int items) {
 template <int T, int IPL, int RB>
 __global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y, const float *__restrict__ x,
                                                           const uint8_t *__restrict__ w, int n, int d,
-                                                          int64_t row_bytes) {
+                                                          int64_t row_bytes, int accumulate) {
     using F = Reg<T>;
     constexpr int NS = F::NS;
     const int lane = threadIdx.x & 63;
@@ -109,24 +113,32 @@ __global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y,
                 if (it < items) acc += F::compute(raw[rr][m], it, xr[m], xs[m]);
             }
             acc = group_sum<64>(acc);
-            if (lane == 63 && r0 + rr < d) y[r0 + rr] = acc;
+            if (lane == 63 && r0 + rr < d) y[r0 + rr] = accumulate ? __fadd_rn(y[r0 + rr], acc) : acc;
         }
     }
 }
 
-template <int T>
-int launch_reg(float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, hipStream_t s) {
-    constexpr int RB = 8;
+template <int T, int RB>
+int launch_reg_rb(float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, int acc, hipStream_t s) {
     const int items = n / 32;
     int64_t blocks = (int64_t(d) + 4 * RB - 1) / (4 * RB);
     const int64_t cap = int64_t(vh_num_cus()) * 8;
     if (blocks > cap) blocks = cap;
     dim3 g(static_cast<unsigned>(blocks)), b(256);
     if (items <= 64)
-        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 1, RB>), g, b, 0, s, y, x, w, n, d, rb);
+        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 1, RB>), g, b, 0, s, y, x, w, n, d, rb, acc);
     else
-        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 2, RB>), g, b, 0, s, y, x, w, n, d, rb);
+        hipLaunchKernelGGL((qmatvec_reg_kernel<T, 2, RB>), g, b, 0, s, y, x, w, n, d, rb, acc);
     return vh_check(hipGetLastError());
+}
+
+// 8 rows per wave in flight, or 2 below 8192 rows, where 8 would leave too
+// few workgroups to fill the chip (4096 Q4_K rows of 2048: 6.1 us at 8,
+// 4.1 us at 2, 4.7 us at 1; 8192 Q8_0 rows: 5.9 us at 8, 7.2 us at 2)
+template <int T>
+int launch_reg(float *y, const float *x, const uint8_t *w, int n, int d, int64_t rb, int acc, hipStream_t s) {
+    if (d >= 8192) return launch_reg_rb<T, 8>(y, x, w, n, d, rb, acc, s);
+    return launch_reg_rb<T, 2>(y, x, w, n, d, rb, acc, s);
 }
 
 // the register-input kernel applies to Q8_0 / Q4_K / Q6_K rows of 32..128
@@ -210,7 +222,9 @@ static int check_weights(uint32_t type, const void *data, int n, int d, int64_t 
     return 0;
 }
 
-extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int n, int d, void *stream) {
+namespace {
+
+int qmv(float *y, const float *x, const gguf_tensor *w, int n, int d, int acc, void *stream) {
     if (!w || (!y && d) || (!x && d)) return -EINVAL;
     int64_t rb;
     if (int rc = check_weights(w->ggml_type, w->data, n, d, &rb)) return rc;
@@ -219,22 +233,32 @@ extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int
     const uint8_t *wd = static_cast<const uint8_t *>(w->data);
     if (reg_path(w->ggml_type, x, n, d)) {
         switch (w->ggml_type) {
-        case VT_Q8_0: return launch_reg<VT_Q8_0>(y, x, wd, n, d, rb, s);
-        case VT_Q4_K: return launch_reg<VT_Q4_K>(y, x, wd, n, d, rb, s);
-        default: return launch_reg<VT_Q6_K>(y, x, wd, n, d, rb, s);
+        case VT_Q8_0: return launch_reg<VT_Q8_0>(y, x, wd, n, d, rb, acc, s);
+        case VT_Q4_K: return launch_reg<VT_Q4_K>(y, x, wd, n, d, rb, acc, s);
+        default: return launch_reg<VT_Q6_K>(y, x, wd, n, d, rb, acc, s);
         }
     }
     switch (w->ggml_type) {
     case VT_Q8_0:
-        if (n % 64 == 0) return launch_L<VT_Q8_0, true>(pick_lanes(n / 64), y, x, wd, n, d, rb, s);
-        return launch_L<VT_Q8_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
-    case VT_Q4_K: return launch_L<VT_Q4_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
-    case VT_Q6_K: return launch_L<VT_Q6_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
-    case VT_Q5_0: return launch_L<VT_Q5_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, s);
-    case VT_F16: return launch_L<VT_F16, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, s);
-    case VT_F32: return launch_L<VT_F32, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, s);
+        if (n % 64 == 0) return launch_L<VT_Q8_0, true>(pick_lanes(n / 64), y, x, wd, n, d, rb, acc, s);
+        return launch_L<VT_Q8_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, acc, s);
+    case VT_Q4_K: return launch_L<VT_Q4_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, acc, s);
+    case VT_Q6_K: return launch_L<VT_Q6_K, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, acc, s);
+    case VT_Q5_0: return launch_L<VT_Q5_0, false>(pick_lanes(n / 32), y, x, wd, n, d, rb, acc, s);
+    case VT_F16: return launch_L<VT_F16, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, acc, s);
+    case VT_F32: return launch_L<VT_F32, false>(pick_lanes((n + 31) / 32), y, x, wd, n, d, rb, acc, s);
     default: return -EINVAL;
     }
+}
+
+}  // namespace
+
+extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int n, int d, void *stream) {
+    return qmv(y, x, w, n, d, 0, stream);
+}
+
+int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s) {
+    return qmv(y, x, w, n, d, 1, s);
 }
 
 extern "C" int qmatvec(float *y, const float *x, const gguf_tensor *w, int n, int d) {

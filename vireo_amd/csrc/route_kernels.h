@@ -23,6 +23,8 @@ extern "C" uint64_t vh_store_capacity(const ExpertStore *s);
 
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
                         hipStream_t s);
+// y += W x (qmatvec_async with each result added to y[r], one rounding)
+int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
