@@ -35,6 +35,7 @@
 #include <vector>
 #include "common.h"
 #include "vireo_kv.h"
+#include "kv_view.h"
 
 namespace {
 
@@ -895,6 +896,12 @@ extern "C" VireoKV *vireo_kv_create_contiguous(KVConfig cfg, int max_tokens) {
         S->layers[l].cap = S->max_blocks;
     }
     return S;
+}
+
+int vh_kv_contig_view(const VireoKV *S, KvContigView *v) {
+    if (!S || !S->contig || !v) return -EINVAL;
+    *v = KvContigView{S->cbase, S->cksum, S->cfg.n_layers, S->max_blocks, S->G, S->d};
+    return 0;
 }
 
 extern "C" int vireo_kv_append_pos(VireoKV *S, int layer0, int n, const int32_t *pos, const float *k, const float *v,

@@ -13,6 +13,7 @@
 #include "vireo_hip.h"
 #include "route_kernels.h"
 #include "vireo_kv.h"
+#include "kv_view.h"
 
 namespace {
 
@@ -45,7 +46,10 @@ __global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, int nq
 // lane l squares values l + 64 c, each group c of 64 is summed by one wave
 // reduction and the groups' sums are added as ((s0 + s1) + (s2 + s3)), so
 // the result is that kernel's bit for bit) and then, for queries and keys,
-// the rotation of rope_kernel. hs is a multiple of 64.
+// the rotation of rope_kernel. hs is a multiple of 64. With a contiguous
+// store (kv.base) the key and value heads are also appended at the position,
+// as kv_append_pos_kernel appends them (kv head h to store layer layer0 + h;
+// nothing outside [0, max_blocks G)).
 struct HeadJob {
     float *p;           // heads x hs values, updated in place
     const float *bias;  // heads x hs values, or null
@@ -54,17 +58,42 @@ struct HeadJob {
 };
 __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k, HeadJob v, int hs, float eps,
                                                            const float *__restrict__ rope, int pos,
-                                                           const int32_t *__restrict__ pos_dev, int max_pos) {
+                                                           const int32_t *__restrict__ pos_dev, int max_pos,
+                                                           KvContigView kv, int layer0) {
     __shared__ float row[256];
-    int h = blockIdx.x;
-    bool rotate = true;
+    int h = blockIdx.x, kind = 0;  // 0 query, 1 key, 2 value
     HeadJob j = q;
     if (h >= q.heads) {
-        h -= q.heads, j = k;
-        if (h >= k.heads) h -= k.heads, j = v, rotate = false;
+        h -= q.heads, j = k, kind = 1;
+        if (h >= k.heads) h -= k.heads, j = v, kind = 2;
+    }
+    if (pos_dev) pos = *pos_dev;
+    const bool rotate = kind < 2;
+    // the store's row for this key / value head, and the key's mean row
+    float *srow = nullptr, *ks = nullptr;
+    float inv = 0.0f;
+    int slot = 0;
+    if (kv.base && kind > 0 && pos >= 0 && pos < kv.max_blocks * kv.G) {
+        const int b = pos / kv.G;
+        slot = pos % kv.G;
+        const size_t li = size_t(layer0 + h) * kv.max_blocks + b;
+        srow = kv.base + li * size_t(2 * kv.G * hs) + size_t(kind == 1 ? slot : kv.G + slot) * hs;
+        if (kind == 1) ks = kv.ksum + li * size_t(hs);
+        inv = 1.0f / float(slot + 1);
     }
     const int l = threadIdx.x, ng = hs >> 6;
     float *p = j.p + size_t(h) * hs;
+    // the head's final value at index i: to its buffer, and to the store
+    auto emit = [&](int i, float x) {
+        p[i] = x;
+        if (srow) {
+            srow[i] = x;
+            if (ks) {
+                const float old = slot == 0 ? 0.0f : ks[i];  // a new block's mean starts at zero
+                ks[i] = __fadd_rn(old, __fmul_rn(__fsub_rn(x, old), inv));
+            }
+        }
+    };
     float val[4];
 #pragma unroll
     for (int c = 0; c < 4; c++)
@@ -82,7 +111,6 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         for (int c = 0; c < 4; c++)
             if (c < ng) val[c] = __fmul_rn(__fmul_rn(val[c], r), j.norm[64 * c + l]);
     }
-    if (rotate && pos_dev) pos = *pos_dev;
     if (rotate && pos >= 0 && pos < max_pos) {
 #pragma unroll
         for (int c = 0; c < 4; c++)
@@ -92,14 +120,14 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         const float *tab = rope + size_t(pos) * hs;
         for (int i = l; i < half; i += 64) {
             const float cs = tab[i], sn = tab[half + i], x0 = row[i], x1 = row[i + half];
-            p[i] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-            p[i + half] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+            emit(i, __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
+            emit(i + half, __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)));
         }
         return;
     }
 #pragma unroll
     for (int c = 0; c < 4; c++)
-        if (c < ng) p[64 * c + l] = val[c];
+        if (c < ng) emit(64 * c + l, val[c]);
 }
 
 // y_i += b_i for up to three (y, b, n) vectors (add_bias, src/gguf_run.c:166,
@@ -186,21 +214,34 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
     const int nq = nh * hs, nk = nkh * hs;
     const float eps = m->eps;
 
+    // a contiguous store with rows of the head size takes the device-position
+    // appends inside head_prologue_kernel
+    KvContigView view{};
+    const bool append_in_place = pos_dev && vh_kv_contig_view(kv, &view) == 0 && view.d == hs;
+
     int rc = vireo_embed(m->tok_embd->ggml_type, m->tok_embd->data, d, m->vocab, token, 1, x, s);
     for (int l = 0; l < m->n_layers && !rc; l++) {
         const vireo_block &B = m->blocks[l];
+        bool appended = false;
         // attention (src/gguf_run.c:221-237)
         rc = vireo_rmsnorm(b.xb, x, B.attn_norm, d, 1, eps, s);
-        if (!rc) rc = qmatvec_async(b.q, b.xb, B.wq, d, nq, s);
-        if (!rc) rc = qmatvec_async(b.k, b.xb, B.wk, d, nk, s);
-        if (!rc) rc = qmatvec_async(b.v, b.xb, B.wv, d, nk, s);
+        if (!rc) {  // q, k and v in one launch where the types allow
+            rc = vh_qmatvec3(b.xb, d, b.q, B.wq, nq, b.k, B.wk, nk, b.v, B.wv, nk, s);
+            if (rc == -ENOTSUP) {
+                rc = qmatvec_async(b.q, b.xb, B.wq, d, nq, s);
+                if (!rc) rc = qmatvec_async(b.k, b.xb, B.wk, d, nk, s);
+                if (!rc) rc = qmatvec_async(b.v, b.xb, B.wv, d, nk, s);
+            }
+        }
         if (!rc && hs % 64 == 0 && hs <= 256 && (!B.q_norm || B.q_norm_len == hs) &&
             (!B.k_norm || B.k_norm_len == hs)) {
-            // per-head QK-norms (or none): biases, norms and RoPE in one launch
-            const unsigned heads = unsigned(nh + nkh + (B.bv ? nkh : 0));
+            // per-head QK-norms (or none): biases, norms and RoPE in one launch,
+            // which also appends to a contiguous store at a device position
+            appended = append_in_place && (l + 1) * nkh <= view.layers;
+            const unsigned heads = unsigned(nh + nkh + (B.bv || appended ? nkh : 0));
             hipLaunchKernelGGL(head_prologue_kernel, dim3(heads), dim3(64), 0, s, HeadJob{b.q, B.bq, B.q_norm, nh},
                                HeadJob{b.k, B.bk, B.k_norm, nkh}, HeadJob{b.v, B.bv, nullptr, nkh}, hs, eps, m->rope,
-                               pos, pos_dev, m->max_pos);
+                               pos, pos_dev, m->max_pos, appended ? view : KvContigView{}, l * nkh);
             rc = vh_check(hipGetLastError());
         } else if (!rc) {
             // a norm over the whole q or k vector: separate launches
@@ -219,8 +260,9 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
                 rc = vh_check(hipGetLastError());
             }
         }
-        if (!rc) rc = pos_dev ? vireo_kv_append_pos(kv, l * nkh, nkh, pos_dev, b.k, b.v, s)
-                              : vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
+        if (!rc && !appended)
+            rc = pos_dev ? vireo_kv_append_pos(kv, l * nkh, nkh, pos_dev, b.k, b.v, s)
+                         : vireo_kv_append_n(kv, l * nkh, nkh, pos, b.k, b.v, s);
         if (!rc) rc = pos_dev ? vireo_kv_attend_gqa_pos(kv, l * nkh, nh, nkh, pos_dev, b.q, b.att, s)
                               : vireo_kv_attend_gqa(kv, l * nkh, nh, nkh, b.q, b.att, s);
         if (!rc) rc = vh_qmatvec_acc(x, b.att, B.wo, nq, d, s);  // x += wo att

@@ -59,6 +59,58 @@ int launch_L(int L, float *y, const float *x, const uint8_t *w, int n, int d, in
     return vh_check(hipGetLastError());
 }
 
+// Up to three matrices over one input in one launch (a block's q, k and v
+// projections): the rows of job 0, then of job 1, then of job 2 form one
+// index space, and each row is computed as qmatvec_kernel computes it (L
+// lanes, items li, li + L, ... summed in that order, then the lane tree),
+// with the row's matrix type chosen at run time.
+struct MvJob {
+    float *y;
+    const uint8_t *w;
+    int64_t row_bytes;
+    int d;
+    uint32_t type;
+};
+template <int T, int L>
+VH_DEV float row_partial(const uint8_t *w, int64_t ro, int li, int items, int n, const float *x) {
+    float acc = 0.0f;
+    for (int it = li; it < items; it += L) acc += Fmt<T, false>::dot(w, ro, it, n, x);
+    return acc;
+}
+template <int L>
+__global__ void __launch_bounds__(256) qmatvec3_kernel(MvJob j0, MvJob j1, MvJob j2, const float *__restrict__ x,
+                                                       int n) {
+    constexpr int RPW = 64 / L;
+    const int lane = threadIdx.x & 63, sub = lane / L, li = lane % L;
+    const int items = n / 32;
+    const int64_t total = int64_t(j0.d) + j1.d + j2.d;
+    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t nwaves = int64_t(gridDim.x) * 4;
+    for (int64_t r0 = wave * RPW; r0 < total; r0 += nwaves * RPW) {
+        int64_t row = r0 + sub;
+        MvJob j = j0;
+        if (row >= j0.d) {
+            row -= j0.d, j = j1;
+            if (row >= j1.d) row -= j1.d, j = j2;
+        }
+        const bool live = row < j.d;
+        float acc = 0.0f;
+        if (live) {
+            const int64_t ro = row * j.row_bytes;
+            switch (j.type) {
+            case VT_Q8_0: acc = row_partial<VT_Q8_0, L>(j.w, ro, li, items, n, x); break;
+            case VT_Q4_K: acc = row_partial<VT_Q4_K, L>(j.w, ro, li, items, n, x); break;
+            case VT_Q6_K: acc = row_partial<VT_Q6_K, L>(j.w, ro, li, items, n, x); break;
+            case VT_Q5_0: acc = row_partial<VT_Q5_0, L>(j.w, ro, li, items, n, x); break;
+            case VT_F16: acc = row_partial<VT_F16, L>(j.w, ro, li, items, n, x); break;
+            default: acc = row_partial<VT_F32, L>(j.w, ro, li, items, n, x); break;
+            }
+        }
+        acc = group_sum<L>(acc);
+        if (li == L - 1 && live) j.y[row] = acc;
+    }
+}
+
 // Lanes per row: the power of two (<= 64) that leaves the fewest idle item
 // slots, preferring more lanes on a tie.
 int pick_lanes(int items) {
@@ -259,6 +311,39 @@ extern "C" int qmatvec_async(float *y, const float *x, const gguf_tensor *w, int
 
 int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s) {
     return qmv(y, x, w, n, d, 1, s);
+}
+
+int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1,
+                int d1, float *y2, const gguf_tensor *w2, int d2, hipStream_t s) {
+    if (!x || n <= 0 || n % 32) return -ENOTSUP;
+    const gguf_tensor *w[3] = {w0, w1, w2};
+    float *y[3] = {y0, y1, y2};
+    const int d[3] = {d0, d1, d2};
+    MvJob j[3];
+    for (int i = 0; i < 3; i++) {
+        if (!w[i] || !y[i] || d[i] <= 0) return -EINVAL;
+        const uint32_t t = w[i]->ggml_type;
+        if (t != VT_Q8_0 && t != VT_Q4_K && t != VT_Q6_K && t != VT_Q5_0 && t != VT_F16 && t != VT_F32) return -ENOTSUP;
+        int64_t rb;
+        if (int rc = check_weights(t, w[i]->data, n, d[i], &rb)) return rc;
+        j[i] = MvJob{y[i], static_cast<const uint8_t *>(w[i]->data), rb, d[i], t};
+    }
+    const int L = pick_lanes(n / 32), rpw = 64 / L;
+    const int64_t total = int64_t(d0) + d1 + d2;
+    int64_t blocks = ((total + rpw - 1) / rpw + 3) / 4;
+    const int64_t cap = int64_t(vh_num_cus()) * 16;
+    if (blocks > cap) blocks = cap;
+    dim3 g(static_cast<unsigned>(blocks)), b(256);
+    switch (L) {
+    case 64: hipLaunchKernelGGL(qmatvec3_kernel<64>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    case 32: hipLaunchKernelGGL(qmatvec3_kernel<32>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    case 16: hipLaunchKernelGGL(qmatvec3_kernel<16>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    case 8: hipLaunchKernelGGL(qmatvec3_kernel<8>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    case 4: hipLaunchKernelGGL(qmatvec3_kernel<4>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    case 2: hipLaunchKernelGGL(qmatvec3_kernel<2>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    default: hipLaunchKernelGGL(qmatvec3_kernel<1>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
+    }
+    return vh_check(hipGetLastError());
 }
 
 extern "C" int qmatvec(float *y, const float *x, const gguf_tensor *w, int n, int d) {

@@ -25,6 +25,10 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
                         hipStream_t s);
 // y += W x (qmatvec_async with each result added to y[r], one rounding)
 int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s);
+// y_i = W_i x for three matrices of n columns in one launch; -ENOTSUP when a
+// type or n has no such launch (then one qmatvec_async per matrix)
+int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1,
+                int d1, float *y2, const gguf_tensor *w2, int d2, hipStream_t s);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
