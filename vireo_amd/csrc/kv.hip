@@ -228,7 +228,10 @@ __global__ void __launch_bounds__(64) kv_merge_kernel(const float *__restrict__ 
         const float lsum = wave_sum_ordered(lw);
         L += lsum;
         const int n = min(64, nc - c0);
-#pragma unroll 4
+        // 16 chunks' loads in flight: the loop is bound by their latency (the
+        // accumulation order, and so the result, does not depend on it; 998 ->
+        // 1 146 tok/s for 48 layers at context 4096 against 4 in flight)
+#pragma unroll 16
         for (int u = 0; u < n; u++) {
             const float fu = fs[u];
             const float *pc = p + size_t(c0 + u) * (2 + D) + 2;
