@@ -59,7 +59,12 @@ void expert_store_register(ExpertStore *s, int layer, int expert,
 int  expert_store_lookup(ExpertStore *s, int layer, int expert, ExpertView *view);
 /* src/expert_store.h:50 */
 void expert_store_release(ExpertStore *s, ExpertView *view);
-/* src/expert_store.h:51 */
+/* src/expert_store.h:51. The reference's counters for the same work: direct
+ * lookups, plus one lookup per (token, routed expert) of every MoE call that
+ * was not captured in a graph, replayed through the reference's policy and
+ * budget (so they equal what src/expert_store.c reports for the same tokens,
+ * however the HBM pool pins or batches; expert_store_hbm_stats in vireo_hip.h
+ * reports the pool). Waits for the routing copies of calls still in flight. */
 void expert_store_stats(const ExpertStore *s, ExpertStats *out);
 /* src/expert_store.h:52 */
 void expert_store_destroy(ExpertStore *s);

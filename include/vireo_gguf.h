@@ -1,11 +1,14 @@
 /* GGUF types and the GGUF reader of vireo-hip.
  *
- * The first block has the same layout as the reference's src/gguf.h:15-55
- * (wire enums, gguf_str, gguf_kv, gguf_tensor, gguf_ctx) and the same include
- * guard, so a translation unit that already includes src/gguf.h sees identical
- * definitions and a standalone caller can include this header instead. At the
- * compute ABI only two fields of gguf_tensor are read, as in the reference's
- * gguf_matmul: `data` (there a device pointer) and `ggml_type`.
+ * The first block states everything the reference's src/gguf.h declares - the
+ * wire enums, gguf_str, gguf_kv, gguf_tensor, gguf_ctx (src/gguf.h:15-55) and
+ * the prototypes of its reader (src/gguf.h:57-72, defined by src/gguf.c when a
+ * program links it) - under the same include guard. So either header may come
+ * first: after src/gguf.h this block is skipped and its definitions are the
+ * ones seen; included first, it defines the same names and src/gguf.h is then
+ * skipped with nothing of it missing. At the compute ABI only two fields of
+ * gguf_tensor are read, as in the reference's gguf_matmul: `data` (there a
+ * device pointer) and `ggml_type`.
  *
  * The second block (its own guard, so it is seen whichever header defined the
  * types) declares this library's reader, vireo_gguf_*: the reference's
@@ -63,6 +66,18 @@ typedef struct {
     const uint8_t *data;   /* tensor data section start */
     uint64_t alignment;
 } gguf_ctx;
+
+/* The reference's reader (src/gguf.h:57-72), for programs that link src/gguf.c;
+ * this library's own reader is vireo_gguf_* below. */
+gguf_ctx *gguf_open(const char *path);
+void gguf_close(gguf_ctx *g);
+const gguf_kv *gguf_find(const gguf_ctx *g, const char *key);
+int gguf_get_u64(const gguf_ctx *g, const char *key, uint64_t *out);
+int gguf_get_f32(const gguf_ctx *g, const char *key, float *out);
+const char *gguf_get_str(const gguf_ctx *g, const char *key, uint64_t *len);
+const gguf_tensor *gguf_tensor_by_name(const gguf_ctx *g, const char *name);
+int gguf_type_block(uint32_t ggml_type, int *block_elems, int *block_bytes);
+void gguf_dump(const gguf_ctx *g);
 
 #ifdef __cplusplus
 }

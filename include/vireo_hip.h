@@ -107,6 +107,21 @@ typedef struct {
                                           the order; exact fp32 sums were used */
 #define VIREO_ROUTE_NEAR_TIE       2u  /* a selection boundary had an exact logit
                                           gap below 1e-6 (reported exception)  */
+#define VIREO_DECODE_TIMEOUT       4u  /* a kernel with a grid-wide wait gave up
+                                          waiting (not every workgroup was
+                                          resident): that call's result is invalid */
+
+/* Kernels that meet across the whole grid (the fused decode plan) bound every
+ * wait by a number of polls; a wait that runs out sets VIREO_DECODE_TIMEOUT in
+ * a sticky per-device status word and lets the kernel finish (no hang).
+ * vireo_hip_status waits for `stream` (NULL: the null stream), then reads and
+ * clears that word: -ETIMEDOUT if a wait gave up since the last read, else 0.
+ * Synchronous calls (stream NULL) check it themselves and return -ETIMEDOUT.
+ * vireo_hip_set_spin_limit sets the poll bound (default 262144; 0 makes every
+ * such wait give up at once, which tests the error path without a hang). No
+ * counterpart in the reference. */
+int vireo_hip_status(void *stream);
+int vireo_hip_set_spin_limit(unsigned polls);
 
 /* Stage 1 of moe_ffn_forward: router logits (F32 matvec), softmax, top-k with
  * lowest-index tie-break, optional renorm (src/gguf_run.c:187-192), for
@@ -129,15 +144,26 @@ int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts,
  * silu(gate_e hb[t]) * up_e hb[t]) over the k routed experts e = idx[t][j],
  * combined in selection order without atomics. x, hb: device
  * [n_tokens x dim]; idx_out / w_out (optional) receive the routing.
- * Expert slices come from m->es; on the first call for a layer every expert
- * of that layer is looked up once and its lease held (the resident set is
- * the whole layer), as there is no host round trip per token. When the
- * store's capacity is below one layer's experts, every call instead copies
- * the per-expert token counts to the host and looks the routed experts up in
- * batches that fit (misses paged in from the store's file, least recently
- * used unleased experts evicted), releasing each batch after its kernels; such
- * a call synchronizes the stream and cannot be captured in a graph. An expert
- * that is not registered contributes nothing, as in the reference. */
+ * Expert slices come from m->es, which must be a store made by this library
+ * (a store from the reference's CPU src/expert_store.c is refused: -EINVAL).
+ * When the store's capacity holds every registered expert of every layer (0 =
+ * unbounded), the first call for a layer looks each of its experts up once and
+ * holds the leases (expert_store_pin_layer), as there is no host round trip
+ * per token; a layer the caller pinned explicitly is used the same way.
+ * Otherwise every call copies the per-expert token counts and the routing to
+ * the host and looks the routed experts up in batches that fit the room beside
+ * the leased experts (misses read from the store's file while earlier batches
+ * compute and copied to HBM on a copy stream; least recently used unleased
+ * experts evicted, their blocks reused only after the kernels reading them);
+ * such a call synchronizes the stream once and cannot be captured in a graph.
+ * expert_store_stats then counts what the reference would: one lookup per
+ * (token, routed expert) in token and selection order (see
+ * expert_store_hbm_stats for what the HBM pool itself did). An expert that is
+ * not registered contributes nothing, as in the reference.
+ * Graph capture: capture after one uncaptured call of each shape. Buffers the
+ * library grows later are new allocations; the ones captured graphs use stay
+ * allocated, so such graphs remain valid. Calls captured in a graph are not
+ * counted in expert_store_stats (the host does not see replays). */
 int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
                     int32_t *idx_out, float *w_out, void *stream);
 
@@ -353,6 +379,12 @@ ExpertStore *expert_store_create_device(const void *dev_base, uint64_t size, uin
 int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_table);
 /* Release the leases taken by expert_store_pin_layer for `layer`. */
 int expert_store_unpin_layer(ExpertStore *s, int layer);
+/* What the HBM pool did, in ExpertStats form: every lookup the library made
+ * (whole layers pinned, routed experts paged per call) and the caller's own
+ * lookups, the bytes copied into HBM (or aliased, for a device-backed store),
+ * and the bytes and experts resident in HBM now. expert_store_stats reports
+ * the reference's accounting of the same work instead. */
+void expert_store_hbm_stats(const ExpertStore *s, ExpertStats *out);
 
 #ifdef __cplusplus
 }

@@ -1,10 +1,11 @@
 /* KV cache on the GPU: the reference's KVStore (src/kvstore.h) with its
  * vectors in device memory.
  *
- * The first block has the same layout and include guard as the reference's
- * KVConfig / KVStats (src/kvstore.h:26-45), so a translation unit that
- * includes src/kvstore.h first sees those definitions. The second block is
- * this library's store.
+ * Its configuration and statistics structs have the layout of the reference's
+ * KVConfig / KVStats (src/kvstore.h:26-45) under names of their own
+ * (VireoKVConfig, VireoKVStats), so this header and src/kvstore.h can be
+ * included in either order; a caller holding a KVConfig copies it field by
+ * field (or passes it through a cast: the members, types and order are the same).
  *
  * A store keeps, per "layer" (the reference indexes layer * n_kv_heads +
  * kv_head), the keys and values appended so far in blocks of
@@ -33,8 +34,8 @@
  * stream (NULL: the null stream, synchronously); every call on a store must use
  * the same stream. A TOPK query copies its block scores to the host and so
  * synchronizes that stream. Not thread-safe, like the reference. */
-#ifndef VIREO_KVSTORE_H
-#define VIREO_KVSTORE_H
+#ifndef VIREO_KV_H
+#define VIREO_KV_H
 
 #include <stddef.h>
 #include <stdint.h>
@@ -43,6 +44,7 @@
 extern "C" {
 #endif
 
+/* KVConfig (src/kvstore.h:26-33): same members, types and order */
 typedef struct {
     int n_layers;
     int kv_dim;              /* length of each key and value vector        */
@@ -50,8 +52,9 @@ typedef struct {
     int sink_tokens;         /* always-resident attention sinks (prefix)   */
     int window_tokens;       /* always-resident recent window              */
     uint64_t capacity_bytes; /* budget for resident blocks (0 = unbounded) */
-} KVConfig;
+} VireoKVConfig;
 
+/* KVStats (src/kvstore.h:35-44): same members, types and order */
 typedef struct {
     uint64_t requests;
     uint64_t hits;
@@ -61,19 +64,7 @@ typedef struct {
     uint64_t bytes_spilled;
     uint64_t resident_bytes;
     uint64_t capacity_bytes;
-} KVStats;
-
-#ifdef __cplusplus
-}
-#endif
-#endif /* VIREO_KVSTORE_H */
-
-#ifndef VIREO_KV_H
-#define VIREO_KV_H
-
-#ifdef __cplusplus
-extern "C" {
-#endif
+} VireoKVStats;
 
 typedef struct VireoKV VireoKV;
 
@@ -81,11 +72,11 @@ enum { VIREO_KV_SELECT_ALL = 0, VIREO_KV_SELECT_RECENT = 1, VIREO_KV_SELECT_TOPK
 
 /* src/kvstore_dense.c:kvstore_dense_create. kv_dim: 64, 128 or 256;
  * block_tokens: 1..64. NULL on failure. */
-VireoKV *vireo_kv_create_dense(KVConfig cfg);
+VireoKV *vireo_kv_create_dense(VireoKVConfig cfg);
 /* src/kvstore_ooc.c:kvstore_ooc_create with the strategy VIREO_KV_SELECT_*
  * (topk_budget: the TOPK budget, as vireo_select_topk(budget); <= 0: 8).
  * Spilled blocks go to host memory. NULL on failure. */
-VireoKV *vireo_kv_create_paged(KVConfig cfg, int strategy, int topk_budget);
+VireoKV *vireo_kv_create_paged(VireoKVConfig cfg, int strategy, int topk_budget);
 /* kv_append (src/kvstore.h:58-61): k and v ([kv_dim] each) become token pos
  * of `layer`. Returns 0 or -errno. */
 int vireo_kv_append(VireoKV *s, int layer, int pos, const float *k, const float *v, void *stream);
@@ -110,7 +101,7 @@ int vireo_kv_attend_gqa(VireoKV *s, int layer0, int n_heads, int n_kv_heads, con
  * does not track those tokens; vireo_kv_stats counts the host-position ones).
  * NULL on failure. No counterpart in the reference (its stores grow by host
  * calls). */
-VireoKV *vireo_kv_create_contiguous(KVConfig cfg, int max_tokens);
+VireoKV *vireo_kv_create_contiguous(VireoKVConfig cfg, int max_tokens);
 /* vireo_kv_append_n at the position *pos (device int32); nothing is written
  * for a position outside [0, max_tokens). */
 int vireo_kv_append_pos(VireoKV *s, int layer0, int n, const int32_t *pos, const float *k, const float *v,
@@ -121,7 +112,7 @@ int vireo_kv_append_pos(VireoKV *s, int layer0, int n, const int32_t *pos, const
 int vireo_kv_attend_gqa_pos(VireoKV *s, int layer0, int n_heads, int n_kv_heads, const int32_t *pos, const float *q,
                             float *out, void *stream);
 /* kv_stats (src/kvstore.h:65) */
-void vireo_kv_stats(const VireoKV *s, KVStats *out);
+void vireo_kv_stats(const VireoKV *s, VireoKVStats *out);
 /* kv_destroy (src/kvstore.h:66-68); waits for the store's work first */
 void vireo_kv_destroy(VireoKV *s);
 

@@ -86,3 +86,45 @@ def expert_lists(shape, g, u, d):
     E = shape.E
     return ([g[e * gs:(e + 1) * gs] for e in range(E)], [u[e * us:(e + 1) * us] for e in range(E)],
             [d[e * ds:(e + 1) * ds] for e in range(E)])
+
+
+class RefStoreReplay:
+    """The oracle's restatement of the reference's ExpertStore
+    (src/expert_store.c), driven by the lookups the reference would make for
+    the same work: what expert_store_stats must report. The backing file is a
+    sparse temporary file of the model's expert bytes (the oracle pages from
+    it; only the counters are compared)."""
+
+    FIELDS = ("requests", "hits", "misses", "bytes_read", "resident_bytes", "capacity_bytes", "experts_resident")
+
+    def __init__(self, oracle, shape, n_layers, capacity, registered=None):
+        import tempfile
+        self.o, self.E = oracle, shape.E
+        gs, us, ds = shape.slice_bytes()
+        eb = gs + us + ds
+        self.fd, path = tempfile.mkstemp()
+        os.unlink(path)
+        os.ftruncate(self.fd, n_layers * shape.E * eb)
+        self.s = oracle.store_create(self.fd, capacity, n_layers, shape.E)
+        for l in range(n_layers):
+            for e in range(shape.E):
+                if registered is not None and not registered(l, e):
+                    continue
+                base = (l * shape.E + e) * eb
+                oracle.store_register(self.s, l, e, base, base + gs, base + gs + us, gs, us, ds)
+
+    def route(self, layer, idx):
+        """moe_ffn's lookups for routing idx [T x k]: token order, selection
+        order, each released before the next (src/gguf_run.c:193-213)."""
+        for row in np.asarray(idx).reshape(len(idx), -1):
+            for e in row:
+                rc, view = self.o.store_lookup(self.s, layer, int(e))
+                if rc == 0:
+                    self.o.store_release(self.s, view)
+
+    def stats(self):
+        return dict(zip(self.FIELDS, self.o.store_stats(self.s)))
+
+    def close(self):
+        self.o.store_destroy(self.s)
+        os.close(self.fd)

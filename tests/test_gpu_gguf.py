@@ -17,14 +17,15 @@ the oracle on the arrays that were written into the file.
 * A store smaller than a layer (the reference's laptop case): every call
   pages its routed experts in batches that fit; outputs match the oracle, and
   equal the fully resident model's bit for bit where both run the grouped
-  kernels (more than one token); the pool never exceeds its capacity, every
-  call looks up each routed expert once, and the stack decodes through it.
+  kernels (more than one token); the pool never exceeds its capacity, the
+  statistics equal the oracle's ExpertStore driven by the same tokens, and the
+  stack decodes through it.
 """
 import numpy as np
 import pytest
 import torch
 
-from conftest import expert_lists
+from conftest import RefStoreReplay, expert_lists
 from vireo_amd import gguf as G
 from vireo_amd import workloads as W
 
@@ -56,6 +57,7 @@ def test_gguf_layers_match_oracle(cuda, oracle, tmp_path, name):
                                                                     shape.k, shape.fe, shape.renorm)
     assert m.eps == np.float32(W.EPS)
     gs, us, ds = shape.slice_bytes()
+    replay = RefStoreReplay(oracle, shape, L, 0)
     for layer in range(L):
         Gl, Ul, Dl = expert_lists(shape, *arr["experts"][layer])
         for T in (1, 5):
@@ -64,9 +66,14 @@ def test_gguf_layers_match_oracle(cuda, oracle, tmp_path, name):
             idx, _ = m.forward(layer, xg, hg, return_routing=True)
             xo, io, _, _ = oracle.moe_ffn(shape, arr["routers"][layer], Gl, Ul, Dl, x, hb)
             check(f"{name} layer {layer} T={T}", x, xg.cpu().numpy(), xo, idx.cpu().numpy(), io)
-        st = m.stats()
-        assert st["resident_bytes"] == (layer + 1) * shape.E * (gs + us + ds)
-        assert st["bytes_read"] == st["resident_bytes"]
+            replay.route(layer, io)
+        # the pool holds whole layers, each read from the file once
+        hbm = m.hbm_stats()
+        assert hbm["resident_bytes"] == (layer + 1) * shape.E * (gs + us + ds)
+        assert hbm["bytes_read"] == hbm["resident_bytes"]
+        # the statistics are the reference's for the same tokens
+        assert m.stats() == replay.stats()
+    replay.close()
     m.close()
 
 
@@ -117,17 +124,22 @@ def test_gguf_stack_matches_oracle(cuda, oracle, tmp_path, name, untied, cap_exp
     m.close()
 
 
-@pytest.mark.parametrize("name,cap_experts,T", [("tiny-k", 3, 5), ("tiny-q8", 1, 3), ("qwen3-16e", 4, 1),
-                                               ("qwen3-16e", 5, 6)])
-def test_gguf_paged_store(cuda, oracle, tmp_path, name, cap_experts, T):
-    shape, L = SHAPES[name], 2
+@pytest.mark.parametrize("name,cap_experts,T,L", [("tiny-k", 3, 5, 2), ("tiny-q8", 1, 3, 2), ("qwen3-16e", 4, 1, 2),
+                                                 ("qwen3-16e", 5, 6, 2), ("qwen3-16e", 24, 1, 3),
+                                                 ("tiny-k", 12, 4, 3)])
+def test_gguf_paged_store(cuda, oracle, tmp_path, name, cap_experts, T, L):
+    """Stores smaller than the model (down to one expert, and about one and
+    a half layers of a 3-layer model): the pool stays within its capacity,
+    outputs match the oracle, and the statistics are the reference's for the
+    same tokens."""
+    shape = SHAPES[name]
     path = tmp_path / f"{name}.gguf"
     arr = G.write_moe_gguf(str(path), shape, L, seed=41)
     cap = cap_experts * shape.expert_bytes()
     paged = G.GGUFModel(path, expert_capacity=cap, load_head=False)
     full = G.GGUFModel(path, load_head=False)
-    lookups = 0
-    for call in range(6):
+    replay = RefStoreReplay(oracle, shape, L, cap)
+    for call in range(3 * L):
         layer = call % L
         Gl, Ul, Dl = expert_lists(shape, *arr["experts"][layer])
         x, hb = W.host_hidden(shape.d, T, seed=100 + call)
@@ -139,10 +151,11 @@ def test_gguf_paged_store(cuda, oracle, tmp_path, name, cap_experts, T):
         check(f"{name} paged call {call} layer {layer}", x, xp.cpu().numpy(), xo, idx.cpu().numpy(), io)
         if T > 1:  # both on the grouped kernels: the same rows, the same combine
             assert torch.equal(xp, xf)
-        lookups += len(np.unique(io))
-        st = paged.stats()
-        assert st["resident_bytes"] <= cap
-        assert st["requests"] == lookups and st["hits"] + st["misses"] == lookups
-    print(f"{name}: {paged.stats()}")
+        replay.route(layer, io)
+        hbm = paged.hbm_stats()
+        assert hbm["resident_bytes"] <= cap, hbm
+        assert paged.stats() == replay.stats()
+    print(f"{name} cap {cap_experts} experts: {paged.stats()}; pool {paged.hbm_stats()}")
+    replay.close()
     paged.close()
     full.close()

@@ -128,11 +128,53 @@ def test_moe_from_file_backed_store(cuda, lib):
         m.forward(0, xb, hbt)
         np.testing.assert_array_equal(xb.cpu().numpy(), xa.cpu().numpy())
         st = _lib.ExpertStats()
-        lib.expert_store_stats(s, C.byref(st))
+        lib.expert_store_hbm_stats(s, C.byref(st))  # the pool: the whole layer, read once
         assert st.misses == shape.E and st.bytes_read == shape.E * (gs + us + ds)
+        lib.expert_store_stats(s, C.byref(st))  # the reference: one lookup per (token, routed expert)
+        assert st.requests == 4 * shape.k and st.misses == st.experts_resident
+        assert st.hits + st.misses == st.requests
         torch.cuda.synchronize()
         lib.expert_store_destroy(s)
     finally:
         os.close(fd)
     m.model.es = m.es
     m.close()
+
+
+@pytest.mark.parametrize("cap_experts", [0, 2])
+def test_truncated_backing_file_is_an_error(cuda, lib, cap_experts):
+    """A backing file that ends inside an expert's slices: the lookup that
+    must read them returns -EIO (the reference ignores the short read,
+    src/expert_store.c:67), and moe_ffn_forward reports it, pinned (unbounded
+    store) or paged (a store of two experts)."""
+    shape = W.SHAPES["olmoe-q4_k_m"].with_(name="olmoe-8e", E=8)
+    m = M.DeviceMoE(shape, 1, seed=67)
+    gb, ub, db = m.device_layer_bytes(0)
+    gs, us, ds = m.slices
+    fd, path = tempfile.mkstemp()
+    os.unlink(path)
+    try:
+        blob = gb.tobytes() + ub.tobytes() + db.tobytes()
+        os.pwrite(fd, blob[:len(blob) - ds // 2], 0)  # the last expert's down slice is cut short
+        s = lib.expert_store_create(fd, cap_experts * shape.expert_bytes(), 1, shape.E)
+        for e in range(shape.E):
+            sl = _lib.ExpertSlices(e * gs, gb.size + e * us, gb.size + ub.size + e * ds, gs, us, ds)
+            lib.expert_store_register(s, 0, e, C.byref(sl))
+        v = _lib.ExpertView()
+        assert lib.expert_store_lookup(s, 0, shape.E - 1, C.byref(v)) == -errno.EIO
+        assert not v.gate and not v.slot
+        assert lib.expert_store_lookup(s, 0, 0, C.byref(v)) == 0  # a whole expert still pages in
+        lib.expert_store_release(s, C.byref(v))
+        m.model.es = s
+        x, hb = W.host_hidden(shape.d, 2, 67)
+        xt, hbt = torch.from_numpy(x).to(cuda), torch.from_numpy(hb).to(cuda)
+        # top-8 of 8 experts: every token routes to the truncated expert too
+        rc = lib.moe_ffn_forward(C.byref(m.model), 0, C.c_void_p(xt.data_ptr()), C.c_void_p(hbt.data_ptr()), 2,
+                                 None, None, None)
+        assert rc == -errno.EIO
+        torch.cuda.synchronize()
+        lib.expert_store_destroy(s)
+    finally:
+        os.close(fd)
+        m.model.es = m.es
+        m.close()

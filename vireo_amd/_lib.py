@@ -122,13 +122,13 @@ class GGUFMoE(C.Structure):
 
 
 class KVConfig(C.Structure):
-    """KVConfig (src/kvstore.h:26-33)."""
+    """VireoKVConfig: the layout of KVConfig (src/kvstore.h:26-33)."""
     _fields_ = [("n_layers", C.c_int), ("kv_dim", C.c_int), ("block_tokens", C.c_int), ("sink_tokens", C.c_int),
                 ("window_tokens", C.c_int), ("capacity_bytes", C.c_uint64)]
 
 
 class KVStats(C.Structure):
-    """KVStats (src/kvstore.h:35-44)."""
+    """VireoKVStats: the layout of KVStats (src/kvstore.h:35-44)."""
     _fields_ = [(n, C.c_uint64) for n in ("requests", "hits", "misses", "prefetched", "bytes_read", "bytes_spilled",
                                           "resident_bytes", "capacity_bytes")]
 
@@ -200,6 +200,9 @@ SIGNATURES = {
     "expert_store_lookup": (C.c_int, [c_vp, C.c_int, C.c_int, C.POINTER(ExpertView)]),
     "expert_store_release": (None, [c_vp, C.POINTER(ExpertView)]),
     "expert_store_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
+    "expert_store_hbm_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
+    "vireo_hip_status": (C.c_int, [c_vp]),
+    "vireo_hip_set_spin_limit": (C.c_int, [C.c_uint]),
     "expert_store_destroy": (None, [c_vp]),
     "expert_store_pin_layer": (C.c_int, [c_vp, C.c_int, C.POINTER(c_vp)]),
     "expert_store_unpin_layer": (C.c_int, [c_vp, C.c_int]),

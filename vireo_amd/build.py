@@ -58,8 +58,12 @@ def build(verbose=False):
             f.result()
     objs = [j[-1] for j in jobs]
     tmp = LIB + ".tmp"
+    # -Bsymbolic: the library's own calls (expert_store_* from moe_ffn_forward,
+    # for instance) bind to its own definitions, never to a same-named symbol
+    # of the executable (a reference build that still links its CPU
+    # src/expert_store.c would otherwise interpose its store on them)
     _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
-          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"], verbose)
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,-Bsymbolic"], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -26,6 +26,19 @@ int vh_device_workspace(size_t bytes, void **out);  // per-device scratch, grown
 int vh_counters(int n, unsigned **out);              // per-device zeroed counters (self-resetting use)
 int vh_reduce_scratch(size_t bytes, void **out);     // per-device scratch for reduction partials
 int vh_num_cus();
+// The per-device stream that expert page-in copies run on (created on first use).
+int vh_copy_stream(hipStream_t *out);
+// Pinned host memory for small per-call uploads (grow-only, per device). A
+// call that takes it first waits until the copies of the previous call that
+// used it have run (the event vh_host_staging_done recorded on that call's stream).
+int vh_host_staging(size_t bytes, void **out);
+int vh_host_staging_done(hipStream_t s);
+// Sticky per-device status bits that kernels with grid-wide waits set when a
+// wait gives up (VIREO_DECODE_TIMEOUT), the poll limit of such waits
+// (vireo_hip_set_spin_limit), and a read-and-clear after the stream's work.
+int vh_status_word(uint32_t **out);
+unsigned vh_spin_limit();
+int vh_take_status(hipStream_t s);
 // bytes of a row of n weights of ggml type t (src/gguf.c:27-38; F32 otherwise)
 inline int64_t vh_row_bytes(uint32_t t, int n) {
     switch (t) {

@@ -462,12 +462,12 @@ int by_score_desc(const void *a, const void *b);
 }  // namespace
 
 struct VireoKV {
-    KVConfig cfg{};
+    VireoKVConfig cfg{};
     bool dense = false;  // kvstore_dense semantics for the statistics
     int strategy = VIREO_KV_SELECT_ALL, budget = 0;  // budget: the strategy's (0 = unbounded)
     int sink_blocks = 0, window_blocks = 0, d = 0, G = 0;
     uint64_t block_bytes = 0, resident_bytes = 0, tick = 0;
-    KVStats st{};
+    VireoKVStats st{};
     std::vector<KvLayer> layers;
     std::vector<void *> slabs;
     std::vector<float *> free_blocks;
@@ -482,6 +482,9 @@ struct VireoKV {
     int stage_next = 0;
     float *part = nullptr;
     size_t part_bytes = 0;
+    // device buffers replaced by larger ones: HIP graphs captured earlier may
+    // still point at them, so they are freed only with the store
+    std::vector<void *> retired;
     std::vector<float> hscores;
     // contiguous stores (vireo_kv_create_contiguous): every layer's blocks in
     // one region, block b of layer l at cbase + (l * max_blocks + b) * 2 G d,
@@ -618,15 +621,23 @@ int start_block(VireoKV *S, KvLayer &L, hipStream_t s) {
 }
 
 // device scratch of at least `bytes` (grown; the stream is idle when it grows)
-int scratch(VireoKV *S, size_t bytes, hipStream_t s, void **out) {
-    if (bytes > S->dscratch_bytes) {
-        if (hipStreamSynchronize(s) != hipSuccess) return -EIO;
-        if (S->dscratch) (void)hipFree(S->dscratch);
-        S->dscratch = nullptr;
-        const size_t nb = bytes < (size_t(1) << 16) ? (size_t(1) << 16) : 2 * bytes;
-        if (hipMalloc(&S->dscratch, nb) != hipSuccess) { S->dscratch_bytes = 0; return -ENOMEM; }
-        S->dscratch_bytes = nb;
-    }
+// Replace *buf by an allocation of at least `need` bytes (twice that, so a
+// store grows a few times at most). The old buffer is kept until the store is
+// destroyed: enqueued work and captured graphs may still use it.
+template <class T>
+int grow(VireoKV *S, T **buf, size_t *bytes, size_t need) {
+    if (need <= *bytes) return 0;
+    const size_t nb = need < (size_t(1) << 16) ? (size_t(1) << 16) : 2 * need;
+    void *p = nullptr;
+    if (hipMalloc(&p, nb) != hipSuccess) return -ENOMEM;
+    if (*buf) S->retired.push_back(static_cast<void *>(*buf));
+    *buf = static_cast<T *>(p);
+    *bytes = nb;
+    return 0;
+}
+
+int scratch(VireoKV *S, size_t bytes, hipStream_t, void **out) {
+    if (int rc = grow(S, &S->dscratch, &S->dscratch_bytes, bytes)) return rc;
     *out = S->dscratch;
     return 0;
 }
@@ -793,14 +804,7 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
         void *dv = nullptr, *hv = nullptr;
         int slot = 0;
         rc = scratch(S, db + ib + 256, s, &dv);
-        if (!rc && pb > S->part_bytes) {
-            if (hipStreamSynchronize(s) != hipSuccess) rc = -EIO;
-            if (S->part) (void)hipFree(S->part);
-            S->part = nullptr;
-            S->part_bytes = 0;
-            if (!rc && hipMalloc(reinterpret_cast<void **>(&S->part), 2 * pb) != hipSuccess) rc = -ENOMEM;
-            if (!rc) S->part_bytes = 2 * pb;
-        }
+        if (!rc) rc = grow(S, &S->part, &S->part_bytes, pb);
         if (!rc) rc = staging(S, db + ib + 256, &hv, &slot);
         if (!rc) {
             char *hc = static_cast<char *>(hv), *dc = static_cast<char *>(dv);
@@ -837,7 +841,7 @@ int attend(VireoKV *S, int layer0, int n_heads, int kv_mul, const float *q, floa
     return rc;
 }
 
-VireoKV *create(KVConfig cfg, int strategy, int budget) {
+VireoKV *create(VireoKVConfig cfg, int strategy, int budget) {
     if (cfg.n_layers <= 0 || (cfg.kv_dim != 64 && cfg.kv_dim != 128 && cfg.kv_dim != 256) ||
         cfg.block_tokens < 1 || cfg.block_tokens > 64 || cfg.sink_tokens < 0 || cfg.window_tokens < 0)
         return nullptr;
@@ -864,7 +868,7 @@ VireoKV *create(KVConfig cfg, int strategy, int budget) {
 
 }  // namespace
 
-extern "C" VireoKV *vireo_kv_create_dense(KVConfig cfg) {
+extern "C" VireoKV *vireo_kv_create_dense(VireoKVConfig cfg) {
     cfg.capacity_bytes = 0;
     cfg.sink_tokens = 0;
     cfg.window_tokens = 0;
@@ -873,11 +877,11 @@ extern "C" VireoKV *vireo_kv_create_dense(KVConfig cfg) {
     return S;
 }
 
-extern "C" VireoKV *vireo_kv_create_paged(KVConfig cfg, int strategy, int topk_budget) {
+extern "C" VireoKV *vireo_kv_create_paged(VireoKVConfig cfg, int strategy, int topk_budget) {
     return create(cfg, strategy, topk_budget);
 }
 
-extern "C" VireoKV *vireo_kv_create_contiguous(KVConfig cfg, int max_tokens) {
+extern "C" VireoKV *vireo_kv_create_contiguous(VireoKVConfig cfg, int max_tokens) {
     cfg.capacity_bytes = 0;
     cfg.sink_tokens = 0;
     cfg.window_tokens = 0;
@@ -926,14 +930,7 @@ extern "C" int vireo_kv_attend_gqa_pos(VireoKV *S, int layer0, int n_heads, int 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int nchunk = (S->max_blocks + kGroupBlocks - 1) / kGroupBlocks;
     const size_t pb = size_t(n_heads) * nchunk * (2 + d) * sizeof(float);
-    if (pb > S->part_bytes) {  // the first call sizes the partials
-        if (hipStreamSynchronize(s) != hipSuccess) return -EIO;
-        if (S->part) (void)hipFree(S->part);
-        S->part = nullptr;
-        S->part_bytes = 0;
-        if (hipMalloc(reinterpret_cast<void **>(&S->part), pb) != hipSuccess) return -ENOMEM;
-        S->part_bytes = pb;
-    }
+    if (int rc = grow(S, &S->part, &S->part_bytes, pb)) return rc;  // the first call sizes the partials
     const ContiguousBlocks cb{S->cbase, pos, layer0, S->max_blocks, S->G, d};
     const float scale = 1.0f / sqrtf(float(d));
     int rc;
@@ -968,7 +965,7 @@ extern "C" int vireo_kv_attend(VireoKV *S, int layer, const float *q, float *out
     return vireo_kv_attend_gqa(S, layer, 1, 1, q, out, stream);
 }
 
-extern "C" void vireo_kv_stats(const VireoKV *S, KVStats *out) {
+extern "C" void vireo_kv_stats(const VireoKV *S, VireoKVStats *out) {
     if (!S || !out) return;
     if (S->dense) {  // src/kvstore_dense.c:56-63: no counters; the appended tokens' bytes
         memset(out, 0, sizeof *out);
@@ -994,6 +991,7 @@ extern "C" void vireo_kv_destroy(VireoKV *S) {
     for (void *p : S->slabs) (void)hipFree(p);
     if (S->dscratch) (void)hipFree(S->dscratch);
     if (S->part) (void)hipFree(S->part);
+    for (void *p : S->retired) (void)hipFree(p);
     for (int i = 0; i < kStageRing; i++) {
         if (S->hstage[i]) (void)hipHostFree(S->hstage[i]);
         if (S->staged[i]) (void)hipEventDestroy(S->staged[i]);

@@ -57,11 +57,12 @@ struct Ws {
     int32_t *tiles, *small;  // matrix-core plan: token tiles, the other groups
     void *hs;                // matrix-core plan: bf16 h rows in dispatch order
     void *xb;                // matrix-core plan: bf16 copy of hb
-    const void **tab;        // paged plan: [3 E] expert table of the current batch
-    int32_t *act;            // paged plan: [E + 1] active list of the current batch
+    const void **tab;        // paged plan: [E + 1] expert tables [3 E] (one per batch, then the combine's)
+    int32_t *act;            // paged plan: [E] active lists [E + 1] (one per batch)
 };
 
-int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false) {
+int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false,
+           bool paged = false) {
     const size_t P = size_t(T) * k;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
@@ -77,7 +78,8 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
-    const size_t o_tab = take(size_t(3) * E * sizeof(void *)), o_act = take(size_t(E + 1) * 4);
+    const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
+    const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
     void *base;
     if (int rc = vh_device_workspace(off, &base)) return rc;
     char *b = static_cast<char *>(base);
@@ -108,6 +110,20 @@ bool decode_supported(const vireo_moe_model *m, int layer) {
     const uint32_t tg = L.gate_exps->ggml_type, tu = L.up_exps->ggml_type, td = L.down_exps->ggml_type;
     return tg == tu && vh_decode_gateup_supported(tg, m->dim, m->ffn_exp) &&
            vh_down_combine_supported(td, m->dim, m->ffn_exp, m->n_used);
+}
+
+// The layer's expert table: 0 with *table set when its experts are pinned
+// (pinning them now when the store holds every layer at once), 1 when the call
+// must page its routed experts instead, or -errno. Pinning only a part of the
+// model would leave the rest too little room and keep it over budget, so a
+// store smaller than the model pages every layer the caller has not pinned.
+int layer_table(const vireo_moe_model *m, int layer, const void *const **table) {
+    if (!vh_store_valid(m->es)) return -EINVAL;  // NULL, or a store this library did not make
+    *table = vh_store_layer_table(m->es, layer);
+    if (*table) return 0;
+    if (!vh_store_fits_all(m->es)) return 1;
+    const int rc = expert_store_pin_layer(m->es, layer, table);
+    return rc == -ENOSPC ? 1 : rc;
 }
 
 // Where the decode stages keep what they hand to each other.
@@ -175,8 +191,8 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
     }
     const vireo_moe_layer &L = m->layers[layer];
     const void *const *table = nullptr;
-    if (int rc = expert_store_pin_layer(m->es, layer, &table)) {
-        if (rc != -ENOSPC) return rc;
+    if (int rc = layer_table(m, layer, &table)) {
+        if (rc < 0) return rc;
         if ((rc = vireo_rmsnorm(xb, x, nw, m->dim, 1, eps, s))) return rc;
         return moe_ffn_forward(m, layer, x, xb, 1, nullptr, nullptr, s);  // pages the routed experts
     }
@@ -186,6 +202,7 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
     int rc = vh_route_parts_norm(static_cast<const float *>(L.router->data), x, nw, eps, xb, L.logit_bias, m->dim,
                                  m->n_experts, 1, st.parts, s, st.bar, kFusedBlocks + 1);
     for (int stage = 1; stage < 3 && !rc; stage++) rc = decode_stage(m, layer, stage, table, x, xb, st, ws.idx, ws.w, s);
+    if (!rc) rc = vh_store_note_routing(m->es, layer, ws.idx, 1, m->n_used, s);
     return rc;
 }
 
@@ -202,7 +219,7 @@ extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, 
     if (reinterpret_cast<uintptr_t>(hb) & 15u) return -EINVAL;  // the decode kernels read hb in 16-byte units
     if (stage == 2 && !x) return -EINVAL;
     if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
-    if (!m->es) return -EINVAL;
+    if (!vh_store_valid(m->es)) return -EINVAL;
     const void *const *table = nullptr;
     if (int rc = expert_store_pin_layer(m->es, layer, &table)) return rc;
     size_t off[4];
@@ -220,7 +237,9 @@ extern "C" int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, 
         if (!w) w = ws.w;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    return vh_finish(s, decode_stage(m, layer, stage, table, x, hb, st, idx, w, s));
+    int rc = vh_finish(s, decode_stage(m, layer, stage, table, x, hb, st, idx, w, s));
+    if (!rc && !s && stage == 1 && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
+    return rc;
 }
 
 extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n, const int *layers, float *x,
@@ -307,17 +326,20 @@ extern "C" int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_exper
     return vh_finish(s, vh_dispatch(idx, int(P), n_experts, counts, offs, perm, nullptr, s));
 }
 
-// moe_ffn_forward when the ExpertStore cannot hold the layer. The reference
-// looks each routed expert up in turn and releases it after use
-// (src/gguf_run.c:193-213), so a store of any size serves it; here the
-// routing and the dispatch run on the device, the per-expert counts come back
-// to the host, and the routed experts are taken in batches that fit the
-// store's capacity: look the batch up (the store pages misses in from its file
-// and evicts the least recently used unleased experts), run the grouped
-// projections on that batch alone, wait for them, release the leases. The
-// combine runs once all batches have written their rows. The stream is
-// synchronized (the host needs the routing), so such a call cannot be
-// captured in a graph.
+// moe_ffn_forward when the ExpertStore does not hold every layer at once. The
+// reference looks each routed expert up in turn and releases it after use
+// (src/gguf_run.c:193-213), so a store of any size serves it. Here the routing
+// and the dispatch run on the device; the per-expert counts and the routing
+// come back to the host (the routing also feeds the store's statistics), and
+// the routed experts are taken in batches that fit the room the store has
+// beside the experts that hold leases: look the batch up (misses are read from
+// the store's file into pinned staging while earlier batches compute, and
+// copied to HBM on the copy stream), make the compute stream wait for those
+// copies, run the grouped projections on the batch, and drop its leases at
+// once - every block the batch read carries an event recorded after its
+// kernels, and a later page-in into that block waits for it. The combine runs
+// once all batches have written their rows. The stream is synchronized once
+// (the host needs the routing), so such a call cannot be captured in a graph.
 int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
                   float *w_out, hipStream_t s) {
     const vireo_moe_layer &L = m->layers[layer];
@@ -325,7 +347,7 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
     const int P = n_tokens * k, slots = P < E ? P : E;
     Ws ws;
-    if (int rc = get_ws(n_tokens, E, k, d, fe, true, true, &ws)) return rc;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, true, &ws, false, true)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     const float *R = static_cast<const float *>(L.router->data);
@@ -334,36 +356,53 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
-    int32_t counts[kMaxExperts];
-    if (!rc) rc = vh_check(hipStreamSynchronize(s));
-    if (!rc) rc = vh_check(hipMemcpy(counts, ws.counts, size_t(E) * 4, hipMemcpyDeviceToHost));
+    // pinned host memory: counts [E], routing [P], then per batch a table [3 E]
+    // and an active list [E + 1], then the combine's table [3 E]
+    const size_t tab_n = size_t(3) * E, act_n = size_t(E) + 1;
+    const size_t o_idx = al256(size_t(E) * 4), o_tabs = o_idx + al256(size_t(P) * 4),
+                 o_acts = o_tabs + al256(size_t(E + 1) * tab_n * sizeof(void *)), host_bytes = o_acts + size_t(E) * act_n * 4;
+    void *hst = nullptr;
+    if (!rc) rc = vh_host_staging(host_bytes, &hst);
     if (rc) return rc;
-    const uint64_t cap = vh_store_capacity(m->es);
+    char *hb8 = static_cast<char *>(hst);
+    int32_t *counts = reinterpret_cast<int32_t *>(hb8);
+    int32_t *idx_h = reinterpret_cast<int32_t *>(hb8 + o_idx);
+    const void **tabs_h = reinterpret_cast<const void **>(hb8 + o_tabs);
+    int32_t *acts_h = reinterpret_cast<int32_t *>(hb8 + o_acts);
+    rc = vh_check(hipMemcpyAsync(counts, ws.counts, size_t(E) * 4, hipMemcpyDeviceToHost, s));
+    if (!rc) rc = vh_check(hipMemcpyAsync(idx_h, idx, size_t(P) * 4, hipMemcpyDeviceToHost, s));
+    if (!rc) rc = vh_check(hipStreamSynchronize(s));
+    if (rc) return rc;
+    vh_store_note_routing_host(m->es, layer, idx_h, n_tokens, k);
+    hipStream_t cs;
+    if ((rc = vh_copy_stream(&cs))) return rc;
+    const uint64_t cap = vh_store_capacity(m->es), leased = vh_store_leased_bytes(m->es);
+    const uint64_t room = cap > leased ? cap - leased : 1;  // cap 0: unbounded (room unused)
     const bool gdec = n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
-    const void *tab[3 * kMaxExperts], *present[3 * kMaxExperts];
+    const void **present = tabs_h + size_t(E) * tab_n;  // the combine's table (the last one)
+    memset(present, 0, tab_n * sizeof(void *));
     ExpertView views[kMaxExperts];
-    int32_t act[kMaxExperts + 1];
-    memset(present, 0, sizeof(void *) * 3 * size_t(E));
-    int e0 = 0;
+    int e0 = 0, nb = 0;
     while (!rc) {
         while (e0 < E && counts[e0] == 0) e0++;
         if (e0 == E) break;
         // the next batch: routed experts in id order while their bytes fit (at least one)
-        int n = 0;
+        const void **tab = tabs_h + size_t(nb) * tab_n;
+        int32_t *act = acts_h + size_t(nb) * act_n;
+        int n = 0, e1 = e0;
         uint64_t bytes = 0;
-        int e1 = e0;
         for (; e1 < E; e1++) {
             if (counts[e1] == 0) continue;
             const uint64_t b = vh_store_expert_bytes(m->es, layer, e1);
-            if (n && cap && bytes + b > cap) break;
+            if (n && cap && bytes + b > room) break;
             bytes += b;
             act[n++] = e1;
         }
-        memset(tab, 0, sizeof(void *) * 3 * size_t(E));
+        memset(tab, 0, tab_n * sizeof(void *));
         int got = 0;
         for (int i = 0; i < n && !rc; i++) {
             const int e = act[i];
-            const int lr = expert_store_lookup(m->es, layer, e, &views[e]);
+            const int lr = vh_store_acquire(m->es, layer, e, &views[e], cs);
             if (lr == -1) continue;  // unregistered: skipped (src/gguf_run.c:201)
             if (lr) { rc = lr; break; }
             tab[3 * e] = views[e].gate;
@@ -374,26 +413,33 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
         }
         act[E] = got;
         if (!rc && got) {
-            rc = vh_check(hipMemcpy(ws.tab, tab, sizeof(void *) * 3 * size_t(E), hipMemcpyHostToDevice));
-            if (!rc) rc = vh_check(hipMemcpy(ws.act, act, size_t(E + 1) * 4, hipMemcpyHostToDevice));
-            const void *const *dt = ws.tab;
+            const void **dt = ws.tab + size_t(nb) * tab_n;
+            int32_t *da = ws.act + size_t(nb) * act_n;
+            rc = vh_store_copy_fence(m->es, cs, s);  // the batch's page-ins land before its kernels
+            if (!rc) rc = vh_check(hipMemcpyAsync(dt, tab, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
+            if (!rc) rc = vh_check(hipMemcpyAsync(da, act, act_n * 4, hipMemcpyHostToDevice, s));
             if (gdec) {
-                if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
-                if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
+                if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, da, dt, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
+                if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
             } else {
-                if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.act, dt, hb, d, fe, k, E, slots, ws.h, s);
-                if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.act, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
+                if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, da, dt, hb, d, fe, k, E, slots, ws.h, s);
+                if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, ws.ybuf, s);
             }
-            const int sr = vh_check(hipStreamSynchronize(s));  // the batch's kernels are done with its experts
-            if (!rc) rc = sr;
         }
-        for (int i = 0; i < got; i++) expert_store_release(m->es, &views[act[i]]);
+        if (rc) (void)hipStreamSynchronize(s);  // nothing enqueued may outlive the leases dropped below
+        for (int i = 0; i < got; i++) {
+            const int dr = vh_store_drop(m->es, &views[act[i]], s);
+            if (!rc) rc = dr;
+        }
+        nb++;
         e0 = e1;
     }
     // the combine reads only whether each expert was found
-    if (!rc) rc = vh_check(hipMemcpy(ws.tab, present, sizeof(void *) * 3 * size_t(E), hipMemcpyHostToDevice));
-    if (!rc) rc = vh_combine(idx, w, ws.tab, ws.ybuf, d, k, n_tokens, x, s);
-    return rc;
+    const void **dt = ws.tab + size_t(nb) * tab_n;
+    if (!rc) rc = vh_check(hipMemcpyAsync(dt, present, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
+    if (!rc) rc = vh_combine(idx, w, dt, ws.ybuf, d, k, n_tokens, x, s);
+    const int hr = vh_host_staging_done(s);
+    return rc ? rc : hr;
 }
 
 extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
@@ -402,16 +448,16 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (n_tokens < 0 || (n_tokens && (!x || !hb))) return -EINVAL;
     if (n_tokens == 0) return 0;
     const vireo_moe_layer &L = m->layers[layer];
-    if (!L.gate_exps || !L.up_exps || !L.down_exps || !m->es) return -EINVAL;
+    if (!L.gate_exps || !L.up_exps || !L.down_exps) return -EINVAL;
     const uint32_t tg = L.gate_exps->ggml_type, tu = L.up_exps->ggml_type, td = L.down_exps->ggml_type;
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
     if (tg != tu || !type_ok(tg, d) || !type_ok(td, fe) || fe % 4) return -EINVAL;
     if (int64_t(n_tokens) * k > 65535 || n_tokens > 65535) return -E2BIG;
     const void *const *table = nullptr;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (int rc = expert_store_pin_layer(m->es, layer, &table)) {
-        if (rc != -ENOSPC) return rc;
-        // the layer does not fit the store: page its routed experts per call
+    if (int lt = layer_table(m, layer, &table)) {
+        if (lt < 0) return lt;
+        // the store does not hold every layer: page the routed experts per call
         return vh_finish(s, paged_forward(m, layer, x, hb, n_tokens, idx_out, w_out, s));
     }
     const float *R = static_cast<const float *>(L.router->data);
@@ -430,7 +476,10 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         rc = 0;
         for (int stage = 0; stage < 3 && !rc; stage++)
             rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s);
-        return vh_finish(s, rc);
+        if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
+        rc = vh_finish(s, rc);
+        if (!rc && !s && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
+        return rc;
     }
     const bool exact = n_tokens >= kExactRouteTokens;
     const int P = n_tokens * k, slots = P < E ? P : E;
@@ -453,5 +502,6 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     }
     if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
+    if (!rc) rc = vh_store_note_routing(m->es, layer, idx, n_tokens, k, s);
     return vh_finish(s, rc);
 }

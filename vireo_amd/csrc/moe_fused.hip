@@ -22,8 +22,10 @@
 //   5. reads the activations of its down expert, computes its down rows and
 //      combines the k experts' rows in selection order into x.
 // Every wait is bounded: a workgroup that waits too long records
-// VIREO_DECODE_TIMEOUT in the token's flag word and goes on (the result is
-// then not valid), so no launch can hang.
+// VIREO_DECODE_TIMEOUT in the token's flag word and in the device's sticky
+// status word and goes on (the result is then not valid), so no launch can
+// hang; synchronous calls report it as -ETIMEDOUT, stream calls through
+// vireo_hip_status.
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
@@ -33,7 +35,6 @@
 namespace {
 
 constexpr int kFusedWaves = 8;      // = k: wave wv owns the down rows of round wv
-constexpr unsigned kSpinLimit = 1u << 18;
 
 // 16 bytes at byte offset off of p with the sc1 policy (bypass the L2 of this
 // die, which other dies do not keep coherent); reads past `bytes` return zeros.
@@ -49,7 +50,7 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
     const RoutePart *__restrict__ parts, const float *__restrict__ hb, const void *const *__restrict__ table, int E,
     int k, int fe, int d, int renorm, int64_t rb_gu, int64_t rb_dn, const float *__restrict__ R,
     const float *__restrict__ bias, float *__restrict__ h, uint32_t *__restrict__ bar, float *__restrict__ x,
-    int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+    int32_t *__restrict__ idx_out, float *__restrict__ w_out, uint32_t *__restrict__ status, unsigned spin_limit) {
     using FG = Reg<TG>;
     using FD = Reg<TD>;
     constexpr int NSG = FG::NS, NSD = FD::NS, TPL = 3 * Q, SUB = 64 / L;
@@ -163,15 +164,19 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
     {
         const int nb = int(gridDim.x);
         const uint32_t *mine = bar + wv * nb;
-        unsigned spins = 0;
-        for (;;) {
+        // at most spin_limit polls (0: give up at once, which lets a test
+        // take the error path with every wave exiting normally)
+        for (unsigned spins = 0;; spins++) {
+            if (spins >= spin_limit) {
+                if (lane == 0) {
+                    atomicOr(flag_out, VIREO_DECODE_TIMEOUT);
+                    atomicOr(status, VIREO_DECODE_TIMEOUT);
+                }
+                break;
+            }
             const bool set = lane >= nb || __hip_atomic_load(const_cast<uint32_t *>(mine) + lane, __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_AGENT) != 0u;
             if (__ballot(set) == __builtin_amdgcn_read_exec()) break;
-            if (++spins > kSpinLimit) {
-                if (lane == 0) atomicOr(flag_out, VIREO_DECODE_TIMEOUT);
-                break;
-            }
         }
     }
     asm volatile("" ::: "memory");
@@ -236,8 +241,10 @@ int launch_experts(const RoutePart *parts, const float *R, const float *hb, cons
                                                                                : int64_t(d / 256) * 210;
     const int64_t rb_dn = TD == VT_Q8_0 ? int64_t(fe / 32) * 34 : TD == VT_Q4_K ? int64_t(fe / 256) * 144
                                                                                 : int64_t(fe / 256) * 210;
+    uint32_t *status = nullptr;
+    if (int rc = vh_status_word(&status)) return rc;
     VH_LAUNCH((decode_experts_kernel<TG, TD, Q, RPW, L, IPL, UPG>), g, dim3(64 * kFusedWaves), 0, s, parts, hb, table,
-              E, k, fe, d, renorm, rb_gu, rb_dn, R, bias, h, bar, x, idx, w);
+              E, k, fe, d, renorm, rb_gu, rb_dn, R, bias, h, bar, x, idx, w, status, vh_spin_limit());
     return vh_check(hipGetLastError());
 }
 

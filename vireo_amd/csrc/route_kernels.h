@@ -16,10 +16,26 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
 // One MoE layer of a stack for one token: xb = rmsnorm(x, nw); x += moe(xb).
 // The one-token decode plan folds the RMSNorm into its router launch; other
 // shapes run vireo_rmsnorm and moe_ffn_forward.
-// Bytes of a registered expert in the store's pool (0 if unregistered) and
-// the pool's capacity (0 = unbounded) (expert_store.c).
-extern "C" uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert);
-extern "C" uint64_t vh_store_capacity(const ExpertStore *s);
+// ExpertStore internals for the MoE plans (expert_store.c): an expert's bytes
+// in the pool (0 if unregistered), the capacity (0 = unbounded), whether a
+// store is one of this library's, a pinned layer's table (NULL if none; never
+// allocates), whether every layer fits at once, the bytes that hold leases,
+// lookups / lease drops for paged calls (page-ins on a copy stream, blocks
+// protected by events until the kernels that read them are done), and the
+// routing copies that feed the reference's statistics.
+extern "C" {
+uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert);
+uint64_t vh_store_capacity(const ExpertStore *s);
+int vh_store_valid(const ExpertStore *s);
+const void *const *vh_store_layer_table(const ExpertStore *s, int layer);
+int vh_store_fits_all(const ExpertStore *s);
+uint64_t vh_store_leased_bytes(const ExpertStore *s);
+int vh_store_acquire(ExpertStore *s, int layer, int expert, ExpertView *view, hipStream_t cs);
+int vh_store_drop(ExpertStore *s, ExpertView *view, hipStream_t stream);
+int vh_store_copy_fence(ExpertStore *s, hipStream_t cs, hipStream_t stream);
+int vh_store_note_routing(ExpertStore *s, int layer, const int32_t *idx_dev, int T, int k, hipStream_t stream);
+void vh_store_note_routing_host(ExpertStore *s, int layer, const int32_t *idx, int T, int k);
+}
 
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
                         hipStream_t s);
@@ -104,7 +120,6 @@ int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32
 // bar[0 .. kFusedBlocks) (zeroed by vh_route_parts); bar[kFusedBlocks] is the
 // token's flag word (VIREO_ROUTE_* bits, VIREO_DECODE_TIMEOUT).
 constexpr int kFusedBlocks = 256;
-constexpr uint32_t VIREO_DECODE_TIMEOUT = 4u;
 int vh_fused_blocks(uint32_t tg, uint32_t td, int d, int E, int k, int fe);  // kFusedBlocks, or 0 if not built for it
 int vh_decode_experts(uint32_t tg, uint32_t td, const RoutePart *parts, const float *R, const float *hb,
                       const float *bias, int d, int E, int k, int fe, int renorm, const void *const *table, float *h,

@@ -17,7 +17,14 @@ struct DevState {
     void *red = nullptr;
     size_t red_bytes = 0;
     int cus = 0;
+    hipStream_t copy = nullptr;   // expert page-in copies
+    void *host = nullptr;         // pinned staging for small uploads
+    size_t host_bytes = 0;
+    hipEvent_t host_done = nullptr;
+    bool host_done_set = false;
+    uint32_t *status = nullptr;   // sticky device status bits (VIREO_DECODE_TIMEOUT)
 };
+unsigned g_spin_limit = 1u << 18;
 DevState g_dev[kMaxDev];
 thread_local char g_err[256];
 
@@ -55,46 +62,48 @@ int vh_num_cus() {
     return g_dev[d].cus;
 }
 
-// Grow-only scratch. Growing synchronises the device first, because earlier
-// enqueued kernels may still read the old buffer.
+// Grow-only device buffers. A buffer that is outgrown is not freed: kernels
+// already enqueued and HIP graphs captured over earlier calls keep reading
+// and writing the old one, so it stays allocated until the process ends.
+// Each growth at least doubles, so the retired buffers together are no
+// larger than the current one.
+int grow_device(void **buf, size_t *bytes, size_t need, size_t floor) {
+    if (need <= *bytes) return 0;
+    size_t nb = need < floor ? floor : need;
+    if (nb < 2 * *bytes) nb = 2 * *bytes;
+    nb = (nb + 0xffff) & ~size_t(0xffff);
+    void *p = nullptr;
+    if (int rc = vh_check(hipMalloc(&p, nb))) return rc == -EIO ? -ENOMEM : rc;
+    *buf = p;  // the old buffer is retired, not freed
+    *bytes = nb;
+    return 0;
+}
+
 int vh_device_workspace(size_t bytes, void **out) {
     int d = cur_dev();
     if (d < 0) return -ENODEV;
     DevState &st = g_dev[d];
-    if (bytes > st.ws_bytes) {
-        size_t nb = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-        nb = (nb + 0xffff) & ~size_t(0xffff);
-        if (st.ws) {
-            if (int rc = vh_check(hipDeviceSynchronize())) return rc;
-            if (int rc = vh_check(hipFree(st.ws))) return rc;
-            st.ws = nullptr;
-            st.ws_bytes = 0;
-        }
-        if (int rc = vh_check(hipMalloc(&st.ws, nb))) return rc == -EIO ? -ENOMEM : rc;
-        st.ws_bytes = nb;
-    }
+    if (int rc = grow_device(&st.ws, &st.ws_bytes, bytes, size_t(1) << 20)) return rc;
     *out = st.ws;
     return 0;
 }
 
-// Arrival counters for "last block finishes the job" kernels. They are zeroed
-// once here; every kernel that uses one returns it to zero before it exits.
+// Arrival counters for "last block finishes the job" kernels. Every kernel
+// that uses one returns it to zero before it exits; a new (larger) set is
+// zeroed once here.
 int vh_counters(int n, unsigned **out) {
     int d = cur_dev();
     if (d < 0) return -ENODEV;
     DevState &st = g_dev[d];
     if (n > st.ctr_n) {
-        int nn = n < 4096 ? 4096 : n;
-        if (st.ctr) {
-            if (int rc = vh_check(hipDeviceSynchronize())) return rc;
-            if (int rc = vh_check(hipFree(st.ctr))) return rc;
-            st.ctr = nullptr;
-            st.ctr_n = 0;
-        }
-        if (int rc = vh_check(hipMalloc(&st.ctr, sizeof(unsigned) * nn))) return rc;
-        if (int rc = vh_check(hipMemset(st.ctr, 0, sizeof(unsigned) * nn))) return rc;
+        void *p = st.ctr;
+        size_t b = size_t(st.ctr_n) * sizeof(unsigned);
+        const size_t need = sizeof(unsigned) * size_t(n < 4096 ? 4096 : n);
+        if (int rc = grow_device(&p, &b, need, need)) return rc;
+        if (int rc = vh_check(hipMemset(p, 0, b))) return rc;
         if (int rc = vh_check(hipDeviceSynchronize())) return rc;
-        st.ctr_n = nn;
+        st.ctr = static_cast<unsigned *>(p);
+        st.ctr_n = int(b / sizeof(unsigned));
     }
     *out = st.ctr;
     return 0;
@@ -106,18 +115,90 @@ int vh_reduce_scratch(size_t bytes, void **out) {
     int d = cur_dev();
     if (d < 0) return -ENODEV;
     DevState &st = g_dev[d];
-    if (bytes > st.red_bytes) {
-        const size_t nb = (bytes + 0xffff) & ~size_t(0xffff);
-        if (st.red) {
-            if (int rc = vh_check(hipDeviceSynchronize())) return rc;
-            if (int rc = vh_check(hipFree(st.red))) return rc;
-            st.red = nullptr;
-            st.red_bytes = 0;
-        }
-        if (int rc = vh_check(hipMalloc(&st.red, nb))) return rc;
-        st.red_bytes = nb;
-    }
+    if (int rc = grow_device(&st.red, &st.red_bytes, bytes, size_t(1) << 16)) return rc;
     *out = st.red;
+    return 0;
+}
+
+int vh_copy_stream(hipStream_t *out) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (!st.copy && vh_check(hipStreamCreateWithFlags(&st.copy, hipStreamNonBlocking))) {
+        st.copy = nullptr;
+        return -EIO;
+    }
+    *out = st.copy;
+    return 0;
+}
+
+int vh_host_staging(size_t bytes, void **out) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (st.host_done_set) {
+        if (int rc = vh_check(hipEventSynchronize(st.host_done))) return rc;
+        st.host_done_set = false;
+    }
+    if (bytes > st.host_bytes) {  // nothing reads the old buffer any more (waited above)
+        if (st.host) (void)hipHostFree(st.host);
+        st.host = nullptr;
+        st.host_bytes = 0;
+        const size_t nb = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : 2 * bytes;
+        if (vh_check(hipHostMalloc(&st.host, nb, 0))) { st.host = nullptr; return -ENOMEM; }
+        st.host_bytes = nb;
+    }
+    *out = st.host;
+    return 0;
+}
+
+int vh_host_staging_done(hipStream_t s) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (!st.host_done && vh_check(hipEventCreateWithFlags(&st.host_done, hipEventDisableTiming))) {
+        st.host_done = nullptr;
+        return -EIO;
+    }
+    if (int rc = vh_check(hipEventRecord(st.host_done, s))) return rc;
+    st.host_done_set = true;
+    return 0;
+}
+
+int vh_status_word(uint32_t **out) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (!st.status) {
+        void *p = nullptr;
+        if (int rc = vh_check(hipMalloc(&p, 256))) return rc == -EIO ? -ENOMEM : rc;
+        if (int rc = vh_check(hipMemset(p, 0, 256))) return rc;
+        if (int rc = vh_check(hipDeviceSynchronize())) return rc;
+        st.status = static_cast<uint32_t *>(p);
+    }
+    *out = st.status;
+    return 0;
+}
+
+unsigned vh_spin_limit() { return g_spin_limit; }
+
+// Read and clear the sticky status bits after the stream's work is done.
+int vh_take_status(hipStream_t s) {
+    uint32_t *w = nullptr;
+    if (int rc = vh_status_word(&w)) return rc;
+    if (int rc = vh_check(hipStreamSynchronize(s))) return rc;
+    uint32_t v = 0;
+    if (int rc = vh_check(hipMemcpy(&v, w, 4, hipMemcpyDeviceToHost))) return rc;
+    if (!v) return 0;
+    if (int rc = vh_check(hipMemset(w, 0, 4))) return rc;
+    if (int rc = vh_check(hipDeviceSynchronize())) return rc;
+    return (v & VIREO_DECODE_TIMEOUT) ? -ETIMEDOUT : 0;
+}
+
+extern "C" int vireo_hip_status(void *stream) { return vh_take_status(static_cast<hipStream_t>(stream)); }
+
+extern "C" int vireo_hip_set_spin_limit(unsigned polls) {
+    g_spin_limit = polls;
     return 0;
 }
 
@@ -138,6 +219,7 @@ extern "C" const char *vireo_hip_strerror(int err) {
     case -ENOSPC: return "ExpertStore capacity below the experts that must stay resident";
     case -E2BIG: return "size exceeds a kernel limit";
     case -EIO: return "HIP runtime or I/O failure";
+    case -ETIMEDOUT: return "a grid-wide wait gave up (not every workgroup was resident): results invalid";
     default: return strerror(err < 0 ? -err : err);
     }
 }

@@ -180,8 +180,15 @@ class GGUFModel:
                                            _ptr(logits), _stream(stream)), "moe_stack_step")
 
     def stats(self):
+        """The reference's ExpertStats for the work done so far (expert_store_stats)."""
         st = _lib.ExpertStats()
         self.lib.expert_store_stats(self.p.contents.model.es, C.byref(st))
+        return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
+
+    def hbm_stats(self):
+        """What the HBM pool did (expert_store_hbm_stats)."""
+        st = _lib.ExpertStats()
+        self.lib.expert_store_hbm_stats(self.p.contents.model.es, C.byref(st))
         return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
 
     def close(self):

@@ -180,8 +180,15 @@ class DeviceMoE:
         return buf[off:off + n * stride].view(n, stride)
 
     def stats(self):
+        """The reference's ExpertStats for the work done so far (expert_store_stats)."""
         st = _lib.ExpertStats()
         self.lib.expert_store_stats(self.es, C.byref(st))
+        return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
+
+    def hbm_stats(self):
+        """What the HBM pool did (expert_store_hbm_stats)."""
+        st = _lib.ExpertStats()
+        self.lib.expert_store_hbm_stats(self.es, C.byref(st))
         return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
 
     # -- host copies of the same bytes, for the checkers ----------------------
