@@ -167,6 +167,22 @@ int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts,
 int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
                     int32_t *idx_out, float *w_out, void *stream);
 
+/* moe_ffn_forward for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc): no counterpart in
+ * the reference. The same results as moe_ffn_forward, but every intermediate
+ * lives in a fixed 32 MiB region of device memory that the library holds per
+ * device from its first use (vireo_hip_init, or the first call on a device)
+ * until the process ends, and the call makes no allocation of any kind.
+ * Limits: the layer must already be resident and pinned
+ * (expert_store_pin_layer, or one earlier moe_ffn_forward on it; else
+ * -EINVAL); calls whose intermediates exceed the region return -E2BIG (about
+ * 300 tokens for the Qwen3-30B-A3B layer); the fused plan (vireo_hip_set_path
+ * 3) is not used; calls are not counted in expert_store_stats. Every call on a
+ * device shares the region, which keeps the last call's contents: calls that
+ * may overlap on one device (other streams, other threads) race. */
+int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
+                            int32_t *idx_out, float *w_out, void *stream);
+
 /* Execution plan for moe_ffn_forward (a tuning and testing knob; no
  * counterpart in the reference): 0 = automatic (default), 1 = the one-token
  * decode plan whenever it applies, 2 = always the grouped plan, 3 = the

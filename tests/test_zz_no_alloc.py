@@ -1,0 +1,73 @@
+"""moe_ffn_forward_noalloc: the entry point for callers that cannot allocate
+(its workspace is a fixed static device region). Its results equal
+moe_ffn_forward's bit for bit on the same inputs (the same kernels run), on
+consecutive calls whose second is smaller than the first, on every plan it
+takes (matrix-core groups, decode-batch groups, the one-token decode plan);
+it refuses calls whose intermediates exceed the region (-E2BIG) and layers
+that are not pinned yet (-EINVAL), and it allocates no device memory."""
+import ctypes as C
+import errno
+
+import numpy as np
+import pytest
+import torch
+
+from vireo_amd import _lib
+from vireo_amd import moe as M
+from vireo_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(lib, fn, m, layer, x, hb, T, idx, w):
+    return fn(C.byref(m.model), layer, C.c_void_p(x.data_ptr()), C.c_void_p(hb.data_ptr()), T,
+              C.c_void_p(idx.data_ptr()), C.c_void_p(w.data_ptr()), None)
+
+
+def test_noalloc_matches_moe_ffn_forward(cuda, lib):
+    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
+    m = M.DeviceMoE(shape, 2, seed=91)
+    sizes = [(0, 96), (1, 5), (0, 1), (1, 1)]  # each call smaller than (or as small as) the one before
+    inputs = {}
+    for layer, T in sizes:
+        x, hb = W.host_hidden(shape.d, T, 91 + T)
+        inputs[(layer, T)] = (x, torch.from_numpy(hb).to(cuda))
+    # refused before the layer is pinned: pinning allocates
+    x0, hb0 = inputs[(1, 5)]
+    xg = torch.from_numpy(x0).to(cuda)
+    idx = torch.empty((5, shape.k), dtype=torch.int32, device=cuda)
+    w = torch.empty((5, shape.k), dtype=torch.float32, device=cuda)
+    assert _call(lib, lib.moe_ffn_forward_noalloc, m, 1, xg, hb0, 5, idx, w) == -errno.EINVAL
+    # the reference results (this also pins both layers)
+    want = {}
+    for layer, T in sizes:
+        x, hb = inputs[(layer, T)]
+        xr = torch.from_numpy(x).to(cuda)
+        ir = torch.empty((T, shape.k), dtype=torch.int32, device=cuda)
+        wr = torch.empty((T, shape.k), dtype=torch.float32, device=cuda)
+        _lib.check(_call(lib, lib.moe_ffn_forward, m, layer, xr, hb, T, ir, wr), "moe_ffn_forward")
+        want[(layer, T)] = (xr.cpu().numpy(), ir.cpu().numpy(), wr.cpu().numpy())
+    outs = {}
+    for layer, T in sizes:
+        x, hb = inputs[(layer, T)]
+        outs[(layer, T)] = (torch.from_numpy(x).to(cuda), torch.empty((T, shape.k), dtype=torch.int32, device=cuda),
+                            torch.empty((T, shape.k), dtype=torch.float32, device=cuda))
+    big_x = torch.zeros((2048, shape.d), dtype=torch.float32, device=cuda)
+    big_i = torch.empty((2048, shape.k), dtype=torch.int32, device=cuda)
+    big_w = torch.empty((2048, shape.k), dtype=torch.float32, device=cuda)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for layer, T in sizes:
+        x, hb = inputs[(layer, T)]
+        xo, io, wo = outs[(layer, T)]
+        _lib.check(_call(lib, lib.moe_ffn_forward_noalloc, m, layer, xo, hb, T, io, wo), "moe_ffn_forward_noalloc")
+    # a call whose intermediates exceed the fixed region
+    assert _call(lib, lib.moe_ffn_forward_noalloc, m, 0, big_x, big_x, 2048, big_i, big_w) == -errno.E2BIG
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0, "device memory was allocated"
+    for key, (xo, io, wo) in outs.items():
+        xw, iw, ww = want[key]
+        np.testing.assert_array_equal(io.cpu().numpy(), iw, err_msg=str(key))
+        np.testing.assert_array_equal(wo.cpu().numpy(), ww, err_msg=str(key))
+        np.testing.assert_array_equal(xo.cpu().numpy(), xw, err_msg=str(key))
+    m.close()

@@ -194,6 +194,7 @@ SIGNATURES = {
     "moe_decode_stage_timed": (C.c_int, [C.POINTER(MoEModel), C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp, C.c_int64,
                                          c_vp, c_vp, c_vp, c_vp]),
     "moe_ffn_forward": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp]),
+    "moe_ffn_forward_noalloc": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp]),
     "expert_store_create": (c_vp, [C.c_int, C.c_uint64, C.c_int, C.c_int]),
     "expert_store_create_device": (c_vp, [c_vp, C.c_uint64, C.c_uint64, C.c_int, C.c_int]),
     "expert_store_register": (None, [c_vp, C.c_int, C.c_int, C.POINTER(ExpertSlices)]),

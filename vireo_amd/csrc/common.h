@@ -39,6 +39,9 @@ int vh_host_staging_done(hipStream_t s);
 int vh_status_word(uint32_t **out);
 unsigned vh_spin_limit();
 int vh_take_status(hipStream_t s);
+// This device's address of moe_ffn_forward_noalloc's static scratch (moe.hip),
+// looked up once per device; out may be NULL.
+int vh_noalloc_setup(void **out);
 // bytes of a row of n weights of ggml type t (src/gguf.c:27-38; F32 otherwise)
 inline int64_t vh_row_bytes(uint32_t t, int n) {
     switch (t) {

@@ -61,8 +61,16 @@ struct Ws {
     int32_t *act;            // paged plan: [E] active lists [E + 1] (one per batch)
 };
 
+// Where a call's workspace comes from: the library's grow-only per-device
+// buffer (base == nullptr), or a fixed region of cap bytes that is never
+// grown (the scratch of moe_ffn_forward_noalloc).
+struct WsSource {
+    char *base;
+    size_t cap;
+};
+
 int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *ws, bool mfma = false,
-           bool paged = false) {
+           bool paged = false, const WsSource *src = nullptr) {
     const size_t P = size_t(T) * k;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
@@ -81,7 +89,12 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
     const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
     void *base;
-    if (int rc = vh_device_workspace(off, &base)) return rc;
+    if (src && src->base) {
+        if (off > src->cap) return -E2BIG;
+        base = src->base;
+    } else if (int rc = vh_device_workspace(off, &base)) {
+        return rc;
+    }
     char *b = static_cast<char *>(base);
     ws->parts = reinterpret_cast<RoutePart *>(b + o_parts);
     ws->idx = reinterpret_cast<int32_t *>(b + o_idx);
@@ -156,7 +169,8 @@ bool fused(const vireo_moe_model *m, int layer) {
 // stage 2 has nothing left to do), else top-k + gate/up. Stage 2: down +
 // combine.
 int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *const *table, float *x,
-                 const float *hb, const DecodeState &st, int32_t *idx, float *w, hipStream_t s) {
+                 const float *hb, const DecodeState &st, int32_t *idx, float *w, hipStream_t s,
+                 bool allow_fused = true) {
     const vireo_moe_layer &L = m->layers[layer];
     const float *R = static_cast<const float *>(L.router->data);
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
@@ -164,13 +178,13 @@ int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *con
     switch (stage) {
     case 0: return vh_route_parts(R, hb, L.logit_bias, d, E, 1, false, st.parts, s, st.bar, kFusedBlocks + 1);
     case 1:
-        if (fused(m, layer))
+        if (allow_fused && fused(m, layer))
             return vh_decode_experts(tg, td, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h,
                                      st.bar, x, idx, w, s);
         return vh_decode_gateup(tg, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h, idx, w,
                                 st.flags(), st.plan, td, s);
     case 2:
-        if (fused(m, layer)) return 0;
+        if (allow_fused && fused(m, layer)) return 0;
         return vh_down_combine(td, st.plan, st.h, d, fe, k, x, s);
     default: return -EINVAL;
     }
@@ -442,8 +456,14 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     return rc ? rc : hr;
 }
 
-extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
-                               int32_t *idx_out, float *w_out, void *stream) {
+namespace {
+
+// moe_ffn_forward; with src, on a fixed workspace and allocating nothing: the
+// layer must already be pinned (the paged plan and the first pin allocate),
+// the fused plan is not used (its status word is allocated on first use) and
+// the routing is not copied for the store's statistics (its host ring is).
+int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
+                float *w_out, hipStream_t s, const WsSource *src) {
     if (int rc = check_model(m, layer)) return rc;
     if (n_tokens < 0 || (n_tokens && (!x || !hb))) return -EINVAL;
     if (n_tokens == 0) return 0;
@@ -454,8 +474,9 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     if (tg != tu || !type_ok(tg, d) || !type_ok(td, fe) || fe % 4) return -EINVAL;
     if (int64_t(n_tokens) * k > 65535 || n_tokens > 65535) return -E2BIG;
     const void *const *table = nullptr;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (int lt = layer_table(m, layer, &table)) {
+    if (src) {
+        if (!vh_store_valid(m->es) || !(table = vh_store_layer_table(m->es, layer))) return -EINVAL;
+    } else if (int lt = layer_table(m, layer, &table)) {
         if (lt < 0) return lt;
         // the store does not hold every layer: page the routed experts per call
         return vh_finish(s, paged_forward(m, layer, x, hb, n_tokens, idx_out, w_out, s));
@@ -467,7 +488,7 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
     const bool mfma = !decode && g_path != 4 && n_tokens >= kMfmaMinCall && vh_mfma_supported(tg, td, d, fe, E) &&
                       (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
     Ws ws;
-    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws, mfma)) return rc;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws, mfma, false, src)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
@@ -475,10 +496,10 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
         rc = 0;
         for (int stage = 0; stage < 3 && !rc; stage++)
-            rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s);
-        if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
+            rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s, !src);
+        if (!rc && !src) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
         rc = vh_finish(s, rc);
-        if (!rc && !s && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
+        if (!rc && !s && !src && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
         return rc;
     }
     const bool exact = n_tokens >= kExactRouteTokens;
@@ -502,6 +523,44 @@ extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, co
         if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     }
     if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
-    if (!rc) rc = vh_store_note_routing(m->es, layer, idx, n_tokens, k, s);
+    if (!rc && !src) rc = vh_store_note_routing(m->es, layer, idx, n_tokens, k, s);
     return vh_finish(s, rc);
+}
+
+// The workspace of moe_ffn_forward_noalloc: a fixed region of device memory
+// in the library's code object (each device holds its own copy until the
+// process ends), shared by every such call on a device.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+void *g_scratch_dev[64];  // per device: scratch's device address (host code never uses the symbol itself)
+
+}  // namespace
+
+// Look up this device's address of `scratch` once (from vireo_hip_init, or the
+// first moe_ffn_forward_noalloc on a device).
+int vh_noalloc_setup(void **out) {
+    int dev = 0;
+    if (int rc = vh_check(hipGetDevice(&dev))) return rc;
+    if (dev < 0 || dev >= 64) return -ENODEV;
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        if (int rc = vh_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))) return rc;
+        if (!p) return -EIO;
+        g_scratch_dev[dev] = p;
+    }
+    if (out) *out = g_scratch_dev[dev];
+    return 0;
+}
+
+extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
+                               int32_t *idx_out, float *w_out, void *stream) {
+    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), nullptr);
+}
+
+extern "C" int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
+                                       int32_t *idx_out, float *w_out, void *stream) {
+    void *base = nullptr;
+    if (int rc = vh_noalloc_setup(&base)) return rc;
+    const WsSource src{static_cast<char *>(base), kNoAllocScratchBytes};
+    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), &src);
 }

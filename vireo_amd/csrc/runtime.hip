@@ -206,7 +206,8 @@ extern "C" int vireo_hip_init(int device) {
     int n = 0;
     if (int rc = vh_check(hipGetDeviceCount(&n))) return rc;
     if (device < 0 || device >= n || device >= kMaxDev) return -EINVAL;
-    return vh_check(hipSetDevice(device));
+    if (int rc = vh_check(hipSetDevice(device))) return rc;
+    return vh_noalloc_setup(nullptr);  // the static scratch's address on this device
 }
 
 extern "C" const char *vireo_hip_strerror(int err) {
@@ -217,7 +218,7 @@ extern "C" const char *vireo_hip_strerror(int err) {
     case -ENOMEM: return "out of device or host memory";
     case -ENODEV: return "no HIP device";
     case -ENOSPC: return "ExpertStore capacity below the experts that must stay resident";
-    case -E2BIG: return "size exceeds a kernel limit";
+    case -E2BIG: return "size exceeds a kernel limit or the fixed scratch of an entry point that allocates nothing";
     case -EIO: return "HIP runtime or I/O failure";
     case -ETIMEDOUT: return "a grid-wide wait gave up (not every workgroup was resident): results invalid";
     default: return strerror(err < 0 ? -err : err);
