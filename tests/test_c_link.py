@@ -55,3 +55,49 @@ def test_foreign_store_refused(tmp_path):
          "-o", exe, *LDFLAGS], tmp_path)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_c_caller_runs_against_oracle(cuda, oracle, tmp_path):
+    """tests/c/moe_caller.c on a synthetic GGUF MoE file: every layer's
+    moe_ffn_forward from C (synchronous, stream NULL) and one stack step
+    match the oracle on the bytes written into the file."""
+    import numpy as np
+    from conftest import expert_lists
+    from vireo_amd import gguf as G
+    from vireo_amd import workloads as W
+    exe = str(tmp_path / "moe_caller")
+    gcc([*CFLAGS, os.path.join(CDIR, "moe_caller.c"), "-o", exe, *LDFLAGS], tmp_path)
+    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"].with_(name="qwen3-16e", E=16)
+    L, vocab = 3, 512
+    path = str(tmp_path / "m.gguf")
+    arr = G.write_moe_gguf(path, shape, L, seed=83, vocab=vocab)
+    x, xb = W.host_hidden(shape.d, 1, 83)
+    x, xb = x[0], xb[0]
+    x.tofile(str(tmp_path / "x.bin"))
+    xb.tofile(str(tmp_path / "xb.bin"))
+    r = subprocess.run([exe, path, str(tmp_path / "x.bin"), str(tmp_path / "xb.bin"), str(tmp_path / "out.bin")],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = np.fromfile(str(tmp_path / "out.bin"), np.float32)
+    d = shape.d
+    xo = x.copy()
+    layers = [expert_lists(shape, *arr["experts"][l]) for l in range(L)]
+    for l in range(L):
+        xo = oracle.moe_ffn(shape, arr["routers"][l], *layers[l], xo[None], xb[None])[0][0]
+        got = out[:d] if l == 0 else out[d:2 * d]
+        if l in (0, L - 1):
+            rel = np.abs((got - x) - (xo - x)).max() / np.abs(xo - x).max()
+            assert rel <= 2e-3, (l, rel)
+    # the stack step from token 3 (tied or untied head as written)
+    rb = W.row_bytes(W.Q8_0, d)
+    emb, head = arr["token_embd"], arr["output"]
+    xs = oracle.dequant_row(W.Q8_0, emb[3 * rb:4 * rb], d)
+    for l in range(L):
+        xs = oracle.moe_ffn(shape, arr["routers"][l], *layers[l], xs[None],
+                            oracle.rmsnorm(xs, arr["ffn_norm"][l], W.EPS)[None])[0][0]
+    logits = oracle.matmul(W.Q8_0, head, oracle.rmsnorm(xs, arr["out_norm"], W.EPS), d, vocab)
+    top2 = np.sort(logits)[-2:]
+    if top2[1] - top2[0] > 2e-3 * np.abs(logits).max():
+        assert int(out[2 * d]) == oracle.argmax(logits)
+    print(r.stdout.strip())
