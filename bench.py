@@ -10,15 +10,22 @@ token, so the routed weights stream from HBM rather than from the 256 MB
 last-level cache. The K timed steps are one HIP-graph replay bracketed by
 events on the launch stream.
 
-The roofline object is for the dominant kernel, the decode plan's fused
-top-k + gate/up SwiGLU (stage 1 of moe_decode_stage): the same kernel is
-launched alone over 8 x layers distinct (layer, token) states, and each
-launch's duration comes from HIP events that the dispatch itself records
-(moe_decode_stage_timed); the average of those durations prices it.
+The roofline object prices the whole layer call: its algorithmic bytes
+(router, the distinct routed experts' slices, activations) over the measured
+time per step, against 8 TB/s; prefill is priced by its expert FLOPs against
+the 2.5 PFLOP/s dense bf16 matrix-core peak. `traffic` is the layer's HBM
+bytes from FETCH_SIZE / WRITE_SIZE counter runs (profiles/traffic_*.json,
+made by --traffic from rocprofv3 output). For the one-token decode plan,
+`kernels` prices each of its kernels on its own bytes: each is launched alone
+over 8 x layers distinct (layer, token) states and each launch's duration
+comes from HIP events that the dispatch itself records
+(moe_decode_stage_timed).
 
 cpu_baseline times the reference's own moe_ffn (compiled from its sources
-into oracle/_ref) on a bounded sample of the same workload on the host
-cores, or the oracle's restatement where that library is absent.
+into oracle/_ref) on a bounded sample of the same workload on the host, at 4
+OpenMP threads and at every physical core available (OMP_PROC_BIND=close,
+median of 10 runs, CPU model stated), or the oracle's restatement where that
+library is absent.
 
 Other workloads (--workload) print the same JSON schema: OLMoE shapes,
 batched decode and 2048-token prefill.
@@ -26,16 +33,22 @@ batched decode and 2048-token prefill.
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
-import numpy as np
+# The CPU baseline binds its OpenMP threads to neighbouring cores, as the
+# reference's baseline plan asks; the runtime reads this when it starts.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+
+import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer decode tok/s + achieved HBM GB/s (% of peak); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of one MI355X
 
 WORKLOADS = {
     # name: (shape, tokens per step, layers rotated, router logit bias)
@@ -69,6 +82,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--traffic", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="no GPU run: read four rocprofv3 --pmc output directories (FETCH_SIZE and WRITE_SIZE of "
+                         "this workload, then of --workload copy-512MiB) and write profiles/traffic_<workload>.json")
     ap.add_argument("--plan", type=int, default=0,
                     help="execution plan (vireo_hip_set_path): 0 automatic, 1 decode, 2 grouped, 3 fused, 4 fp32")
     return ap.parse_args()
@@ -80,37 +96,105 @@ def alg_bytes_layer(shape, idx, B):
     return shape.E * shape.d * 4 + distinct * shape.expert_bytes() + 3 * B * shape.d * 4, distinct
 
 
-def alg_bytes_experts(shape):
-    """Fused stage 1 for one token: the k experts' gate, up and down slices,
-    hb, the router parts and expert table it reads, h written and read back,
-    x read and written."""
+def alg_bytes_stages(shape):
+    """Algorithmic bytes of each kernel of the one-token decode plan, each
+    charged with the weights it computes on:
+      route   the F32 router, hb, the router parts written;
+      gate/up the k routed experts' gate and up slices, hb, the parts, the
+              expert table, the k x fe activations written (the down rows it
+              touches ahead of the down kernel are charged to the down kernel);
+      down    the k experts' down slices, the activations, x read and written."""
     gs, us, ds = shape.slice_bytes()
-    return (shape.k * (gs + us + ds) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + 2 * shape.k * shape.fe * 4
-            + 2 * shape.d * 4)
+    E, d, k, fe = shape.E, shape.d, shape.k, shape.fe
+    return {"route": E * d * 4 + d * 4 + E * 16,
+            "topk_gateup": k * (gs + us) + d * 4 + E * 16 + E * 3 * 8 + k * fe * 4,
+            "down_combine": k * ds + k * fe * 4 + 2 * d * 4}
 
 
-def alg_bytes_gateup(shape):
-    """Stage 1 for one token: k experts' gate and up slices, and their down
-    slices too (the kernel loads every 64-byte line of the down rows ahead of
-    the down kernel, so these bytes leave HBM in this kernel), hb, the router
-    parts and expert table it reads, the k x fe activations it writes."""
-    gs, us, ds = shape.slice_bytes()
-    return shape.k * (gs + us + ds) + shape.d * 4 + shape.E * 16 + shape.E * 3 * 8 + shape.k * shape.fe * 4
+def expert_flops(shape, B):
+    """FLOPs of the expert projections of a call: gate, up and down, 2 d fe
+    each per (token, routed expert)."""
+    return 6 * B * shape.k * shape.d * shape.fe
+
+
+def layer_traffic(workload):
+    """HBM bytes per layer call measured with rocprofv3 counters
+    (profiles/traffic_<workload>.json, written by --traffic), or None."""
+    tf = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(tf):
+        return None, None
+    with open(tf) as f:
+        t = json.load(f)
+    return t.get("hbm_bytes_per_layer"), t
+
+
+def host_cpu():
+    """The host's CPU model and the physical cores this process may use: the
+    cores of the CPUs in its affinity mask, capped by OMP_NUM_THREADS where
+    the environment sets it (a GPU machine's share of a larger host)."""
+    model, cores, cur, smt = "unknown", {}, {}, 1
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    cur = {"cpu": int(v)}
+                elif k == "model name":
+                    model = v
+                elif k in ("physical id", "core id", "siblings", "cpu cores"):
+                    cur[k] = v
+                if "cpu" in cur and "physical id" in cur and "core id" in cur:
+                    cores[cur["cpu"]] = (cur["physical id"], cur["core id"])
+                if "siblings" in cur and "cpu cores" in cur and int(cur["cpu cores"]) > 0:
+                    smt = max(1, int(cur["siblings"]) // int(cur["cpu cores"]))
+    except (OSError, ValueError):
+        pass
+    allowed = os.sched_getaffinity(0)
+    phys = len({cores[c] for c in allowed if c in cores})
+    # a virtualised /proc/cpuinfo may give every CPU the same core id: then
+    # count the CPUs available divided by the hardware threads per core
+    phys = max(phys, len(allowed) // smt)
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return model, phys, min(phys, cap) if cap > 0 else phys
+
+
+def _omp_threads(n):
+    """Set the thread count of the OpenMP runtime the reference library uses
+    (the system libgomp, which it links)."""
+    import ctypes
+    ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+
+
+def _timed_runs(run, per_run, runs, first):
+    """runs timings of per_run consecutive tokens each (tokens first,
+    first + 1, ...): microseconds per token of every run."""
+    out, t = [], first
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for _ in range(per_run):
+            run(t)
+            t += 1
+        out.append((time.perf_counter() - t0) / per_run * 1e6)
+    return out, t
 
 
 def cpu_baseline(shape, B, seed, seconds):
     """The reference's moe_ffn on the host: tokens one at a time, as the
-    reference runs them (it has no batched path)."""
+    reference runs them (it has no batched path), weights warm in RAM, with
+    OMP_PROC_BIND=close; timed at 4 OpenMP threads (the reference's default,
+    src/gguf_run.c:267) and at every physical core available, the median of
+    10 runs each. The all-core figure is the value."""
     from vireo_amd import workloads as W
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    model, phys, all_cores = host_cpu()
     g, u, d = W.host_layer(shape, 0, seed)
     router = W.host_router(shape, 0, seed)
-    warm, n_max = 48, 4096
-    x, hb = W.host_hidden(shape.d, warm + n_max, seed, stream=W.stream_id(0, W.KIND_HIDDEN) + 7)
+    warm, n_tok = 24, 4096
+    x, hb = W.host_hidden(shape.d, n_tok, seed, stream=W.stream_id(0, W.KIND_HIDDEN) + 7)
     from oracle.oracle import Reference, RefMoE, Oracle
     if Reference.available():
         rm = RefMoE(Reference(), shape, [router], [g], [u], [d])
-        run = lambda t: rm.run(0, x[t:t + 1], hb[t:t + 1])  # noqa: E731
+        run = lambda t: rm.run(0, x[t % n_tok:t % n_tok + 1], hb[t % n_tok:t % n_tok + 1])  # noqa: E731
         kind = "reference"
     else:
         o = Oracle()
@@ -118,22 +202,38 @@ def cpu_baseline(shape, B, seed, seconds):
         G = [g[e * gs:(e + 1) * gs] for e in range(shape.E)]
         U = [u[e * us:(e + 1) * us] for e in range(shape.E)]
         D = [d[e * ds:(e + 1) * ds] for e in range(shape.E)]
-        run = lambda t: o.moe_ffn(shape, router, G, U, D, x[t:t + 1], hb[t:t + 1])  # noqa: E731
+        run = lambda t: o.moe_ffn(shape, router, G, U, D, x[t % n_tok:t % n_tok + 1],  # noqa: E731
+                                  hb[t % n_tok:t % n_tok + 1])
         rm = None
         kind = "port"
-    for t in range(warm):  # page every expert the sample will touch into RAM
+    runs, res, t = 10, {}, 0
+    for threads in dict.fromkeys((4, all_cores)):
+        if kind == "reference":
+            _omp_threads(threads)
+        for _ in range(warm):  # page every expert the sample will touch into RAM, start the threads
+            run(t)
+            t += 1
+        t0 = time.perf_counter()
         run(t)
-    n, t0 = 0, time.perf_counter()
-    while n < n_max and (time.perf_counter() - t0 < seconds or n < 5):
-        run(warm + n)
-        n += 1
-    dt = time.perf_counter() - t0
+        t += 1
+        one = time.perf_counter() - t0
+        # 10 runs within about seconds / 2 per thread count
+        per_run = max(3, min(200, int(seconds / 2 / runs / max(one, 1e-6))))
+        us, t = _timed_runs(run, per_run, runs, t)
+        res[threads] = (statistics.median(us), per_run, us)
     if rm is not None:
         rm.close()
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n} single-token {shape.name} MoE-layer calls (one layer, weights warm in RAM after "
-                      f"{warm} untimed tokens), {dt:.1f} s, OpenMP threads={threads}",
-            "us_per_layer": round(dt / n * 1e6, 1)}
+    us_all, per_run, _ = res[all_cores]
+    us_4 = res[4][0]
+    return {"value": round(1e6 / us_all, 3), "unit": "tok/s", "cores": all_cores, "kind": kind,
+            "cpu_model": model, "physical_cores_available": phys, "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+            "statistic": f"median of {runs} runs of {per_run} tokens",
+            "sample": f"single-token {shape.name} MoE-layer calls through the reference's moe_ffn (one layer, "
+                      f"weights warm in RAM), {runs} runs per thread count, OMP_PROC_BIND=close, "
+                      f"{all_cores} threads = every physical core available ({model})",
+            "us_per_layer": round(us_all, 1),
+            "threads_4": {"value": round(1e6 / us_4, 3), "unit": "tok/s", "us_per_layer": round(us_4, 1),
+                          "note": "4 OpenMP threads, the reference's default (src/gguf_run.c:267)"}}
 
 
 def cpu_baseline_stack(shape, L, vocab, seed, seconds):
@@ -148,17 +248,24 @@ def cpu_baseline_stack(shape, L, vocab, seed, seconds):
     head = W.host_matrix(W.Q8_0, shape.d, 0, rows, seed, W.stream_id(0, W.KIND_LM_HEAD))
     x = W.host_normal(shape.d, seed, 99)
     lib = Reference() if Reference.available() else Oracle()
+    if layer["kind"] == "reference":
+        _omp_threads(layer["cores"])
     lib.matmul(W.Q8_0, head, x, shape.d, rows)
-    n, t0 = 0, time.perf_counter()
-    while n < 3 or time.perf_counter() - t0 < 1.0:
+    times = []
+    for _ in range(10):
+        t0 = time.perf_counter()
         lib.matmul(W.Q8_0, head, x, shape.d, rows)
-        n += 1
-    head_s = (time.perf_counter() - t0) / n * vocab / rows
+        times.append(time.perf_counter() - t0)
+    head_s = statistics.median(times) * vocab / rows
     tok_s = 1.0 / (L * layer["us_per_layer"] * 1e-6 + head_s)
-    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": layer["cores"], "kind": layer["kind"],
-            "sample": f"{layer['sample']}; times {L} layers, plus the LM head matmul timed on {rows} of its "
-                      f"{vocab} rows ({head_s * 1e3:.1f} ms scaled)",
-            "us_per_layer": layer["us_per_layer"], "lm_head_ms": round(head_s * 1e3, 2)}
+    out = dict(layer)
+    out.update({"value": round(tok_s, 4),
+                "sample": f"{layer['sample']}; times {L} layers, plus the LM head matmul timed on {rows} of its "
+                          f"{vocab} rows (median of 10, {head_s * 1e3:.1f} ms scaled)",
+                "lm_head_ms": round(head_s * 1e3, 2)})
+    out["threads_4"] = dict(layer["threads_4"], value=None,
+                            note="per-layer figure only (the 4-thread head matmul is not timed)")
+    return out
 
 
 def bench_stack(args):
@@ -499,8 +606,67 @@ def bench_model(args):
     print(json.dumps(result), flush=True)
 
 
+# The kernels one layer call launches, by workload (name prefixes as the
+# kernel trace reports them), for the per-layer traffic.
+LAYER_KERNELS = {
+    "decode": ("route_parts_kernel", "decode_gateup_kernel", "down_combine_kernel"),
+}
+
+
+def _counter_medians(d, counter):
+    """Median per dispatch of `counter` (KiB) for every kernel name in the
+    rocprofv3 CSV files under directory d."""
+    import csv
+    import glob
+    vals = {}
+    for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(fn) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row["Kernel_Name"]
+                vals.setdefault(name, {}).setdefault(row.get("Dispatch_Id", len(vals)), 0.0)
+                vals[name][row.get("Dispatch_Id")] += float(row["Counter_Value"])
+    return {k: (float(np.median(list(v.values()))), len(v)) for k, v in vals.items()}
+
+
+def traffic_report(args):
+    """HBM traffic per layer call from counter runs: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch, the median over the run) of each kernel the layer
+    launches, each scaled by what the same counter reads for a plain copy of
+    512 MiB (whose bytes are known), summed over the layer's kernels."""
+    fetch, write, cfetch, cwrite = (_counter_medians(d, c) for d, c in zip(
+        args.traffic, ("FETCH_SIZE", "WRITE_SIZE", "FETCH_SIZE", "WRITE_SIZE")))
+    copy_kib = 512 * 1024
+    cf = max(cfetch.values(), key=lambda v: v[0])[0]
+    cw = max(cwrite.values(), key=lambda v: v[0])[0]
+    f_factor, w_factor = copy_kib / cf, copy_kib / cw
+    prefixes = LAYER_KERNELS["decode"]
+    per_kernel, total = {}, 0.0
+    for name in sorted(fetch):
+        short = name.split("(")[0].split("<")[0].replace("void ", "").split("::")[-1].strip()
+        if not any(short.startswith(p) for p in prefixes):
+            continue
+        fk, n = fetch[name]
+        wk = write.get(name, (0.0, 0))[0]
+        b = fk * 1024 * f_factor + wk * 1024 * w_factor
+        per_kernel[name] = {"fetch_kib_median": round(fk, 1), "write_kib_median": round(wk, 1), "dispatches": n,
+                            "hbm_bytes": int(b)}
+        total += b
+    out = {"workload": args.workload, "hbm_bytes_per_layer": int(total), "kernels": per_kernel,
+           "calibration": {"copy_kib": copy_kib, "fetch_kib": round(cf, 1), "write_kib": round(cw, 1),
+                           "fetch_factor": round(f_factor, 4), "write_factor": round(w_factor, 4)},
+           "dirs": list(args.traffic)}
+    path = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
+    if args.traffic:
+        return traffic_report(args)
     if args.workload == "copy-512MiB":
         return copy_calibration(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -589,12 +755,22 @@ def main():
         "layer_GBps": round(layer_gbs, 1), "layer_frac_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
     }
 
-    if B == 1 and lib.moe_decode_state_bytes(M.C.byref(m.model)) > 0:
-        result.update(decode_stage_roofline(m, shape, L, x_all, hb_all, dev))
+    traffic, _ = layer_traffic(args.workload) if args.plan == 0 else (None, None)
+    if B >= 64:  # prefill: the expert GEMMs run on the matrix cores
+        tflops = expert_flops(shape, B) / (ms_per_step / 1e3) / 1e12
+        result["roofline"] = {"kernel": "moe_ffn_forward (every kernel of the layer call)", "bound": "mfma",
+                              "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                              "flops_per_step": expert_flops(shape, B),
+                              "hbm": {"achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "alg_bytes": int(lb)}}
     else:
-        result["roofline"] = {"kernel": "moe_ffn_forward (all kernels of the layer)", "bound": "hbm",
+        result["roofline"] = {"kernel": "moe_ffn_forward (every kernel of the layer call)", "bound": "hbm",
                               "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": None}
+                              "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                              "alg_bytes_per_launch": int(lb)}
+    if B == 1 and lib.moe_decode_state_bytes(M.C.byref(m.model)) > 0:
+        result["roofline"]["kernels"] = decode_stage_roofline(m, shape, L, x_all, hb_all, dev)
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(shape, B, args.seed, args.cpu_seconds)
@@ -603,11 +779,11 @@ def main():
 
 
 def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
-    """Time each decode stage alone over NS distinct (layer, token) states:
-    moe_decode_stage_timed launches the stage back to back and reads every
-    launch's begin and end from HIP events recorded by the dispatch itself
-    (hipExtLaunchKernelGGL), the same timestamps a kernel trace reports.
-    The dominant kernel (stage 1, top-k + gate/up) is priced against HBM."""
+    """Each kernel of the one-token decode plan alone over NS distinct
+    (layer, token) states: moe_decode_stage_timed launches a stage back to
+    back and reads every launch's begin and end from HIP events recorded by
+    the dispatch itself (hipExtLaunchKernelGGL), the timestamps a kernel
+    trace reports. Each kernel is priced against HBM on its own bytes."""
     import torch
     NS = 8 * L
     if x_all.shape[0] < NS or hb_all.shape[0] < NS:
@@ -618,29 +794,23 @@ def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):
     x = x_all[:NS].clone()
     hb = hb_all[:NS]
     layers = [j % L for j in range(NS)]
-    times = {}
+    names = {0: ("route", "route_parts_kernel (router logits and bounds)"),
+             1: ("topk_gateup", "decode_gateup_kernel (top-k, gate/up SwiGLU, down rows touched ahead)"),
+             2: ("down_combine", "down_combine_kernel (down projections, weighted combine, residual)")}
+    alg = alg_bytes_stages(shape)
+    out = []
     for stage in (0, 1, 2):
         us = m.decode_stage_timed(stage, layers, x, hb, states, idx, w)
-        times[stage] = (float(us.mean()), float(np.median(us)))
-    fused = times[2][0] == 0.0  # stage 1 was the fused kernel: gate/up, down and combine in one launch
-    nb = alg_bytes_experts(shape) if fused else alg_bytes_gateup(shape)
-    kname = ("decode_experts_kernel (top-k, gate/up, down, combine; stage 1)" if fused
-             else "decode_gateup_kernel (top-k + gate/up SwiGLU + down rows warmed, stage 1)")
-    avg = times[1][0]
-    gbs = nb / (avg * 1e-6) / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_{'decode_experts' if fused else 'decode_gateup'}_{shape.name}.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-    return {
-        "roofline": {"kernel": kname, "bound": "hbm",
-                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "alg_bytes_per_launch": nb,
-                     "avg_launch_us": round(avg, 3), "median_launch_us": round(times[1][1], 3), "launches": NS},
-        "stages_us": {"route": round(times[0][0], 3), "experts" if fused else "topk_gateup": round(times[1][0], 3),
-                      "down_combine": round(times[2][0], 3)},
-    }
+        key, kname = names[stage]
+        avg = float(us.mean())
+        if avg <= 0.0:  # the fused plan: stage 1 did the down work too
+            continue
+        gbs = alg[key] / (avg * 1e-6) / 1e9
+        out.append({"stage": key, "kernel": kname, "avg_launch_us": round(avg, 3),
+                    "median_launch_us": round(float(np.median(us)), 3), "launches": NS,
+                    "alg_bytes_per_launch": alg[key], "achieved": round(gbs, 1), "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return out
 
 
 if __name__ == "__main__":

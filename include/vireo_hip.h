@@ -256,6 +256,13 @@ typedef struct {
  * caller can capture a loop of steps in a graph (after one uncaptured step:
  * the first call on a layer pins its expert leases). */
 int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits, void *stream);
+/* moe_stack_step that also records every layer's routing: idx (device int32
+ * [n_layers x n_used]) receives layer l's experts in selection order and
+ * flags (device uint32 [n_layers]) its VIREO_ROUTE_* bits. The same launches
+ * as moe_stack_step plus one 4-byte copy per layer; for parity checks of a
+ * whole stack. No counterpart in the reference. */
+int moe_stack_step_trace(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits,
+                         int32_t *idx, uint32_t *flags, void *stream);
 
 /* ---- MoE models from GGUF files (src/gguf_run.c:266-333) ---------------------- */
 

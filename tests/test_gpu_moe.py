@@ -170,9 +170,9 @@ def test_layers_are_independent(cuda, oracle):
 @pytest.mark.slow
 def test_prefill_2048_zipf(cuda, oracle):
     """Qwen3-30B-A3B Q8_0 prefill of 2048 tokens under a Zipf(1.1) router
-    bias: every token's experts bit-exact with the oracle, the per-expert
-    loads equal to the oracle's, and a sample of tokens' outputs within
-    tolerance (the oracle needs seconds per token at this size)."""
+    bias: every token's experts bit-exact with the oracle and every token's
+    output within the bf16 matrix-core tolerance (the oracle takes a few ms
+    per token here, a few seconds for the call)."""
     shape = W.SHAPES["qwen3-30b-a3b-q8_0"]
     bias = W.zipf_bias(shape.E, 1.1, seed=7)
     m = M.DeviceMoE(shape, 1, seed=56, logit_bias=bias)
@@ -187,9 +187,8 @@ def test_prefill_2048_zipf(cuda, oracle):
         lg = (oracle.matmul(W.F32, router, hb[t], shape.d, shape.E) + bias).astype(np.float32)
         oi[t] = oracle.topk(oracle.softmax(lg), shape.k, shape.renorm)[0]
     np.testing.assert_array_equal(ig, oi)
-    sample = np.array([0, 1, 777, 1500, 2047])
-    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
-    check("prefill sample", x[sample], xt.cpu().numpy()[sample], xo, ig[sample], io, tol=TOL_BF16)
+    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb)
+    check("prefill, all 2048 tokens", x, xt.cpu().numpy(), xo, ig, io, tol=TOL_BF16)
     m.close()
 
 
@@ -216,8 +215,8 @@ def test_grouped_plan_large_groups(cuda, oracle, path, name, T, zipf, plan):
     """Calls of >= 64 tokens with groups of every size (1-15 tokens, and 16 to
     over 128): under plan 0 every group runs as bf16 matrix-core GEMMs, one
     tile or several, ragged or not; plan 4 runs all of them on the fp32
-    kernels. Every token's experts bit-exact; a sample of tokens against the
-    oracle; the same call twice gives the same bits."""
+    kernels. Every token's experts bit-exact and every token's output
+    against the oracle; the same call twice gives the same bits."""
     path(plan)
     shape = W.SHAPES[name]
     bias = W.zipf_bias(shape.E, 1.1, seed=8) if zipf else None
@@ -236,10 +235,8 @@ def test_grouped_plan_large_groups(cuda, oracle, path, name, T, zipf, plan):
     assert counts.max() >= 16 and ((counts > 0) & (counts < 16)).any(), counts
     if zipf:
         assert counts.max() > 128, counts.max()
-    sample = np.unique(np.concatenate([np.arange(0, T, T // 10), [T - 1]]))
-    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
-    check(f"{name} T={T} plan={plan}", x[sample], outs[0][sample], xo, ig[sample], io,
-          tol=TOL_BF16 if plan == 0 else TOL)
+    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"{name} T={T} plan={plan}", x, outs[0], xo, ig, io, tol=TOL_BF16 if plan == 0 else TOL)
     m.close()
 
 
@@ -259,10 +256,9 @@ def test_grouped_plan_large_groups_unregistered(cuda, oracle, path):
     m._unregistered = drop
     xt = torch.from_numpy(x).to(cuda)
     idx, _ = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
-    sample = np.flatnonzero((ig == big[0]).any(axis=1))[:6]
-    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb, tokens=sample)
-    check("unregistered large groups", x[sample], xt.cpu().numpy()[sample], xo, idx.cpu().numpy()[sample], io,
-          tol=TOL_BF16)
+    assert (ig == big[0]).any(axis=1).sum() >= 16  # the dropped expert had a matrix-core group
+    xo, io, _, _ = oracle_layer(oracle, m, 0, x, hb)
+    check("unregistered large groups, all tokens", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io, tol=TOL_BF16)
     m.close()
 
 

@@ -186,6 +186,7 @@ SIGNATURES = {
     "vireo_argmax": (C.c_int, [c_vp, C.c_int, c_vp, c_vp]),
     "vireo_embed": (C.c_int, [C.c_uint32, c_vp, C.c_int, C.c_int, c_vp, C.c_int, c_vp, c_vp]),
     "moe_stack_step": (C.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "moe_stack_step_trace": (C.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_route": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_dispatch": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
     "vireo_hip_set_path": (C.c_int, [C.c_int]),

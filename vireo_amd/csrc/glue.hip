@@ -3,6 +3,8 @@
 // decode step of an MoE stack (src/gguf_run.c:216-251 without attention).
 #include <hip/hip_runtime.h>
 #include "common.h"
+#include "route.h"
+#include "route_kernels.h"
 #include "qdecode.h"
 #include "route_kernels.h"
 #include "vireo_hip.h"
@@ -130,8 +132,9 @@ extern "C" int vireo_embed(uint32_t type, const void *table, int n, int n_rows, 
     return vh_finish(s, vh_check(hipGetLastError()));
 }
 
-extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits,
-                              void *stream) {
+namespace {
+int stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits, int32_t *idx,
+               uint32_t *flags, void *stream) {
     if (!st || !st->moe || !st->lm_head || !token || !x || !xb || !logits || st->vocab <= 0) return -EINVAL;
     const vireo_moe_model *m = st->moe;
     const int d = m->dim;
@@ -140,11 +143,38 @@ extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *
     int rc = vireo_embed(emb->ggml_type, emb->data, d, st->vocab, token, 1, x, s);
     for (int l = 0; l < m->n_layers && !rc; l++)
         rc = vh_moe_layer_normed(m, l, x, st->ffn_norm ? st->ffn_norm[l] : nullptr, st->eps, xb,
-                                 static_cast<hipStream_t>(s));
+                                 static_cast<hipStream_t>(s), idx ? idx + size_t(l) * m->n_used : nullptr,
+                                 flags ? flags + l : nullptr);
     if (!rc) rc = vireo_rmsnorm(xb, x, st->out_norm, d, 1, st->eps, s);
     if (!rc) rc = qmatvec_async(logits, xb, st->lm_head, d, st->vocab, s);
     if (!rc) rc = vireo_argmax(logits, st->vocab, token, s);
     return vh_finish(static_cast<hipStream_t>(s), rc);
+}
+}  // namespace
+
+extern "C" int moe_stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits,
+                              void *stream) {
+    return stack_step(st, token, x, xb, logits, nullptr, nullptr, stream);
+}
+
+extern "C" int moe_stack_step_trace(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, float *logits,
+                                    int32_t *idx, uint32_t *flags, void *stream) {
+    if (!idx || !flags) return -EINVAL;
+    return stack_step(st, token, x, xb, logits, idx, flags, stream);
+}
+
+// One row of the reference's RMSNorm, bit for bit (its in-order fp32 sum of
+// squares: one thread adds them, the rest of the row is parallel).
+__global__ void __launch_bounds__(256) rmsnorm_ref_kernel(float *__restrict__ o, const float *__restrict__ x,
+                                                          const float *__restrict__ w, int n, float eps) {
+    __shared__ float red;
+    reference_rmsnorm_block(o, x, w, eps, n, &red);
+}
+
+int vh_rmsnorm_ref(float *o, const float *x, const float *w, int n, float eps, hipStream_t s) {
+    if (n <= 0 || !o || !x || o == x) return -EINVAL;
+    hipLaunchKernelGGL(rmsnorm_ref_kernel, dim3(1), dim3(256), 0, s, o, x, w, n, eps);
+    return vh_check(hipGetLastError());
 }
 
 extern "C" int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream) {

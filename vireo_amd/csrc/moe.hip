@@ -170,7 +170,7 @@ bool fused(const vireo_moe_model *m, int layer) {
 // combine.
 int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *const *table, float *x,
                  const float *hb, const DecodeState &st, int32_t *idx, float *w, hipStream_t s,
-                 bool allow_fused = true) {
+                 bool allow_fused = true, NormRef nref = NormRef{}) {
     const vireo_moe_layer &L = m->layers[layer];
     const float *R = static_cast<const float *>(L.router->data);
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
@@ -180,9 +180,9 @@ int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *con
     case 1:
         if (allow_fused && fused(m, layer))
             return vh_decode_experts(tg, td, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h,
-                                     st.bar, x, idx, w, s);
+                                     st.bar, x, idx, w, nref, s);
         return vh_decode_gateup(tg, st.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, st.h, idx, w,
-                                st.flags(), st.plan, td, s);
+                                st.flags(), st.plan, td, nref, s);
     case 2:
         if (allow_fused && fused(m, layer)) return 0;
         return vh_down_combine(td, st.plan, st.h, d, fe, k, x, s);
@@ -192,31 +192,46 @@ int decode_stage(const vireo_moe_model *m, int layer, int stage, const void *con
 
 }  // namespace
 
+namespace {
+int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
+                float *w_out, hipStream_t s, const WsSource *src, uint32_t *flags_out);
+}  // namespace
+
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
-                        hipStream_t s) {
+                        hipStream_t s, int32_t *idx_out, uint32_t *flags_out) {
     if (int rc = check_model(m, layer)) return rc;
     if (!x || !xb || !m->es) return -EINVAL;
     const bool decode = g_path != 2 && g_path != 4 && decode_supported(m, layer) && m->dim == 2048 &&
                         !((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xb)) & 15u) &&
                         !(reinterpret_cast<uintptr_t>(m->layers[layer].router->data) & 15u);
-    if (!decode) {
-        if (int rc = vireo_rmsnorm(xb, x, nw, m->dim, 1, eps, s)) return rc;
-        return moe_ffn_forward(m, layer, x, xb, 1, nullptr, nullptr, s);
+    if (!decode) {  // the reference's own RMSNorm, bit for bit, so the routing is certified on its xb
+        if (int rc = vh_rmsnorm_ref(xb, x, nw, m->dim, eps, s)) return rc;
+        return ffn_forward(m, layer, x, xb, 1, idx_out, nullptr, s, nullptr, flags_out);
     }
     const vireo_moe_layer &L = m->layers[layer];
     const void *const *table = nullptr;
     if (int rc = layer_table(m, layer, &table)) {
         if (rc < 0) return rc;
-        if ((rc = vireo_rmsnorm(xb, x, nw, m->dim, 1, eps, s))) return rc;
-        return moe_ffn_forward(m, layer, x, xb, 1, nullptr, nullptr, s);  // pages the routed experts
+        if ((rc = vh_rmsnorm_ref(xb, x, nw, m->dim, eps, s))) return rc;
+        return ffn_forward(m, layer, x, xb, 1, idx_out, nullptr, s, nullptr, flags_out);  // pages the routed experts
     }
     Ws ws;
     if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, true, false, &ws)) return rc;
     const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
     int rc = vh_route_parts_norm(static_cast<const float *>(L.router->data), x, nw, eps, xb, L.logit_bias, m->dim,
                                  m->n_experts, 1, st.parts, s, st.bar, kFusedBlocks + 1);
-    for (int stage = 1; stage < 3 && !rc; stage++) rc = decode_stage(m, layer, stage, table, x, xb, st, ws.idx, ws.w, s);
-    if (!rc) rc = vh_store_note_routing(m->es, layer, ws.idx, 1, m->n_used, s);
+    int32_t *idx = idx_out ? idx_out : ws.idx;
+    // hb is the fp64-normalised x: the router parts carry the widened bounds
+    // (route_part_on_own_norm) and an uncertified token is ranked on the
+    // reference's own xb, recomputed from x
+    NormRef nref;
+    nref.x = x;
+    nref.nw = nw;
+    nref.eps = eps;
+    for (int stage = 1; stage < 3 && !rc; stage++)
+        rc = decode_stage(m, layer, stage, table, x, xb, st, idx, ws.w, s, true, nref);
+    if (!rc && flags_out) rc = vh_check(hipMemcpyAsync(flags_out, st.flags(), 4, hipMemcpyDeviceToDevice, s));
+    if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, m->n_used, s);
     return rc;
 }
 
@@ -355,7 +370,7 @@ extern "C" int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_exper
 // once all batches have written their rows. The stream is synchronized once
 // (the host needs the routing), so such a call cannot be captured in a graph.
 int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
-                  float *w_out, hipStream_t s) {
+                  float *w_out, hipStream_t s, uint32_t *flags_out) {
     const vireo_moe_layer &L = m->layers[layer];
     const uint32_t tg = L.gate_exps->ggml_type, td = L.down_exps->ggml_type;
     const int d = m->dim, fe = m->ffn_exp, k = m->n_used, E = m->n_experts;
@@ -370,6 +385,8 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    if (!rc && flags_out)
+        rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     // pinned host memory: counts [E], routing [P], then per batch a table [3 E]
     // and an active list [E + 1], then the combine's table [3 E]
     const size_t tab_n = size_t(3) * E, act_n = size_t(E) + 1;
@@ -463,7 +480,7 @@ namespace {
 // the fused plan is not used (its status word is allocated on first use) and
 // the routing is not copied for the store's statistics (its host ring is).
 int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
-                float *w_out, hipStream_t s, const WsSource *src) {
+                float *w_out, hipStream_t s, const WsSource *src, uint32_t *flags_out) {
     if (int rc = check_model(m, layer)) return rc;
     if (n_tokens < 0 || (n_tokens && (!x || !hb))) return -EINVAL;
     if (n_tokens == 0) return 0;
@@ -479,7 +496,7 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     } else if (int lt = layer_table(m, layer, &table)) {
         if (lt < 0) return lt;
         // the store does not hold every layer: page the routed experts per call
-        return vh_finish(s, paged_forward(m, layer, x, hb, n_tokens, idx_out, w_out, s));
+        return vh_finish(s, paged_forward(m, layer, x, hb, n_tokens, idx_out, w_out, s, flags_out));
     }
     const float *R = static_cast<const float *>(L.router->data);
 
@@ -497,6 +514,7 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         rc = 0;
         for (int stage = 0; stage < 3 && !rc; stage++)
             rc = decode_stage(m, layer, stage, table, x, hb, st, idx, w, s, !src);
+        if (!rc && flags_out) rc = vh_check(hipMemcpyAsync(flags_out, st.flags(), 4, hipMemcpyDeviceToDevice, s));
         if (!rc && !src) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
         rc = vh_finish(s, rc);
         if (!rc && !s && !src && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
@@ -508,6 +526,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    if (!rc && flags_out)
+        rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     if (mfma) {  // every group on the matrix cores (its small list stays empty)
         const int mt = vh_mfma_max_tiles(P, E);
         if (!rc) rc = vh_mfma_plan(ws.counts, E, 1, ws.tiles, ws.small, s);
@@ -554,7 +574,8 @@ int vh_noalloc_setup(void **out) {
 
 extern "C" int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
                                int32_t *idx_out, float *w_out, void *stream) {
-    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), nullptr);
+    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), nullptr,
+                       nullptr);
 }
 
 extern "C" int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens,
@@ -562,5 +583,6 @@ extern "C" int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, floa
     void *base = nullptr;
     if (int rc = vh_noalloc_setup(&base)) return rc;
     const WsSource src{static_cast<char *>(base), kNoAllocScratchBytes};
-    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), &src);
+    return ffn_forward(m, layer, x, hb, n_tokens, idx_out, w_out, static_cast<hipStream_t>(stream), &src,
+                       nullptr);
 }

@@ -64,10 +64,11 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
                                                             int32_t *__restrict__ idx_out, float *__restrict__ w_out,
                                                             uint32_t *__restrict__ flags_out,
                                                             DecodePlan *__restrict__ plan, int pf_rows, int pf_nbd,
-                                                            int64_t pf_rb) {
+                                                            int64_t pf_rb, NormRef nref) {
     using F = Reg<T>;
     constexpr int NS = F::NS, TPL = 3 * Q;
     __shared__ TopKSmem sm;         // the exact fallback's workspace
+    __shared__ __align__(16) float xref[2048];  // the fallback on a library-normalised hb: the reference's xb
     __shared__ float2 stage[64];    // the weights, in the workgroup that writes the plan
     __shared__ double2 cert[kGuWaves][64];  // per wave: the chosen experts' intervals
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -100,7 +101,12 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     const bool ok = route_select_wave<Q>(p, E, k, j, e_j, j, e_unused, rank, cert[wv]);
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
     if (!ok) {
-        route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);
+        const float *xe = hb;
+        if (nref.x) {  // rank on the reference's own xb, not on the fp64-normalised hb
+            reference_rmsnorm_block(xref, nref.x, nref.nw, nref.eps, d, &sm.red[0][0]);
+            xe = xref;
+        }
+        route_topk_block(sm, parts, R, xe, bias, d, E, k, renorm, false, nullptr);
         e_j = sm.sel[j];
         if (writer && wv == 0 && lane < k) {
             const int e = sm.sel[lane];
@@ -179,7 +185,7 @@ struct DownPrefetch {
 template <int T, int Q, int RPW>
 int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E,
                          int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx,
-                         float *w, uint32_t *flags, DecodePlan *plan, DownPrefetch pf, hipStream_t s) {
+                         float *w, uint32_t *flags, DecodePlan *plan, DownPrefetch pf, NormRef nref, hipStream_t s) {
     constexpr int rows_per_block = kGuWaves * RPW;
     dim3 g((fe + rows_per_block - 1) / rows_per_block, k);
     bool warm = pf.rows > 0 && g.x % 8 == 0 && pf.nbd % 8 == 0 && (pf.nbd / 8) % (g.x / 8) == 0;
@@ -188,7 +194,7 @@ int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb
         warm = per * lines <= 512 * kPfPerThread;
     }
     VH_LAUNCH((decode_gateup_kernel<T, Q, RPW>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe, d, renorm,
-              rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb);
+              rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref);
     return vh_check(hipGetLastError());
 }
 
@@ -201,29 +207,29 @@ int gateup_rpw(int fe, int k) {
 template <int T, int Q>
 int launch_gateup_rpw(int rpw, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                       int E, int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx,
-                      float *w, uint32_t *flags, DecodePlan *plan, DownPrefetch pf, hipStream_t s) {
+                      float *w, uint32_t *flags, DecodePlan *plan, DownPrefetch pf, NormRef nref, hipStream_t s) {
     if (rpw == 2)
         return launch_decode_gateup<T, Q, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                             plan, pf, s);
+                                             plan, pf, nref, s);
     if (rpw == 3)
         return launch_decode_gateup<T, Q, 3>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                             plan, pf, s);
+                                             plan, pf, nref, s);
     return launch_decode_gateup<T, Q, 4>(parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan,
-                                         pf, s);
+                                         pf, nref, s);
 }
 
 template <int T>
 int launch_gateup_t(int rpw, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E,
                     int k, int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
-                    uint32_t *flags, DecodePlan *plan, DownPrefetch pf, hipStream_t s) {
+                    uint32_t *flags, DecodePlan *plan, DownPrefetch pf, NormRef nref, hipStream_t s) {
     if (E <= 64)
         return launch_gateup_rpw<T, 1>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                       plan, pf, s);
+                                       plan, pf, nref, s);
     if (E <= 128)
         return launch_gateup_rpw<T, 2>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags,
-                                       plan, pf, s);
+                                       plan, pf, nref, s);
     return launch_gateup_rpw<T, 4>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan,
-                                   pf, s);
+                                   pf, nref, s);
 }
 
 // ------------------------------------------------------------------ down + combine
@@ -336,7 +342,7 @@ bool vh_decode_gateup_supported(uint32_t type, int d, int fe) {
 
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
-                     uint32_t *flags, DecodePlan *plan, uint32_t down_type, hipStream_t s) {
+                     uint32_t *flags, DecodePlan *plan, uint32_t down_type, NormRef nref, hipStream_t s) {
     if (!vh_decode_gateup_supported(type, d, fe) || E > kMaxExperts || k > 64) return -EINVAL;
     const int64_t rb = row_bytes_of(type, d);
     const int rpw = gateup_rpw(fe, k);
@@ -352,9 +358,9 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
         pf.rb = row_bytes_of(down_type, fe);
     }
     switch (type) {
-    case VT_Q4_K: return launch_gateup_t<VT_Q4_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, s);
-    case VT_Q8_0: return launch_gateup_t<VT_Q8_0>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, s);
-    case VT_Q6_K: return launch_gateup_t<VT_Q6_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, s);
+    case VT_Q4_K: return launch_gateup_t<VT_Q4_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, nref, s);
+    case VT_Q8_0: return launch_gateup_t<VT_Q8_0>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, nref, s);
+    case VT_Q6_K: return launch_gateup_t<VT_Q6_K>(rpw, parts, R, hb, bias, d, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, pf, nref, s);
     default: return -EINVAL;
     }
 }

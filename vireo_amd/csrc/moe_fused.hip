@@ -50,12 +50,14 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
     const RoutePart *__restrict__ parts, const float *__restrict__ hb, const void *const *__restrict__ table, int E,
     int k, int fe, int d, int renorm, int64_t rb_gu, int64_t rb_dn, const float *__restrict__ R,
     const float *__restrict__ bias, float *__restrict__ h, uint32_t *__restrict__ bar, float *__restrict__ x,
-    int32_t *__restrict__ idx_out, float *__restrict__ w_out, uint32_t *__restrict__ status, unsigned spin_limit) {
+    int32_t *__restrict__ idx_out, float *__restrict__ w_out, uint32_t *__restrict__ status, unsigned spin_limit,
+    NormRef nref) {
     using FG = Reg<TG>;
     using FD = Reg<TD>;
     constexpr int NSG = FG::NS, NSD = FD::NS, TPL = 3 * Q, SUB = 64 / L;
     constexpr int RB = SUB * UPG;  // output rows per workgroup
     __shared__ TopKSmem sm;
+    __shared__ __align__(16) float xref[2048];  // the fallback on a library-normalised hb: the reference's xb
     __shared__ float2 stage[64];
     __shared__ double2 cert[kFusedWaves][64];
     __shared__ float ys[kFusedWaves][RB];
@@ -91,7 +93,12 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
     float w_sel = 0.0f;  // wave 0, lane t < k: weight of round t
     int e_sel = 0;
     if (!ok) {  // the same verdict in every wave: the whole workgroup ranks on exact logits
-        route_topk_block(sm, parts, R, hb, bias, d, E, k, renorm, false, nullptr);
+        const float *xe = hb;
+        if (nref.x) {  // on the reference's own xb, not on the fp64-normalised hb
+            reference_rmsnorm_block(xref, nref.x, nref.nw, nref.eps, d, &sm.red[0][0]);
+            xe = xref;
+        }
+        route_topk_block(sm, parts, R, xe, bias, d, E, k, renorm, false, nullptr);
         e_j = sm.sel[j];
         e_dn = sm.sel[wv];
         if (wv == 0 && lane < k) {
@@ -234,7 +241,7 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
 template <int TG, int TD, int Q, int RPW, int L, int IPL, int UPG>
 int launch_experts(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                    int fe, int renorm, const void *const *table, float *h, uint32_t *bar, float *x, int32_t *idx,
-                   float *w, hipStream_t s) {
+                   float *w, NormRef nref, hipStream_t s) {
     constexpr int rows_per_block = kFusedWaves * RPW;
     const dim3 g(fe / rows_per_block, k);
     const int64_t rb_gu = TG == VT_Q8_0 ? int64_t(d / 32) * 34 : TG == VT_Q4_K ? int64_t(d / 256) * 144
@@ -244,7 +251,7 @@ int launch_experts(const RoutePart *parts, const float *R, const float *hb, cons
     uint32_t *status = nullptr;
     if (int rc = vh_status_word(&status)) return rc;
     VH_LAUNCH((decode_experts_kernel<TG, TD, Q, RPW, L, IPL, UPG>), g, dim3(64 * kFusedWaves), 0, s, parts, hb, table,
-              E, k, fe, d, renorm, rb_gu, rb_dn, R, bias, h, bar, x, idx, w, status, vh_spin_limit());
+              E, k, fe, d, renorm, rb_gu, rb_dn, R, bias, h, bar, x, idx, w, status, vh_spin_limit(), nref);
     return vh_check(hipGetLastError());
 }
 
@@ -270,20 +277,20 @@ int vh_fused_blocks(uint32_t tg, uint32_t td, int d, int E, int k, int fe) {
 
 int vh_decode_experts(uint32_t tg, uint32_t td, const RoutePart *parts, const float *R, const float *hb,
                       const float *bias, int d, int E, int k, int fe, int renorm, const void *const *table, float *h,
-                      uint32_t *bar, float *x, int32_t *idx, float *w, hipStream_t s) {
+                      uint32_t *bar, float *x, int32_t *idx, float *w, NormRef nref, hipStream_t s) {
     switch (fused_variant(tg, td, d, E, k, fe)) {
     case 1:  // 768 rows of gate/up per expert: 3 per wave; down rows 8 per workgroup, 8 lanes x 3 items each
         if (tg == VT_Q4_K)
             return launch_experts<VT_Q4_K, VT_Q6_K, 2, 3, 8, 3, 1>(parts, R, hb, bias, d, E, k, fe, renorm, table, h,
-                                                                    bar, x, idx, w, s);
+                                                                    bar, x, idx, w, nref, s);
         return launch_experts<VT_Q8_0, VT_Q8_0, 2, 3, 8, 3, 1>(parts, R, hb, bias, d, E, k, fe, renorm, table, h, bar,
-                                                                x, idx, w, s);
+                                                                x, idx, w, nref, s);
     case 2:  // 1024 rows: 4 per wave; down items 32 per row: 16 lanes x 2 items, 2 rows per lane group
         if (tg == VT_Q4_K)
             return launch_experts<VT_Q4_K, VT_Q6_K, 1, 4, 16, 2, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, h,
-                                                                     bar, x, idx, w, s);
+                                                                     bar, x, idx, w, nref, s);
         return launch_experts<VT_Q8_0, VT_Q8_0, 1, 4, 16, 2, 2>(parts, R, hb, bias, d, E, k, fe, renorm, table, h, bar,
-                                                                 x, idx, w, s);
+                                                                 x, idx, w, nref, s);
     default: return -EINVAL;
     }
 }

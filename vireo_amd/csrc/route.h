@@ -29,7 +29,8 @@ constexpr int kMaxExperts = 256;
 // The same part from the lane's C inputs already in registers (columns
 // lane*C .. lane*C + C - 1; d == 64*C).
 template <int C>
-VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&xv)[C], int lane) {
+VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&xv)[C], int lane,
+                                     double *abs_products = nullptr) {
     float p[C];
     const float4 *r4 = reinterpret_cast<const float4 *>(r + lane * C);
 #pragma unroll
@@ -40,9 +41,12 @@ VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&
         p[4 * i + 2] = __fmul_rn(a.z, xv[4 * i + 2]);
         p[4 * i + 3] = __fmul_rn(a.w, xv[4 * i + 3]);
     }
-    double tot = 0.0, absum = 0.0;
+    double tot = 0.0, absum = 0.0, pabs = 0.0;
 #pragma unroll
-    for (int i = 0; i < C; i++) tot += double(p[i]);
+    for (int i = 0; i < C; i++) {
+        tot += double(p[i]);
+        pabs += fabs(double(p[i]));
+    }
     double run = wave_incl_scan_d(tot) - tot;
 #pragma unroll
     for (int i = 0; i < C; i++) {
@@ -52,7 +56,55 @@ VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&
     RoutePart out;
     out.c = wave_sum_d(tot);
     out.beta = 1.001 * 5.9604644775390625e-08 * wave_sum_d(absum) + 1e-30;
+    if (abs_products) *abs_products = wave_sum_d(pabs);
     return out;
+}
+
+// Certification of a router part computed on hb = our own RMSNorm of x
+// (sum of squares in fp64, rounded once) instead of the reference's xb (an
+// in-order fp32 sum, src/gguf_run.c:162). Both are fl(fl(x_i r) w_i) with a
+// different scale r, so xb_i = s hb_i (1 + theta_i), |theta_i| <= 4u, with one
+// s > 0 for all experts; the reference's products fl(R_i xb_i) are then
+// s p_i (1 + phi_i), |phi_i| <= 6u, p_i = fl(R_i hb_i). The reference's logit
+// divided by s therefore lies within beta' + 6.0003 u sum|p_i| of c (beta'
+// slightly above beta: its prefix sums are ours scaled by s within 6u), and a
+// ranking certified on these intervals is the reference's ranking - a common
+// positive scale changes no order. (The reference's prefix sums carry the same
+// 6u per product, which adds 1.001 n u * 6u sum|p_i| to beta': the second term
+// of the widening.) A logit bias is not scaled with the rest;
+// with one, the interval also covers |s - 1| <= sigma (the in-order fp32 sum of
+// n squares is within 1.001 n u of the exact one, r moves by half of that plus
+// the roundings of the scale).
+VH_DEV RoutePart route_part_on_own_norm(RoutePart p, double abs_products, int n, const float *bias, int e) {
+    constexpr double u = 5.9604644775390625e-08;
+    p.beta = p.beta * 1.000001 + (6.0002 + 6.01 * double(n) * u) * u * abs_products;
+    if (bias) {
+        const double sigma = 0.5 * 1.001 * double(n) * u + 8.0 * u;
+        p.beta += sigma * (fabs(p.c) + p.beta);
+        p.c += double(bias[e]);
+    }
+    return p;
+}
+
+// The reference's RMSNorm of x (src/gguf_run.c:161-165) into dst[0..d) by a
+// whole workgroup, bit for bit: the squares in parallel, their in-order fp32
+// sum by one thread (d dependent adds: used only where exactness needs it),
+// r = 1/sqrtf(ss/n + eps), then (x_i r) w_i. dst: d floats (LDS or global),
+// red: one float of LDS. All threads of the workgroup call it.
+VH_DEV void reference_rmsnorm_block(float *dst, const float *__restrict__ x, const float *__restrict__ nw, float eps,
+                                    int d, float *red) {
+    for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = __fmul_rn(x[i], x[i]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int i = 0; i < d; i++) ss = __fadd_rn(ss, dst[i]);
+        *red = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(d)), eps)));
+    }
+    __syncthreads();
+    const float r = *red;
+    for (int i = threadIdx.x; i < d; i += blockDim.x)
+        dst[i] = nw ? __fmul_rn(__fmul_rn(x[i], r), nw[i]) : __fmul_rn(x[i], r);
+    __syncthreads();
 }
 
 template <int C>

@@ -70,11 +70,10 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
 #pragma unroll
         for (int i = 0; i < C / 4; i++) h4[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
     }
-    RoutePart p = route_row_part_regs<C>(R + size_t(e) * d, xv, lane);
-    if (lane == 0) {
-        if (bias) p.c += double(bias[e]);
-        parts[size_t(t) * E + e] = p;
-    }
+    double abs_products;
+    RoutePart p = route_row_part_regs<C>(R + size_t(e) * d, xv, lane, &abs_products);
+    p = route_part_on_own_norm(p, abs_products, d, bias, e);  // certified against the reference's xb
+    if (lane == 0) parts[size_t(t) * E + e] = p;
 }
 
 constexpr int kExTok = 64, kExExp = 16, kExChunk = 64;

@@ -37,8 +37,10 @@ int vh_store_note_routing(ExpertStore *s, int layer, const int32_t *idx_dev, int
 void vh_store_note_routing_host(ExpertStore *s, int layer, const int32_t *idx, int T, int k);
 }
 
+// idx_out (k entries) / flags_out (one word), device, optional: the layer's
+// routing and VIREO_ROUTE_* flags.
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
-                        hipStream_t s);
+                        hipStream_t s, int32_t *idx_out = nullptr, uint32_t *flags_out = nullptr);
 // y += W x (qmatvec_async with each result added to y[r], one rounding)
 int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s);
 // y_i = W_i x for three matrices of n columns in one launch; -ENOTSUP when a
@@ -50,6 +52,19 @@ int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, con
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
                     hipStream_t s);
 
+// Where hb came from when the library normalised it itself (the stack and
+// model paths): the residual x, the norm weight (NULL: unit) and eps, so that
+// an uncertified routing can be decided on the reference's own xb (its
+// in-order RMSNorm, recomputed exactly). x == NULL: hb is the caller's input.
+struct NormRef {
+    const float *x = nullptr;
+    const float *nw = nullptr;
+    float eps = 0.0f;
+};
+// hb_out = the reference's RMSNorm of x (src/gguf_run.c:161-165) bit for bit
+// (its in-order fp32 sum of squares), for one row of n.
+int vh_rmsnorm_ref(float *hb_out, const float *x, const float *nw, int n, float eps, hipStream_t s);
+
 // What the decode gate/up kernel hands to the down kernel: the chosen experts'
 // down matrices (NULL for an unregistered expert) and weights, in selection order.
 struct DecodePlan {
@@ -60,7 +75,7 @@ struct DecodePlan {
 // Decode path (one token): gate/up with the top-k fused in, then down + combine.
 int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias, int d,
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
-                     uint32_t *flags, DecodePlan *plan, uint32_t down_type, hipStream_t s);
+                     uint32_t *flags, DecodePlan *plan, uint32_t down_type, NormRef nref, hipStream_t s);
 bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
 // Down projection + weighted combine + residual for one token:
 // x += sum_j plan.w[j] * down_j h[j], in selection order.
@@ -123,4 +138,4 @@ constexpr int kFusedBlocks = 256;
 int vh_fused_blocks(uint32_t tg, uint32_t td, int d, int E, int k, int fe);  // kFusedBlocks, or 0 if not built for it
 int vh_decode_experts(uint32_t tg, uint32_t td, const RoutePart *parts, const float *R, const float *hb,
                       const float *bias, int d, int E, int k, int fe, int renorm, const void *const *table, float *h,
-                      uint32_t *bar, float *x, int32_t *idx, float *w, hipStream_t s);
+                      uint32_t *bar, float *x, int32_t *idx, float *w, NormRef nref, hipStream_t s);

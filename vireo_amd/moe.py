@@ -199,6 +199,16 @@ class DeviceMoE:
     def host_router(self, layer):
         return self.routers[layer].cpu().numpy()
 
+    def expert_bytes(self, layer, e):
+        """One expert's gate, up and down slices copied from HBM (host uint8)."""
+        E = self.shape.E
+        gs, us, ds = self.slices
+        off = layer * self.layer_bytes
+        g = self.buf[off + e * gs:off + (e + 1) * gs]
+        u = self.buf[off + E * gs + e * us:off + E * gs + (e + 1) * us]
+        d = self.buf[off + E * (gs + us) + e * ds:off + E * (gs + us) + (e + 1) * ds]
+        return g.cpu().numpy(), u.cpu().numpy(), d.cpu().numpy()
+
     def device_layer_bytes(self, layer):
         """The layer's stacked expert bytes as stored in HBM (gate, up, down)."""
         E = self.shape.E

@@ -43,6 +43,17 @@ class DeviceStack:
         _lib.check(self.lib.moe_stack_step(C.byref(self.st), M._ptr(token), M._ptr(self.x), M._ptr(self.xb),
                                            M._ptr(self.logits), M._stream_handle(stream)), "moe_stack_step")
 
+    def step_trace(self, token, idx, flags, stream=None):
+        """step() that also records every layer's routing: idx (device int32
+        [layers x k]) and flags (device uint32 [layers])."""
+        _lib.check(self.lib.moe_stack_step_trace(C.byref(self.st), M._ptr(token), M._ptr(self.x), M._ptr(self.xb),
+                                                 M._ptr(self.logits), M._ptr(idx), M._ptr(flags),
+                                                 M._stream_handle(stream)), "moe_stack_step_trace")
+
+    def device_lm_head(self):
+        """The LM head's bytes copied from HBM (host uint8)."""
+        return self.lm[:W.row_bytes(self.lm_type, self.shape.d) * self.vocab].cpu().numpy()
+
     def host_lm_head(self):
         return W.host_matrix(self.lm_type, self.shape.d, 0, self.vocab, self.seed, W.stream_id(0, W.KIND_LM_HEAD))
 
