@@ -188,7 +188,12 @@ int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const
  * decode plan whenever it applies, 2 = always the grouped plan, 3 = the
  * one-token decode plan with its experts fused into one kernel where that
  * kernel is built for the shapes (see moe_decode_stage), 4 = always the
- * grouped plan, with every group on the fp32 kernels.
+ * grouped plan, with every group on the fp32 kernels, 5 = one token through
+ * the whole layer (router, top-k, experts, combine; with the RMSNorm in front
+ * in moe_stack_step and vireo_model_step) in one launch whose workgroups meet
+ * through tagged records, where it is built for the shapes (d = 2048, k = 8,
+ * up to 128 experts, expert width 768 or 1024, Q4_K/Q6_K or Q8_0 experts,
+ * 256 CUs); its waits are bounded like plan 3's (vireo_hip_status).
  * Under plans 0 and 2, calls of at least 64 tokens run every group as bf16
  * matrix-core GEMMs (inputs and dequantized weights rounded
  * to bf16, fp32 accumulation; the layer's contribution then agrees with the

@@ -247,3 +247,57 @@ def test_whole_model_file_binds_in_the_reference(tmp_path):
         if la is not None:
             assert np.isfinite(la).all()
             np.testing.assert_array_equal(la, lb)
+
+
+def test_reader_under_sanitizers(vl, tmp_path):
+    """The library's GGUF reader built with AddressSanitizer and
+    UndefinedBehaviorSanitizer (host code only) reads the malformed files of
+    test_reader_rejects_malformed - every truncation, bad magic and version,
+    impossible counts, a zero alignment, random corruption - without a
+    report, and accepts exactly the files the product library accepts."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = str(tmp_path / "gguf_open_check")
+    r = subprocess.run(["gcc", "-std=c11", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                        "-fno-omit-frame-pointer", "-I", os.path.join(root, "include"),
+                        os.path.join(root, "tests", "c", "gguf_open_check.c"),
+                        os.path.join(root, "vireo_amd", "csrc", "gguf.c"), "-o", exe],
+                       capture_output=True, text=True)
+    if r.returncode != 0 and "asan" in (r.stderr or "").lower():
+        pytest.skip("sanitizer runtime not available: " + r.stderr[-200:])
+    assert r.returncode == 0, r.stderr
+    path, data = small_file(tmp_path)
+    blobs = [data[:n] for n in range(len(data) + 1)]
+    blobs += [b"GGUG" + data[4:], data[:4] + struct.pack("<I", 1) + data[8:], data[:4] + struct.pack("<I", 4) + data[8:],
+              data[:8] + struct.pack("<Q", 1 << 40) + data[16:]]
+    w = G.GGUFWriter()
+    w.add("general.alignment", G.U32, 0)
+    zero = str(tmp_path / "zero.gguf")
+    w.write(zero)
+    blobs.append(open(zero, "rb").read())
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        blob = bytearray(data)
+        for pos in rng.integers(0, len(blob), size=rng.integers(1, 6)):
+            blob[pos] = int(rng.integers(0, 256))
+        blobs.append(bytes(blob))
+    files = []
+    for i, b in enumerate(blobs):
+        fn = str(tmp_path / f"m{i}.gguf")
+        with open(fn, "wb") as f:
+            f.write(b)
+        files.append(fn)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([exe, *files], capture_output=True, text=True, env=env, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    got = [int(x) for x in r.stdout.split()]
+    want = []
+    for fn in files:
+        p = vl.vireo_gguf_open(fn.encode())
+        want.append(int(bool(p)))
+        if p:
+            vl.vireo_gguf_close(p)
+    assert got == want

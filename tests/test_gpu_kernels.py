@@ -99,3 +99,38 @@ def test_qmatvec_many_rows(cuda, oracle, typ, n, d):
     M.qmatvec(y, torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), typ, n, d)
     want = oracle.matmul(typ, w, x, n, d)
     assert np.abs(y.cpu().numpy() - want).max() <= 2e-3 * np.abs(want).max()
+
+
+# binary16 scales that exercise every branch of gguf_f16_to_f32 (src/gguf_compute.c:17-36):
+# zero and negative zero, the smallest and largest subnormals, the smallest normal, the largest
+# finite value, both infinities, quiet and signalling NaNs
+SPECIAL_F16 = [0x0000, 0x8000, 0x0001, 0x83FF, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFD55]
+
+
+@pytest.mark.parametrize("typ,n", [(W.Q8_0, 256), (W.Q4_K, 512), (W.Q6_K, 512)])
+def test_dequant_special_scales(cuda, oracle, typ, n):
+    """Blocks whose fp16 scales (d, and dmin for Q4_K) are subnormal, infinite
+    or NaN dequantize on the GPU to the reference's values: bit-equal where
+    finite, the same infinities and NaN in the same places (products of inf
+    and a zero quant are NaN in both)."""
+    rows = len(SPECIAL_F16)
+    w = _weights(typ, n, rows, seed=13).copy()
+    rb = w.size // rows
+    bb = {W.Q8_0: 34, W.Q4_K: 144, W.Q6_K: 210}[typ]
+    for r, h in enumerate(SPECIAL_F16):
+        for b in range(rb // bb):
+            blk = r * rb + b * bb
+            hb = np.array([h], np.uint16).view(np.uint8)
+            if typ == W.Q8_0:
+                w[blk:blk + 2] = hb
+            elif typ == W.Q4_K:  # d, then dmin (the special value with another one beside it)
+                w[blk:blk + 2] = hb
+                w[blk + 2:blk + 4] = np.array([SPECIAL_F16[(r + b + 3) % rows]], np.uint16).view(np.uint8)
+            else:  # Q6_K: d is the last two bytes of the block
+                w[blk + 208:blk + 210] = hb
+    out = M.dequant_rows(typ, torch.from_numpy(w).to(cuda), n, rows).cpu().numpy()
+    want = np.stack([oracle.dequant_row(typ, w[i * rb:(i + 1) * rb], n) for i in range(rows)])
+    np.testing.assert_array_equal(np.isnan(out), np.isnan(want))
+    fin = ~np.isnan(want)
+    np.testing.assert_array_equal(out[fin], want[fin])
+    assert np.isinf(want).any() and np.isnan(want).any()

@@ -53,10 +53,10 @@ CONFIGS = [("olmoe-q8_0", 1), ("olmoe-q4_k_m", 1), ("olmoe-q4_k_m", 4), ("olmoe-
 
 
 @pytest.mark.parametrize("name,T", CONFIGS)
-@pytest.mark.parametrize("plan", [0, 2, 3])
+@pytest.mark.parametrize("plan", [0, 2, 3, 5])
 def test_moe_ffn_matches_oracle(cuda, oracle, path, name, T, plan):
-    if plan == 3 and T > 1:
-        pytest.skip("plan 3 (fused experts kernel) is a one-token decode plan")
+    if plan in (3, 5) and T > 1:
+        pytest.skip("plans 3 and 5 (fused experts kernel, whole-layer kernel) are one-token decode plans")
     path(plan)
     shape = W.SHAPES[name]
     m = M.DeviceMoE(shape, 1, seed=51)
@@ -287,7 +287,7 @@ def test_decode_stages_equal_forward(cuda, path, name, plan):
     m.close()
 
 
-@pytest.mark.parametrize("plan", [1, 3])
+@pytest.mark.parametrize("plan", [1, 3, 5])
 @pytest.mark.parametrize("name", ["olmoe-q8_0", "qwen3-30b-a3b-q4_k_m"])
 def test_decode_plan_ties_take_the_exact_path(cuda, oracle, path, name, plan):
     """Exactly tied router rows inside and at the edge of the top-k: the
@@ -314,4 +314,35 @@ def test_decode_plan_ties_take_the_exact_path(cuda, oracle, path, name, plan):
         m.decode_stage(0, stage, xs[0], hbt[0], state, ib, wb)
     flags = state[-256:].view(torch.int32)  # the flag word is the state's last 256-byte slot
     assert int(flags[0].cpu()) & 2, "near tie not reported"
+    m.close()
+
+
+@pytest.mark.parametrize("name", ["qwen3-30b-a3b-q4_k_m", "olmoe-q8_0", "olmoe-q4_k_m", "qwen3-30b-a3b-q8_0"])
+def test_layer_kernel_sequence(cuda, oracle, path, name):
+    """Plan 5 runs the whole one-token layer in one launch whose workgroups
+    meet through records tagged with the launch's number: many calls in a
+    row, over two layers and distinct tokens, each matching the oracle and
+    the separate-kernel plan (the same decoders and combine order; the router
+    sums may differ in their last fp64 bits)."""
+    shape = W.SHAPES[name]
+    m = M.DeviceMoE(shape, 2, seed=62)
+    n = 12
+    x, hb = W.host_hidden(shape.d, n, 62)
+    hbt = torch.from_numpy(hb).to(cuda)
+    outs = {}
+    for plan in (1, 5):
+        path(plan)
+        xs = torch.from_numpy(x).to(cuda)
+        ids = []
+        for t in range(n):
+            idx, _ = m.forward(t % 2, xs[t:t + 1], hbt[t:t + 1], return_routing=True)
+            ids.append(idx.cpu().numpy()[0])
+        outs[plan] = (xs.cpu().numpy(), np.array(ids))
+    for layer in (0, 1):
+        sel = np.arange(layer, n, 2)
+        xo, io, _, _ = oracle_layer(oracle, m, layer, x, hb, tokens=sel)
+        check(f"{name} plan 5 layer {layer}", x[sel], outs[5][0][sel], xo, outs[5][1][sel], io)
+    np.testing.assert_array_equal(outs[5][1], outs[1][1])
+    d5, d1 = outs[5][0] - x, outs[1][0] - x
+    assert np.abs(d5 - d1).max() <= 1e-5 * np.abs(d1).max()
     m.close()

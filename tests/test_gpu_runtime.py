@@ -52,8 +52,10 @@ def test_graph_survives_workspace_growth(cuda, lib):
     m.close()
 
 
-def test_fused_wait_timeout_is_reported(cuda, lib):
-    """Plan 3 (one fused experts kernel whose workgroups meet once): with the
+@pytest.mark.parametrize("plan", [3, 5])
+def test_fused_wait_timeout_is_reported(cuda, lib, plan):
+    """Plan 3 (one fused experts kernel whose workgroups meet once) and plan 5
+    (the whole layer in one launch, meeting twice): with the
     poll limit at 0 every workgroup gives up at once, the kernel still ends,
     a synchronous call returns -ETIMEDOUT and a stream call's status reads
     -ETIMEDOUT; with the default limit the same call succeeds and equals the
@@ -65,7 +67,7 @@ def test_fused_wait_timeout_is_reported(cuda, lib):
     ref = torch.from_numpy(x0).to(cuda)
     m.forward(0, ref, hb)  # plan 0 (separate kernels)
     torch.cuda.synchronize()
-    _lib.check(lib.vireo_hip_set_path(3), "set_path")
+    _lib.check(lib.vireo_hip_set_path(plan), "set_path")
     try:
         assert lib.vireo_hip_status(None) == 0
         _lib.check(lib.vireo_hip_set_spin_limit(0), "set_spin_limit")

@@ -41,10 +41,11 @@ def oracle_stack(oracle, st):
     return step
 
 
-@pytest.mark.parametrize("name", ["qwen3-16e", "tiny"])
-def test_stack_decode_matches_oracle(cuda, oracle, name):
+@pytest.mark.parametrize("name,plan", [("qwen3-16e", 0), ("qwen3-16e", 5), ("tiny", 0)])
+def test_stack_decode_matches_oracle(cuda, oracle, name, plan):
     """qwen3-16e: Qwen3-30B-A3B layers (Q4_K / Q6_K, d=2048, fe=768, top-8
-    renormalised) with 16 experts each, on the one-token decode plan; tiny:
+    renormalised) with 16 experts each, on the one-token decode plan (plan 0)
+    and on the whole-layer kernel with the RMSNorm fused in (plan 5); tiny:
     d=256 layers, which take the grouped plan."""
     if name == "qwen3-16e":
         shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"].with_(name=name, E=16)
@@ -52,6 +53,9 @@ def test_stack_decode_matches_oracle(cuda, oracle, name):
     else:
         shape = W.MoEShape(name, 256, 8, 2, 256, True, W.Q4_K, W.Q4_K, W.Q6_K)
         n_layers, vocab = 4, 1000
+    from vireo_amd import _lib
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_set_path(plan), "vireo_hip_set_path")
     st = S.DeviceStack(shape, n_layers, vocab=vocab, seed=61)
     ref = oracle_stack(oracle, st)
     token = torch.empty(1, dtype=torch.int32, device=cuda)
@@ -68,6 +72,7 @@ def test_stack_decode_matches_oracle(cuda, oracle, name):
         if top2[1] - top2[0] > TOL * np.abs(lo).max():
             assert tg == to
     st.close()
+    lib.vireo_hip_set_path(0)
 
 
 def test_embed_rows_and_range(cuda, oracle):

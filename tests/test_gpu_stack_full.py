@@ -41,7 +41,11 @@ def oracle_routing(oracle, shape, router, xb):
     return idx, float(gaps.min())
 
 
-def test_stack48_full_size_matches_oracle(cuda, oracle):
+@pytest.mark.parametrize("plan", [0, 5])
+def test_stack48_full_size_matches_oracle(cuda, oracle, plan):
+    from vireo_amd import _lib
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_set_path(plan), "vireo_hip_set_path")
     shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
     L, vocab, steps = 48, 151936, 8
     st = S.DeviceStack(shape, L, vocab=vocab, seed=2024)
@@ -96,3 +100,4 @@ def test_stack48_full_size_matches_oracle(cuda, oracle):
     print(f"{compared} layer routings equal to the oracle's, {near} near ties, {fallback} exact-logit fallbacks")
     assert compared >= L * steps // 2
     st.close()
+    lib.vireo_hip_set_path(0)

@@ -157,6 +157,47 @@ size_t decode_state_layout(const vireo_moe_model *m, size_t off[4]) {
     return o;
 }
 
+// Plan 5 (and plan 0 once it is measured faster): the whole layer in one launch.
+bool layer_kernel(const vireo_moe_model *m, int layer, const float *xin, const float *x) {
+    if (g_path != 5) return false;
+    const vireo_moe_layer &L = m->layers[layer];
+    if ((reinterpret_cast<uintptr_t>(xin) | reinterpret_cast<uintptr_t>(x) |
+         reinterpret_cast<uintptr_t>(L.router->data)) & 15u)
+        return false;
+    return vh_layer_supported(L.gate_exps->ggml_type, L.down_exps->ggml_type, m->dim, m->n_experts, m->n_used,
+                              m->ffn_exp) != 0;
+}
+
+// One token through layer `layer` with the layer kernel: xin = hb (norm false)
+// or the residual x (norm true, RMSNorm by nw / eps in front; hb_out receives hb).
+int run_layer_kernel(const vireo_moe_model *m, int layer, const void *const *table, const float *xin, float *x,
+                     bool norm, const float *nw, float eps, float *hb_out, int32_t *idx, float *w, uint32_t *flags,
+                     hipStream_t s) {
+    const vireo_moe_layer &L = m->layers[layer];
+    LayerXchg *xg = nullptr;
+    if (int rc = vh_layer_xchg(&xg)) return rc;
+    LayerArgs a;
+    a.R = static_cast<const float *>(L.router->data);
+    a.xin = xin;
+    a.table = table;
+    a.xg = xg;
+    a.E = m->n_experts;
+    a.k = m->n_used;
+    a.fe = m->ffn_exp;
+    a.d = m->dim;
+    a.renorm = m->topk_renorm;
+    a.bias = L.logit_bias;
+    a.x = x;
+    a.idx = idx;
+    a.w = w;
+    a.flags = flags;
+    a.norm = norm;
+    a.nw = nw;
+    a.eps = eps;
+    a.hb_out = hb_out;
+    return vh_moe_layer(L.gate_exps->ggml_type, L.down_exps->ggml_type, a, s);
+}
+
 bool fused(const vireo_moe_model *m, int layer) {
     if (g_path != 3) return false;
     const vireo_moe_layer &L = m->layers[layer];
@@ -217,6 +258,12 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
     }
     Ws ws;
     if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, true, false, &ws)) return rc;
+    if (layer_kernel(m, layer, x, x)) {  // RMSNorm, router, experts and combine in one launch
+        int32_t *idx = idx_out ? idx_out : ws.idx;
+        int rc = run_layer_kernel(m, layer, table, x, x, true, nw, eps, xb, idx, ws.w, flags_out, s);
+        if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, m->n_used, s);
+        return rc;
+    }
     const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
     int rc = vh_route_parts_norm(static_cast<const float *>(L.router->data), x, nw, eps, xb, L.logit_bias, m->dim,
                                  m->n_experts, 1, st.parts, s, st.bar, kFusedBlocks + 1);
@@ -322,7 +369,7 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
 }
 
 extern "C" int vireo_hip_set_path(int path) {
-    if (path < 0 || path > 4) return -EINVAL;
+    if (path < 0 || path > 5) return -EINVAL;
     g_path = path;
     return 0;
 }
@@ -509,6 +556,13 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
+    if (decode && !src && layer_kernel(m, layer, hb, x)) {  // the whole layer in one launch
+        rc = run_layer_kernel(m, layer, table, hb, x, false, nullptr, 0.0f, nullptr, idx, w, flags_out, s);
+        if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
+        rc = vh_finish(s, rc);
+        if (!rc && !s) rc = vh_take_status(s);  // a grid-wide wait that gave up
+        return rc;
+    }
     if (decode) {
         const DecodeState st{ws.parts, ws.plan, ws.h, ws.bar};
         rc = 0;

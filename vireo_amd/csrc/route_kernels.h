@@ -139,3 +139,35 @@ int vh_fused_blocks(uint32_t tg, uint32_t td, int d, int E, int k, int fe);  // 
 int vh_decode_experts(uint32_t tg, uint32_t td, const RoutePart *parts, const float *R, const float *hb,
                       const float *bias, int d, int E, int k, int fe, int renorm, const void *const *table, float *h,
                       uint32_t *bar, float *x, int32_t *idx, float *w, NormRef nref, hipStream_t s);
+
+// One MoE layer for one token in one launch (moe_layer.hip): router, top-k,
+// gate/up, down, combine, residual, with the RMSNorm in front when norm is
+// set (xin is then the residual x itself). kLayerBlocks workgroups, all
+// resident at once, meet through tagged records in a LayerXchg that is zeroed
+// once per device (vh_layer_xchg) and shared by every launch there.
+constexpr int kLayerBlocks = 256;
+constexpr int kMaxLayerFe = 1024;
+struct LayerXchg {
+    uint32_t gen[kLayerBlocks];        // per workgroup: the number of its last launch
+    uint64_t parts[2 * 128];           // router parts, two tagged words per expert
+    uint64_t h[8 * kMaxLayerFe];       // SwiGLU activations per round, tagged
+};
+struct LayerArgs {
+    const float *R;                    // router [E x d]
+    const float *xin;                  // hb, or (norm) the residual x
+    const void *const *table;          // the layer's expert table [E x 3]
+    LayerXchg *xg;
+    int E, k, fe, d, renorm;
+    const float *bias;                 // logit bias or NULL
+    float *x;                          // residual, updated in place
+    int32_t *idx;                      // [k] routing out
+    float *w;                          // [k] weights out
+    uint32_t *flags;                   // [1] VIREO_ROUTE_* bits out, or NULL
+    bool norm;
+    const float *nw;                   // norm weight or NULL (unit)
+    float eps;
+    float *hb_out;                     // (norm) hb written here when not NULL
+};
+int vh_layer_supported(uint32_t tg, uint32_t td, int d, int E, int k, int fe);
+int vh_moe_layer(uint32_t tg, uint32_t td, const LayerArgs &a, hipStream_t s);
+int vh_layer_xchg(LayerXchg **out);

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 #include "common.h"
+#include "route_kernels.h"
 #include "vireo_hip.h"
 
 namespace {
@@ -23,6 +24,7 @@ struct DevState {
     hipEvent_t host_done = nullptr;
     bool host_done_set = false;
     uint32_t *status = nullptr;   // sticky device status bits (VIREO_DECODE_TIMEOUT)
+    LayerXchg *xchg = nullptr;    // the layer kernel's exchange area (zeroed once)
 };
 unsigned g_spin_limit = 1u << 18;
 DevState g_dev[kMaxDev];
@@ -181,6 +183,21 @@ int vh_status_word(uint32_t **out) {
 }
 
 unsigned vh_spin_limit() { return g_spin_limit; }
+
+int vh_layer_xchg(LayerXchg **out) {
+    int d = cur_dev();
+    if (d < 0) return -ENODEV;
+    DevState &st = g_dev[d];
+    if (!st.xchg) {
+        void *p = nullptr;
+        if (int rc = vh_check(hipMalloc(&p, sizeof(LayerXchg)))) return rc == -EIO ? -ENOMEM : rc;
+        if (int rc = vh_check(hipMemset(p, 0, sizeof(LayerXchg)))) return rc;
+        if (int rc = vh_check(hipDeviceSynchronize())) return rc;
+        st.xchg = static_cast<LayerXchg *>(p);
+    }
+    *out = st.xchg;
+    return 0;
+}
 
 // Read and clear the sticky status bits after the stream's work is done.
 int vh_take_status(hipStream_t s) {
