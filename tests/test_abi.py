@@ -78,7 +78,7 @@ def test_strerror(lib):
 
 def test_argument_checks_before_device_work(lib):
     EINVAL = -errno.EINVAL
-    assert lib.vireo_hip_set_path(5) == EINVAL
+    assert lib.vireo_hip_set_path(6) == EINVAL and lib.vireo_hip_set_path(-1) == EINVAL
     assert lib.vireo_hip_set_path(0) == 0
     assert lib.moe_ffn_forward(None, 0, None, None, 1, None, None, None) == EINVAL
     assert lib.moe_route(None, 0, None, 1, None, None, None, None, None) == EINVAL

@@ -123,6 +123,14 @@ template <int CTRL, int ROW_MASK = 0xf>
 VH_DEV uint32_t dpp_u(uint32_t v) {
     return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, ROW_MASK, 0xf, false));
 }
+// A workgroup barrier that orders LDS only: it waits for this wave's LDS
+// operations, not for its global loads in flight (__syncthreads waits for
+// those too), so loads issued before it keep streaming across it.
+VH_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 // Sum over aligned groups of L lanes (L a power of two <= 64). The total is in
 // the last lane of each group (lane % L == L-1); for L <= 16 every lane of the
 // group holds it. Must be called with all 64 lanes active.

@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     __shared__ double2 cert[kWaves][64];
     __shared__ RoutePart sparts[64 * Q];
     __shared__ double red_d[3][kWaves];
-    __shared__ float hs[kWaves][1024];
+    __shared__ __align__(16) float hs[kWaves][1024];
     __shared__ float ys[kWaves][kRB];
     __shared__ int pres[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -177,15 +177,23 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
                 timed_out = true;
                 break;
             }
+            // every load of the round first (each agent-scope load is awaited
+            // where its value is used, so loads used one by one would travel
+            // one round trip at a time), then the checks
+            uint64_t a[Q], w2[Q];
+#pragma unroll
+            for (int q = 0; q < Q; q++) {
+                const int e = min(lane + 64 * q, E - 1);
+                a[q] = ld_agent64(xg->parts + 2 * e);
+                w2[q] = ld_agent64(xg->parts + 2 * e + 1);
+            }
             bool good = true;
 #pragma unroll
             for (int q = 0; q < Q; q++) {
                 const int e = lane + 64 * q;
                 if (e < E) {
-                    const uint64_t a = ld_agent64(xg->parts + 2 * e), w2 = ld_agent64(xg->parts + 2 * e + 1);
-                    const bool fresh = (a & 0xffu) == (epoch & 0xffu) && uint32_t(w2 >> 32) == epoch;
-                    good &= fresh;
-                    sparts[e] = RoutePart{__longlong_as_double(int64_t(a)), double(__uint_as_float(uint32_t(w2)))};
+                    good &= (a[q] & 0xffu) == (epoch & 0xffu) && uint32_t(w2[q] >> 32) == epoch;
+                    sparts[e] = RoutePart{__longlong_as_double(int64_t(a[q])), double(__uint_as_float(uint32_t(w2[q])))};
                 }
             }
             if (__ballot(good) == __builtin_amdgcn_read_exec()) break;
@@ -199,13 +207,26 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
         p[q] = e < E ? sparts[e] : RoutePart{0.0, 0.0};
     }
 
-    // ---- 3. selection: gate/up expert of slot j, down expert of round wv
+    // ---- 3. the ranking, by the whole workgroup in one counting pass, and
+    //         its certification by every wave on its own (the same verdict in
+    //         every wave and workgroup): gate/up expert of slot j, down expert
+    //         of round wv. An order that cannot be certified is ranked again on
+    //         exact logits by the whole workgroup (rare), before any weight is
+    //         loaded.
     const int j = b / (kLB / kWaves);
-    int e_j, e_dn, rank[Q];
-    const bool ok = route_select_wave<Q>(p, E, k, j, e_j, wv, e_dn, rank, cert[wv]);
+    __shared__ __align__(16) uint32_t rkeys[64 * Q];
+    __shared__ int rcnt[512];
+    int rank[Q];
+    route_rank_block<Q>(p, E, k, rkeys, rcnt, rank, nullptr);
+    const bool certified = route_certify_wave<Q>(p, E, k, rank, cert[wv]);
     float w_sel = 0.0f;  // wave 0, lane t < k: the weight of round t
     int e_sel = 0;
-    if (!ok) {  // the same verdict in every wave: the whole workgroup ranks on exact logits
+    int e_j, e_dn;
+    if (certified) {
+        e_j = rank_owner<Q>(rank, j);
+        e_dn = rank_owner<Q>(rank, wv);
+        if (b == 0 && tid == 0 && flags_out) flags_out[0] = 0u;
+    } else {
         const float *xe = xin;
         if constexpr (NORM) {  // on the reference's own xb, not on the fp64-normalised hb
             reference_rmsnorm_block(xref, xin, nw, eps, d, &sm.red[0][0]);
@@ -219,13 +240,6 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
             w_sel = sm.sel_w[lane];
         }
         if (b == 0 && tid == 0 && flags_out) flags_out[0] = sm.flag;
-    } else {
-        if (wv == 0) route_weights_wave<Q>(p, rank, E, k, renorm, stage, e_sel, w_sel);
-        if (b == 0 && tid == 0 && flags_out) flags_out[0] = 0u;
-    }
-    if (b == 0 && wv == 0 && lane < k) {
-        idx_out[lane] = e_sel;
-        w_out[lane] = w_sel;
     }
 
     // ---- 4. every weight load of the workgroup: gate/up rows, then down rows
@@ -254,6 +268,14 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
                 rd[u][m] = FD::fetch(gmem(Dp), int64_t(o_dn + grp * UPG + u) * rb_dn, min(li + L * m, items_dn - 1));
     }
 
+    // the softmax weights of the certified order, by wave 0 while its loads
+    // are in flight
+    if (certified && wv == 0) route_weights_wave<Q>(p, rank, E, k, renorm, stage, e_sel, w_sel);
+    if (b == 0 && wv == 0 && lane < k) {
+        idx_out[lane] = e_sel;
+        w_out[lane] = w_sel;
+    }
+
     // ---- 5. gate/up rows of expert slot j, published as tagged values
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
@@ -269,21 +291,38 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
             st_agent64(xg->h + size_t(j) * kMaxLayerFe + o0 + r, (uint64_t(epoch) << 32) | __float_as_uint(hval));
         }
     }
+    // the workgroup's activations are stored (not necessarily visible yet):
+    // one small record that consumers poll before reading the values, which
+    // carry their own tags and are checked again, so the barrier orders
+    // nothing in memory and need not wait for the down rows in flight
+    lds_barrier();
+    if (tid == 0) st_agent64(&xg->done[j][b % (kLB / kWaves)], epoch);
 
-    // ---- 6. wave wv polls the activations of the expert of round wv
+    // ---- 6. wave wv polls the producers of the expert of round wv, then reads
+    //         its activations (and reads them again until every tag is fresh)
     {
         const uint64_t *hw = xg->h + size_t(wv) * kMaxLayerFe;
-        const int per = fe / 64;  // values per lane (fe is a multiple of 64)
+        const uint64_t *dw = xg->done[wv];
+        constexpr int per = RPW * 4;  // values per lane: fe = 256 RPW (768 or 1024)
+        bool producers = false;
         for (unsigned spins = 0;; spins++) {
             if (spins >= spin_limit) {
                 timed_out = true;
                 break;
             }
+            if (!producers) {
+                const bool fresh = lane >= kLB / kWaves || uint32_t(ld_agent64(dw + lane)) == epoch;
+                producers = __ballot(fresh) == __builtin_amdgcn_read_exec();
+                if (!producers) continue;
+            }
+            uint64_t v[per];  // all of the round's loads first, then the checks
+#pragma unroll
+            for (int q = 0; q < per; q++) v[q] = ld_agent64(hw + lane + 64 * q);
             bool good = true;
+#pragma unroll
             for (int q = 0; q < per; q++) {
-                const uint64_t v = ld_agent64(hw + lane + 64 * q);
-                good &= uint32_t(v >> 32) == epoch;
-                hs[wv][lane + 64 * q] = __uint_as_float(uint32_t(v));
+                good &= uint32_t(v[q] >> 32) == epoch;
+                hs[wv][lane + 64 * q] = __uint_as_float(uint32_t(v[q]));
             }
             if (__ballot(good) == __builtin_amdgcn_read_exec()) break;
         }
@@ -297,15 +336,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     float xv[IPL][32], xsd[IPL][NSD];
 #pragma unroll
     for (int m = 0; m < IPL; m++) {
-        const int it = min(li + L * m, items_dn - 1);
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            int c;
-            if constexpr (TD == VT_Q6_K) c = Split<VT_Q6_K>::col0(it) + 32 * (i >> 3) + (i & 7);
-            else if constexpr (TD == VT_Q4_K) c = Split<VT_Q4_K>::col0(it) + (i < 16 ? i : i + 16);
-            else c = 32 * it + i;
-            xv[m][i] = hs[wv][c];
-        }
+        FD::load_x(&hs[wv][0], min(li + L * m, items_dn - 1), xv[m]);  // the item's inputs, 16-byte LDS reads
         FD::sums(xv[m], xsd[m]);
     }
 #pragma unroll
@@ -380,6 +411,7 @@ int vh_layer_supported(uint32_t tg, uint32_t td, int d, int E, int k, int fe) {
 }
 
 int vh_moe_layer(uint32_t tg, uint32_t td, const LayerArgs &a, hipStream_t s) {
+    // fe = 256 RPW of the variant (the activation polls take fe / 64 values per lane)
     if (!vh_layer_supported(tg, td, a.d, a.E, a.k, a.fe) || !a.xg || !a.idx || !a.w) return -EINVAL;
     const int v = layer_variant(tg, td, a.d, a.E, a.k, a.fe);
     return a.E <= 64 ? launch_q<1>(tg, v, a, s) : launch_q<2>(tg, v, a, s);

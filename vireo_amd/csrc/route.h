@@ -365,6 +365,119 @@ VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, i
     return __builtin_amdgcn_read_exec() == __ballot(good);
 }
 
+// The two halves of route_select_wave, for callers that act on the ranking
+// before it is certified (and redo the work when it is not): k rounds of the
+// wave-wide max over the 32-bit keys (rank[q] = the round of slot q, -1 if not
+// chosen; sel[t] (LDS, k entries) = the expert of round t, written by the lane
+// that owns it), then the certification of that order as route_select_wave
+// does it (cert: 64 entries of this wave's LDS; the same verdict on every
+// lane, and in every wave or workgroup given the same parts).
+template <int Q>
+VH_DEV void route_rank_wave(const RoutePart (&p)[Q], int E, int k, int (&rank)[Q], int *sel) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? ((ordered_u32(float(p[q].c)) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
+        rank[q] = -1;
+    }
+    for (int t = 0; t < k; t++) {
+        uint32_t best = 0u;
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (rank[q] < 0 && key[q] > best) best = key[q];
+        const uint32_t wb = wave_max_u(best);
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (key[q] == wb) {  // keys are distinct: one slot of one lane
+                rank[q] = t;
+                sel[t] = lane + 64 * q;
+            }
+    }
+}
+
+// The same ranking as route_rank_wave by a whole workgroup of 512 threads in
+// one counting pass instead of k dependent wave-wide rounds: every wave holds
+// the same parts; the keys go to LDS, thread t counts the keys above the key of
+// expert t mod 64Q among one share of 64Q / (512 / 64Q) keys, and the shares'
+// counts meet in LDS. The rank of an expert is its count (distinct keys: the
+// same order as k rounds of the maximum). rank[q] is the rank of slot q when
+// below k, else -1, in every wave; sel[t] (LDS, k entries) is the expert of
+// rank t, written by wave 0 when sel is not null. Contains two LDS-only
+// workgroup barriers (global loads in flight keep streaming); keys holds 64Q
+// entries and cnt 512.
+template <int Q>
+VH_DEV void route_rank_block(const RoutePart (&p)[Q], int E, int k, uint32_t *keys, int *cnt, int (&rank)[Q],
+                             int *sel) {
+    constexpr int EP = 64 * Q, S = 512 / EP, N = EP / S;
+    static_assert(S * EP == 512 && N % 4 == 0, "512 threads cover the experts in whole shares");
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t key[Q], mine = 0u;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? ((ordered_u32(float(p[q].c)) & 0xffffff00u) | uint32_t(255 - e)) : 0u;
+        if (q == wv % Q) mine = key[q];
+    }
+    if (wv < Q) keys[tid] = mine;
+    lds_barrier();
+    const int s = wv / Q;  // this thread's share of keys
+    const uint4 *kv = reinterpret_cast<const uint4 *>(keys + s * N);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < N / 4; i++) {
+        const uint4 v = kv[i];
+        c += int(v.x > mine) + int(v.y > mine) + int(v.z > mine) + int(v.w > mine);
+    }
+    cnt[s * EP + (tid % EP)] = c;
+    lds_barrier();
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int e = lane + 64 * q;
+        int r = 0;
+#pragma unroll
+        for (int t = 0; t < S; t++) r += cnt[t * EP + e];
+        rank[q] = e < E && r < k ? r : -1;
+        if (sel && wv == 0 && rank[q] >= 0) sel[r] = e;
+    }
+}
+
+// The expert of rank t (0 <= t < k) from rank[] as route_rank_block leaves
+// it, on every lane of the wave.
+template <int Q>
+VH_DEV int rank_owner(const int (&rank)[Q], int t) {
+    int e = 0;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const uint64_t m = __ballot(rank[q] == t);
+        if (m) e = 64 * q + __builtin_ctzll(m);
+    }
+    return e;
+}
+
+template <int Q>
+VH_DEV bool route_certify_wave(const RoutePart (&p)[Q], int E, int k, const int (&rank)[Q], double2 *cert) {
+    const int lane = threadIdx.x & 63;
+    float rest = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        if (rank[q] >= 0) cert[rank[q]] = make_double2(p[q].c - p[q].beta, p[q].c + p[q].beta);
+        else if (lane + 64 * q < E) rest = fmaxf(rest, __double2float_ru(p[q].c + p[q].beta));
+    }
+    rest = wave_max_f(rest);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool good = true;
+    if (lane < k) {
+        const double lo = cert[lane].x;
+        if (lane + 1 < k) good = lo - cert[lane + 1].y > kRouteMargin;
+        else if (k < E) good = lo - double(rest) > kRouteMargin;
+    }
+    return __builtin_amdgcn_read_exec() == __ballot(good);
+}
+
 // Softmax weights of the experts chosen by route_select_wave (src/gguf_run.c:
 // 181-192), by one wave: lane t < k returns the expert of round t in e_out and
 // its weight (renormalised over the k in selection order when renorm).

@@ -151,6 +151,7 @@ struct LayerXchg {
     uint32_t gen[kLayerBlocks];        // per workgroup: the number of its last launch
     uint64_t parts[2 * 128];           // router parts, two tagged words per expert
     uint64_t h[8 * kMaxLayerFe];       // SwiGLU activations per round, tagged
+    uint64_t done[8][kLayerBlocks / 8];  // per round and producer workgroup: its activations are stored
 };
 struct LayerArgs {
     const float *R;                    // router [E x d]
