@@ -94,6 +94,53 @@ def test_decode_batch_every_type(cuda, oracle, types, T):
     m.close()
 
 
+@pytest.mark.parametrize("plan", [0, 1, 3, 5])
+def test_decode_probability_ties(cuda, oracle, path, plan):
+    """A token whose inputs are so large that all but a few probabilities
+    underflow to zero: every one-token plan chooses as the reference does (the
+    lowest ids among the zero-probability experts)."""
+    path(plan)
+    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
+    m = M.DeviceMoE(shape, 1, seed=58)
+    x, hb = W.host_hidden(shape.d, 1, 58)
+    hb *= np.float32(3.0e5)
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    assert (wo == 0).any()
+    check(f"probability ties plan={plan}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    np.testing.assert_allclose(w.cpu().numpy(), wo, rtol=1e-5, atol=1e-30)
+    m.close()
+
+
+@pytest.mark.parametrize("T", [1, 7, 40])
+@pytest.mark.parametrize("plan", [0, 4])
+def test_decode_batch_matrix_cores(cuda, oracle, path, T, plan):
+    """Q4_K_M calls of fewer than 64 tokens run on the matrix cores (plan 0)
+    or on the fp32 decode-batch kernels (plan 4). With 40 tokens over 8
+    experts (top 4) every group holds more than one 16-token tile. Token 0's
+    inputs are scaled past the fp16 range (their split takes a power of two
+    per token) and token 1's far below it."""
+    path(plan)
+    shape = W.MoEShape("mdec-8e", 2048, 8, 4, 768, True, W.Q4_K, W.Q4_K, W.Q6_K)
+    m = M.DeviceMoE(shape, 1, seed=57)
+    x, hb = W.host_hidden(shape.d, T, 57)
+    hb[0] *= 3.0e5
+    if T > 1:  # a contribution of about 1e-12: the residual is zeroed so that it shows in x
+        hb[1] *= 1.0e-6
+        x[1] = 0.0
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    np.testing.assert_array_equal(idx.cpu().numpy(), io)
+    xg = xt.cpu().numpy()
+    for t in range(T):  # per token: token 0's contribution is 10^11 times token 1's
+        check(f"mdec T={T} plan={plan} token {t}", x[t:t + 1], xg[t:t + 1], xo[t:t + 1], io[t:t + 1], io[t:t + 1])
+    if T == 40:  # most groups span two token tiles
+        assert (np.bincount(io.reshape(-1), minlength=shape.E) > 16).sum() >= 4
+    m.close()
+
+
 @pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
 def test_golden_moe_on_gpu(cuda, case):
     g = golden(f"moe_{case}.npz")

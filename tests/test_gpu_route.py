@@ -44,8 +44,7 @@ def test_route_matches_oracle(cuda, oracle, name, T):
     np.testing.assert_allclose(probs.cpu().numpy(), op, rtol=1e-5, atol=1e-8)
     fl = flags.cpu().numpy()
     assert not np.any(fl & NEAR_TIE)
-    if T >= 64:  # prefill: exact sequential logits, never a fallback
-        assert not np.any(fl & FALLBACK)
+    assert not np.any(fl & FALLBACK)  # routed calls take exact sequential logits: never a fallback
     m.close()
 
 
@@ -70,6 +69,26 @@ def test_route_exact_ties(cuda, oracle):
         assert flags.cpu().numpy()[0] & NEAR_TIE  # a tie inside or at the edge of the top-k is reported
     got = idx.cpu().numpy()
     assert 5 in got[0] and 9 in got[0]
+    m.close()
+
+
+@pytest.mark.parametrize("T", [1, 5, 70])
+def test_route_probability_ties(cuda, oracle, T):
+    """Inputs scaled until most probabilities underflow to exactly zero: the
+    reference ranks probabilities with the lowest id winning a tie, so the
+    experts after the few nonzero ones are the lowest ids left, not the next
+    largest logits (decode, routing and prefill paths)."""
+    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
+    m = M.DeviceMoE(shape, 1, seed=45)
+    x, hb = W.host_hidden(shape.d, T, 45)
+    hb *= np.float32(3.0e5)
+    idx, w, flags, probs = m.route(0, torch.from_numpy(hb).to(cuda), want_probs=True)
+    oi, ow, op = oracle_route(oracle, shape, m.host_router(0), hb)
+    assert (ow == 0).any(axis=1).all()  # every token chooses zero-probability experts
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5, atol=1e-30)
+    np.testing.assert_allclose(probs.cpu().numpy(), op, rtol=1e-5, atol=1e-30)
+    assert np.all(flags.cpu().numpy() & NEAR_TIE)  # the zero ties are reported
     m.close()
 
 

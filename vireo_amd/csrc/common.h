@@ -206,5 +206,22 @@ VH_DEV double wave_incl_scan_d(double v) {
     return v;
 }
 
+// ---- fp32 operations rounded one at a time ---------------------------------------
+// The reference's C arithmetic rounds every product and every sum. HIP's
+// __fmul_rn / __fadd_rn are plain * and +, which the compiler fuses into one
+// fma (one rounding) under its default contraction; these never fuse.
+VH_DEV float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+VH_DEV float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+VH_DEV float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+
 // ---- SwiGLU gate: silu(g) * u, as src/gguf_run.c:207 -----------------------------
 VH_DEV float swiglu(float g, float u) { return (g / (1.0f + expf(-g))) * u; }

@@ -23,15 +23,15 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(float *o, const float *x,
     double acc = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = xr[i];
-        acc += double(__fmul_rn(v, v));
+        acc += double(mul_rn(v, v));
     }
     acc = wave_sum_d(acc);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
     __syncthreads();
     const float ss = float((part[0] + part[1]) + (part[2] + part[3]));
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(n)), eps)));
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(n)), eps)));
     // w == nullptr: unit weight (x * r * 1.0f is x * r)
-    for (int i = threadIdx.x; i < n; i += 256) orow[i] = w ? __fmul_rn(__fmul_rn(xr[i], r), w[i]) : __fmul_rn(xr[i], r);
+    for (int i = threadIdx.x; i < n; i += 256) orow[i] = w ? mul_rn(mul_rn(xr[i], r), w[i]) : mul_rn(xr[i], r);
 }
 
 // argmax in two launches: workgroup g of argmax_part_kernel reduces the
@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(256) embed_kernel(const uint8_t *__restrict__ 
     for (int c = threadIdx.x; c < n; c += 256) {
         if constexpr (T == VT_Q8_0) {  // src/gguf_compute.c:112-120: qs * d, exact
             const uint8_t *b = r + 34 * (c >> 5);
-            o[c] = __fmul_rn(float(int8_t(ld_u8(b + 2 + (c & 31)))), h2f(ld_u16(b)));
+            o[c] = mul_rn(float(int8_t(ld_u8(b + 2 + (c & 31)))), h2f(ld_u16(b)));
         } else if constexpr (T == VT_F16) {
             o[c] = h2f(ld_u16(r + 2 * c));
         } else {

@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(256) kv_append_kernel(AppendArgs a, const floa
         a.dst[i][gd + j] = vi[j];
         // ks += (k - ks) * inv, three roundings as in the reference
         const float ks = a.ks[i][j];
-        a.ks[i][j] = __fadd_rn(ks, __fmul_rn(__fsub_rn(kj, ks), a.inv[i]));
+        a.ks[i][j] = add_rn(ks, mul_rn(sub_rn(kj, ks), a.inv[i]));
     }
 }
 
@@ -102,7 +102,7 @@ __global__ void __launch_bounds__(256) kv_score_kernel(const float *const *__res
     if (c >= ncand[h]) return;
     const float *a = q + size_t(h) * d, *b = ksum[h] + size_t(lo[h] + c) * d;
     float s = 0.0f;
-    for (int i = 0; i < d; i++) s = __fadd_rn(s, __fmul_rn(a[i], b[i]));
+    for (int i = 0; i < d; i++) s = add_rn(s, mul_rn(a[i], b[i]));
     scores[size_t(h) * stride + c] = s;
 }
 
@@ -451,7 +451,7 @@ __global__ void __launch_bounds__(256) kv_append_pos_kernel(float *__restrict__ 
         blk[size_t(slot) * d + j] = kj;
         blk[size_t(G + slot) * d + j] = v[size_t(i) * d + j];
         const float old = slot == 0 ? 0.0f : ks[j];  // a new block's mean starts at zero
-        ks[j] = __fadd_rn(old, __fmul_rn(__fsub_rn(kj, old), inv));
+        ks[j] = add_rn(old, mul_rn(sub_rn(kj, old), inv));
     }
 }
 

@@ -35,8 +35,8 @@ __global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, int nq
     float *p = h < nq ? q + size_t(h) * hs : k + size_t(h - nq) * hs;
     const float c = tab[j], s = tab[half + j];
     const float x0 = p[j], x1 = p[j + half];
-    p[j] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-    p[j + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+    p[j] = sub_rn(mul_rn(x0, c), mul_rn(x1, s));
+    p[j + half] = add_rn(mul_rn(x0, s), mul_rn(x1, c));
 }
 
 // The attention inputs of one token in one launch: workgroup h (one wave)
@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
             srow[i] = x;
             if (ks) {
                 const float old = slot == 0 ? 0.0f : ks[i];  // a new block's mean starts at zero
-                ks[i] = __fadd_rn(old, __fmul_rn(__fsub_rn(x, old), inv));
+                ks[i] = add_rn(old, mul_rn(sub_rn(x, old), inv));
             }
         }
     };
@@ -99,17 +99,17 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
     for (int c = 0; c < 4; c++)
         if (c < ng) {
             val[c] = p[64 * c + l];
-            if (j.bias) val[c] = __fadd_rn(val[c], j.bias[size_t(h) * hs + 64 * c + l]);
+            if (j.bias) val[c] = add_rn(val[c], j.bias[size_t(h) * hs + 64 * c + l]);
         }
     if (j.norm) {
         double part[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) part[c] = c < ng ? wave_sum_d(double(__fmul_rn(val[c], val[c]))) : 0.0;
+        for (int c = 0; c < 4; c++) part[c] = c < ng ? wave_sum_d(double(mul_rn(val[c], val[c]))) : 0.0;
         const float ss = float((part[0] + part[1]) + (part[2] + part[3]));
-        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(hs)), eps)));
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(hs)), eps)));
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            if (c < ng) val[c] = __fmul_rn(__fmul_rn(val[c], r), j.norm[64 * c + l]);
+            if (c < ng) val[c] = mul_rn(mul_rn(val[c], r), j.norm[64 * c + l]);
     }
     if (rotate && pos >= 0 && pos < max_pos) {
 #pragma unroll
@@ -120,8 +120,8 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         const float *tab = rope + size_t(pos) * hs;
         for (int i = l; i < half; i += 64) {
             const float cs = tab[i], sn = tab[half + i], x0 = row[i], x1 = row[i + half];
-            emit(i, __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
-            emit(i + half, __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)));
+            emit(i, sub_rn(mul_rn(x0, cs), mul_rn(x1, sn)));
+            emit(i + half, add_rn(mul_rn(x0, sn), mul_rn(x1, cs)));
         }
         return;
     }
@@ -140,7 +140,7 @@ struct AddJob {
 __global__ void __launch_bounds__(256) add_kernel(AddJob j0, AddJob j1, AddJob j2) {
     const AddJob &j = blockIdx.y == 0 ? j0 : blockIdx.y == 1 ? j1 : j2;
     if (!j.b) return;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < j.n; i += gridDim.x * 256) j.y[i] = __fadd_rn(j.y[i], j.b[i]);
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < j.n; i += gridDim.x * 256) j.y[i] = add_rn(j.y[i], j.b[i]);
 }
 
 // *pos += 1 (the device position of a captured decode loop)

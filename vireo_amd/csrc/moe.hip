@@ -25,7 +25,13 @@ namespace {
 // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the
 // fused experts kernel, 4 grouped plan without the matrix-core GEMMs
 int g_path = 0;
-constexpr int kExactRouteTokens = 64;  // from this many tokens on, exact sequential logits
+// From this many tokens on, every logit of a routed call is the reference's
+// exact sequential fp32 sum (route_exact_small_kernel for a decode batch,
+// route_exact_kernel for more): one chain's latency, cheaper than certifying
+// a batch whose uncertain tokens each wait for exact contenders, and the same
+// logits (so the same weights) for a token whatever batch it is in. The
+// one-token decode plans route inside their own kernels.
+constexpr int kExactRouteTokens = 1;
 
 bool type_ok(uint32_t t, int n) {
     switch (t) {  // the expert formats of the MoE models: Q8_0, Q4_K (gate/up), Q6_K (down)
@@ -57,6 +63,8 @@ struct Ws {
     int32_t *tiles, *small;  // matrix-core plan: token tiles, the other groups
     void *hs;                // matrix-core plan: bf16 h rows in dispatch order
     void *xb;                // matrix-core plan: bf16 copy of hb
+    void *xp;                // decode-batch matrix-core plan: split inputs [T x d x 4 bytes]
+    float *xsc;              // and their per-token scales [T]
     const void **tab;        // paged plan: [E + 1] expert tables [3 E] (one per batch, then the combine's)
     int32_t *act;            // paged plan: [E] active lists [E + 1] (one per batch)
 };
@@ -86,6 +94,8 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
+    const bool small = experts && grouped && T < kMfmaMinCall;
+    const size_t o_xp = small ? take(size_t(T) * d * 4) : 0, o_xsc = small ? take(size_t(T) * 4) : 0;
     const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
     const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
     void *base;
@@ -112,6 +122,8 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->small = mfma ? reinterpret_cast<int32_t *>(b + o_small) : nullptr;
     ws->hs = mfma ? b + o_hs : nullptr;
     ws->xb = mfma ? b + o_xb : nullptr;
+    ws->xp = small ? b + o_xp : nullptr;
+    ws->xsc = small ? reinterpret_cast<float *>(b + o_xsc) : nullptr;
     ws->tab = reinterpret_cast<const void **>(b + o_tab);
     ws->act = reinterpret_cast<int32_t *>(b + o_act);
     return 0;
@@ -456,7 +468,9 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     if ((rc = vh_copy_stream(&cs))) return rc;
     const uint64_t cap = vh_store_capacity(m->es), leased = vh_store_leased_bytes(m->es);
     const uint64_t room = cap > leased ? cap - leased : 1;  // cap 0: unbounded (room unused)
-    const bool gdec = n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
+    const bool mdec = n_tokens < kMfmaMinCall && g_path != 4 && vh_mdec_supported(tg, td, d, fe);
+    const bool gdec = !mdec && n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
+    if (mdec) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
     const void **present = tabs_h + size_t(E) * tab_n;  // the combine's table (the last one)
     memset(present, 0, tab_n * sizeof(void *));
     ExpertView views[kMaxExperts];
@@ -496,7 +510,12 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
             rc = vh_store_copy_fence(m->es, cs, s);  // the batch's page-ins land before its kernels
             if (!rc) rc = vh_check(hipMemcpyAsync(dt, tab, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
             if (!rc) rc = vh_check(hipMemcpyAsync(da, act, act_n * 4, hipMemcpyHostToDevice, s));
-            if (gdec) {
+            if (mdec) {
+                if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, da, dt, ws.xp, ws.xsc, d, fe, k, E, slots,
+                                             n_tokens, ws.h, s);
+                if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens,
+                                           ws.ybuf, s);
+            } else if (gdec) {
                 if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, da, dt, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
                 if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
             } else {
@@ -588,6 +607,13 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
+    } else if (n_tokens < kMfmaMinCall && g_path != 4 && vh_mdec_supported(tg, td, d, fe)) {
+        // calls of a decode batch's size, Q4_K_M experts: the matrix cores
+        if (!rc) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
+        if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, d, fe, k, E, slots,
+                                     n_tokens, ws.h, s);
+        if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, n_tokens,
+                                   ws.ybuf, s);
     } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
         // calls of a decode batch's size (a few tokens per group): inputs in registers
         if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, n_tokens, ws.h, s);

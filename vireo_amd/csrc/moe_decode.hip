@@ -298,9 +298,9 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
             const int present = __builtin_amdgcn_readlane(pres, j2);
             const float wv2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj2), j2));
             if (!present) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-            if (tid < R) a = __fadd_rn(a, __fmul_rn(wv2, ys[j2 * R + tid]));
+            if (tid < R) a = add_rn(a, mul_rn(wv2, ys[j2 * R + tid]));
         }
-        if (tid < R) x[o0 + tid] = __fadd_rn(xo, a);
+        if (tid < R) x[o0 + tid] = add_rn(xo, a);
     }
 }
 

@@ -232,9 +232,9 @@ __global__ void __launch_bounds__(512) decode_experts_kernel(
         for (int t = 0; t < k; t++) {
             const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_sel), t));
             if (!pres[t]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-            if (lane < RB) a = __fadd_rn(a, __fmul_rn(wt, ys[t][lane]));
+            if (lane < RB) a = add_rn(a, mul_rn(wt, ys[t][lane]));
         }
-        if (lane < RB) x[o_dn + lane] = __fadd_rn(xo, a);
+        if (lane < RB) x[o_dn + lane] = add_rn(xo, a);
     }
 }
 

@@ -379,9 +379,9 @@ __global__ void __launch_bounds__(256) combine_kernel(const int32_t *__restrict_
     for (int j = 0; j < k; j++) {
         const int e = idx[size_t(t) * k + j];
         if (e < 0 || !table[3 * e + 2]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-        a = __fadd_rn(a, __fmul_rn(w[size_t(t) * k + j], ybuf[(size_t(t) * k + j) * d + o]));
+        a = add_rn(a, mul_rn(w[size_t(t) * k + j], ybuf[(size_t(t) * k + j) * d + o]));
     }
-    x[size_t(t) * d + o] = __fadd_rn(x[size_t(t) * d + o], a);
+    x[size_t(t) * d + o] = add_rn(x[size_t(t) * d + o], a);
 }
 
 // tokens staged per chunk: 4 (more would not fit the registers of 512-thread

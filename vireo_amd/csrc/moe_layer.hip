@@ -109,16 +109,16 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     //      of the squares, rounded once): the same operations in every workgroup
     float4 hv = xin4;
     if constexpr (NORM) {
-        double ss = double(__fmul_rn(xin4.x, xin4.x)) + double(__fmul_rn(xin4.y, xin4.y)) +
-                    double(__fmul_rn(xin4.z, xin4.z)) + double(__fmul_rn(xin4.w, xin4.w));
+        double ss = double(mul_rn(xin4.x, xin4.x)) + double(mul_rn(xin4.y, xin4.y)) +
+                    double(mul_rn(xin4.z, xin4.z)) + double(mul_rn(xin4.w, xin4.w));
         ss = wave_sum_d(ss);
         if (lane == 0) red_d[2][wv] = ss;
         __syncthreads();
         double tot = 0.0;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) tot += red_d[2][w];
-        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(float(tot), float(d)), eps)));
-        auto scale = [&](float v, float wgt) { return nw ? __fmul_rn(__fmul_rn(v, r), wgt) : __fmul_rn(v, r); };
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(float(tot), float(d)), eps)));
+        auto scale = [&](float v, float wgt) { return nw ? mul_rn(mul_rn(v, r), wgt) : mul_rn(v, r); };
         hv = make_float4(scale(xin4.x, nw4.x), scale(xin4.y, nw4.y), scale(xin4.z, nw4.z), scale(xin4.w, nw4.w));
 #pragma unroll
         for (int i = 0; i < 32; i++) xr[i] = scale(xr[i], nw ? nwr[i] : 1.0f);
@@ -129,8 +129,8 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     // ---- 1. the router part of expert b: fp64 sum of the rounded products in
     //         column order and 1.001 u sum_k |S_k| over its prefix sums
     if (b < E) {
-        const float p0 = __fmul_rn(r4.x, hv.x), p1 = __fmul_rn(r4.y, hv.y), p2 = __fmul_rn(r4.z, hv.z),
-                    p3 = __fmul_rn(r4.w, hv.w);
+        const float p0 = mul_rn(r4.x, hv.x), p1 = mul_rn(r4.y, hv.y), p2 = mul_rn(r4.z, hv.z),
+                    p3 = mul_rn(r4.w, hv.w);
         const double t4 = ((double(p0) + double(p1)) + double(p2)) + double(p3);
         const double incl = wave_incl_scan_d(t4);
         if (lane == 63) red_d[0][wv] = incl;  // the wave's total
@@ -356,9 +356,9 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
         for (int t = 0; t < k; t++) {
             const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_sel), t));
             if (!pres[t]) continue;  // failed lookup: skipped (src/gguf_run.c:201)
-            if (lane < kRB) a = __fadd_rn(a, __fmul_rn(wt, ys[t][lane]));
+            if (lane < kRB) a = add_rn(a, mul_rn(wt, ys[t][lane]));
         }
-        if (lane < kRB) x[o_dn + lane] = __fadd_rn(xo, a);
+        if (lane < kRB) x[o_dn + lane] = add_rn(xo, a);
     }
     if (timed_out) atomicOr(status, VIREO_DECODE_TIMEOUT);
     if (tid == 0) xg->gen[b] = epoch;

@@ -1,0 +1,450 @@
+// Decode-batch grouped projections on the matrix cores, for calls of fewer
+// than kMfmaMinCall tokens whose experts are Q4_K (gate, up) and Q6_K (down),
+// the Q4_K_M layout. Such a call sends a few tokens to each expert (32 tokens,
+// top-8 of 128 experts: about two), and the fp32 decode-batch kernels
+// (moe_gdec.hip) convert every weight to fp32 again for each of them: they are
+// bound by the vector ALUs, not by HBM. Here a weight is converted once into a
+// 16-bit matrix operand and up to 16 tokens of its expert are multiplied
+// against it in one instruction.
+//
+// The operands hold the reference's values exactly - split where one 16-bit
+// value cannot hold them - and products are summed in fp32 (the weights of
+// src/gguf_compute.c:52-66 and :83-103, the sums of the matvec of :202-207):
+//  - gate/up, v_mfma_f32_16x16x32_f16. A Q4_K weight of sub-block s is
+//    d*sc_s*q - dmin*m_s. One operand holds sc_s*q (an integer below 1024,
+//    exact in fp16, formed by a packed fp16 fma that rounds once), another
+//    m_s; per super-block the matrix cores form C = sum sc*q*x and M = sum
+//    m*x, and the row adds d*C - dmin*M in fp32. The inputs, scaled by a
+//    power of two per token that keeps them below 2^14 in magnitude (no fp16
+//    overflow), are split into fp16 parts hi + lo (22 significant bits) by
+//    mdec_prep_kernel, in the order the weight operand's slots take.
+//  - down, v_mfma_f32_16x16x16_bf16. A Q6_K weight of sub-block s (16
+//    weights) is d*sc_s*(q - 32). The operand holds q + 128 (exact in bf16)
+//    and a second product with the constant -160 completes q - 32; each
+//    sub-block's sum is scaled by d*sc_s in fp32. The activations h are split
+//    into bf16 parts hi + lo (16 significant bits, fp32's range, no scale) by
+//    the gate/up kernel as it writes them, in the order the down operand's
+//    slots take.
+// Products of 16-bit parts are exact in fp32, so the results differ from the
+// fp32 kernels' only by the order of the fp32 sums and the dropped low bits of
+// the split inputs (relative 2^-22 and 2^-17 of the largest input).
+//
+// Matrix operands (both instructions): A is tokens x K - lane l supplies
+// token l % 16 -, B is K x weight rows - lane l supplies row l % 16 -, and the
+// lanes l / 16 = g supply the same K positions of A and B (8 per lane for
+// 16x16x32, 4 for 16x16x16); lane l receives rows 4 g .. 4 g + 3 (tokens) of
+// column l % 16 (weight row) of the result. Which K position a slot holds is
+// free as long as A and B agree: it is fixed by how a weight word is unpacked,
+// and the inputs are laid out to match.
+//
+// Grids: (row chunk, active expert slot, 16-token tile), 256 threads; gate/up
+// waves own 16 rows of gate and the same 16 of up, down waves 32 rows. Q6_K
+// rows (210 bytes per super-block) start at any even address; their 16-byte
+// loads rely on global memory accepting any alignment.
+#include <hip/hip_runtime.h>
+#include "common.h"
+#include "qdecode.h"
+#include "route_kernels.h"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTok = 16;  // tokens per tile (the A operand's rows)
+
+VH_DEV f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// ---- gate/up operand layout ---------------------------------------------------
+// Super-block b (256 weights), step u (0..7), lane group g: the qs word 8 g + u
+// (bytes 32 g + 4 u .. + 3 of the 128 qs bytes: weights 4 u .. 4 u + 3 of
+// sub-blocks 2 g (low nibbles) and 2 g + 1 (high nibbles)). Slot j of the
+// operand holds weight 32 (2 g + j / 4) + 4 u + {0, 2, 1, 3}[j % 4] of the
+// super-block. The inputs of one token: 16 fp16 values per (b, u, g) - the 8
+// hi parts, then the 8 lo parts - at ((b * 8 + u) * 4 + g) * 16.
+VH_DEV int q4k_slot_of(int r, int &chunk) {  // r = position in the super-block
+    const int g = r >> 6, hsub = (r >> 5) & 1, e = r & 31, u = e >> 2, p = e & 3;
+    chunk = u * 4 + g;
+    return 4 * hsub + (p == 1 ? 2 : p == 2 ? 1 : p);
+}
+
+// sc*q for the 8 nibbles of qs word w: nibbles as fp16 1024 + q (exponent
+// bits or'ed in), then (1024 + q) * sc - 1024 * sc in one packed fp16 fma,
+// exact (the result is an integer below 1024)
+VH_DEV f16x8 q4k_operand(uint32_t w, f16x2 s0, f16x2 n0, f16x2 s1, f16x2 n1) {
+    constexpr uint32_t kM = 0x000f000fu, kE = 0x64006400u;
+    const f16x2 a = __builtin_elementwise_fma(as_h2((w & kM) | kE), s0, n0);
+    const f16x2 b = __builtin_elementwise_fma(as_h2(((w >> 8) & kM) | kE), s0, n0);
+    const f16x2 c = __builtin_elementwise_fma(as_h2(((w >> 4) & kM) | kE), s1, n1);
+    const f16x2 e = __builtin_elementwise_fma(as_h2(((w >> 12) & kM) | kE), s1, n1);
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
+}
+
+// The 6-bit scale and min of sub-block j (0..7, a per-lane value) from the 12
+// packed bytes s0..s2 (src/gguf_compute.c:45-51), without branches.
+VH_DEV void q4k_scale_min_v(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &mn) {
+    const uint32_t bj = uint32_t(((uint64_t(s1) << 32) | s0) >> (8 * j)) & 0xffu;             // byte j
+    const uint32_t bj4 = (j < 4 ? s1 >> (8 * j) : s2 >> (8 * (j - 4))) & 0xffu;            // byte j + 4
+    const uint32_t bjm4 = (s0 >> (8 * (j & 3))) & 0xffu;                                   // byte j - 4 (j >= 4)
+    const int lo_sc = int(bj & 63u), lo_mn = int(bj4 & 63u);
+    const int hi_sc = int((bj4 & 15u) | ((bjm4 >> 6) << 4)), hi_mn = int((bj4 >> 4) | ((bj >> 6) << 4));
+    sc = j < 4 ? lo_sc : hi_sc;
+    mn = j < 4 ? lo_mn : hi_mn;
+}
+
+// ---- down operand layout -------------------------------------------------------
+// Q6_K sub-block s = 8 h + 2 j + lh of super-block b holds weights
+// 128 h + 32 j + 16 lh + (0..15) (src/gguf_compute.c:83-103); lane group g
+// takes weights 16 s + 4 g + {0, 2, 1, 3} (slot order). Activation k of a pair
+// is slot {0, 2, 1, 3}^-1 (k % 4) of chunk k / 4: 8 bf16 values per chunk,
+// the 4 hi parts then the 4 lo parts.
+VH_DEV int q6k_slot_of(int k) {
+    const int p = k & 3;
+    return p == 1 ? 2 : p == 2 ? 1 : p;
+}
+
+// One workgroup of 256 threads per token: the largest |x|, the power of two,
+// and the fp16 split of every input into the gate/up operand order.
+__global__ void __launch_bounds__(256) mdec_prep_kernel(const float *__restrict__ hb, int d,
+                                                        _Float16 *__restrict__ xp, float *__restrict__ xsc) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *x = hb + size_t(t) * d;
+    float m = 0.0f;
+    for (int i = tid; i < d; i += 256) m = fmaxf(m, fabsf(x[i]));
+    m = wave_max_f(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int ex = 0;
+    if (m > 0.0f && m <= 3.4028234663852886e38f) frexpf(m, &ex);  // m < 2^ex
+    const int sh = max(-120, min(120, 14 - ex));                  // |x 2^sh| < 2^14
+    const float up = ldexpf(1.0f, sh);
+    if (tid == 0) xsc[t] = ldexpf(1.0f, -sh);
+    _Float16 *o = xp + size_t(t) * d * 2;
+    for (int i = tid; i < d; i += 256) {
+        const float v = x[i] * up;
+        const _Float16 hi = _Float16(v);
+        const _Float16 lo = _Float16(v - float(hi));  // v - hi is exact in fp32
+        int chunk;
+        const int j = q4k_slot_of(i & 255, chunk);
+        const size_t c = (size_t(i >> 8) * 32 + chunk) * 16;
+        o[c + j] = hi;
+        o[c + 8 + j] = lo;
+    }
+}
+
+// gate/up: wave w of workgroup (c, s, z) owns rows 64 c + 16 w .. + 15 of gate
+// and up of expert active[s] for tokens 16 z .. of its group, and writes
+// h = silu(gate . x) * (up . x) (src/gguf_run.c:205-207) as bf16 hi + lo parts
+// in the down operand's order into hp (4 bytes per activation, rows of fe).
+// The tile's split inputs pass through LDS one super-block at a time, double
+// buffered (every wave reads them; they are loaded once per workgroup), and
+// each wave's weights for the next super-block are in flight while it
+// computes the current one.
+constexpr int kGuTokStride = 260;  // dwords per token and super-block in LDS: 256 + 4 (no bank conflicts)
+
+__global__ void __launch_bounds__(256) mdec_gateup_kernel(const int32_t *__restrict__ counts,
+                                                          const int32_t *__restrict__ offs,
+                                                          const int32_t *__restrict__ perm,
+                                                          const int32_t *__restrict__ active,
+                                                          const void *const *__restrict__ table,
+                                                          const uint4 *__restrict__ xp, const float *__restrict__ xsc,
+                                                          int d, int fe, int k, int E, int64_t row_bytes,
+                                                          uint16_t *__restrict__ hp) {
+    __shared__ __align__(16) uint32_t xs[2][kTok * kGuTokStride];
+    const int s = blockIdx.y;
+    if (s >= active[E]) return;
+    const int e = active[s], cnt = counts[e], base = offs[e], t0 = blockIdx.z * kTok;
+    if (t0 >= cnt) return;
+    const int tn = min(kTok, cnt - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int o = min((blockIdx.x * 4 + wv) * 16, fe - 16) + r;  // fe % 16 == 0: a wave past fe repeats rows
+    const bool live = (blockIdx.x * 4 + wv) * 16 < fe;
+    auto put = [&](int tt, float v) {  // activation of token tt of the tile at row o
+        const int pair = perm[base + t0 + tt];
+        const __bf16 hi = __bf16(v);
+        const __bf16 lo = __bf16(v - float(hi));
+        uint16_t *row = hp + size_t(pair) * fe * 2 + (o >> 2) * 8;
+        const int j = q6k_slot_of(o);
+        row[j] = __builtin_bit_cast(uint16_t, hi);
+        row[4 + j] = __builtin_bit_cast(uint16_t, lo);
+    };
+    gbyte *G = gmem(table[3 * e]);
+    gbyte *U = gmem(table[3 * e + 1]);
+    if (!G || !U) {  // an unregistered expert contributes nothing (src/gguf_run.c:201)
+        if (live)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (4 * g + i < tn) put(4 * g + i, 0.0f);
+        return;
+    }
+    // the split inputs of the tile's tokens: thread tid copies 16-byte piece
+    // tid % 64 of token tid / 64 + 4 i's super-block (rows past the tile's
+    // tokens repeat its last token; nothing reads them)
+    const int pc = tid & 63, pt = tid >> 6;
+    uint32_t srow[4];  // the tokens' rows of xp, in 16-byte pieces
+#pragma unroll
+    for (int i = 0; i < 4; i++) srow[i] = uint32_t(perm[base + t0 + min(pt + 4 * i, tn - 1)] / k) * uint32_t(d / 4) + pc;
+    uint32_t *xdst = &xs[0][pt * kGuTokStride + 4 * pc];
+    gbyte *gr = G + int64_t(o) * row_bytes;
+    gbyte *ur = U + int64_t(o) * row_bytes;
+    const int nb = d / 256;
+    struct Wt {
+        uint4 hd, q0, q1;
+    };
+    auto load = [&](gbyte *row, int b, Wt &w) {
+        gbyte *p = row + 144 * b;
+        w.hd = ld_u128(p);
+        w.q0 = ld_u128(p + 16 + 32 * g);
+        w.q1 = ld_u128(p + 32 + 32 * g);
+    };
+    Wt ng, nu;
+    uint4 xv0, xv1, xv2, xv3;
+    xv0 = xp[srow[0]];
+    xv1 = xp[srow[1]];
+    xv2 = xp[srow[2]];
+    xv3 = xp[srow[3]];
+    load(gr, 0, ng);
+    load(ur, 0, nu);
+    *reinterpret_cast<uint4 *>(xdst) = xv0;
+    *reinterpret_cast<uint4 *>(xdst + 4 * kGuTokStride) = xv1;
+    *reinterpret_cast<uint4 *>(xdst + 8 * kGuTokStride) = xv2;
+    *reinterpret_cast<uint4 *>(xdst + 12 * kGuTokStride) = xv3;
+    __syncthreads();
+    const uint32_t *xr = &xs[0][min(r, tn - 1) * kGuTokStride + 8 * g];  // this lane's token, lane group g
+    f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg;
+    for (int b = 0; b < nb; b++) {
+        const Wt cg = ng, cu = nu;
+        if (b + 1 < nb) {
+            xv0 = xp[srow[0] + 64 * (b + 1)];
+            xv1 = xp[srow[1] + 64 * (b + 1)];
+            xv2 = xp[srow[2] + 64 * (b + 1)];
+            xv3 = xp[srow[3] + 64 * (b + 1)];
+            load(gr, b + 1, ng);
+            load(ur, b + 1, nu);
+        }
+        const uint32_t *xb = xr + (b & 1) * (kTok * kGuTokStride);
+        f16x2 s0g, n0g, s1g, n1g, s0u, n0u, s1u, n1u;
+        f16x8 mopg, mopu;
+        auto scales = [&](const uint4 &hd, f16x2 &s0, f16x2 &n0, f16x2 &s1, f16x2 &n1, f16x8 &mop) {
+            int sc0, mn0, sc1, mn1;
+            q4k_scale_min_v(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
+            q4k_scale_min_v(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
+            const _Float16 a0 = _Float16(sc0), a1 = _Float16(sc1), m0 = _Float16(mn0), m1 = _Float16(mn1);
+            s0 = f16x2{a0, a0};
+            s1 = f16x2{a1, a1};
+            n0 = f16x2{_Float16(-1024 * sc0), _Float16(-1024 * sc0)};
+            n1 = f16x2{_Float16(-1024 * sc1), _Float16(-1024 * sc1)};
+            mop = f16x8{m0, m0, m0, m0, m1, m1, m1, m1};
+        };
+        scales(cg.hd, s0g, n0g, s1g, n1g, mopg);
+        scales(cu.hd, s0u, n0u, s1u, n1u, mopu);
+        const uint32_t wgs[8] = {cg.q0.x, cg.q0.y, cg.q0.z, cg.q0.w, cg.q1.x, cg.q1.y, cg.q1.z, cg.q1.w};
+        const uint32_t wus[8] = {cu.q0.x, cu.q0.y, cu.q0.z, cu.q0.w, cu.q1.x, cu.q1.y, cu.q1.z, cu.q1.w};
+        f32x4 c_g = {0.f, 0.f, 0.f, 0.f}, m_g = c_g, c_u = c_g, m_u = c_g;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const f16x8 xh = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4 *>(xb + 32 * u));
+            const f16x8 xl = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4 *>(xb + 32 * u + 4));
+            const f16x8 bg = q4k_operand(wgs[u], s0g, n0g, s1g, n1g);
+            const f16x8 bu = q4k_operand(wus[u], s0u, n0u, s1u, n1u);
+            c_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bg, c_g, 0, 0, 0);
+            c_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bg, c_g, 0, 0, 0);
+            m_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, mopg, m_g, 0, 0, 0);
+            m_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, mopg, m_g, 0, 0, 0);
+            c_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bu, c_u, 0, 0, 0);
+            c_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bu, c_u, 0, 0, 0);
+            m_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, mopu, m_u, 0, 0, 0);
+            m_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, mopu, m_u, 0, 0, 0);
+        }
+        const float dg = h2f(cg.hd.x & 0xffffu), mg = h2f(cg.hd.x >> 16);
+        const float du = h2f(cu.hd.x & 0xffffu), mu = h2f(cu.hd.x >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            accg[i] = fmaf(dg, c_g[i], fmaf(-mg, m_g[i], accg[i]));
+            accu[i] = fmaf(du, c_u[i], fmaf(-mu, m_u[i], accu[i]));
+        }
+        if (b + 1 < nb) {  // into the buffer read two super-blocks ago
+            uint32_t *dst = xdst + ((b + 1) & 1) * (kTok * kGuTokStride);
+            *reinterpret_cast<uint4 *>(dst) = xv0;
+            *reinterpret_cast<uint4 *>(dst + 4 * kGuTokStride) = xv1;
+            *reinterpret_cast<uint4 *>(dst + 8 * kGuTokStride) = xv2;
+            *reinterpret_cast<uint4 *>(dst + 12 * kGuTokStride) = xv3;
+            __syncthreads();
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int tt = 4 * g + i;
+        if (tt >= tn) continue;
+        const float sc = xsc[perm[base + t0 + tt] / k];
+        put(tt, swiglu(accg[i] * sc, accu[i] * sc));
+    }
+}
+
+// down: wave w of workgroup (c, s, z) owns rows 128 c + 32 w .. + 31 of down
+// of expert active[s] (two 16-row tiles) for tokens 16 z .. of its group, and
+// writes y[pair][row] = down_row . h[pair] (src/gguf_run.c:208), combined
+// afterwards in selection order by the combine kernel. The tile's activations
+// (all of fe) are copied to LDS once; each wave passes its rows' ql and qh
+// bytes through its own LDS (coalesced 16-byte loads in, the words its lanes
+// need out), the next super-block's in flight while it computes the current.
+constexpr int kDnRowStride = 52;  // dwords per weight row in LDS: 32 ql + 16 qh + 4 (no bank conflicts)
+
+__global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restrict__ counts,
+                                                        const int32_t *__restrict__ offs,
+                                                        const int32_t *__restrict__ perm,
+                                                        const int32_t *__restrict__ active,
+                                                        const void *const *__restrict__ table,
+                                                        const uint4 *__restrict__ hp, int fe, int d, int E,
+                                                        int64_t row_bytes, float *__restrict__ y) {
+    extern __shared__ __align__(16) uint32_t hs[];  // [kTok][fe + 4]
+    __shared__ __align__(16) uint32_t wq[4][2][16 * kDnRowStride];
+    const int s = blockIdx.y;
+    if (s >= active[E]) return;
+    const int e = active[s], cnt = counts[e], base = offs[e], t0 = blockIdx.z * kTok;
+    if (t0 >= cnt) return;
+    gbyte *D = gmem(table[3 * e + 2]);
+    if (!D) return;  // the combine skips an unregistered expert (src/gguf_run.c:201)
+    const int tn = min(kTok, cnt - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int hstride = fe + 4;
+    // the tile's activations: token i's fe / 4 pieces of 16 bytes
+    const int npc = fe / 4;
+    for (int i = tid; i < tn * npc; i += 256) {
+        const int tt = i / npc, c = i - tt * npc;
+        *reinterpret_cast<uint4 *>(&hs[tt * hstride + 4 * c]) = hp[size_t(perm[base + t0 + tt]) * npc + c];
+    }
+    const int o0 = min((blockIdx.x * 4 + wv) * 32, d - 32);  // d % 32 == 0: a wave past d repeats rows
+    const bool live = (blockIdx.x * 4 + wv) * 32 < d;
+    gbyte *rows[2] = {D + int64_t(o0 + r) * row_bytes, D + int64_t(o0 + 16 + r) * row_bytes};
+    const int nb = fe / 256;
+    struct Wt {
+        uint4 a0, a1, qq, sc;
+        uint32_t dd;
+    };
+    auto load = [&](int b, Wt (&w)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            gbyte *p = rows[t] + 210 * b;
+            w[t].a0 = ld_u128(p + 16 * g);
+            w[t].a1 = ld_u128(p + 64 + 16 * g);
+            w[t].qq = ld_u128(p + 128 + 16 * g);
+            w[t].sc = ld_u128(p + 192);
+            w[t].dd = ld_u16(p + 208);
+        }
+    };
+    Wt nw[2];
+    load(0, nw);
+    __syncthreads();  // the activations are in LDS
+    const uint4 *xr = reinterpret_cast<const uint4 *>(&hs[min(r, tn - 1) * hstride]) + g;
+    constexpr uint32_t kB = 0x43004300u;  // bf16 128 in both halves
+    const s16x4 k160 = __builtin_bit_cast(s16x4, make_uint2(0xC320C320u, 0xC320C320u));  // bf16 -160
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    uint32_t *wl[2] = {&wq[wv][0][r * kDnRowStride], &wq[wv][1][r * kDnRowStride]};
+    for (int b = 0; b < nb; b++) {
+        Wt cw[2] = {nw[0], nw[1]};
+        if (b + 1 < nb) load(b + 1, nw);
+        // ql chunks g and g + 4, qh chunk g of each row into the wave's LDS;
+        // then lane group g reads word g of the chunk each step needs
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            *reinterpret_cast<uint4 *>(wl[t] + 4 * g) = cw[t].a0;
+            *reinterpret_cast<uint4 *>(wl[t] + 16 + 4 * g) = cw[t].a1;
+            *reinterpret_cast<uint4 *>(wl[t] + 32 + 4 * g) = cw[t].qq;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float dd[2] = {h2f(cw[0].dd), h2f(cw[1].dd)};
+        const uint32_t scw[2][4] = {{cw[0].sc.x, cw[0].sc.y, cw[0].sc.z, cw[0].sc.w},
+                                    {cw[1].sc.x, cw[1].sc.y, cw[1].sc.z, cw[1].sc.w}};
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int lh = 0; lh < 2; lh++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int sb = 8 * h + 2 * j + lh, ql_c = 4 * h + 2 * (j & 1) + lh, qh_c = 2 * h + lh;
+                    const uint4 hx = xr[64 * b + 4 * sb];
+                    const s16x4 xh = __builtin_bit_cast(s16x4, make_uint2(hx.x, hx.y));
+                    const s16x4 xl = __builtin_bit_cast(s16x4, make_uint2(hx.z, hx.w));
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const uint32_t lw = wl[t][4 * ql_c + g], hw = wl[t][32 + 4 * qh_c + g];
+                        const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
+                        const s16x4 w = __builtin_bit_cast(
+                            s16x4, make_uint2((q & 0x00ff00ffu) | kB, ((q >> 8) & 0x00ff00ffu) | kB));
+                        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, w, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, w, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, k160, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, k160, c, 0, 0, 0);
+                        const float ds = dd[t] * float(int(int8_t(scw[t][sb >> 2] >> (8 * (sb & 3)))));
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[t][i] = fmaf(ds, c[i], acc[t][i]);
+                    }
+                }
+        // every lane is done with this super-block's words before the next overwrite them
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int tt = 4 * g + i;
+        if (tt >= tn) continue;
+        float *yr = y + size_t(perm[base + t0 + tt]) * d + o0 + r;
+        yr[0] = acc[0][i];
+        yr[16] = acc[1][i];
+    }
+}
+
+}  // namespace
+
+bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe) {
+    // d: whole super-blocks and 32-row waves; fe: whole super-blocks, 16-row
+    // waves and the activations of a 16-token tile in LDS
+    return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && fe % 256 == 0 && fe <= 4096;
+}
+
+int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s) {
+    if (T < 1 || d % 256) return -EINVAL;
+    hipLaunchKernelGGL(mdec_prep_kernel, dim3(T), dim3(256), 0, s, hb, d, static_cast<_Float16 *>(xp), xsc);
+    return vh_check(hipGetLastError());
+}
+
+int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
+                   const void *const *table, const void *xp, const float *xsc, int d, int fe, int k, int E,
+                   int max_slots, int max_count, void *hp, hipStream_t s) {
+    if (max_count < 1 || d % 256 || fe % 16) return -EINVAL;
+    const dim3 g((fe + 63) / 64, max_slots, (max_count + kTok - 1) / kTok);
+    hipLaunchKernelGGL(mdec_gateup_kernel, g, dim3(256), 0, s, counts, offs, perm, active, table,
+                       static_cast<const uint4 *>(xp), xsc, d, fe, k, E, vh_row_bytes(VT_Q4_K, d),
+                       static_cast<uint16_t *>(hp));
+    return vh_check(hipGetLastError());
+}
+
+int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
+                 const void *const *table, const void *hp, int d, int fe, int E, int max_slots, int max_count,
+                 float *ybuf, hipStream_t s) {
+    if (max_count < 1 || d % 32 || fe % 256) return -EINVAL;
+    const dim3 g((d + 127) / 128, max_slots, (max_count + kTok - 1) / kTok);
+    const size_t lds = size_t(kTok) * (fe + 4) * 4;
+    static bool attr = false;  // dynamic LDS above the default limit: raised once per process
+    if (!attr) {
+        if (int rc = vh_check(hipFuncSetAttribute(reinterpret_cast<const void *>(&mdec_down_kernel),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024)))
+            return rc;
+        attr = true;
+    }
+    if (lds > 96 * 1024) return -EINVAL;
+    hipLaunchKernelGGL(mdec_down_kernel, g, dim3(256), lds, s, counts, offs, perm, active, table,
+                       static_cast<const uint4 *>(hp), fe, d, E, vh_row_bytes(VT_Q6_K, fe), ybuf);
+    return vh_check(hipGetLastError());
+}

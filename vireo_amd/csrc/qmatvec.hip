@@ -34,7 +34,7 @@ __global__ void __launch_bounds__(256) qmatvec_kernel(float *__restrict__ y, con
             for (int it = li; it < items; it += L) acc += F::dot(w, ro, it, n, x);
         }
         acc = group_sum<L>(acc);
-        if (li == L - 1 && row < d) y[row] = accumulate ? __fadd_rn(y[row], acc) : acc;
+        if (li == L - 1 && row < d) y[row] = accumulate ? add_rn(y[row], acc) : acc;
     }
 }
 
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y,
                 if (it < items) acc += F::compute(raw[rr][m], it, xr[m], xs[m]);
             }
             acc = group_sum<64>(acc);
-            if (lane == 63 && r0 + rr < d) y[r0 + rr] = accumulate ? __fadd_rn(y[r0 + rr], acc) : acc;
+            if (lane == 63 && r0 + rr < d) y[r0 + rr] = accumulate ? add_rn(y[r0 + rr], acc) : acc;
         }
     }
 }
@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict_
     if constexpr (T == VT_Q8_0) {
         const uint8_t *b = r + 34 * it;
         const float d = h2f(ld_u16(b));
-        for (int i = 0; i < 32; i++) o[32 * it + i] = __fmul_rn(float(int8_t(ld_u8(b + 2 + i))), d);
+        for (int i = 0; i < 32; i++) o[32 * it + i] = mul_rn(float(int8_t(ld_u8(b + 2 + i))), d);
     } else if constexpr (T == VT_Q4_K) {
         // one 32-element sub-block j per thread (items = n/32): y = (d*sc)*q - dmin*m
         const int sbi = it >> 3, j = it & 7;
@@ -224,23 +224,23 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict_
         const uint32_t s0 = ld_u32(sb + 4), s1 = ld_u32(sb + 8), s2 = ld_u32(sb + 12);
         int sc, m;
         q4k_scale_min(j, s0, s1, s2, sc, m);
-        const float d1 = __fmul_rn(d, float(sc)), m1 = __fmul_rn(dmin, float(m));
+        const float d1 = mul_rn(d, float(sc)), m1 = mul_rn(dmin, float(m));
         const uint8_t *q = sb + 16 + 32 * (j >> 1);
         const int sh = (j & 1) ? 4 : 0;
-        for (int l = 0; l < 32; l++) o[256 * sbi + 32 * j + l] = __fsub_rn(__fmul_rn(d1, float((ld_u8(q + l) >> sh) & 15u)), m1);
+        for (int l = 0; l < 32; l++) o[256 * sbi + 32 * j + l] = sub_rn(mul_rn(d1, float((ld_u8(q + l) >> sh) & 15u)), m1);
     } else if constexpr (T == VT_Q6_K) {
         // 16 elements sharing one scale per thread (items = n/16)
         const int sbi = it >> 4, s = it & 15;
         const uint8_t *sb = r + 210 * sbi;
         const float d = h2f(ld_u16(sb + 208));
-        const float ds = __fmul_rn(d, float(int8_t(ld_u8(sb + 192 + s))));
+        const float ds = mul_rn(d, float(int8_t(ld_u8(sb + 192 + s))));
         const int hh = s >> 3, g = (s >> 1) & 3, half = s & 1;
         for (int i = 0; i < 16; i++) {
             const int l = 16 * half + i;
             const uint32_t qlb = ld_u8(sb + 64 * hh + l + 32 * (g & 1));
             const uint32_t lo4 = g >= 2 ? (qlb >> 4) : (qlb & 15u);
             const uint32_t hi2 = (ld_u8(sb + 128 + 32 * hh + l) >> (2 * g)) & 3u;
-            o[256 * sbi + 128 * hh + 32 * g + l] = __fmul_rn(ds, float(int(lo4 | (hi2 << 4)) - 32));
+            o[256 * sbi + 128 * hh + 32 * g + l] = mul_rn(ds, float(int(lo4 | (hi2 << 4)) - 32));
         }
     } else if constexpr (T == VT_Q5_0) {
         const uint8_t *b = r + 22 * it;
@@ -248,8 +248,8 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict_
         const uint32_t qh = ld_u16(b + 2) | (ld_u16(b + 4) << 16);
         for (int j = 0; j < 16; j++) {
             const uint32_t qs = ld_u8(b + 6 + j);
-            o[32 * it + j] = __fmul_rn(float(int((qs & 15u) | (((qh >> j) & 1u) << 4)) - 16), d);
-            o[32 * it + j + 16] = __fmul_rn(float(int((qs >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16), d);
+            o[32 * it + j] = mul_rn(float(int((qs & 15u) | (((qh >> j) & 1u) << 4)) - 16), d);
+            o[32 * it + j + 16] = mul_rn(float(int((qs >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16), d);
         }
     } else if constexpr (T == VT_F16) {
         for (int i = 32 * it; i < n && i < 32 * it + 32; i++) o[i] = h2f(ld_u16(r + 2 * i));

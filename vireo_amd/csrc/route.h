@@ -36,10 +36,10 @@ VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&
 #pragma unroll
     for (int i = 0; i < C / 4; i++) {
         const float4 a = r4[i];
-        p[4 * i + 0] = __fmul_rn(a.x, xv[4 * i + 0]);
-        p[4 * i + 1] = __fmul_rn(a.y, xv[4 * i + 1]);
-        p[4 * i + 2] = __fmul_rn(a.z, xv[4 * i + 2]);
-        p[4 * i + 3] = __fmul_rn(a.w, xv[4 * i + 3]);
+        p[4 * i + 0] = mul_rn(a.x, xv[4 * i + 0]);
+        p[4 * i + 1] = mul_rn(a.y, xv[4 * i + 1]);
+        p[4 * i + 2] = mul_rn(a.z, xv[4 * i + 2]);
+        p[4 * i + 3] = mul_rn(a.w, xv[4 * i + 3]);
     }
     double tot = 0.0, absum = 0.0, pabs = 0.0;
 #pragma unroll
@@ -93,17 +93,17 @@ VH_DEV RoutePart route_part_on_own_norm(RoutePart p, double abs_products, int n,
 // red: one float of LDS. All threads of the workgroup call it.
 VH_DEV void reference_rmsnorm_block(float *dst, const float *__restrict__ x, const float *__restrict__ nw, float eps,
                                     int d, float *red) {
-    for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = __fmul_rn(x[i], x[i]);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = mul_rn(x[i], x[i]);
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
-        for (int i = 0; i < d; i++) ss = __fadd_rn(ss, dst[i]);
-        *red = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(d)), eps)));
+        for (int i = 0; i < d; i++) ss = add_rn(ss, dst[i]);
+        *red = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(d)), eps)));
     }
     __syncthreads();
     const float r = *red;
     for (int i = threadIdx.x; i < d; i += blockDim.x)
-        dst[i] = nw ? __fmul_rn(__fmul_rn(x[i], r), nw[i]) : __fmul_rn(x[i], r);
+        dst[i] = nw ? mul_rn(mul_rn(x[i], r), nw[i]) : mul_rn(x[i], r);
     __syncthreads();
 }
 
@@ -118,10 +118,10 @@ VH_DEV RoutePart route_row_part(const float *__restrict__ r, const float *__rest
 #pragma unroll
         for (int i = 0; i < C / 4; i++) {
             const float4 a = r4[i], b = x4[i];
-            p[4 * i + 0] = __fmul_rn(a.x, b.x);
-            p[4 * i + 1] = __fmul_rn(a.y, b.y);
-            p[4 * i + 2] = __fmul_rn(a.z, b.z);
-            p[4 * i + 3] = __fmul_rn(a.w, b.w);
+            p[4 * i + 0] = mul_rn(a.x, b.x);
+            p[4 * i + 1] = mul_rn(a.y, b.y);
+            p[4 * i + 2] = mul_rn(a.z, b.z);
+            p[4 * i + 3] = mul_rn(a.w, b.w);
         }
 #pragma unroll
         for (int i = 0; i < C; i++) tot += double(p[i]);
@@ -133,10 +133,10 @@ VH_DEV RoutePart route_row_part(const float *__restrict__ r, const float *__rest
         }
     } else {
         const int cpl = (d + 63) / 64, i0 = lane * cpl, i1 = min(d, i0 + cpl);
-        for (int i = i0; i < i1; i++) tot += double(__fmul_rn(r[i], x[i]));
+        for (int i = i0; i < i1; i++) tot += double(mul_rn(r[i], x[i]));
         run = wave_incl_scan_d(tot) - tot;
         for (int i = i0; i < i1; i++) {
-            run += double(__fmul_rn(r[i], x[i]));
+            run += double(mul_rn(r[i], x[i]));
             absum += fabs(run);
         }
     }
@@ -164,17 +164,17 @@ VH_DEV float exact_logit(const float *__restrict__ r, const float *__restrict__ 
             for (int i = 0; i < 16; i++) { rn[i] = r4[16 * nxt + i]; xn[i] = x4[16 * nxt + i]; }
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                a = __fadd_rn(a, __fmul_rn(rc[i].x, xc[i].x));
-                a = __fadd_rn(a, __fmul_rn(rc[i].y, xc[i].y));
-                a = __fadd_rn(a, __fmul_rn(rc[i].z, xc[i].z));
-                a = __fadd_rn(a, __fmul_rn(rc[i].w, xc[i].w));
+                a = add_rn(a, mul_rn(rc[i].x, xc[i].x));
+                a = add_rn(a, mul_rn(rc[i].y, xc[i].y));
+                a = add_rn(a, mul_rn(rc[i].z, xc[i].z));
+                a = add_rn(a, mul_rn(rc[i].w, xc[i].w));
             }
 #pragma unroll
             for (int i = 0; i < 16; i++) { rc[i] = rn[i]; xc[i] = xn[i]; }
         }
         return a;
     }
-    for (int i = 0; i < d; i++) a = __fadd_rn(a, __fmul_rn(r[i], x[i]));
+    for (int i = 0; i < d; i++) a = add_rn(a, mul_rn(r[i], x[i]));
     return a;
 }
 
@@ -186,32 +186,48 @@ VH_DEV uint32_t ordered_u32(float v) {
 
 // Workspace of route_topk_block (LDS).
 struct TopKSmem {
-    uint32_t key[kMaxExperts];       // 32-bit rank keys
+    uint32_t key[kMaxExperts];       // 32-bit rank keys; then the exact path's exponentials
     uint64_t key64[kMaxExperts];     // full-precision keys (re-ranking)
     int sel[64];                     // chosen experts in order
     float sel_w[64];                 // their weights
     double sel_lo[65], sel_hi[64];   // their intervals; sel_lo[64]: best remaining
     float red[2][8];                 // per-wave partials (up to 8 waves)
     float m;                         // max logit
+    float s, p_next;                 // exact path: the softmax's sum, the best probability left out
     uint32_t flag;
     int uncertain;
 };
 
+// Logit span of a certified top k: the k-th chosen expert's logit lies within
+// kRouteSpan of the largest. The reference ranks probabilities
+// p = expf(l - m) / s (src/gguf_run.c:180-191) and lets the lowest id win a
+// tie; distinct logits can give equal probabilities only where l - m is
+// rounded coarser than kRouteMargin (|l - m| >= 32, fp32 spacing 3.8e-6) or
+// expf underflows, so within the span a certified logit order is the
+// reference's probability order.
+constexpr double kRouteSpan = 30.0;
+
 // Top-k of one token by a workgroup of 256 to 512 threads (all threads call
-// it; E <= 256, k <= 64). Thread e owns expert e. Its rank is the number of experts with a
-// larger key, so the k chosen experts and their order come out of one parallel
-// pass. The ranking is certified with the fp64 intervals; when any gap that
-// decides the set or its order is not wider than both bounds plus
-// kRouteMargin, every expert that could still be among the k is recomputed
-// exactly (in-order fp32, as the reference) and the experts are ranked again
-// on full-precision keys. With exact_parts the parts already hold exact fp32
-// logits (beta = 0) and only full-precision ranking and near-tie reporting
-// are needed. On return (after a barrier) sm.sel / sm.sel_w / sm.flag hold the
-// result; probs (optional, [E]) receives the softmax.
+// it; E <= 256, k <= 64). Thread e owns expert e. Its rank is the number of
+// experts with a larger key, so the k chosen experts and their order come out
+// of one parallel pass. The ranking is certified with the fp64 intervals:
+// every gap that decides the set or its order wider than both bounds plus
+// kRouteMargin, and the chosen within kRouteSpan of the top. Otherwise the
+// reference's softmax is formed exactly - every logit in-order fp32 (or
+// exact_parts: the parts hold them, beta = 0), m, expf(l - m), their in-order
+// fp32 sum s and p = e / s (src/gguf_run.c:180-182) - and the experts are
+// ranked on p with the lowest id winning a tie (:189-191); the weights are
+// those p. The device's expf can differ from the reference's C library by an
+// ulp: it decides only exact ties of the exponentials, and a chosen
+// probability equal to the next one, or exact logits closer than kNearTie, is
+// reported (VIREO_ROUTE_NEAR_TIE). On return (after a barrier) sm.sel /
+// sm.sel_w / sm.flag hold the result; probs (optional, [E]) receives the
+// softmax.
 VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, const float *__restrict__ R,
                              const float *__restrict__ x, const float *__restrict__ bias, int d, int E, int k,
                              int renorm, bool exact_parts, float *__restrict__ probs) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nwaves = int(blockDim.x) >> 6;
     const bool mine = tid < E;
     double lo = -INFINITY, hi = -INFINITY;
     float lg = -INFINITY;
@@ -223,7 +239,7 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     }
     // 8 mantissa bits give way to the id (lowest id wins a tie of the truncated
     // keys): values that close can never be certified, so a wrong truncated
-    // order always reaches the full-precision re-ranking below.
+    // order always reaches the exact ranking below.
     const uint32_t key = mine ? ((ordered_u32(lg) & 0xffffff00u) | uint32_t(255 - tid)) : 0u;
     if (tid < kMaxExperts) sm.key[tid] = key;
     if (tid == 0) { sm.uncertain = 0; sm.flag = 0; }
@@ -242,7 +258,6 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
     }
     // the largest upper bound outside the chosen k, rounded up to fp32 (an
     // upper bound is all the certification needs)
-    const int nwaves = int(blockDim.x) >> 6;
     const float rest = (mine && rank >= k) ? __double2float_ru(hi) : -INFINITY;
     const float rw = wave_max_f(rest);
     if (lane == 0) sm.red[0][wv] = rw;
@@ -251,57 +266,73 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
         float rh = sm.red[0][0];
         for (int i = 1; i < nwaves; i++) rh = fmaxf(rh, sm.red[0][i]);
         const double next_hi = tid + 1 < k ? sm.sel_hi[tid + 1] : (k < E ? double(rh) : -INFINITY);
-        if (!(sm.sel_lo[tid] - next_hi > (exact_parts ? 0.0 : kRouteMargin))) atomicOr(&sm.uncertain, 1);
-        if (exact_parts && sm.sel_lo[tid] - next_hi < double(kNearTie)) atomicOr(&sm.flag, VIREO_ROUTE_NEAR_TIE);
+        if (!(sm.sel_lo[tid] - next_hi > kRouteMargin)) atomicOr(&sm.uncertain, 1);
+        if (!(sm.sel_lo[tid] > sm.sel_hi[0] - kRouteSpan)) atomicOr(&sm.uncertain, 1);
     }
     __syncthreads();
     if (sm.uncertain) {
-        // exact logits for every possible member of the top k
-        double thr = INFINITY;
-        for (int t = 0; t < k; t++) thr = fmin(thr, sm.sel_lo[t]);
-        thr -= kRouteMargin;
-        const bool cand = mine && hi >= thr;
-        if (cand && !exact_parts) {
+        // the reference's softmax, exactly: every logit, their maximum, the
+        // exponentials, their in-order sum (one thread), the probabilities
+        if (mine && !exact_parts) {
             float a = exact_logit(R + size_t(tid) * d, x, d);
-            if (bias) a = __fadd_rn(a, bias[tid]);
+            if (bias) a = add_rn(a, bias[tid]);
             lg = a;
         }
-        if (tid < kMaxExperts) sm.key64[tid] = cand ? ((uint64_t(ordered_u32(lg)) << 8) | uint64_t(255 - tid)) : 0ull;
+        const float wm = wave_max_f(mine ? lg : -INFINITY);
+        __syncthreads();  // every thread is done with the first ranking's LDS
+        if (lane == 0) sm.red[0][wv] = wm;
+        __syncthreads();
+        float m = sm.red[0][0];
+        for (int i = 1; i < nwaves; i++) m = fmaxf(m, sm.red[0][i]);
+        const float ev = mine ? expf(sub_rn(lg, m)) : 0.0f;
+        if (tid < kMaxExperts) sm.key[tid] = __float_as_uint(ev);
         if (tid == 0) {
-            // the near-tie verdict is taken again on the full-precision ranking
             sm.flag = exact_parts ? 0u : VIREO_ROUTE_EXACT_FALLBACK;
+            sm.p_next = -1.0f;
             sm.sel_lo[64] = -INFINITY;
         }
         __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;
+            for (int i = 0; i < E; i++) s = add_rn(s, __uint_as_float(sm.key[i]));
+            sm.s = s;
+        }
+        __syncthreads();
+        const float pr = __fdiv_rn(ev, sm.s);
+        if (tid < kMaxExperts) sm.key64[tid] = mine ? ((uint64_t(ordered_u32(pr)) << 8) | uint64_t(255 - tid)) : 0ull;
+        __syncthreads();
         rank = 1 << 30;
-        if (cand) {
+        if (mine) {
             const uint64_t k64 = sm.key64[tid];
             int r = 0;
             for (int j = 0; j < E; j++) r += int(sm.key64[j] > k64);
             rank = r;
-            if (rank < k) { sm.sel[rank] = tid; sm.sel_lo[rank] = double(lg); }
-            if (rank == k) sm.sel_lo[64] = double(lg);  // best contender left out
-            if (rank == 0) sm.m = lg;
+            if (probs) probs[tid] = pr;
+            if (rank < k) { sm.sel[rank] = tid; sm.sel_w[rank] = pr; sm.sel_lo[rank] = double(lg); }
+            if (rank == k) { sm.sel_lo[64] = double(lg); sm.p_next = pr; }  // best contender left out
         }
         __syncthreads();
         if (tid < k) {
             const double nxt = tid + 1 < k ? sm.sel_lo[tid + 1] : sm.sel_lo[64];
-            if (sm.sel_lo[tid] - nxt < double(kNearTie)) atomicOr(&sm.flag, VIREO_ROUTE_NEAR_TIE);
+            const float pn = tid + 1 < k ? sm.sel_w[tid + 1] : sm.p_next;
+            if (fabs(sm.sel_lo[tid] - nxt) < double(kNearTie) || sm.sel_w[tid] == pn)
+                atomicOr(&sm.flag, VIREO_ROUTE_NEAR_TIE);
+        }
+        __syncthreads();
+    } else {
+        // softmax over all experts (src/gguf_run.c:181-182) on the certified logits
+        const float ex = mine ? expf(lg - sm.m) : 0.0f;
+        const float part_sum = wave_sum_f(ex);
+        if (lane == 0) sm.red[1][wv] = part_sum;
+        __syncthreads();
+        float s = sm.red[1][0];
+        for (int i = 1; i < nwaves; i++) s += sm.red[1][i];
+        if (mine) {
+            if (probs) probs[tid] = ex / s;
+            if (rank < k) sm.sel_w[rank] = ex / s;
         }
         __syncthreads();
     }
-    // softmax over all experts (src/gguf_run.c:181-182)
-    const float ex = mine ? expf(lg - sm.m) : 0.0f;
-    const float part_sum = wave_sum_f(ex);
-    if (lane == 0) sm.red[1][wv] = part_sum;
-    __syncthreads();
-    float s = sm.red[1][0];
-    for (int i = 1; i < nwaves; i++) s += sm.red[1][i];
-    if (mine) {
-        if (probs) probs[tid] = ex / s;
-        if (rank < k) sm.sel_w[rank] = ex / s;
-    }
-    __syncthreads();
     if (tid == 0 && renorm) {
         float wsum = 0.0f;
         for (int t = 0; t < k; t++) wsum += sm.sel_w[t];  // in selection order
@@ -361,6 +392,7 @@ VH_DEV bool route_select_wave(const RoutePart (&p)[Q], int E, int k, int want, i
         const double lo = cert[lane].x;
         if (lane + 1 < k) good = lo - cert[lane + 1].y > kRouteMargin;
         else if (k < E) good = lo - double(rest) > kRouteMargin;
+        good = good && lo > cert[0].y - kRouteSpan;  // no probability ties (route_topk_block)
     }
     return __builtin_amdgcn_read_exec() == __ballot(good);
 }
@@ -474,6 +506,7 @@ VH_DEV bool route_certify_wave(const RoutePart (&p)[Q], int E, int k, const int 
         const double lo = cert[lane].x;
         if (lane + 1 < k) good = lo - cert[lane + 1].y > kRouteMargin;
         else if (k < E) good = lo - double(rest) > kRouteMargin;
+        good = good && lo > cert[0].y - kRouteSpan;  // no probability ties (route_topk_block)
     }
     return __builtin_amdgcn_read_exec() == __ballot(good);
 }
