@@ -25,13 +25,13 @@ namespace {
 // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the
 // fused experts kernel, 4 grouped plan without the matrix-core GEMMs
 int g_path = 0;
-// From this many tokens on, every logit of a routed call is the reference's
-// exact sequential fp32 sum (route_exact_small_kernel for a decode batch,
-// route_exact_kernel for more): one chain's latency, cheaper than certifying
-// a batch whose uncertain tokens each wait for exact contenders, and the same
-// logits (so the same weights) for a token whatever batch it is in. The
-// one-token decode plans route inside their own kernels.
-constexpr int kExactRouteTokens = 1;
+// From this many tokens on, every logit is the reference's exact sequential
+// fp32 sum (route_exact_kernel): its latency, one chain of 2 d dependent
+// operations, is then hidden by the chains of many tokens. Fewer tokens take
+// the certified fp64 parts, whose exact recomputation (route_topk_block) is
+// needed for the few tokens whose order the bounds leave open; a token's
+// result does not depend on the other tokens of its call either way.
+constexpr int kExactRouteTokens = 64;
 
 bool type_ok(uint32_t t, int n) {
     switch (t) {  // the expert formats of the MoE models: Q8_0, Q4_K (gate/up), Q6_K (down)

@@ -37,10 +37,11 @@
 // free as long as A and B agree: it is fixed by how a weight word is unpacked,
 // and the inputs are laid out to match.
 //
-// Grids: (row chunk, active expert slot, 16-token tile), 256 threads; gate/up
-// waves own 16 rows of gate and the same 16 of up, down waves 32 rows. Q6_K
-// rows (210 bytes per super-block) start at any even address; their 16-byte
-// loads rely on global memory accepting any alignment.
+// Grids: (row chunk, active expert slot, 16-token tile); gate/up: 256
+// threads, waves of 16 rows of gate and the same 16 of up; down: 512
+// threads, waves of 16 rows. Q6_K rows (210 bytes per super-block) start at
+// any even address; their 16-byte loads rely on global memory accepting any
+// alignment.
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
@@ -286,24 +287,27 @@ __global__ void __launch_bounds__(256) mdec_gateup_kernel(const int32_t *__restr
     }
 }
 
-// down: wave w of workgroup (c, s, z) owns rows 128 c + 32 w .. + 31 of down
-// of expert active[s] (two 16-row tiles) for tokens 16 z .. of its group, and
+// down: wave w of workgroup (c, s, z) owns rows 128 c + 16 w .. + 15 of down
+// of expert active[s] (one 16-row tile) for tokens 16 z .. of its group, and
 // writes y[pair][row] = down_row . h[pair] (src/gguf_run.c:208), combined
-// afterwards in selection order by the combine kernel. The tile's activations
-// (all of fe) are copied to LDS once; each wave passes its rows' ql and qh
-// bytes through its own LDS (coalesced 16-byte loads in, the words its lanes
-// need out), the next super-block's in flight while it computes the current.
+// afterwards in selection order by the combine kernel. Every super-block of
+// the lane's row is requested first; then the tile's activations (all of fe)
+// are copied to LDS for the workgroup's eight waves; each wave passes its
+// rows' ql and qh bytes through its own LDS (coalesced 16-byte loads in, the
+// words its lanes need out).
 constexpr int kDnRowStride = 52;  // dwords per weight row in LDS: 32 ql + 16 qh + 4 (no bank conflicts)
+constexpr int kDnMaxBlocks = 4;   // fe <= 1024
+constexpr int kDnWaves = 8;
 
-__global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restrict__ counts,
-                                                        const int32_t *__restrict__ offs,
-                                                        const int32_t *__restrict__ perm,
-                                                        const int32_t *__restrict__ active,
-                                                        const void *const *__restrict__ table,
-                                                        const uint4 *__restrict__ hp, int fe, int d, int E,
-                                                        int64_t row_bytes, float *__restrict__ y) {
+__global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t *__restrict__ counts,
+                                                                  const int32_t *__restrict__ offs,
+                                                                  const int32_t *__restrict__ perm,
+                                                                  const int32_t *__restrict__ active,
+                                                                  const void *const *__restrict__ table,
+                                                                  const uint4 *__restrict__ hp, int fe, int d, int E,
+                                                                  int64_t row_bytes, float *__restrict__ y) {
     extern __shared__ __align__(16) uint32_t hs[];  // [kTok][fe + 4]
-    __shared__ __align__(16) uint32_t wq[4][2][16 * kDnRowStride];
+    __shared__ __align__(16) uint32_t wq[kDnWaves][16 * kDnRowStride];
     const int s = blockIdx.y;
     if (s >= active[E]) return;
     const int e = active[s], cnt = counts[e], base = offs[e], t0 = blockIdx.z * kTok;
@@ -312,57 +316,47 @@ __global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restric
     if (!D) return;  // the combine skips an unregistered expert (src/gguf_run.c:201)
     const int tn = min(kTok, cnt - t0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int hstride = fe + 4;
+    const int o0 = min((blockIdx.x * kDnWaves + wv) * 16, d - 16);  // d % 16 == 0: a wave past d repeats rows
+    const bool live = (blockIdx.x * kDnWaves + wv) * 16 < d;
+    gbyte *row = D + int64_t(o0 + r) * row_bytes;
+    const int nb = fe / 256;
+    uint4 a0[kDnMaxBlocks], a1[kDnMaxBlocks], qq[kDnMaxBlocks], scb[kDnMaxBlocks];
+    uint32_t ddb[kDnMaxBlocks];
+#pragma unroll
+    for (int b = 0; b < kDnMaxBlocks; b++) {
+        if (b >= nb) break;
+        gbyte *p = row + 210 * b;
+        a0[b] = ld_u128(p + 16 * g);
+        a1[b] = ld_u128(p + 64 + 16 * g);
+        qq[b] = ld_u128(p + 128 + 16 * g);
+        scb[b] = ld_u128(p + 192);
+        ddb[b] = ld_u16(p + 208);
+    }
     // the tile's activations: token i's fe / 4 pieces of 16 bytes
-    const int npc = fe / 4;
-    for (int i = tid; i < tn * npc; i += 256) {
+    const int hstride = fe + 4, npc = fe / 4;
+    for (int i = tid; i < tn * npc; i += 64 * kDnWaves) {
         const int tt = i / npc, c = i - tt * npc;
         *reinterpret_cast<uint4 *>(&hs[tt * hstride + 4 * c]) = hp[size_t(perm[base + t0 + tt]) * npc + c];
     }
-    const int o0 = min((blockIdx.x * 4 + wv) * 32, d - 32);  // d % 32 == 0: a wave past d repeats rows
-    const bool live = (blockIdx.x * 4 + wv) * 32 < d;
-    gbyte *rows[2] = {D + int64_t(o0 + r) * row_bytes, D + int64_t(o0 + 16 + r) * row_bytes};
-    const int nb = fe / 256;
-    struct Wt {
-        uint4 a0, a1, qq, sc;
-        uint32_t dd;
-    };
-    auto load = [&](int b, Wt (&w)[2]) {
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            gbyte *p = rows[t] + 210 * b;
-            w[t].a0 = ld_u128(p + 16 * g);
-            w[t].a1 = ld_u128(p + 64 + 16 * g);
-            w[t].qq = ld_u128(p + 128 + 16 * g);
-            w[t].sc = ld_u128(p + 192);
-            w[t].dd = ld_u16(p + 208);
-        }
-    };
-    Wt nw[2];
-    load(0, nw);
-    __syncthreads();  // the activations are in LDS
+    __syncthreads();  // the activations are in LDS (and the weights have arrived)
     const uint4 *xr = reinterpret_cast<const uint4 *>(&hs[min(r, tn - 1) * hstride]) + g;
     constexpr uint32_t kB = 0x43004300u;  // bf16 128 in both halves
     const s16x4 k160 = __builtin_bit_cast(s16x4, make_uint2(0xC320C320u, 0xC320C320u));  // bf16 -160
-    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    uint32_t *wl[2] = {&wq[wv][0][r * kDnRowStride], &wq[wv][1][r * kDnRowStride]};
-    for (int b = 0; b < nb; b++) {
-        Wt cw[2] = {nw[0], nw[1]};
-        if (b + 1 < nb) load(b + 1, nw);
-        // ql chunks g and g + 4, qh chunk g of each row into the wave's LDS;
-        // then lane group g reads word g of the chunk each step needs
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    uint32_t *wl = &wq[wv][r * kDnRowStride];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            *reinterpret_cast<uint4 *>(wl[t] + 4 * g) = cw[t].a0;
-            *reinterpret_cast<uint4 *>(wl[t] + 16 + 4 * g) = cw[t].a1;
-            *reinterpret_cast<uint4 *>(wl[t] + 32 + 4 * g) = cw[t].qq;
-        }
+    for (int b = 0; b < kDnMaxBlocks; b++) {
+        if (b >= nb) break;
+        // ql chunks g and g + 4, qh chunk g of the row into the wave's LDS;
+        // lane group g then reads word g of the chunk each step needs
+        *reinterpret_cast<uint4 *>(wl + 4 * g) = a0[b];
+        *reinterpret_cast<uint4 *>(wl + 16 + 4 * g) = a1[b];
+        *reinterpret_cast<uint4 *>(wl + 32 + 4 * g) = qq[b];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const float dd[2] = {h2f(cw[0].dd), h2f(cw[1].dd)};
-        const uint32_t scw[2][4] = {{cw[0].sc.x, cw[0].sc.y, cw[0].sc.z, cw[0].sc.w},
-                                    {cw[1].sc.x, cw[1].sc.y, cw[1].sc.z, cw[1].sc.w}};
+        const float dd = h2f(ddb[b]);
+        const uint32_t scw[4] = {scb[b].x, scb[b].y, scb[b].z, scb[b].w};
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -373,21 +367,18 @@ __global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restric
                     const uint4 hx = xr[64 * b + 4 * sb];
                     const s16x4 xh = __builtin_bit_cast(s16x4, make_uint2(hx.x, hx.y));
                     const s16x4 xl = __builtin_bit_cast(s16x4, make_uint2(hx.z, hx.w));
+                    const uint32_t lw = wl[4 * ql_c + g], hw = wl[32 + 4 * qh_c + g];
+                    const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
+                    const s16x4 w =
+                        __builtin_bit_cast(s16x4, make_uint2((q & 0x00ff00ffu) | kB, ((q >> 8) & 0x00ff00ffu) | kB));
+                    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, w, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, w, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, k160, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, k160, c, 0, 0, 0);
+                    const float ds = dd * float(int(int8_t(scw[sb >> 2] >> (8 * (sb & 3)))));
 #pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const uint32_t lw = wl[t][4 * ql_c + g], hw = wl[t][32 + 4 * qh_c + g];
-                        const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
-                        const s16x4 w = __builtin_bit_cast(
-                            s16x4, make_uint2((q & 0x00ff00ffu) | kB, ((q >> 8) & 0x00ff00ffu) | kB));
-                        f32x4 c = {0.f, 0.f, 0.f, 0.f};
-                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, w, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, w, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, k160, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, k160, c, 0, 0, 0);
-                        const float ds = dd[t] * float(int(int8_t(scw[t][sb >> 2] >> (8 * (sb & 3)))));
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[t][i] = fmaf(ds, c[i], acc[t][i]);
-                    }
+                    for (int i = 0; i < 4; i++) acc[i] = fmaf(ds, c[i], acc[i]);
                 }
         // every lane is done with this super-block's words before the next overwrite them
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -398,10 +389,7 @@ __global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restric
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int tt = 4 * g + i;
-        if (tt >= tn) continue;
-        float *yr = y + size_t(perm[base + t0 + tt]) * d + o0 + r;
-        yr[0] = acc[0][i];
-        yr[16] = acc[1][i];
+        if (tt < tn) y[size_t(perm[base + t0 + tt]) * d + o0 + r] = acc[i];
     }
 }
 
@@ -410,7 +398,7 @@ __global__ void __launch_bounds__(256) mdec_down_kernel(const int32_t *__restric
 bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe) {
     // d: whole super-blocks and 32-row waves; fe: whole super-blocks, 16-row
     // waves and the activations of a 16-token tile in LDS
-    return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && fe % 256 == 0 && fe <= 4096;
+    return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && fe % 256 == 0 && fe <= 256 * kDnMaxBlocks;
 }
 
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s) {
@@ -433,8 +421,8 @@ int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *pe
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                  const void *const *table, const void *hp, int d, int fe, int E, int max_slots, int max_count,
                  float *ybuf, hipStream_t s) {
-    if (max_count < 1 || d % 32 || fe % 256) return -EINVAL;
-    const dim3 g((d + 127) / 128, max_slots, (max_count + kTok - 1) / kTok);
+    if (max_count < 1 || d % 16 || fe % 256 || fe > 256 * kDnMaxBlocks) return -EINVAL;
+    const dim3 g((d + 16 * kDnWaves - 1) / (16 * kDnWaves), max_slots, (max_count + kTok - 1) / kTok);
     const size_t lds = size_t(kTok) * (fe + 4) * 4;
     static bool attr = false;  // dynamic LDS above the default limit: raised once per process
     if (!attr) {
@@ -444,7 +432,7 @@ int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm
         attr = true;
     }
     if (lds > 96 * 1024) return -EINVAL;
-    hipLaunchKernelGGL(mdec_down_kernel, g, dim3(256), lds, s, counts, offs, perm, active, table,
+    hipLaunchKernelGGL(mdec_down_kernel, g, dim3(64 * kDnWaves), lds, s, counts, offs, perm, active, table,
                        static_cast<const uint4 *>(hp), fe, d, E, vh_row_bytes(VT_Q6_K, fe), ybuf);
     return vh_check(hipGetLastError());
 }

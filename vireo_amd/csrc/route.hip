@@ -12,9 +12,6 @@
 //                       chains in flight per workgroup, so with many tokens the
 //                       dependency is hidden and the result is exact: used for
 //                       prefill.
-//   route_exact_small_kernel  the same exact logits for a decode batch: one
-//                       chain per lane (lane = expert), so the latency is one
-//                       chain whatever the token count.
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "route.h"
@@ -80,7 +77,6 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
 }
 
 constexpr int kExTok = 64, kExExp = 16, kExChunk = 64;
-constexpr int kExactSmallTokens = 64;  // below this many tokens: route_exact_small_kernel
 
 // grid (ceil(T/64), ceil(E/16)), 256 threads: lane = token t0 + lane, wave g
 // = experts e0 + 4g .. +3 (four independent in-order chains per lane). Each
@@ -168,98 +164,6 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     }
 }
 
-// The exact logits of a few tokens (a decode batch): one in-order fp32 chain
-// per lane, so a call's latency is one chain (2 d dependent operations)
-// however few tokens it has. Workgroup (8 tokens, 32 experts), 256 threads:
-// lane tid owns token t0 + tid / 32 and expert e0 + tid % 32. The columns go in
-// chunks of 128 through double-buffered LDS (router rows padded to 132 words:
-// 16-byte accesses without bank conflicts); each thread's share of a chunk
-// (four pieces of router rows, one of the inputs) is loaded two chunks ahead,
-// so the loads have two chunks' sums to arrive. d % 256 == 0.
-constexpr int kSmTok = 8, kSmExp = 32, kSmCol = 128, kSmRS = kSmCol + 4;
-
-__global__ void __launch_bounds__(256) route_exact_small_kernel(const float *__restrict__ R,
-                                                                const float *__restrict__ hb,
-                                                                const float *__restrict__ bias, int d, int E, int T,
-                                                                RoutePart *__restrict__ parts) {
-    __shared__ __align__(16) float rs[2][kSmExp * kSmRS];
-    __shared__ __align__(16) float xs[2][kSmTok * kSmCol];
-    const int tid = threadIdx.x;
-    const int t0 = blockIdx.x * kSmTok, e0 = blockIdx.y * kSmExp;
-    const int t = t0 + (tid >> 5), e = e0 + (tid & 31);
-    // staging: router piece i of thread tid is column 4 (tid % 32) of row
-    // tid / 32 + 8 i (i < 4); the input piece is column 4 (tid % 32) of token tid / 32
-    uint32_t rsrc[4];  // offsets into R (under 2^32 floats for a router of E <= 256 rows)
-#pragma unroll
-    for (int i = 0; i < 4; i++) rsrc[i] = uint32_t(min(e0 + 8 * i + (tid >> 5), E - 1)) * uint32_t(d) + 4 * (tid & 31);
-    float *rdst = &rs[0][(tid >> 5) * kSmRS + 4 * (tid & 31)];  // piece i: 8 i rows further
-    const float *xsrc = hb + size_t(min(t, T - 1)) * d + 4 * (tid & 31);
-    float *xdst = &xs[0][(tid >> 5) * kSmCol + 4 * (tid & 31)];
-    const float *rrow = &rs[0][(tid & 31) * kSmRS];
-    const float *xrow = &xs[0][(tid >> 5) * kSmCol];
-    float a = 0.0f;
-    const int nc = d / kSmCol;  // even (d % 256 == 0)
-    // register sets A and B hold chunks c + 2 and c + 1 while chunk c is summed
-    float4 ra0, ra1, ra2, ra3, xa, rb0, rb1, rb2, rb3, xb;
-#define VH_SM_LOAD(c0, r0, r1, r2, r3, xx)                               \
-    do {                                                                 \
-        r0 = *reinterpret_cast<const float4 *>(R + rsrc[0] + (c0));      \
-        r1 = *reinterpret_cast<const float4 *>(R + rsrc[1] + (c0));      \
-        r2 = *reinterpret_cast<const float4 *>(R + rsrc[2] + (c0));      \
-        r3 = *reinterpret_cast<const float4 *>(R + rsrc[3] + (c0));      \
-        xx = *reinterpret_cast<const float4 *>(xsrc + (c0));             \
-    } while (0)
-#define VH_SM_STORE(buf, r0, r1, r2, r3, xx)                                                   \
-    do {                                                                                       \
-        float *rd = rdst + (buf) * (kSmExp * kSmRS);                                           \
-        *reinterpret_cast<float4 *>(rd) = r0;                                                  \
-        *reinterpret_cast<float4 *>(rd + 8 * kSmRS) = r1;                                      \
-        *reinterpret_cast<float4 *>(rd + 16 * kSmRS) = r2;                                     \
-        *reinterpret_cast<float4 *>(rd + 24 * kSmRS) = r3;                                     \
-        *reinterpret_cast<float4 *>(xdst + (buf) * (kSmTok * kSmCol)) = xx;                    \
-    } while (0)
-    VH_SM_LOAD(0, ra0, ra1, ra2, ra3, xa);
-    VH_SM_LOAD(kSmCol, rb0, rb1, rb2, rb3, xb);
-    VH_SM_STORE(0, ra0, ra1, ra2, ra3, xa);
-    __syncthreads();
-    for (int c = 0; c < nc; c += 2) {
-        // chunk c from buffer 0 (set B holds chunk c + 1), then chunk c + 1 from buffer 1
-        if (c + 2 < nc) VH_SM_LOAD((c + 2) * kSmCol, ra0, ra1, ra2, ra3, xa);
-        VH_SM_STORE(1, rb0, rb1, rb2, rb3, xb);
-        for (int h = 0; h < 2; h++) {
-            if (h == 1) {
-                __syncthreads();
-                if (c + 3 < nc) VH_SM_LOAD((c + 3) * kSmCol, rb0, rb1, rb2, rb3, xb);
-                if (c + 2 < nc) VH_SM_STORE(0, ra0, ra1, ra2, ra3, xa);
-            }
-            // the chunk's products 32 at a time, each group added in order
-            const float4 *r4 = reinterpret_cast<const float4 *>(rrow + h * (kSmExp * kSmRS));
-            const float4 *x4 = reinterpret_cast<const float4 *>(xrow + h * (kSmTok * kSmCol));
-#pragma unroll 1
-            for (int q = 0; q < 4; q++) {
-                float pr[32];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float4 rv = r4[8 * q + i], xv = x4[8 * q + i];
-                    pr[4 * i + 0] = mul_rn(rv.x, xv.x);
-                    pr[4 * i + 1] = mul_rn(rv.y, xv.y);
-                    pr[4 * i + 2] = mul_rn(rv.z, xv.z);
-                    pr[4 * i + 3] = mul_rn(rv.w, xv.w);
-                }
-#pragma unroll
-                for (int k2 = 0; k2 < 32; k2++) a = add_rn(a, pr[k2]);
-            }
-        }
-        __syncthreads();
-    }
-#undef VH_SM_LOAD
-#undef VH_SM_STORE
-    if (e < E && t < T) {
-        if (bias) a = add_rn(a, bias[e]);
-        parts[size_t(t) * E + e] = RoutePart{double(a), 0.0};
-    }
-}
-
 // one 256-thread workgroup per token
 __global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__restrict__ parts,
                                                            const float *__restrict__ R, const float *__restrict__ hb,
@@ -295,15 +199,8 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
     if (nzero > E * T * 64) return -EINVAL;
     if (exact) {
         if (nzero) return -EINVAL;
-        const bool small = T < kExactSmallTokens && d % 256 == 0 &&
-                           ((reinterpret_cast<uintptr_t>(R) | reinterpret_cast<uintptr_t>(hb)) & 15u) == 0;
-        if (small) {
-            VH_LAUNCH(route_exact_small_kernel, dim3((T + kSmTok - 1) / kSmTok, (E + kSmExp - 1) / kSmExp),
-                      dim3(256), 0, s, R, hb, bias, d, E, T, parts);
-        } else {
-            dim3 g((T + kExTok - 1) / kExTok, (E + kExExp - 1) / kExExp);
-            hipLaunchKernelGGL(route_exact_kernel, g, dim3(256), 0, s, R, hb, bias, d, E, T, parts);
-        }
+        dim3 g((T + kExTok - 1) / kExTok, (E + kExExp - 1) / kExExp);
+        hipLaunchKernelGGL(route_exact_kernel, g, dim3(256), 0, s, R, hb, bias, d, E, T, parts);
     } else {
         const bool fast = d == 2048 && (reinterpret_cast<uintptr_t>(R) & 15u) == 0 &&
                           (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
