@@ -139,6 +139,7 @@ __global__ void __launch_bounds__(256) dispatch_count_kernel(const int32_t *__re
     __shared__ int wsum[4];
     const int e = blockIdx.x;
     int c = 0;
+#pragma unroll 16  // independent loads in flight together
     for (int p = threadIdx.x; p < P; p += 256) c += idx[p] == e ? 1 : 0;
     int total;
     block_excl_scan(c, total, wsum);
@@ -368,10 +369,55 @@ __global__ void __launch_bounds__(512) grouped_proj_kernel(const int32_t *__rest
     }
 }
 
+// x[t][o] += sum_j w[t][j] y[t k + j][o] in selection order, fp32, each
+// product and sum rounded (src/gguf_run.c:208-213). A thread owns four
+// consecutive outputs (d % 4 == 0): the token's routing and the experts'
+// presence are read first, then every y row's four values are loaded at
+// once, then summed in order. K = k, a compile-time count.
+template <int K>
 __global__ void __launch_bounds__(256) combine_kernel(const int32_t *__restrict__ idx, const float *__restrict__ w,
                                                       const void *const *__restrict__ table,
-                                                      const float *__restrict__ ybuf, int d, int k,
+                                                      const float *__restrict__ ybuf, int d,
                                                       float *__restrict__ x) {
+    const int t = blockIdx.y;
+    const int o = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (o >= d) return;
+    float wt[K];
+    bool use[K];
+#pragma unroll
+    for (int j = 0; j < K; j++) {
+        const int e = idx[size_t(t) * K + j];
+        wt[j] = w[size_t(t) * K + j];
+        use[j] = e >= 0 && table[3 * e + 2] != nullptr;  // a failed lookup is skipped (src/gguf_run.c:201)
+    }
+    float4 yv[K];
+#pragma unroll
+    for (int j = 0; j < K; j++) yv[j] = *reinterpret_cast<const float4 *>(ybuf + (size_t(t) * K + j) * d + o);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < K; j++) {
+        if (!use[j]) continue;
+        a.x = add_rn(a.x, mul_rn(wt[j], yv[j].x));
+        a.y = add_rn(a.y, mul_rn(wt[j], yv[j].y));
+        a.z = add_rn(a.z, mul_rn(wt[j], yv[j].z));
+        a.w = add_rn(a.w, mul_rn(wt[j], yv[j].w));
+    }
+    float4 *xp = reinterpret_cast<float4 *>(x + size_t(t) * d + o);
+    float4 xv = *xp;
+    xv.x = add_rn(xv.x, a.x);
+    xv.y = add_rn(xv.y, a.y);
+    xv.z = add_rn(xv.z, a.z);
+    xv.w = add_rn(xv.w, a.w);
+    *xp = xv;
+}
+
+// the general case (another k, or d not a multiple of 4, or unaligned
+// rows): one output per thread
+__global__ void __launch_bounds__(256) combine_any_kernel(const int32_t *__restrict__ idx,
+                                                          const float *__restrict__ w,
+                                                          const void *const *__restrict__ table,
+                                                          const float *__restrict__ ybuf, int d, int k,
+                                                          float *__restrict__ x) {
     const int t = blockIdx.y;
     const int o = blockIdx.x * 256 + threadIdx.x;
     if (o >= d) return;
@@ -479,7 +525,16 @@ int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, c
 
 int vh_combine(const int32_t *idx, const float *w, const void *const *table, const float *ybuf, int d, int k, int T,
                float *x, hipStream_t s) {
-    dim3 g((d + 255) / 256, T);
-    hipLaunchKernelGGL(combine_kernel, g, dim3(256), 0, s, idx, w, table, ybuf, d, k, x);
+    const bool vec = (k == 8 || k == 4 || k == 2) && d % 4 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(ybuf) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+    if (vec) {
+        dim3 g((d / 4 + 255) / 256, T);
+        if (k == 8) hipLaunchKernelGGL(combine_kernel<8>, g, dim3(256), 0, s, idx, w, table, ybuf, d, x);
+        else if (k == 4) hipLaunchKernelGGL(combine_kernel<4>, g, dim3(256), 0, s, idx, w, table, ybuf, d, x);
+        else hipLaunchKernelGGL(combine_kernel<2>, g, dim3(256), 0, s, idx, w, table, ybuf, d, x);
+    } else {
+        dim3 g((d + 255) / 256, T);
+        hipLaunchKernelGGL(combine_any_kernel, g, dim3(256), 0, s, idx, w, table, ybuf, d, k, x);
+    }
     return vh_check(hipGetLastError());
 }

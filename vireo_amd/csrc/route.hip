@@ -76,15 +76,16 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
     if (lane == 0) parts[size_t(t) * E + e] = p;
 }
 
-constexpr int kExTok = 64, kExExp = 16, kExChunk = 64;
+constexpr int kExTok = 64, kExCpl = 2, kExExp = 4 * kExCpl, kExChunk = 64;
 
-// grid (ceil(T/64), ceil(E/16)), 256 threads: lane = token t0 + lane, wave g
-// = experts e0 + 4g .. +3 (four independent in-order chains per lane). Each
-// 64-column chunk of the tokens' inputs (transposed, xs[column][token], padded
-// so that both the staging writes and the per-column reads are conflict-free)
-// and of the 16 router rows (read four columns at a time, one address for the
-// whole wave) goes through LDS; the next chunk is loaded into registers while
-// the current one is summed.
+// grid (ceil(T/64), ceil(E/8)), 256 threads: lane = token t0 + lane, wave g
+// = experts e0 + 2g, e0 + 2g + 1 (two independent in-order chains per lane;
+// two workgroups per CU keep the dependent adds of more waves in flight).
+// Each 64-column chunk of the tokens' inputs (transposed, xs[column][token],
+// padded so that both the staging writes and the per-column reads are
+// conflict-free) and of the 8 router rows (read four columns at a time, one
+// address for the whole wave) goes through LDS; the next chunk is loaded into
+// registers while the current one is summed.
 __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restrict__ R, const float *__restrict__ hb,
                                                           const float *__restrict__ bias, int d, int E, int T,
                                                           RoutePart *__restrict__ parts) {
@@ -93,9 +94,9 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     const int tid = threadIdx.x, tl = tid & 63, g = tid >> 6;
     const int t0 = blockIdx.x * kExTok, e0 = blockIdx.y * kExExp;
     // staging: thread tid loads column tid & 63 of token rows (tid >> 6) + 4j
-    // (j < 16) and of router rows (tid >> 6) + 4j (j < 4)
+    // (j < 16) and of router rows (tid >> 6) + 4j (j < kExCpl)
     const int cc = tid & 63, r0 = tid >> 6;
-    float xr[16], rr[4];
+    float xr[16], rr[kExCpl];
     auto load = [&](int c0) {
         const bool in = c0 + cc < d;
 #pragma unroll
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
             xr[j] = (in && t0 + tt < T) ? hb[size_t(t0 + tt) * d + c0 + cc] : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < kExCpl; j++) {
             const int ee = r0 + 4 * j;
             rr[j] = (in && e0 + ee < E) ? R[size_t(e0 + ee) * d + c0 + cc] : 0.0f;
         }
@@ -113,9 +114,9 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
 #pragma unroll
         for (int j = 0; j < 16; j++) xs[cc][r0 + 4 * j] = xr[j];
 #pragma unroll
-        for (int j = 0; j < 4; j++) reinterpret_cast<float *>(&rs[r0 + 4 * j][0])[cc] = rr[j];
+        for (int j = 0; j < kExCpl; j++) reinterpret_cast<float *>(&rs[r0 + 4 * j][0])[cc] = rr[j];
     };
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[kExCpl] = {};
     load(0);
     for (int c0 = 0; c0 < d; c0 += kExChunk) {
         store();
@@ -124,14 +125,14 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
         if (d - c0 >= kExChunk) {
 #pragma unroll
             for (int i4 = 0; i4 < kExChunk / 4; i4++) {
-                float4 r[4];
+                float4 r[kExCpl];
 #pragma unroll
-                for (int q = 0; q < 4; q++) r[q] = rs[4 * g + q][i4];
+                for (int q = 0; q < kExCpl; q++) r[q] = rs[kExCpl * g + q][i4];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     const float xv = xs[4 * i4 + u][tl];
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
+                    for (int q = 0; q < kExCpl; q++) {
                         const float rv = u == 0 ? r[q].x : u == 1 ? r[q].y : u == 2 ? r[q].z : r[q].w;
                         acc[q] = add_rn(acc[q], mul_rn(rv, xv));
                     }
@@ -141,8 +142,8 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
             for (int i = 0; i < d - c0; i++) {
                 const float xv = xs[i][tl];
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    acc[q] = add_rn(acc[q], mul_rn(reinterpret_cast<const float *>(&rs[4 * g + q][0])[i], xv));
+                for (int q = 0; q < kExCpl; q++)
+                    acc[q] = add_rn(acc[q], mul_rn(reinterpret_cast<const float *>(&rs[kExCpl * g + q][0])[i], xv));
             }
         }
         __syncthreads();
@@ -150,8 +151,8 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     const int t = t0 + tl;
     if (t < T) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int e = e0 + 4 * g + q;
+        for (int q = 0; q < kExCpl; q++) {
+            const int e = e0 + kExCpl * g + q;
             if (e < E) {
                 float a = acc[q];
                 if (bias) a = add_rn(a, bias[e]);
