@@ -37,10 +37,6 @@ import statistics
 import sys
 import time
 
-# The CPU baseline binds its OpenMP threads to neighbouring cores, as the
-# reference's baseline plan asks; the runtime reads this when it starts.
-os.environ.setdefault("OMP_PROC_BIND", "close")
-
 import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -63,6 +59,9 @@ WORKLOADS = {
 DEFAULT = "qwen3-q4km-decode-b1"
 # name: (shape, layers, vocab): greedy decode of a whole MoE stack + Q8_0 LM head
 STACKS = {"qwen3-q4km-stack48": ("qwen3-30b-a3b-q4_k_m", 48, 151936)}
+# name: (shape, layers, vocab, HBM expert pool bytes): the same stack read from a GGUF file on disk through the
+# ExpertStore, its experts paged into a pool smaller than the model
+PAGED = {"qwen3-q4km-stack48-paged4g": ("qwen3-30b-a3b-q4_k_m", 48, 151936, 4 << 30)}
 # name: (transformer layers, query heads, kv heads, head dim, context tokens, block tokens):
 # decode attention over the GPU KV store (dense, every block attended)
 ATTN = {"qwen3-attn-ctx4096": (48, 32, 4, 128, 4096, 32)}
@@ -77,7 +76,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 48 cycles of the layer rotation)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=DEFAULT,
-                    choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(ATTN) + sorted(MODELS) + ["copy-512MiB"])
+                    choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(PAGED) + sorted(ATTN) + sorted(MODELS)
+                    + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -330,6 +330,94 @@ def bench_stack(args):
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline_stack(shape, L, vocab, args.seed, args.cpu_seconds)
     st.close()
+    print(json.dumps(result), flush=True)
+
+
+def bench_paged_stack(args):
+    """The stack of bench_stack served from a GGUF file through an
+    ExpertStore whose HBM pool holds a fraction of the experts: every layer's
+    routed experts not resident are read from the file (the page cache) into
+    the pool on the copy stream before their kernels run, and the experts the
+    next layer's router guesses are read while each layer's routing is on its
+    way. Steps are timed one by one (a paged step makes host decisions between
+    layers, so it is not captured in a graph); the pool's counters give the
+    bytes paged per token, read-ahead included."""
+    import tempfile
+    import torch
+    from vireo_amd import _lib
+    from vireo_amd import gguf as G
+    from vireo_amd import workloads as W
+
+    lib = _lib.load()
+    _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
+    shape_name, L, vocab, cap = PAGED[args.workload]
+    L = args.layers or L
+    shape = W.SHAPES[shape_name]
+    K = args.steps or 8
+    Wm = args.warmup if args.warmup is not None else 2
+    tmp = tempfile.mkdtemp(prefix="vireo_paged_")
+    path = os.path.join(tmp, "stack.gguf")
+    try:
+        print(f"[bench] {args.workload}: writing {L} layers of {shape.name} ({L * shape.E * shape.expert_bytes() / 2**30:.1f} "
+              f"GiB of experts) and a [{vocab} x {shape.d}] Q8_0 head to {path}", file=sys.stderr, flush=True)
+        # the experts are made on the device (the host generator's bytes) and copied out layer by layer
+        from vireo_amd import moe as M
+        dm = M.DeviceMoE(shape, L, seed=args.seed)
+        G.write_moe_gguf(path, shape, L, seed=args.seed, vocab=vocab,
+                         progress=lambda msg: print(f"[bench] {msg}", file=sys.stderr, flush=True),
+                         layer_bytes=dm.device_layer_bytes)
+        dm.close()
+        del dm
+        torch.cuda.empty_cache()
+        print(f"[bench] loading with a {cap / 2**30:.1f} GiB expert pool", file=sys.stderr, flush=True)
+        m = G.GGUFModel(path, expert_capacity=cap)
+        d = shape.d
+        x = torch.empty(d, dtype=torch.float32, device="cuda")
+        xb = torch.empty_like(x)
+        logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
+        token = torch.full((1,), 17, dtype=torch.int32, device="cuda")
+        stream = torch.cuda.Stream()  # a stream of its own, as a serving loop would pass
+        for i in range(Wm):
+            m.step(token, x, xb, logits, stream=stream)
+            torch.cuda.synchronize()
+            print(f"[bench] warm-up step {i} done", file=sys.stderr, flush=True)
+        before, pf0 = m.hbm_stats(), m.prefetch_stats()
+        t0 = time.perf_counter()
+        for i in range(K):
+            m.step(token, x, xb, logits, stream=stream)
+            torch.cuda.synchronize()
+            print(f"[bench] step {i} done", file=sys.stderr, flush=True)
+        secs = time.perf_counter() - t0
+        after, pf1 = m.hbm_stats(), m.prefetch_stats()
+        paged = after["bytes_read"] - before["bytes_read"]
+        misses = after["misses"] - before["misses"]
+        ms_per_step = secs * 1e3 / K
+        gbs = paged / K / (ms_per_step / 1e3) / 1e9
+        result = {
+            "metric": METRIC, "value": round(K / secs, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+            "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": f"{L}-layer {shape.name} MoE stack (attention omitted) + Q8_0 LM head "
+                                   f"[{vocab} x {shape.d}] from a GGUF file, experts paged into a "
+                                   f"{cap / 2**30:.1f} GiB HBM pool, greedy decode batch 1",
+                       "layers": L, "experts": shape.E, "top_k": shape.k, "pool_bytes": cap,
+                       "model_expert_bytes": L * shape.E * shape.expert_bytes()},
+            "paged_bytes_per_token": int(paged / K), "pool_misses_per_token": round(misses / K, 2),
+            "prefetch_per_token": {"read_ahead": round((pf1["issued"] - pf0["issued"]) / K, 2),
+                                   "used": round((pf1["used"] - pf0["used"]) / K, 2),
+                                   "bytes": int((pf1["bytes"] - pf0["bytes"]) / K)},
+            "pool": after,
+            "roofline": {"kernel": "moe_stack_step with paging (file -> pinned staging -> HBM pool)", "bound": "pcie",
+                         "achieved": round(gbs, 2), "unit": "GB/s", "traffic": None,
+                         "note": "paged bytes per second of decode; the page-ins cross PCIe from the page cache"},
+        }
+        m.close()
+    finally:
+        try:
+            os.remove(path)
+        except OSError:
+            pass
+        os.rmdir(tmp)
     print(json.dumps(result), flush=True)
 
 
@@ -675,6 +763,15 @@ def main():
               f"(no collectives, no sharding); --gpus {args.gpus} / WORLD_SIZE {world} is not supported.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload in PAGED:
+        # no OpenMP binding here: once torch loads the OpenMP runtime it would
+        # bind this thread to one core, and the ExpertStore's reader threads,
+        # started from it, would inherit that single core
+        return bench_paged_stack(args)
+    # The CPU baseline binds its OpenMP threads to neighbouring cores, as the
+    # reference's baseline plan asks; the runtime reads this when it starts
+    # (nothing has loaded it yet: torch is imported below).
+    os.environ.setdefault("OMP_PROC_BIND", "close")
     if args.workload in STACKS:
         return bench_stack(args)
     if args.workload in ATTN:

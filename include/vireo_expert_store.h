@@ -14,7 +14,13 @@
  * backing file, -ENOMEM when device memory runs out.
  *
  * Threading: like the reference, a store is not locked; use it from one host
- * thread at a time. */
+ * thread at a time. Inside, an expert of 256 KiB or more is read from the
+ * file by eight threads at once (seven workers the store starts on its first
+ * such read and joins in expert_store_destroy), since one thread's copy out of
+ * the page cache runs at about half the host-to-device link. The workers
+ * inherit the CPU affinity of the thread that starts them: a program that has
+ * bound that thread to one core (OpenMP's OMP_PROC_BIND does so once its
+ * runtime starts) runs all eight readers on that core. */
 #ifndef VIREO_EXPERT_STORE_H
 #define VIREO_EXPERT_STORE_H
 

@@ -156,6 +156,11 @@ int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_experts,
  * compute and copied to HBM on a copy stream; least recently used unleased
  * experts evicted, their blocks reused only after the kernels reading them);
  * such a call synchronizes the stream once and cannot be captured in a graph.
+ * A paged call of at most 8 tokens on a file-backed store also guesses the
+ * next layer's experts - that layer's router applied to this call's hb - and
+ * the next call on that layer reads the guessed experts not yet resident
+ * while it waits for its own routing (expert_store_set_prefetch turns this
+ * off); a guess changes what the pool holds, never a result.
  * expert_store_stats then counts what the reference would: one lookup per
  * (token, routed expert) in token and selection order (see
  * expert_store_hbm_stats for what the HBM pool itself did). An expert that is
@@ -413,6 +418,14 @@ int expert_store_unpin_layer(ExpertStore *s, int layer);
  * and the bytes and experts resident in HBM now. expert_store_stats reports
  * the reference's accounting of the same work instead. */
 void expert_store_hbm_stats(const ExpertStore *s, ExpertStats *out);
+/* Prefetch by paged calls (no counterpart in the reference, whose
+ * ROADMAP.md:46-47 lists it as open): on by default for a store that reads a
+ * file; 0 turns it off. -EINVAL for a store this library did not make. */
+int expert_store_set_prefetch(ExpertStore *s, int on);
+/* out[0] experts read ahead, out[1] of those looked up before being evicted,
+ * out[2] bytes read ahead (also counted in expert_store_hbm_stats's
+ * bytes_read). */
+void expert_store_prefetch_stats(const ExpertStore *s, uint64_t out[3]);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,8 @@ the oracle on the arrays that were written into the file.
   kernels (more than one token); the pool never exceeds its capacity, the
   statistics equal the oracle's ExpertStore driven by the same tokens, and the
   stack decodes through it.
+* Prefetch: the paged stack with and without reading the next layer's
+  guessed experts ahead gives equal results bit for bit and equal statistics.
 """
 import numpy as np
 import pytest
@@ -159,3 +161,43 @@ def test_gguf_paged_store(cuda, oracle, tmp_path, name, cap_experts, T, L):
     replay.close()
     paged.close()
     full.close()
+
+
+@pytest.mark.parametrize("name,cap_experts,L", [("qwen3-16e", 12, 4), ("tiny-k", 6, 4)])
+def test_gguf_prefetch_changes_no_result(cuda, oracle, tmp_path, name, cap_experts, L):
+    """Paged decode through the stack with the next-layer guess on and off:
+    every step's state, logits and token are equal bit for bit (the guess
+    changes what the pool holds, not the batches or kernels), the reference's
+    statistics are equal, the pool stays within its capacity, and guessed
+    experts are read ahead and then looked up (the residual stream moves
+    little between layers, so the next router's choice on this layer's input
+    is often right)."""
+    shape, vocab = SHAPES[name], 300
+    path = tmp_path / "pf.gguf"
+    G.write_moe_gguf(str(path), shape, L, seed=53, vocab=vocab)
+    cap = cap_experts * shape.expert_bytes()
+    runs = {}
+    for on in (True, False):
+        m = G.GGUFModel(path, expert_capacity=cap)
+        m.set_prefetch(on)
+        x = torch.empty(shape.d, dtype=torch.float32, device=cuda)
+        xb = torch.empty_like(x)
+        logits = torch.empty(vocab, dtype=torch.float32, device=cuda)
+        token = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+        stream = torch.cuda.Stream()
+        seen = []
+        for _ in range(6):
+            m.step(token, x, xb, logits, stream=stream)
+            torch.cuda.synchronize()
+            seen.append((x.cpu().clone(), logits.cpu().clone(), int(token.cpu()[0])))
+            assert m.hbm_stats()["resident_bytes"] <= cap
+        runs[on] = (seen, m.stats(), m.prefetch_stats())
+        m.close()
+    (a, sa, pa), (b, sb, pb) = runs[True], runs[False]
+    for i, ((xa, la, ta), (xb_, lb, tb)) in enumerate(zip(a, b)):
+        assert torch.equal(xa, xb_) and torch.equal(la, lb) and ta == tb, f"step {i}"
+    assert sa == sb
+    print(f"{name}: prefetch {pa}; off {pb}")
+    assert pb == {"issued": 0, "used": 0, "bytes": 0}
+    assert pa["issued"] > 0 and 0 < pa["used"] <= pa["issued"]
+    assert pa["bytes"] == pa["issued"] * shape.expert_bytes()

@@ -141,6 +141,43 @@ def test_moe_from_file_backed_store(cuda, lib):
     m.close()
 
 
+@pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
+def test_golden_store_stats(cuda, lib, case):
+    """The reference's own ExpertStore statistics after its moe_ffn over the
+    golden tokens (an unbounded store, as the golden run had; one lookup per
+    token and routed expert, src/expert_store.c:72-92): the same layer served
+    from a file-backed store reports the same seven numbers, and the same
+    outputs."""
+    g = golden(f"moe_{case}.npz")
+    d, E, k, fe, renorm, gt, ut, dt = (int(v) for v in g["shape"])
+    shape = W.MoEShape(case, d, E, k, fe, bool(renorm), gt, ut, dt)
+    m = M.DeviceMoE(shape, 1, seed=int(g["seed"][0]))
+    gb, ub, db = m.device_layer_bytes(0)
+    gs, us, ds = m.slices
+    fd, path = tempfile.mkstemp()
+    os.unlink(path)
+    try:
+        os.pwrite(fd, gb.tobytes() + ub.tobytes() + db.tobytes(), 0)
+        s = lib.expert_store_create(fd, 0, 1, E)
+        for e in range(E):
+            sl = _lib.ExpertSlices(e * gs, gb.size + e * us, gb.size + ub.size + e * ds, gs, us, ds)
+            lib.expert_store_register(s, 0, e, C.byref(sl))
+        m.model.es = s
+        xt = torch.from_numpy(g["x"]).to(cuda)
+        idx, _ = m.forward(0, xt, torch.from_numpy(g["hb"]).to(cuda), return_routing=True)
+        np.testing.assert_array_equal(idx.cpu().numpy(), g["idx"])
+        torch.cuda.synchronize()
+        st = _lib.ExpertStats()
+        lib.expert_store_stats(s, C.byref(st))
+        got = [getattr(st, f) for f, _ in _lib.ExpertStats._fields_]
+        assert got == [int(v) for v in g["store_stats"]], (got, g["store_stats"])
+        lib.expert_store_destroy(s)
+    finally:
+        os.close(fd)
+        m.model.es = m.es
+        m.close()
+
+
 @pytest.mark.parametrize("cap_experts", [0, 2])
 def test_truncated_backing_file_is_an_error(cuda, lib, cap_experts):
     """A backing file that ends inside an expert's slices: the lookup that

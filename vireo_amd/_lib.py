@@ -203,6 +203,8 @@ SIGNATURES = {
     "expert_store_release": (None, [c_vp, C.POINTER(ExpertView)]),
     "expert_store_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
     "expert_store_hbm_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
+    "expert_store_set_prefetch": (C.c_int, [c_vp, C.c_int]),
+    "expert_store_prefetch_stats": (None, [c_vp, C.POINTER(C.c_uint64)]),
     "vireo_hip_status": (C.c_int, [c_vp]),
     "vireo_hip_set_spin_limit": (C.c_int, [C.c_uint]),
     "expert_store_destroy": (None, [c_vp]),

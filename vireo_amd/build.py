@@ -26,7 +26,7 @@ HIP_FLAGS = [
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", INCLUDE, "-I", CSRC,
 ]
-C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-I", INCLUDE, "-I", os.path.join(ROCM, "include")]
+C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-pthread", "-Wall", "-Wextra", "-I", INCLUDE, "-I", os.path.join(ROCM, "include")]
 
 
 def _run(cmd, verbose):
@@ -63,7 +63,7 @@ def build(verbose=False):
     # of the executable (a reference build that still links its CPU
     # src/expert_store.c would otherwise interpose its store on them)
     _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
-          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,-Bsymbolic"], verbose)
+          f"-L{ROCM}/lib", "-lamdhip64", "-lpthread", f"-Wl,-rpath,{ROCM}/lib", "-Wl,-Bsymbolic"], verbose)
     os.replace(tmp, LIB)
     return LIB
 

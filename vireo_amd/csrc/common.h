@@ -28,9 +28,11 @@ int vh_reduce_scratch(size_t bytes, void **out);     // per-device scratch for r
 int vh_num_cus();
 // The per-device stream that expert page-in copies run on (created on first use).
 int vh_copy_stream(hipStream_t *out);
-// Pinned host memory for small per-call uploads (grow-only, per device). A
-// call that takes it first waits until the copies of the previous call that
-// used it have run (the event vh_host_staging_done recorded on that call's stream).
+// Pinned host memory for small per-call transfers (grow-only, per device; two
+// buffers taken in turn, so a call does not wait for the one just before it).
+// A call that takes a buffer first waits until the copies of the last call
+// that used that buffer have run (the event vh_host_staging_done recorded on
+// that call's stream).
 int vh_host_staging(size_t bytes, void **out);
 int vh_host_staging_done(hipStream_t s);
 // Sticky per-device status bits that kernels with grid-wide waits set when a

@@ -29,6 +29,7 @@
 #define _POSIX_C_SOURCE 200809L
 #define __HIP_PLATFORM_AMD__ 1
 #include <errno.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
@@ -48,6 +49,9 @@ typedef struct {
     /* the reference's book */
     int ref_resident, ref_lease;
     uint64_t ref_last_used;
+    /* places in the two books' LRU lists (slot indices, -1 at the ends) */
+    int lru_prev, lru_next, ref_prev, ref_next;
+    int prefetched;       /* paged in ahead of use and not yet looked up */
 } Slot;
 
 typedef struct { void *ptr; uint64_t size; hipEvent_t busy; int busy_set; } FreeBlock;
@@ -61,10 +65,36 @@ typedef struct {
 } Note;
 #define VH_NOTES 64
 
-/* Staging buffers for asynchronous page-in: pread fills one, an H2D copy on
- * the copy stream drains it; `done` marks when it may be filled again. */
+/* Staging buffers for asynchronous page-in: one expert's three slices are
+ * read into one buffer, laid out as its HBM block, and one H2D copy on the
+ * copy stream drains it; `done` marks when it may be filled again. */
 #define VH_STAGES 8
 typedef struct { void *buf; size_t bytes; hipEvent_t done; int done_set; } Stage;
+
+/* Where one read puts a slice: file offset, length, offset in the buffer. */
+typedef struct { uint64_t off; uint32_t len; uint64_t at; } Span;
+
+/* Parallel reads: an expert of at least VH_PAR_MIN bytes is read by
+ * VH_READERS threads at once, each pread-ing a 4 KiB-aligned piece of its
+ * slices laid end to end - one thread's copy out of the page cache runs at
+ * about half the host-to-device link. The workers start with the store's
+ * first large read and stop in expert_store_destroy; a store that cannot
+ * start them reads serially. */
+#define VH_READERS 8
+#define VH_PAR_MIN (256u << 10)
+typedef struct {
+    pthread_mutex_t mu;
+    pthread_cond_t go, done;
+    pthread_t th[VH_READERS - 1];
+    int nth, quit;
+    unsigned gen;              /* job number: workers run each job once */
+    int pending, err;          /* workers still reading the job; the first error */
+    int fd;
+    uint8_t *dst;
+    Span sp[3];
+    int nsp;
+    uint64_t total;
+} ReadPool;
 
 /* First word of every store made here. A store handed in by a program that
  * still links the reference's CPU src/expert_store.c starts with its int fd
@@ -87,7 +117,12 @@ struct ExpertStore {
     void **tables;             /* per layer: device [n_experts x 3] pointer table */
     FreeBlock *freel;          /* device blocks of evicted experts, kept for reuse */
     int nfree, capfree;
+    uint8_t *arena;            /* one allocation the pool's blocks are cut from (bounded pools) */
+    uint64_t arena_size, arena_used;
+    int arena_failed;
     Stage ring[VH_STAGES];     /* asynchronous page-in */
+    ReadPool *readers;         /* parallel pread workers (NULL until the first large read) */
+    int readers_failed;
     int ring_next;
     hipEvent_t copied;         /* after the last asynchronous page-in copy */
     /* the reference's book */
@@ -95,6 +130,16 @@ struct ExpertStore {
     ExpertStats ref;
     Note notes[VH_NOTES];
     int nhead, ncount;
+    /* Resident slots from least to most recently used, one list per book:
+     * the eviction victim of src/expert_store.c:52-63 (the resident expert
+     * without a lease used longest ago) is the first unleased slot of its
+     * list, as every use moves a slot to the end. */
+    int lru_head, lru_tail, ref_head, ref_tail;
+    uint64_t registered_bytes;
+    /* prefetch: the experts of one layer expected next, most likely first */
+    int hint_layer, hint_n, hint_pos, prefetch_off;
+    int32_t hint[64];
+    uint64_t pf_issued, pf_used, pf_bytes;
 };
 
 static uint64_t al256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
@@ -119,6 +164,10 @@ static ExpertStore *store_new(int n_layers, int n_experts, uint64_t capacity_byt
     s->tables = calloc((size_t)n_layers, sizeof(void *));
     if (!s->slots || !s->tables) { free(s->slots); free(s->tables); free(s); return NULL; }
     s->capacity_bytes = capacity_bytes;
+    for (int i = 0; i < s->n_slots; i++)
+        s->slots[i].lru_prev = s->slots[i].lru_next = s->slots[i].ref_prev = s->slots[i].ref_next = -1;
+    s->lru_head = s->lru_tail = s->ref_head = s->ref_tail = -1;
+    s->hint_layer = -1;
     return s;
 }
 
@@ -139,9 +188,42 @@ ExpertStore *expert_store_create_device(const void *dev_base, uint64_t size, uin
 void expert_store_register(ExpertStore *s, int layer, int expert, const ExpertSlices *loc) {
     Slot *sl = slot_at(s, layer, expert);
     if (!sl || !loc) return;
+    if (sl->registered) s->registered_bytes -= sl->bytes;
     sl->loc = *loc;
     sl->bytes = (uint64_t)loc->gate_bytes + loc->up_bytes + loc->down_bytes;
     sl->registered = 1;
+    s->registered_bytes += sl->bytes;
+}
+
+/* ------------------------------------------------------------------ LRU lists */
+
+/* book 0: the pool's residency; book 1: the reference's replayed one */
+static int *link_prev(Slot *sl, int book) { return book ? &sl->ref_prev : &sl->lru_prev; }
+static int *link_next(Slot *sl, int book) { return book ? &sl->ref_next : &sl->lru_next; }
+
+static void lru_unlink(ExpertStore *s, Slot *sl, int book) {
+    int *head = book ? &s->ref_head : &s->lru_head, *tail = book ? &s->ref_tail : &s->lru_tail;
+    const int p = *link_prev(sl, book), n = *link_next(sl, book);
+    if (p >= 0) *link_next(&s->slots[p], book) = n;
+    else *head = n;
+    if (n >= 0) *link_prev(&s->slots[n], book) = p;
+    else *tail = p;
+    *link_prev(sl, book) = *link_next(sl, book) = -1;
+}
+
+/* sl has just been used: to the end of the list (linked in if new) */
+static void lru_touch(ExpertStore *s, Slot *sl, int book, int linked) {
+    int *head = book ? &s->ref_head : &s->lru_head, *tail = book ? &s->ref_tail : &s->lru_tail;
+    const int i = (int)(sl - s->slots);
+    if (linked) {
+        if (*tail == i) return;
+        lru_unlink(s, sl, book);
+    }
+    *link_prev(sl, book) = *tail;
+    *link_next(sl, book) = -1;
+    if (*tail >= 0) *link_next(&s->slots[*tail], book) = i;
+    else *head = i;
+    *tail = i;
 }
 
 /* ------------------------------------------------------------------ the reference's book */
@@ -151,11 +233,10 @@ static void ref_make_room(ExpertStore *s, uint64_t need) {
     if (!s->capacity_bytes) return;
     while (s->ref_resident_bytes + need > s->capacity_bytes) {
         Slot *victim = NULL;
-        for (int i = 0; i < s->n_slots; i++) {
-            Slot *c = &s->slots[i];
-            if (c->ref_resident && !c->ref_lease && (!victim || c->ref_last_used < victim->ref_last_used)) victim = c;
-        }
+        for (int i = s->ref_head; i >= 0 && !victim; i = s->slots[i].ref_next)
+            if (!s->slots[i].ref_lease) victim = &s->slots[i];
         if (!victim) break;
+        lru_unlink(s, victim, 1);
         victim->ref_resident = 0;
         s->ref_resident_bytes -= victim->bytes;
         s->ref.experts_resident--;
@@ -167,6 +248,7 @@ static void ref_make_room(ExpertStore *s, uint64_t need) {
 static int ref_lookup(ExpertStore *s, Slot *sl, int lease) {
     s->ref.requests++;
     if (!sl->registered) return -1;
+    const int was = sl->ref_resident;
     if (sl->ref_resident) {
         s->ref.hits++;
     } else {
@@ -178,6 +260,7 @@ static int ref_lookup(ExpertStore *s, Slot *sl, int lease) {
         s->ref.experts_resident++;
     }
     sl->ref_last_used = ++s->ref_tick;
+    lru_touch(s, sl, 1, was);
     if (lease) sl->ref_lease++;
     return 0;
 }
@@ -255,6 +338,13 @@ void vh_store_note_routing_host(ExpertStore *s, int layer, const int32_t *idx, i
 
 /* ------------------------------------------------------------------ the pool */
 
+/* Free a device block: blocks cut from the arena go back with the arena. */
+static void block_free(ExpertStore *s, void *p) {
+    const uint8_t *b = (const uint8_t *)p;
+    if (s->arena && b >= s->arena && b < s->arena + s->arena_size) return;
+    (void)hipFree(p);
+}
+
 static void release_block(ExpertStore *s, Slot *v) {
     if (v->dev) {
         if (s->nfree == s->capfree) {
@@ -270,7 +360,7 @@ static void release_block(ExpertStore *s, Slot *v) {
             v->busy_set = 0;
         } else {
             if (v->busy_set) (void)hipEventSynchronize(v->busy);
-            (void)hipFree(v->dev);
+            block_free(s, v->dev);
         }
     }
     v->dev = NULL;
@@ -279,6 +369,8 @@ static void release_block(ExpertStore *s, Slot *v) {
 
 static void evict_one(ExpertStore *s, Slot *v) {
     release_block(s, v);
+    lru_unlink(s, v, 0);
+    v->prefetched = 0;  /* read ahead for nothing */
     v->resident = 0;
     s->resident_bytes -= v->bytes;
     s->hbm.experts_resident--;
@@ -289,17 +381,20 @@ static void make_room(ExpertStore *s, uint64_t need) {
     if (!s->capacity_bytes) return;
     while (s->resident_bytes + need > s->capacity_bytes) {
         Slot *victim = NULL;
-        for (int i = 0; i < s->n_slots; i++) {
-            Slot *c = &s->slots[i];
-            if (c->resident && !c->lease && (!victim || c->last_used < victim->last_used)) victim = c;
-        }
+        for (int i = s->lru_head; i >= 0 && !victim; i = s->slots[i].lru_next)
+            if (!s->slots[i].lease) victim = &s->slots[i];
         if (!victim) break; /* everything resident is leased: stay over budget */
         evict_one(s, victim);
     }
 }
 
 /* A device block of `size` bytes: a cached one (with the event its last
- * readers left, to be waited on before it is overwritten) or a new one. */
+ * readers left, to be waited on before it is overwritten) or a new one. A
+ * bounded pool cuts new blocks from one allocation of its capacity (plus
+ * 1/32 for the 256-byte padding of slices), made on its first page-in, so
+ * filling the pool costs no allocation per expert; past it (a pool over
+ * budget because every resident expert is leased, or blocks of several
+ * sizes) a block is allocated on its own. */
 static void *take_block(ExpertStore *s, uint64_t size, hipEvent_t *busy, int *busy_set) {
     *busy = NULL;
     *busy_set = 0;
@@ -311,13 +406,31 @@ static void *take_block(ExpertStore *s, uint64_t size, hipEvent_t *busy, int *bu
             s->freel[i] = s->freel[--s->nfree];
             return p;
         }
+    if (s->capacity_bytes && s->capacity_bytes <= (1ull << 44) && !s->arena && !s->arena_failed) {
+        const uint64_t want = s->capacity_bytes + (s->capacity_bytes >> 5);
+        void *a = NULL;
+        if (hipMalloc(&a, want) == hipSuccess) {
+            s->arena = (uint8_t *)a;
+            s->arena_size = want;
+            s->arena_used = 0;
+        } else {
+            (void)hipGetLastError();
+            s->arena_failed = 1;
+        }
+    }
+    if (s->arena && s->arena_size - s->arena_used >= size) {
+        void *p = s->arena + s->arena_used;
+        s->arena_used += (size + 255u) & ~(uint64_t)255u;
+        if (s->arena_used > s->arena_size) s->arena_used = s->arena_size;
+        return p;
+    }
     void *p = NULL;
     if (hipMalloc(&p, size) != hipSuccess) {
         /* drop cached blocks and retry once */
         for (int i = 0; i < s->nfree; i++) {
             if (s->freel[i].busy_set) (void)hipEventSynchronize(s->freel[i].busy);
             if (s->freel[i].busy) (void)hipEventDestroy(s->freel[i].busy);
-            (void)hipFree(s->freel[i].ptr);
+            block_free(s, s->freel[i].ptr);
         }
         s->nfree = 0;
         if (hipMalloc(&p, size) != hipSuccess) return NULL;
@@ -337,42 +450,154 @@ static int pread_all(int fd, void *dst, uint32_t bytes, uint64_t off) {
     return 0;
 }
 
-static int read_slice(ExpertStore *s, uint64_t off, uint32_t bytes, void *dst) {
-    if ((size_t)bytes > s->stage_bytes) {
-        if (s->stage) (void)hipHostFree(s->stage);
-        s->stage = NULL;
-        s->stage_bytes = 0;
-        size_t nb = bytes < (1u << 20) ? (1u << 20) : bytes;
-        if (hipHostMalloc(&s->stage, nb, 0) != hipSuccess) { s->stage = NULL; return -ENOMEM; }
-        s->stage_bytes = nb;
+/* Piece `id` of VH_READERS of a job: bytes [lo, hi) of its spans laid end to
+ * end, each part pread into its place in dst. */
+static int read_piece(int fd, uint8_t *dst, const Span *sp, int nsp, uint64_t total, int id) {
+    uint64_t per = (total + VH_READERS - 1) / VH_READERS;
+    per = (per + 4095u) & ~(uint64_t)4095u;
+    const uint64_t lo = per * (uint64_t)id < total ? per * (uint64_t)id : total;
+    const uint64_t hi = lo + per < total ? lo + per : total;
+    uint64_t base = 0;
+    for (int i = 0; i < nsp && lo < hi; i++) {
+        const uint64_t a = base, b = base + sp[i].len;
+        const uint64_t x = a > lo ? a : lo, y = b < hi ? b : hi;
+        if (x < y && pread_all(fd, dst + sp[i].at + (x - a), (uint32_t)(y - x), sp[i].off + (x - a))) return -EIO;
+        base = b;
     }
-    if (pread_all(s->fd, s->stage, bytes, off)) return -EIO;
-    if (hipMemcpy(dst, s->stage, bytes, hipMemcpyHostToDevice) != hipSuccess) return -EIO;
     return 0;
 }
 
-/* The same through the staging ring: pread into the next buffer (once the
- * copy that last drained it has finished), then an H2D copy on `cs`. The
- * host reads the next slice while earlier copies and kernels run. */
-static int read_slice_async(ExpertStore *s, uint64_t off, uint32_t bytes, void *dst, hipStream_t cs) {
+typedef struct { ReadPool *p; int id; } ReaderArg;
+
+static void *reader_main(void *arg) {
+    ReaderArg a = *(ReaderArg *)arg;
+    free(arg);
+    ReadPool *p = a.p;
+    unsigned seen = 0;
+    pthread_mutex_lock(&p->mu);
+    for (;;) {
+        while (!p->quit && p->gen == seen) pthread_cond_wait(&p->go, &p->mu);
+        if (p->quit) break;
+        seen = p->gen;
+        Span sp[3];
+        memcpy(sp, p->sp, sizeof sp);
+        const int fd = p->fd, nsp = p->nsp;
+        uint8_t *dst = p->dst;
+        const uint64_t total = p->total;
+        pthread_mutex_unlock(&p->mu);
+        const int rc = read_piece(fd, dst, sp, nsp, total, a.id);
+        pthread_mutex_lock(&p->mu);
+        if (rc && !p->err) p->err = rc;
+        if (--p->pending == 0) pthread_cond_signal(&p->done);
+    }
+    pthread_mutex_unlock(&p->mu);
+    return NULL;
+}
+
+static void readers_stop(ExpertStore *s) {
+    ReadPool *p = s->readers;
+    if (!p) return;
+    pthread_mutex_lock(&p->mu);
+    p->quit = 1;
+    pthread_cond_broadcast(&p->go);
+    pthread_mutex_unlock(&p->mu);
+    for (int i = 0; i < p->nth; i++) pthread_join(p->th[i], NULL);
+    pthread_cond_destroy(&p->go);
+    pthread_cond_destroy(&p->done);
+    pthread_mutex_destroy(&p->mu);
+    free(p);
+    s->readers = NULL;
+}
+
+static int readers_start(ExpertStore *s) {
+    if (s->readers) return 0;
+    if (s->readers_failed) return -1;
+    ReadPool *p = (ReadPool *)calloc(1, sizeof(ReadPool));
+    if (!p) { s->readers_failed = 1; return -1; }
+    pthread_mutex_init(&p->mu, NULL);
+    pthread_cond_init(&p->go, NULL);
+    pthread_cond_init(&p->done, NULL);
+    s->readers = p;
+    for (int i = 0; i < VH_READERS - 1; i++) {
+        ReaderArg *a = (ReaderArg *)malloc(sizeof(ReaderArg));
+        if (!a) break;
+        a->p = p;
+        a->id = i + 1;
+        if (pthread_create(&p->th[i], NULL, reader_main, a) != 0) { free(a); break; }
+        p->nth++;
+    }
+    if (p->nth != VH_READERS - 1) {  /* all or nothing: the pieces assume every worker */
+        readers_stop(s);
+        s->readers_failed = 1;
+        return -1;
+    }
+    return 0;
+}
+
+/* Read the spans into dst: by the reader pool when they are large (the
+ * calling thread reads piece 0 and waits for the rest), else in turn. */
+static int read_spans(ExpertStore *s, uint8_t *dst, const Span *sp, int nsp) {
+    uint64_t total = 0;
+    for (int i = 0; i < nsp; i++) total += sp[i].len;
+    if (total < VH_PAR_MIN || readers_start(s)) {
+        for (int i = 0; i < nsp; i++)
+            if (pread_all(s->fd, dst + sp[i].at, sp[i].len, sp[i].off)) return -EIO;
+        return 0;
+    }
+    ReadPool *p = s->readers;
+    pthread_mutex_lock(&p->mu);
+    p->fd = s->fd;
+    p->dst = dst;
+    memcpy(p->sp, sp, (size_t)nsp * sizeof(Span));
+    p->nsp = nsp;
+    p->total = total;
+    p->err = 0;
+    p->pending = VH_READERS - 1;
+    p->gen++;
+    pthread_cond_broadcast(&p->go);
+    pthread_mutex_unlock(&p->mu);
+    int rc = read_piece(s->fd, dst, sp, nsp, total, 0);
+    pthread_mutex_lock(&p->mu);
+    while (p->pending > 0) pthread_cond_wait(&p->done, &p->mu);
+    if (!rc) rc = p->err;
+    pthread_mutex_unlock(&p->mu);
+    return rc;
+}
+
+/* A pinned buffer of at least `bytes` in *buf (grown as needed). */
+static int stage_fit(void **buf, size_t *have, size_t bytes) {
+    if (bytes <= *have) return 0;
+    if (*buf) (void)hipHostFree(*buf);
+    *buf = NULL;
+    *have = 0;
+    const size_t nb = bytes < (4u << 20) ? (4u << 20) : bytes;
+    if (hipHostMalloc(buf, nb, 0) != hipSuccess) { *buf = NULL; return -ENOMEM; }
+    *have = nb;
+    return 0;
+}
+
+/* Read one expert's slices from the file into the device block `blk` (at
+ * offsets sp[i].at, `len` bytes in all): through pinned staging and a
+ * synchronous copy, or through the next buffer of the staging ring (once the
+ * copy that last drained it has finished) and a copy on `cs`, so the host
+ * reads the next expert while earlier copies and kernels run. */
+static int read_block(ExpertStore *s, const Span *sp, uint64_t len, uint8_t *blk, hipStream_t cs) {
+    if (!cs) {
+        if (stage_fit(&s->stage, &s->stage_bytes, len)) return -ENOMEM;
+        if (read_spans(s, (uint8_t *)s->stage, sp, 3)) return -EIO;
+        return hipMemcpy(blk, s->stage, len, hipMemcpyHostToDevice) == hipSuccess ? 0 : -EIO;
+    }
     Stage *st = &s->ring[s->ring_next];
     s->ring_next = (s->ring_next + 1) % VH_STAGES;
     if (st->done_set && hipEventSynchronize(st->done) != hipSuccess) return -EIO;
     st->done_set = 0;
-    if ((size_t)bytes > st->bytes) {
-        if (st->buf) (void)hipHostFree(st->buf);
-        st->buf = NULL;
-        st->bytes = 0;
-        size_t nb = bytes < (2u << 20) ? (2u << 20) : bytes;
-        if (hipHostMalloc(&st->buf, nb, 0) != hipSuccess) { st->buf = NULL; return -ENOMEM; }
-        st->bytes = nb;
-    }
+    if (stage_fit(&st->buf, &st->bytes, len)) return -ENOMEM;
     if (!st->done && hipEventCreateWithFlags(&st->done, hipEventDisableTiming) != hipSuccess) {
         st->done = NULL;
         return -EIO;
     }
-    if (pread_all(s->fd, st->buf, bytes, off)) return -EIO;
-    if (hipMemcpyAsync(dst, st->buf, bytes, hipMemcpyHostToDevice, cs) != hipSuccess) return -EIO;
+    if (read_spans(s, (uint8_t *)st->buf, sp, 3)) return -EIO;
+    if (hipMemcpyAsync(blk, st->buf, len, hipMemcpyHostToDevice, cs) != hipSuccess) return -EIO;
     if (hipEventRecord(st->done, cs) != hipSuccess) return -EIO;
     st->done_set = 1;
     return 0;
@@ -408,11 +633,8 @@ static int page_in(ExpertStore *s, Slot *sl, hipStream_t cs) {
         sl->busy = busy;
         sl->busy_set = 0;
     }
-    const uint64_t offs[3] = {L->gate_off, L->up_off, L->down_off};
-    const uint32_t lens[3] = {L->gate_bytes, L->up_bytes, L->down_bytes};
-    const uint64_t dsts[3] = {og, ou, od};
-    for (int i = 0; i < 3 && !rc; i++)
-        rc = cs ? read_slice_async(s, offs[i], lens[i], blk + dsts[i], cs) : read_slice(s, offs[i], lens[i], blk + dsts[i]);
+    const Span sp[3] = {{L->gate_off, L->gate_bytes, og}, {L->up_off, L->up_bytes, ou}, {L->down_off, L->down_bytes, od}};
+    if (!rc) rc = read_block(s, sp, od + L->down_bytes, blk, cs);
     if (rc) {
         if (cs) (void)hipStreamSynchronize(cs);  /* no copy may still target the block */
         Slot tmp = *sl;
@@ -437,8 +659,10 @@ static int page_in(ExpertStore *s, Slot *sl, hipStream_t cs) {
 static int pool_lookup(ExpertStore *s, Slot *sl, ExpertView *view, hipStream_t cs) {
     s->hbm.requests++;
     if (!sl->registered) { memset(view, 0, sizeof *view); return -1; }
+    const int was = sl->resident;
     if (sl->resident) {
         s->hbm.hits++;
+        if (sl->prefetched) { s->pf_used++; sl->prefetched = 0; }
     } else {
         s->hbm.misses++;
         make_room(s, sl->bytes);
@@ -449,6 +673,7 @@ static int pool_lookup(ExpertStore *s, Slot *sl, ExpertView *view, hipStream_t c
         s->hbm.experts_resident++;
     }
     sl->last_used = ++s->tick;
+    lru_touch(s, sl, 0, was);
     sl->lease++;
     view->gate = sl->gate;
     view->up = sl->up;
@@ -557,16 +782,18 @@ int expert_store_unpin_layer(ExpertStore *s, int layer) {
 void expert_store_destroy(ExpertStore *s) {
     if (!store_ok(s)) return;
     s->magic = 0;
+    readers_stop(s);
     (void)hipDeviceSynchronize();
     for (int l = 0; l < s->n_layers; l++) if (s->tables[l]) (void)hipFree(s->tables[l]);
     for (int i = 0; i < s->n_slots; i++) {
-        if (s->slots[i].dev) (void)hipFree(s->slots[i].dev);
+        if (s->slots[i].dev) block_free(s, s->slots[i].dev);
         if (s->slots[i].busy) (void)hipEventDestroy(s->slots[i].busy);
     }
     for (int i = 0; i < s->nfree; i++) {
-        (void)hipFree(s->freel[i].ptr);
+        block_free(s, s->freel[i].ptr);
         if (s->freel[i].busy) (void)hipEventDestroy(s->freel[i].busy);
     }
+    if (s->arena) (void)hipFree(s->arena);
     for (int i = 0; i < VH_NOTES; i++) {
         if (s->notes[i].host) (void)hipHostFree(s->notes[i].host);
         if (s->notes[i].ev) (void)hipEventDestroy(s->notes[i].ev);
@@ -607,11 +834,7 @@ const void *const *vh_store_layer_table(const ExpertStore *s, int layer) {
  * only then does the MoE path pin whole layers. */
 int vh_store_fits_all(const ExpertStore *s) {
     if (!store_ok(s)) return 0;
-    if (!s->capacity_bytes) return 1;
-    uint64_t all = 0;
-    for (int i = 0; i < s->n_slots; i++)
-        if (s->slots[i].registered) all += s->slots[i].bytes;
-    return all <= s->capacity_bytes;
+    return !s->capacity_bytes || s->registered_bytes <= s->capacity_bytes;
 }
 
 /* Bytes of resident experts that hold a lease (pinned layers, a caller's
@@ -666,6 +889,69 @@ int vh_store_copy_fence(ExpertStore *s, hipStream_t cs, hipStream_t stream) {
     }
     if (hipEventRecord(s->copied, cs) != hipSuccess) return -EIO;
     return hipStreamWaitEvent(stream, s->copied, 0) == hipSuccess ? 0 : -EIO;
+}
+
+/* ------------------------------------------------------------------ prefetch */
+
+/* The experts of `layer` that the next call on it is expected to route to,
+ * most likely first (up to 64; ids not registered are skipped when read). */
+void vh_store_hint(ExpertStore *s, int layer, const int32_t *ids, int n) {
+    if (!store_ok(s)) return;
+    if (n > 64) n = 64;
+    s->hint_layer = n > 0 ? layer : -1;
+    s->hint_n = n > 0 ? n : 0;
+    s->hint_pos = 0;
+    if (n > 0) memcpy(s->hint, ids, (size_t)n * sizeof(int32_t));
+}
+
+/* Read the next hinted expert of `layer` that is not resident into the pool,
+ * without a lease, its copy on cs: 1 after a read, 0 when none is left (or
+ * the hint is for another layer, the store is device-backed, prefetch is off,
+ * or the pool has no room without going over its capacity), < 0 on a failed
+ * read. The pool's requests, hits and misses do not count it; its
+ * bytes_read does, and a later lookup of it counts as a hit. */
+int vh_store_prefetch_next(ExpertStore *s, int layer, hipStream_t cs) {
+    if (!store_ok(s) || s->prefetch_off || s->dev_base || !cs || layer != s->hint_layer) return 0;
+    while (s->hint_pos < s->hint_n) {
+        Slot *sl = slot_at(s, layer, s->hint[s->hint_pos++]);
+        if (!sl || !sl->registered || sl->resident) continue;
+        if (s->capacity_bytes) {
+            make_room(s, sl->bytes);
+            if (s->resident_bytes + sl->bytes > s->capacity_bytes) { s->hint_pos = s->hint_n; return 0; }
+        }
+        const int rc = page_in(s, sl, cs);
+        if (rc) return rc;
+        sl->resident = 1;
+        s->resident_bytes += sl->bytes;
+        s->hbm.experts_resident++;
+        sl->last_used = ++s->tick;
+        lru_touch(s, sl, 0, 0);
+        sl->prefetched = 1;
+        s->pf_issued++;
+        s->pf_bytes += sl->bytes;
+        return 1;
+    }
+    return 0;
+}
+
+/* 1 when paged calls may read hinted experts ahead (a store reading a file
+ * with prefetch on). */
+int vh_store_prefetching(const ExpertStore *s) { return store_ok(s) && !s->dev_base && !s->prefetch_off; }
+
+int expert_store_set_prefetch(ExpertStore *s, int on) {
+    if (!store_ok(s)) return -EINVAL;
+    s->prefetch_off = !on;
+    if (!on) s->hint_layer = -1;
+    return 0;
+}
+
+void expert_store_prefetch_stats(const ExpertStore *s, uint64_t out[3]) {
+    if (!out) return;
+    out[0] = out[1] = out[2] = 0;
+    if (!store_ok(s)) return;
+    out[0] = s->pf_issued;
+    out[1] = s->pf_used;
+    out[2] = s->pf_bytes;
 }
 
 /* The store's own file descriptor, for callers that need to know whether

@@ -67,6 +67,9 @@ struct Ws {
     float *xsc;              // and their per-token scales [T]
     const void **tab;        // paged plan: [E + 1] expert tables [3 E] (one per batch, then the combine's)
     int32_t *act;            // paged plan: [E] active lists [E + 1] (one per batch)
+    int32_t *pidx;           // paged plan: the next layer's guessed routing [T x k]
+    float *pw;               // and its weights (unused)
+    uint32_t *pflags;        // and flags (unused)
 };
 
 // Where a call's workspace comes from: the library's grow-only per-device
@@ -98,6 +101,8 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_xp = small ? take(size_t(T) * d * 4) : 0, o_xsc = small ? take(size_t(T) * 4) : 0;
     const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
     const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
+    const size_t o_pidx = paged ? take(P * 4) : 0, o_pw = paged ? take(P * 4) : 0,
+                 o_pflags = paged ? take(size_t(T) * 4) : 0;
     void *base;
     if (src && src->base) {
         if (off > src->cap) return -E2BIG;
@@ -126,6 +131,9 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->xsc = small ? reinterpret_cast<float *>(b + o_xsc) : nullptr;
     ws->tab = reinterpret_cast<const void **>(b + o_tab);
     ws->act = reinterpret_cast<int32_t *>(b + o_act);
+    ws->pidx = paged ? reinterpret_cast<int32_t *>(b + o_pidx) : nullptr;
+    ws->pw = paged ? reinterpret_cast<float *>(b + o_pw) : nullptr;
+    ws->pflags = paged ? reinterpret_cast<uint32_t *>(b + o_pflags) : nullptr;
     return 0;
 }
 
@@ -428,6 +436,32 @@ extern "C" int moe_dispatch(const int32_t *idx, int n_tokens, int k, int n_exper
 // kernels, and a later page-in into that block waits for it. The combine runs
 // once all batches have written their rows. The stream is synchronized once
 // (the host needs the routing), so such a call cannot be captured in a graph.
+//
+// Prefetch (the reference lists it as open, ROADMAP.md:46-47): a call of at
+// most 8 tokens also applies the next layer's router to this call's hb - the
+// residual stream changes little from one layer to the next - and hands the
+// guessed experts, most likely first, to the store. The next call on that
+// layer reads the guessed experts that are not resident while the device
+// runs the kernels before its routing (the previous layer's experts, this
+// layer's router), and stops as soon as its routing has landed: the host is
+// otherwise idle then. A wrong guess costs pool room and copy bandwidth, never
+// a result; the reference's statistics do not see guesses.
+int paged_events(hipEvent_t **out) {
+    static hipEvent_t ev[64][2];
+    int dev = 0;
+    if (int rc = vh_check(hipGetDevice(&dev))) return rc;
+    if (dev < 0 || dev >= 64) return -ENODEV;
+    for (int i = 0; i < 2; i++)
+        if (!ev[dev][i] && vh_check(hipEventCreateWithFlags(&ev[dev][i], hipEventDisableTiming))) {
+            ev[dev][i] = nullptr;
+            return -EIO;
+        }
+    *out = ev[dev];
+    return 0;
+}
+
+constexpr int kPrefetchIds = 64;  // guessed (token, rank) pairs per call at most
+
 int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, int n_tokens, int32_t *idx_out,
                   float *w_out, hipStream_t s, uint32_t *flags_out) {
     const vireo_moe_layer &L = m->layers[layer];
@@ -450,7 +484,11 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     // and an active list [E + 1], then the combine's table [3 E]
     const size_t tab_n = size_t(3) * E, act_n = size_t(E) + 1;
     const size_t o_idx = al256(size_t(E) * 4), o_tabs = o_idx + al256(size_t(P) * 4),
-                 o_acts = o_tabs + al256(size_t(E + 1) * tab_n * sizeof(void *)), host_bytes = o_acts + size_t(E) * act_n * 4;
+                 o_acts = o_tabs + al256(size_t(E + 1) * tab_n * sizeof(void *)),
+                 o_pred = o_acts + al256(size_t(E) * act_n * 4), host_bytes = o_pred + size_t(P) * 4;
+    const int nl = layer + 1;
+    const bool predict = P <= kPrefetchIds && nl < m->n_layers && vh_store_prefetching(m->es) &&
+                         m->layers[nl].router && m->layers[nl].router->data;
     void *hst = nullptr;
     if (!rc) rc = vh_host_staging(host_bytes, &hst);
     if (rc) return rc;
@@ -459,13 +497,37 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     int32_t *idx_h = reinterpret_cast<int32_t *>(hb8 + o_idx);
     const void **tabs_h = reinterpret_cast<const void **>(hb8 + o_tabs);
     int32_t *acts_h = reinterpret_cast<int32_t *>(hb8 + o_acts);
-    rc = vh_check(hipMemcpyAsync(counts, ws.counts, size_t(E) * 4, hipMemcpyDeviceToHost, s));
+    int32_t *pred_h = reinterpret_cast<int32_t *>(hb8 + o_pred);
+    hipEvent_t *ev = nullptr;
+    rc = paged_events(&ev);
+    if (!rc) rc = vh_check(hipMemcpyAsync(counts, ws.counts, size_t(E) * 4, hipMemcpyDeviceToHost, s));
     if (!rc) rc = vh_check(hipMemcpyAsync(idx_h, idx, size_t(P) * 4, hipMemcpyDeviceToHost, s));
-    if (!rc) rc = vh_check(hipStreamSynchronize(s));
-    if (rc) return rc;
+    if (!rc) rc = vh_check(hipEventRecord(ev[0], s));
+    if (!rc && predict) {  // the next layer's router on this hb: a guess of its routing
+        const vireo_moe_layer &N = m->layers[nl];
+        const float *RN = static_cast<const float *>(N.router->data);
+        rc = vh_route_parts(RN, hb, N.logit_bias, d, E, n_tokens, false, ws.parts, s);
+        if (!rc) rc = vh_route_finish(ws.parts, RN, hb, N.logit_bias, d, E, k, m->topk_renorm, false, n_tokens,
+                                      ws.pidx, ws.pw, ws.pflags, nullptr, s);
+        if (!rc) rc = vh_check(hipMemcpyAsync(pred_h, ws.pidx, size_t(P) * 4, hipMemcpyDeviceToHost, s));
+        if (!rc) rc = vh_check(hipEventRecord(ev[1], s));
+    }
+    hipStream_t cs = nullptr;
+    if (!rc) rc = vh_copy_stream(&cs);
+    // while the routing is on its way: read the experts an earlier call guessed for this layer
+    while (!rc && hipEventQuery(ev[0]) == hipErrorNotReady) {
+        const int r = vh_store_prefetch_next(m->es, layer, cs);
+        if (r < 0) rc = r;
+        if (r <= 0) break;
+    }
+    (void)hipGetLastError();  // a query that found the copy not done yet is no error
+    if (!rc) rc = vh_check(hipEventSynchronize(ev[0]));
+    if (rc) {
+        (void)hipStreamSynchronize(s);  // no copy may still target the host staging
+        (void)vh_host_staging_done(s);
+        return rc;
+    }
     vh_store_note_routing_host(m->es, layer, idx_h, n_tokens, k);
-    hipStream_t cs;
-    if ((rc = vh_copy_stream(&cs))) return rc;
     const uint64_t cap = vh_store_capacity(m->es), leased = vh_store_leased_bytes(m->es);
     const uint64_t room = cap > leased ? cap - leased : 1;  // cap 0: unbounded (room unused)
     const bool mdec = n_tokens < kMfmaMinCall && g_path != 4 && vh_mdec_supported(tg, td, d, fe);
@@ -535,6 +597,13 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     const void **dt = ws.tab + size_t(nb) * tab_n;
     if (!rc) rc = vh_check(hipMemcpyAsync(dt, present, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
     if (!rc) rc = vh_combine(idx, w, dt, ws.ybuf, d, k, n_tokens, x, s);
+    if (!rc && predict) {  // hand the guess to the store, every token's first choice first
+        rc = vh_check(hipEventSynchronize(ev[1]));
+        int32_t hint[kPrefetchIds];
+        for (int j = 0; j < k; j++)
+            for (int t = 0; t < n_tokens; t++) hint[j * n_tokens + t] = pred_h[t * k + j];
+        if (!rc) vh_store_hint(m->es, nl, hint, P);
+    }
     const int hr = vh_host_staging_done(s);
     return rc ? rc : hr;
 }

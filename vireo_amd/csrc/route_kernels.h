@@ -33,6 +33,9 @@ uint64_t vh_store_leased_bytes(const ExpertStore *s);
 int vh_store_acquire(ExpertStore *s, int layer, int expert, ExpertView *view, hipStream_t cs);
 int vh_store_drop(ExpertStore *s, ExpertView *view, hipStream_t stream);
 int vh_store_copy_fence(ExpertStore *s, hipStream_t cs, hipStream_t stream);
+void vh_store_hint(ExpertStore *s, int layer, const int32_t *ids, int n);
+int vh_store_prefetch_next(ExpertStore *s, int layer, hipStream_t cs);
+int vh_store_prefetching(const ExpertStore *s);
 int vh_store_note_routing(ExpertStore *s, int layer, const int32_t *idx_dev, int T, int k, hipStream_t stream);
 void vh_store_note_routing_host(ExpertStore *s, int layer, const int32_t *idx, int T, int k);
 }

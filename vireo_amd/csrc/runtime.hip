@@ -19,10 +19,13 @@ struct DevState {
     size_t red_bytes = 0;
     int cus = 0;
     hipStream_t copy = nullptr;   // expert page-in copies
-    void *host = nullptr;         // pinned staging for small uploads
-    size_t host_bytes = 0;
-    hipEvent_t host_done = nullptr;
-    bool host_done_set = false;
+    // pinned staging for small per-call transfers: two buffers used in turn
+    void *host[2] = {nullptr, nullptr};
+    size_t host_bytes[2] = {0, 0};
+    hipEvent_t host_done[2] = {nullptr, nullptr};
+    bool host_done_set[2] = {false, false};
+    int host_next = 0;            // the buffer the next call takes
+    int host_cur = 0;             // the buffer the current call took
     uint32_t *status = nullptr;   // sticky device status bits (VIREO_DECODE_TIMEOUT)
     LayerXchg *xchg = nullptr;    // the layer kernel's exchange area (zeroed once)
 };
@@ -138,19 +141,22 @@ int vh_host_staging(size_t bytes, void **out) {
     int d = cur_dev();
     if (d < 0) return -ENODEV;
     DevState &st = g_dev[d];
-    if (st.host_done_set) {
-        if (int rc = vh_check(hipEventSynchronize(st.host_done))) return rc;
-        st.host_done_set = false;
+    const int i = st.host_next;
+    if (st.host_done_set[i]) {
+        if (int rc = vh_check(hipEventSynchronize(st.host_done[i]))) return rc;
+        st.host_done_set[i] = false;
     }
-    if (bytes > st.host_bytes) {  // nothing reads the old buffer any more (waited above)
-        if (st.host) (void)hipHostFree(st.host);
-        st.host = nullptr;
-        st.host_bytes = 0;
+    if (bytes > st.host_bytes[i]) {  // nothing reads the old buffer any more (waited above)
+        if (st.host[i]) (void)hipHostFree(st.host[i]);
+        st.host[i] = nullptr;
+        st.host_bytes[i] = 0;
         const size_t nb = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : 2 * bytes;
-        if (vh_check(hipHostMalloc(&st.host, nb, 0))) { st.host = nullptr; return -ENOMEM; }
-        st.host_bytes = nb;
+        if (vh_check(hipHostMalloc(&st.host[i], nb, 0))) { st.host[i] = nullptr; return -ENOMEM; }
+        st.host_bytes[i] = nb;
     }
-    *out = st.host;
+    st.host_cur = i;
+    st.host_next = i ^ 1;
+    *out = st.host[i];
     return 0;
 }
 
@@ -158,12 +164,13 @@ int vh_host_staging_done(hipStream_t s) {
     int d = cur_dev();
     if (d < 0) return -ENODEV;
     DevState &st = g_dev[d];
-    if (!st.host_done && vh_check(hipEventCreateWithFlags(&st.host_done, hipEventDisableTiming))) {
-        st.host_done = nullptr;
+    const int i = st.host_cur;
+    if (!st.host_done[i] && vh_check(hipEventCreateWithFlags(&st.host_done[i], hipEventDisableTiming))) {
+        st.host_done[i] = nullptr;
         return -EIO;
     }
-    if (int rc = vh_check(hipEventRecord(st.host_done, s))) return rc;
-    st.host_done_set = true;
+    if (int rc = vh_check(hipEventRecord(st.host_done[i], s))) return rc;
+    st.host_done_set[i] = true;
     return 0;
 }
 

@@ -59,7 +59,8 @@ class GGUFWriter:
         """dims in GGUF order: dims[0] is the row length."""
         self.tensors.append((name, list(dims), ggml_type, np.ascontiguousarray(data).view(np.uint8).reshape(-1)))
 
-    def write(self, path):
+    def write(self, path, progress=None):
+        """progress (optional): called with a message every 64 tensors written."""
         a = self.alignment
         head = [b"GGUF", struct.pack("<IQQ", 3, len(self.tensors), len(self.kv))]
         for key, vtype, value, arr_type in self.kv:
@@ -75,9 +76,11 @@ class GGUFWriter:
         with open(path, "wb") as f:
             f.write(blob)
             f.write(b"\0" * ((a - len(blob) % a) % a))
-            for (_, _, _, data), o in zip(self.tensors, offsets):
-                f.write(data.tobytes())
+            for i, ((_, _, _, data), o) in enumerate(zip(self.tensors, offsets)):
+                f.write(memoryview(data))
                 f.write(b"\0" * ((a - len(data) % a) % a))
+                if progress and i % 64 == 63:
+                    progress(f"{i + 1} of {len(self.tensors)} tensors written")
 
 
 def moe_arch(shape):
@@ -87,10 +90,13 @@ def moe_arch(shape):
 
 
 def write_moe_gguf(path, shape, n_layers, seed, vocab=0, untied=False, norms=True, alignment=32, arch=None,
-                   lm_type=W.Q8_0):
+                   lm_type=W.Q8_0, progress=None, layer_bytes=None):
     """Write a synthetic MoE GGUF file; returns the host arrays written, for
     checking (routers [L][E x d], experts [L] (gate_all, up_all, down_all),
-    ffn_norm [L][d] or None, and with vocab: out_norm, token_embd, output)."""
+    ffn_norm [L][d] or None, and with vocab: out_norm, token_embd, output).
+    progress (optional): called with a message as layers are made and written.
+    layer_bytes (optional): layer -> (gate_all, up_all, down_all), the same
+    bytes as workloads.host_layer (e.g. copied from a device-made layer)."""
     d, E, fe = shape.d, shape.E, shape.fe
     arch = arch or moe_arch(shape)
     w = GGUFWriter(alignment)
@@ -109,13 +115,15 @@ def write_moe_gguf(path, shape, n_layers, seed, vocab=0, untied=False, norms=Tru
     out = {"routers": [], "experts": [], "ffn_norm": [] if norms else None}
     for l in range(n_layers):
         r = W.host_router(shape, l, seed)
-        g, u, dn = W.host_layer(shape, l, seed)
+        g, u, dn = layer_bytes(l) if layer_bytes else W.host_layer(shape, l, seed)
         w.add_tensor(f"blk.{l}.ffn_gate_inp.weight", [d, E], W.F32, r)
         w.add_tensor(f"blk.{l}.ffn_gate_exps.weight", [d, fe, E], shape.gate_type, g)
         w.add_tensor(f"blk.{l}.ffn_up_exps.weight", [d, fe, E], shape.up_type, u)
         w.add_tensor(f"blk.{l}.ffn_down_exps.weight", [fe, d, E], shape.down_type, dn)
         out["routers"].append(r)
         out["experts"].append((g, u, dn))
+        if progress and l % 8 == 7:
+            progress(f"{l + 1} of {n_layers} layers made")
         if norms:
             nw = (1.0 + 0.25 * W.host_normal(d, seed, W.stream_id(l, 15))).astype(np.float32)
             w.add_tensor(f"blk.{l}.ffn_norm.weight", [d], W.F32, nw)
@@ -130,7 +138,7 @@ def write_moe_gguf(path, shape, n_layers, seed, vocab=0, untied=False, norms=Tru
             head = W.host_matrix(lm_type, d, 0, vocab, seed + 1, W.stream_id(0, W.KIND_LM_HEAD))
             w.add_tensor("output.weight", [d, vocab], lm_type, head)
             out["output"] = head
-    w.write(path)
+    w.write(path, progress)
     return out
 
 
@@ -190,6 +198,17 @@ class GGUFModel:
         st = _lib.ExpertStats()
         self.lib.expert_store_hbm_stats(self.p.contents.model.es, C.byref(st))
         return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
+
+    def set_prefetch(self, on):
+        """Let paged calls read guessed next-layer experts ahead (expert_store_set_prefetch)."""
+        _lib.check(self.lib.expert_store_set_prefetch(self.p.contents.model.es, int(bool(on))),
+                   "expert_store_set_prefetch")
+
+    def prefetch_stats(self):
+        """Experts read ahead, those of them looked up before eviction, bytes read ahead."""
+        out = (C.c_uint64 * 3)()
+        self.lib.expert_store_prefetch_stats(self.p.contents.model.es, out)
+        return {"issued": out[0], "used": out[1], "bytes": out[2]}
 
     def close(self):
         if getattr(self, "p", None):
