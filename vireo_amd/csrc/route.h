@@ -196,7 +196,22 @@ struct TopKSmem {
     float s, p_next;                 // exact path: the softmax's sum, the best probability left out
     uint32_t flag;
     int uncertain;
+    // the contenders' exact logits (route_topk_block's first fallback)
+    int cand[64], corder[64];
+    float cl[64];
+    double cut;
+    int ncand, near;
 };
+
+// Fp32 spacing at |v| (the distance to the next float away from zero).
+VH_DEV float ulp_f(float v) {
+    const float a = fabsf(v);
+    return __uint_as_float(__float_as_uint(a) + 1u) - a;
+}
+
+// Margin below the chosen experts' lowest lower bound within which an expert
+// still contends for the top k when the ranking is not certified.
+constexpr double kContend = 1e-4;
 
 // Logit span of a certified top k: the k-th chosen expert's logit lies within
 // kRouteSpan of the largest. The reference ranks probabilities
@@ -213,7 +228,8 @@ constexpr double kRouteSpan = 30.0;
 // of one parallel pass. The ranking is certified with the fp64 intervals:
 // every gap that decides the set or its order wider than both bounds plus
 // kRouteMargin, and the chosen within kRouteSpan of the top. Otherwise the
-// reference's softmax is formed exactly - every logit in-order fp32 (or
+// contenders' exact logits decide (see below) or, when they are too close,
+// the reference's softmax is formed exactly - every logit in-order fp32 (or
 // exact_parts: the parts hold them, beta = 0), m, expf(l - m), their in-order
 // fp32 sum s and p = e / s (src/gguf_run.c:180-182) - and the experts are
 // ranked on p with the lowest id winning a tie (:189-191); the weights are
@@ -270,7 +286,76 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
         if (!(sm.sel_lo[tid] > sm.sel_hi[0] - kRouteSpan)) atomicOr(&sm.uncertain, 1);
     }
     __syncthreads();
-    if (sm.uncertain) {
+    // Not certified: first the exact in-order logits of the contenders only -
+    // the k experts ranked first and every expert whose upper bound reaches
+    // the lowest of their lower bounds less kContend (any other expert's
+    // exact logit lies more than kContend below each of those k, so the
+    // reference's top k is among the contenders). Ranked on those logits
+    // (lowest id first on equal ones), the result is the reference's ranking
+    // when every decision down to the k-th place is a gap wider than 2 ulp of
+    // the larger |l - m| plus 1e-6: then the reference's rounded l - m,
+    // its expf and the division by the common sum keep the order strictly, so
+    // the probabilities rank the same and no tie rule applies. Otherwise (or
+    // with more than 64 contenders) the whole softmax is formed exactly below.
+    bool full = sm.uncertain != 0, resolved = false;
+    if (full && !exact_parts) {
+        if (tid == 0) {
+            double L = sm.sel_lo[0];
+            for (int t = 1; t < k; t++) L = fmin(L, sm.sel_lo[t]);
+            sm.cut = L - kContend;
+            sm.ncand = 0;
+            sm.near = 0;
+        }
+        __syncthreads();
+        if (mine && (rank < k || hi >= sm.cut)) {
+            const int j = atomicAdd(&sm.ncand, 1);
+            if (j < 64) sm.cand[j] = tid;
+        }
+        __syncthreads();
+        const int n = sm.ncand;
+        if (n <= 64) {
+            if (wv == 0 && lane < n) {
+                const int e = sm.cand[lane];
+                float a = exact_logit(R + size_t(e) * d, x, d);
+                if (bias) a = add_rn(a, bias[e]);
+                sm.cl[lane] = a;
+            }
+            __syncthreads();
+            if (tid < n) {
+                const float a = sm.cl[tid];
+                const int e = sm.cand[tid];
+                int r = 0;
+                for (int i = 0; i < n; i++) {
+                    const float b = sm.cl[i];
+                    r += int(b > a || (b == a && sm.cand[i] < e));
+                }
+                sm.corder[r] = tid;
+            }
+            __syncthreads();
+            if (tid < k) {
+                // place tid against place tid + 1 (the best contender left
+                // out, or below the cut everything outside the contenders)
+                const float m = sm.cl[sm.corder[0]], a = sm.cl[sm.corder[tid]];
+                const float b = tid + 1 < n ? sm.cl[sm.corder[tid + 1]] : float(sm.cut);
+                const float span = fmaxf(fabsf(sub_rn(a, m)), fabsf(sub_rn(b, m)));
+                const double gap = tid + 1 < n ? double(a) - double(b) : double(a) - sm.cut;
+                if (!(gap > 2.0 * double(ulp_f(span)) + 1e-6)) atomicOr(&sm.near, 1);
+                if (tid == k - 1) {  // the experts outside the contenders lie below the cut
+                    const float sc = fabsf(sub_rn(float(sm.cut), m));
+                    if (!(kContend > 2.0 * double(ulp_f(sc)) + 1e-6)) atomicOr(&sm.near, 1);
+                }
+            }
+            __syncthreads();
+            if (!sm.near) {
+                full = false;
+                resolved = true;
+                if (tid < k) sm.sel[tid] = sm.cand[sm.corder[tid]];
+                if (tid == 0) sm.flag = VIREO_ROUTE_EXACT_FALLBACK;
+                __syncthreads();
+            }
+        }
+    }
+    if (full) {
         // the reference's softmax, exactly: every logit, their maximum, the
         // exponentials, their in-order sum (one thread), the probabilities
         if (mine && !exact_parts) {
@@ -320,7 +405,9 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
         }
         __syncthreads();
     } else {
-        // softmax over all experts (src/gguf_run.c:181-182) on the certified logits
+        // softmax over all experts (src/gguf_run.c:181-182) on the certified
+        // logits (also for a ranking the contenders' exact logits resolved:
+        // only the order had to be exact)
         const float ex = mine ? expf(lg - sm.m) : 0.0f;
         const float part_sum = wave_sum_f(ex);
         if (lane == 0) sm.red[1][wv] = part_sum;
@@ -329,8 +416,9 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
         for (int i = 1; i < nwaves; i++) s += sm.red[1][i];
         if (mine) {
             if (probs) probs[tid] = ex / s;
-            if (rank < k) sm.sel_w[rank] = ex / s;
+            if (!resolved && rank < k) sm.sel_w[rank] = ex / s;
         }
+        if (resolved && tid < k) sm.sel_w[tid] = expf(float(part[sm.sel[tid]].c) - sm.m) / s;
         __syncthreads();
     }
     if (tid == 0 && renorm) {
