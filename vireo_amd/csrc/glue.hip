@@ -164,16 +164,19 @@ extern "C" int moe_stack_step_trace(const vireo_moe_stack *st, int32_t *token, f
 }
 
 // One row of the reference's RMSNorm, bit for bit (its in-order fp32 sum of
-// squares: one thread adds them, the rest of the row is parallel).
+// squares: one thread adds them from LDS, the rest of the row is parallel).
+constexpr int kRmsRefMaxLds = 16384;  // floats of squares kept in LDS (longer rows use the output row)
 __global__ void __launch_bounds__(256) rmsnorm_ref_kernel(float *__restrict__ o, const float *__restrict__ x,
                                                           const float *__restrict__ w, int n, float eps) {
+    extern __shared__ float4 sq4[];
     __shared__ float red;
-    reference_rmsnorm_block(o, x, w, eps, n, &red);
+    reference_rmsnorm_block(o, x, w, eps, n, &red, n <= kRmsRefMaxLds ? reinterpret_cast<float *>(sq4) : nullptr);
 }
 
 int vh_rmsnorm_ref(float *o, const float *x, const float *w, int n, float eps, hipStream_t s) {
     if (n <= 0 || !o || !x || o == x) return -EINVAL;
-    hipLaunchKernelGGL(rmsnorm_ref_kernel, dim3(1), dim3(256), 0, s, o, x, w, n, eps);
+    const size_t lds = n <= kRmsRefMaxLds ? size_t(n + 3) / 4 * 16 : 0;
+    hipLaunchKernelGGL(rmsnorm_ref_kernel, dim3(1), dim3(256), lds, s, o, x, w, n, eps);
     return vh_check(hipGetLastError());
 }
 

@@ -92,12 +92,21 @@ VH_DEV RoutePart route_part_on_own_norm(RoutePart p, double abs_products, int n,
 // r = 1/sqrtf(ss/n + eps), then (x_i r) w_i. dst: d floats (LDS or global),
 // red: one float of LDS. All threads of the workgroup call it.
 VH_DEV void reference_rmsnorm_block(float *dst, const float *__restrict__ x, const float *__restrict__ nw, float eps,
-                                    int d, float *red) {
-    for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = mul_rn(x[i], x[i]);
+                                    int d, float *red, float *sq = nullptr) {
+    // the squares go to sq (LDS, when the caller has it; else dst), and one
+    // thread adds them in order, four per 16-byte read where aligned
+    float *q = sq ? sq : dst;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) q[i] = mul_rn(x[i], x[i]);
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
-        for (int i = 0; i < d; i++) ss = add_rn(ss, dst[i]);
+        int i = 0;
+        if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0)
+            for (; i + 4 <= d; i += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(q + i);
+                ss = add_rn(add_rn(add_rn(add_rn(ss, v.x), v.y), v.z), v.w);
+            }
+        for (; i < d; i++) ss = add_rn(ss, q[i]);
         *red = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(d)), eps)));
     }
     __syncthreads();
