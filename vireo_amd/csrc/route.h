@@ -86,28 +86,53 @@ VH_DEV RoutePart route_part_on_own_norm(RoutePart p, double abs_products, int n,
     return p;
 }
 
+// The in-order fp32 sum of q[0 .. d) by one thread (the reference's
+// sequence of roundings), 16 values per step with the next 16 read while
+// these are added.
+VH_DEV float inorder_sum(const float *q, int d) {
+    float ss = 0.0f;
+    int i = 0;
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && d >= 16) {
+        const float4 *q4 = reinterpret_cast<const float4 *>(q);
+        float4 c0 = q4[0], c1 = q4[1], c2 = q4[2], c3 = q4[3];
+        for (; i + 32 <= d; i += 16) {
+            const int j = (i >> 2) + 4;
+            const float4 n0 = q4[j], n1 = q4[j + 1], n2 = q4[j + 2], n3 = q4[j + 3];
+            ss = add_rn(add_rn(add_rn(add_rn(ss, c0.x), c0.y), c0.z), c0.w);
+            ss = add_rn(add_rn(add_rn(add_rn(ss, c1.x), c1.y), c1.z), c1.w);
+            ss = add_rn(add_rn(add_rn(add_rn(ss, c2.x), c2.y), c2.z), c2.w);
+            ss = add_rn(add_rn(add_rn(add_rn(ss, c3.x), c3.y), c3.z), c3.w);
+            c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        }
+        ss = add_rn(add_rn(add_rn(add_rn(ss, c0.x), c0.y), c0.z), c0.w);
+        ss = add_rn(add_rn(add_rn(add_rn(ss, c1.x), c1.y), c1.z), c1.w);
+        ss = add_rn(add_rn(add_rn(add_rn(ss, c2.x), c2.y), c2.z), c2.w);
+        ss = add_rn(add_rn(add_rn(add_rn(ss, c3.x), c3.y), c3.z), c3.w);
+        i += 16;
+    }
+    for (; i < d; i++) ss = add_rn(ss, q[i]);
+    return ss;
+}
+
 // The reference's RMSNorm of x (src/gguf_run.c:161-165) into dst[0..d) by a
 // whole workgroup, bit for bit: the squares in parallel, their in-order fp32
 // sum by one thread (d dependent adds: used only where exactness needs it),
 // r = 1/sqrtf(ss/n + eps), then (x_i r) w_i. dst: d floats (LDS or global),
-// red: one float of LDS. All threads of the workgroup call it.
+// red: one float of LDS; sq (optional): d floats of LDS for the squares
+// (each branch keeps its pointer's own address space, so the sum reads LDS
+// with LDS loads), else they go to dst. All threads of the workgroup call it.
 VH_DEV void reference_rmsnorm_block(float *dst, const float *__restrict__ x, const float *__restrict__ nw, float eps,
                                     int d, float *red, float *sq = nullptr) {
-    // the squares go to sq (LDS, when the caller has it; else dst), and one
-    // thread adds them in order, four per 16-byte read where aligned
-    float *q = sq ? sq : dst;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) q[i] = mul_rn(x[i], x[i]);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float ss = 0.0f;
-        int i = 0;
-        if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0)
-            for (; i + 4 <= d; i += 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(q + i);
-                ss = add_rn(add_rn(add_rn(add_rn(ss, v.x), v.y), v.z), v.w);
-            }
-        for (; i < d; i++) ss = add_rn(ss, q[i]);
-        *red = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(d)), eps)));
+    if (sq) {
+        for (int i = threadIdx.x; i < d; i += blockDim.x) sq[i] = mul_rn(x[i], x[i]);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            *red = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(inorder_sum(sq, d), float(d)), eps)));
+    } else {
+        for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = mul_rn(x[i], x[i]);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            *red = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(inorder_sum(dst, d), float(d)), eps)));
     }
     __syncthreads();
     const float r = *red;
