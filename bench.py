@@ -40,6 +40,10 @@ import time
 import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
+# the CPUs this process may use, read before any OpenMP runtime starts: with
+# OMP_PROC_BIND set, loading one (torch does) binds the calling thread to a
+# single core, and its affinity then names that core alone
+START_CPUS = frozenset(os.sched_getaffinity(0))
 sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer decode tok/s + achieved HBM GB/s (% of peak); prefill tok/s"
@@ -150,7 +154,7 @@ def host_cpu():
                     smt = max(1, int(cur["siblings"]) // int(cur["cpu cores"]))
     except (OSError, ValueError):
         pass
-    allowed = os.sched_getaffinity(0)
+    allowed = START_CPUS
     phys = len({cores[c] for c in allowed if c in cores})
     # a virtualised /proc/cpuinfo may give every CPU the same core id: then
     # count the CPUs available divided by the hardware threads per core
@@ -701,6 +705,15 @@ LAYER_KERNELS = {
 }
 
 
+def kernel_short_name(name):
+    """A kernel's bare name out of a profiler's demangled signature:
+    "void (anonymous namespace)::foo_kernel<8, 1>(int, ...)" -> "foo_kernel"."""
+    n = name.replace("(anonymous namespace)::", "").strip()
+    if n.startswith("void "):
+        n = n[5:]
+    return n.split("(")[0].split("<")[0].split("::")[-1].strip()
+
+
 def _counter_medians(d, counter):
     """Median per dispatch of `counter` (KiB) for every kernel name in the
     rocprofv3 CSV files under directory d."""
@@ -732,7 +745,7 @@ def traffic_report(args):
     prefixes = LAYER_KERNELS["decode"]
     per_kernel, total = {}, 0.0
     for name in sorted(fetch):
-        short = name.split("(")[0].split("<")[0].replace("void ", "").split("::")[-1].strip()
+        short = kernel_short_name(name)
         if not any(short.startswith(p) for p in prefixes):
             continue
         fk, n = fetch[name]
@@ -741,10 +754,17 @@ def traffic_report(args):
         per_kernel[name] = {"fetch_kib_median": round(fk, 1), "write_kib_median": round(wk, 1), "dispatches": n,
                             "hbm_bytes": int(b)}
         total += b
+    run = f"python3 <repo>/bench.py --workload {args.workload} --no-cpu --steps 96"
+    copy = "python3 <repo>/bench.py --workload copy-512MiB --steps 3"
     out = {"workload": args.workload, "hbm_bytes_per_layer": int(total), "kernels": per_kernel,
            "calibration": {"copy_kib": copy_kib, "fetch_kib": round(cf, 1), "write_kib": round(cw, 1),
                            "fetch_factor": round(f_factor, 4), "write_factor": round(w_factor, 4)},
-           "dirs": list(args.traffic)}
+           "commands": [f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc {c} --output-format csv "
+                        f"-d <out>/{d} -o run -- {cmd}"
+                        for c, d, cmd in (("FETCH_SIZE", "fetch", run), ("WRITE_SIZE", "write", run),
+                                          ("FETCH_SIZE", "copy_fetch", copy), ("WRITE_SIZE", "copy_write", copy))]
+                       + [f"python3 <repo>/bench.py --workload {args.workload} --traffic <out>/fetch <out>/write "
+                          "<out>/copy_fetch <out>/copy_write"]}
     path = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
