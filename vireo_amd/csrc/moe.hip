@@ -10,9 +10,11 @@
 // The grouped plan reads each routed expert's weights once per call however
 // many tokens chose it. In calls of at least kMfmaMinCall tokens every group
 // runs as bf16 matrix-core GEMMs (moe_mfma.hip; 4 more kernels); calls of
-// fewer tokens run their groups on moe_gdec.hip's kernels, which keep a
-// group's inputs in registers and stream each weight row once, and plan 4
-// runs every call on the fp32 grouped kernels (moe_grouped.hip).
+// kMdecMinTokens to kMfmaMinCall - 1 tokens with Q4_K_M experts run their
+// groups on the matrix cores with exact 16-bit operands (moe_mdec.hip), and
+// smaller calls (or other types) on moe_gdec.hip's kernels, which keep a
+// group's inputs in registers and stream each weight row once; plan 4 runs
+// every call on the fp32 grouped kernels (moe_grouped.hip).
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 #include <string.h>
@@ -32,6 +34,13 @@ int g_path = 0;
 // needed for the few tokens whose order the bounds leave open; a token's
 // result does not depend on the other tokens of its call either way.
 constexpr int kExactRouteTokens = 64;
+// From this many tokens on, a decode-batch call's groups run on the matrix
+// cores (moe_mdec.hip): a tile takes 16 tokens of an expert, and below 8
+// tokens per call (about one token per routed expert) converting each weight
+// for the fp32 kernels costs less than the tile's unused rows. Measured per
+// layer (matrix cores / fp32): OLMoE Q4_K_M B=6 92.2 / 89.9 us, B=8 96.9 /
+// 120.2; Qwen3 Q4_K_M B=4 67.7 / 59.4, B=8 94.0 / 104.8.
+constexpr int kMdecMinTokens = 8;
 
 bool type_ok(uint32_t t, int n) {
     switch (t) {  // the expert formats of the MoE models: Q8_0, Q4_K (gate/up), Q6_K (down)
@@ -530,7 +539,8 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     vh_store_note_routing_host(m->es, layer, idx_h, n_tokens, k);
     const uint64_t cap = vh_store_capacity(m->es), leased = vh_store_leased_bytes(m->es);
     const uint64_t room = cap > leased ? cap - leased : 1;  // cap 0: unbounded (room unused)
-    const bool mdec = n_tokens < kMfmaMinCall && g_path != 4 && vh_mdec_supported(tg, td, d, fe);
+    const bool mdec = n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
+                      vh_mdec_supported(tg, td, d, fe);
     const bool gdec = !mdec && n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
     if (mdec) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
     const void **present = tabs_h + size_t(E) * tab_n;  // the combine's table (the last one)
@@ -676,7 +686,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
-    } else if (n_tokens < kMfmaMinCall && g_path != 4 && vh_mdec_supported(tg, td, d, fe)) {
+    } else if (n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
+               vh_mdec_supported(tg, td, d, fe)) {
         // calls of a decode batch's size, Q4_K_M experts: the matrix cores
         if (!rc) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
         if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, d, fe, k, E, slots,
