@@ -128,6 +128,17 @@ VH_DEV uint32_t dpp_u(uint32_t v) {
 // A workgroup barrier that orders LDS only: it waits for this wave's LDS
 // operations, not for its global loads in flight (__syncthreads waits for
 // those too), so loads issued before it keep streaming across it.
+// s_waitcnt for vmcnt <= n, the other counters left as they are (gfx9 encoding)
+#define VH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+// A workgroup barrier that waits for nothing itself. The fence of
+// __syncthreads (and of a local-only fence) makes the compiler drain every
+// direct-to-LDS load first, prefetches included; callers of this one have
+// waited for the loads the next step reads (VH_WAIT_VMCNT) and consumed the
+// LDS values read before it. The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+VH_DEV void dma_barrier() { asm volatile("s_barrier" ::: "memory"); }
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gvoid;
 VH_DEV void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();

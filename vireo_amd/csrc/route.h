@@ -98,6 +98,9 @@ VH_DEV float inorder_sum(const float *q, int d) {
         for (; i + 32 <= d; i += 16) {
             const int j = (i >> 2) + 4;
             const float4 n0 = q4[j], n1 = q4[j + 1], n2 = q4[j + 2], n3 = q4[j + 3];
+            // the reads stay ahead of the adds: memory operations do not cross
+            // this asm, and the chain passes through it (the compiler would sink them)
+            asm volatile("" : "+v"(ss)::"memory");
             ss = add_rn(add_rn(add_rn(add_rn(ss, c0.x), c0.y), c0.z), c0.w);
             ss = add_rn(add_rn(add_rn(add_rn(ss, c1.x), c1.y), c1.z), c1.w);
             ss = add_rn(add_rn(add_rn(add_rn(ss, c2.x), c2.y), c2.z), c2.w);
@@ -218,6 +221,83 @@ VH_DEV uint32_t ordered_u32(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// The contenders' exact logits with their router rows streamed through LDS:
+// wave 1 copies chunks of 256 columns of up to kStageRows rows by direct
+// global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the
+// wave-uniform base + 16 i) into three buffers, two chunks ahead of the
+// chains, and lane c (< n) of wave 0 runs contender c's chain
+// a = fl(a + fl(r_i x_i)), i = 0 .. d-1, in order, exactly as exact_logit
+// does, reading its row and the inputs (already in LDS: xs) four at a time.
+// Rows are 16 bytes apart beyond their 1 KB, so the chains' reads of one
+// column group fall in different banks. Every chunk issues kStageRows loads
+// (rows past n repeat contender 0 into their own slots), so an explicit
+// vmcnt wait leaves the two later chunks in flight; the barriers are bare
+// s_barriers for the same reason. Needs d % 256 == 0, n <= kStageRows, R
+// 16-byte aligned and at least two waves; every thread calls it. Returns lane
+// c's logit on wave 0 (without the bias), 0 elsewhere.
+constexpr int kStageRows = 16, kStageRowF4 = 65;  // a row chunk is 64 float4s, plus one of padding
+constexpr int kStageBufF4 = kStageRows * kStageRowF4;
+constexpr int kStageScrF4 = 3 * kStageBufF4;  // 49 920 bytes of LDS
+VH_DEV bool exact_staged_ok(const float *R, int d, int n) {
+    return n <= kStageRows && d % 256 == 0 && (reinterpret_cast<uintptr_t>(R) & 15u) == 0 && blockDim.x >= 128;
+}
+VH_DEV float exact_logits_staged(const float *__restrict__ R, const float *xs, int d, const int *cand, int n,
+                                 float4 *scr) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nch = d / 256;
+    auto issue = [&](int buf, int c) {  // wave 1: chunk c of every row into buffer buf
+        const float *src = R + 256 * c + 4 * lane;
+#pragma unroll
+        for (int j = 0; j < kStageRows; j++) {
+            const int e = cand[j < n ? j : 0];
+            __builtin_amdgcn_global_load_lds((gvoid *)(src + size_t(e) * d),
+                                             (lds_void *)(scr + buf * kStageBufF4 + j * kStageRowF4), 16, 0, 0);
+        }
+    };
+    if (wv == 1) {
+        issue(0, 0);
+        issue(1, min(1, nch - 1));
+    }
+    float a = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        if (wv == 1) {
+            issue((c + 2) % 3, min(c + 2, nch - 1));  // past the last chunk: the last again, into a spent buffer
+            VH_WAIT_VMCNT(2 * kStageRows);             // chunk c has landed; c + 1 and c + 2 stay in flight
+        }
+        dma_barrier();
+        if (wv == 0 && lane < n) {
+            // 16 columns per step, the next 16 read before these are added
+            const float4 *row = scr + (c % 3) * kStageBufF4 + lane * kStageRowF4;
+            const float4 *x4 = reinterpret_cast<const float4 *>(xs + 256 * c);
+            float4 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3];
+            float4 x0 = x4[0], x1 = x4[1], x2 = x4[2], x3 = x4[3];
+            auto step = [&](const float4 &r, const float4 &xv) {
+                a = add_rn(a, mul_rn(r.x, xv.x));
+                a = add_rn(a, mul_rn(r.y, xv.y));
+                a = add_rn(a, mul_rn(r.z, xv.z));
+                a = add_rn(a, mul_rn(r.w, xv.w));
+            };
+            for (int c4 = 0; c4 < 64; c4 += 4) {
+                const int nx = c4 + 4 < 64 ? c4 + 4 : c4;
+                const float4 q0 = row[nx], q1 = row[nx + 1], q2 = row[nx + 2], q3 = row[nx + 3];
+                const float4 y0 = x4[nx], y1 = x4[nx + 1], y2 = x4[nx + 2], y3 = x4[nx + 3];
+                asm volatile("" : "+v"(a)::"memory");  // the reads stay ahead of the chain
+                step(r0, x0);
+                step(r1, x1);
+                step(r2, x2);
+                step(r3, x3);
+                r0 = q0; r1 = q1; r2 = q2; r3 = q3;
+                x0 = y0; x1 = y1; x2 = y2; x3 = y3;
+            }
+        }
+        dma_barrier();  // buffer c % 3 is read before chunk c + 3 goes into it
+    }
+    if (wv == 1) VH_WAIT_VMCNT(0);  // no load may land after the buffers are given back
+    dma_barrier();
+    return a;
+}
+
+constexpr int kXScrFloats = 2048;  // inputs route_topk_block can copy into its caller's x_scr
+
 // Workspace of route_topk_block (LDS).
 struct TopKSmem {
     uint32_t key[kMaxExperts];       // 32-bit rank keys; then the exact path's exponentials
@@ -272,10 +352,13 @@ constexpr double kRouteSpan = 30.0;
 // probability equal to the next one, or exact logits closer than kNearTie, is
 // reported (VIREO_ROUTE_NEAR_TIE). On return (after a barrier) sm.sel /
 // sm.sel_w / sm.flag hold the result; probs (optional, [E]) receives the
-// softmax.
+// softmax. stage_scr (kStageScrF4 float4s) and x_scr (kXScrFloats floats), both
+// LDS and optional, let the contenders' chains read their rows and inputs
+// from LDS (exact_logits_staged).
 VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, const float *__restrict__ R,
                              const float *__restrict__ x, const float *__restrict__ bias, int d, int E, int k,
-                             int renorm, bool exact_parts, float *__restrict__ probs) {
+                             int renorm, bool exact_parts, float *__restrict__ probs,
+                             float4 *stage_scr = nullptr, float *x_scr = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nwaves = int(blockDim.x) >> 6;
     const bool mine = tid < E;
@@ -348,7 +431,17 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
         __syncthreads();
         const int n = sm.ncand;
         if (n <= 64) {
-            if (wv == 0 && lane < n) {
+            // with LDS from the caller: the rows streamed through it (the inputs
+            // copied there first unless they already are); else each
+            // contender's lane reads its own row
+            const bool staged = stage_scr && x_scr && d <= kXScrFloats && exact_staged_ok(R, d, n);
+            if (staged) {
+                if (x != x_scr)
+                    for (int i = tid; i < d; i += blockDim.x) x_scr[i] = x[i];
+                __syncthreads();
+                const float a = exact_logits_staged(R, x_scr, d, sm.cand, n, stage_scr);
+                if (wv == 0 && lane < n) sm.cl[lane] = bias ? add_rn(a, bias[sm.cand[lane]]) : a;
+            } else if (wv == 0 && lane < n) {
                 const int e = sm.cand[lane];
                 float a = exact_logit(R + size_t(e) * d, x, d);
                 if (bias) a = add_rn(a, bias[e]);

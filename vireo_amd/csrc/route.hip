@@ -173,9 +173,11 @@ __global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__re
                                                            float *__restrict__ w, uint32_t *__restrict__ flags,
                                                            float *__restrict__ probs) {
     __shared__ TopKSmem sm;
+    __shared__ float4 stage[kStageScrF4];            // the contenders' router rows, streamed
+    __shared__ __align__(16) float xbuf[kXScrFloats];  // the token's inputs, for them
     const int t = blockIdx.x, tid = threadIdx.x;
     route_topk_block(sm, parts + size_t(t) * E, R, hb + size_t(t) * d, bias, d, E, k, renorm, exact != 0,
-                     probs ? probs + size_t(t) * E : nullptr);
+                     probs ? probs + size_t(t) * E : nullptr, stage, xbuf);
     if (tid < k) {
         idx[size_t(t) * k + tid] = sm.sel[tid];
         w[size_t(t) * k + tid] = sm.sel_w[tid];
