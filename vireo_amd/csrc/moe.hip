@@ -107,7 +107,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
     const bool small = experts && grouped && T < kMfmaMinCall;
-    const size_t o_xp = small ? take(size_t(T) * d * 4) : 0, o_xsc = small ? take(size_t(T) * 4) : 0;
+    const size_t o_xp = small ? take(vh_mdec_xp_bytes(T, d)) : 0, o_xsc = small ? take(size_t(T) * 4) : 0;
     const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
     const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
     const size_t o_pidx = paged ? take(P * 4) : 0, o_pw = paged ? take(P * 4) : 0,
@@ -583,8 +583,8 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
             if (!rc) rc = vh_check(hipMemcpyAsync(dt, tab, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
             if (!rc) rc = vh_check(hipMemcpyAsync(da, act, act_n * 4, hipMemcpyHostToDevice, s));
             if (mdec) {
-                if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, da, dt, ws.xp, ws.xsc, d, fe, k, E, slots,
-                                             n_tokens, ws.h, s);
+                if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, da, dt, ws.xp, ws.xsc, n_tokens, d, fe, k,
+                                             E, slots, n_tokens, ws.h, s);
                 if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens,
                                            ws.ybuf, s);
             } else if (gdec) {
@@ -690,8 +690,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
                vh_mdec_supported(tg, td, d, fe)) {
         // calls of a decode batch's size, Q4_K_M experts: the matrix cores
         if (!rc) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
-        if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, d, fe, k, E, slots,
-                                     n_tokens, ws.h, s);
+        if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, n_tokens, d, fe,
+                                     k, E, slots, n_tokens, ws.h, s);
         if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, n_tokens,
                                    ws.ybuf, s);
     } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {

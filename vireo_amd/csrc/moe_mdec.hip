@@ -11,13 +11,15 @@
 // value cannot hold them - and products are summed in fp32 (the weights of
 // src/gguf_compute.c:52-66 and :83-103, the sums of the matvec of :202-207):
 //  - gate/up, v_mfma_f32_16x16x32_f16. A Q4_K weight of sub-block s is
-//    d*sc_s*q - dmin*m_s. One operand holds sc_s*q (an integer below 1024,
-//    exact in fp16, formed by a packed fp16 fma that rounds once), another
-//    m_s; per super-block the matrix cores form C = sum sc*q*x and M = sum
-//    m*x, and the row adds d*C - dmin*M in fp32. The inputs, scaled by a
-//    power of two per token that keeps them below 2^14 in magnitude (no fp16
-//    overflow), are split into fp16 parts hi + lo (22 significant bits) by
-//    mdec_prep_kernel, in the order the weight operand's slots take.
+//    d*sc_s*q - dmin*m_s. The weight operand holds sc_s*q (an integer below
+//    1024, exact in fp16, formed by a packed fp16 fma that rounds once); per
+//    super-block the matrix cores form C = sum sc*q*x, and M = sum_s m_s X_s
+//    from the sub-blocks' input sums X_s (one instruction per super-block);
+//    the row adds d*C - dmin*M in fp32. The inputs, scaled by a power of two
+//    per token that keeps them below 2^14 in magnitude (no fp16 overflow),
+//    are split into fp16 parts hi + lo (22 significant bits) by
+//    mdec_prep_kernel, in the order the weight operand's slots take; it also
+//    writes X_s / 32 (below 2^14) as fp16 hi + lo.
 //  - down, v_mfma_f32_16x16x16_bf16. A Q6_K weight of sub-block s (16
 //    weights) is d*sc_s*(q - 32). The operand holds q + 128 (exact in bf16)
 //    and a second product with the constant -160 completes q - 32; each
@@ -71,15 +73,27 @@ VH_DEV int q4k_slot_of(int r, int &chunk) {  // r = position in the super-block
     return 4 * hsub + (p == 1 ? 2 : p == 2 ? 1 : p);
 }
 
-// sc*q for the 8 nibbles of qs word w: nibbles as fp16 1024 + q (exponent
-// bits or'ed in), then (1024 + q) * sc - 1024 * sc in one packed fp16 fma,
-// exact (the result is an integer below 1024)
-VH_DEV f16x8 q4k_operand(uint32_t w, f16x2 s0, f16x2 n0, f16x2 s1, f16x2 n1) {
-    constexpr uint32_t kM = 0x000f000fu, kE = 0x64006400u;
-    const f16x2 a = __builtin_elementwise_fma(as_h2((w & kM) | kE), s0, n0);
-    const f16x2 b = __builtin_elementwise_fma(as_h2(((w >> 8) & kM) | kE), s0, n0);
-    const f16x2 c = __builtin_elementwise_fma(as_h2(((w >> 4) & kM) | kE), s1, n1);
-    const f16x2 e = __builtin_elementwise_fma(as_h2(((w >> 12) & kM) | kE), s1, n1);
+// (a & m) | e with all three in vector registers: the compiler's own form
+// takes at most one constant from outside them and splits the operation in two
+VH_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t e) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(e));
+    return r;
+}
+
+// sc*q for the 8 nibbles of qs word w: each nibble becomes the mantissa bits
+// of an fp16 with exponent 2^10 in place - bits 0-3 give 1024 + q, bits 4-7
+// give 1024 + 16 q - and one packed fp16 fma per pair, (1024 + q) sc - 1024 sc
+// or (1024 + 16 q) (sc / 16) - 64 sc, forms the product exactly (an integer
+// below 1024; sc / 16 and 64 sc have at most 6 significant bits). kLo =
+// 0x000f000f, kHi = 0x00f000f0 and kE = 0x64006400 come in registers.
+VH_DEV f16x8 q4k_operand(uint32_t w, f16x2 s0, f16x2 n0, f16x2 s1, f16x2 n1, uint32_t kLo, uint32_t kHi,
+                         uint32_t kE) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 a = __builtin_elementwise_fma(as_h2(and_or(w, kLo, kE)), s0, n0);
+    const f16x2 b = __builtin_elementwise_fma(as_h2(and_or(w8, kLo, kE)), s0, n0);
+    const f16x2 c = __builtin_elementwise_fma(as_h2(and_or(w, kHi, kE)), s1, n1);
+    const f16x2 e = __builtin_elementwise_fma(as_h2(and_or(w8, kHi, kE)), s1, n1);
     return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
 }
 
@@ -107,11 +121,15 @@ VH_DEV int q6k_slot_of(int k) {
 }
 
 // One workgroup of 256 threads per token: the largest |x|, the power of two,
-// and the fp16 split of every input into the gate/up operand order.
+// the fp16 split of every input into the gate/up operand order, and the sums
+// X_s of the scaled inputs over each 32-input sub-block, X_s / 32 split into
+// fp16 hi + lo at xsum + ((t * nb + b) * 4 + g) * 4: hi, lo of sub-block 2 g,
+// then of 2 g + 1 (the slots lane group g supplies to the min term).
 __global__ void __launch_bounds__(256) mdec_prep_kernel(const float *__restrict__ hb, int d,
-                                                        _Float16 *__restrict__ xp, float *__restrict__ xsc) {
+                                                        _Float16 *__restrict__ xp, float *__restrict__ xsc,
+                                                        _Float16 *__restrict__ xsum) {
     __shared__ float red[4];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x, nb = d / 256;
     const float *x = hb + size_t(t) * d;
     float m = 0.0f;
     for (int i = tid; i < d; i += 256) m = fmaxf(m, fabsf(x[i]));
@@ -125,15 +143,26 @@ __global__ void __launch_bounds__(256) mdec_prep_kernel(const float *__restrict_
     const float up = ldexpf(1.0f, sh);
     if (tid == 0) xsc[t] = ldexpf(1.0f, -sh);
     _Float16 *o = xp + size_t(t) * d * 2;
-    for (int i = tid; i < d; i += 256) {
-        const float v = x[i] * up;
+    int chunk;
+    const int j = q4k_slot_of(tid, chunk);
+    for (int b = 0; b < nb; b++) {  // d % 256 == 0: every thread takes every step
+        const float v = x[256 * b + tid] * up;
         const _Float16 hi = _Float16(v);
         const _Float16 lo = _Float16(v - float(hi));  // v - hi is exact in fp32
-        int chunk;
-        const int j = q4k_slot_of(i & 255, chunk);
-        const size_t c = (size_t(i >> 8) * 32 + chunk) * 16;
+        const size_t c = (size_t(b) * 32 + chunk) * 16;
         o[c + j] = hi;
         o[c + 8 + j] = lo;
+        float sv = v;  // sub-block tid / 32: lanes 32 s .. 32 s + 31 of the workgroup
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) sv += __shfl_xor(sv, off, 32);
+        if ((tid & 31) == 0) {
+            const int sb = tid >> 5;
+            const float q = sv * 0.03125f;  // |X_s| < 2^19
+            const _Float16 qh = _Float16(q);
+            _Float16 *xs = xsum + ((size_t(t) * nb + b) * 4 + (sb >> 1)) * 4 + 2 * (sb & 1);
+            xs[0] = qh;
+            xs[1] = _Float16(q - float(qh));
+        }
     }
 }
 
@@ -142,19 +171,24 @@ __global__ void __launch_bounds__(256) mdec_prep_kernel(const float *__restrict_
 // h = silu(gate . x) * (up . x) (src/gguf_run.c:205-207) as bf16 hi + lo parts
 // in the down operand's order into hp (4 bytes per activation, rows of fe).
 // The tile's split inputs pass through LDS one super-block at a time, double
-// buffered (every wave reads them; they are loaded once per workgroup), and
-// each wave's weights for the next super-block are in flight while it
-// computes the current one.
+// buffered (every wave reads them; they are loaded once per workgroup). Each
+// wave's weights are requested two super-blocks ahead of the one it
+// multiplies (three register sets in turn: the loop over the NB = d / 256
+// super-blocks is unrolled), so two blocks of its rows are in flight from
+// HBM while it computes.
 constexpr int kGuTokStride = 260;  // dwords per token and super-block in LDS: 256 + 4 (no bank conflicts)
+constexpr int kGuMaxBlocks = 8;    // d <= 2048
 
-__global__ void __launch_bounds__(256) mdec_gateup_kernel(const int32_t *__restrict__ counts,
+template <int NB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) mdec_gateup_kernel(const int32_t *__restrict__ counts,
                                                           const int32_t *__restrict__ offs,
                                                           const int32_t *__restrict__ perm,
                                                           const int32_t *__restrict__ active,
                                                           const void *const *__restrict__ table,
                                                           const uint4 *__restrict__ xp, const float *__restrict__ xsc,
-                                                          int d, int fe, int k, int E, int64_t row_bytes,
-                                                          uint16_t *__restrict__ hp) {
+                                                          const uint2 *__restrict__ xsum, int fe, int k, int E,
+                                                          int64_t row_bytes, uint16_t *__restrict__ hp) {
+    constexpr int d = 256 * NB;
     __shared__ __align__(16) uint32_t xs[2][kTok * kGuTokStride];
     const int s = blockIdx.y;
     if (s >= active[E]) return;
@@ -183,97 +217,129 @@ __global__ void __launch_bounds__(256) mdec_gateup_kernel(const int32_t *__restr
         return;
     }
     // the split inputs of the tile's tokens: thread tid copies 16-byte piece
-    // tid % 64 of token tid / 64 + 4 i's super-block (rows past the tile's
-    // tokens repeat its last token; nothing reads them)
+    // tid % 64 of token tid / 64 + 4 i's super-block
     const int pc = tid & 63, pt = tid >> 6;
     uint32_t srow[4];  // the tokens' rows of xp, in 16-byte pieces
 #pragma unroll
     for (int i = 0; i < 4; i++) srow[i] = uint32_t(perm[base + t0 + min(pt + 4 * i, tn - 1)] / k) * uint32_t(d / 4) + pc;
     uint32_t *xdst = &xs[0][pt * kGuTokStride + 4 * pc];
+    // this lane's token (row r of the input operand) in the sub-block sums
+    const uint2 *xsr = xsum + size_t(perm[base + t0 + min(r, tn - 1)] / k) * NB * 4 + g;
     gbyte *gr = G + int64_t(o) * row_bytes;
     gbyte *ur = U + int64_t(o) * row_bytes;
-    const int nb = d / 256;
     struct Wt {
         uint4 hd, q0, q1;
     };
-    auto load = [&](gbyte *row, int b, Wt &w) {
-        gbyte *p = row + 144 * b;
-        w.hd = ld_u128(p);
-        w.q0 = ld_u128(p + 16 + 32 * g);
-        w.q1 = ld_u128(p + 32 + 32 * g);
+    struct Blk {
+        Wt gw, uw;
+        uint2 xsm;
     };
-    Wt ng, nu;
+    auto load = [&](int b, Blk &w) {
+        gbyte *p = gr + 144 * b;
+        w.gw.hd = ld_u128(p);
+        w.gw.q0 = ld_u128(p + 16 + 32 * g);
+        w.gw.q1 = ld_u128(p + 32 + 32 * g);
+        p = ur + 144 * b;
+        w.uw.hd = ld_u128(p);
+        w.uw.q0 = ld_u128(p + 16 + 32 * g);
+        w.uw.q1 = ld_u128(p + 32 + 32 * g);
+        w.xsm = xsr[4 * b];
+    };
+    Blk blk[3];
+    // rows 4 .. 15 only when the tile has more than 4 tokens (a branch the
+    // whole workgroup takes alike); lanes of padding rows read the last
+    // token's row
+    const bool wide = tn > 4;
     uint4 xv0, xv1, xv2, xv3;
     xv0 = xp[srow[0]];
-    xv1 = xp[srow[1]];
-    xv2 = xp[srow[2]];
-    xv3 = xp[srow[3]];
-    load(gr, 0, ng);
-    load(ur, 0, nu);
+    if (wide) {
+        xv1 = xp[srow[1]];
+        xv2 = xp[srow[2]];
+        xv3 = xp[srow[3]];
+    }
+    load(0, blk[0]);
+    if (NB > 1) load(1, blk[1]);
     *reinterpret_cast<uint4 *>(xdst) = xv0;
-    *reinterpret_cast<uint4 *>(xdst + 4 * kGuTokStride) = xv1;
-    *reinterpret_cast<uint4 *>(xdst + 8 * kGuTokStride) = xv2;
-    *reinterpret_cast<uint4 *>(xdst + 12 * kGuTokStride) = xv3;
+    if (wide) {
+        *reinterpret_cast<uint4 *>(xdst + 4 * kGuTokStride) = xv1;
+        *reinterpret_cast<uint4 *>(xdst + 8 * kGuTokStride) = xv2;
+        *reinterpret_cast<uint4 *>(xdst + 12 * kGuTokStride) = xv3;
+    }
     __syncthreads();
+    // the nibble masks and the fp16 exponent, held in registers (see and_or)
+    uint32_t kLo = 0x000f000fu, kHi = 0x00f000f0u, kE = 0x64006400u;
+    asm volatile("" : "+v"(kLo), "+v"(kHi), "+v"(kE));
     const uint32_t *xr = &xs[0][min(r, tn - 1) * kGuTokStride + 8 * g];  // this lane's token, lane group g
     f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg;
-    for (int b = 0; b < nb; b++) {
-        const Wt cg = ng, cu = nu;
-        if (b + 1 < nb) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (b + 1 < NB) {
             xv0 = xp[srow[0] + 64 * (b + 1)];
-            xv1 = xp[srow[1] + 64 * (b + 1)];
-            xv2 = xp[srow[2] + 64 * (b + 1)];
-            xv3 = xp[srow[3] + 64 * (b + 1)];
-            load(gr, b + 1, ng);
-            load(ur, b + 1, nu);
+            if (wide) {
+                xv1 = xp[srow[1] + 64 * (b + 1)];
+                xv2 = xp[srow[2] + 64 * (b + 1)];
+                xv3 = xp[srow[3] + 64 * (b + 1)];
+            }
         }
+        if (b + 2 < NB) load(b + 2, blk[(b + 2) % 3]);
+        const Blk &cb = blk[b % 3];
+        const Wt &cg = cb.gw, &cu = cb.uw;
         const uint32_t *xb = xr + (b & 1) * (kTok * kGuTokStride);
         f16x2 s0g, n0g, s1g, n1g, s0u, n0u, s1u, n1u;
         f16x8 mopg, mopu;
+        // the fp16 factors of sub-blocks 2 g and 2 g + 1 (see q4k_operand), and
+        // the min operand m_2g, m_2g, m_2g+1, m_2g+1 against the sums' slots
         auto scales = [&](const uint4 &hd, f16x2 &s0, f16x2 &n0, f16x2 &s1, f16x2 &n1, f16x8 &mop) {
             int sc0, mn0, sc1, mn1;
             q4k_scale_min_v(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
             q4k_scale_min_v(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
-            const _Float16 a0 = _Float16(sc0), a1 = _Float16(sc1), m0 = _Float16(mn0), m1 = _Float16(mn1);
+            const _Float16 a0 = _Float16(sc0), a1 = _Float16(float(sc1) * 0.0625f);
+            const _Float16 m0 = _Float16(mn0), m1 = _Float16(mn1), z = _Float16(0.0f);
             s0 = f16x2{a0, a0};
             s1 = f16x2{a1, a1};
             n0 = f16x2{_Float16(-1024 * sc0), _Float16(-1024 * sc0)};
-            n1 = f16x2{_Float16(-1024 * sc1), _Float16(-1024 * sc1)};
-            mop = f16x8{m0, m0, m0, m0, m1, m1, m1, m1};
+            n1 = f16x2{_Float16(-64 * sc1), _Float16(-64 * sc1)};
+            mop = f16x8{m0, m0, m1, m1, z, z, z, z};
         };
         scales(cg.hd, s0g, n0g, s1g, n1g, mopg);
         scales(cu.hd, s0u, n0u, s1u, n1u, mopu);
         const uint32_t wgs[8] = {cg.q0.x, cg.q0.y, cg.q0.z, cg.q0.w, cg.q1.x, cg.q1.y, cg.q1.z, cg.q1.w};
         const uint32_t wus[8] = {cu.q0.x, cu.q0.y, cu.q0.z, cu.q0.w, cu.q1.x, cu.q1.y, cu.q1.z, cu.q1.w};
-        f32x4 c_g = {0.f, 0.f, 0.f, 0.f}, m_g = c_g, c_u = c_g, m_u = c_g;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f16x8 xsop = __builtin_bit_cast(f16x8, make_uint4(cb.xsm.x, cb.xsm.y, 0u, 0u));
+        const f32x4 m_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xsop, mopg, zero, 0, 0, 0);
+        const f32x4 m_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xsop, mopu, zero, 0, 0, 0);
+        f32x4 c_g = zero, c_u = zero;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const f16x8 xh = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4 *>(xb + 32 * u));
             const f16x8 xl = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4 *>(xb + 32 * u + 4));
-            const f16x8 bg = q4k_operand(wgs[u], s0g, n0g, s1g, n1g);
-            const f16x8 bu = q4k_operand(wus[u], s0u, n0u, s1u, n1u);
+            const f16x8 bg = q4k_operand(wgs[u], s0g, n0g, s1g, n1g, kLo, kHi, kE);
+            const f16x8 bu = q4k_operand(wus[u], s0u, n0u, s1u, n1u, kLo, kHi, kE);
             c_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bg, c_g, 0, 0, 0);
             c_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bg, c_g, 0, 0, 0);
-            m_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, mopg, m_g, 0, 0, 0);
-            m_g = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, mopg, m_g, 0, 0, 0);
             c_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bu, c_u, 0, 0, 0);
             c_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bu, c_u, 0, 0, 0);
-            m_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, mopu, m_u, 0, 0, 0);
-            m_u = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, mopu, m_u, 0, 0, 0);
         }
-        const float dg = h2f(cg.hd.x & 0xffffu), mg = h2f(cg.hd.x >> 16);
-        const float du = h2f(cu.hd.x & 0xffffu), mu = h2f(cu.hd.x >> 16);
+        // M holds sum m_s X_s / 32
+        const float dg = h2f(cg.hd.x & 0xffffu), mg = 32.0f * h2f(cg.hd.x >> 16);
+        const float du = h2f(cu.hd.x & 0xffffu), mu = 32.0f * h2f(cu.hd.x >> 16);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             accg[i] = fmaf(dg, c_g[i], fmaf(-mg, m_g[i], accg[i]));
             accu[i] = fmaf(du, c_u[i], fmaf(-mu, m_u[i], accu[i]));
         }
-        if (b + 1 < nb) {  // into the buffer read two super-blocks ago
+        // the block's sums are added here, not deferred past the later blocks
+        // (which would hold every block's results in registers)
+        asm volatile("" : "+v"(accg), "+v"(accu));
+        if (b + 1 < NB) {  // into the buffer read two super-blocks ago
             uint32_t *dst = xdst + ((b + 1) & 1) * (kTok * kGuTokStride);
             *reinterpret_cast<uint4 *>(dst) = xv0;
-            *reinterpret_cast<uint4 *>(dst + 4 * kGuTokStride) = xv1;
-            *reinterpret_cast<uint4 *>(dst + 8 * kGuTokStride) = xv2;
-            *reinterpret_cast<uint4 *>(dst + 12 * kGuTokStride) = xv3;
+            if (wide) {
+                *reinterpret_cast<uint4 *>(dst + 4 * kGuTokStride) = xv1;
+                *reinterpret_cast<uint4 *>(dst + 8 * kGuTokStride) = xv2;
+                *reinterpret_cast<uint4 *>(dst + 12 * kGuTokStride) = xv3;
+            }
             __syncthreads();
         }
     }
@@ -396,25 +462,38 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
 }  // namespace
 
 bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe) {
-    // d: whole super-blocks and 32-row waves; fe: whole super-blocks, 16-row
-    // waves and the activations of a 16-token tile in LDS
-    return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && fe % 256 == 0 && fe <= 256 * kDnMaxBlocks;
+    // d: whole super-blocks (at most kGuMaxBlocks, the gate/up kernel's
+    // unrolled loop) and 32-row waves; fe: whole super-blocks, 16-row waves and
+    // the activations of a 16-token tile in LDS
+    return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && d <= 256 * kGuMaxBlocks && fe % 256 == 0 &&
+           fe <= 256 * kDnMaxBlocks;
 }
 
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s) {
     if (T < 1 || d % 256) return -EINVAL;
-    hipLaunchKernelGGL(mdec_prep_kernel, dim3(T), dim3(256), 0, s, hb, d, static_cast<_Float16 *>(xp), xsc);
+    hipLaunchKernelGGL(mdec_prep_kernel, dim3(T), dim3(256), 0, s, hb, d, static_cast<_Float16 *>(xp), xsc,
+                       static_cast<_Float16 *>(vh_mdec_xsum(xp, T, d)));
     return vh_check(hipGetLastError());
 }
 
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                   const void *const *table, const void *xp, const float *xsc, int d, int fe, int k, int E,
+                   const void *const *table, const void *xp, const float *xsc, int T, int d, int fe, int k, int E,
                    int max_slots, int max_count, void *hp, hipStream_t s) {
-    if (max_count < 1 || d % 256 || fe % 16) return -EINVAL;
+    if (max_count < 1 || T < 1 || d % 256 || d > 256 * kGuMaxBlocks || fe % 16) return -EINVAL;
     const dim3 g((fe + 63) / 64, max_slots, (max_count + kTok - 1) / kTok);
-    hipLaunchKernelGGL(mdec_gateup_kernel, g, dim3(256), 0, s, counts, offs, perm, active, table,
-                       static_cast<const uint4 *>(xp), xsc, d, fe, k, E, vh_row_bytes(VT_Q4_K, d),
-                       static_cast<uint16_t *>(hp));
+    const uint4 *x4 = static_cast<const uint4 *>(xp);
+    const uint2 *xs = static_cast<const uint2 *>(vh_mdec_xsum(const_cast<void *>(xp), T, d));
+    const int64_t rb = vh_row_bytes(VT_Q4_K, d);
+    uint16_t *h = static_cast<uint16_t *>(hp);
+#define VH_GU(NB)                                                                                                  \
+    case NB:                                                                                                       \
+        hipLaunchKernelGGL(mdec_gateup_kernel<NB>, g, dim3(256), 0, s, counts, offs, perm, active, table, x4, xsc, \
+                           xs, fe, k, E, rb, h);                                                                   \
+        break;
+    switch (d / 256) {
+        VH_GU(1) VH_GU(2) VH_GU(3) VH_GU(4) VH_GU(5) VH_GU(6) VH_GU(7) VH_GU(8)
+    }
+#undef VH_GU
     return vh_check(hipGetLastError());
 }
 

@@ -113,12 +113,15 @@ int vh_gdec_down(uint32_t type, const int32_t *counts, const int32_t *offs, cons
 // Decode-batch projections on the matrix cores (moe_mdec.hip), for calls of
 // fewer than kMfmaMinCall tokens with Q4_K gate/up and Q6_K down: the same
 // groups and outputs as vh_gdec_*. vh_mdec_prep splits hb [T x d] into xp
-// (T x d x 4 bytes) and xsc [T]; gate/up writes the activations as hp
-// (P x fe x 4 bytes, not fp32 h) for vh_mdec_down.
+// (vh_mdec_xp_bytes: the split inputs, T x d x 4 bytes, then their sub-block
+// sums, T x d / 8 bytes, at vh_mdec_xsum) and xsc [T]; gate/up writes the
+// activations as hp (P x fe x 4 bytes, not fp32 h) for vh_mdec_down.
+inline size_t vh_mdec_xp_bytes(int T, int d) { return size_t(T) * d * 4 + size_t(T) * (d / 8); }
+inline void *vh_mdec_xsum(void *xp, int T, int d) { return static_cast<char *>(xp) + size_t(T) * d * 4; }
 bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe);
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s);
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                   const void *const *table, const void *xp, const float *xsc, int d, int fe, int k, int E,
+                   const void *const *table, const void *xp, const float *xsc, int T, int d, int fe, int k, int E,
                    int max_slots, int max_count, void *hp, hipStream_t s);
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                  const void *const *table, const void *hp, int d, int fe, int E, int max_slots, int max_count,
