@@ -483,7 +483,11 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     float *w = w_out ? w_out : ws.w;
     const float *R = static_cast<const float *>(L.router->data);
     const bool exact = n_tokens >= kExactRouteTokens;
-    int rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
+    const bool mdec = n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
+                      vh_mdec_supported(tg, td, d, fe);
+    int rc = mdec ? vh_route_parts_tiled(R, hb, L.logit_bias, d, E, n_tokens, ws.parts, ws.xp, ws.xsc, s) : -EINVAL;
+    const bool prepped = rc == 0;
+    if (rc == -EINVAL) rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
@@ -539,10 +543,8 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
     vh_store_note_routing_host(m->es, layer, idx_h, n_tokens, k);
     const uint64_t cap = vh_store_capacity(m->es), leased = vh_store_leased_bytes(m->es);
     const uint64_t room = cap > leased ? cap - leased : 1;  // cap 0: unbounded (room unused)
-    const bool mdec = n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
-                      vh_mdec_supported(tg, td, d, fe);
     const bool gdec = !mdec && n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb);
-    if (mdec) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
+    if (mdec && !prepped) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
     const void **present = tabs_h + size_t(E) * tab_n;  // the combine's table (the last one)
     memset(present, 0, tab_n * sizeof(void *));
     ExpertView views[kMaxExperts];
@@ -674,7 +676,12 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     }
     const bool exact = n_tokens >= kExactRouteTokens;
     const int P = n_tokens * k, slots = P < E ? P : E;
-    rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
+    const bool mdec = !mfma && n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
+                      vh_mdec_supported(tg, td, d, fe);
+    // the matrix-core decode batch's split inputs come with the router parts where the tiled kernel runs
+    rc = mdec ? vh_route_parts_tiled(R, hb, L.logit_bias, d, E, n_tokens, ws.parts, ws.xp, ws.xsc, s) : -EINVAL;
+    const bool prepped = rc == 0;
+    if (rc == -EINVAL) rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
@@ -686,10 +693,9 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
         if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
-    } else if (n_tokens >= kMdecMinTokens && n_tokens < kMfmaMinCall && g_path != 4 &&
-               vh_mdec_supported(tg, td, d, fe)) {
+    } else if (mdec) {
         // calls of a decode batch's size, Q4_K_M experts: the matrix cores
-        if (!rc) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
+        if (!rc && !prepped) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
         if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, n_tokens, d, fe,
                                      k, E, slots, n_tokens, ws.h, s);
         if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, n_tokens,

@@ -47,6 +47,7 @@
 #include <hip/hip_runtime.h>
 #include "common.h"
 #include "qdecode.h"
+#include "route.h"
 #include "route_kernels.h"
 
 namespace {
@@ -163,6 +164,113 @@ __global__ void __launch_bounds__(256) mdec_prep_kernel(const float *__restrict_
             xs[0] = qh;
             xs[1] = _Float16(q - float(qh));
         }
+    }
+}
+
+// Router parts of T >= 2 tokens, d = 2048, by tiles of 4 experts x 4 tokens:
+// the arithmetic of route_row_part<32> per (expert, token) - lane l's 32
+// products, their fp64 sum and the bound on the reference's rounding - so
+// the same parts as one wave per pair, with the tokens' inputs read once per
+// tile (through LDS) instead of once per expert, and each wave's router row
+// read once for its 4 tokens. Wave w copies token t0 + w and takes expert
+// e0 + w. With xp given, the workgroups of experts 0..3 also write
+// mdec_prep_kernel's outputs for their tokens (lane l's 32 inputs are
+// sub-block l % 8 of super-block l / 8; its sum is taken in order in the lane).
+constexpr int kRpTile = 4, kRpLaneF = 36;  // 32 inputs per lane in LDS, plus 4 floats (no bank conflicts)
+
+__global__ void __launch_bounds__(256) mdec_route_prep_kernel(const float *__restrict__ R, const float *__restrict__ hb,
+                                                              const float *__restrict__ bias, int E, int T,
+                                                              RoutePart *__restrict__ parts, _Float16 *__restrict__ xp,
+                                                              float *__restrict__ xsc, _Float16 *__restrict__ xsum) {
+    constexpr int d = 2048, C = 32, nb = d / 256;
+    __shared__ __align__(16) float xs[kRpTile][64 * kRpLaneF];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int e = blockIdx.x * kRpTile + w, t0 = blockIdx.y * kRpTile;
+    float rv[C], xv[C];
+    const float4 *x4 = reinterpret_cast<const float4 *>(hb + size_t(min(t0 + w, T - 1)) * d + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 4; i++) {
+        const float4 v = x4[i];
+        xv[4 * i] = v.x;
+        xv[4 * i + 1] = v.y;
+        xv[4 * i + 2] = v.z;
+        xv[4 * i + 3] = v.w;
+    }
+    const float4 *r4 = reinterpret_cast<const float4 *>(R + size_t(min(e, E - 1)) * d + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 4; i++) {
+        const float4 v = r4[i];
+        rv[4 * i] = v.x;
+        rv[4 * i + 1] = v.y;
+        rv[4 * i + 2] = v.z;
+        rv[4 * i + 3] = v.w;
+    }
+    float4 *dst = reinterpret_cast<float4 *>(&xs[w][lane * kRpLaneF]);
+#pragma unroll
+    for (int i = 0; i < C / 4; i++) dst[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+    const int t = t0 + w;
+    if (xp && blockIdx.x == 0 && t < T) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < C; i++) m = fmaxf(m, fabsf(xv[i]));
+        m = wave_max_f(m);
+        int ex = 0;
+        if (m > 0.0f && m <= 3.4028234663852886e38f) frexpf(m, &ex);  // m < 2^ex
+        const int sh = max(-120, min(120, 14 - ex));                  // |x 2^sh| < 2^14
+        const float up = ldexpf(1.0f, sh);
+        if (lane == 0) xsc[t] = ldexpf(1.0f, -sh);
+        const int b = lane >> 3, g = (lane & 7) >> 1, hs = lane & 1;
+        _Float16 *o = xp + size_t(t) * d * 2;
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float v = xv[4 * u + q] * up;
+                hi[q] = _Float16(v);
+                lo[q] = _Float16(v - float(hi[q]));  // exact in fp32
+                sum += v;
+            }
+            // slots 4 hs .. 4 hs + 3 of chunk (b, u, g) hold positions 0, 2, 1, 3
+            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+            f16x4 *c = reinterpret_cast<f16x4 *>(o + (size_t(b) * 32 + u * 4 + g) * 16 + 4 * hs);
+            c[0] = f16x4{hi[0], hi[2], hi[1], hi[3]};
+            c[2] = f16x4{lo[0], lo[2], lo[1], lo[3]};
+        }
+        const float q = sum * 0.03125f;  // |X_s| < 2^19
+        const _Float16 qh = _Float16(q);
+        _Float16 *xsp = xsum + ((size_t(t) * nb + b) * 4 + g) * 4 + 2 * hs;
+        xsp[0] = qh;
+        xsp[1] = _Float16(q - float(qh));
+    }
+    __syncthreads();
+    if (e >= E) return;
+    for (int j = 0; j < kRpTile && t0 + j < T; j++) {
+        const float4 *src = reinterpret_cast<const float4 *>(&xs[j][lane * kRpLaneF]);
+        float p[C];
+#pragma unroll
+        for (int i = 0; i < C / 4; i++) {
+            const float4 v = src[i];
+            p[4 * i] = mul_rn(rv[4 * i], v.x);
+            p[4 * i + 1] = mul_rn(rv[4 * i + 1], v.y);
+            p[4 * i + 2] = mul_rn(rv[4 * i + 2], v.z);
+            p[4 * i + 3] = mul_rn(rv[4 * i + 3], v.w);
+        }
+        double tot = 0.0, absum = 0.0;
+#pragma unroll
+        for (int i = 0; i < C; i++) tot += double(p[i]);
+        double run = wave_incl_scan_d(tot) - tot;
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            run += double(p[i]);
+            absum += fabs(run);
+        }
+        RoutePart out;
+        out.c = wave_sum_d(tot);
+        out.beta = 1.001 * 5.9604644775390625e-08 * wave_sum_d(absum) + 1e-30;
+        if (bias) out.c += double(bias[e]);
+        if (lane == 0) parts[size_t(t0 + j) * E + e] = out;
     }
 }
 
@@ -467,6 +575,17 @@ bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe) {
     // the activations of a 16-token tile in LDS
     return tg == VT_Q4_K && td == VT_Q6_K && d % 256 == 0 && d <= 256 * kGuMaxBlocks && fe % 256 == 0 &&
            fe <= 256 * kDnMaxBlocks;
+}
+
+int vh_route_parts_tiled(const float *R, const float *hb, const float *bias, int d, int E, int T, RoutePart *parts,
+                         void *xp, float *xsc, hipStream_t s) {
+    if (d != 2048 || T < 2 || E < 1 || ((reinterpret_cast<uintptr_t>(R) | reinterpret_cast<uintptr_t>(hb)) & 15u))
+        return -EINVAL;
+    const dim3 g((E + kRpTile - 1) / kRpTile, (T + kRpTile - 1) / kRpTile);
+    hipLaunchKernelGGL(mdec_route_prep_kernel, g, dim3(256), 0, s, R, hb, bias, E, T, parts,
+                       static_cast<_Float16 *>(xp), xsc,
+                       xp ? static_cast<_Float16 *>(vh_mdec_xsum(xp, T, d)) : nullptr);
+    return vh_check(hipGetLastError());
 }
 
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s) {

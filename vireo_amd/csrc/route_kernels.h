@@ -119,6 +119,11 @@ int vh_gdec_down(uint32_t type, const int32_t *counts, const int32_t *offs, cons
 inline size_t vh_mdec_xp_bytes(int T, int d) { return size_t(T) * d * 4 + size_t(T) * (d / 8); }
 inline void *vh_mdec_xsum(void *xp, int T, int d) { return static_cast<char *>(xp) + size_t(T) * d * 4; }
 bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe);
+// The router parts of T >= 2 tokens (the same values as vh_route_parts'
+// bounded parts) by 4 x 4 tiles of (expert, token), d == 2048 and 16-byte
+// aligned R and hb, else -EINVAL; with xp given, also vh_mdec_prep's outputs.
+int vh_route_parts_tiled(const float *R, const float *hb, const float *bias, int d, int E, int T, RoutePart *parts,
+                         void *xp, float *xsc, hipStream_t s);
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s);
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                    const void *const *table, const void *xp, const float *xsc, int T, int d, int fe, int k, int E,
