@@ -20,21 +20,22 @@
 //    are split into fp16 parts hi + lo (22 significant bits) by
 //    mdec_prep_kernel, in the order the weight operand's slots take; it also
 //    writes X_s / 32 (below 2^14) as fp16 hi + lo.
-//  - down, v_mfma_f32_16x16x16_bf16. A Q6_K weight of sub-block s (16
+//  - down, v_mfma_f32_16x16x32_bf16. A Q6_K weight of sub-block s (16
 //    weights) is d*sc_s*(q - 32). The operand holds q + 128 (exact in bf16)
 //    and a second product with the constant -160 completes q - 32; each
 //    sub-block's sum is scaled by d*sc_s in fp32. The activations h are split
 //    into bf16 parts hi + lo (16 significant bits, fp32's range, no scale) by
 //    the gate/up kernel as it writes them, in the order the down operand's
-//    slots take.
+//    slots take; one instruction's 32 k slots take a sub-block's 16 hi parts
+//    and its 16 lo parts against the weights repeated.
 // Products of 16-bit parts are exact in fp32, so the results differ from the
 // fp32 kernels' only by the order of the fp32 sums and the dropped low bits of
 // the split inputs (relative 2^-22 and 2^-17 of the largest input).
 //
 // Matrix operands (both instructions): A is tokens x K - lane l supplies
 // token l % 16 -, B is K x weight rows - lane l supplies row l % 16 -, and the
-// lanes l / 16 = g supply the same K positions of A and B (8 per lane for
-// 16x16x32, 4 for 16x16x16); lane l receives rows 4 g .. 4 g + 3 (tokens) of
+// lanes l / 16 = g supply the same K positions of A and B (8 per lane); lane
+// l receives rows 4 g .. 4 g + 3 (tokens) of
 // column l % 16 (weight row) of the result. Which K position a slot holds is
 // free as long as A and B agree: it is fixed by how a weight word is unpacked,
 // and the inputs are laid out to match.
@@ -54,7 +55,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTok = 16;  // tokens per tile (the A operand's rows)
@@ -515,7 +516,7 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
     __syncthreads();  // the activations are in LDS (and the weights have arrived)
     const uint4 *xr = reinterpret_cast<const uint4 *>(&hs[min(r, tn - 1) * hstride]) + g;
     constexpr uint32_t kB = 0x43004300u;  // bf16 128 in both halves
-    const s16x4 k160 = __builtin_bit_cast(s16x4, make_uint2(0xC320C320u, 0xC320C320u));  // bf16 -160
+    const bf16x8 k160 = __builtin_bit_cast(bf16x8, make_uint4(0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u));  // bf16 -160
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     uint32_t *wl = &wq[wv][r * kDnRowStride];
 #pragma unroll
@@ -538,18 +539,16 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int sb = 8 * h + 2 * j + lh, ql_c = 4 * h + 2 * (j & 1) + lh, qh_c = 2 * h + lh;
-                    const uint4 hx = xr[64 * b + 4 * sb];
-                    const s16x4 xh = __builtin_bit_cast(s16x4, make_uint2(hx.x, hx.y));
-                    const s16x4 xl = __builtin_bit_cast(s16x4, make_uint2(hx.z, hx.w));
+                    // slots 0-3: the hi parts of the lane's 4 activations, 4-7 their lo parts;
+                    // the weight operand repeats q + 128 for both
+                    const bf16x8 xa = __builtin_bit_cast(bf16x8, xr[64 * b + 4 * sb]);
                     const uint32_t lw = wl[4 * ql_c + g], hw = wl[32 + 4 * qh_c + g];
                     const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
-                    const s16x4 w =
-                        __builtin_bit_cast(s16x4, make_uint2((q & 0x00ff00ffu) | kB, ((q >> 8) & 0x00ff00ffu) | kB));
+                    const uint32_t w0 = (q & 0x00ff00ffu) | kB, w1 = ((q >> 8) & 0x00ff00ffu) | kB;
+                    const bf16x8 wb = __builtin_bit_cast(bf16x8, make_uint4(w0, w1, w0, w1));
                     f32x4 c = {0.f, 0.f, 0.f, 0.f};
-                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, w, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, w, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xh, k160, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xl, k160, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wb, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, k160, c, 0, 0, 0);
                     const float ds = dd * float(int(int8_t(scw[sb >> 2] >> (8 * (sb & 3)))));
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[i] = fmaf(ds, c[i], acc[i]);
