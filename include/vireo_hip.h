@@ -66,6 +66,14 @@ int qdequant_rows(uint32_t ggml_type, const void *src, float *dst, int n, int ro
  * o = x * (1/sqrt(mean(x^2) + eps)) * w. w: device [n] F32 weight, or NULL
  * for a unit weight. o may equal x. */
 int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream);
+/* The router logits exactly as the reference forms them (the F32 gguf_matmul,
+ * src/gguf_compute.c:202-207: per expert an in-order fp32 sum of fp32
+ * products, no contraction): out[t*E + e] = row e of R . hb[t], for T
+ * tokens. R: device [E x d] F32; hb: [T x d]; out: [T x E]. The routing
+ * kernels compute these chains for the tokens whose fp64 bounds do not
+ * certify their top k; for d = 2048 (16-byte aligned rows) a whole wave
+ * shares one chain. */
+int vireo_router_logits(const float *R, const float *hb, int d, int E, int T, float *out, void *stream);
 /* argmax (src/gguf_run.c:254): first index of the maximum of v[0..n). */
 int vireo_argmax(const float *v, int n, int32_t *out, void *stream);
 /* Embedding lookup (src/gguf_run.c:218, gguf_dequant_row of a tok_embd row):

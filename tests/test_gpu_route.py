@@ -124,3 +124,40 @@ def test_dispatch_is_a_stable_sort(cuda, T, k, E, skew):
     np.testing.assert_array_equal(counts.cpu().numpy(), np.bincount(flat, minlength=E))
     np.testing.assert_array_equal(offs.cpu().numpy(), np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]))
     np.testing.assert_array_equal(perm.cpu().numpy(), np.argsort(flat, kind="stable"))
+
+
+@pytest.mark.parametrize("case", ["random", "alternating", "range", "subnormal", "d1024"])
+def test_router_logits_exact(cuda, oracle, lib, case):
+    """vireo_router_logits is the reference's in-order fp32 chain bit for bit
+    (the chain the routing kernels run for tokens they cannot certify). For
+    d = 2048 a wave shares one chain, 32 steps per lane, and re-runs it until
+    every lane starts from its neighbour's end, so the cases are the ones that
+    make guessed starts wrong and keep them wrong: products of alternating sign
+    that take the sum back across zero (a new binade) at every step,
+    magnitudes over 36 decades, subnormal products and sums; d = 1024 takes
+    one thread per chain."""
+    import ctypes as C
+    from vireo_amd import _lib
+    rng = np.random.default_rng(71)
+    d = 1024 if case == "d1024" else 2048
+    E, T = 40, 5
+    R = (rng.standard_normal((E, d)) * 0.05).astype(np.float32)
+    hb = rng.standard_normal((T, d)).astype(np.float32)
+    if case == "alternating":
+        sign = np.where(np.arange(d) % 2 == 0, 1.0, -1.0).astype(np.float32)
+        R = ((np.abs(R) + 0.5) * sign).astype(np.float32)
+        hb = (np.abs(hb) * 1000.0 + 1.0).astype(np.float32)
+    elif case == "range":
+        hb = (hb * 10.0 ** rng.uniform(-18, 18, (T, d))).astype(np.float32)
+    elif case == "subnormal":
+        R = (R * 1e-20).astype(np.float32)
+        hb = (hb * 1e-19).astype(np.float32)
+    Rt, ht = torch.from_numpy(R).to(cuda), torch.from_numpy(hb).to(cuda)
+    out = torch.empty((T, E), dtype=torch.float32, device=cuda)
+    _lib.check(lib.vireo_router_logits(C.c_void_p(Rt.data_ptr()), C.c_void_p(ht.data_ptr()), d, E, T,
+                                       C.c_void_p(out.data_ptr()), None), "vireo_router_logits")
+    want = np.stack([oracle.matmul(W.F32, R, hb[t], d, E) for t in range(T)])
+    got = out.cpu().numpy()
+    if case == "subnormal":
+        assert np.count_nonzero(np.abs(want) < 1.1754944e-38) > 0
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -183,6 +183,7 @@ SIGNATURES = {
     "qmatvec_async": (C.c_int, [c_vp, c_vp, C.POINTER(GGUFTensor), C.c_int, C.c_int, c_vp]),
     "qdequant_rows": (C.c_int, [C.c_uint32, c_vp, c_vp, C.c_int, C.c_int, c_vp]),
     "vireo_rmsnorm": (C.c_int, [c_vp, c_vp, c_vp, C.c_int, C.c_int, C.c_float, c_vp]),
+    "vireo_router_logits": (C.c_int, [c_vp, c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp]),
     "vireo_argmax": (C.c_int, [c_vp, C.c_int, c_vp, c_vp]),
     "vireo_embed": (C.c_int, [C.c_uint32, c_vp, C.c_int, C.c_int, c_vp, C.c_int, c_vp, c_vp]),
     "moe_stack_step": (C.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),

@@ -296,6 +296,46 @@ VH_DEV float exact_logits_staged(const float *__restrict__ R, const float *xs, i
     return a;
 }
 
+// The reference logit exactly (exact_logit's in-order chain a = fl(a +
+// fl(r_i x_i)), i = 0 .. 2047) by a whole wave, for d = 2048: lane l runs
+// steps 32 l .. 32 l + 31 from a guess of the chain's value there and hands
+// its end to lane l + 1, until every lane's start equals, bit for bit, the
+// end of the lane before it (lane 0 starts at the reference's 0). Then every
+// lane ran from the chain's true value, by induction from lane 0, and lane
+// 63's end is the reference's sum. Each round fixes at least one more lane,
+// so 64 rounds always suffice; the first guesses - the fp64 prefix sums of
+// the products rounded to fp32 - and chains from nearby starts meeting on
+// the coarser grid as the sum grows leave a few in practice, each 32
+// dependent steps instead of 2048. r and xv: the lane's 32 elements of the
+// row (16-byte aligned) and of the inputs. Every lane gets the result.
+VH_DEV float exact_logit_wave(const float *__restrict__ r, const float (&xv)[32], int lane) {
+    float p[32];
+    const float4 *r4 = reinterpret_cast<const float4 *>(r + lane * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 a = r4[i];
+        p[4 * i] = mul_rn(a.x, xv[4 * i]);
+        p[4 * i + 1] = mul_rn(a.y, xv[4 * i + 1]);
+        p[4 * i + 2] = mul_rn(a.z, xv[4 * i + 2]);
+        p[4 * i + 3] = mul_rn(a.w, xv[4 * i + 3]);
+    }
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) tot += double(p[i]);
+    const double pre = wave_incl_scan_d(tot) - tot;
+    float g = lane == 0 ? 0.0f : float(pre), e = 0.0f;
+    for (int round = 0; round <= 64; round++) {
+        e = g;
+#pragma unroll
+        for (int i = 0; i < 32; i++) e = add_rn(e, p[i]);
+        const float from = __shfl_up(e, 1, 64);
+        const float ng = lane == 0 ? 0.0f : from;
+        if (__ballot(__float_as_uint(ng) != __float_as_uint(g)) == 0ull) break;
+        g = ng;
+    }
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 63));
+}
+
 constexpr int kXScrFloats = 2048;  // inputs route_topk_block can copy into its caller's x_scr
 
 // Workspace of route_topk_block (LDS).
@@ -435,7 +475,24 @@ VH_DEV void route_topk_block(TopKSmem &sm, const RoutePart *__restrict__ part, c
             // copied there first unless they already are); else each
             // contender's lane reads its own row
             const bool staged = stage_scr && x_scr && d <= kXScrFloats && exact_staged_ok(R, d, n);
-            if (staged) {
+            const bool waves = d == 2048 && ((reinterpret_cast<uintptr_t>(R) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+            if (waves) {  // one contender per wave at a time, the chain split over its lanes
+                float xv[32];
+                const float4 *x4 = reinterpret_cast<const float4 *>(x + lane * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 v = x4[i];
+                    xv[4 * i] = v.x;
+                    xv[4 * i + 1] = v.y;
+                    xv[4 * i + 2] = v.z;
+                    xv[4 * i + 3] = v.w;
+                }
+                for (int c = wv; c < n; c += nwaves) {
+                    const int e = sm.cand[c];
+                    const float a = exact_logit_wave(R + size_t(e) * d, xv, lane);
+                    if (lane == 0) sm.cl[c] = bias ? add_rn(a, bias[e]) : a;
+                }
+            } else if (staged) {
                 if (x != x_scr)
                     for (int i = tid; i < d; i += blockDim.x) x_scr[i] = x[i];
                 __syncthreads();

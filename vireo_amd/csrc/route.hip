@@ -165,8 +165,9 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     }
 }
 
-// one 256-thread workgroup per token
-__global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__restrict__ parts,
+// one 512-thread workgroup per token (eight waves share an uncertified
+// token's contenders)
+__global__ void __launch_bounds__(512) route_finish_kernel(const RoutePart *__restrict__ parts,
                                                            const float *__restrict__ R, const float *__restrict__ hb,
                                                            const float *__restrict__ bias, int d, int E, int k,
                                                            int renorm, int exact, int32_t *__restrict__ idx,
@@ -185,7 +186,40 @@ __global__ void __launch_bounds__(256) route_finish_kernel(const RoutePart *__re
     if (tid == 0 && flags) flags[t] = sm.flag;
 }
 
+// one 64-thread workgroup per (expert, token): the wave-split chain for
+// d == 2048 with aligned rows, else lane 0's sequential chain
+__global__ void __launch_bounds__(64) router_logits_kernel(const float *__restrict__ R, const float *__restrict__ hb,
+                                                           int d, int E, float *__restrict__ out) {
+    const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const float *r = R + size_t(e) * d, *x = hb + size_t(t) * d;
+    float a;
+    if (d == 2048 && ((reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0) {
+        float xv[32];
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + lane * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = x4[i];
+            xv[4 * i] = v.x;
+            xv[4 * i + 1] = v.y;
+            xv[4 * i + 2] = v.z;
+            xv[4 * i + 3] = v.w;
+        }
+        a = exact_logit_wave(r, xv, lane);
+    } else {
+        a = lane == 0 ? exact_logit(r, x, d) : 0.0f;
+    }
+    if (lane == 0) out[size_t(t) * E + e] = a;
+}
+
 }  // namespace
+
+extern "C" int vireo_router_logits(const float *R, const float *hb, int d, int E, int T, float *out, void *stream) {
+    if (d <= 0 || E <= 0 || T < 0 || E > 65535 || T > 65535 || (T && (!R || !hb || !out))) return -EINVAL;
+    if (T == 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(router_logits_kernel, dim3(E, T), dim3(64), 0, s, R, hb, d, E, out);
+    return vh_finish(s, vh_check(hipGetLastError()));
+}
 
 int vh_route_parts_norm(const float *R, const float *x, const float *nw, float eps, float *hb_out, const float *bias,
                         int d, int E, int T, RoutePart *parts, hipStream_t s, uint32_t *zero, int nzero) {
@@ -221,7 +255,7 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
                     hipStream_t s) {
-    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(256), 0, s, parts, R, hb, bias, d, E, k, renorm,
+    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(512), 0, s, parts, R, hb, bias, d, E, k, renorm,
                        exact ? 1 : 0, idx, w, flags, probs);
     return vh_check(hipGetLastError());
 }
