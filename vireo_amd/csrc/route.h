@@ -303,11 +303,12 @@ VH_DEV float exact_logits_staged(const float *__restrict__ R, const float *xs, i
 // end of the lane before it (lane 0 starts at the reference's 0). Then every
 // lane ran from the chain's true value, by induction from lane 0, and lane
 // 63's end is the reference's sum. Each round fixes at least one more lane,
-// so 64 rounds always suffice; the first guesses - the fp64 prefix sums of
-// the products rounded to fp32 - and chains from nearby starts meeting on
-// the coarser grid as the sum grows leave a few in practice, each 32
-// dependent steps instead of 2048. r and xv: the lane's 32 elements of the
-// row (16-byte aligned) and of the inputs. Every lane gets the result.
+// so 64 rounds always suffice (the first guesses are the fp64 prefix sums of
+// the products rounded to fp32). Chains from starts a few ulps apart rarely
+// meet, so on router-like data most of the 64 rounds run and the chain takes
+// about as long as one lane's; the gain is that a workgroup's waves each
+// take a contender. r and xv: the lane's 32 elements of the row (16-byte
+// aligned) and of the inputs. Every lane gets the result.
 VH_DEV float exact_logit_wave(const float *__restrict__ r, const float (&xv)[32], int lane) {
     float p[32];
     const float4 *r4 = reinterpret_cast<const float4 *>(r + lane * 32);
