@@ -70,6 +70,7 @@ __global__ void __launch_bounds__(256) argmax_part_kernel(const float *__restric
     const int lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
     float bv = v[lo];
     int bi = lo;
+#pragma unroll 4
     for (int i = lo + threadIdx.x; i < hi; i += 256) arg_merge(bv, bi, v[i], i);
     arg_block(bv, bi, sv, si);
     if (threadIdx.x == 0) part[blockIdx.x] = ArgBest{bv, bi};
@@ -191,8 +192,8 @@ extern "C" int vireo_rmsnorm(float *o, const float *x, const float *w, int n, in
 extern "C" int vireo_argmax(const float *v, int n, int32_t *out, void *stream) {
     if (n <= 0 || !v || !out) return -EINVAL;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // about 4 K values per workgroup, at most 1 024 workgroups
-    int np = (n + 4095) / 4096;
+    // about 1 K values per workgroup (four loads per thread in flight), at most 1 024 workgroups
+    int np = (n + 1023) / 1024;
     if (np > 1024) np = 1024;
     const int chunk = (n + np - 1) / np;
     np = (n + chunk - 1) / chunk;

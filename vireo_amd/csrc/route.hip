@@ -234,7 +234,7 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
 int vh_route_parts(const float *R, const float *hb, const float *bias, int d, int E, int T, bool exact,
                    RoutePart *parts, hipStream_t s, uint32_t *zero, int nzero) {
     if (nzero > E * T * 64) return -EINVAL;
-    if (!exact && T >= 2 && nzero == 0) {  // d == 2048: inputs shared by 4 x 4 tiles
+    if (!exact && T >= 8 && nzero == 0) {  // d == 2048: inputs shared by 4 x 4 tiles (fewer tokens: too few waves)
         const int rc = vh_route_parts_tiled(R, hb, bias, d, E, T, parts, nullptr, nullptr, s);
         if (rc != -EINVAL) return rc;
     }
