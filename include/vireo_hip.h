@@ -214,6 +214,21 @@ int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const
  * routing is unaffected. */
 int vireo_hip_set_path(int path);
 
+/* Decode-batch calls (8 to 63 tokens) on a pinned layer with Q4_K gate/up and
+ * Q6_K down run on the matrix cores, whose loads read 16 rows of a matrix at
+ * a time. With packing on (the default), the first such call on a layer that
+ * may allocate (not moe_ffn_forward_noalloc, not under graph capture) copies
+ * the layer's experts once into tiles of 16 rows x one super-block, the same
+ * bytes reordered so that every load instruction reads 1 KB of consecutive
+ * memory; later calls read the copy. The copy is device memory outside the
+ * store's capacity (as much again as the layer's expert bytes), made from the
+ * pinned views and freed with the pin (expert_store_unpin_layer) or the store;
+ * a caller that rewrites a pinned layer's expert bytes in place must unpin
+ * and pin it again. Results are the same bit for bit either way. 0 turns it
+ * off for later calls (existing copies stay until unpinned). No counterpart in
+ * the reference. */
+int vireo_hip_set_packed(int on);
+
 /* The one-token decode plan of moe_ffn_forward as separate launches over a
  * caller-owned device `state` buffer of moe_decode_state_bytes(m) bytes (no
  * counterpart in the reference, whose moe_ffn is one function):

@@ -142,6 +142,33 @@ def test_decode_batch_matrix_cores(cuda, oracle, path, T, plan):
     m.close()
 
 
+@pytest.mark.parametrize("T", [8, 40])
+def test_decode_batch_packed_tiles(cuda, T):
+    """The matrix-core decode batch on a pinned layer reads its experts from a
+    copy in 16-row tiles made by the first call with packing on: the same
+    bytes reordered, so the outputs equal the GGUF-row kernels' bit for bit,
+    on the call that makes the copy and on the next one. The test layer
+    leaves two experts unregistered (NULL in both tables)."""
+    lib = _lib.load()
+    shape = W.MoEShape("mdec-8e", 2048, 8, 4, 768, True, W.Q4_K, W.Q4_K, W.Q6_K)
+    m = M.DeviceMoE(shape, 1, seed=61, unregistered={(0, 2), (0, 5)})
+    x, hb = W.host_hidden(shape.d, T, 61)
+    hbt = torch.from_numpy(hb).to(cuda)
+    outs = []
+    try:
+        for packed in (0, 1, 1):
+            _lib.check(lib.vireo_hip_set_packed(packed), "vireo_hip_set_packed")
+            xt = torch.from_numpy(x).to(cuda)
+            m.forward(0, xt, hbt)
+            outs.append(xt.cpu().numpy())
+    finally:
+        lib.vireo_hip_set_packed(1)
+    assert np.abs(outs[0] - x).max() > 0  # the layer contributed
+    np.testing.assert_array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32))
+    np.testing.assert_array_equal(outs[2].view(np.uint32), outs[0].view(np.uint32))
+    m.close()
+
+
 @pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
 def test_golden_moe_on_gpu(cuda, case):
     g = golden(f"moe_{case}.npz")

@@ -191,6 +191,7 @@ SIGNATURES = {
     "moe_route": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_dispatch": (C.c_int, [c_vp, C.c_int, C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp]),
     "vireo_hip_set_path": (C.c_int, [C.c_int]),
+    "vireo_hip_set_packed": (C.c_int, [C.c_int]),
     "moe_decode_state_bytes": (C.c_int64, [C.POINTER(MoEModel)]),
     "moe_decode_stage": (C.c_int, [C.POINTER(MoEModel), C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_decode_stage_timed": (C.c_int, [C.POINTER(MoEModel), C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp, C.c_int64,

@@ -115,6 +115,7 @@ struct ExpertStore {
     void *stage;               /* pinned staging for synchronous pread */
     size_t stage_bytes;
     void **tables;             /* per layer: device [n_experts x 3] pointer table */
+    void **ptables, **pbufs;   /* per pinned layer: its experts in 16-row tiles (a second copy) and their table */
     FreeBlock *freel;          /* device blocks of evicted experts, kept for reuse */
     int nfree, capfree;
     uint8_t *arena;            /* one allocation the pool's blocks are cut from (bounded pools) */
@@ -162,7 +163,12 @@ static ExpertStore *store_new(int n_layers, int n_experts, uint64_t capacity_byt
     s->n_slots = n_layers * n_experts;
     s->slots = calloc((size_t)s->n_slots, sizeof(Slot));
     s->tables = calloc((size_t)n_layers, sizeof(void *));
-    if (!s->slots || !s->tables) { free(s->slots); free(s->tables); free(s); return NULL; }
+    s->ptables = calloc((size_t)n_layers, sizeof(void *));
+    s->pbufs = calloc((size_t)n_layers, sizeof(void *));
+    if (!s->slots || !s->tables || !s->ptables || !s->pbufs) {
+        free(s->slots); free(s->tables); free(s->ptables); free(s->pbufs); free(s);
+        return NULL;
+    }
     s->capacity_bytes = capacity_bytes;
     for (int i = 0; i < s->n_slots; i++)
         s->slots[i].lru_prev = s->slots[i].lru_next = s->slots[i].ref_prev = s->slots[i].ref_next = -1;
@@ -772,6 +778,9 @@ int expert_store_unpin_layer(ExpertStore *s, int layer) {
     if (hipDeviceSynchronize() != hipSuccess) return -EIO;
     (void)hipFree(s->tables[layer]);
     s->tables[layer] = NULL;
+    if (s->ptables[layer]) (void)hipFree(s->ptables[layer]);
+    if (s->pbufs[layer]) (void)hipFree(s->pbufs[layer]);
+    s->ptables[layer] = s->pbufs[layer] = NULL;
     for (int e = 0; e < s->n_experts; e++) {
         Slot *sl = slot_at(s, layer, e);
         if (sl->pinned) { sl->pinned = 0; if (sl->lease > 0) sl->lease--; }
@@ -784,7 +793,11 @@ void expert_store_destroy(ExpertStore *s) {
     s->magic = 0;
     readers_stop(s);
     (void)hipDeviceSynchronize();
-    for (int l = 0; l < s->n_layers; l++) if (s->tables[l]) (void)hipFree(s->tables[l]);
+    for (int l = 0; l < s->n_layers; l++) {
+        if (s->tables[l]) (void)hipFree(s->tables[l]);
+        if (s->ptables[l]) (void)hipFree(s->ptables[l]);
+        if (s->pbufs[l]) (void)hipFree(s->pbufs[l]);
+    }
     for (int i = 0; i < s->n_slots; i++) {
         if (s->slots[i].dev) block_free(s, s->slots[i].dev);
         if (s->slots[i].busy) (void)hipEventDestroy(s->slots[i].busy);
@@ -806,6 +819,8 @@ void expert_store_destroy(ExpertStore *s) {
     if (s->stage) (void)hipHostFree(s->stage);
     free(s->freel);
     free(s->tables);
+    free(s->ptables);
+    free(s->pbufs);
     free(s->slots);
     free(s);
 }
@@ -828,6 +843,23 @@ int vh_store_valid(const ExpertStore *s) { return store_ok(s); }
 const void *const *vh_store_layer_table(const ExpertStore *s, int layer) {
     if (!store_ok(s) || layer < 0 || layer >= s->n_layers) return NULL;
     return (const void *const *)s->tables[layer];
+}
+
+/* A pinned layer's experts in the matrix-core decode batch's 16-row tiles:
+ * their device table, or NULL (never allocates). vh_store_set_packed hands
+ * the store a copy made for a pinned layer (buf: one device allocation,
+ * tab: device [n_experts x 3] table into it); the store frees both when the
+ * layer is unpinned or the store destroyed. -EINVAL (the caller keeps them)
+ * when the layer is not pinned or already has one. */
+const void *const *vh_store_packed_table(const ExpertStore *s, int layer) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || !s->tables[layer]) return NULL;
+    return (const void *const *)s->ptables[layer];
+}
+int vh_store_set_packed(ExpertStore *s, int layer, void *buf, void *tab) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || !s->tables[layer] || s->ptables[layer]) return -EINVAL;
+    s->pbufs[layer] = buf;
+    s->ptables[layer] = tab;
+    return 0;
 }
 
 /* 1 when every registered expert of every layer fits the capacity at once:

@@ -27,6 +27,9 @@ namespace {
 // 0 auto, 1 decode plan when possible, 2 grouped plan, 3 decode plan with the
 // fused experts kernel, 4 grouped plan without the matrix-core GEMMs
 int g_path = 0;
+// 1: a pinned layer's first matrix-core decode-batch call copies its experts
+// into 16-row tiles (vh_mdec_pack_layer) that later calls read; 0: GGUF rows
+int g_packed = 1;
 // From this many tokens on, every logit is the reference's exact sequential
 // fp32 sum (route_exact_kernel): its latency, one chain of 2 d dependent
 // operations, is then hidden by the chains of many tokens. Fewer tokens take
@@ -397,6 +400,34 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
     return rc;
 }
 
+// The tiled copy of a pinned layer's experts for the matrix-core decode batch,
+// made on the first call that may allocate (never under graph capture) and
+// held by the store with the pin; NULL: read the GGUF rows.
+const void *const *packed_table(const vireo_moe_model *m, int layer, const void *const *table, bool may_alloc,
+                                hipStream_t s) {
+    if (!g_packed) return nullptr;
+    const void *const *pt = vh_store_packed_table(m->es, layer);
+    if (pt || !may_alloc) return pt;
+    void *buf = nullptr, *tab = nullptr;
+    if (vh_mdec_pack_layer(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s)) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (vh_store_set_packed(m->es, layer, buf, tab)) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(tab);
+        (void)hipFree(buf);
+        return nullptr;
+    }
+    return static_cast<const void *const *>(tab);
+}
+
+extern "C" int vireo_hip_set_packed(int on) {
+    if (on != 0 && on != 1) return -EINVAL;
+    g_packed = on;
+    return 0;
+}
+
 extern "C" int vireo_hip_set_path(int path) {
     if (path < 0 || path > 5) return -EINVAL;
     g_path = path;
@@ -585,10 +616,10 @@ int paged_forward(const vireo_moe_model *m, int layer, float *x, const float *hb
             if (!rc) rc = vh_check(hipMemcpyAsync(dt, tab, tab_n * sizeof(void *), hipMemcpyHostToDevice, s));
             if (!rc) rc = vh_check(hipMemcpyAsync(da, act, act_n * 4, hipMemcpyHostToDevice, s));
             if (mdec) {
-                if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, da, dt, ws.xp, ws.xsc, n_tokens, d, fe, k,
-                                             E, slots, n_tokens, ws.h, s);
-                if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens,
-                                           ws.ybuf, s);
+                if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, da, dt, false, ws.xp, ws.xsc, n_tokens, d,
+                                             fe, k, E, slots, n_tokens, ws.h, s);
+                if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, da, dt, false, ws.h, d, fe, E, slots,
+                                           n_tokens, ws.ybuf, s);
             } else if (gdec) {
                 if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, da, dt, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
                 if (!rc) rc = vh_gdec_down(td, ws.counts, ws.offs, ws.perm, da, dt, ws.h, d, fe, E, slots, n_tokens, ws.ybuf, s);
@@ -696,10 +727,12 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     } else if (mdec) {
         // calls of a decode batch's size, Q4_K_M experts: the matrix cores
         if (!rc && !prepped) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
-        if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, table, ws.xp, ws.xsc, n_tokens, d, fe,
-                                     k, E, slots, n_tokens, ws.h, s);
-        if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, n_tokens,
-                                   ws.ybuf, s);
+        const void *const *pt = rc ? nullptr : packed_table(m, layer, table, !src, s);
+        const void *const *tb = pt ? pt : table;
+        if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, tb, pt != nullptr, ws.xp, ws.xsc,
+                                     n_tokens, d, fe, k, E, slots, n_tokens, ws.h, s);
+        if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, tb, pt != nullptr, ws.h, d, fe, E, slots,
+                                   n_tokens, ws.ybuf, s);
     } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
         // calls of a decode batch's size (a few tokens per group): inputs in registers
         if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, n_tokens, ws.h, s);

@@ -46,6 +46,7 @@
 // any even address; their 16-byte loads rely on global memory accepting any
 // alignment.
 #include <hip/hip_runtime.h>
+#include <vector>
 #include "common.h"
 #include "qdecode.h"
 #include "route.h"
@@ -275,6 +276,63 @@ __global__ void __launch_bounds__(256) mdec_route_prep_kernel(const float *__res
     }
 }
 
+// The experts of a pinned layer can be copied once into 16-row tiles, so that
+// every load instruction of the gate/up and down kernels reads 1 KB of
+// consecutive bytes (the GGUF rows give each instruction 16 rows' short
+// pieces: half the rate from HBM). Tile (G, b) of a matrix - rows 16 G ..
+// 16 G + 15, super-block b - sits at (G * nb + b) * tile bytes; its bytes are
+// the rows' own, reordered so that lane l = r + 16 g of a wave loads 16
+// consecutive bytes from each part:
+//   Q4_K (2304 bytes): the 16 rows' headers (d, dmin, scales; row r at 16 r),
+//     then qs bytes 32 g .. 32 g + 15 of row r at 256 + 16 l, then qs bytes
+//     32 g + 16 .. 32 g + 31 at 1280 + 16 l;
+//   Q6_K (3360 bytes): ql bytes 16 g .. of row r at 16 l, ql bytes 64 + 16 g
+//     .. at 1024 + 16 l, qh bytes 16 g .. at 2048 + 16 l, the rows' scales
+//     (16 bytes each) at 3072 + 16 r, their d at 3328 + 2 r.
+constexpr int kQ4Tile = 16 * 144, kQ6Tile = 16 * 210;
+
+// the byte of row `row`'s super-block that tile byte o (even) holds
+VH_DEV int pk_src_q4k(int o, int &row) {
+    if (o < 256) {
+        row = o >> 4;
+        return o & 15;
+    }
+    const int q = o < 1280 ? o - 256 : o - 1280, L = q >> 4;
+    row = L & 15;
+    return (o < 1280 ? 16 : 32) + 32 * (L >> 4) + (q & 15);
+}
+VH_DEV int pk_src_q6k(int o, int &row) {
+    if (o < 3072) {
+        const int q = o & 1023, L = q >> 4;
+        row = L & 15;
+        return (o < 1024 ? 0 : o < 2048 ? 64 : 128) + 16 * (L >> 4) + (q & 15);
+    }
+    if (o < 3328) {
+        row = (o - 3072) >> 4;
+        return 192 + ((o - 3072) & 15);
+    }
+    row = (o - 3328) >> 1;
+    return 208 + ((o - 3328) & 1);
+}
+
+// one workgroup per (tile, expert) of matrix `which` (0 gate, 1 up, 2 down),
+// two bytes per thread and step (every field is at an even offset)
+template <int SB, int TB>
+__global__ void __launch_bounds__(256) mdec_pack_kernel(const void *const *__restrict__ src_tab,
+                                                        void *const *__restrict__ dst_tab, int which, int nb,
+                                                        int64_t row_bytes) {
+    const int e = blockIdx.y, tile = blockIdx.x, G = tile / nb, b = tile - G * nb;
+    const uint8_t *src = static_cast<const uint8_t *>(src_tab[3 * e + which]);
+    uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + which]);
+    if (!src || !dst) return;
+    for (int o = 2 * int(threadIdx.x); o < TB; o += 512) {
+        int row;
+        const int off = SB == 144 ? pk_src_q4k(o, row) : pk_src_q6k(o, row);
+        const uint16_t v = *reinterpret_cast<const uint16_t *>(src + int64_t(16 * G + row) * row_bytes + SB * b + off);
+        *reinterpret_cast<uint16_t *>(dst + int64_t(tile) * TB + o) = v;
+    }
+}
+
 // gate/up: wave w of workgroup (c, s, z) owns rows 64 c + 16 w .. + 15 of gate
 // and up of expert active[s] for tokens 16 z .. of its group, and writes
 // h = silu(gate . x) * (up . x) (src/gguf_run.c:205-207) as bf16 hi + lo parts
@@ -288,7 +346,7 @@ __global__ void __launch_bounds__(256) mdec_route_prep_kernel(const float *__res
 constexpr int kGuTokStride = 260;  // dwords per token and super-block in LDS: 256 + 4 (no bank conflicts)
 constexpr int kGuMaxBlocks = 8;    // d <= 2048
 
-template <int NB>
+template <int NB, bool PK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) mdec_gateup_kernel(const int32_t *__restrict__ counts,
                                                           const int32_t *__restrict__ offs,
                                                           const int32_t *__restrict__ perm,
@@ -334,8 +392,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
     uint32_t *xdst = &xs[0][pt * kGuTokStride + 4 * pc];
     // this lane's token (row r of the input operand) in the sub-block sums
     const uint2 *xsr = xsum + size_t(perm[base + t0 + min(r, tn - 1)] / k) * NB * 4 + g;
-    gbyte *gr = G + int64_t(o) * row_bytes;
-    gbyte *ur = U + int64_t(o) * row_bytes;
+    // PK: the wave's 16-row group's tiles (see mdec_pack_kernel); else its rows
+    gbyte *gr = PK ? G + int64_t(o - r) / 16 * NB * kQ4Tile : G + int64_t(o) * row_bytes;
+    gbyte *ur = PK ? U + int64_t(o - r) / 16 * NB * kQ4Tile : U + int64_t(o) * row_bytes;
     struct Wt {
         uint4 hd, q0, q1;
     };
@@ -344,14 +403,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
         uint2 xsm;
     };
     auto load = [&](int b, Blk &w) {
-        gbyte *p = gr + 144 * b;
-        w.gw.hd = ld_u128(p);
-        w.gw.q0 = ld_u128(p + 16 + 32 * g);
-        w.gw.q1 = ld_u128(p + 32 + 32 * g);
-        p = ur + 144 * b;
-        w.uw.hd = ld_u128(p);
-        w.uw.q0 = ld_u128(p + 16 + 32 * g);
-        w.uw.q1 = ld_u128(p + 32 + 32 * g);
+        if constexpr (PK) {  // three 1 KB-wide loads per matrix: headers, first and second 16 qs bytes
+            gbyte *p = gr + kQ4Tile * b;
+            w.gw.hd = ld_u128(p + 16 * r);
+            w.gw.q0 = ld_u128(p + 256 + 16 * lane);
+            w.gw.q1 = ld_u128(p + 1280 + 16 * lane);
+            p = ur + kQ4Tile * b;
+            w.uw.hd = ld_u128(p + 16 * r);
+            w.uw.q0 = ld_u128(p + 256 + 16 * lane);
+            w.uw.q1 = ld_u128(p + 1280 + 16 * lane);
+        } else {
+            gbyte *p = gr + 144 * b;
+            w.gw.hd = ld_u128(p);
+            w.gw.q0 = ld_u128(p + 16 + 32 * g);
+            w.gw.q1 = ld_u128(p + 32 + 32 * g);
+            p = ur + 144 * b;
+            w.uw.hd = ld_u128(p);
+            w.uw.q0 = ld_u128(p + 16 + 32 * g);
+            w.uw.q1 = ld_u128(p + 32 + 32 * g);
+        }
         w.xsm = xsr[4 * b];
     };
     Blk blk[3];
@@ -474,6 +544,7 @@ constexpr int kDnRowStride = 52;  // dwords per weight row in LDS: 32 ql + 16 qh
 constexpr int kDnMaxBlocks = 4;   // fe <= 1024
 constexpr int kDnWaves = 8;
 
+template <bool PK>
 __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t *__restrict__ counts,
                                                                   const int32_t *__restrict__ offs,
                                                                   const int32_t *__restrict__ perm,
@@ -500,12 +571,21 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
 #pragma unroll
     for (int b = 0; b < kDnMaxBlocks; b++) {
         if (b >= nb) break;
-        gbyte *p = row + 210 * b;
-        a0[b] = ld_u128(p + 16 * g);
-        a1[b] = ld_u128(p + 64 + 16 * g);
-        qq[b] = ld_u128(p + 128 + 16 * g);
-        scb[b] = ld_u128(p + 192);
-        ddb[b] = ld_u16(p + 208);
+        if constexpr (PK) {  // the wave's tile of super-block b: 1 KB-wide loads of ql, ql, qh, then scales and d
+            gbyte *p = D + (int64_t(o0 / 16) * nb + b) * kQ6Tile;
+            a0[b] = ld_u128(p + 16 * lane);
+            a1[b] = ld_u128(p + 1024 + 16 * lane);
+            qq[b] = ld_u128(p + 2048 + 16 * lane);
+            scb[b] = ld_u128(p + 3072 + 16 * r);
+            ddb[b] = ld_u16(p + 3328 + 2 * r);
+        } else {
+            gbyte *p = row + 210 * b;
+            a0[b] = ld_u128(p + 16 * g);
+            a1[b] = ld_u128(p + 64 + 16 * g);
+            qq[b] = ld_u128(p + 128 + 16 * g);
+            scb[b] = ld_u128(p + 192);
+            ddb[b] = ld_u16(p + 208);
+        }
     }
     // the tile's activations: token i's fe / 4 pieces of 16 bytes
     const int hstride = fe + 4, npc = fe / 4;
@@ -595,8 +675,8 @@ int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_
 }
 
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                   const void *const *table, const void *xp, const float *xsc, int T, int d, int fe, int k, int E,
-                   int max_slots, int max_count, void *hp, hipStream_t s) {
+                   const void *const *table, bool packed, const void *xp, const float *xsc, int T, int d, int fe,
+                   int k, int E, int max_slots, int max_count, void *hp, hipStream_t s) {
     if (max_count < 1 || T < 1 || d % 256 || d > 256 * kGuMaxBlocks || fe % 16) return -EINVAL;
     const dim3 g((fe + 63) / 64, max_slots, (max_count + kTok - 1) / kTok);
     const uint4 *x4 = static_cast<const uint4 *>(xp);
@@ -605,8 +685,12 @@ int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *pe
     uint16_t *h = static_cast<uint16_t *>(hp);
 #define VH_GU(NB)                                                                                                  \
     case NB:                                                                                                       \
-        hipLaunchKernelGGL(mdec_gateup_kernel<NB>, g, dim3(256), 0, s, counts, offs, perm, active, table, x4, xsc, \
-                           xs, fe, k, E, rb, h);                                                                   \
+        if (packed)                                                                                                \
+            hipLaunchKernelGGL((mdec_gateup_kernel<NB, true>), g, dim3(256), 0, s, counts, offs, perm, active,    \
+                               table, x4, xsc, xs, fe, k, E, rb, h);                                               \
+        else                                                                                                       \
+            hipLaunchKernelGGL((mdec_gateup_kernel<NB, false>), g, dim3(256), 0, s, counts, offs, perm, active,   \
+                               table, x4, xsc, xs, fe, k, E, rb, h);                                               \
         break;
     switch (d / 256) {
         VH_GU(1) VH_GU(2) VH_GU(3) VH_GU(4) VH_GU(5) VH_GU(6) VH_GU(7) VH_GU(8)
@@ -616,20 +700,73 @@ int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *pe
 }
 
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                 const void *const *table, const void *hp, int d, int fe, int E, int max_slots, int max_count,
-                 float *ybuf, hipStream_t s) {
+                 const void *const *table, bool packed, const void *hp, int d, int fe, int E, int max_slots,
+                 int max_count, float *ybuf, hipStream_t s) {
     if (max_count < 1 || d % 16 || fe % 256 || fe > 256 * kDnMaxBlocks) return -EINVAL;
     const dim3 g((d + 16 * kDnWaves - 1) / (16 * kDnWaves), max_slots, (max_count + kTok - 1) / kTok);
     const size_t lds = size_t(kTok) * (fe + 4) * 4;
     static bool attr = false;  // dynamic LDS above the default limit: raised once per process
     if (!attr) {
-        if (int rc = vh_check(hipFuncSetAttribute(reinterpret_cast<const void *>(&mdec_down_kernel),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024)))
-            return rc;
+        for (const void *f : {reinterpret_cast<const void *>(&mdec_down_kernel<true>),
+                              reinterpret_cast<const void *>(&mdec_down_kernel<false>)})
+            if (int rc = vh_check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024)))
+                return rc;
         attr = true;
     }
     if (lds > 96 * 1024) return -EINVAL;
-    hipLaunchKernelGGL(mdec_down_kernel, g, dim3(64 * kDnWaves), lds, s, counts, offs, perm, active, table,
-                       static_cast<const uint4 *>(hp), fe, d, E, vh_row_bytes(VT_Q6_K, fe), ybuf);
+    const uint4 *h4 = static_cast<const uint4 *>(hp);
+    const int64_t rb = vh_row_bytes(VT_Q6_K, fe);
+    if (packed)
+        hipLaunchKernelGGL(mdec_down_kernel<true>, g, dim3(64 * kDnWaves), lds, s, counts, offs, perm, active, table,
+                           h4, fe, d, E, rb, ybuf);
+    else
+        hipLaunchKernelGGL(mdec_down_kernel<false>, g, dim3(64 * kDnWaves), lds, s, counts, offs, perm, active,
+                           table, h4, fe, d, E, rb, ybuf);
     return vh_check(hipGetLastError());
+}
+
+int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out,
+                       hipStream_t s) {
+    *buf_out = *tab_out = nullptr;
+    if (E < 1 || d % 256 || fe % 256) return -EINVAL;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
+    if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
+    const int64_t rg = vh_row_bytes(VT_Q4_K, d), rd = vh_row_bytes(VT_Q6_K, fe);
+    const size_t gb = size_t(fe) * rg, db = size_t(d) * rd, per = 2 * gb + db;
+    std::vector<const void *> src(size_t(3) * E), dst(size_t(3) * E, nullptr);
+    if (int rc = vh_check(hipMemcpyAsync(src.data(), table, src.size() * sizeof(void *), hipMemcpyDeviceToHost, s)))
+        return rc;
+    if (int rc = vh_check(hipStreamSynchronize(s))) return rc;
+    void *buf = nullptr, *tab = nullptr;
+    if (hipMalloc(&buf, per * E) != hipSuccess) return -ENOMEM;
+    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) {
+        (void)hipFree(buf);
+        return -ENOMEM;
+    }
+    char *b = static_cast<char *>(buf);
+    for (int e = 0; e < E; e++) {
+        if (!src[3 * e] || !src[3 * e + 1] || !src[3 * e + 2]) continue;  // unregistered: stays NULL
+        dst[3 * e] = b + per * e;
+        dst[3 * e + 1] = b + per * e + gb;
+        dst[3 * e + 2] = b + per * e + 2 * gb;
+    }
+    int rc = vh_check(hipMemcpy(tab, dst.data(), dst.size() * sizeof(void *), hipMemcpyHostToDevice));
+    if (!rc) {
+        void *const *dt = static_cast<void *const *>(tab);
+        const dim3 gg(fe / 16 * (d / 256), E), gd(d / 16 * (fe / 256), E);
+        hipLaunchKernelGGL((mdec_pack_kernel<144, kQ4Tile>), gg, dim3(256), 0, s, table, dt, 0, d / 256, rg);
+        hipLaunchKernelGGL((mdec_pack_kernel<144, kQ4Tile>), gg, dim3(256), 0, s, table, dt, 1, d / 256, rg);
+        hipLaunchKernelGGL((mdec_pack_kernel<210, kQ6Tile>), gd, dim3(256), 0, s, table, dt, 2, fe / 256, rd);
+        rc = vh_check(hipGetLastError());
+    }
+    if (rc) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(tab);
+        (void)hipFree(buf);
+        return rc;
+    }
+    *buf_out = buf;
+    *tab_out = tab;
+    return 0;
 }

@@ -19,7 +19,9 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
 // ExpertStore internals for the MoE plans (expert_store.c): an expert's bytes
 // in the pool (0 if unregistered), the capacity (0 = unbounded), whether a
 // store is one of this library's, a pinned layer's table (NULL if none; never
-// allocates), whether every layer fits at once, the bytes that hold leases,
+// allocates) and its copy in the decode batch's 16-row tiles (held and freed
+// by the store with the pin), whether every layer fits at once, the bytes
+// that hold leases,
 // lookups / lease drops for paged calls (page-ins on a copy stream, blocks
 // protected by events until the kernels that read them are done), and the
 // routing copies that feed the reference's statistics.
@@ -28,6 +30,8 @@ uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert);
 uint64_t vh_store_capacity(const ExpertStore *s);
 int vh_store_valid(const ExpertStore *s);
 const void *const *vh_store_layer_table(const ExpertStore *s, int layer);
+const void *const *vh_store_packed_table(const ExpertStore *s, int layer);
+int vh_store_set_packed(ExpertStore *s, int layer, void *buf, void *tab);
 int vh_store_fits_all(const ExpertStore *s);
 uint64_t vh_store_leased_bytes(const ExpertStore *s);
 int vh_store_acquire(ExpertStore *s, int layer, int expert, ExpertView *view, hipStream_t cs);
@@ -125,12 +129,19 @@ bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe);
 int vh_route_parts_tiled(const float *R, const float *hb, const float *bias, int d, int E, int T, RoutePart *parts,
                          void *xp, float *xsc, hipStream_t s);
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s);
+// `packed`: table points at vh_mdec_pack_layer's tiles instead of GGUF rows.
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                   const void *const *table, const void *xp, const float *xsc, int T, int d, int fe, int k, int E,
-                   int max_slots, int max_count, void *hp, hipStream_t s);
+                   const void *const *table, bool packed, const void *xp, const float *xsc, int T, int d, int fe,
+                   int k, int E, int max_slots, int max_count, void *hp, hipStream_t s);
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
-                 const void *const *table, const void *hp, int d, int fe, int E, int max_slots, int max_count,
-                 float *ybuf, hipStream_t s);
+                 const void *const *table, bool packed, const void *hp, int d, int fe, int E, int max_slots,
+                 int max_count, float *ybuf, hipStream_t s);
+// A copy of the experts behind `table` (device [E x 3]: Q4_K gate, up; Q6_K
+// down) in the decode batch's 16-row tiles: buf_out, one allocation, and
+// tab_out, its device table (NULL where table is). Enqueued on s after a
+// synchronizing read of the table; -EBUSY while s is being captured.
+int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out,
+                       hipStream_t s);
 
 // Matrix-core grouped GEMMs (moe_mfma.hip) for the groups of calls of at
 // least kMfmaMinCall tokens. vh_mfma_plan lists the token tiles of groups of
