@@ -283,24 +283,18 @@ __global__ void __launch_bounds__(256) mdec_route_prep_kernel(const float *__res
 // 16 G + 15, super-block b - sits at (G * nb + b) * tile bytes; its bytes are
 // the rows' own, reordered so that lane l = r + 16 g of a wave loads 16
 // consecutive bytes from each part:
-//   Q4_K (2304 bytes): the 16 rows' headers (d, dmin, scales; row r at 16 r),
-//     then qs bytes 32 g .. 32 g + 15 of row r at 256 + 16 l, then qs bytes
-//     32 g + 16 .. 32 g + 31 at 1280 + 16 l;
+//   Q4_K (2368 bytes): the 16 rows' d and dmin (4 bytes, row r at 4 r), then
+//     lane l's four 6-bit scales and mins, decoded once - sc and m of
+//     sub-blocks 2 g and 2 g + 1 of row r, one byte each - at 64 + 4 l, then
+//     qs bytes 32 g .. 32 g + 15 of row r at 320 + 16 l, then qs bytes 32 g +
+//     16 .. 32 g + 31 at 1344 + 16 l (64 bytes more than the rows: the
+//     kernel's scale decoding is gone);
 //   Q6_K (3360 bytes): ql bytes 16 g .. of row r at 16 l, ql bytes 64 + 16 g
 //     .. at 1024 + 16 l, qh bytes 16 g .. at 2048 + 16 l, the rows' scales
 //     (16 bytes each) at 3072 + 16 r, their d at 3328 + 2 r.
-constexpr int kQ4Tile = 16 * 144, kQ6Tile = 16 * 210;
+constexpr int kQ4Tile = 2368, kQ6Tile = 16 * 210;
 
-// the byte of row `row`'s super-block that tile byte o (even) holds
-VH_DEV int pk_src_q4k(int o, int &row) {
-    if (o < 256) {
-        row = o >> 4;
-        return o & 15;
-    }
-    const int q = o < 1280 ? o - 256 : o - 1280, L = q >> 4;
-    row = L & 15;
-    return (o < 1280 ? 16 : 32) + 32 * (L >> 4) + (q & 15);
-}
+// the byte of row `row`'s super-block that Q6_K tile byte o (even) holds
 VH_DEV int pk_src_q6k(int o, int &row) {
     if (o < 3072) {
         const int q = o & 1023, L = q >> 4;
@@ -315,21 +309,47 @@ VH_DEV int pk_src_q6k(int o, int &row) {
     return 208 + ((o - 3328) & 1);
 }
 
-// one workgroup per (tile, expert) of matrix `which` (0 gate, 1 up, 2 down),
-// two bytes per thread and step (every field is at an even offset)
-template <int SB, int TB>
-__global__ void __launch_bounds__(256) mdec_pack_kernel(const void *const *__restrict__ src_tab,
-                                                        void *const *__restrict__ dst_tab, int which, int nb,
-                                                        int64_t row_bytes) {
+// One workgroup per (tile, expert) of matrix `which` (0 gate, 1 up, 2 down).
+// Q6_K: two bytes per thread and step (every field is at an even offset).
+__global__ void __launch_bounds__(256) mdec_pack_q6k_kernel(const void *const *__restrict__ src_tab,
+                                                            void *const *__restrict__ dst_tab, int which, int nb,
+                                                            int64_t row_bytes) {
     const int e = blockIdx.y, tile = blockIdx.x, G = tile / nb, b = tile - G * nb;
     const uint8_t *src = static_cast<const uint8_t *>(src_tab[3 * e + which]);
     uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + which]);
     if (!src || !dst) return;
-    for (int o = 2 * int(threadIdx.x); o < TB; o += 512) {
+    for (int o = 2 * int(threadIdx.x); o < kQ6Tile; o += 512) {
         int row;
-        const int off = SB == 144 ? pk_src_q4k(o, row) : pk_src_q6k(o, row);
-        const uint16_t v = *reinterpret_cast<const uint16_t *>(src + int64_t(16 * G + row) * row_bytes + SB * b + off);
-        *reinterpret_cast<uint16_t *>(dst + int64_t(tile) * TB + o) = v;
+        const int off = pk_src_q6k(o, row);
+        const uint16_t v = *reinterpret_cast<const uint16_t *>(src + int64_t(16 * G + row) * row_bytes + 210 * b + off);
+        *reinterpret_cast<uint16_t *>(dst + int64_t(tile) * kQ6Tile + o) = v;
+    }
+}
+// Q4_K: threads 0-15 copy row t's d and dmin, 16-79 decode lane t - 16's
+// scales and mins (q4k_scale_min_v, as the kernels did), 80-207 copy the qs
+// pieces (16-byte aligned: Q4_K rows are 144 bytes per super-block).
+__global__ void __launch_bounds__(256) mdec_pack_q4k_kernel(const void *const *__restrict__ src_tab,
+                                                            void *const *__restrict__ dst_tab, int which, int nb,
+                                                            int64_t row_bytes) {
+    const int e = blockIdx.y, tile = blockIdx.x, G = tile / nb, b = tile - G * nb, t = threadIdx.x;
+    const uint8_t *src = static_cast<const uint8_t *>(src_tab[3 * e + which]);
+    uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + which]) + int64_t(tile) * kQ4Tile;
+    if (!src || !dst) return;
+    auto blk = [&](int row) { return src + int64_t(16 * G + row) * row_bytes + 144 * b; };
+    if (t < 16) {
+        *reinterpret_cast<uint32_t *>(dst + 4 * t) = *reinterpret_cast<const uint32_t *>(blk(t));
+    } else if (t < 80) {
+        const int l = t - 16, r = l & 15, g = l >> 4;
+        const uint32_t *h = reinterpret_cast<const uint32_t *>(blk(r));
+        int sc0, mn0, sc1, mn1;
+        q4k_scale_min_v(2 * g, h[1], h[2], h[3], sc0, mn0);
+        q4k_scale_min_v(2 * g + 1, h[1], h[2], h[3], sc1, mn1);
+        *reinterpret_cast<uint32_t *>(dst + 64 + 4 * l) =
+            uint32_t(sc0) | (uint32_t(sc1) << 8) | (uint32_t(mn0) << 16) | (uint32_t(mn1) << 24);
+    } else if (t < 208) {
+        const int P = t - 80, l = P & 63, r = l & 15, g = l >> 4, second = P >> 6;
+        *reinterpret_cast<uint4 *>(dst + (second ? 1344 : 320) + 16 * l) =
+            *reinterpret_cast<const uint4 *>(blk(r) + (second ? 32 : 16) + 32 * g);
     }
 }
 
@@ -403,15 +423,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
         uint2 xsm;
     };
     auto load = [&](int b, Blk &w) {
-        if constexpr (PK) {  // three 1 KB-wide loads per matrix: headers, first and second 16 qs bytes
+        if constexpr (PK) {  // per matrix: d and dmin, the decoded scales, two 1 KB-wide qs loads
             gbyte *p = gr + kQ4Tile * b;
-            w.gw.hd = ld_u128(p + 16 * r);
-            w.gw.q0 = ld_u128(p + 256 + 16 * lane);
-            w.gw.q1 = ld_u128(p + 1280 + 16 * lane);
+            w.gw.hd = make_uint4(ld_u32(p + 4 * r), ld_u32(p + 64 + 4 * lane), 0u, 0u);
+            w.gw.q0 = ld_u128(p + 320 + 16 * lane);
+            w.gw.q1 = ld_u128(p + 1344 + 16 * lane);
             p = ur + kQ4Tile * b;
-            w.uw.hd = ld_u128(p + 16 * r);
-            w.uw.q0 = ld_u128(p + 256 + 16 * lane);
-            w.uw.q1 = ld_u128(p + 1280 + 16 * lane);
+            w.uw.hd = make_uint4(ld_u32(p + 4 * r), ld_u32(p + 64 + 4 * lane), 0u, 0u);
+            w.uw.q0 = ld_u128(p + 320 + 16 * lane);
+            w.uw.q1 = ld_u128(p + 1344 + 16 * lane);
         } else {
             gbyte *p = gr + 144 * b;
             w.gw.hd = ld_u128(p);
@@ -470,8 +490,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
         // the min operand m_2g, m_2g, m_2g+1, m_2g+1 against the sums' slots
         auto scales = [&](const uint4 &hd, f16x2 &s0, f16x2 &n0, f16x2 &s1, f16x2 &n1, f16x8 &mop) {
             int sc0, mn0, sc1, mn1;
-            q4k_scale_min_v(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
-            q4k_scale_min_v(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
+            if constexpr (PK) {  // decoded when the tiles were made
+                sc0 = int(hd.y & 0xffu);
+                sc1 = int((hd.y >> 8) & 0xffu);
+                mn0 = int((hd.y >> 16) & 0xffu);
+                mn1 = int(hd.y >> 24);
+            } else {
+                q4k_scale_min_v(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
+                q4k_scale_min_v(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
+            }
             const _Float16 a0 = _Float16(sc0), a1 = _Float16(float(sc1) * 0.0625f);
             const _Float16 m0 = _Float16(mn0), m1 = _Float16(mn1), z = _Float16(0.0f);
             s0 = f16x2{a0, a0};
@@ -733,7 +760,7 @@ int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **bu
     if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
     if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
     const int64_t rg = vh_row_bytes(VT_Q4_K, d), rd = vh_row_bytes(VT_Q6_K, fe);
-    const size_t gb = size_t(fe) * rg, db = size_t(d) * rd, per = 2 * gb + db;
+    const size_t gb = size_t(fe / 16) * (d / 256) * kQ4Tile, db = size_t(d) * rd, per = 2 * gb + db;
     std::vector<const void *> src(size_t(3) * E), dst(size_t(3) * E, nullptr);
     if (int rc = vh_check(hipMemcpyAsync(src.data(), table, src.size() * sizeof(void *), hipMemcpyDeviceToHost, s)))
         return rc;
@@ -755,9 +782,9 @@ int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **bu
     if (!rc) {
         void *const *dt = static_cast<void *const *>(tab);
         const dim3 gg(fe / 16 * (d / 256), E), gd(d / 16 * (fe / 256), E);
-        hipLaunchKernelGGL((mdec_pack_kernel<144, kQ4Tile>), gg, dim3(256), 0, s, table, dt, 0, d / 256, rg);
-        hipLaunchKernelGGL((mdec_pack_kernel<144, kQ4Tile>), gg, dim3(256), 0, s, table, dt, 1, d / 256, rg);
-        hipLaunchKernelGGL((mdec_pack_kernel<210, kQ6Tile>), gd, dim3(256), 0, s, table, dt, 2, fe / 256, rd);
+        hipLaunchKernelGGL(mdec_pack_q4k_kernel, gg, dim3(256), 0, s, table, dt, 0, d / 256, rg);
+        hipLaunchKernelGGL(mdec_pack_q4k_kernel, gg, dim3(256), 0, s, table, dt, 1, d / 256, rg);
+        hipLaunchKernelGGL(mdec_pack_q6k_kernel, gd, dim3(256), 0, s, table, dt, 2, fe / 256, rd);
         rc = vh_check(hipGetLastError());
     }
     if (rc) {
