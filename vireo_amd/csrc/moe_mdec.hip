@@ -62,6 +62,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kTok = 16;  // tokens per tile (the A operand's rows)
 
 VH_DEV f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+VH_DEV uint32_t u4_at(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // ---- gate/up operand layout ---------------------------------------------------
 // Super-block b (256 weights), step u (0..7), lane group g: the qs word 8 g + u
@@ -289,17 +290,20 @@ __global__ void __launch_bounds__(256) mdec_route_prep_kernel(const float *__res
 //     qs bytes 32 g .. 32 g + 15 of row r at 320 + 16 l, then qs bytes 32 g +
 //     16 .. 32 g + 31 at 1344 + 16 l (64 bytes more than the rows: the
 //     kernel's scale decoding is gone);
-//   Q6_K (3360 bytes): ql bytes 16 g .. of row r at 16 l, ql bytes 64 + 16 g
-//     .. at 1024 + 16 l, qh bytes 16 g .. at 2048 + 16 l, the rows' scales
-//     (16 bytes each) at 3072 + 16 r, their d at 3328 + 2 r.
+//   Q6_K (3360 bytes): the words lane l's sub-block steps read - word g of
+//     each of row r's 16-byte ql chunks 0-3 at 16 l, of chunks 4-7 at 1024 +
+//     16 l, of its qh chunks 0-3 at 2048 + 16 l (so no exchange through LDS)
+//     - then the rows' scales (16 bytes each) at 3072 + 16 r, their d at
+//     3328 + 2 r.
 constexpr int kQ4Tile = 2368, kQ6Tile = 16 * 210;
 
 // the byte of row `row`'s super-block that Q6_K tile byte o (even) holds
 VH_DEV int pk_src_q6k(int o, int &row) {
-    if (o < 3072) {
-        const int q = o & 1023, L = q >> 4;
+    if (o < 3072) {  // word w of lane L's piece: word g of ql chunk w (w + 4), or of qh chunk w
+        const int part = o >> 10, q = o & 1023, L = q >> 4, g = L >> 4, w = (q & 15) >> 2;
         row = L & 15;
-        return (o < 1024 ? 0 : o < 2048 ? 64 : 128) + 16 * (L >> 4) + (q & 15);
+        const int c = part == 1 ? w + 4 : w;
+        return (part == 2 ? 128 : 0) + 16 * c + 4 * g + (q & 3);
     }
     if (o < 3328) {
         row = (o - 3072) >> 4;
@@ -580,7 +584,7 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                                                                   const uint4 *__restrict__ hp, int fe, int d, int E,
                                                                   int64_t row_bytes, float *__restrict__ y) {
     extern __shared__ __align__(16) uint32_t hs[];  // [kTok][fe + 4]
-    __shared__ __align__(16) uint32_t wq[kDnWaves][16 * kDnRowStride];
+    __shared__ __align__(16) uint32_t wq[PK ? 1 : kDnWaves][PK ? 4 : 16 * kDnRowStride];  // GGUF rows only
     const int s = blockIdx.y;
     if (s >= active[E]) return;
     const int e = active[s], cnt = counts[e], base = offs[e], t0 = blockIdx.z * kTok;
@@ -625,18 +629,20 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
     constexpr uint32_t kB = 0x43004300u;  // bf16 128 in both halves
     const bf16x8 k160 = __builtin_bit_cast(bf16x8, make_uint4(0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u));  // bf16 -160
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    uint32_t *wl = &wq[wv][r * kDnRowStride];
+    uint32_t *wl = PK ? &wq[0][0] : &wq[wv][r * kDnRowStride];
 #pragma unroll
     for (int b = 0; b < kDnMaxBlocks; b++) {
         if (b >= nb) break;
         // ql chunks g and g + 4, qh chunk g of the row into the wave's LDS;
         // lane group g then reads word g of the chunk each step needs
-        *reinterpret_cast<uint4 *>(wl + 4 * g) = a0[b];
-        *reinterpret_cast<uint4 *>(wl + 16 + 4 * g) = a1[b];
-        *reinterpret_cast<uint4 *>(wl + 32 + 4 * g) = qq[b];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (!PK) {
+            *reinterpret_cast<uint4 *>(wl + 4 * g) = a0[b];
+            *reinterpret_cast<uint4 *>(wl + 16 + 4 * g) = a1[b];
+            *reinterpret_cast<uint4 *>(wl + 32 + 4 * g) = qq[b];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
         const float dd = h2f(ddb[b]);
         const uint32_t scw[4] = {scb[b].x, scb[b].y, scb[b].z, scb[b].w};
 #pragma unroll
@@ -649,7 +655,11 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                     // slots 0-3: the hi parts of the lane's 4 activations, 4-7 their lo parts;
                     // the weight operand repeats q + 128 for both
                     const bf16x8 xa = __builtin_bit_cast(bf16x8, xr[64 * b + 4 * sb]);
-                    const uint32_t lw = wl[4 * ql_c + g], hw = wl[32 + 4 * qh_c + g];
+                    // word g of ql chunk ql_c and of qh chunk qh_c: from LDS, or (tiles) the
+                    // lane's own loads, which hold exactly those words
+                    const uint4 la = PK ? (ql_c < 4 ? a0[b] : a1[b]) : make_uint4(0u, 0u, 0u, 0u);
+                    const uint32_t lw = PK ? u4_at(la, ql_c & 3) : wl[4 * ql_c + g];
+                    const uint32_t hw = PK ? u4_at(qq[b], qh_c) : wl[32 + 4 * qh_c + g];
                     const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
                     const uint32_t w0 = (q & 0x00ff00ffu) | kB, w1 = ((q >> 8) & 0x00ff00ffu) | kB;
                     const bf16x8 wb = __builtin_bit_cast(bf16x8, make_uint4(w0, w1, w0, w1));
@@ -660,10 +670,11 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[i] = fmaf(ds, c[i], acc[i]);
                 }
-        // every lane is done with this super-block's words before the next overwrite them
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (!PK) {  // every lane is done with this super-block's words before the next overwrite them
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
     }
     if (!live) return;
 #pragma unroll
