@@ -363,15 +363,17 @@ __global__ void __launch_bounds__(256) mdec_pack_q4k_kernel(const void *const *_
 // in the down operand's order into hp (4 bytes per activation, rows of fe).
 // The tile's split inputs pass through LDS one super-block at a time, double
 // buffered (every wave reads them; they are loaded once per workgroup). Each
-// wave's weights are requested two super-blocks ahead of the one it
+// wave's GGUF rows are requested two super-blocks ahead of the one it
 // multiplies (three register sets in turn: the loop over the NB = d / 256
 // super-blocks is unrolled), so two blocks of its rows are in flight from
-// HBM while it computes.
+// HBM while it computes; from tiles (PK), whose loads stream at full rate,
+// one ahead, which keeps the kernel within 128 registers (four waves per
+// SIMD instead of three).
 constexpr int kGuTokStride = 260;  // dwords per token and super-block in LDS: 256 + 4 (no bank conflicts)
 constexpr int kGuMaxBlocks = 8;    // d <= 2048
 
 template <int NB, bool PK>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) mdec_gateup_kernel(const int32_t *__restrict__ counts,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PK ? 4 : 3))) mdec_gateup_kernel(const int32_t *__restrict__ counts,
                                                           const int32_t *__restrict__ offs,
                                                           const int32_t *__restrict__ perm,
                                                           const int32_t *__restrict__ active,
@@ -448,7 +450,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
         }
         w.xsm = xsr[4 * b];
     };
-    Blk blk[3];
+    // weights this many super-blocks ahead: two for GGUF rows, one for tiles
+    // (their loads stream at full rate; the registers saved keep four waves per SIMD)
+    constexpr int AH = PK ? 1 : 2;
+    Blk blk[AH + 1];
     // rows 4 .. 15 only when the tile has more than 4 tokens (a branch the
     // whole workgroup takes alike); lanes of padding rows read the last
     // token's row
@@ -461,7 +466,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
         xv3 = xp[srow[3]];
     }
     load(0, blk[0]);
-    if (NB > 1) load(1, blk[1]);
+    if (AH > 1 && NB > 1) load(1, blk[1]);
     *reinterpret_cast<uint4 *>(xdst) = xv0;
     if (wide) {
         *reinterpret_cast<uint4 *>(xdst + 4 * kGuTokStride) = xv1;
@@ -484,8 +489,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) m
                 xv3 = xp[srow[3] + 64 * (b + 1)];
             }
         }
-        if (b + 2 < NB) load(b + 2, blk[(b + 2) % 3]);
-        const Blk &cb = blk[b % 3];
+        if (b + AH < NB) load(b + AH, blk[(b + AH) % (AH + 1)]);
+        const Blk &cb = blk[b % (AH + 1)];
         const Wt &cg = cb.gw, &cu = cb.uw;
         const uint32_t *xb = xr + (b & 1) * (kTok * kGuTokStride);
         f16x2 s0g, n0g, s1g, n1g, s0u, n0u, s1u, n1u;
