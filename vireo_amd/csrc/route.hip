@@ -165,17 +165,20 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     }
 }
 
-// one 512-thread workgroup per token (eight waves share an uncertified
-// token's contenders)
+// One workgroup per token: 512 threads for certified parts (eight waves
+// share an uncertified token's contenders), 256 for exact ones. Dynamic LDS
+// (only where route_topk_block can stream the contenders' rows: d != 2048,
+// parts not exact): the rows' buffers, then the token's inputs.
 __global__ void __launch_bounds__(512) route_finish_kernel(const RoutePart *__restrict__ parts,
                                                            const float *__restrict__ R, const float *__restrict__ hb,
                                                            const float *__restrict__ bias, int d, int E, int k,
                                                            int renorm, int exact, int32_t *__restrict__ idx,
                                                            float *__restrict__ w, uint32_t *__restrict__ flags,
-                                                           float *__restrict__ probs) {
+                                                           float *__restrict__ probs, int staged) {
     __shared__ TopKSmem sm;
-    __shared__ float4 stage[kStageScrF4];            // the contenders' router rows, streamed
-    __shared__ __align__(16) float xbuf[kXScrFloats];  // the token's inputs, for them
+    extern __shared__ float4 dyn[];
+    float4 *stage = staged ? dyn : nullptr;                                            // the contenders' rows
+    float *xbuf = staged ? reinterpret_cast<float *>(dyn + kStageScrF4) : nullptr;  // the token's inputs
     const int t = blockIdx.x, tid = threadIdx.x;
     route_topk_block(sm, parts + size_t(t) * E, R, hb + size_t(t) * d, bias, d, E, k, renorm, exact != 0,
                      probs ? probs + size_t(t) * E : nullptr, stage, xbuf);
@@ -255,7 +258,10 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
                     hipStream_t s) {
-    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(512), 0, s, parts, R, hb, bias, d, E, k, renorm,
-                       exact ? 1 : 0, idx, w, flags, probs);
+    // a small LDS footprint where the rows are not streamed: prefill calls run thousands of these
+    const bool staged = !exact && d != 2048 && d <= kXScrFloats;
+    const size_t lds = staged ? size_t(kStageScrF4) * 16 + size_t(kXScrFloats) * 4 : 0;
+    hipLaunchKernelGGL(route_finish_kernel, dim3(T), dim3(exact ? 256 : 512), lds, s, parts, R, hb, bias, d, E, k,
+                       renorm, exact ? 1 : 0, idx, w, flags, probs, staged ? 1 : 0);
     return vh_check(hipGetLastError());
 }
