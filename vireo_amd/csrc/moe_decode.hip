@@ -69,7 +69,6 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     constexpr int NS = F::NS, TPL = 3 * Q;
     __shared__ TopKSmem sm;         // the exact fallback's workspace
     __shared__ __align__(16) float xref[2048];  // the fallback's inputs (with a library-normalised hb: the reference's xb)
-    __shared__ float4 rstage[kStageScrF4];      // the fallback's contender rows, streamed
     __shared__ float2 stage[64];    // the weights, in the workgroup that writes the plan
     __shared__ double2 cert[kGuWaves][64];  // per wave: the chosen experts' intervals
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -107,7 +106,8 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             reference_rmsnorm_block(xref, nref.x, nref.nw, nref.eps, d, &sm.red[0][0]);
             xe = xref;
         }
-        route_topk_block(sm, parts, R, xe, bias, d, E, k, renorm, false, nullptr, rstage, d <= 2048 ? xref : nullptr);
+        // d = 2048: the contenders' chains are shared by the waves (no row buffers in LDS)
+        route_topk_block(sm, parts, R, xe, bias, d, E, k, renorm, false, nullptr);
         e_j = sm.sel[j];
         if (writer && wv == 0 && lane < k) {
             const int e = sm.sel[lane];
