@@ -169,6 +169,32 @@ def test_decode_batch_packed_tiles(cuda, T):
     m.close()
 
 
+def test_prefill_q8_row_octets(cuda):
+    """The matrix-core GEMMs of a call of 64+ tokens on a pinned Q8_0 layer
+    read a copy of its experts in row octets (eight rows' bytes of each
+    64-column step together) made by the first call with packing on: the
+    outputs equal the GGUF-row kernels' bit for bit, on that call and the
+    next. Two experts are unregistered."""
+    lib = _lib.load()
+    shape = W.SHAPES["olmoe-q8_0"]
+    m = M.DeviceMoE(shape, 1, seed=67, unregistered={(0, 3), (0, 40)})
+    x, hb = W.host_hidden(shape.d, 130, 67)
+    hbt = torch.from_numpy(hb).to(cuda)
+    outs = []
+    try:
+        for packed in (0, 1, 1):
+            _lib.check(lib.vireo_hip_set_packed(packed), "vireo_hip_set_packed")
+            xt = torch.from_numpy(x).to(cuda)
+            m.forward(0, xt, hbt)
+            outs.append(xt.cpu().numpy())
+    finally:
+        lib.vireo_hip_set_packed(1)
+    assert np.abs(outs[0] - x).max() > 0
+    np.testing.assert_array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32))
+    np.testing.assert_array_equal(outs[2].view(np.uint32), outs[0].view(np.uint32))
+    m.close()
+
+
 @pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
 def test_golden_moe_on_gpu(cuda, case):
     g = golden(f"moe_{case}.npz")

@@ -101,6 +101,7 @@ typedef struct {
  * and n_layers instead, so the GPU entry points can refuse it rather than
  * read host pointers from a foreign layout. */
 #define VH_STORE_MAGIC 0x4d42485f4f455256ull /* "VREO_HBM" */
+#define VH_PACK_KINDS 2 /* decode-batch 16-row tiles; prefill Q8_0 row octets */
 
 struct ExpertStore {
     uint64_t magic;
@@ -115,7 +116,7 @@ struct ExpertStore {
     void *stage;               /* pinned staging for synchronous pread */
     size_t stage_bytes;
     void **tables;             /* per layer: device [n_experts x 3] pointer table */
-    void **ptables, **pbufs;   /* per pinned layer: its experts in 16-row tiles (a second copy) and their table */
+    void **ptables, **pbufs;   /* per kind and pinned layer: a reordered copy of its experts and its table */
     FreeBlock *freel;          /* device blocks of evicted experts, kept for reuse */
     int nfree, capfree;
     uint8_t *arena;            /* one allocation the pool's blocks are cut from (bounded pools) */
@@ -163,8 +164,8 @@ static ExpertStore *store_new(int n_layers, int n_experts, uint64_t capacity_byt
     s->n_slots = n_layers * n_experts;
     s->slots = calloc((size_t)s->n_slots, sizeof(Slot));
     s->tables = calloc((size_t)n_layers, sizeof(void *));
-    s->ptables = calloc((size_t)n_layers, sizeof(void *));
-    s->pbufs = calloc((size_t)n_layers, sizeof(void *));
+    s->ptables = calloc((size_t)n_layers * VH_PACK_KINDS, sizeof(void *));
+    s->pbufs = calloc((size_t)n_layers * VH_PACK_KINDS, sizeof(void *));
     if (!s->slots || !s->tables || !s->ptables || !s->pbufs) {
         free(s->slots); free(s->tables); free(s->ptables); free(s->pbufs); free(s);
         return NULL;
@@ -778,9 +779,12 @@ int expert_store_unpin_layer(ExpertStore *s, int layer) {
     if (hipDeviceSynchronize() != hipSuccess) return -EIO;
     (void)hipFree(s->tables[layer]);
     s->tables[layer] = NULL;
-    if (s->ptables[layer]) (void)hipFree(s->ptables[layer]);
-    if (s->pbufs[layer]) (void)hipFree(s->pbufs[layer]);
-    s->ptables[layer] = s->pbufs[layer] = NULL;
+    for (int kd = 0; kd < VH_PACK_KINDS; kd++) {
+        const size_t i = (size_t)kd * s->n_layers + layer;
+        if (s->ptables[i]) (void)hipFree(s->ptables[i]);
+        if (s->pbufs[i]) (void)hipFree(s->pbufs[i]);
+        s->ptables[i] = s->pbufs[i] = NULL;
+    }
     for (int e = 0; e < s->n_experts; e++) {
         Slot *sl = slot_at(s, layer, e);
         if (sl->pinned) { sl->pinned = 0; if (sl->lease > 0) sl->lease--; }
@@ -795,8 +799,11 @@ void expert_store_destroy(ExpertStore *s) {
     (void)hipDeviceSynchronize();
     for (int l = 0; l < s->n_layers; l++) {
         if (s->tables[l]) (void)hipFree(s->tables[l]);
-        if (s->ptables[l]) (void)hipFree(s->ptables[l]);
-        if (s->pbufs[l]) (void)hipFree(s->pbufs[l]);
+        for (int kd = 0; kd < VH_PACK_KINDS; kd++) {
+            const size_t i = (size_t)kd * s->n_layers + l;
+            if (s->ptables[i]) (void)hipFree(s->ptables[i]);
+            if (s->pbufs[i]) (void)hipFree(s->pbufs[i]);
+        }
     }
     for (int i = 0; i < s->n_slots; i++) {
         if (s->slots[i].dev) block_free(s, s->slots[i].dev);
@@ -845,20 +852,25 @@ const void *const *vh_store_layer_table(const ExpertStore *s, int layer) {
     return (const void *const *)s->tables[layer];
 }
 
-/* A pinned layer's experts in the matrix-core decode batch's 16-row tiles:
- * their device table, or NULL (never allocates). vh_store_set_packed hands
- * the store a copy made for a pinned layer (buf: one device allocation,
- * tab: device [n_experts x 3] table into it); the store frees both when the
- * layer is unpinned or the store destroyed. -EINVAL (the caller keeps them)
- * when the layer is not pinned or already has one. */
-const void *const *vh_store_packed_table(const ExpertStore *s, int layer) {
-    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || !s->tables[layer]) return NULL;
-    return (const void *const *)s->ptables[layer];
+/* A pinned layer's experts reordered for a kernel (kind 0: the matrix-core
+ * decode batch's 16-row tiles, 1: the prefill GEMMs' Q8_0 row octets): their
+ * device table, or NULL (never allocates). vh_store_set_packed hands the
+ * store a copy made for a pinned layer (buf: one device allocation, tab:
+ * device [n_experts x 3] table into it); the store frees both when the layer
+ * is unpinned or the store destroyed. -EINVAL (the caller keeps them) when
+ * the layer is not pinned or already has one of that kind. */
+const void *const *vh_store_packed_table(const ExpertStore *s, int layer, int kind) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS || !s->tables[layer])
+        return NULL;
+    return (const void *const *)s->ptables[(size_t)kind * s->n_layers + layer];
 }
-int vh_store_set_packed(ExpertStore *s, int layer, void *buf, void *tab) {
-    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || !s->tables[layer] || s->ptables[layer]) return -EINVAL;
-    s->pbufs[layer] = buf;
-    s->ptables[layer] = tab;
+int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *buf, void *tab) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS || !s->tables[layer])
+        return -EINVAL;
+    const size_t i = (size_t)kind * s->n_layers + layer;
+    if (s->ptables[i]) return -EINVAL;
+    s->pbufs[i] = buf;
+    s->ptables[i] = tab;
     return 0;
 }
 

@@ -403,17 +403,21 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
 // The tiled copy of a pinned layer's experts for the matrix-core decode batch,
 // made on the first call that may allocate (never under graph capture) and
 // held by the store with the pin; NULL: read the GGUF rows.
+// kind 0: the decode batch's tiles (vh_mdec_pack_layer), 1: the prefill
+// GEMMs' Q8_0 row octets (vh_mfma_pack_q8).
 const void *const *packed_table(const vireo_moe_model *m, int layer, const void *const *table, bool may_alloc,
-                                hipStream_t s) {
+                                hipStream_t s, int kind = 0) {
     if (!g_packed) return nullptr;
-    const void *const *pt = vh_store_packed_table(m->es, layer);
+    const void *const *pt = vh_store_packed_table(m->es, layer, kind);
     if (pt || !may_alloc) return pt;
     void *buf = nullptr, *tab = nullptr;
-    if (vh_mdec_pack_layer(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s)) {
+    const int rc = kind ? vh_mfma_pack_q8(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s)
+                        : vh_mdec_pack_layer(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s);
+    if (rc) {
         (void)hipGetLastError();
         return nullptr;
     }
-    if (vh_store_set_packed(m->es, layer, buf, tab)) {
+    if (vh_store_set_packed(m->es, layer, kind, buf, tab)) {
         (void)hipStreamSynchronize(s);
         (void)hipFree(tab);
         (void)hipFree(buf);
@@ -722,8 +726,14 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         const int mt = vh_mfma_max_tiles(P, E);
         if (!rc) rc = vh_mfma_plan(ws.counts, E, 1, ws.tiles, ws.small, s);
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
-        if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.xb, d, fe, k, ws.hs, s);
-        if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, table, ws.hs, d, fe, ws.ybuf, s);
+        // Q8_0 experts of a pinned layer: the row-octet copy (made on the first such call that may allocate)
+        const void *const *pt =
+            (!rc && tg == VT_Q8_0 && td == VT_Q8_0) ? packed_table(m, layer, table, !src, s, 1) : nullptr;
+        const void *const *tb = pt ? pt : table;
+        if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, tb, pt != nullptr, ws.xb, d, fe, k,
+                                     ws.hs, s);
+        if (!rc) rc = vh_mfma_down(td, ws.tiles, mt, ws.counts, ws.offs, ws.perm, tb, pt != nullptr, ws.hs, d, fe,
+                                   ws.ybuf, s);
     } else if (mdec) {
         // calls of a decode batch's size, Q4_K_M experts: the matrix cores
         if (!rc && !prepped) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);

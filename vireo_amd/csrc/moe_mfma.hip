@@ -29,6 +29,7 @@
 // so the down GEMM reads its A operand contiguously; down writes the fp32 row
 // y[pair] that the combine kernel reads, as on the fp32 plan.
 #include <hip/hip_runtime.h>
+#include <vector>
 #include <algorithm>
 #include "common.h"
 #include "qdecode.h"
@@ -50,7 +51,7 @@ constexpr int kChunks = kBK / 8;  // 16-byte chunks per row and K step
 // sets<T>() - 1 K steps before its words are dequantized into LDS (a Q4_K
 // set holds 64 registers, a Q6_K set 96: two fit)
 template <int T>
-constexpr int sets() { return T == VT_Q8_0 ? VH_MFMA_SETS : 2; }
+constexpr int sets() { return (T & 0xff) == VT_Q8_0 ? VH_MFMA_SETS : 2; }
 
 // The raw bytes of 8 consecutive weights of one row - K chunk kc (columns
 // 64 s + 8 kc .. + 7) of K step s - and their dequantization to fp32 with the
@@ -91,6 +92,32 @@ struct Chunk<VT_Q8_0> {  // src/gguf_compute.c:112-120: y = qs * d, exact
         const uint32_t w[2] = {u0, u1};
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = fmaf(float((w[i >> 2] >> (8 * (i & 3))) & 0xffu), sc, off);
+    }
+};
+
+// Q8_0 rows copied once into row octets for these GEMMs (kQ8Oct): tile (row
+// octet o, K step s) at (o * ns + s) * 544 holds rows 8 o .. 8 o + 7's bytes
+// 68 s .. 68 s + 67 (the step's two blocks) one after the other, so each
+// staging load instruction - eight consecutive rows' chunks of one step -
+// reads 544 consecutive bytes instead of eight 68-byte pieces 2176 bytes
+// apart. A tile column of 8 rows takes ns * 544 = 8 * row_bytes bytes, as
+// the rows do: the per-q base pointers are the same. Values as Chunk<VT_Q8_0>.
+constexpr int kQ8Oct = 0x100 | VT_Q8_0;
+template <>
+struct Chunk<kQ8Oct> {
+    using Pos = Chunk<VT_Q8_0>::Pos;
+    using Raw = Chunk<VT_Q8_0>::Raw;
+    static VH_DEV void setup_row(Pos &p, uint32_t row, uint32_t row_bytes, int kc) {
+        p.ob = (row >> 3) * 8u * row_bytes + (row & 7u) * 68u + 34u * uint32_t(kc >> 2);
+        p.oq = p.ob + 2u + 8u * uint32_t(kc & 3);
+    }
+    static VH_DEV void load(const Pos &p, Raw &r, gbyte *m, int s) {
+        gbyte *ms = m + 544 * s;
+        r.d = ld_u16(ms + p.ob);
+        r.q = ld_u64(ms + p.oq);
+    }
+    static VH_DEV void values(const Pos &p, const Raw &r, int s, float (&v)[8]) {
+        Chunk<VT_Q8_0>::values(p, r, s, v);
     }
 };
 
@@ -269,7 +296,10 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         using C = Chunk<T>;
         constexpr int kSets = sets<T>();
         typename C::Pos bp;
-        C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
+        if constexpr (T == kQ8Oct)
+            C::setup_row(bp, uint32_t(n0 + (p >> 3)), uint32_t(row_bytes), kc);
+        else
+            C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
         gbyte *bm[8];
 #pragma unroll
         for (int q = 0; q < 8; q++) bm[q] = (GATEUP && q >= 4 ? M1 : M0) + (GATEUP ? q & 3 : q) * 32 * row_bytes;
@@ -418,14 +448,19 @@ __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restric
 
 template <bool GATEUP>
 int mfma_launch(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                const int32_t *perm, const void *const *table, const __bf16 *src, int K, int rows, int k,
+                const int32_t *perm, const void *const *table, bool packed, const __bf16 *src, int K, int rows, int k,
                 void *out, hipStream_t s) {
+    if (packed && type != VT_Q8_0) return -EINVAL;
     const int64_t nwg = int64_t(rows / (GATEUP ? kBRows / 2 : kBRows)) * max_tiles;
     const dim3 g(unsigned((nwg + kXcds - 1) / kXcds * kXcds));
     switch (type) {
     case VT_Q8_0:
-        hipLaunchKernelGGL((mfma_proj_kernel<VT_Q8_0, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs, perm,
-                           table, src, K, rows, k, vh_row_bytes(type, K), out);
+        if (packed)
+            hipLaunchKernelGGL((mfma_proj_kernel<kQ8Oct, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs,
+                               perm, table, src, K, rows, k, vh_row_bytes(type, K), out);
+        else
+            hipLaunchKernelGGL((mfma_proj_kernel<VT_Q8_0, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs,
+                               perm, table, src, K, rows, k, vh_row_bytes(type, K), out);
         break;
     case VT_Q4_K:
         hipLaunchKernelGGL((mfma_proj_kernel<VT_Q4_K, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs, perm,
@@ -467,15 +502,76 @@ int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s) {
 }
 
 int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                   const int32_t *perm, const void *const *table, const void *xb, int d, int fe, int k, void *hs,
-                   hipStream_t s) {
-    return mfma_launch<true>(type, tiles, max_tiles, counts, offs, perm, table, static_cast<const __bf16 *>(xb), d,
-                             fe, k, hs, s);
+                   const int32_t *perm, const void *const *table, bool packed, const void *xb, int d, int fe, int k,
+                   void *hs, hipStream_t s) {
+    return mfma_launch<true>(type, tiles, max_tiles, counts, offs, perm, table, packed,
+                             static_cast<const __bf16 *>(xb), d, fe, k, hs, s);
 }
 
 int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                 const int32_t *perm, const void *const *table, const void *hs, int d, int fe, float *ybuf,
-                 hipStream_t s) {
-    return mfma_launch<false>(type, tiles, max_tiles, counts, offs, perm, table, static_cast<const __bf16 *>(hs), fe,
-                              d, 1, ybuf, s);
+                 const int32_t *perm, const void *const *table, bool packed, const void *hs, int d, int fe,
+                 float *ybuf, hipStream_t s) {
+    return mfma_launch<false>(type, tiles, max_tiles, counts, offs, perm, table, packed,
+                              static_cast<const __bf16 *>(hs), fe, d, 1, ybuf, s);
+}
+
+namespace {
+// One workgroup per (tile, expert) of matrix `which`: 272 threads copy two
+// bytes each of the tile's 544 (row rr = t / 34 of the octet).
+__global__ void __launch_bounds__(320) q8_octet_pack_kernel(const void *const *__restrict__ src_tab,
+                                                            void *const *__restrict__ dst_tab, int which, int ns,
+                                                            int64_t row_bytes) {
+    const int e = blockIdx.y, tile = blockIdx.x, o = tile / ns, st = tile - o * ns, t = threadIdx.x;
+    const uint8_t *src = static_cast<const uint8_t *>(src_tab[3 * e + which]);
+    uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + which]);
+    if (!src || !dst || t >= 272) return;
+    const int rr = t / 34, b = 2 * (t - 34 * rr);
+    *reinterpret_cast<uint16_t *>(dst + int64_t(tile) * 544 + 68 * rr + b) =
+        *reinterpret_cast<const uint16_t *>(src + int64_t(8 * o + rr) * row_bytes + 68 * st + b);
+}
+}  // namespace
+
+int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s) {
+    *buf_out = *tab_out = nullptr;
+    if (E < 1 || d % kBK || fe % kBK || d % 8 || fe % 8) return -EINVAL;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
+    if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
+    const int64_t rg = vh_row_bytes(VT_Q8_0, d), rd = vh_row_bytes(VT_Q8_0, fe);
+    const size_t gb = size_t(fe) * rg, db = size_t(d) * rd, per = 2 * gb + db;
+    std::vector<const void *> src(size_t(3) * E), dst(size_t(3) * E, nullptr);
+    if (int rc = vh_check(hipMemcpyAsync(src.data(), table, src.size() * sizeof(void *), hipMemcpyDeviceToHost, s)))
+        return rc;
+    if (int rc = vh_check(hipStreamSynchronize(s))) return rc;
+    void *buf = nullptr, *tab = nullptr;
+    if (hipMalloc(&buf, per * E) != hipSuccess) return -ENOMEM;
+    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) {
+        (void)hipFree(buf);
+        return -ENOMEM;
+    }
+    char *b = static_cast<char *>(buf);
+    for (int e = 0; e < E; e++) {
+        if (!src[3 * e] || !src[3 * e + 1] || !src[3 * e + 2]) continue;  // unregistered: stays NULL
+        dst[3 * e] = b + per * e;
+        dst[3 * e + 1] = b + per * e + gb;
+        dst[3 * e + 2] = b + per * e + 2 * gb;
+    }
+    int rc = vh_check(hipMemcpy(tab, dst.data(), dst.size() * sizeof(void *), hipMemcpyHostToDevice));
+    if (!rc) {
+        void *const *dt = static_cast<void *const *>(tab);
+        const dim3 gg(fe / 8 * (d / kBK), E), gd(d / 8 * (fe / kBK), E);
+        hipLaunchKernelGGL(q8_octet_pack_kernel, gg, dim3(320), 0, s, table, dt, 0, d / kBK, rg);
+        hipLaunchKernelGGL(q8_octet_pack_kernel, gg, dim3(320), 0, s, table, dt, 1, d / kBK, rg);
+        hipLaunchKernelGGL(q8_octet_pack_kernel, gd, dim3(320), 0, s, table, dt, 2, fe / kBK, rd);
+        rc = vh_check(hipGetLastError());
+    }
+    if (rc) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(tab);
+        (void)hipFree(buf);
+        return rc;
+    }
+    *buf_out = buf;
+    *tab_out = tab;
+    return 0;
 }

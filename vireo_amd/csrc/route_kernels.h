@@ -19,8 +19,9 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
 // ExpertStore internals for the MoE plans (expert_store.c): an expert's bytes
 // in the pool (0 if unregistered), the capacity (0 = unbounded), whether a
 // store is one of this library's, a pinned layer's table (NULL if none; never
-// allocates) and its copy in the decode batch's 16-row tiles (held and freed
-// by the store with the pin), whether every layer fits at once, the bytes
+// allocates) and its reordered copies for the decode batch's and the
+// prefill's kernels (held and freed by the store with the pin), whether every
+// layer fits at once, the bytes
 // that hold leases,
 // lookups / lease drops for paged calls (page-ins on a copy stream, blocks
 // protected by events until the kernels that read them are done), and the
@@ -30,8 +31,8 @@ uint64_t vh_store_expert_bytes(const ExpertStore *s, int layer, int expert);
 uint64_t vh_store_capacity(const ExpertStore *s);
 int vh_store_valid(const ExpertStore *s);
 const void *const *vh_store_layer_table(const ExpertStore *s, int layer);
-const void *const *vh_store_packed_table(const ExpertStore *s, int layer);
-int vh_store_set_packed(ExpertStore *s, int layer, void *buf, void *tab);
+const void *const *vh_store_packed_table(const ExpertStore *s, int layer, int kind);
+int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *buf, void *tab);
 int vh_store_fits_all(const ExpertStore *s);
 uint64_t vh_store_leased_bytes(const ExpertStore *s);
 int vh_store_acquire(ExpertStore *s, int layer, int expert, ExpertView *view, hipStream_t cs);
@@ -159,12 +160,17 @@ int vh_mfma_max_tiles(int P, int E);
 int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, int32_t *small, hipStream_t s);
 // xb: the bf16 copy of hb (vh_to_bf16)
 int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s);
+// `packed`: table points at vh_mfma_pack_q8's row octets (Q8_0 only).
 int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                   const int32_t *perm, const void *const *table, const void *xb, int d, int fe, int k, void *hs,
-                   hipStream_t s);
+                   const int32_t *perm, const void *const *table, bool packed, const void *xb, int d, int fe, int k,
+                   void *hs, hipStream_t s);
 int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
-                 const int32_t *perm, const void *const *table, const void *hs, int d, int fe, float *ybuf,
-                 hipStream_t s);
+                 const int32_t *perm, const void *const *table, bool packed, const void *hs, int d, int fe,
+                 float *ybuf, hipStream_t s);
+// A copy of the Q8_0 experts behind `table` (gate, up: fe rows of d; down: d
+// rows of fe) in the GEMMs' row octets, as vh_mdec_pack_layer does for the
+// decode batch (the same bytes; -EBUSY under capture).
+int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s);
 
 // Fused one-token experts kernel (moe_fused.hip): top-k, gate/up, down and
 // combine in one launch of kFusedBlocks workgroups that meet once through
