@@ -105,7 +105,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
                  o_active = take(size_t(E + 1) * 4);
     const size_t o_h = experts ? take(P * fe * 4) : 0;
     const size_t o_y = (experts && grouped) ? take(P * d * 4) : 0;
-    const size_t o_tiles = mfma ? take((1 + 2 * size_t(vh_mfma_max_tiles(int(P), E))) * 4) : 0;
+    const size_t o_tiles = mfma ? take(size_t(vh_mfma_plan_words(int(P), E)) * 4) : 0;
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
     const size_t o_hs = mfma ? take(P * fe * 2) : 0;
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
@@ -724,7 +724,7 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     if (mfma) {  // every group on the matrix cores (its small list stays empty)
         const int mt = vh_mfma_max_tiles(P, E);
-        if (!rc) rc = vh_mfma_plan(ws.counts, E, 1, ws.tiles, ws.small, s);
+        if (!rc) rc = vh_mfma_plan(ws.counts, E, P, 1, tg, td, d, fe, ws.tiles, ws.small, s);
         if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         // Q8_0 experts of a pinned layer: the row-octet copy (made on the first such call that may allocate)
         const void *const *pt =

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 #include <vector>
 #include <algorithm>
+#include <type_traits>
 #include "common.h"
 #include "qdecode.h"
 #include "route_kernels.h"
@@ -92,32 +93,6 @@ struct Chunk<VT_Q8_0> {  // src/gguf_compute.c:112-120: y = qs * d, exact
         const uint32_t w[2] = {u0, u1};
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = fmaf(float((w[i >> 2] >> (8 * (i & 3))) & 0xffu), sc, off);
-    }
-};
-
-// Q8_0 rows copied once into row octets for these GEMMs (kQ8Oct): tile (row
-// octet o, K step s) at (o * ns + s) * 544 holds rows 8 o .. 8 o + 7's bytes
-// 68 s .. 68 s + 67 (the step's two blocks) one after the other, so each
-// staging load instruction - eight consecutive rows' chunks of one step -
-// reads 544 consecutive bytes instead of eight 68-byte pieces 2176 bytes
-// apart. A tile column of 8 rows takes ns * 544 = 8 * row_bytes bytes, as
-// the rows do: the per-q base pointers are the same. Values as Chunk<VT_Q8_0>.
-constexpr int kQ8Oct = 0x100 | VT_Q8_0;
-template <>
-struct Chunk<kQ8Oct> {
-    using Pos = Chunk<VT_Q8_0>::Pos;
-    using Raw = Chunk<VT_Q8_0>::Raw;
-    static VH_DEV void setup_row(Pos &p, uint32_t row, uint32_t row_bytes, int kc) {
-        p.ob = (row >> 3) * 8u * row_bytes + (row & 7u) * 68u + 34u * uint32_t(kc >> 2);
-        p.oq = p.ob + 2u + 8u * uint32_t(kc & 3);
-    }
-    static VH_DEV void load(const Pos &p, Raw &r, gbyte *m, int s) {
-        gbyte *ms = m + 544 * s;
-        r.d = ld_u16(ms + p.ob);
-        r.q = ld_u64(ms + p.oq);
-    }
-    static VH_DEV void values(const Pos &p, const Raw &r, int s, float (&v)[8]) {
-        Chunk<VT_Q8_0>::values(p, r, s, v);
     }
 };
 
@@ -227,66 +202,48 @@ VH_DEV bf16x8 to_bf16(const float (&v)[8]) {
     return __builtin_convertvector(f, bf16x8);
 }
 
-// 1-D grid of at least (column tiles) x (tile-plan capacity) workgroups, a
-// multiple of kXcds; 512 threads. Tile t of the plan is (expert e, first row
-// m0 of its group). A is bf16: GATEUP: xb [T x K], row perm[i] / k; else hs
-// [P x K], row i. GATEUP: B = gate and up rows, out = hs (bf16 [P x rows],
-// row i); else B = down rows, out = y (fp32 [P x rows], row perm[i]). i runs
-// over offs[e] + m0 .. + kBM - 1 within the group.
+// One token tile of BM rows (32, 64 or 128) against kBRows weight rows, by
+// the 512 threads of mfma_proj_kernel. A is bf16: GATEUP: xb [T x K], row
+// perm[i] / k; else hs [P x K], row i. GATEUP: B = gate and up rows, out = hs
+// (bf16 [P x rows], row i); else B = down rows, out = y (fp32 [P x rows], row
+// perm[i]). i runs over base + m0 .. + mcnt - 1 (mcnt <= BM) within the
+// group; rows of the tile past mcnt repeat the group's last row and are not
+// stored.
 //
-// Waves 0-3 only multiply: wave c owns rows 64 (c / 2) .. + 63 of the tile
-// and 128 of its weight rows (gate/up: 64 columns of gate and the same 64 of
-// up), eight 32 x 32 accumulator fragments. Waves 4-7 only stage: their global loads run
-// two K steps ahead in two register sets, and each step they dequantize the
-// set that arrived a step ago into the LDS buffer the multiplying waves will
-// read next. Every SIMD holds one wave of each kind, so the matrix cores and
-// the vector ALUs work at the same time; one barrier per K step.
-template <int T, bool GATEUP>
-__global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__restrict__ tiles,
-                                                             const int32_t *__restrict__ counts,
-                                                             const int32_t *__restrict__ offs,
-                                                             const int32_t *__restrict__ perm,
-                                                             const void *const *__restrict__ table,
-                                                             const __bf16 *__restrict__ src, int K, int rows, int k,
-                                                             int64_t row_bytes, void *__restrict__ out) {
+// Waves 0-3 only multiply: WM x WN of them share the tile (BM = 128 and 64:
+// 2 x 2, BM = 32: 1 x 4), wave c owning rows (BM / WM) (c / WN) .. + BM / WM - 1
+// and kBRows / WN of the weight rows (gate/up: as many columns of gate as of
+// up), FI x FJ 32 x 32 accumulator fragments. Waves 4-7 only stage: their
+// global loads run sets<T>() K steps ahead in register sets, and each step
+// they dequantize the set that arrived a step ago into the LDS buffer the
+// multiplying waves will read next. Every SIMD holds one wave of each kind,
+// so the matrix cores and the vector ALUs work at the same time; one barrier
+// per K step. A tile of fewer rows stages fewer input bytes per step for the
+// same weight bytes: small groups cost less than a full tile.
+template <int T, bool GATEUP, int BM>
+VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kBRows], gbyte *M0, gbyte *M1,
+                      const int32_t *__restrict__ perm, const __bf16 *__restrict__ src, int K, int rows, int k,
+                      int64_t row_bytes, void *__restrict__ out, int base, int m0, int mcnt, int n0) {
+    static_assert(BM == 32 || BM == 64 || BM == 128, "token tiles of 32, 64 or 128 rows");
     constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;  // output columns per workgroup
-    __shared__ bf16x8 As[2][kChunks][kBM];
-    __shared__ bf16x8 Bs[2][kChunks][kBRows];
-    // XCD-contiguous numbering of the live (token tile, column tile) pairs
-    const int nct = rows / NCOL, live = tiles[0] * nct, per = (live + kXcds - 1) / kXcds;
-    const int slot = blockIdx.x / kXcds, L = (blockIdx.x % kXcds) * per + slot;
-    if (slot >= per || L >= live) return;
-    const int t = L / nct, n0 = (L % nct) * NCOL;
-    const int e = tiles[1 + 2 * t], m0 = tiles[2 + 2 * t];
-    const int base = offs[e], mcnt = min(kBM, counts[e] - m0);
+    constexpr int WM = BM >= 64 ? 2 : 1, WN = 4 / WM;    // multiplying waves along rows, columns
+    constexpr int FI = BM / 32 / WM, FJ = kBRows / WN / 32;  // fragments per wave
+    constexpr int AQ = BM / 32;                          // input rows staged per staging thread
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const bool mult = wv < 4;
-
-    gbyte *M0 = gmem(table[3 * e + (GATEUP ? 0 : 2)]);
-    gbyte *M1 = GATEUP ? gmem(table[3 * e + 1]) : M0;
-    if (!M0 || !M1) {
-        // an unregistered expert contributes nothing (src/gguf_run.c:201): its
-        // h rows are zero, and the combine skips its y rows
-        if (GATEUP)
-            for (int i = tid; i < mcnt * NCOL; i += kThreads)
-                static_cast<__bf16 *>(out)[size_t(base + m0 + i / NCOL) * rows + n0 + i % NCOL] = __bf16(0.0f);
-        return;
-    }
     const int nk = K / kBK;
 
-    if (!mult) {
+    if (wv >= 4) {
         // ---- staging waves: thread p stages K chunk kc = p & 7 of A rows
-        // (p >> 3) + 32 q (q < 4; rows past the group repeat its last row,
-        // whose results are not stored) and of B rows (p >> 3) + 32 q (q < 8).
+        // (p >> 3) + 32 q (q < AQ) and of B rows (p >> 3) + 32 q (q < 8).
         // In LDS, chunk kc of row r sits at [kc][r ^ kc]: the 8 lanes of a row
         // write 8 different bank groups, and a 32-lane operand read stays
         // conflict-free. The K step enters the global addresses only through
         // uniform base pointers.
         const int p = tid - 256, kc = p & 7, rx = (p >> 3) ^ kc;
         gbyte *abase = gmem(src);
-        uint32_t aoff[4];
+        uint32_t aoff[AQ];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < AQ; q++) {
             const int i = base + m0 + min((p >> 3) + 32 * q, mcnt - 1);
             aoff[q] = uint32_t((GATEUP ? size_t(perm[i] / k) : size_t(i)) * K * 2) + 16u * uint32_t(kc);
         }
@@ -296,28 +253,25 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         using C = Chunk<T>;
         constexpr int kSets = sets<T>();
         typename C::Pos bp;
-        if constexpr (T == kQ8Oct)
-            C::setup_row(bp, uint32_t(n0 + (p >> 3)), uint32_t(row_bytes), kc);
-        else
-            C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
+        C::setup(bp, uint32_t(n0 + (p >> 3)) * uint32_t(row_bytes), kc);
         gbyte *bm[8];
 #pragma unroll
         for (int q = 0; q < 8; q++) bm[q] = (GATEUP && q >= 4 ? M1 : M0) + (GATEUP ? q & 3 : q) * 32 * row_bytes;
 
         struct Stage {
-            uint4 ah[4];
+            uint4 ah[AQ];
             typename C::Raw bw[8];
         } st[kSets];
         auto load = [&](Stage &g, int step) {
             gbyte *as = abase + 128 * step;
 #pragma unroll
-            for (int q = 0; q < 4; q++) g.ah[q] = ld_u128(as + aoff[q]);
+            for (int q = 0; q < AQ; q++) g.ah[q] = ld_u128(as + aoff[q]);
 #pragma unroll
             for (int q = 0; q < 8; q++) C::load(bp, g.bw[q], bm[q], step);
         };
         auto store = [&](const Stage &g, int buf, int step) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) As[buf][kc][rx + 32 * q] = __builtin_bit_cast(bf16x8, g.ah[q]);
+            for (int q = 0; q < AQ; q++) As[buf][kc][rx + 32 * q] = __builtin_bit_cast(bf16x8, g.ah[q]);
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 float w[8];
@@ -349,17 +303,18 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
     // ---- multiplying waves: v_mfma_f32_32x32x16_bf16 (lane l supplies row
     // l % 32, K values 8 (l / 32) .. + 7 of each operand; it holds column
     // l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 of the 32 x 32 result)
-    const int wm = wv >> 1, wn = wv & 1;
-    // B rows of the wave's four 32-column fragments (gate/up: two of gate,
-    // the same two of up)
-    int bfr[4];
+    const int wm = wv / WN, wn = wv % WN;
+    // B rows of the wave's FJ 32-column fragments (gate/up: FJ / 2 of gate,
+    // the same FJ / 2 of up)
+    int bfr[FJ];
 #pragma unroll
-    for (int j = 0; j < 4; j++) bfr[j] = GATEUP ? (j < 2 ? 0 : NCOL) + 64 * wn + 32 * (j & 1) : 128 * wn + 32 * j;
-    f32x16 acc[2][4];
+    for (int j = 0; j < FJ; j++)
+        bfr[j] = GATEUP ? (j < FJ / 2 ? 0 : NCOL) + (NCOL / WN) * wn + 32 * (j % (FJ / 2)) : (kBRows / WN) * wn + 32 * j;
+    f32x16 acc[FI][FJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FI; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < FJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
     __syncthreads();  // buffer 0 staged
@@ -368,38 +323,252 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int kg = 2 * ks + (lane >> 5), lx = (lane & 31) ^ kg;
-            bf16x8 a[2], b[4];
+            bf16x8 a[FI], b[FJ];
 #pragma unroll
-            for (int i = 0; i < 2; i++) a[i] = As[buf][kg][lx + 64 * wm + 32 * i];
+            for (int i = 0; i < FI; i++) a[i] = As[buf][kg][lx + (BM / WM) * wm + 32 * i];
 #pragma unroll
-            for (int j = 0; j < 4; j++) b[j] = Bs[buf][kg][lx + bfr[j]];
+            for (int j = 0; j < FJ; j++) b[j] = Bs[buf][kg][lx + bfr[j]];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < FI; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         __syncthreads();
     }
 
     // epilogue
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int row = (BM / WM) * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (row >= mcnt) continue;
             const int pos = base + m0 + row;
             if (GATEUP) {
                 __bf16 *hs = static_cast<__bf16 *>(out) + size_t(pos) * rows;
 #pragma unroll
-                for (int jj = 0; jj < 2; jj++)
-                    hs[n0 + 64 * wn + 32 * jj + (lane & 31)] = __bf16(swiglu(acc[i][jj][r], acc[i][2 + jj][r]));
+                for (int jj = 0; jj < FJ / 2; jj++)
+                    hs[n0 + (NCOL / WN) * wn + 32 * jj + (lane & 31)] = __bf16(swiglu(acc[i][jj][r], acc[i][FJ / 2 + jj][r]));
             } else {
                 float *y = static_cast<float *>(out) + size_t(perm[pos]) * rows;
 #pragma unroll
-                for (int j = 0; j < 4; j++) y[n0 + 128 * wn + 32 * j + (lane & 31)] = acc[i][j][r];
+                for (int j = 0; j < FJ; j++) y[n0 + (kBRows / WN) * wn + 32 * j + (lane & 31)] = acc[i][j][r];
             }
         }
+}
+
+// kXcds x slots workgroups of 512 threads (slots from tile_cost). The plan
+// (mfma_plan_kernel) holds n tiles (expert, size, first row of its group)
+// and, per launch, where each XCD's run of (tile, column tile) pairs starts:
+// workgroup b runs on XCD b mod 8 (hardware dispatch) and takes pair
+// start[b mod 8] + b / 8 of that XCD's contiguous run, column tiles fastest,
+// so the workgroups sharing a token tile, and the consecutive token tiles of
+// one expert that share its weight tiles, meet in the same L2. The runs are
+// cut at equal shares of the staged bytes (tiles of fewer rows cost less).
+template <int T, bool GATEUP>
+__global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__restrict__ tiles,
+                                                             const int32_t *__restrict__ counts,
+                                                             const int32_t *__restrict__ offs,
+                                                             const int32_t *__restrict__ perm,
+                                                             const void *const *__restrict__ table,
+                                                             const __bf16 *__restrict__ src, int K, int rows, int k,
+                                                             int64_t row_bytes, void *__restrict__ out) {
+    constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;  // output columns per workgroup
+    __shared__ bf16x8 As[2][kChunks][kBM];
+    __shared__ bf16x8 Bs[2][kChunks][kBRows];
+    const int nct = rows / NCOL, xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+    const int32_t *run = tiles + (GATEUP ? kPlanRunsGU : kPlanRunsDN);
+    const int L = run[xcd] + slot;
+    if (L >= run[xcd + 1]) return;
+    const int t = L / nct, n0 = (L % nct) * NCOL;
+    const int code = tiles[kPlanHead + 2 * t], m0 = tiles[kPlanHead + 2 * t + 1];
+    const int e = code & 0xffff, bmt = code >> 16;
+    const int base = offs[e], mcnt = min(bmt, counts[e] - m0);
+    const int tid = threadIdx.x;
+
+    gbyte *M0 = gmem(table[3 * e + (GATEUP ? 0 : 2)]);
+    gbyte *M1 = GATEUP ? gmem(table[3 * e + 1]) : M0;
+    if (!M0 || !M1) {
+        // an unregistered expert contributes nothing (src/gguf_run.c:201): its
+        // h rows are zero, and the combine skips its y rows
+        if (GATEUP)
+            for (int i = tid; i < mcnt * NCOL; i += kThreads)
+                static_cast<__bf16 *>(out)[size_t(base + m0 + i / NCOL) * rows + n0 + i % NCOL] = __bf16(0.0f);
+        return;
+    }
+    if (bmt == 32)
+        mfma_tile<T, GATEUP, 32>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+    else if (bmt == 64)
+        mfma_tile<T, GATEUP, 64>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+    else
+        mfma_tile<T, GATEUP, 128>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+}
+
+// ---- Q8_0 experts packed in the matrix cores' operand order (kQ8Frag) ----
+//
+// A pinned Q8_0 layer's experts are copied once (vh_mfma_pack_q8) into
+// fragments: fragment (g, s) of a matrix is the 32 weight rows one
+// v_mfma_f32_32x32x16_bf16 B operand takes (gate/up: rows 16 g .. 16 g + 15 of
+// gate, then the same rows of up; down: rows 32 g .. 32 g + 31) over K step s
+// (64 columns), kFragBytes bytes: first, lane l's 32 quant bytes - row l % 32,
+// columns 64 s + 16 ks + 8 (l / 32) .. + 7 for ks = 0..3, the 8 bytes it
+// supplies to sub-step ks - then the rows' two block scales (2 x fp16 per row,
+// blocks 2 s and 2 s + 1). A wave reads its B operand for a K step with two
+// 1 KB and one 128 B load instructions of consecutive bytes and dequantizes
+// it in its own registers; only the activations pass through LDS.
+constexpr int kFragBytes = 2176;
+
+// One token tile of BM rows against 8 fragments (gate/up: 128 output columns;
+// down: 256), 512 threads: wave w multiplies all BM rows by fragment w, FI =
+// BM / 32 accumulators. Per K step every thread dequantizes its wave's B
+// operand loaded two steps earlier (the values of Chunk<VT_Q8_0>, rounded to
+// bf16 the same way, in the same K order: the results equal mfma_tile's bit for
+// bit), issues the loads of two steps ahead, multiplies, and stores the
+// inputs of the next step into the other LDS buffer. The barrier is LDS-only:
+// global loads stay in flight across it.
+template <bool GATEUP, int BM>
+VH_DEV void frag_tile(bf16x8 (&As)[2][kChunks][kBM], gbyte *F, const int32_t *__restrict__ perm,
+                      const __bf16 *__restrict__ src, int K, int rows, int k, void *__restrict__ out, int base, int m0,
+                      int mcnt, int n0) {
+    constexpr int FI = BM / 32, AQ = (BM * kChunks + kThreads - 1) / kThreads;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nk = K / kBK;
+    // this wave's fragments: g = n0 / 16 + wv (gate/up) or n0 / 32 + wv (down)
+    gbyte *fb = F + size_t((GATEUP ? n0 / 16 : n0 / 32) + wv) * nk * kFragBytes;
+    gbyte *fq = fb + 32 * lane, *fs = fb + 2048 + 4 * (lane & 31);
+    // input staging: chunk slot c = tid + 512 q holds K chunk c & 7 of tile row
+    // c >> 3 (rows past the group repeat its last row; slots past the tile
+    // fill LDS rows that are not read). Every load is unconditional (steps
+    // past the end repeat the last one), so the waits before each use count
+    // exactly the loads issued after it.
+    gbyte *abase = gmem(src);
+    uint32_t aoff[AQ];
+    int arow[AQ];
+#pragma unroll
+    for (int q = 0; q < AQ; q++) {
+        const int c = tid + kThreads * q, r = c >> 3, kc = c & 7;
+        const int i = base + m0 + min(r, mcnt - 1);
+        aoff[q] = uint32_t((GATEUP ? size_t(perm[i] / k) : size_t(i)) * K * 2) + 16u * uint32_t(kc);
+        arow[q] = r ^ kc;
+    }
+    uint4 av[2][AQ], bq[2][2];
+    uint32_t bs[2];
+    auto loadA = [&](int set, int step) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++) av[set][q] = ld_u128(abase + 128 * step + aoff[q]);
+    };
+    auto storeA = [&](int set, int buf) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++)
+            As[buf][(tid + kThreads * q) & 7][arow[q]] = __builtin_bit_cast(bf16x8, av[set][q]);
+    };
+    auto loadB = [&](int set, int step) {
+        bq[set][0] = ld_u128(fq + size_t(step) * kFragBytes);
+        bq[set][1] = ld_u128(fq + size_t(step) * kFragBytes + 16);
+        bs[set] = ld_u32(fs + size_t(step) * kFragBytes);
+    };
+    f32x16 acc[FI];
+#pragma unroll
+    for (int i = 0; i < FI; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+
+    // K step s: B(s) in register set s % 2, A(s + 1) in set (s + 1) % 2, LDS
+    // buffer s % 2 holds A(s)
+    auto step = [&](int s, auto SET) {
+        constexpr int set = decltype(SET)::value, nset = 1 - set;
+        // B(s): (q + 128) * d - 128 * d = q * d exactly, then bf16
+        bf16x8 b[4];
+        const uint32_t w[8] = {bq[set][0].x, bq[set][0].y, bq[set][0].z, bq[set][0].w,
+                               bq[set][1].x, bq[set][1].y, bq[set][1].z, bq[set][1].w};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const float sc = h2f(ks < 2 ? bs[set] & 0xffffu : bs[set] >> 16), off = -128.0f * sc;
+            uint32_t u0 = w[2 * ks] ^ 0x80808080u, u1 = w[2 * ks + 1] ^ 0x80808080u;
+            asm volatile("" : "+v"(u0), "+v"(u1));
+            const uint32_t uu[2] = {u0, u1};
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = fmaf(float((uu[i >> 2] >> (8 * (i & 3))) & 0xffu), sc, off);
+            b[ks] = to_bf16(v);
+        }
+        loadB(set, min(s + 2, nk - 1));
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int kg = 2 * ks + (lane >> 5), lx = (lane & 31) ^ kg;
+#pragma unroll
+            for (int i = 0; i < FI; i++)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(As[set][kg][lx + 32 * i], b[ks], acc[i], 0, 0, 0);
+        }
+        storeA(nset, nset);
+        loadA(nset, min(s + 3, nk - 1));
+        lds_barrier();
+    };
+    loadA(0, 0);
+    loadB(0, 0);
+    loadA(1, min(1, nk - 1));
+    loadB(1, min(1, nk - 1));
+    storeA(0, 0);
+    loadA(0, min(2, nk - 1));
+    lds_barrier();
+    int s = 0;
+    for (; s + 1 < nk; s += 2) {
+        step(s, std::integral_constant<int, 0>());
+        step(s + 1, std::integral_constant<int, 1>());
+    }
+    if (s < nk) step(s, std::integral_constant<int, 0>());
+
+    // epilogue: lane l holds column l % 32 of the fragment (gate/up: gate
+    // column l % 16 in lanes l % 32 < 16, up in the others)
+#pragma unroll
+    for (int i = 0; i < FI; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (GATEUP) {
+                const float g = acc[i][r], u = __shfl_xor(g, 16, 64);
+                if (row < mcnt && !(lane & 16))
+                    static_cast<__bf16 *>(out)[size_t(base + m0 + row) * rows + n0 + 16 * wv + (lane & 15)] =
+                        __bf16(swiglu(g, u));
+            } else if (row < mcnt) {
+                static_cast<float *>(out)[size_t(perm[base + m0 + row]) * rows + n0 + 32 * wv + (lane & 31)] = acc[i][r];
+            }
+        }
+}
+
+// mfma_proj_kernel's grid, plan and outputs on kQ8Frag experts: table[3 e] =
+// the expert's gate/up fragments, table[3 e + 2] its down fragments.
+template <bool GATEUP>
+__global__ void __launch_bounds__(kThreads) mfma_frag_kernel(const int32_t *__restrict__ tiles,
+                                                             const int32_t *__restrict__ counts,
+                                                             const int32_t *__restrict__ offs,
+                                                             const int32_t *__restrict__ perm,
+                                                             const void *const *__restrict__ table,
+                                                             const __bf16 *__restrict__ src, int K, int rows, int k,
+                                                             void *__restrict__ out) {
+    constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;
+    __shared__ bf16x8 As[2][kChunks][kBM];
+    const int nct = rows / NCOL, xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+    const int32_t *run = tiles + (GATEUP ? kPlanRunsGU : kPlanRunsDN);
+    const int L = run[xcd] + slot;
+    if (L >= run[xcd + 1]) return;
+    const int t = L / nct, n0 = (L % nct) * NCOL;
+    const int code = tiles[kPlanHead + 2 * t], m0 = tiles[kPlanHead + 2 * t + 1];
+    const int e = code & 0xffff, bmt = code >> 16;
+    const int base = offs[e], mcnt = min(bmt, counts[e] - m0);
+    gbyte *F = gmem(table[3 * e + (GATEUP ? 0 : 2)]);
+    if (!F) {
+        // an unregistered expert contributes nothing (src/gguf_run.c:201)
+        if (GATEUP)
+            for (int i = threadIdx.x; i < mcnt * NCOL; i += kThreads)
+                static_cast<__bf16 *>(out)[size_t(base + m0 + i / NCOL) * rows + n0 + i % NCOL] = __bf16(0.0f);
+        return;
+    }
+    if (bmt == 32)
+        frag_tile<GATEUP, 32>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
+    else if (bmt == 64)
+        frag_tile<GATEUP, 64>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
+    else
+        frag_tile<GATEUP, 128>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
 }
 
 // bf16 copy of n fp32 values (n a multiple of 4, both 16-byte aligned)
@@ -413,37 +582,143 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const float4 *__restrict__
     }
 }
 
-// One workgroup: tiles = {n, (e, m0) x n} for the groups of at least
-// min_tokens tokens (kBM rows per tile, experts ascending), and the list of
-// the other non-empty groups in the dispatch kernel's `active` format
-// (small[0 .. n), n at small[E]).
+// The bytes a token tile of bm rows stages per K step (the weights' wb and
+// the inputs), in 64-byte units: the cost by which the XCDs' runs are cut.
+__host__ __device__ constexpr int tile_step_cost(int wb, int bm) { return (wb + bm * kBK * 2) / 64; }
+
+// One workgroup of 256 threads (thread e = expert e, E <= 256). The plan:
+//   tiles[0]               n, the number of token tiles
+//   tiles[kPlanRunsGU + x]  x = 0..8: where XCD x's run of gate/up (tile,
+//                           column tile) pairs starts (x = 8: the end)
+//   tiles[kPlanRunsDN + x]  the same for the down launch
+//   tiles[kPlanHead + 2 t]  tile t: expert | rows << 16 (rows 32, 64 or 128),
+//                           then the tile's first row within its group
+// for the groups of at least min_tokens tokens (experts ascending; a group
+// takes whole 128-row tiles and its remainder one tile of 32 or 64 rows, or
+// a last 128-row tile above 64), and the list of the other non-empty groups
+// in the dispatch kernel's `active` format (small[0 .. n), n at small[E]).
+// The runs are cut at equal shares of the launch's staged bytes
+// (tile_step_bytes per pair); a cut that would give an XCD more pairs than
+// the launch has slots per XCD falls back to equal shares of pairs.
 __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restrict__ counts, int E, int min_tokens,
-                                                        int32_t *__restrict__ tiles, int32_t *__restrict__ small) {
+                                                        int nct_gu, int wb_gu, int slots_gu, int nct_dn,
+                                                        int wb_dn, int slots_dn, int32_t *__restrict__ tiles,
+                                                        int32_t *__restrict__ small) {
     __shared__ int wsum[4][2];
+    __shared__ int wcost[4][2];
+    __shared__ int runs[2][kXcds + 1];
+    __shared__ int total[2];
+    __shared__ int ntiles;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int cnt = t < E ? counts[t] : 0;
-    const bool big = cnt >= min_tokens;
-    const int nt = big ? (cnt + kBM - 1) / kBM : 0, sm = (!big && cnt > 0) ? 1 : 0;
+    const bool big = cnt > 0 && cnt >= min_tokens;
+    int n128 = cnt / kBM, rem = cnt % kBM;
+    if (rem > kBM / 2) {
+        n128++;
+        rem = 0;
+    }
+    const int rbm = rem == 0 ? 0 : rem <= 32 ? 32 : 64;
+    const int nt = big ? n128 + (rbm ? 1 : 0) : 0, sm = (!big && cnt > 0) ? 1 : 0;
+    const int ncts[2] = {nct_gu, nct_dn};
+    const int wbs[2] = {wb_gu, wb_dn};
+    int c[2];
+#pragma unroll
+    for (int l = 0; l < 2; l++)
+        c[l] = big ? ncts[l] * (n128 * tile_step_cost(wbs[l], kBM) + (rbm ? tile_step_cost(wbs[l], rbm) : 0)) : 0;
     int it = nt, is = sm;
+    int ic[2] = {c[0], c[1]};
 #pragma unroll
     for (int sh = 1; sh < 64; sh <<= 1) {
         const int ot = __shfl_up(it, sh, 64), os = __shfl_up(is, sh, 64);
-        if (lane >= sh) { it += ot; is += os; }
+        const int o0 = __shfl_up(ic[0], sh, 64), o1 = __shfl_up(ic[1], sh, 64);
+        if (lane >= sh) {
+            it += ot;
+            is += os;
+            ic[0] += o0;
+            ic[1] += o1;
+        }
     }
-    if (lane == 63) { wsum[wv][0] = it; wsum[wv][1] = is; }
+    if (lane == 63) {
+        wsum[wv][0] = it;
+        wsum[wv][1] = is;
+        wcost[wv][0] = ic[0];
+        wcost[wv][1] = ic[1];
+    }
     __syncthreads();
     int bt = 0, bs = 0;
-    for (int w = 0; w < wv; w++) { bt += wsum[w][0]; bs += wsum[w][1]; }
+    int bc[2] = {0, 0};
+    for (int w = 0; w < wv; w++) {
+        bt += wsum[w][0];
+        bs += wsum[w][1];
+        bc[0] += wcost[w][0];
+        bc[1] += wcost[w][1];
+    }
     const int ex_t = bt + it - nt, ex_s = bs + is - sm;
     for (int i = 0; i < nt; i++) {
-        tiles[1 + 2 * (ex_t + i)] = t;
-        tiles[2 + 2 * (ex_t + i)] = i * kBM;
+        tiles[kPlanHead + 2 * (ex_t + i)] = t | ((i < n128 ? kBM : rbm) << 16);
+        tiles[kPlanHead + 2 * (ex_t + i) + 1] = i * kBM;
     }
     if (sm) small[ex_s] = t;
     if (t == 255) {
+        ntiles = ex_t + nt;
+        total[0] = bc[0] + ic[0];
+        total[1] = bc[1] + ic[1];
         tiles[0] = ex_t + nt;
         small[E] = ex_s + sm;
     }
+    __syncthreads();
+    // the cuts: XCD x's run starts at the pair holding staged byte x * total / 8
+#pragma unroll
+    for (int l = 0; l < 2; l++) {
+        const int ex_c = bc[l] + ic[l] - c[l];
+        for (int x = 1; x < kXcds; x++) {
+            const int target = int(int64_t(x) * total[l] / kXcds);
+            if (c[l] > 0 && ex_c <= target && target < ex_c + c[l]) {
+                const int off = target - ex_c, c128 = tile_step_cost(wbs[l], kBM), full = n128 * ncts[l] * c128;
+                int tl, col;
+                if (off < full) {
+                    tl = off / (ncts[l] * c128);
+                    col = (off - tl * ncts[l] * c128) / c128;
+                } else {
+                    tl = n128;
+                    col = (off - full) / tile_step_cost(wbs[l], rbm);
+                }
+                runs[l][x] = (ex_t + tl) * ncts[l] + col;
+            }
+        }
+    }
+    if (t == 0) {
+        runs[0][0] = runs[1][0] = 0;
+        runs[0][kXcds] = ntiles * nct_gu;
+        runs[1][kXcds] = ntiles * nct_dn;
+        if (total[0] == 0)
+            for (int x = 1; x < kXcds; x++) runs[0][x] = 0;
+        if (total[1] == 0)
+            for (int x = 1; x < kXcds; x++) runs[1][x] = 0;
+    }
+    __syncthreads();
+    if (t < 2) {
+        const int slots = t ? slots_dn : slots_gu, live = runs[t][kXcds];
+        bool ok = true;
+        for (int x = 0; x < kXcds; x++) ok = ok && runs[t][x] <= runs[t][x + 1] && runs[t][x + 1] - runs[t][x] <= slots;
+        const int per = (live + kXcds - 1) / kXcds;
+        for (int x = 0; x <= kXcds; x++) tiles[(t ? kPlanRunsDN : kPlanRunsGU) + x] = ok ? runs[t][x] : min(x * per, live);
+    }
+}
+
+// The column tiles, weight bytes per K step and workgroup slots per XCD of a
+// launch: enough slots for any cut mfma_plan_kernel makes (an XCD's share of
+// the staged bytes plus one pair, at the cheapest pair's cost).
+struct TileCost {
+    int nct, wb, slots;
+};
+TileCost tile_cost(uint32_t type, int K, int rows, bool gateup, int max_tiles) {
+    TileCost c;
+    c.nct = rows / (gateup ? kBRows / 2 : kBRows);
+    c.wb = int(int64_t(kBRows) * vh_row_bytes(type, K) * kBK / K);  // a multiple of 64 for these types
+    const int64_t cmax = tile_step_cost(c.wb, kBM), cmin = tile_step_cost(c.wb, 32);
+    c.slots = int((int64_t(max_tiles) * c.nct * cmax / kXcds + cmax) / cmin + 1);
+    return c;
 }
 
 template <bool GATEUP>
@@ -451,13 +726,13 @@ int mfma_launch(uint32_t type, const int32_t *tiles, int max_tiles, const int32_
                 const int32_t *perm, const void *const *table, bool packed, const __bf16 *src, int K, int rows, int k,
                 void *out, hipStream_t s) {
     if (packed && type != VT_Q8_0) return -EINVAL;
-    const int64_t nwg = int64_t(rows / (GATEUP ? kBRows / 2 : kBRows)) * max_tiles;
-    const dim3 g(unsigned((nwg + kXcds - 1) / kXcds * kXcds));
+    const TileCost tc = tile_cost(type, K, rows, GATEUP, max_tiles);
+    const dim3 g(unsigned(tc.slots) * kXcds);
     switch (type) {
     case VT_Q8_0:
         if (packed)
-            hipLaunchKernelGGL((mfma_proj_kernel<kQ8Oct, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs,
-                               perm, table, src, K, rows, k, vh_row_bytes(type, K), out);
+            hipLaunchKernelGGL((mfma_frag_kernel<GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs, perm, table,
+                               src, K, rows, k, out);
         else
             hipLaunchKernelGGL((mfma_proj_kernel<VT_Q8_0, GATEUP>), g, dim3(kThreads), 0, s, tiles, counts, offs,
                                perm, table, src, K, rows, k, vh_row_bytes(type, K), out);
@@ -486,9 +761,17 @@ bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E) {
 
 int vh_mfma_max_tiles(int P, int E) { return P / kBM + E; }
 
-int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, int32_t *small, hipStream_t s) {
+int vh_mfma_plan_words(int P, int E) { return kPlanHead + 2 * vh_mfma_max_tiles(P, E); }
+
+int vh_mfma_plan(const int32_t *counts, int E, int P, int min_tokens, uint32_t tg, uint32_t td, int d, int fe,
+                 int32_t *tiles, int32_t *small, hipStream_t s) {
     if (E > 256) return -EINVAL;
-    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1), dim3(256), 0, s, counts, E, min_tokens, tiles, small);
+    const int mt = vh_mfma_max_tiles(P, E);
+    const TileCost gu = tile_cost(tg, d, fe, true, mt), dn = tile_cost(td, fe, d, false, mt);
+    // the plan's costs are 32-bit sums over every (tile, column tile) pair
+    if (int64_t(mt) * std::max(gu.nct, dn.nct) * tile_step_cost(std::max(gu.wb, dn.wb), kBM) > INT32_MAX) return -E2BIG;
+    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1), dim3(256), 0, s, counts, E, min_tokens, gu.nct, gu.wb, gu.slots,
+                       dn.nct, dn.wb, dn.slots, tiles, small);
     return vh_check(hipGetLastError());
 }
 
@@ -516,24 +799,37 @@ int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32
 }
 
 namespace {
-// One workgroup per (tile, expert) of matrix `which`: 272 threads copy two
-// bytes each of the tile's 544 (row rr = t / 34 of the octet).
-__global__ void __launch_bounds__(320) q8_octet_pack_kernel(const void *const *__restrict__ src_tab,
-                                                            void *const *__restrict__ dst_tab, int which, int ns,
-                                                            int64_t row_bytes) {
-    const int e = blockIdx.y, tile = blockIdx.x, o = tile / ns, st = tile - o * ns, t = threadIdx.x;
-    const uint8_t *src = static_cast<const uint8_t *>(src_tab[3 * e + which]);
-    uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + which]);
-    if (!src || !dst || t >= 272) return;
-    const int rr = t / 34, b = 2 * (t - 34 * rr);
-    *reinterpret_cast<uint16_t *>(dst + int64_t(tile) * 544 + 68 * rr + b) =
-        *reinterpret_cast<const uint16_t *>(src + int64_t(8 * o + rr) * row_bytes + 68 * st + b);
+// One workgroup per (fragment, expert), 544 threads: thread w writes word w
+// of the fragment's kFragBytes (kQ8Frag layout, above) from the expert's
+// GGUF rows. gateup: fragments of gate and up (rows 16 g + r % 16 of gate for
+// r < 16, of up above), else of down (rows 32 g + r); nk K steps per row.
+__global__ void __launch_bounds__(576) q8_frag_pack_kernel(const void *const *__restrict__ src_tab,
+                                                           void *const *__restrict__ dst_tab, int gateup, int nk,
+                                                           int64_t row_bytes) {
+    const int e = blockIdx.y, f = blockIdx.x, g = f / nk, st = f - g * nk, w = threadIdx.x;
+    uint8_t *dst = static_cast<uint8_t *>(dst_tab[3 * e + (gateup ? 0 : 2)]);
+    if (!dst || w >= kFragBytes / 4) return;
+    const int r = w < 512 ? (w >> 3) & 31 : w - 512;  // the fragment row this word belongs to
+    const uint8_t *row = gateup ? static_cast<const uint8_t *>(src_tab[3 * e + (r < 16 ? 0 : 1)]) +
+                                      int64_t(16 * g + (r & 15)) * row_bytes
+                                : static_cast<const uint8_t *>(src_tab[3 * e + 2]) + int64_t(32 * g + r) * row_bytes;
+    uint32_t v;
+    if (w < 512) {
+        // lane w / 8, bytes 4 (w % 8) .. + 3 of its 32: sub-step (w % 8) / 2, half w % 2
+        const int lane = w >> 3, ks = (w & 7) >> 1, K0 = 64 * st + 16 * ks + 8 * (lane >> 5) + 4 * (w & 1);
+        const uint8_t *q = row + 34 * (K0 >> 5) + 2 + (K0 & 31);  // even: two 16-bit loads
+        v = uint32_t(*reinterpret_cast<const uint16_t *>(q)) | uint32_t(*reinterpret_cast<const uint16_t *>(q + 2)) << 16;
+    } else {
+        v = uint32_t(*reinterpret_cast<const uint16_t *>(row + 68 * st)) |
+            uint32_t(*reinterpret_cast<const uint16_t *>(row + 68 * st + 34)) << 16;
+    }
+    *reinterpret_cast<uint32_t *>(dst + int64_t(f) * kFragBytes + 4 * w) = v;
 }
 }  // namespace
 
 int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s) {
     *buf_out = *tab_out = nullptr;
-    if (E < 1 || d % kBK || fe % kBK || d % 8 || fe % 8) return -EINVAL;
+    if (E < 1 || d % kBRows || fe % (kBRows / 2) || d % kBK || fe % kBK) return -EINVAL;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
     if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
@@ -552,17 +848,15 @@ int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_o
     char *b = static_cast<char *>(buf);
     for (int e = 0; e < E; e++) {
         if (!src[3 * e] || !src[3 * e + 1] || !src[3 * e + 2]) continue;  // unregistered: stays NULL
-        dst[3 * e] = b + per * e;
-        dst[3 * e + 1] = b + per * e + gb;
-        dst[3 * e + 2] = b + per * e + 2 * gb;
+        dst[3 * e] = dst[3 * e + 1] = b + per * e;  // gate/up fragments
+        dst[3 * e + 2] = b + per * e + 2 * gb;       // down fragments
     }
     int rc = vh_check(hipMemcpy(tab, dst.data(), dst.size() * sizeof(void *), hipMemcpyHostToDevice));
     if (!rc) {
         void *const *dt = static_cast<void *const *>(tab);
-        const dim3 gg(fe / 8 * (d / kBK), E), gd(d / 8 * (fe / kBK), E);
-        hipLaunchKernelGGL(q8_octet_pack_kernel, gg, dim3(320), 0, s, table, dt, 0, d / kBK, rg);
-        hipLaunchKernelGGL(q8_octet_pack_kernel, gg, dim3(320), 0, s, table, dt, 1, d / kBK, rg);
-        hipLaunchKernelGGL(q8_octet_pack_kernel, gd, dim3(320), 0, s, table, dt, 2, fe / kBK, rd);
+        const dim3 gg(fe / 16 * (d / kBK), E), gd(d / 32 * (fe / kBK), E);
+        hipLaunchKernelGGL(q8_frag_pack_kernel, gg, dim3(576), 0, s, table, dt, 1, d / kBK, rg);
+        hipLaunchKernelGGL(q8_frag_pack_kernel, gd, dim3(576), 0, s, table, dt, 0, fe / kBK, rd);
         rc = vh_check(hipGetLastError());
     }
     if (rc) {

@@ -146,8 +146,10 @@ int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **bu
 
 // Matrix-core grouped GEMMs (moe_mfma.hip) for the groups of calls of at
 // least kMfmaMinCall tokens. vh_mfma_plan lists the token tiles of groups of
-// at least min_tokens tokens in tiles[0 .. 1 + 2 * vh_mfma_max_tiles) and the
-// other non-empty groups in small[E + 1] (the `active` format); gate/up writes
+// at least min_tokens tokens (32, 64 or 128 rows each) and the two launches'
+// per-XCD runs in tiles[0 .. vh_mfma_plan_words) (layout: mfma_plan_kernel),
+// for the expert types and sizes the launches will get, and the other
+// non-empty groups in small[E + 1] (the `active` format); gate/up writes
 // bf16 h rows in dispatch order into hs [P x fe]; down writes ybuf rows like
 // vh_grouped_down. The forward pass sends every group of such a call to the
 // matrix cores (min_tokens 1): a tile's cost is its weight staging, so even a
@@ -156,11 +158,14 @@ int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **bu
 // 666 / 678 / 727 us with groups below 4 / 8 / 16 tokens on the fp32 kernels).
 constexpr int kMfmaMinCall = 64;
 bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E);
+constexpr int kPlanRunsGU = 1, kPlanRunsDN = 10, kPlanHead = 19;  // offsets in the tile plan
 int vh_mfma_max_tiles(int P, int E);
-int vh_mfma_plan(const int32_t *counts, int E, int min_tokens, int32_t *tiles, int32_t *small, hipStream_t s);
+int vh_mfma_plan_words(int P, int E);
+int vh_mfma_plan(const int32_t *counts, int E, int P, int min_tokens, uint32_t tg, uint32_t td, int d, int fe,
+                 int32_t *tiles, int32_t *small, hipStream_t s);
 // xb: the bf16 copy of hb (vh_to_bf16)
 int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s);
-// `packed`: table points at vh_mfma_pack_q8's row octets (Q8_0 only).
+// `packed`: table points at vh_mfma_pack_q8's fragments (Q8_0 only).
 int vh_mfma_gateup(uint32_t type, const int32_t *tiles, int max_tiles, const int32_t *counts, const int32_t *offs,
                    const int32_t *perm, const void *const *table, bool packed, const void *xb, int d, int fe, int k,
                    void *hs, hipStream_t s);
@@ -168,8 +173,9 @@ int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32
                  const int32_t *perm, const void *const *table, bool packed, const void *hs, int d, int fe,
                  float *ybuf, hipStream_t s);
 // A copy of the Q8_0 experts behind `table` (gate, up: fe rows of d; down: d
-// rows of fe) in the GEMMs' row octets, as vh_mdec_pack_layer does for the
-// decode batch (the same bytes; -EBUSY under capture).
+// rows of fe) in the matrix cores' operand order (32-row fragments per K step
+// of 64, each lane's bytes together; the same bytes, -EBUSY under capture),
+// for the GEMMs of pinned layers.
 int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s);
 
 // Fused one-token experts kernel (moe_fused.hip): top-k, gate/up, down and
