@@ -724,11 +724,11 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     if (mfma) {  // every group on the matrix cores (its small list stays empty)
         const int mt = vh_mfma_max_tiles(P, E);
-        if (!rc) rc = vh_mfma_plan(ws.counts, E, P, 1, tg, td, d, fe, ws.tiles, ws.small, s);
-        if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
-        // Q8_0 experts of a pinned layer: the row-octet copy (made on the first such call that may allocate)
+        // Q8_0 experts of a pinned layer: the fragment copy (made on the first such call that may allocate)
         const void *const *pt =
             (!rc && tg == VT_Q8_0 && td == VT_Q8_0) ? packed_table(m, layer, table, !src, s, 1) : nullptr;
+        if (!rc) rc = vh_mfma_plan(ws.counts, E, P, 1, tg, td, d, fe, ws.tiles, ws.small, s);
+        if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
         const void *const *tb = pt ? pt : table;
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, tb, pt != nullptr, ws.xb, d, fe, k,
                                      ws.hs, s);

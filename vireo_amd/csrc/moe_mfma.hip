@@ -11,19 +11,22 @@
 // dequantized exactly (src/gguf_compute.c:52-120) and then rounded to bf16
 // while they are staged, and products are accumulated in fp32.
 //
-// Tiles: a workgroup (512 threads) owns kBM = 128 rows of one group (a token
-// tile) and kBRows = 256 weight rows (gate/up: 128 rows of gate and the same
-// 128 rows of up; down: 256 rows), and steps over K in kBK = 64 columns. Each
-// step stages both operands in LDS as 16-byte chunks of 8 consecutive K
-// values laid out [K/8][row] (row index XOR-swizzled by the chunk), so a
-// 32-lane group's operand read is one contiguous 512-byte run. Four waves
-// multiply and four stage (see mfma_proj_kernel).
+// Tiles: a workgroup (512 threads) owns a token tile of 32, 64 or 128 rows of
+// one group (whole 128-row tiles, the remainder in the smallest that holds
+// it) and kBRows = 256 weight rows (gate/up: 128 rows of gate and the same
+// 128 rows of up; down: 256 rows), and steps over K in kBK = 64 columns. The
+// inputs pass through LDS as 16-byte chunks of 8 consecutive K values laid
+// out [K/8][row] (row index XOR-swizzled by the chunk), so a 32-lane group's
+// operand read is one contiguous 512-byte run. GGUF-row experts: four waves
+// multiply and four stage the weights through LDS too (mfma_proj_kernel);
+// pinned Q8_0 experts come from a copy in the operand order and every wave
+// multiplies, reading its own weights (mfma_frag_kernel).
 //
 // Order: the workgroups are numbered so that each XCD (hardware dispatch sends
 // workgroup b to XCD b mod 8) takes a contiguous run of (token tile, column
 // tile) pairs, column tiles fastest: the workgroups sharing a token tile, and
 // the consecutive token tiles of one expert that share its weight tiles, meet
-// in the same L2.
+// in the same L2. The runs are cut at equal shares of the staged bytes.
 //
 // Outputs: gate/up writes h as bf16 rows in dispatch order (hs[offs[e] + i]),
 // so the down GEMM reads its A operand contiguously; down writes the fp32 row
@@ -536,9 +539,11 @@ VH_DEV void frag_tile(bf16x8 (&As)[2][kChunks][kBM], gbyte *F, const int32_t *__
 }
 
 // mfma_proj_kernel's grid, plan and outputs on kQ8Frag experts: table[3 e] =
-// the expert's gate/up fragments, table[3 e + 2] its down fragments.
+// the expert's gate/up fragments, table[3 e + 2] its down fragments. Held to
+// 128 registers (four waves per SIMD): two workgroups share a CU, one
+// multiplying while the other waits at its barrier.
 template <bool GATEUP>
-__global__ void __launch_bounds__(kThreads) mfma_frag_kernel(const int32_t *__restrict__ tiles,
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) mfma_frag_kernel(const int32_t *__restrict__ tiles,
                                                              const int32_t *__restrict__ counts,
                                                              const int32_t *__restrict__ offs,
                                                              const int32_t *__restrict__ perm,
@@ -586,20 +591,37 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const float4 *__restrict__
 // the inputs), in 64-byte units: the cost by which the XCDs' runs are cut.
 __host__ __device__ constexpr int tile_step_cost(int wb, int bm) { return (wb + bm * kBK * 2) / 64; }
 
+// A group's token tiles: n128 of 128 rows, then one of rbm (32 or 64) rows if
+// rbm != 0 - the remainder in the smallest tile that holds it (above 64 rows,
+// a whole tile).
+struct GroupTiles {
+    int n128, rbm;
+    __host__ __device__ explicit GroupTiles(int cnt) {
+        n128 = cnt / 128;
+        int r = cnt - 128 * n128;
+        if (r > 64) {
+            n128++;
+            r = 0;
+        }
+        rbm = r == 0 ? 0 : r <= 32 ? 32 : 64;
+    }
+    __host__ __device__ int count() const { return n128 + (rbm ? 1 : 0); }
+    __host__ __device__ int rows(int i) const { return i < n128 ? 128 : rbm; }
+};
+
 // One workgroup of 256 threads (thread e = expert e, E <= 256). The plan:
 //   tiles[0]               n, the number of token tiles
 //   tiles[kPlanRunsGU + x]  x = 0..8: where XCD x's run of gate/up (tile,
 //                           column tile) pairs starts (x = 8: the end)
 //   tiles[kPlanRunsDN + x]  the same for the down launch
-//   tiles[kPlanHead + 2 t]  tile t: expert | rows << 16 (rows 32, 64 or 128),
-//                           then the tile's first row within its group
-// for the groups of at least min_tokens tokens (experts ascending; a group
-// takes whole 128-row tiles and its remainder one tile of 32 or 64 rows, or
-// a last 128-row tile above 64), and the list of the other non-empty groups
-// in the dispatch kernel's `active` format (small[0 .. n), n at small[E]).
-// The runs are cut at equal shares of the launch's staged bytes
-// (tile_step_bytes per pair); a cut that would give an XCD more pairs than
-// the launch has slots per XCD falls back to equal shares of pairs.
+//   tiles[kPlanHead + 2 t]  tile t: expert | rows << 16 (32, 64 or 128), then
+//                           the tile's first row within its group
+// for the groups of at least min_tokens tokens (experts ascending, tiles as
+// GroupTiles), and the list of the other non-empty groups in the dispatch
+// kernel's `active` format (small[0 .. n), n at small[E]). The runs are cut
+// at equal shares of the launch's staged bytes (tile_step_cost per pair); a
+// cut that would give an XCD more pairs than the launch has slots per XCD
+// falls back to equal shares of pairs.
 __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restrict__ counts, int E, int min_tokens,
                                                         int nct_gu, int wb_gu, int slots_gu, int nct_dn,
                                                         int wb_dn, int slots_dn, int32_t *__restrict__ tiles,
@@ -611,20 +633,15 @@ __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restric
     __shared__ int ntiles;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int cnt = t < E ? counts[t] : 0;
-    const bool big = cnt > 0 && cnt >= min_tokens;
-    int n128 = cnt / kBM, rem = cnt % kBM;
-    if (rem > kBM / 2) {
-        n128++;
-        rem = 0;
-    }
-    const int rbm = rem == 0 ? 0 : rem <= 32 ? 32 : 64;
-    const int nt = big ? n128 + (rbm ? 1 : 0) : 0, sm = (!big && cnt > 0) ? 1 : 0;
+    const bool on = cnt > 0 && cnt >= min_tokens;
+    const GroupTiles gt(on ? cnt : 0);
+    const int nt = gt.count(), sm = (!on && cnt > 0) ? 1 : 0;
     const int ncts[2] = {nct_gu, nct_dn};
     const int wbs[2] = {wb_gu, wb_dn};
     int c[2];
 #pragma unroll
     for (int l = 0; l < 2; l++)
-        c[l] = big ? ncts[l] * (n128 * tile_step_cost(wbs[l], kBM) + (rbm ? tile_step_cost(wbs[l], rbm) : 0)) : 0;
+        c[l] = ncts[l] * (gt.n128 * tile_step_cost(wbs[l], kBM) + (gt.rbm ? tile_step_cost(wbs[l], gt.rbm) : 0));
     int it = nt, is = sm;
     int ic[2] = {c[0], c[1]};
 #pragma unroll
@@ -655,8 +672,8 @@ __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restric
     }
     const int ex_t = bt + it - nt, ex_s = bs + is - sm;
     for (int i = 0; i < nt; i++) {
-        tiles[kPlanHead + 2 * (ex_t + i)] = t | ((i < n128 ? kBM : rbm) << 16);
-        tiles[kPlanHead + 2 * (ex_t + i) + 1] = i * kBM;
+        tiles[kPlanHead + 2 * (ex_t + i)] = t | (gt.rows(i) << 16);
+        tiles[kPlanHead + 2 * (ex_t + i) + 1] = kBM * i;
     }
     if (sm) small[ex_s] = t;
     if (t == 255) {
@@ -674,16 +691,11 @@ __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restric
         for (int x = 1; x < kXcds; x++) {
             const int target = int(int64_t(x) * total[l] / kXcds);
             if (c[l] > 0 && ex_c <= target && target < ex_c + c[l]) {
-                const int off = target - ex_c, c128 = tile_step_cost(wbs[l], kBM), full = n128 * ncts[l] * c128;
-                int tl, col;
-                if (off < full) {
-                    tl = off / (ncts[l] * c128);
-                    col = (off - tl * ncts[l] * c128) / c128;
-                } else {
-                    tl = n128;
-                    col = (off - full) / tile_step_cost(wbs[l], rbm);
-                }
-                runs[l][x] = (ex_t + tl) * ncts[l] + col;
+                // the tile holding the target (a whole 128-row tile or the last), then its column
+                const int off = target - ex_c, c128 = tile_step_cost(wbs[l], kBM), full = gt.n128 * ncts[l] * c128;
+                const int i = off < full ? off / (ncts[l] * c128) : gt.n128;
+                const int rest = off - i * ncts[l] * c128;
+                runs[l][x] = (ex_t + i) * ncts[l] + min(rest / tile_step_cost(wbs[l], gt.rows(i)), ncts[l] - 1);
             }
         }
     }
@@ -769,9 +781,10 @@ int vh_mfma_plan(const int32_t *counts, int E, int P, int min_tokens, uint32_t t
     const int mt = vh_mfma_max_tiles(P, E);
     const TileCost gu = tile_cost(tg, d, fe, true, mt), dn = tile_cost(td, fe, d, false, mt);
     // the plan's costs are 32-bit sums over every (tile, column tile) pair
-    if (int64_t(mt) * std::max(gu.nct, dn.nct) * tile_step_cost(std::max(gu.wb, dn.wb), kBM) > INT32_MAX) return -E2BIG;
-    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1), dim3(256), 0, s, counts, E, min_tokens, gu.nct, gu.wb, gu.slots,
-                       dn.nct, dn.wb, dn.slots, tiles, small);
+    if (int64_t(mt) * std::max(gu.nct, dn.nct) * tile_step_cost(std::max(gu.wb, dn.wb), kBM) > INT32_MAX)
+        return -E2BIG;
+    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1), dim3(256), 0, s, counts, E, min_tokens, gu.nct, gu.wb,
+                       gu.slots, dn.nct, dn.wb, dn.slots, tiles, small);
     return vh_check(hipGetLastError());
 }
 
