@@ -174,8 +174,7 @@ def test_prefill_q8_fragments(cuda):
     read a copy of its experts in matrix-operand fragments (each lane's bytes
     of a 32-row, 64-column step together) made by the first call with
     packing on: the outputs equal the GGUF-row kernels' bit for bit, on that
-    call and the next. Two experts are unregistered; 130 tokens give groups
-    of every tile size."""
+    call and the next. Two experts are unregistered."""
     lib = _lib.load()
     shape = W.SHAPES["olmoe-q8_0"]
     m = M.DeviceMoE(shape, 1, seed=67, unregistered={(0, 3), (0, 40)})
