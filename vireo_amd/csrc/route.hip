@@ -96,32 +96,28 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
     // staging: thread tid loads column tid & 63 of token rows (tid >> 6) + 4j
     // (j < 16) and of router rows (tid >> 6) + 4j (j < kExCpl)
     const int cc = tid & 63, r0 = tid >> 6;
-    float xr[16], rr[kExCpl];
-    auto load = [&](int c0) {
-        const bool in = c0 + cc < d;
+    // two register sets, loaded two chunks ahead; every load unconditional
+    // (rows and columns past the end repeat the last one, and their values are
+    // never used), so the wait before a set's store counts only older loads
+    float xr2[2][16], rr2[2][kExCpl];
+    auto load = [&](int set, int c0) {
+        const int c = min(c0 + cc, d - 1);
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int tt = r0 + 4 * j;
-            xr[j] = (in && t0 + tt < T) ? hb[size_t(t0 + tt) * d + c0 + cc] : 0.0f;
-        }
+        for (int j = 0; j < 16; j++) xr2[set][j] = hb[size_t(min(t0 + r0 + 4 * j, T - 1)) * d + c];
 #pragma unroll
-        for (int j = 0; j < kExCpl; j++) {
-            const int ee = r0 + 4 * j;
-            rr[j] = (in && e0 + ee < E) ? R[size_t(e0 + ee) * d + c0 + cc] : 0.0f;
-        }
+        for (int j = 0; j < kExCpl; j++) rr2[set][j] = R[size_t(min(e0 + r0 + 4 * j, E - 1)) * d + c];
     };
-    auto store = [&]() {
+    auto store = [&](int set) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) xs[cc][r0 + 4 * j] = xr[j];
+        for (int j = 0; j < 16; j++) xs[cc][r0 + 4 * j] = xr2[set][j];
 #pragma unroll
-        for (int j = 0; j < kExCpl; j++) reinterpret_cast<float *>(&rs[r0 + 4 * j][0])[cc] = rr[j];
+        for (int j = 0; j < kExCpl; j++) reinterpret_cast<float *>(&rs[r0 + 4 * j][0])[cc] = rr2[set][j];
     };
     float acc[kExCpl] = {};
-    load(0);
-    for (int c0 = 0; c0 < d; c0 += kExChunk) {
-        store();
-        __syncthreads();
-        if (c0 + kExChunk < d) load(c0 + kExChunk);
+    auto chunk = [&](int set, int c0) {
+        store(set);
+        lds_barrier();  // LDS only: the loads in flight stay in flight
+        load(set, c0 + 2 * kExChunk);
         if (d - c0 >= kExChunk) {
 #pragma unroll
             for (int i4 = 0; i4 < kExChunk / 4; i4++) {
@@ -146,8 +142,16 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
                     acc[q] = add_rn(acc[q], mul_rn(reinterpret_cast<const float *>(&rs[kExCpl * g + q][0])[i], xv));
             }
         }
-        __syncthreads();
+        lds_barrier();
+    };
+    load(0, 0);
+    load(1, kExChunk);
+    int c0 = 0;
+    for (; c0 + kExChunk < d; c0 += 2 * kExChunk) {
+        chunk(0, c0);
+        chunk(1, c0 + kExChunk);
     }
+    if (c0 < d) chunk(0, c0);
     const int t = t0 + tl;
     if (t < T) {
 #pragma unroll
