@@ -171,12 +171,23 @@ __global__ void __launch_bounds__(256) dispatch_place_kernel(const int32_t *__re
         }
     }
     int run = base;
+    const bool al16 = (reinterpret_cast<uintptr_t>(idx) & 15u) == 0;
     for (int p0 = 0; p0 < P; p0 += 256 * kPlacePer) {
         const int q0 = p0 + kPlacePer * tid;
         uint32_t hit = 0;
+        if (q0 + kPlacePer <= P && al16) {  // four 16-byte loads (q0 is a multiple of 16)
+            const int4 *q4 = reinterpret_cast<const int4 *>(idx + q0);
 #pragma unroll
-        for (int j = 0; j < kPlacePer; j++)
-            if (q0 + j < P && idx[q0 + j] == e) hit |= 1u << j;
+            for (int j = 0; j < kPlacePer / 4; j++) {
+                const int4 v = q4[j];
+                hit |= uint32_t(v.x == e) << (4 * j) | uint32_t(v.y == e) << (4 * j + 1) |
+                       uint32_t(v.z == e) << (4 * j + 2) | uint32_t(v.w == e) << (4 * j + 3);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kPlacePer; j++)
+                if (q0 + j < P && idx[q0 + j] == e) hit |= 1u << j;
+        }
         int total;
         int pos = run + block_excl_scan(__popc(hit), total, wsum);
         while (hit) {
