@@ -224,9 +224,11 @@ int vireo_hip_set_path(int path);
  * store's capacity (as much again as the layer's expert bytes), made from the
  * pinned views and freed with the pin (expert_store_unpin_layer) or the store;
  * a caller that rewrites a pinned layer's expert bytes in place must unpin
- * and pin it again. Results are the same bit for bit either way. 0 turns it
- * off for later calls (existing copies stay until unpinned). No counterpart in
- * the reference. */
+ * and pin it again. Calls of 64 or more tokens on a pinned Q8_0 layer make
+ * and read, the same way, a copy in matrix-operand fragments (each lane's
+ * bytes of a 32-row, 64-column step together) for the prefill GEMMs. Results
+ * are the same bit for bit either way. 0 turns both off for later calls
+ * (existing copies stay until unpinned). No counterpart in the reference. */
 int vireo_hip_set_packed(int on);
 
 /* The one-token decode plan of moe_ffn_forward as separate launches over a
