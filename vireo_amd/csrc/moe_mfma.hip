@@ -285,19 +285,18 @@ VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kB
         // step t's words live in register set t % kSets: issued at step
         // t - kSets, dequantized into LDS at step t - 1
 #pragma unroll
-        for (int j = 0; j < kSets; j++)
-            if (j < nk) load(st[j], j);
+        for (int j = 0; j < kSets; j++) load(st[j], min(j, nk - 1));
         store(st[0], 0, 0);
-        __syncthreads();
+        lds_barrier();
         for (int s0 = 0; s0 < nk; s0 += kSets) {
 #pragma unroll
             for (int j = 0; j < kSets; j++) {
                 // step s: the multiplying waves read buffer s & 1
                 const int s = s0 + j;
                 if (s >= nk) break;
-                if (s + kSets < nk) load(st[j], s + kSets);
+                load(st[j], min(s + kSets, nk - 1));  // unconditional: the waits count only older loads
                 if (s + 1 < nk) store(st[(j + 1) % kSets], (s + 1) & 1, s + 1);
-                __syncthreads();
+                lds_barrier();  // LDS only: the loads in flight stay in flight
             }
         }
         return;
@@ -320,7 +319,7 @@ VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kB
         for (int j = 0; j < FJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-    __syncthreads();  // buffer 0 staged
+    lds_barrier();  // buffer 0 staged
     for (int s = 0; s < nk; s++) {
         const int buf = s & 1;
 #pragma unroll
@@ -336,7 +335,7 @@ VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kB
 #pragma unroll
                 for (int j = 0; j < FJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // epilogue
