@@ -727,8 +727,9 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         // Q8_0 experts of a pinned layer: the fragment copy (made on the first such call that may allocate)
         const void *const *pt =
             (!rc && tg == VT_Q8_0 && td == VT_Q8_0) ? packed_table(m, layer, table, !src, s, 1) : nullptr;
-        if (!rc) rc = vh_mfma_plan(ws.counts, E, P, 1, tg, td, d, fe, ws.tiles, ws.small, s);
-        if (!rc) rc = vh_to_bf16(hb, ws.xb, int64_t(n_tokens) * d, s);
+        // the tile plan and the GEMMs' bf16 inputs in one launch
+        if (!rc) rc = vh_mfma_plan(ws.counts, E, P, 1, tg, td, d, fe, ws.tiles, ws.small, hb, ws.xb,
+                                   int64_t(n_tokens) * d, s);
         const void *const *tb = pt ? pt : table;
         if (!rc) rc = vh_mfma_gateup(tg, ws.tiles, mt, ws.counts, ws.offs, ws.perm, tb, pt != nullptr, ws.xb, d, fe, k,
                                      ws.hs, s);

@@ -575,15 +575,19 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         frag_tile<GATEUP, 128>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
 }
 
-// bf16 copy of n fp32 values (n a multiple of 4, both 16-byte aligned)
-__global__ void __launch_bounds__(256) to_bf16_kernel(const float4 *__restrict__ x, uint2 *__restrict__ y, int64_t n4) {
-    for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+// bf16 copy of n4 x 4 fp32 values (both 16-byte aligned) by workgroup blk of nblk
+VH_DEV void bf16_copy(const float4 *__restrict__ x, uint2 *__restrict__ y, int64_t n4, int blk, int nblk) {
+    for (int64_t i = blk * int64_t(256) + threadIdx.x; i < n4; i += int64_t(nblk) * 256) {
         const float4 v = x[i];
         typedef float f32x4_ __attribute__((ext_vector_type(4)));
         typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
         const bf16x4 b = __builtin_convertvector(f32x4_{v.x, v.y, v.z, v.w}, bf16x4);
         y[i] = __builtin_bit_cast(uint2, b);
     }
+}
+
+__global__ void __launch_bounds__(256) to_bf16_kernel(const float4 *__restrict__ x, uint2 *__restrict__ y, int64_t n4) {
+    bf16_copy(x, y, n4, blockIdx.x, gridDim.x);
 }
 
 // The bytes a token tile of bm rows stages per K step (the weights' wb and
@@ -624,7 +628,12 @@ struct GroupTiles {
 __global__ void __launch_bounds__(256) mfma_plan_kernel(const int32_t *__restrict__ counts, int E, int min_tokens,
                                                         int nct_gu, int wb_gu, int slots_gu, int nct_dn,
                                                         int wb_dn, int slots_dn, int32_t *__restrict__ tiles,
-                                                        int32_t *__restrict__ small) {
+                                                        int32_t *__restrict__ small, const float4 *__restrict__ x,
+                                                        uint2 *__restrict__ y, int64_t n4) {
+    if (blockIdx.x > 0) {  // the other workgroups: the bf16 copy of the inputs (to_bf16_kernel)
+        bf16_copy(x, y, n4, blockIdx.x - 1, gridDim.x - 1);
+        return;
+    }
     __shared__ int wsum[4][2];
     __shared__ int wcost[4][2];
     __shared__ int runs[2][kXcds + 1];
@@ -775,15 +784,19 @@ int vh_mfma_max_tiles(int P, int E) { return P / kBM + E; }
 int vh_mfma_plan_words(int P, int E) { return kPlanHead + 2 * vh_mfma_max_tiles(P, E); }
 
 int vh_mfma_plan(const int32_t *counts, int E, int P, int min_tokens, uint32_t tg, uint32_t td, int d, int fe,
-                 int32_t *tiles, int32_t *small, hipStream_t s) {
-    if (E > 256) return -EINVAL;
+                 int32_t *tiles, int32_t *small, const float *hb, void *xb, int64_t n, hipStream_t s) {
+    if (E > 256 || (hb && (n % 4 || ((reinterpret_cast<uintptr_t>(hb) | reinterpret_cast<uintptr_t>(xb)) & 15u))))
+        return -EINVAL;
+    const int64_t n4 = hb ? n / 4 : 0;
+    const unsigned copy_blocks = unsigned(std::min<int64_t>((n4 + 255) / 256, 4096));
     const int mt = vh_mfma_max_tiles(P, E);
     const TileCost gu = tile_cost(tg, d, fe, true, mt), dn = tile_cost(td, fe, d, false, mt);
     // the plan's costs are 32-bit sums over every (tile, column tile) pair
     if (int64_t(mt) * std::max(gu.nct, dn.nct) * tile_step_cost(std::max(gu.wb, dn.wb), kBM) > INT32_MAX)
         return -E2BIG;
-    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1), dim3(256), 0, s, counts, E, min_tokens, gu.nct, gu.wb,
-                       gu.slots, dn.nct, dn.wb, dn.slots, tiles, small);
+    hipLaunchKernelGGL(mfma_plan_kernel, dim3(1 + copy_blocks), dim3(256), 0, s, counts, E, min_tokens, gu.nct,
+                       gu.wb, gu.slots, dn.nct, dn.wb, dn.slots, tiles, small,
+                       reinterpret_cast<const float4 *>(hb), static_cast<uint2 *>(xb), n4);
     return vh_check(hipGetLastError());
 }
 

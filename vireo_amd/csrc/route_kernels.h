@@ -161,8 +161,10 @@ bool vh_mfma_supported(uint32_t tg, uint32_t td, int d, int fe, int E);
 constexpr int kPlanRunsGU = 1, kPlanRunsDN = 10, kPlanHead = 19;  // offsets in the tile plan
 int vh_mfma_max_tiles(int P, int E);
 int vh_mfma_plan_words(int P, int E);
+// hb (optional): the same launch also writes xb, the bf16 copy of hb's n
+// values (as vh_to_bf16).
 int vh_mfma_plan(const int32_t *counts, int E, int P, int min_tokens, uint32_t tg, uint32_t td, int d, int fe,
-                 int32_t *tiles, int32_t *small, hipStream_t s);
+                 int32_t *tiles, int32_t *small, const float *hb, void *xb, int64_t n, hipStream_t s);
 // xb: the bf16 copy of hb (vh_to_bf16)
 int vh_to_bf16(const float *x, void *y, int64_t n, hipStream_t s);
 // `packed`: table points at vh_mfma_pack_q8's fragments (Q8_0 only).
