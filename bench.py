@@ -89,6 +89,8 @@ def parse():
     ap.add_argument("--traffic", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="no GPU run: read four rocprofv3 --pmc output directories (FETCH_SIZE and WRITE_SIZE of "
                          "this workload, then of --workload copy-512MiB) and write profiles/traffic_<workload>.json")
+    ap.add_argument("--phases", action="store_true",
+                    help="only the per-phase breakdown of one-token calls (moe_decode_phases), no timed replay")
     ap.add_argument("--plan", type=int, default=0,
                     help="execution plan (vireo_hip_set_path): 0 automatic, 1 decode, 2 grouped, 3 fused, 4 fp32")
     return ap.parse_args()
@@ -832,6 +834,13 @@ def main():
 
     for l in range(L):  # pin every layer and size the workspace outside the timed graph
         step(l)
+    if args.phases:
+        if B != 1:
+            raise SystemExit("--phases: one-token workloads only")
+        print(json.dumps({"workload": args.workload, "plan": args.plan,
+                          "phases": decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)}), flush=True)
+        m.close()
+        return
     for i in range(Wm):
         step(i)
     torch.cuda.synchronize()
@@ -888,11 +897,82 @@ def main():
                               "alg_bytes_per_launch": int(lb)}
     if B == 1 and lib.moe_decode_state_bytes(M.C.byref(m.model)) > 0:
         result["roofline"]["kernels"] = decode_stage_roofline(m, shape, L, x_all, hb_all, dev)
+        result["phases"] = decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(shape, B, args.seed, args.cpu_seconds)
     m.close()
     print(json.dumps(result), flush=True)
+
+
+# Phases of the one-token decode kernels as moe_decode_phases records them
+# (per kernel, the stamp slots after slot 0 = the workgroup's start), for the
+# three-kernel plan and for the one-launch layer kernel.
+PHASES_3K = {0: ["router part"], 1: ["router parts loaded", "top-k chosen", "first gate/up row", "gate/up rows done"],
+             2: ["down plan loaded", "first down row", "down rows done", "combine written"]}
+PHASES_1K = {0: ["router part", "parts received", "top-k chosen", "first gate/up row", "activations published",
+                 "activations received", "down + combine written"]}
+PHASES_SLOTS = {0: ["router part published", "parts received", "top-k chosen", "first gate/up row",
+                    "slot's activations received", "down rows computed", "combine written"]}
+STAMP_HZ = 100e6  # s_memrealtime
+
+
+def phase_breakdown(stamps, one_launch_names=None):
+    """The critical path of one-token layer calls from moe_decode_phases
+    stamps [n x 3*256*8]: per kernel, its first workgroup's start, the spread
+    of its workgroups' starts, and for each phase the time at which the last
+    workgroup reached it; the gap between one kernel's last phase and the next
+    kernel's first start is the kernel boundary. Returns the median over calls
+    of each step in microseconds, in order, and the share of calls whose top-k
+    took the exact-logit path."""
+    st = stamps.reshape(stamps.shape[0], 3, 256, 8).astype(np.int64)
+    present = [kk for kk in range(3) if (st[:, kk, :, 0] > 0).any()]
+    names = PHASES_3K if len(present) == 3 else (one_launch_names or PHASES_SLOTS)
+    steps, exact = {}, []
+    for call in st:
+        prev_end, t0 = None, None
+        for kk in present:
+            wg = call[kk][call[kk][:, 0] > 0]
+            start = wg[:, 0].min()
+            t0 = start if t0 is None else t0
+            if prev_end is not None:
+                steps.setdefault(f"k{kk} boundary (previous kernel's last phase -> first workgroup start)",
+                                 []).append(start - prev_end)
+            steps.setdefault(f"k{kk} workgroup start spread", []).append(wg[:, 0].max() - start)
+            last = start
+            for i, nm in enumerate(names[kk], start=1):
+                t = wg[:, i].max()
+                steps.setdefault(f"k{kk} {nm}", []).append(t - last)
+                last = t
+            prev_end = last
+        steps.setdefault("total (first start -> last phase)", []).append(prev_end - t0)
+        if len(present) == 3:
+            exact.append(bool((call[1][:, 7] == 1).any()))
+    out = [{"step": k, "us": round(float(np.median(v)) / STAMP_HZ * 1e6, 3)} for k, v in steps.items()]
+    return out, (round(float(np.mean(exact)), 4) if exact else None)
+
+
+def decode_phases(m, shape, L, x_all, hb_all, dev, plan=0):
+    """moe_decode_phases over 8 x layers distinct (layer, token) calls captured
+    in one HIP graph (replayed twice, the second replay read back)."""
+    import torch
+    n = 8 * L
+    layers = [j % L for j in range(n)]
+    x = x_all[:n].clone()
+    hb = hb_all[:n].contiguous()
+    stamps = torch.zeros((n, 3 * 256 * 8), dtype=torch.int64, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        m.decode_phases(layers, x, hb, stream=s, stamps=stamps)
+    torch.cuda.synchronize()
+    g.replay()
+    g.replay()
+    torch.cuda.synchronize()
+    steps, exact = phase_breakdown(stamps.cpu().numpy(), PHASES_1K if plan == 5 else None)
+    return {"calls": n, "source": "moe_decode_phases (s_memrealtime per workgroup and phase, one HIP graph)",
+            "steps": steps, "exact_path_share": exact}
 
 
 def decode_stage_roofline(m, shape, L, x_all, hb_all, dev):

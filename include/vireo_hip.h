@@ -266,6 +266,27 @@ int moe_decode_stage(const vireo_moe_model *m, int layer, int stage, float *x, c
  * us_out (host). Results are those of n moe_decode_stage calls. */
 int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n, const int *layers, float *x, const float *hb,
                            void *states, int64_t state_stride, int32_t *idx, float *w, float *us_out, void *stream);
+/* Per-phase timestamps of one-token layer calls (a measurement aid with no
+ * counterpart in the reference). Enqueues n moe_ffn_forward calls on stream,
+ * call i on layer layers[i] (host array) with token row i of x / hb (device
+ * [n x dim]); the one-token decode kernels of call i record, per workgroup
+ * (the first 256) and phase, the device clock (s_memrealtime, 100 MHz, one
+ * clock for all CUs) into stamps + i * VIREO_PHASE_WORDS (device uint64_t,
+ * zeroed by the caller): word (kernel * 256 + workgroup) * 8 + phase.
+ * Kernels and phases of the three-kernel decode plan:
+ *   0 router:    0 start, 1 the expert's router part computed
+ *   1 gate/up:   0 start, 1 router parts loaded, 2 top-k chosen, 3 first
+ *                row computed, 4 every row written; word 7 is 1 when the
+ *                order took the exact-logit path
+ *   2 down:      0 start, 1 plan loaded, 2 first row computed, 3 every row
+ *                computed, 4 outputs written
+ * and of the one-launch layer kernel (kernel 0): 0 start, 1 router part,
+ * 2 every part received, 3 top-k chosen, 4 first gate/up row, 5 activations
+ * published, 6 activations received, 7 end. Results are moe_ffn_forward's.
+ * The calls may be captured in a HIP graph. */
+#define VIREO_PHASE_WORDS (3 * 256 * 8)
+int moe_decode_phases(const vireo_moe_model *m, int n, const int *layers, float *x, const float *hb,
+                      uint64_t *stamps, void *stream);
 
 /* ---- MoE stack decode step (src/gguf_run.c:216-254) --------------------------- */
 

@@ -453,3 +453,36 @@ def test_layer_kernel_sequence(cuda, oracle, path, name):
     d5, d1 = outs[5][0] - x, outs[1][0] - x
     assert np.abs(d5 - d1).max() <= 1e-5 * np.abs(d1).max()
     m.close()
+
+
+@pytest.mark.parametrize("name", ["qwen3-30b-a3b-q4_k_m", "olmoe-q8_0"])
+def test_decode_phases_stamps(cuda, name):
+    """moe_decode_phases: the same results as moe_ffn_forward bit for bit, and
+    for every call three kernels whose workgroups' stamps never go backwards,
+    each kernel starting after the previous one's phases (stream order)."""
+    shape = W.SHAPES[name]
+    m = M.DeviceMoE(shape, 2, seed=64)
+    n = 6
+    x, hb = W.host_hidden(shape.d, n, 64)
+    hbt = torch.from_numpy(hb).to(cuda)
+    xs = torch.from_numpy(x).to(cuda)
+    layers = [t % 2 for t in range(n)]
+    st = m.decode_phases(layers, xs, hbt)
+    torch.cuda.synchronize()
+    xr = torch.from_numpy(x).to(cuda)
+    for t in range(n):
+        m.forward(layers[t], xr[t:t + 1], hbt[t:t + 1])
+    torch.cuda.synchronize()
+    assert torch.equal(xs, xr)
+    stamps = st.cpu().numpy().reshape(n, 3, 256, 8)
+    nphase = {0: 2, 1: 5, 2: 5}
+    for call in stamps:
+        prev_end = 0
+        for kk in range(3):
+            wg = call[kk][call[kk][:, 0] > 0]
+            assert len(wg) > 0, f"kernel {kk} recorded nothing"
+            ph = wg[:, :nphase[kk]]
+            assert (np.diff(ph, axis=1) >= 0).all(), f"kernel {kk}: a stamp went backwards"
+            assert wg[:, 0].min() >= prev_end
+            prev_end = ph.max()
+    m.close()

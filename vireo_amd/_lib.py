@@ -196,6 +196,7 @@ SIGNATURES = {
     "moe_decode_stage": (C.c_int, [C.POINTER(MoEModel), C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_decode_stage_timed": (C.c_int, [C.POINTER(MoEModel), C.c_int, C.c_int, c_vp, c_vp, c_vp, c_vp, C.c_int64,
                                          c_vp, c_vp, c_vp, c_vp]),
+    "moe_decode_phases": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "moe_ffn_forward": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp]),
     "moe_ffn_forward_noalloc": (C.c_int, [C.POINTER(MoEModel), C.c_int, c_vp, c_vp, C.c_int, c_vp, c_vp, c_vp]),
     "expert_store_create": (c_vp, [C.c_int, C.c_uint64, C.c_int, C.c_int]),

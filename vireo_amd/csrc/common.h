@@ -19,6 +19,47 @@ extern VhLaunchTiming g_vh_timing;
 
 enum { VT_F32 = 0, VT_F16 = 1, VT_Q4_0 = 2, VT_Q5_0 = 6, VT_Q8_0 = 8, VT_Q4_K = 12, VT_Q6_K = 14 };
 
+// ---- phase timestamps ----------------------------------------------------------
+// The one-token decode kernels can record when each workgroup reaches each of
+// its phases: wave 0 reads s_memrealtime (the device's 100 MHz clock, the
+// same on every CU) and thread 0 stores up to kStampSlots stamps per
+// workgroup at stamps[workgroup * kStampSlots + slot], for the first
+// kStampBlocks workgroups. A null stamps argument records nothing (one scalar
+// branch per stamp). g_vh_stamps is where the launches being issued record:
+// kernel i of a layer call at g_vh_stamps + i * kStampBlocks * kStampSlots;
+// null except inside moe_decode_phases.
+constexpr int kStampSlots = 8, kStampBlocks = 256, kStampKernels = 3;
+extern uint64_t *g_vh_stamps;
+inline uint64_t *vh_stamps_for(int kernel) {
+    return g_vh_stamps ? g_vh_stamps + size_t(kernel) * kStampBlocks * kStampSlots : nullptr;
+}
+struct PhaseStamps {
+    uint64_t *out;
+    uint64_t t[kStampSlots];
+    __device__ explicit PhaseStamps(uint64_t *o) : out(o) {
+        for (int i = 0; i < kStampSlots; i++) t[i] = 0;
+    }
+    __device__ __forceinline__ void now(int i) {
+        if (out) t[i] = __builtin_amdgcn_s_memrealtime();
+    }
+    // the stamp after v is available (the wait for a load that produces v comes first)
+    template <class V>
+    __device__ __forceinline__ void after(int i, V v) {
+        if (out) {
+            asm volatile("" ::"v"(v));
+            t[i] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+    __device__ __forceinline__ void mark(int i, uint64_t v) {
+        if (out) t[i] = v;
+    }
+    __device__ __forceinline__ void store() {
+        const int b = int(blockIdx.y * gridDim.x + blockIdx.x);
+        if (out && threadIdx.x == 0 && b < kStampBlocks)
+            for (int i = 0; i < kStampSlots; i++) out[size_t(b) * kStampSlots + i] = t[i];
+    }
+};
+
 // ---- host-side helpers ------------------------------------------------------
 int vh_check(hipError_t e);            // hipSuccess -> 0, else records the error and returns -EIO
 int vh_finish(hipStream_t s, int rc);  // synchronise when the caller passed no stream
@@ -89,6 +130,30 @@ VH_DEV uint2 ld_u64(gbyte *p) {
 }
 VH_DEV uint4 ld_u128(gbyte *p) {
     const u32x4 v = ldg<u32x4>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// Global loads with the non-temporal hint, for weights a call streams once:
+// measured on MI355X, streaming 24 MB of weights this way between reads of a
+// 1 MB router keeps the router in the memory-side Infinity Cache (its read
+// 4.4 -> 2.9 us), where ordinary loads let the weights evict it. The same
+// fetch code takes an NtPtr where it takes a gbyte pointer.
+struct NtPtr {
+    gbyte *p;
+    VH_DEV NtPtr operator+(int64_t o) const { return NtPtr{p + o}; }
+    VH_DEV NtPtr operator-(int64_t o) const { return NtPtr{p - o}; }
+};
+VH_DEV NtPtr ntmem(const void *p) { return NtPtr{gmem(p)}; }
+template <class V>
+VH_DEV V ldnt(NtPtr a) { return __builtin_nontemporal_load((const __attribute__((address_space(1))) V *)a.p); }
+VH_DEV uint32_t ld_u32(NtPtr a) { return ldnt<uint32_t>(a); }
+VH_DEV uint32_t ld_u16(NtPtr a) { return ldnt<uint16_t>(a); }
+VH_DEV u32x3 ld_u96(NtPtr a) { return ldnt<u32x3>(a); }
+VH_DEV uint2 ld_u64(NtPtr a) {
+    const u32x2 v = ldnt<u32x2>(a);
+    return make_uint2(v.x, v.y);
+}
+VH_DEV uint4 ld_u128(NtPtr a) {
+    const u32x4 v = ldnt<u32x4>(a);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 // bytes [b, b + 4) of the 8-byte value hi:lo, b in 0..3 (v_alignbyte takes b mod 4)

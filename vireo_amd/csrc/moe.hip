@@ -190,14 +190,15 @@ size_t decode_state_layout(const vireo_moe_model *m, size_t off[4]) {
 }
 
 // Plan 5 (and plan 0 once it is measured faster): the whole layer in one launch.
-bool layer_kernel(const vireo_moe_model *m, int layer, const float *xin, const float *x) {
+bool layer_kernel(const vireo_moe_model *m, int layer, const float *xin, const float *x, hipStream_t s) {
+    (void)s;
     if (g_path != 5) return false;
     const vireo_moe_layer &L = m->layers[layer];
     if ((reinterpret_cast<uintptr_t>(xin) | reinterpret_cast<uintptr_t>(x) |
          reinterpret_cast<uintptr_t>(L.router->data)) & 15u)
         return false;
-    return vh_layer_supported(L.gate_exps->ggml_type, L.down_exps->ggml_type, m->dim, m->n_experts, m->n_used,
-                              m->ffn_exp) != 0;
+    const uint32_t tg = L.gate_exps->ggml_type, td = L.down_exps->ggml_type;
+    return vh_layer_supported(tg, td, m->dim, m->n_experts, m->n_used, m->ffn_exp) != 0;
 }
 
 // One token through layer `layer` with the layer kernel: xin = hb (norm false)
@@ -290,7 +291,7 @@ int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const flo
     }
     Ws ws;
     if (int rc = get_ws(1, m->n_experts, m->n_used, m->dim, m->ffn_exp, true, false, &ws)) return rc;
-    if (layer_kernel(m, layer, x, x)) {  // RMSNorm, router, experts and combine in one launch
+    if (layer_kernel(m, layer, x, x, s)) {  // RMSNorm, router, experts and combine in one launch
         int32_t *idx = idx_out ? idx_out : ws.idx;
         int rc = run_layer_kernel(m, layer, table, x, x, true, nw, eps, xb, idx, ws.w, flags_out, s);
         if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, m->n_used, s);
@@ -398,6 +399,24 @@ extern "C" int moe_decode_stage_timed(const vireo_moe_model *m, int stage, int n
         us_out[i] = ms * 1000.0f;
     }
     return rc;
+}
+
+extern "C" int moe_decode_phases(const vireo_moe_model *m, int n, const int *layers, float *x, const float *hb,
+                                 uint64_t *stamps, void *stream) {
+    if (int rc = check_model(m, 0)) return rc;
+    if (n <= 0 || !layers || !x || !hb || !stamps || (reinterpret_cast<uintptr_t>(stamps) & 7u)) return -EINVAL;
+    for (int i = 0; i < n; i++)
+        if (layers[i] < 0 || layers[i] >= m->n_layers) return -EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int d = m->dim;
+    int rc = 0;
+    for (int i = 0; i < n && !rc; i++) {
+        g_vh_stamps = stamps + size_t(i) * kStampKernels * kStampBlocks * kStampSlots;
+        rc = ffn_forward(m, layers[i], x + size_t(i) * d, hb + size_t(i) * d, 1, nullptr, nullptr, s, nullptr,
+                         nullptr);
+        g_vh_stamps = nullptr;
+    }
+    return vh_finish(s, rc);
 }
 
 // The tiled copy of a pinned layer's experts for the matrix-core decode batch,
@@ -691,7 +710,7 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
-    if (decode && !src && layer_kernel(m, layer, hb, x)) {  // the whole layer in one launch
+    if (decode && !src && layer_kernel(m, layer, hb, x, s)) {  // the whole layer in one launch
         rc = run_layer_kernel(m, layer, table, hb, x, false, nullptr, 0.0f, nullptr, idx, w, flags_out, s);
         if (!rc) rc = vh_store_note_routing(m->es, layer, idx, 1, k, s);
         rc = vh_finish(s, rc);

@@ -64,8 +64,13 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
                                                             int32_t *__restrict__ idx_out, float *__restrict__ w_out,
                                                             uint32_t *__restrict__ flags_out,
                                                             DecodePlan *__restrict__ plan, int pf_rows, int pf_nbd,
-                                                            int64_t pf_rb, NormRef nref) {
+                                                            int64_t pf_rb, NormRef nref,
+                                                            uint64_t *__restrict__ stamps) {
     using F = Reg<T>;
+    // stamps: 0 start, 1 router parts loaded, 2 top-k chosen, 3 first gate/up
+    // row computed, 4 every row written, 7 1 when the order took the exact path
+    PhaseStamps ps(stamps);
+    ps.now(0);
     constexpr int NS = F::NS, TPL = 3 * Q;
     __shared__ TopKSmem sm;         // the exact fallback's workspace
     __shared__ __align__(16) float xref[2048];  // the fallback's inputs (with a library-normalised hb: the reference's xb)
@@ -98,7 +103,9 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     //    order is not certified (the same verdict in every wave) is ranked
     //    again by the whole workgroup on exact logits
     int e_j, e_unused, rank[Q];
+    ps.after(1, p[0].c);
     const bool ok = route_select_wave<Q>(p, E, k, j, e_j, j, e_unused, rank, cert[wv]);
+    ps.mark(7, ok ? 0u : 1u);
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
     if (!ok) {
         const float *xe = hb;
@@ -117,35 +124,25 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             plan->down[lane] = table[3 * e + 2];
         }
         if (writer && tid == 0 && flags_out) flags_out[0] = sm.flag;
-    } else if (writer && wv == 0) {
-        int e;
-        float w;
-        route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
-        if (lane < k) {
-            idx_out[lane] = e;
-            w_out[lane] = w;
-            plan->w[lane] = w;
-            plan->down[lane] = table[3 * e + 2];
-        }
-        if (lane == 0 && flags_out) flags_out[0] = 0u;
     }
 
-    // 3. RPW rows of gate and up of the chosen expert j
+    // 3. RPW rows of gate and up of the chosen expert j: their loads first,
+    //    then the down rows' warm-up, and only then the plan (the writer's
+    //    softmax weights), so the workgroup that writes it is not the last to
+    //    start streaming
+    ps.after(2, e_j);
     const uint8_t *G = table_entry<TPL>(tab, 3 * e_j);
     const uint8_t *U = table_entry<TPL>(tab, 3 * e_j + 1);
+    const bool gu_ok = G && U;
     const int o0 = (blockIdx.x * kGuWaves + wv) * RPW;
-    if (!G || !U) {  // unregistered expert: contributes nothing (src/gguf_run.c:201)
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
-            if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = 0.0f;
-        return;
-    }
     typename F::Raw rg[RPW], ru[RPW];
+    if (gu_ok) {
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const int64_t o = min(o0 + r, fe - 1);
-        rg[r] = F::fetch(gmem(G), o * row_bytes, lane);
-        ru[r] = F::fetch(gmem(U), o * row_bytes, lane);
+        for (int r = 0; r < RPW; r++) {
+            const int64_t o = min(o0 + r, fe - 1);
+            rg[r] = F::fetch(gmem(G), o * row_bytes, lane);
+            ru[r] = F::fetch(gmem(U), o * row_bytes, lane);
+        }
     }
     // the down rows' warm-up, issued after this workgroup's own loads.
     // Unconditional loads (threads past the last line repeat it) whose values
@@ -153,7 +150,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     // for the weights issued before them, comes earlier.
     uint32_t pf[kPfPerThread] = {};
     const uint8_t *D = table_entry<TPL>(tab, 3 * e_j + 2);
-    if (pf_rows > 0 && D) {
+    if (gu_ok && pf_rows > 0 && D) {
         const int gq = gridDim.x >> 3, x8 = (blockIdx.y * gridDim.x + blockIdx.x) & 7, q = blockIdx.x >> 3;
         const int64_t span = int64_t(pf_rows) * pf_rb;           // bytes of one down workgroup's rows
         const int lines = int((span + 63) >> 6), per = (pf_nbd >> 3) / gq;  // down workgroups per gate/up one
@@ -165,6 +162,26 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             pf[u] = ld_u32(gmem(D) + off);
         }
     }
+    if (ok && writer && wv == 0) {
+        int e;
+        float w;
+        route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
+        if (lane < k) {
+            idx_out[lane] = e;
+            w_out[lane] = w;
+            plan->w[lane] = w;
+        }
+        // every lane takes part in the cross-lane reads
+        const void *dn = table_entry_of_lane<TPL>(tab, 3 * (lane < k ? e : 0) + 2);
+        if (lane < k) plan->down[lane] = dn;
+        if (lane == 0 && flags_out) flags_out[0] = 0u;
+    }
+    if (!gu_ok) {  // unregistered expert: contributes nothing (src/gguf_run.c:201)
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+            if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = 0.0f;
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
         float g = F::compute(rg[r], lane, xr, xs);
@@ -172,9 +189,12 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
         g = group_sum<64>(g);
         u = group_sum<64>(u);
         if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = swiglu(g, u);
+        if (r == 0) ps.after(3, g);
     }
 #pragma unroll
     for (int u = 0; u < kPfPerThread; u++) asm volatile("" ::"v"(pf[u]));  // keeps the warm-up loads
+    ps.now(4);
+    ps.store();
 }
 
 // The down kernel's row blocks, for the warm-up (0 rows: none).
@@ -195,7 +215,7 @@ int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb
         warm = per * lines <= 512 * kPfPerThread;
     }
     VH_LAUNCH((decode_gateup_kernel<T, Q, RPW>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe, d, renorm,
-              rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref);
+              rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref, vh_stamps_for(1));
     return vh_check(hipGetLastError());
 }
 
@@ -242,8 +262,13 @@ constexpr int kDnRpg = 2;  // rows per lane group
 template <int T, int L, int IPL>
 __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__restrict__ plan,
                                                            const float *__restrict__ h, int d, int fe, int k, int R,
-                                                           int64_t row_bytes, float *__restrict__ x) {
+                                                           int64_t row_bytes, float *__restrict__ x,
+                                                           uint64_t *__restrict__ stamps) {
     using F = Reg<T>;
+    // stamps: 0 start, 1 plan loaded, 2 first row computed, 3 every row
+    // computed (after the barrier), 4 outputs written
+    PhaseStamps ps(stamps);
+    ps.now(0);
     constexpr int NS = F::NS, NG = 256 / L;
     extern __shared__ float ys[];  // [k][R]
     const int tid = threadIdx.x, g = tid / L, li = tid % L;
@@ -278,6 +303,7 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     }
 #pragma unroll
     for (int m = 0; m < IPL; m++) F::sums(xv[m], xs[m]);
+    ps.after(1, wj2);
 #pragma unroll
     for (int rr = 0; rr < kDnRpg; rr++) {
         float acc = 0.0f;
@@ -290,8 +316,10 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
         }
         acc = group_sum<L>(acc);
         if (li == L - 1) ys[j * R + rf + rr * rstep] = acc;
+        if (rr == 0) ps.after(2, acc);
     }
     __syncthreads();
+    ps.now(3);
     if (tid < 64) {  // R <= 64: the combining threads are in wave 0
         const int pres = dj2 != nullptr;
         float a = 0.0f;
@@ -303,6 +331,8 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
         }
         if (tid < R) x[o0 + tid] = add_rn(xo, a);
     }
+    ps.now(4);
+    ps.store();
 }
 
 // Lanes per row: the smallest of 8 / 16 / 32 with at most 3 items per lane and
@@ -318,7 +348,7 @@ int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, fl
     const int R = kDnRpg * (256 / L) / k;
     const int64_t rb = row_bytes_of(T, fe);
     VH_LAUNCH((down_combine_kernel<T, L, IPL>), dim3(d / R), dim3(256), uint32_t(size_t(k) * R * 4), s, plan, h, d,
-              fe, k, R, rb, x);
+              fe, k, R, rb, x, vh_stamps_for(2));
     return vh_check(hipGetLastError());
 }
 

@@ -62,7 +62,12 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     LayerXchg *__restrict__ xg, int E, int k, int fe, int d, int renorm, int64_t rb_gu, int64_t rb_dn,
     const float *__restrict__ bias, float *x, int32_t *__restrict__ idx_out, float *__restrict__ w_out,
     uint32_t *__restrict__ flags_out, uint32_t *__restrict__ status, unsigned spin_limit, const float *__restrict__ nw,
-    float eps, float *__restrict__ hb_out) {
+    float eps, float *__restrict__ hb_out, uint64_t *__restrict__ stamps) {
+    // stamps: 0 start, 1 router part computed, 2 every part received, 3 top-k
+    // chosen, 4 first gate/up row computed, 5 activations published, 6 the
+    // down expert's activations received, 7 end
+    PhaseStamps ps(stamps);
+    ps.now(0);
     using FG = Reg<TG>;
     using FD = Reg<TD>;
     constexpr int NSG = FG::NS, NSD = FD::NS, TPL = 3 * Q, SUB = 64 / L;
@@ -168,6 +173,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
             put_part(xg->parts + 2 * b, p.c, p.beta, epoch);
         }
     }
+    ps.now(1);
 
     // ---- 2. wave 0 polls the E parts until all carry this launch's number
     bool timed_out = false;
@@ -200,6 +206,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
         }
     }
     __syncthreads();
+    ps.now(2);
     RoutePart p[Q];
 #pragma unroll
     for (int q = 0; q < Q; q++) {
@@ -243,6 +250,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     }
 
     // ---- 4. every weight load of the workgroup: gate/up rows, then down rows
+    ps.after(3, e_j);
     const uint8_t *Gp = table_entry<TPL>(tab, 3 * e_j);
     const uint8_t *Up = table_entry<TPL>(tab, 3 * e_j + 1);
     const uint8_t *Dp = table_entry<TPL>(tab, 3 * e_dn + 2);
@@ -286,6 +294,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
         }
         g = group_sum<64>(g);
         u = group_sum<64>(u);
+        if (r == 0) ps.after(4, g);
         if (lane == 63 && o0 + r < fe) {  // an unregistered expert contributes nothing (src/gguf_run.c:201)
             const float hval = gu_ok ? swiglu(g, u) : 0.0f;
             st_agent64(xg->h + size_t(j) * kMaxLayerFe + o0 + r, (uint64_t(epoch) << 32) | __float_as_uint(hval));
@@ -297,6 +306,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     // nothing in memory and need not wait for the down rows in flight
     lds_barrier();
     if (tid == 0) st_agent64(&xg->done[j][b % (kLB / kWaves)], epoch);
+    ps.now(5);
 
     // ---- 6. wave wv polls the producers of the expert of round wv, then reads
     //         its activations (and reads them again until every tag is fresh)
@@ -330,6 +340,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    ps.now(6);
 
     // ---- 7. down rows of the expert of round wv from registers, then the combine
     if (lane == 0) pres[wv] = Dp != nullptr;
@@ -362,6 +373,8 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     }
     if (timed_out) atomicOr(status, VIREO_DECODE_TIMEOUT);
     if (tid == 0) xg->gen[b] = epoch;
+    ps.now(7);
+    ps.store();
 }
 
 template <int TG, int TD, int Q, int RPW, int L, int IPL, int UPG>
@@ -372,11 +385,11 @@ int launch_layer(const LayerArgs &a, hipStream_t s) {
     if (a.norm)
         VH_LAUNCH((moe_layer_kernel<TG, TD, Q, RPW, L, IPL, UPG, true>), dim3(kLB), dim3(64 * kWaves), 0, s, a.R,
                   a.xin, a.table, a.xg, a.E, a.k, a.fe, a.d, a.renorm, rb_gu, rb_dn, a.bias, a.x, a.idx, a.w, a.flags,
-                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out);
+                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out, vh_stamps_for(0));
     else
         VH_LAUNCH((moe_layer_kernel<TG, TD, Q, RPW, L, IPL, UPG, false>), dim3(kLB), dim3(64 * kWaves), 0, s, a.R,
                   a.xin, a.table, a.xg, a.E, a.k, a.fe, a.d, a.renorm, rb_gu, rb_dn, a.bias, a.x, a.idx, a.w, a.flags,
-                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out);
+                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out, vh_stamps_for(0));
     return vh_check(hipGetLastError());
 }
 

@@ -23,15 +23,19 @@ template <int C>
 __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict__ R, const float *__restrict__ hb,
                                                          const float *__restrict__ bias, int d, int E,
                                                          RoutePart *__restrict__ parts, uint32_t *__restrict__ zero,
-                                                         int nzero) {
+                                                         int nzero, uint64_t *__restrict__ stamps) {
+    PhaseStamps ps(stamps);
+    ps.now(0);
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
     if (gid < nzero) zero[gid] = 0u;
     RoutePart p = route_row_part<C>(R + size_t(e) * d, hb + size_t(t) * d, d, lane);
+    ps.after(1, p.c);
     if (lane == 0) {
         if (bias) p.c += double(bias[e]);
         parts[size_t(t) * E + e] = p;
     }
+    ps.store();
 }
 
 // route_parts_kernel on the RMSNorm of x (src/gguf_run.c:161-165) instead of a
@@ -44,7 +48,10 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
                                                               const float *__restrict__ nw, float eps,
                                                               float *__restrict__ hb_out, const float *__restrict__ bias,
                                                               int d, int E, RoutePart *__restrict__ parts,
-                                                              uint32_t *__restrict__ zero, int nzero) {
+                                                              uint32_t *__restrict__ zero, int nzero,
+                                                              uint64_t *__restrict__ stamps) {
+    PhaseStamps ps(stamps);
+    ps.now(0);
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
     if (gid < nzero) zero[gid] = 0u;
@@ -73,7 +80,9 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
     double abs_products;
     RoutePart p = route_row_part_regs<C>(R + size_t(e) * d, xv, lane, &abs_products);
     p = route_part_on_own_norm(p, abs_products, d, bias, e);  // certified against the reference's xb
+    ps.after(1, p.c);
     if (lane == 0) parts[size_t(t) * E + e] = p;
+    ps.store();
 }
 
 constexpr int kExTok = 64, kExCpl = 2, kExExp = 4 * kExCpl, kExChunk = 64;
@@ -234,7 +243,7 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
         (reinterpret_cast<uintptr_t>(R) & 15u) || nzero > E * T * 64)
         return -EINVAL;
     VH_LAUNCH(route_parts_norm_kernel<32>, dim3(E, T), dim3(64), 0, s, R, x, nw, eps, hb_out, bias, d, E, parts, zero,
-              nzero);
+              nzero, vh_stamps_for(0));
     return vh_check(hipGetLastError());
 }
 
@@ -253,8 +262,9 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
         const bool fast = d == 2048 && (reinterpret_cast<uintptr_t>(R) & 15u) == 0 &&
                           (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
         dim3 g(E, T);
-        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero);
-        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero);
+        uint64_t *st = vh_stamps_for(0);
+        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
+        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
     }
     return vh_check(hipGetLastError());
 }

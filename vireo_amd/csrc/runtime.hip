@@ -41,6 +41,7 @@ int cur_dev() {
 }  // namespace
 
 VhLaunchTiming g_vh_timing = {nullptr, nullptr};
+uint64_t *g_vh_stamps = nullptr;
 
 int vh_check(hipError_t e) {
     if (e == hipSuccess) return 0;

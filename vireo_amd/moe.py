@@ -15,6 +15,9 @@ import torch
 from . import _lib
 from . import workloads as W
 
+# words of stamps per call of moe_decode_phases: [3 kernels][256 workgroups][8 phases]
+PHASE_WORDS = 3 * 256 * 8
+
 
 def _stream_handle(stream=None):
     s = stream if stream is not None else torch.cuda.current_stream()
@@ -168,6 +171,28 @@ class DeviceMoE:
                                                    _ptr(states), states.stride(0), _ptr(idx), _ptr(w), us,
                                                    _stream_handle(stream)), "moe_decode_stage_timed")
         return np.array(us[:], dtype=np.float64)
+
+    def decode_phases(self, layers, x, hb, stream=None, stamps=None):
+        """Enqueue one moe_ffn_forward call per entry of `layers` (token row i
+        of x / hb) with the decode kernels recording per-workgroup phase stamps
+        (moe_decode_phases) into `stamps`, a zeroed int64 tensor of
+        [n x PHASE_WORDS] (made here when None); returns it. The caller reads
+        it after synchronising (or after replaying a graph that captured it)."""
+        n = len(layers)
+        d = self.shape.d
+        for name, t in (("x", x), ("hb", hb)):
+            if t is None or t.dim() != 2 or t.shape[0] < n or t.shape[1] != d or not t.is_contiguous():
+                raise ValueError(f"decode_phases: {name} must be a contiguous [>= {n} x {d}] tensor")
+        if any(not 0 <= l < self.n_layers for l in layers):
+            raise ValueError("decode_phases: layer out of range")
+        if stamps is None:
+            stamps = torch.zeros((n, PHASE_WORDS), dtype=torch.int64, device=x.device)
+        if stamps.dim() != 2 or stamps.shape[0] < n or stamps.shape[1] != PHASE_WORDS or not stamps.is_contiguous():
+            raise ValueError(f"decode_phases: stamps must be a contiguous [>= {n} x {PHASE_WORDS}] int64 tensor")
+        lay = (C.c_int * n)(*layers)
+        _lib.check(self.lib.moe_decode_phases(C.byref(self.model), n, lay, _ptr(x), _ptr(hb), _ptr(stamps),
+                                              _stream_handle(stream)), "moe_decode_phases")
+        return stamps
 
     def decode_states(self, n):
         """n decode states, one per row of a [n x stride] uint8 tensor."""
