@@ -27,6 +27,14 @@ OpenMP threads and at every physical core available (OMP_PROC_BIND=close,
 median of 10 runs, CPU model stated), or the oracle's restatement where that
 library is absent.
 
+The default run then times every other configuration of the benchmark in
+the same process - OLMoE Q8_0 at batch 1, OLMoE Q4_K_M at batch 1, 4 and 16,
+Qwen3 Q4_K_M at batch 32, the 2048-token Zipf-biased Q8_0 prefill and the
+48-layer stack with its LM head - and lists them under `configs`, each with
+its time per layer, roofline and CPU baseline (a shorter CPU sample each);
+`value` stays the headline's. --only times --workload alone; --phases prints
+only the phase breakdown of one-token calls (moe_decode_phases).
+
 Other workloads (--workload) print the same JSON schema: OLMoE shapes,
 batched decode and 2048-token prefill.
 """
@@ -89,6 +97,8 @@ def parse():
     ap.add_argument("--traffic", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="no GPU run: read four rocprofv3 --pmc output directories (FETCH_SIZE and WRITE_SIZE of "
                          "this workload, then of --workload copy-512MiB) and write profiles/traffic_<workload>.json")
+    ap.add_argument("--only", action="store_true",
+                    help="time only --workload (the default run also times every other configuration)")
     ap.add_argument("--phases", action="store_true",
                     help="only the per-phase breakdown of one-token calls (moe_decode_phases), no timed replay")
     ap.add_argument("--plan", type=int, default=0,
@@ -275,6 +285,10 @@ def cpu_baseline_stack(shape, L, vocab, seed, seconds):
 
 
 def bench_stack(args):
+    print(json.dumps(stack_result(args, args.workload, args.cpu_seconds)), flush=True)
+
+
+def stack_result(args, workload, cpu_seconds, steps=None):
     """Greedy decode through moe_stack_step: embedding row (the tied LM head),
     RMSNorm + MoE layer x L, RMSNorm, Q8_0 LM head, argmax; K steps captured
     in one HIP graph, each step reading the token the previous one wrote."""
@@ -286,12 +300,12 @@ def bench_stack(args):
     lib = _lib.load()
     _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
     _lib.check(lib.vireo_hip_set_path(args.plan), "vireo_hip_set_path")
-    shape_name, L, vocab = STACKS[args.workload]
+    shape_name, L, vocab = STACKS[workload]
     L = args.layers or L
     shape = W.SHAPES[shape_name]
-    K = args.steps or 128
+    K = steps or args.steps or 128
     Wm = args.warmup if args.warmup is not None else 2
-    print(f"[bench] {args.workload}: building {L} layers of {shape.name} and a [{vocab} x {shape.d}] Q8_0 LM head",
+    print(f"[bench] {workload}: building {L} layers of {shape.name} and a [{vocab} x {shape.d}] Q8_0 LM head",
           file=sys.stderr, flush=True)
     st = S.DeviceStack(shape, L, vocab=vocab, seed=args.seed)
     token = torch.full((1,), 17, dtype=torch.int32, device="cuda")
@@ -332,11 +346,14 @@ def bench_stack(args):
         "roofline": {"kernel": "moe_stack_step (all kernels of a step)", "bound": "hbm", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
     }
+    st.close()
+    del st, g
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline_stack(shape, L, vocab, args.seed, args.cpu_seconds)
-    st.close()
-    print(json.dumps(result), flush=True)
+        result["cpu_baseline"] = cpu_baseline_stack(shape, L, vocab, args.seed, cpu_seconds)
+    return result
 
 
 def bench_paged_stack(args):
@@ -800,7 +817,41 @@ def main():
         return bench_attn(args)
     if args.workload in MODELS:
         return bench_model(args)
+    if args.phases:
+        return layer_result(args, args.workload, args.cpu_seconds)
+    result = layer_result(args, args.workload, args.cpu_seconds)
+    if args.workload == DEFAULT and not args.only:
+        # every other configuration of the layer benchmark, timed in this run
+        # with a shorter CPU sample each (the headline `value` stays the
+        # default workload's)
+        sub = args.cpu_seconds / 2
+        result["configs"] = [compact(layer_result(args, w, sub)) for w in ALL_CONFIGS]
+        result["configs"].append(compact(stack_result(args, STACK_CONFIG, sub, steps=128)))
+    print(json.dumps(result), flush=True)
 
+
+# the other benchmark configurations the default run times after the headline
+ALL_CONFIGS = ["olmoe-q8_0-decode-b1", "olmoe-q4km-decode-b1", "olmoe-q4km-decode-b4", "olmoe-q4km-decode-b16",
+               "qwen3-q4km-decode-b32", "qwen3-q8_0-prefill-2048"]
+STACK_CONFIG = "qwen3-q4km-stack48"
+
+
+def compact(r):
+    """One configuration's entry of the default run's `configs` list."""
+    out = {"workload": r["config"]["workload"], "tok_s": r["value"], "ms_per_step": r["ms_per_step"],
+           "steps": r["steps"], "us_per_layer": r.get("us_per_layer"), "config": r["config"],
+           "roofline": r.get("roofline"), "cpu_baseline": r.get("cpu_baseline")}
+    for key in ("layer_alg_bytes", "distinct_experts", "layer_GBps", "token_alg_bytes", "step_GBps"):
+        if key in r:
+            out[key] = r[key]
+    return out
+
+
+def layer_result(args, workload, cpu_seconds):
+    """One MoE-layer workload (WORKLOADS): its timed HIP-graph replay, the
+    roofline, for one-token calls the per-kernel prices and the phase
+    breakdown, and the CPU baseline; returns the JSON object (prints only the
+    --phases form)."""
     import torch
     from vireo_amd import _lib
     from vireo_amd import moe as M
@@ -810,13 +861,14 @@ def main():
     _lib.check(lib.vireo_hip_init(0), "vireo_hip_init")
     _lib.check(lib.vireo_hip_set_path(args.plan), "vireo_hip_set_path")
     dev = torch.device("cuda:0")
-    shape_name, B, L, biased = WORKLOADS[args.workload]
-    L = args.layers or L
+    shape_name, B, L, biased = WORKLOADS[workload]
+    headline = workload == args.workload
+    L = (args.layers if headline else None) or L
     shape = W.SHAPES[shape_name]
-    K = args.steps or (48 * L if B < 64 else 8 * L)
+    K = (args.steps if headline else None) or (48 * L if B < 64 else 8 * L)
     Wm = args.warmup if args.warmup is not None else L
     bias = W.zipf_bias(shape.E, 1.1, seed=args.seed) if biased else None
-    print(f"[bench] {args.workload}: building {L} layers of {shape.name} on the GPU", file=sys.stderr, flush=True)
+    print(f"[bench] {workload}: building {L} layers of {shape.name} on the GPU", file=sys.stderr, flush=True)
     m = M.DeviceMoE(shape, L, seed=args.seed, logit_bias=bias)
 
     # a distinct token per step for decode, and at least the 8 x layers tokens
@@ -837,10 +889,10 @@ def main():
     if args.phases:
         if B != 1:
             raise SystemExit("--phases: one-token workloads only")
-        print(json.dumps({"workload": args.workload, "plan": args.plan,
+        print(json.dumps({"workload": workload, "plan": args.plan,
                           "phases": decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)}), flush=True)
         m.close()
-        return
+        return None
     for i in range(Wm):
         step(i)
     torch.cuda.synchronize()
@@ -881,7 +933,7 @@ def main():
         "layer_GBps": round(layer_gbs, 1), "layer_frac_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
     }
 
-    traffic, _ = layer_traffic(args.workload) if args.plan == 0 else (None, None)
+    traffic, _ = layer_traffic(workload) if args.plan == 0 else (None, None)
     if B >= 64:  # prefill: the expert GEMMs run on the matrix cores
         tflops = expert_flops(shape, B) / (ms_per_step / 1e3) / 1e12
         result["roofline"] = {"kernel": "moe_ffn_forward (every kernel of the layer call)", "bound": "mfma",
@@ -897,12 +949,16 @@ def main():
                               "alg_bytes_per_launch": int(lb)}
     if B == 1 and lib.moe_decode_state_bytes(M.C.byref(m.model)) > 0:
         result["roofline"]["kernels"] = decode_stage_roofline(m, shape, L, x_all, hb_all, dev)
-        result["phases"] = decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)
+        if headline:
+            result["phases"] = decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)
+    m.close()
+    del m, g, x_all, hb_all
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(shape, B, args.seed, args.cpu_seconds)
-    m.close()
-    print(json.dumps(result), flush=True)
+        result["cpu_baseline"] = cpu_baseline(shape, B, args.seed, cpu_seconds)
+    return result
 
 
 # Phases of the one-token decode kernels as moe_decode_phases records them
