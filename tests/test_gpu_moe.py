@@ -75,6 +75,31 @@ WIDE_TYPES = {"q6k-q6k-q8": (W.Q6_K, W.Q6_K, W.Q8_0), "q8-q8-q4k": (W.Q8_0, W.Q8
               "q4k-q4k-q6k": (W.Q4_K, W.Q4_K, W.Q6_K)}
 
 
+# expert types beyond the MoE models' own, which the reference's moe_ffn hands
+# to gguf_matmul like any other (src/gguf_run.c:202-208; Q5_0 dequant-then-dot,
+# F16 and F32 direct, src/gguf_compute.c:68-82, 183-213): the grouped fp32 kernels
+OTHER_TYPES = {"q5_0-q5_0-q5_0": (W.Q5_0, W.Q5_0, W.Q5_0), "f16-f16-f16": (W.F16, W.F16, W.F16),
+               "f32-f32-f32": (W.F32, W.F32, W.F32), "q5_0-q5_0-f16": (W.Q5_0, W.Q5_0, W.F16),
+               "f16-f16-q6k": (W.F16, W.F16, W.Q6_K), "q4k-q4k-f32": (W.Q4_K, W.Q4_K, W.F32)}
+
+
+@pytest.mark.parametrize("types", list(OTHER_TYPES))
+@pytest.mark.parametrize("T", [1, 24, 80])
+def test_other_expert_types(cuda, oracle, types, T):
+    """Q5_0, F16 and F32 experts (alone and mixed with the K-quants) at one
+    token, a decode batch and a call of more than 64 tokens, against the
+    oracle; every call takes the grouped fp32 kernels."""
+    shape = W.MoEShape("other-" + types, 2048, 16, 4, 512, True, *OTHER_TYPES[types])
+    m = M.DeviceMoE(shape, 1, seed=57)
+    x, hb = W.host_hidden(shape.d, T, 57)
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"{shape.name} T={T}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    np.testing.assert_allclose(w.cpu().numpy(), wo, rtol=1e-5)
+    m.close()
+
+
 @pytest.mark.parametrize("types", list(WIDE_TYPES))
 @pytest.mark.parametrize("T", [3, 24])
 def test_decode_batch_every_type(cuda, oracle, types, T):

@@ -66,7 +66,9 @@ static int get_key(const gguf_ctx *g, const char *arch, const char *suffix, uint
     return vireo_gguf_get_u64(g, key, v);
 }
 
-static int expert_type_ok(uint32_t t) { return t == GGML_Q8_0 || t == GGML_Q4_K || t == GGML_Q6_K; }
+static int expert_type_ok(uint32_t t) {
+    return t == GGML_Q8_0 || t == GGML_Q4_K || t == GGML_Q6_K || t == GGML_Q5_0 || t == GGML_F16 || t == GGML_F32;
+}
 
 void vireo_gguf_moe_free(vireo_gguf_moe *m) {
     if (!m) return;

@@ -46,8 +46,12 @@ constexpr int kExactRouteTokens = 64;
 constexpr int kMdecMinTokens = 8;
 
 bool type_ok(uint32_t t, int n) {
-    switch (t) {  // the expert formats of the MoE models: Q8_0, Q4_K (gate/up), Q6_K (down)
-    case VT_Q8_0: return n % 32 == 0;
+    // the expert formats of the MoE models (Q8_0, Q4_K gate/up, Q6_K down), and
+    // the other types the reference's gguf_matmul computes (src/gguf_run.c:
+    // 202-208, src/gguf_compute.c:68-82, 183-213), which the grouped fp32
+    // kernels take in items of 32 columns
+    switch (t) {
+    case VT_Q8_0: case VT_Q5_0: case VT_F16: case VT_F32: return n % 32 == 0;
     case VT_Q4_K: case VT_Q6_K: return n % 256 == 0;
     default: return false;
     }

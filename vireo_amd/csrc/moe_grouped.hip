@@ -97,14 +97,7 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(const int32_t *__restric
     }
 }
 
-int64_t rbytes(uint32_t t, int n) {
-    switch (t) {
-    case VT_Q8_0: return int64_t(n / 32) * 34;
-    case VT_Q4_K: return int64_t(n / 256) * 144;
-    case VT_Q6_K: return int64_t(n / 256) * 210;
-    default: return int64_t(n / 32) * 22;  // Q5_0
-    }
-}
+int64_t rbytes(uint32_t t, int n) { return vh_row_bytes(t, n); }
 
 // Large calls: one workgroup per expert, twice. dispatch_count_kernel counts
 // the pairs of expert blockIdx.x; dispatch_place_kernel sums the counts of the
@@ -222,6 +215,35 @@ VH_DEV void deq_raw(const typename Reg<T>::Words &r, float (&w)[32]) {
             w[8 + i] = ds[1] * float(int((qb & 15u) | (((qh >> 2) & 3u) << 4)) - 32);
             w[16 + i] = ds[2] * float(int((qa >> 4) | (((qh >> 4) & 3u) << 4)) - 32);
             w[24 + i] = ds[3] * float(int((qb >> 4) | (((qh >> 6) & 3u) << 4)) - 32);
+        }
+    } else if constexpr (T == VT_Q5_0) {  // src/gguf_compute.c:68-82: ((q | h << 4) - 16) * d
+        const float d = h2f(r.b[0] & 0xffffu);
+        const uint32_t qh = (r.b[0] >> 16) | (r.b[1] << 16);
+        const uint32_t qs[4] = {(r.b[1] >> 16) | (r.b[2] << 16), (r.b[2] >> 16) | (r.b[3] << 16),
+                                (r.b[3] >> 16) | (r.b[4] << 16), (r.b[4] >> 16) | (r.b[5] << 16)};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t q = (qs[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            w[i] = float(int((q & 15u) | (((qh >> i) & 1u) << 4)) - 16) * d;
+            w[16 + i] = float(int((q >> 4) | (((qh >> (i + 16)) & 1u) << 4)) - 16) * d;
+        }
+    } else if constexpr (T == VT_F16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                w[8 * i + 2 * j] = h2f(q[j] & 0xffffu);
+                w[8 * i + 2 * j + 1] = h2f(q[j] >> 16);
+            }
+        }
+    } else if constexpr (T == VT_F32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            w[4 * i] = __uint_as_float(r.q[i].x);
+            w[4 * i + 1] = __uint_as_float(r.q[i].y);
+            w[4 * i + 2] = __uint_as_float(r.q[i].z);
+            w[4 * i + 3] = __uint_as_float(r.q[i].w);
         }
     } else {  // Q8_0
         const float d = h2f((r.w[0] >> (8 * r.s)) & 0xffffu);
@@ -466,7 +488,9 @@ int proj_launch(const int32_t *counts, const int32_t *offs, const int32_t *perm,
                 hipStream_t s) {
     const int items = K / 32, L = proj_lanes(items, GATEUP);
     if (!L || K % 32) return -EINVAL;
-    constexpr int RPL = GATEUP ? 8 : 4;
+    // F16 / F32 items are 64 / 128 raw bytes: one row per lane group (no next
+    // row's words in flight), more workgroups instead
+    constexpr int RPL = (T == VT_F16 || T == VT_F32) ? 1 : GATEUP ? 8 : 4;
     const int ipl = (items + L - 1) / L, RB = 8 * (64 / L) * RPL;
     const dim3 g((rows + RB - 1) / RB, max_slots);
     constexpr int NT = group_tokens<GATEUP>();
@@ -519,6 +543,9 @@ int vh_grouped_gateup(uint32_t type, const int32_t *counts, const int32_t *offs,
     case VT_Q8_0: return proj_launch<VT_Q8_0, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
     case VT_Q4_K: return proj_launch<VT_Q4_K, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
     case VT_Q6_K: return proj_launch<VT_Q6_K, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
+    case VT_Q5_0: return proj_launch<VT_Q5_0, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
+    case VT_F16: return proj_launch<VT_F16, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
+    case VT_F32: return proj_launch<VT_F32, true>(counts, offs, perm, active, table, hb, d, fe, k, E, max_slots, h, s);
     default: return -EINVAL;
     }
 }
@@ -530,6 +557,9 @@ int vh_grouped_down(uint32_t type, const int32_t *counts, const int32_t *offs, c
     case VT_Q8_0: return proj_launch<VT_Q8_0, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
     case VT_Q4_K: return proj_launch<VT_Q4_K, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
     case VT_Q6_K: return proj_launch<VT_Q6_K, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
+    case VT_Q5_0: return proj_launch<VT_Q5_0, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
+    case VT_F16: return proj_launch<VT_F16, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
+    case VT_F32: return proj_launch<VT_F32, false>(counts, offs, perm, active, table, h, fe, d, 1, E, max_slots, ybuf, s);
     default: return -EINVAL;
     }
 }

@@ -567,3 +567,68 @@ struct Reg<VT_Q8_0> {
         return acc * d;
     }
 };
+
+// Expert rows of the other types the reference computes with gguf_matmul
+// (src/gguf_compute.c:68-82 Q5_0 by dequant-then-dot, :202-213 F16 / F32), for
+// the grouped projections: a 32-weight item's words (fetch), resolved into
+// the block's own bytes (resolve); the grouped kernels dequantize them with
+// deq_raw. Items are 32 consecutive columns.
+//   Q5_0 {f16 d; u8 qh[4]; u8 qs[16]} = 22 bytes: the block at an even offset
+//        b is read as the aligned 24-byte window from b - (b & 3) - five dwords
+//        and a last word of two 16-bit loads, as Reg<VT_Q8_0> does, so nothing
+//        past the block is read;
+//   F16  64 bytes, F32 128 bytes per item (rows of n % 32 == 0 elements).
+template <>
+struct Reg<VT_Q5_0> {
+    struct Raw { uint32_t w[5], lo, hi, s; };
+    struct Words { uint32_t b[6]; };  // block bytes [0, 24): bytes 22 and 23 unused
+    static __host__ __device__ int items(int n) { return n / 32; }
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
+        const int64_t b = row + 22 * int64_t(it);
+        Raw r;
+        r.s = uint32_t(b) & 3u;
+        P a = base + (b - int64_t(r.s));
+#pragma unroll
+        for (int i = 0; i < 5; i++) r.w[i] = ld_u32(a + 4 * i);
+        r.lo = ld_u16(a + 20);
+        r.hi = ld_u16(a + 20 + r.s);
+        return r;
+    }
+    static VH_DEV Words resolve(const Raw &r, int) {
+        const uint32_t win[6] = {r.w[0], r.w[1], r.w[2], r.w[3], r.w[4], r.lo | (r.hi << 16)};
+        Words v;
+#pragma unroll
+        for (int i = 0; i < 5; i++) v.b[i] = align2(win[i + 1], win[i], r.s);
+        v.b[5] = r.s ? (win[5] >> 16) : win[5];
+        return v;
+    }
+};
+template <>
+struct Reg<VT_F16> {
+    struct Raw { uint4 q[4]; };
+    using Words = Raw;
+    static __host__ __device__ int items(int n) { return n / 32; }
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.q[i] = ld_u128(base + row + 64 * int64_t(it) + 16 * i);
+        return r;
+    }
+    static VH_DEV const Words &resolve(const Raw &r, int) { return r; }
+};
+template <>
+struct Reg<VT_F32> {
+    struct Raw { uint4 q[8]; };
+    using Words = Raw;
+    static __host__ __device__ int items(int n) { return n / 32; }
+    template <class P>
+    static VH_DEV Raw fetch(P base, int64_t row, int it) {
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.q[i] = ld_u128(base + row + 128 * int64_t(it) + 16 * i);
+        return r;
+    }
+    static VH_DEV const Words &resolve(const Raw &r, int) { return r; }
+};
