@@ -102,7 +102,8 @@ typedef struct {
 typedef struct {
     int dim;          /* d */
     int n_experts;    /* E */
-    int n_used;       /* k (top-k), 1 <= k <= min(E, 64) */
+    int n_used;       /* k (top-k), 1 <= k <= min(E, 64); -EINVAL beyond, where the
+                         reference truncates to 64 (src/gguf_run.c:190) */
     int ffn_exp;      /* expert intermediate size fe */
     int topk_renorm;  /* renormalise the k weights (src/gguf_run.c:292-293) */
     int n_layers;
@@ -189,7 +190,7 @@ int moe_ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *
  * Limits: the layer must already be resident and pinned
  * (expert_store_pin_layer, or one earlier moe_ffn_forward on it; else
  * -EINVAL); calls whose intermediates exceed the region return -E2BIG (about
- * 300 tokens for the Qwen3-30B-A3B layer); the fused plan (vireo_hip_set_path
+ * 400 tokens for the Qwen3-30B-A3B layer); the fused plan (vireo_hip_set_path
  * 3) is not used; calls are not counted in expert_store_stats. Every call on a
  * device shares the region, which keeps the last call's contents: calls that
  * may overlap on one device (other streams, other threads) race. */
@@ -220,11 +221,15 @@ int vireo_hip_set_path(int path);
  * may allocate (not moe_ffn_forward_noalloc, not under graph capture) copies
  * the layer's experts once into tiles of 16 rows x one super-block, the same
  * bytes reordered so that every load instruction reads 1 KB of consecutive
- * memory; later calls read the copy. The copy is device memory outside the
- * store's capacity (as much again as the layer's expert bytes), made from the
- * pinned views and freed with the pin (expert_store_unpin_layer) or the store;
- * a caller that rewrites a pinned layer's expert bytes in place must unpin
- * and pin it again. Calls of 64 or more tokens on a pinned Q8_0 layer make
+ * memory; later calls read the copy. The copy (as much again as the layer's
+ * expert bytes) counts against the store's capacity like resident experts:
+ * it is made only while the resident experts and the copies fit the capacity
+ * with it (cut from the pool's own device block when that has room), else
+ * the calls read the GGUF rows; an unbounded store (capacity 0) always makes
+ * it. expert_store_packed_bytes reports the copies' bytes. A copy is made
+ * from the pinned views and freed with the pin (expert_store_unpin_layer) or
+ * the store; a caller that rewrites a pinned layer's expert bytes in place
+ * must unpin and pin it again. Calls of 64 or more tokens on a pinned Q8_0 layer make
  * and read, the same way, a copy in matrix-operand fragments (each lane's
  * bytes of a 32-row, 64-column step together) for the prefill GEMMs. Results
  * are the same bit for bit either way. 0 turns both off for later calls
@@ -461,9 +466,15 @@ int expert_store_unpin_layer(ExpertStore *s, int layer);
 /* What the HBM pool did, in ExpertStats form: every lookup the library made
  * (whole layers pinned, routed experts paged per call) and the caller's own
  * lookups, the bytes copied into HBM (or aliased, for a device-backed store),
- * and the bytes and experts resident in HBM now. expert_store_stats reports
- * the reference's accounting of the same work instead. */
+ * and the bytes and experts resident in HBM now (resident_bytes includes the
+ * kernels' packed copies of pinned layers, expert_store_packed_bytes).
+ * expert_store_stats reports the reference's accounting of the same work
+ * instead. */
 void expert_store_hbm_stats(const ExpertStore *s, ExpertStats *out);
+/* Device bytes of the packed copies of pinned layers (vireo_hip_set_packed)
+ * the store holds now, 0 for NULL or a foreign store. No counterpart in the
+ * reference. */
+uint64_t expert_store_packed_bytes(const ExpertStore *s);
 /* Prefetch by paged calls (no counterpart in the reference, whose
  * ROADMAP.md:46-47 lists it as open): on by default for a store that reads a
  * file; 0 turns it off. -EINVAL for a store this library did not make. */

@@ -10,6 +10,7 @@ import torch
 
 from vireo_amd import _lib
 from vireo_amd import moe as M
+from vireo_amd import stack as S
 from vireo_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -93,3 +94,32 @@ def test_fused_wait_timeout_is_reported(cuda, lib, plan):
         lib.vireo_hip_set_spin_limit(1 << 18)
         lib.vireo_hip_set_path(0)
         m.close()
+
+
+@pytest.mark.parametrize("plan", [3, 5])
+def test_stack_step_wait_timeout_is_reported(cuda, lib, plan):
+    """A synchronous moe_stack_step under a plan whose workgroups wait for
+    each other returns -ETIMEDOUT when the waits give up (poll limit 0), and
+    the status word is left clear; with the default limit the same step
+    succeeds and picks the plan-0 step's token."""
+    st = S.DeviceStack(W.SHAPES["qwen3-30b-a3b-q4_k_m"], 2, vocab=512, seed=79)
+    token = torch.tensor([7], dtype=torch.int32, device=cuda)
+    try:
+        st.step(token)  # plan 0
+        want = int(token.item())
+        _lib.check(lib.vireo_hip_set_path(plan), "set_path")
+        assert lib.vireo_hip_status(None) == 0
+        _lib.check(lib.vireo_hip_set_spin_limit(0), "set_spin_limit")
+        token.fill_(7)
+        torch.cuda.synchronize()
+        rc = lib.moe_stack_step(C.byref(st.st), M._ptr(token), M._ptr(st.x), M._ptr(st.xb), M._ptr(st.logits), None)
+        assert rc == -errno.ETIMEDOUT
+        assert lib.vireo_hip_status(None) == 0
+        _lib.check(lib.vireo_hip_set_spin_limit(1 << 18), "set_spin_limit")
+        token.fill_(7)
+        st.step(token)
+        assert int(token.item()) == want
+    finally:
+        lib.vireo_hip_set_spin_limit(1 << 18)
+        lib.vireo_hip_set_path(0)
+        st.close()

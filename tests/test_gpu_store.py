@@ -141,6 +141,61 @@ def test_moe_from_file_backed_store(cuda, lib):
     m.close()
 
 
+def test_packed_copy_counts_against_capacity(cuda, lib):
+    """The decode batch's tiled copy of a pinned layer is made only while the
+    resident experts and the copy fit the store's capacity: one byte short
+    and the calls read the GGUF rows (no copy), exactly enough and the copy
+    is made and reported in resident_bytes and expert_store_packed_bytes; an
+    unbounded store always makes it. The outputs are the same bits in every
+    case."""
+    shape = W.SHAPES["olmoe-q4_k_m"]
+    T = 8
+    m = M.DeviceMoE(shape, 1, seed=71)
+    x, hb = W.host_hidden(shape.d, T, 71)
+    hbt = torch.from_numpy(hb).to(cuda)
+    ref = torch.from_numpy(x).to(cuda)
+    try:
+        _lib.check(lib.vireo_hip_set_packed(0), "vireo_hip_set_packed")
+        m.forward(0, ref, hbt)
+    finally:
+        lib.vireo_hip_set_packed(1)
+    gb, ub, db = m.device_layer_bytes(0)
+    gs, us, ds = m.slices
+    layer = shape.E * (gs + us + ds)
+    # 16-row x 256-column Q4_K tiles of 2368 bytes for gate and up; Q6_K down rows
+    q6 = shape.fe // 256 * 210
+    pack = shape.E * (2 * (shape.fe // 16) * (shape.d // 256) * 2368 + shape.d * q6)
+    fd, path = tempfile.mkstemp()
+    os.unlink(path)
+    try:
+        os.pwrite(fd, gb.tobytes() + ub.tobytes() + db.tobytes(), 0)
+        for cap, made in ((layer + pack - 1, False), (layer + pack, True), (0, True)):
+            s = lib.expert_store_create(fd, cap, 1, shape.E)
+            for e in range(shape.E):
+                sl = _lib.ExpertSlices(e * gs, gb.size + e * us, gb.size + ub.size + e * ds, gs, us, ds)
+                lib.expert_store_register(s, 0, e, C.byref(sl))
+            m.model.es = s
+            for rep in range(2):
+                xt = torch.from_numpy(x).to(cuda)
+                m.forward(0, xt, hbt)
+                np.testing.assert_array_equal(xt.cpu().numpy().view(np.uint32), ref.cpu().numpy().view(np.uint32),
+                                              err_msg=f"capacity {cap} call {rep}")
+            packed = lib.expert_store_packed_bytes(s)
+            assert packed == (pack if made else 0), (cap, packed)
+            st = _lib.ExpertStats()
+            lib.expert_store_hbm_stats(s, C.byref(st))
+            assert st.resident_bytes == layer + packed
+            assert cap == 0 or st.resident_bytes <= cap
+            assert lib.expert_store_unpin_layer(s, 0) == 0
+            assert lib.expert_store_packed_bytes(s) == 0
+            torch.cuda.synchronize()
+            lib.expert_store_destroy(s)
+    finally:
+        os.close(fd)
+        m.model.es = m.es
+        m.close()
+
+
 @pytest.mark.parametrize("case", ["tiny_q4km", "tiny_q8", "olmoe_q8_0", "qwen3_q4_k_m"])
 def test_golden_store_stats(cuda, lib, case):
     """The reference's own ExpertStore statistics after its moe_ffn over the

@@ -2,7 +2,9 @@
 (its workspace is a fixed static device region). Its results equal
 moe_ffn_forward's bit for bit on the same inputs (the same kernels run), on
 consecutive calls whose second is smaller than the first, on every plan it
-takes (matrix-core groups, decode-batch groups, the one-token decode plan);
+takes (matrix-core GEMMs on GGUF rows and on packed Q8_0 fragments, the
+matrix-core decode batch on packed tiles, register-input groups, the
+one-token decode plan);
 it refuses calls whose intermediates exceed the region (-E2BIG) and layers
 that are not pinned yet (-EINVAL), and it allocates no device memory."""
 import ctypes as C
@@ -24,21 +26,23 @@ def _call(lib, fn, m, layer, x, hb, T, idx, w):
               C.c_void_p(idx.data_ptr()), C.c_void_p(w.data_ptr()), None)
 
 
-def test_noalloc_matches_moe_ffn_forward(cuda, lib):
-    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
-    m = M.DeviceMoE(shape, 2, seed=91)
-    sizes = [(0, 96), (1, 5), (0, 1), (1, 1)]  # each call smaller than (or as small as) the one before
+def _check_noalloc(cuda, lib, m, shape, sizes, seed, unpinned, too_big):
+    """Runs `sizes` ((layer, tokens), each call no larger than the one before)
+    through moe_ffn_forward, then through moe_ffn_forward_noalloc: the same
+    bits, no device memory allocated. `unpinned` (layer, tokens) is refused
+    while its layer is not pinned; `too_big` tokens exceed the region."""
     inputs = {}
     for layer, T in sizes:
-        x, hb = W.host_hidden(shape.d, T, 91 + T)
+        x, hb = W.host_hidden(shape.d, T, seed + T)
         inputs[(layer, T)] = (x, torch.from_numpy(hb).to(cuda))
     # refused before the layer is pinned: pinning allocates
-    x0, hb0 = inputs[(1, 5)]
+    x0, hb0 = inputs[unpinned]
+    T0 = unpinned[1]
     xg = torch.from_numpy(x0).to(cuda)
-    idx = torch.empty((5, shape.k), dtype=torch.int32, device=cuda)
-    w = torch.empty((5, shape.k), dtype=torch.float32, device=cuda)
-    assert _call(lib, lib.moe_ffn_forward_noalloc, m, 1, xg, hb0, 5, idx, w) == -errno.EINVAL
-    # the reference results (this also pins both layers)
+    idx = torch.empty((T0, shape.k), dtype=torch.int32, device=cuda)
+    w = torch.empty((T0, shape.k), dtype=torch.float32, device=cuda)
+    assert _call(lib, lib.moe_ffn_forward_noalloc, m, unpinned[0], xg, hb0, T0, idx, w) == -errno.EINVAL
+    # the reference results (this also pins the layers and makes their packed copies)
     want = {}
     for layer, T in sizes:
         x, hb = inputs[(layer, T)]
@@ -52,9 +56,9 @@ def test_noalloc_matches_moe_ffn_forward(cuda, lib):
         x, hb = inputs[(layer, T)]
         outs[(layer, T)] = (torch.from_numpy(x).to(cuda), torch.empty((T, shape.k), dtype=torch.int32, device=cuda),
                             torch.empty((T, shape.k), dtype=torch.float32, device=cuda))
-    big_x = torch.zeros((2048, shape.d), dtype=torch.float32, device=cuda)
-    big_i = torch.empty((2048, shape.k), dtype=torch.int32, device=cuda)
-    big_w = torch.empty((2048, shape.k), dtype=torch.float32, device=cuda)
+    big_x = torch.zeros((too_big, shape.d), dtype=torch.float32, device=cuda)
+    big_i = torch.empty((too_big, shape.k), dtype=torch.int32, device=cuda)
+    big_w = torch.empty((too_big, shape.k), dtype=torch.float32, device=cuda)
     torch.cuda.synchronize()
     free0 = torch.cuda.mem_get_info()[0]
     for layer, T in sizes:
@@ -62,7 +66,7 @@ def test_noalloc_matches_moe_ffn_forward(cuda, lib):
         xo, io, wo = outs[(layer, T)]
         _lib.check(_call(lib, lib.moe_ffn_forward_noalloc, m, layer, xo, hb, T, io, wo), "moe_ffn_forward_noalloc")
     # a call whose intermediates exceed the fixed region
-    assert _call(lib, lib.moe_ffn_forward_noalloc, m, 0, big_x, big_x, 2048, big_i, big_w) == -errno.E2BIG
+    assert _call(lib, lib.moe_ffn_forward_noalloc, m, 0, big_x, big_x, too_big, big_i, big_w) == -errno.E2BIG
     torch.cuda.synchronize()
     assert torch.cuda.mem_get_info()[0] == free0, "device memory was allocated"
     for key, (xo, io, wo) in outs.items():
@@ -70,4 +74,26 @@ def test_noalloc_matches_moe_ffn_forward(cuda, lib):
         np.testing.assert_array_equal(io.cpu().numpy(), iw, err_msg=str(key))
         np.testing.assert_array_equal(wo.cpu().numpy(), ww, err_msg=str(key))
         np.testing.assert_array_equal(xo.cpu().numpy(), xw, err_msg=str(key))
-    m.close()
+
+
+def test_noalloc_matches_moe_ffn_forward(cuda, lib):
+    """Q4_K_M experts: the matrix-core GEMMs (96 tokens), the matrix-core
+    decode batch on its packed 16-row tiles (40), the register-input groups
+    (5) and the one-token plan."""
+    shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
+    m = M.DeviceMoE(shape, 2, seed=91)
+    try:
+        _check_noalloc(cuda, lib, m, shape, [(0, 96), (1, 40), (1, 5), (0, 1), (1, 1)], 91, (1, 5), 2048)
+    finally:
+        m.close()
+
+
+def test_noalloc_q8_fragments(cuda, lib):
+    """Q8_0 experts of 64+ tokens: the matrix-core GEMMs reading the packed
+    operand fragments the first moe_ffn_forward made."""
+    shape = W.SHAPES["olmoe-q8_0"]
+    m = M.DeviceMoE(shape, 1, seed=93)
+    try:
+        _check_noalloc(cuda, lib, m, shape, [(0, 130), (0, 70)], 93, (0, 70), 2048)
+    finally:
+        m.close()

@@ -206,6 +206,7 @@ SIGNATURES = {
     "expert_store_release": (None, [c_vp, C.POINTER(ExpertView)]),
     "expert_store_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
     "expert_store_hbm_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
+    "expert_store_packed_bytes": (C.c_uint64, [c_vp]),
     "expert_store_set_prefetch": (C.c_int, [c_vp, C.c_int]),
     "expert_store_prefetch_stats": (None, [c_vp, C.POINTER(C.c_uint64)]),
     "vireo_hip_status": (C.c_int, [c_vp]),

@@ -36,6 +36,8 @@
 #include <hip/hip_runtime_api.h>
 #include "vireo_hip.h"
 
+void vh_store_packed_abort(ExpertStore *s, int layer, int kind);
+
 typedef struct {
     ExpertSlices loc;
     void *dev;            /* device block, NULL when not resident (or aliased) */
@@ -117,6 +119,8 @@ struct ExpertStore {
     size_t stage_bytes;
     void **tables;             /* per layer: device [n_experts x 3] pointer table */
     void **ptables, **pbufs;   /* per kind and pinned layer: a reordered copy of its experts and its table */
+    uint64_t *pbytes;          /* the copies' sizes; they count against the capacity */
+    uint64_t packed_bytes;     /* their sum */
     FreeBlock *freel;          /* device blocks of evicted experts, kept for reuse */
     int nfree, capfree;
     uint8_t *arena;            /* one allocation the pool's blocks are cut from (bounded pools) */
@@ -166,8 +170,9 @@ static ExpertStore *store_new(int n_layers, int n_experts, uint64_t capacity_byt
     s->tables = calloc((size_t)n_layers, sizeof(void *));
     s->ptables = calloc((size_t)n_layers * VH_PACK_KINDS, sizeof(void *));
     s->pbufs = calloc((size_t)n_layers * VH_PACK_KINDS, sizeof(void *));
-    if (!s->slots || !s->tables || !s->ptables || !s->pbufs) {
-        free(s->slots); free(s->tables); free(s->ptables); free(s->pbufs); free(s);
+    s->pbytes = calloc((size_t)n_layers * VH_PACK_KINDS, sizeof(uint64_t));
+    if (!s->slots || !s->tables || !s->ptables || !s->pbufs || !s->pbytes) {
+        free(s->slots); free(s->tables); free(s->ptables); free(s->pbufs); free(s->pbytes); free(s);
         return NULL;
     }
     s->capacity_bytes = capacity_bytes;
@@ -386,7 +391,7 @@ static void evict_one(ExpertStore *s, Slot *v) {
 /* src/expert_store.c:52-63 */
 static void make_room(ExpertStore *s, uint64_t need) {
     if (!s->capacity_bytes) return;
-    while (s->resident_bytes + need > s->capacity_bytes) {
+    while (s->resident_bytes + s->packed_bytes + need > s->capacity_bytes) {
         Slot *victim = NULL;
         for (int i = s->lru_head; i >= 0 && !victim; i = s->slots[i].lru_next)
             if (!s->slots[i].lease) victim = &s->slots[i];
@@ -720,9 +725,11 @@ void expert_store_stats(const ExpertStore *cs, ExpertStats *out) {
 void expert_store_hbm_stats(const ExpertStore *s, ExpertStats *out) {
     if (!store_ok(s) || !out) return;
     *out = s->hbm;
-    out->resident_bytes = s->resident_bytes;
+    out->resident_bytes = s->resident_bytes + s->packed_bytes;
     out->capacity_bytes = s->capacity_bytes;
 }
+
+uint64_t expert_store_packed_bytes(const ExpertStore *s) { return store_ok(s) ? s->packed_bytes : 0; }
 
 int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_table) {
     if (!store_ok(s) || !dev_table || layer < 0 || layer >= s->n_layers) return -EINVAL;
@@ -736,10 +743,10 @@ int expert_store_pin_layer(ExpertStore *s, int layer, const void *const **dev_ta
     }
     /* a layer larger than the store never fits: say so before evicting anything */
     if (s->capacity_bytes && all > s->capacity_bytes) return -ENOSPC;
-    if (s->capacity_bytes && s->resident_bytes + need > s->capacity_bytes) {
+    if (s->capacity_bytes && s->resident_bytes + s->packed_bytes + need > s->capacity_bytes) {
         /* evict what can go; the layer must then fit entirely */
         make_room(s, need);
-        if (s->resident_bytes + need > s->capacity_bytes) return -ENOSPC;
+        if (s->resident_bytes + s->packed_bytes + need > s->capacity_bytes) return -ENOSPC;
     }
     const void **host = calloc((size_t)E * 3, sizeof(void *));
     if (!host) return -ENOMEM;
@@ -780,10 +787,10 @@ int expert_store_unpin_layer(ExpertStore *s, int layer) {
     (void)hipFree(s->tables[layer]);
     s->tables[layer] = NULL;
     for (int kd = 0; kd < VH_PACK_KINDS; kd++) {
-        const size_t i = (size_t)kd * s->n_layers + layer;
-        if (s->ptables[i]) (void)hipFree(s->ptables[i]);
-        if (s->pbufs[i]) (void)hipFree(s->pbufs[i]);
-        s->ptables[i] = s->pbufs[i] = NULL;
+        if (s->ptables[(size_t)kd * s->n_layers + layer])
+            (void)hipFree(s->ptables[(size_t)kd * s->n_layers + layer]);
+        s->ptables[(size_t)kd * s->n_layers + layer] = NULL;
+        vh_store_packed_abort(s, layer, kd);
     }
     for (int e = 0; e < s->n_experts; e++) {
         Slot *sl = slot_at(s, layer, e);
@@ -802,7 +809,7 @@ void expert_store_destroy(ExpertStore *s) {
         for (int kd = 0; kd < VH_PACK_KINDS; kd++) {
             const size_t i = (size_t)kd * s->n_layers + l;
             if (s->ptables[i]) (void)hipFree(s->ptables[i]);
-            if (s->pbufs[i]) (void)hipFree(s->pbufs[i]);
+            if (s->pbufs[i]) block_free(s, s->pbufs[i]);
         }
     }
     for (int i = 0; i < s->n_slots; i++) {
@@ -828,6 +835,7 @@ void expert_store_destroy(ExpertStore *s) {
     free(s->tables);
     free(s->ptables);
     free(s->pbufs);
+    free(s->pbytes);
     free(s->slots);
     free(s);
 }
@@ -854,24 +862,77 @@ const void *const *vh_store_layer_table(const ExpertStore *s, int layer) {
 
 /* A pinned layer's experts reordered for a kernel (kind 0: the matrix-core
  * decode batch's 16-row tiles, 1: the prefill GEMMs' Q8_0 row octets): their
- * device table, or NULL (never allocates). vh_store_set_packed hands the
- * store a copy made for a pinned layer (buf: one device allocation, tab:
- * device [n_experts x 3] table into it); the store frees both when the layer
- * is unpinned or the store destroyed. -EINVAL (the caller keeps them) when
- * the layer is not pinned or already has one of that kind. */
+ * device table, or NULL (never allocates). A copy counts against the
+ * capacity like resident experts: vh_store_packed_begin gives a device
+ * block of `bytes` for one only while resident experts and copies fit the
+ * capacity with it (else NULL, and the caller reads the GGUF rows), cut
+ * from the pool's arena when it has room; vh_store_set_packed then hands
+ * the store the copy's device [n_experts x 3] table, or vh_store_packed_abort
+ * takes the block back. The store frees both when the layer is unpinned or
+ * the store destroyed. */
 const void *const *vh_store_packed_table(const ExpertStore *s, int layer, int kind) {
     if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS || !s->tables[layer])
         return NULL;
     return (const void *const *)s->ptables[(size_t)kind * s->n_layers + layer];
 }
-int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *buf, void *tab) {
+void *vh_store_packed_begin(ExpertStore *s, int layer, int kind, uint64_t bytes) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS || !s->tables[layer] ||
+        !bytes)
+        return NULL;
+    const size_t i = (size_t)kind * s->n_layers + layer;
+    if (s->ptables[i] || s->pbufs[i]) return NULL;
+    if (s->capacity_bytes && s->resident_bytes + s->packed_bytes + bytes > s->capacity_bytes) return NULL;
+    void *p = NULL;
+    for (int j = 0; j < s->nfree && !p; j++)
+        if (s->freel[j].size == bytes) {
+            /* a block of this size: the layer's own copy, dropped at an unpin
+             * that waited for the device */
+            p = s->freel[j].ptr;
+            if (s->freel[j].busy_set) (void)hipEventSynchronize(s->freel[j].busy);
+            if (s->freel[j].busy) (void)hipEventDestroy(s->freel[j].busy);
+            s->freel[j] = s->freel[--s->nfree];
+        }
+    if (!p && s->arena && s->arena_size - s->arena_used >= bytes) {
+        p = s->arena + s->arena_used;
+        s->arena_used += (bytes + 255u) & ~(uint64_t)255u;
+        if (s->arena_used > s->arena_size) s->arena_used = s->arena_size;
+    }
+    if (!p && hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return NULL;
+    }
+    s->pbufs[i] = p;
+    s->pbytes[i] = bytes;
+    s->packed_bytes += bytes;
+    return p;
+}
+
+int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *tab) {
     if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS || !s->tables[layer])
         return -EINVAL;
     const size_t i = (size_t)kind * s->n_layers + layer;
-    if (s->ptables[i]) return -EINVAL;
-    s->pbufs[i] = buf;
+    if (s->ptables[i] || !s->pbufs[i]) return -EINVAL;
     s->ptables[i] = tab;
     return 0;
+}
+
+/* The block of a copy goes back to the free list (the arena's memory stays
+ * with the arena; a re-pinned layer packs into it again). The caller has
+ * waited for the kernels that wrote or read it. */
+void vh_store_packed_abort(ExpertStore *s, int layer, int kind) {
+    if (!store_ok(s) || layer < 0 || layer >= s->n_layers || kind < 0 || kind >= VH_PACK_KINDS) return;
+    const size_t i = (size_t)kind * s->n_layers + layer;
+    if (!s->pbufs[i]) return;
+    if (s->nfree == s->capfree) {
+        int nc = s->capfree ? 2 * s->capfree : 64;
+        FreeBlock *nf = realloc(s->freel, (size_t)nc * sizeof *nf);
+        if (nf) { s->freel = nf; s->capfree = nc; }
+    }
+    if (s->nfree < s->capfree) s->freel[s->nfree++] = (FreeBlock){s->pbufs[i], s->pbytes[i], NULL, 0};
+    else block_free(s, s->pbufs[i]);
+    s->packed_bytes -= s->pbytes[i];
+    s->pbufs[i] = NULL;
+    s->pbytes[i] = 0;
 }
 
 /* 1 when every registered expert of every layer fits the capacity at once:
@@ -961,7 +1022,7 @@ int vh_store_prefetch_next(ExpertStore *s, int layer, hipStream_t cs) {
         if (!sl || !sl->registered || sl->resident) continue;
         if (s->capacity_bytes) {
             make_room(s, sl->bytes);
-            if (s->resident_bytes + sl->bytes > s->capacity_bytes) { s->hint_pos = s->hint_n; return 0; }
+            if (s->resident_bytes + s->packed_bytes + sl->bytes > s->capacity_bytes) { s->hint_pos = s->hint_n; return 0; }
         }
         const int rc = page_in(s, sl, cs);
         if (rc) return rc;

@@ -149,7 +149,9 @@ int stack_step(const vireo_moe_stack *st, int32_t *token, float *x, float *xb, f
     if (!rc) rc = vireo_rmsnorm(xb, x, st->out_norm, d, 1, st->eps, s);
     if (!rc) rc = qmatvec_async(logits, xb, st->lm_head, d, st->vocab, s);
     if (!rc) rc = vireo_argmax(logits, st->vocab, token, s);
-    return vh_finish(static_cast<hipStream_t>(s), rc);
+    rc = vh_finish(static_cast<hipStream_t>(s), rc);
+    if (!rc && !s && vh_plan_waits()) rc = vh_take_status(nullptr);  // a grid-wide wait that gave up
+    return rc;
 }
 }  // namespace
 

@@ -299,7 +299,9 @@ extern "C" int vireo_model_step(const vireo_model *m, VireoKV *kv, int32_t *toke
         return -EINVAL;
     if (reinterpret_cast<uintptr_t>(state) & 255u) return -EINVAL;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    return vh_finish(s, model_step(m, kv, token, pos, nullptr, want_logits, x, logits, state, s));
+    int rc = vh_finish(s, model_step(m, kv, token, pos, nullptr, want_logits, x, logits, state, s));
+    if (!rc && !s && vh_plan_waits()) rc = vh_take_status(nullptr);  // a grid-wide wait that gave up
+    return rc;
 }
 
 extern "C" int vireo_model_step_pos(const vireo_model *m, VireoKV *kv, int32_t *token, int32_t *pos,
@@ -313,5 +315,7 @@ extern "C" int vireo_model_step_pos(const vireo_model *m, VireoKV *kv, int32_t *
         hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pos);
         rc = vh_check(hipGetLastError());
     }
-    return vh_finish(s, rc);
+    rc = vh_finish(s, rc);
+    if (!rc && !s && vh_plan_waits()) rc = vh_take_status(nullptr);  // a grid-wide wait that gave up
+    return rc;
 }

@@ -107,7 +107,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_bar = take((kFusedBlocks + 1) * 4);
     const size_t o_counts = take(size_t(E) * 4), o_offs = take(size_t(E + 1) * 4), o_perm = take(P * 4),
                  o_active = take(size_t(E + 1) * 4);
-    const size_t o_h = experts ? take(P * fe * 4) : 0;
+    const size_t o_h = (experts && !mfma) ? take(P * fe * 4) : 0;  // the matrix cores keep h in hs
     const size_t o_y = (experts && grouped) ? take(P * d * 4) : 0;
     const size_t o_tiles = mfma ? take(size_t(vh_mfma_plan_words(int(P), E)) * 4) : 0;
     const size_t o_small = mfma ? take(size_t(E + 1) * 4) : 0;
@@ -137,7 +137,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->offs = reinterpret_cast<int32_t *>(b + o_offs);
     ws->perm = reinterpret_cast<int32_t *>(b + o_perm);
     ws->active = reinterpret_cast<int32_t *>(b + o_active);
-    ws->h = experts ? reinterpret_cast<float *>(b + o_h) : nullptr;
+    ws->h = (experts && !mfma) ? reinterpret_cast<float *>(b + o_h) : nullptr;
     ws->ybuf = (experts && grouped) ? reinterpret_cast<float *>(b + o_y) : nullptr;
     ws->tiles = mfma ? reinterpret_cast<int32_t *>(b + o_tiles) : nullptr;
     ws->small = mfma ? reinterpret_cast<int32_t *>(b + o_small) : nullptr;
@@ -234,6 +234,14 @@ int run_layer_kernel(const vireo_moe_model *m, int layer, const void *const *tab
     a.hb_out = hb_out;
     return vh_moe_layer(L.gate_exps->ggml_type, L.down_exps->ggml_type, a, s);
 }
+
+}  // namespace
+
+// Plans 3 and 5 launch kernels whose workgroups wait for each other with a
+// bounded poll: a synchronous call then reads the status word.
+bool vh_plan_waits() { return g_path == 3 || g_path == 5; }
+
+namespace {
 
 bool fused(const vireo_moe_model *m, int layer) {
     if (g_path != 3) return false;
@@ -433,17 +441,18 @@ const void *const *packed_table(const vireo_moe_model *m, int layer, const void 
     if (!g_packed) return nullptr;
     const void *const *pt = vh_store_packed_table(m->es, layer, kind);
     if (pt || !may_alloc) return pt;
-    void *buf = nullptr, *tab = nullptr;
-    const int rc = kind ? vh_mfma_pack_q8(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s)
-                        : vh_mdec_pack_layer(table, m->n_experts, m->dim, m->ffn_exp, &buf, &tab, s);
+    const int E = m->n_experts, d = m->dim, fe = m->ffn_exp;
+    const uint64_t bytes = kind ? vh_mfma_pack_bytes(E, d, fe) : vh_mdec_pack_bytes(E, d, fe);
+    void *buf = vh_store_packed_begin(m->es, layer, kind, bytes);
+    if (!buf) return nullptr;  // over the store's capacity: read the GGUF rows
+    void *tab = nullptr;
+    int rc = kind ? vh_mfma_pack_q8(table, E, d, fe, buf, &tab, s) : vh_mdec_pack_layer(table, E, d, fe, buf, &tab, s);
+    if (!rc) rc = vh_store_set_packed(m->es, layer, kind, tab);
     if (rc) {
         (void)hipGetLastError();
-        return nullptr;
-    }
-    if (vh_store_set_packed(m->es, layer, kind, buf, tab)) {
         (void)hipStreamSynchronize(s);
-        (void)hipFree(tab);
-        (void)hipFree(buf);
+        if (tab) (void)hipFree(tab);
+        vh_store_packed_abort(m->es, layer, kind);
         return nullptr;
     }
     return static_cast<const void *const *>(tab);

@@ -768,25 +768,35 @@ int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm
     return vh_check(hipGetLastError());
 }
 
-int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out,
-                       hipStream_t s) {
-    *buf_out = *tab_out = nullptr;
-    if (E < 1 || d % 256 || fe % 256) return -EINVAL;
+namespace {
+// Bytes of one expert's tiles: gate and up, then down.
+size_t mdec_pack_per(int d, int fe, size_t *gb_out) {
+    const size_t gb = size_t(fe / 16) * (d / 256) * kQ4Tile, db = size_t(d) * vh_row_bytes(VT_Q6_K, fe);
+    if (gb_out) *gb_out = gb;
+    return 2 * gb + db;
+}
+}  // namespace
+
+uint64_t vh_mdec_pack_bytes(int E, int d, int fe) {
+    if (E < 1 || d < 256 || fe < 256 || d % 256 || fe % 256) return 0;
+    return uint64_t(mdec_pack_per(d, fe, nullptr)) * E;
+}
+
+int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void *buf, void **tab_out, hipStream_t s) {
+    *tab_out = nullptr;
+    if (!buf || !vh_mdec_pack_bytes(E, d, fe)) return -EINVAL;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
     if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
     const int64_t rg = vh_row_bytes(VT_Q4_K, d), rd = vh_row_bytes(VT_Q6_K, fe);
-    const size_t gb = size_t(fe / 16) * (d / 256) * kQ4Tile, db = size_t(d) * rd, per = 2 * gb + db;
+    size_t gb = 0;
+    const size_t per = mdec_pack_per(d, fe, &gb);
     std::vector<const void *> src(size_t(3) * E), dst(size_t(3) * E, nullptr);
     if (int rc = vh_check(hipMemcpyAsync(src.data(), table, src.size() * sizeof(void *), hipMemcpyDeviceToHost, s)))
         return rc;
     if (int rc = vh_check(hipStreamSynchronize(s))) return rc;
-    void *buf = nullptr, *tab = nullptr;
-    if (hipMalloc(&buf, per * E) != hipSuccess) return -ENOMEM;
-    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) {
-        (void)hipFree(buf);
-        return -ENOMEM;
-    }
+    void *tab = nullptr;
+    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) return -ENOMEM;
     char *b = static_cast<char *>(buf);
     for (int e = 0; e < E; e++) {
         if (!src[3 * e] || !src[3 * e + 1] || !src[3 * e + 2]) continue;  // unregistered: stays NULL
@@ -806,10 +816,8 @@ int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **bu
     if (rc) {
         (void)hipStreamSynchronize(s);
         (void)hipFree(tab);
-        (void)hipFree(buf);
         return rc;
     }
-    *buf_out = buf;
     *tab_out = tab;
     return 0;
 }

@@ -852,9 +852,15 @@ __global__ void __launch_bounds__(576) q8_frag_pack_kernel(const void *const *__
 }
 }  // namespace
 
-int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s) {
-    *buf_out = *tab_out = nullptr;
-    if (E < 1 || d % kBRows || fe % (kBRows / 2) || d % kBK || fe % kBK) return -EINVAL;
+uint64_t vh_mfma_pack_bytes(int E, int d, int fe) {
+    if (E < 1 || d < kBRows || fe < kBK || d % kBRows || fe % (kBRows / 2) || d % kBK || fe % kBK) return 0;
+    const uint64_t gb = uint64_t(fe) * vh_row_bytes(VT_Q8_0, d), db = uint64_t(d) * vh_row_bytes(VT_Q8_0, fe);
+    return (2 * gb + db) * E;
+}
+
+int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void *buf, void **tab_out, hipStream_t s) {
+    *tab_out = nullptr;
+    if (!buf || !vh_mfma_pack_bytes(E, d, fe)) return -EINVAL;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (int rc = vh_check(hipStreamIsCapturing(s, &cap))) return rc;
     if (cap != hipStreamCaptureStatusNone) return -EBUSY;  // no allocation under capture
@@ -864,12 +870,8 @@ int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_o
     if (int rc = vh_check(hipMemcpyAsync(src.data(), table, src.size() * sizeof(void *), hipMemcpyDeviceToHost, s)))
         return rc;
     if (int rc = vh_check(hipStreamSynchronize(s))) return rc;
-    void *buf = nullptr, *tab = nullptr;
-    if (hipMalloc(&buf, per * E) != hipSuccess) return -ENOMEM;
-    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) {
-        (void)hipFree(buf);
-        return -ENOMEM;
-    }
+    void *tab = nullptr;
+    if (hipMalloc(&tab, src.size() * sizeof(void *)) != hipSuccess) return -ENOMEM;
     char *b = static_cast<char *>(buf);
     for (int e = 0; e < E; e++) {
         if (!src[3 * e] || !src[3 * e + 1] || !src[3 * e + 2]) continue;  // unregistered: stays NULL
@@ -887,10 +889,8 @@ int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_o
     if (rc) {
         (void)hipStreamSynchronize(s);
         (void)hipFree(tab);
-        (void)hipFree(buf);
         return rc;
     }
-    *buf_out = buf;
     *tab_out = tab;
     return 0;
 }

@@ -32,7 +32,9 @@ uint64_t vh_store_capacity(const ExpertStore *s);
 int vh_store_valid(const ExpertStore *s);
 const void *const *vh_store_layer_table(const ExpertStore *s, int layer);
 const void *const *vh_store_packed_table(const ExpertStore *s, int layer, int kind);
-int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *buf, void *tab);
+void *vh_store_packed_begin(ExpertStore *s, int layer, int kind, uint64_t bytes);
+int vh_store_set_packed(ExpertStore *s, int layer, int kind, void *tab);
+void vh_store_packed_abort(ExpertStore *s, int layer, int kind);
 int vh_store_fits_all(const ExpertStore *s);
 uint64_t vh_store_leased_bytes(const ExpertStore *s);
 int vh_store_acquire(ExpertStore *s, int layer, int expert, ExpertView *view, hipStream_t cs);
@@ -49,6 +51,9 @@ void vh_store_note_routing_host(ExpertStore *s, int layer, const int32_t *idx, i
 // routing and VIREO_ROUTE_* flags.
 int vh_moe_layer_normed(const vireo_moe_model *m, int layer, float *x, const float *nw, float eps, float *xb,
                         hipStream_t s, int32_t *idx_out = nullptr, uint32_t *flags_out = nullptr);
+// True under the plans whose kernels' workgroups wait for each other with a
+// bounded poll (3, 5): a synchronous caller reads the status word after them.
+bool vh_plan_waits();
 // y += W x (qmatvec_async with each result added to y[r], one rounding)
 int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d, hipStream_t s);
 // y_i = W_i x for three matrices of n columns in one launch; -ENOTSUP when a
@@ -138,11 +143,12 @@ int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm
                  const void *const *table, bool packed, const void *hp, int d, int fe, int E, int max_slots,
                  int max_count, float *ybuf, hipStream_t s);
 // A copy of the experts behind `table` (device [E x 3]: Q4_K gate, up; Q6_K
-// down) in the decode batch's 16-row tiles: buf_out, one allocation, and
-// tab_out, its device table (NULL where table is). Enqueued on s after a
+// down) in the decode batch's 16-row tiles, written into buf (device,
+// vh_mdec_pack_bytes(E, d, fe) bytes, 0 for a shape it does not take), with
+// tab_out its new device table (NULL where table is). Enqueued on s after a
 // synchronizing read of the table; -EBUSY while s is being captured.
-int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out,
-                       hipStream_t s);
+uint64_t vh_mdec_pack_bytes(int E, int d, int fe);
+int vh_mdec_pack_layer(const void *const *table, int E, int d, int fe, void *buf, void **tab_out, hipStream_t s);
 
 // Matrix-core grouped GEMMs (moe_mfma.hip) for the groups of calls of at
 // least kMfmaMinCall tokens. vh_mfma_plan lists the token tiles of groups of
@@ -177,8 +183,10 @@ int vh_mfma_down(uint32_t type, const int32_t *tiles, int max_tiles, const int32
 // A copy of the Q8_0 experts behind `table` (gate, up: fe rows of d; down: d
 // rows of fe) in the matrix cores' operand order (32-row fragments per K step
 // of 64, each lane's bytes together; the same bytes, -EBUSY under capture),
-// for the GEMMs of pinned layers.
-int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void **buf_out, void **tab_out, hipStream_t s);
+// for the GEMMs of pinned layers, written into buf (vh_mfma_pack_bytes(E, d,
+// fe) bytes) with tab_out its new device table.
+uint64_t vh_mfma_pack_bytes(int E, int d, int fe);
+int vh_mfma_pack_q8(const void *const *table, int E, int d, int fe, void *buf, void **tab_out, hipStream_t s);
 
 // Fused one-token experts kernel (moe_fused.hip): top-k, gate/up, down and
 // combine in one launch of kFusedBlocks workgroups that meet once through
