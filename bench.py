@@ -91,6 +91,8 @@ def parse():
                     choices=sorted(WORKLOADS) + sorted(STACKS) + sorted(PAGED) + sorted(ATTN) + sorted(MODELS)
                     + ["copy-512MiB"])
     ap.add_argument("--layers", type=int, default=None, help="distinct layers rotated through")
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="tokens per layer call of --workload (default: the workload's own)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -864,6 +866,7 @@ def layer_result(args, workload, cpu_seconds):
     shape_name, B, L, biased = WORKLOADS[workload]
     headline = workload == args.workload
     L = (args.layers if headline else None) or L
+    B = (args.tokens if headline else None) or B
     shape = W.SHAPES[shape_name]
     K = (args.steps if headline else None) or (48 * L if B < 64 else 8 * L)
     Wm = args.warmup if args.warmup is not None else L
@@ -889,6 +892,8 @@ def layer_result(args, workload, cpu_seconds):
     if args.phases:
         if B != 1:
             raise SystemExit("--phases: one-token workloads only")
+        if args.plan not in (0, 1, 5):
+            raise SystemExit("--phases: plans 0, 1 (three decode kernels) and 5 (one layer kernel) carry the stamps")
         print(json.dumps({"workload": workload, "plan": args.plan,
                           "phases": decode_phases(m, shape, L, x_all, hb_all, dev, args.plan)}), flush=True)
         m.close()

@@ -215,7 +215,7 @@ int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const
  * routing is unaffected. */
 int vireo_hip_set_path(int path);
 
-/* Decode-batch calls (8 to 63 tokens) on a pinned layer with Q4_K gate/up and
+/* Decode-batch calls (3 to 63 tokens) on a pinned layer with Q4_K gate/up and
  * Q6_K down run on the matrix cores, whose loads read 16 rows of a matrix at
  * a time. With packing on (the default), the first such call on a layer that
  * may allocate (not moe_ffn_forward_noalloc, not under graph capture) copies

@@ -138,11 +138,11 @@ def test_decode_probability_ties(cuda, oracle, path, plan):
     m.close()
 
 
-@pytest.mark.parametrize("T", [1, 7, 8, 40])
+@pytest.mark.parametrize("T", [1, 2, 3, 8, 40])
 @pytest.mark.parametrize("plan", [0, 4])
 def test_decode_batch_matrix_cores(cuda, oracle, path, T, plan):
-    """Q4_K_M calls of 8 to 63 tokens run on the matrix cores (plan 0), smaller
-    calls and plan 4 on the fp32 decode-batch kernels (T=7 and T=8 sit on
+    """Q4_K_M calls of 3 to 63 tokens run on the matrix cores (plan 0), smaller
+    calls and plan 4 on the fp32 decode-batch kernels (T=2 and T=3 sit on
     either side of the switch). With 40 tokens over 8 experts (top 4) every
     group holds more than one 16-token tile. Token 0's
     inputs are scaled past the fp16 range (their split takes a power of two
@@ -232,18 +232,20 @@ def test_golden_moe_on_gpu(cuda, case):
     m.close()
 
 
-@pytest.mark.parametrize("plan", [0, 2])
-def test_unregistered_expert_is_skipped(cuda, oracle, path, plan):
+@pytest.mark.parametrize("plan,T", [(0, 1), (2, 3), (0, 12)])
+def test_unregistered_expert_is_skipped(cuda, oracle, path, plan, T):
+    """An expert without slices contributes nothing: the one-token plan, and
+    the matrix-core decode batch, whose down kernel combines (its rows of y
+    are zeros)."""
     path(plan)
     shape = W.SHAPES["olmoe-q4_k_m"]
-    x, hb = W.host_hidden(shape.d, 3, 52)
+    x, hb = W.host_hidden(shape.d, T, 52)
     probe = M.DeviceMoE(shape, 1, seed=52)
     first = probe.route(0, torch.from_numpy(hb).to(cuda))[0].cpu().numpy()
     probe.close()
     drop = {(0, int(first[0, 0])), (0, int(first[0, 3]))}
     m = M.DeviceMoE(shape, 1, seed=52, unregistered=drop)
     m._unregistered = drop
-    T = 1 if plan == 0 else 3
     xt = torch.from_numpy(x[:T]).to(cuda)
     idx, _ = m.forward(0, xt, torch.from_numpy(hb[:T]).to(cuda), return_routing=True)
     xo, io, _, _ = oracle_layer(oracle, m, 0, x[:T], hb[:T])
@@ -262,10 +264,11 @@ def test_zero_tokens_is_a_no_op(cuda):
 def test_deterministic_and_batch_invariant(cuda, path):
     """No float atomics: the same call gives the same bits; on the grouped
     plan a token's result does not depend on the other tokens of its call as
-    long as the calls run on the same kernels - 8 to 63 tokens on the matrix
-    cores (16 tokens against two calls of 8), fewer than 8 on the fp32
-    decode-batch kernels (4 tokens against single tokens). Across the switch
-    the last bits differ, both within the parity tolerance."""
+    long as the calls run on the same kernels - 3 to 63 tokens on the matrix
+    cores (16 tokens against two calls of 8, and 3 tokens against the same
+    tokens in the 16), fewer than 3 on the fp32 decode-batch kernels (2
+    tokens against single tokens). Across the switch the last bits differ,
+    both within the parity tolerance."""
     shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
     m = M.DeviceMoE(shape, 1, seed=54)
     x, hb = W.host_hidden(shape.d, 16, 54)
@@ -280,9 +283,10 @@ def test_deterministic_and_batch_invariant(cuda, path):
     np.testing.assert_array_equal(outs[0], outs[1])
     path(2)
     np.testing.assert_array_equal(np.concatenate([run(0, 8), run(8, 16)]), outs[0])
-    four = run(4, 8)
-    for t in (4, 5, 7):
-        np.testing.assert_array_equal(run(t, t + 1)[0], four[t - 4])
+    np.testing.assert_array_equal(run(5, 8), outs[0][5:8])
+    two = run(4, 6)
+    for t in (4, 5):
+        np.testing.assert_array_equal(run(t, t + 1)[0], two[t - 4])
     m.close()
 
 

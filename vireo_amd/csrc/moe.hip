@@ -38,12 +38,13 @@ int g_packed = 1;
 // result does not depend on the other tokens of its call either way.
 constexpr int kExactRouteTokens = 64;
 // From this many tokens on, a decode-batch call's groups run on the matrix
-// cores (moe_mdec.hip): a tile takes 16 tokens of an expert, and below 8
-// tokens per call (about one token per routed expert) converting each weight
-// for the fp32 kernels costs less than the tile's unused rows. Measured per
-// layer (matrix cores / fp32): OLMoE Q4_K_M B=6 92.2 / 89.9 us, B=8 96.9 /
-// 120.2; Qwen3 Q4_K_M B=4 67.7 / 59.4, B=8 94.0 / 104.8.
-constexpr int kMdecMinTokens = 8;
+// cores (moe_mdec.hip): a tile takes 16 tokens of an expert, and with two
+// tokens per call converting each weight for the fp32 kernels costs less
+// than the tile's unused rows. Measured per layer on the packed tiles
+// (matrix cores / fp32): OLMoE Q4_K_M B=2 43.2 / 42.7 us, B=3 51.2 / 52.2,
+// B=4 54.0 / 67.4, B=6 65.1 / 91.5; Qwen3 Q4_K_M B=2 43.0 / 40.6, B=3
+// 48.8 / 49.5, B=4 52.8 / 59.7, B=6 59.6 / 78.9.
+constexpr int kMdecMinTokens = 3;
 
 bool type_ok(uint32_t t, int n) {
     // the expert formats of the MoE models (Q8_0, Q4_K gate/up, Q6_K down), and
@@ -81,6 +82,7 @@ struct Ws {
     void *xb;                // matrix-core plan: bf16 copy of hb
     void *xp;                // decode-batch matrix-core plan: split inputs [T x d x 4 bytes]
     float *xsc;              // and their per-token scales [T]
+    uint32_t *ctr;           // and the down kernel's arrival counters (vh_mdec_ctr_words)
     const void **tab;        // paged plan: [E + 1] expert tables [3 E] (one per batch, then the combine's)
     int32_t *act;            // paged plan: [E] active lists [E + 1] (one per batch)
     int32_t *pidx;           // paged plan: the next layer's guessed routing [T x k]
@@ -115,6 +117,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     const size_t o_xb = mfma ? take(size_t(T) * d * 2) : 0;
     const bool small = experts && grouped && T < kMfmaMinCall;
     const size_t o_xp = small ? take(vh_mdec_xp_bytes(T, d)) : 0, o_xsc = small ? take(size_t(T) * 4) : 0;
+    const size_t o_ctr = small ? take(size_t(vh_mdec_ctr_words(d)) * 4) : 0;
     const size_t ntab = paged ? size_t(E + 1) : 1, nact = paged ? size_t(E) : 1;
     const size_t o_tab = take(ntab * 3 * E * sizeof(void *)), o_act = take(nact * (E + 1) * 4);
     const size_t o_pidx = paged ? take(P * 4) : 0, o_pw = paged ? take(P * 4) : 0,
@@ -145,6 +148,7 @@ int get_ws(int T, int E, int k, int d, int fe, bool experts, bool grouped, Ws *w
     ws->xb = mfma ? b + o_xb : nullptr;
     ws->xp = small ? b + o_xp : nullptr;
     ws->xsc = small ? reinterpret_cast<float *>(b + o_xsc) : nullptr;
+    ws->ctr = small ? reinterpret_cast<uint32_t *>(b + o_ctr) : nullptr;
     ws->tab = reinterpret_cast<const void **>(b + o_tab);
     ws->act = reinterpret_cast<int32_t *>(b + o_act);
     ws->pidx = paged ? reinterpret_cast<int32_t *>(b + o_pidx) : nullptr;
@@ -751,7 +755,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     if (rc == -EINVAL) rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, exact, ws.parts, s);
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
-    if (!rc) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    // the matrix-core decode batch finds each expert's tokens itself
+    if (!rc && !mdec) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
     if (!rc && flags_out)
         rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     if (mfma) {  // every group on the matrix cores (its small list stays empty)
@@ -772,10 +777,13 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         if (!rc && !prepped) rc = vh_mdec_prep(hb, n_tokens, d, ws.xp, ws.xsc, s);
         const void *const *pt = rc ? nullptr : packed_table(m, layer, table, !src, s);
         const void *const *tb = pt ? pt : table;
+        // no dispatch and no combine kernel: the gate/up and down kernels take
+        // their experts' tokens from idx, and the down kernel combines into x
+        const MdecSelf sf{idx, w, x, ws.ctr, vh_mdec_ctr_words(d), n_tokens, k};
         if (!rc) rc = vh_mdec_gateup(ws.counts, ws.offs, ws.perm, ws.active, tb, pt != nullptr, ws.xp, ws.xsc,
-                                     n_tokens, d, fe, k, E, slots, n_tokens, ws.h, s);
+                                     n_tokens, d, fe, k, E, slots, n_tokens, ws.h, s, &sf);
         if (!rc) rc = vh_mdec_down(ws.counts, ws.offs, ws.perm, ws.active, tb, pt != nullptr, ws.h, d, fe, E, slots,
-                                   n_tokens, ws.ybuf, s);
+                                   n_tokens, ws.ybuf, s, &sf);
     } else if (n_tokens < kMfmaMinCall && vh_gdec_supported(tg, td, d, fe, hb)) {
         // calls of a decode batch's size (a few tokens per group): inputs in registers
         if (!rc) rc = vh_gdec_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, n_tokens, ws.h, s);
@@ -784,7 +792,7 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         if (!rc) rc = vh_grouped_gateup(tg, ws.counts, ws.offs, ws.perm, ws.active, table, hb, d, fe, k, E, slots, ws.h, s);
         if (!rc) rc = vh_grouped_down(td, ws.counts, ws.offs, ws.perm, ws.active, table, ws.h, d, fe, E, slots, ws.ybuf, s);
     }
-    if (!rc) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
+    if (!rc && !mdec) rc = vh_combine(idx, w, table, ws.ybuf, d, k, n_tokens, x, s);
     if (!rc && !src) rc = vh_store_note_routing(m->es, layer, idx, n_tokens, k, s);
     return vh_finish(s, rc);
 }

@@ -135,13 +135,28 @@ bool vh_mdec_supported(uint32_t tg, uint32_t td, int d, int fe);
 int vh_route_parts_tiled(const float *R, const float *hb, const float *bias, int d, int E, int T, RoutePart *parts,
                          void *xp, float *xsc, hipStream_t s);
 int vh_mdec_prep(const float *hb, int T, int d, void *xp, float *xsc, hipStream_t s);
-// `packed`: table points at vh_mdec_pack_layer's tiles instead of GGUF rows.
+// A decode-batch call whose matrix-core kernels find each expert's pairs in
+// the routing themselves (no dispatch: workgroup column e takes expert e)
+// and whose down kernel also combines into x in selection order (no combine
+// kernel): idx and w [T x k], x [T x d], ctr [nctr] arrival counters
+// (vh_mdec_ctr_words), which the gate/up kernel zeroes. T < 64.
+struct MdecSelf {
+    const int32_t *idx;
+    const float *w;
+    float *x;
+    uint32_t *ctr;
+    int nctr, T, k;
+};
+inline int vh_mdec_ctr_words(int d) { return (d + 127) / 128 * 64; }
+// `packed`: table points at vh_mdec_pack_layer's tiles instead of GGUF rows;
+// `self` (optional): the call's routing (counts, offs, perm and active unused).
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                    const void *const *table, bool packed, const void *xp, const float *xsc, int T, int d, int fe,
-                   int k, int E, int max_slots, int max_count, void *hp, hipStream_t s);
+                   int k, int E, int max_slots, int max_count, void *hp, hipStream_t s,
+                   const MdecSelf *self = nullptr);
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                  const void *const *table, bool packed, const void *hp, int d, int fe, int E, int max_slots,
-                 int max_count, float *ybuf, hipStream_t s);
+                 int max_count, float *ybuf, hipStream_t s, const MdecSelf *self = nullptr);
 // A copy of the experts behind `table` (device [E x 3]: Q4_K gate, up; Q6_K
 // down) in the decode batch's 16-row tiles, written into buf (device,
 // vh_mdec_pack_bytes(E, d, fe) bytes, 0 for a shape it does not take), with

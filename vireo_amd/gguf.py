@@ -194,10 +194,15 @@ class GGUFModel:
         return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
 
     def hbm_stats(self):
-        """What the HBM pool did (expert_store_hbm_stats)."""
+        """What the HBM pool did (expert_store_hbm_stats; resident_bytes
+        includes the packed copies of pinned layers)."""
         st = _lib.ExpertStats()
         self.lib.expert_store_hbm_stats(self.p.contents.model.es, C.byref(st))
         return {n: getattr(st, n) for n, _ in _lib.ExpertStats._fields_}
+
+    def packed_bytes(self):
+        """Bytes of the kernels' packed copies of pinned layers (expert_store_packed_bytes)."""
+        return int(self.lib.expert_store_packed_bytes(self.p.contents.model.es))
 
     def set_prefetch(self, on):
         """Let paged calls read guessed next-layer experts ahead (expert_store_set_prefetch)."""
