@@ -366,8 +366,9 @@ static void release_block(ExpertStore *s, Slot *v) {
         }
         if (s->nfree < s->capfree) {
             /* the block keeps the event of the last kernels that read it: a
-             * later asynchronous copy into it waits for them */
-            s->freel[s->nfree++] = (FreeBlock){v->dev, v->alloc, v->busy_set ? v->busy : NULL, v->busy_set};
+             * later asynchronous copy into it waits for them (an event never
+             * recorded goes along too, for the next owner to reuse) */
+            s->freel[s->nfree++] = (FreeBlock){v->dev, v->alloc, v->busy, v->busy_set};
             v->busy = NULL;
             v->busy_set = 0;
         } else {
