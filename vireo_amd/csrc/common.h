@@ -24,8 +24,9 @@ enum { VT_F32 = 0, VT_F16 = 1, VT_Q4_0 = 2, VT_Q5_0 = 6, VT_Q8_0 = 8, VT_Q4_K = 
 // its phases: wave 0 reads s_memrealtime (the device's 100 MHz clock, the
 // same on every CU) and thread 0 stores up to kStampSlots stamps per
 // workgroup at stamps[workgroup * kStampSlots + slot], for the first
-// kStampBlocks workgroups. A null stamps argument records nothing (one scalar
-// branch per stamp). g_vh_stamps is where the launches being issued record:
+// kStampBlocks workgroups. The stamped kernels are separate instantiations
+// (PhaseStamps<true>), launched only while stamps are being recorded: a
+// runtime branch per stamp in the production kernels cost 0.5 us per layer. g_vh_stamps is where the launches being issued record:
 // kernel i of a layer call at g_vh_stamps + i * kStampBlocks * kStampSlots;
 // null except inside moe_decode_phases.
 constexpr int kStampSlots = 8, kStampBlocks = 256, kStampKernels = 3;
@@ -33,30 +34,34 @@ extern uint64_t *g_vh_stamps;
 inline uint64_t *vh_stamps_for(int kernel) {
     return g_vh_stamps ? g_vh_stamps + size_t(kernel) * kStampBlocks * kStampSlots : nullptr;
 }
-struct PhaseStamps {
+template <bool ON>
+struct PhaseStamps {  // ON: the launch's stamps buffer (vh_stamps_for) is set; off, every call compiles to nothing
     uint64_t *out;
-    uint64_t t[kStampSlots];
+    uint64_t t[ON ? kStampSlots : 1];
     __device__ explicit PhaseStamps(uint64_t *o) : out(o) {
-        for (int i = 0; i < kStampSlots; i++) t[i] = 0;
+        if constexpr (ON)
+            for (int i = 0; i < kStampSlots; i++) t[i] = 0;
     }
     __device__ __forceinline__ void now(int i) {
-        if (out) t[i] = __builtin_amdgcn_s_memrealtime();
+        if constexpr (ON) t[i] = __builtin_amdgcn_s_memrealtime();
     }
     // the stamp after v is available (the wait for a load that produces v comes first)
     template <class V>
     __device__ __forceinline__ void after(int i, V v) {
-        if (out) {
+        if constexpr (ON) {
             asm volatile("" ::"v"(v));
             t[i] = __builtin_amdgcn_s_memrealtime();
         }
     }
     __device__ __forceinline__ void mark(int i, uint64_t v) {
-        if (out) t[i] = v;
+        if constexpr (ON) t[i] = v;
     }
     __device__ __forceinline__ void store() {
-        const int b = int(blockIdx.y * gridDim.x + blockIdx.x);
-        if (out && threadIdx.x == 0 && b < kStampBlocks)
-            for (int i = 0; i < kStampSlots; i++) out[size_t(b) * kStampSlots + i] = t[i];
+        if constexpr (ON) {
+            const int b = int(blockIdx.y * gridDim.x + blockIdx.x);
+            if (threadIdx.x == 0 && b < kStampBlocks)
+                for (int i = 0; i < kStampSlots; i++) out[size_t(b) * kStampSlots + i] = t[i];
+        }
     }
 };
 

@@ -54,7 +54,7 @@ constexpr int kGuWaves = 8;
 // a contiguous split of each matrix (18.3 against 18.65 us per Qwen3 layer).
 constexpr int kPfPerThread = 3;  // warm-up lines per thread: at most 1536 per workgroup
 
-template <int T, int Q, int RPW>
+template <int T, int Q, int RPW, bool ST>
 __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__restrict__ parts,
                                                             const float *__restrict__ hb,
                                                             const void *const *__restrict__ table, int E, int k,
@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     using F = Reg<T>;
     // stamps: 0 start, 1 router parts loaded, 2 top-k chosen, 3 first gate/up
     // row computed, 4 every row written, 7 1 when the order took the exact path
-    PhaseStamps ps(stamps);
+    PhaseStamps<ST> ps(stamps);
     ps.now(0);
     constexpr int NS = F::NS, TPL = 3 * Q;
     __shared__ TopKSmem sm;         // the exact fallback's workspace
@@ -124,25 +124,39 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             plan->down[lane] = table[3 * e + 2];
         }
         if (writer && tid == 0 && flags_out) flags_out[0] = sm.flag;
+    } else if (writer && wv == 0) {
+        int e;
+        float w;
+        route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
+        if (lane < k) {
+            idx_out[lane] = e;
+            w_out[lane] = w;
+            plan->w[lane] = w;
+            plan->down[lane] = table[3 * e + 2];
+        }
+        if (lane == 0 && flags_out) flags_out[0] = 0u;
     }
 
-    // 3. RPW rows of gate and up of the chosen expert j: their loads first,
-    //    then the down rows' warm-up, and only then the plan (the writer's
-    //    softmax weights), so the workgroup that writes it is not the last to
-    //    start streaming
+    // 3. RPW rows of gate and up of the chosen expert j, their loads first,
+    //    then the down rows' warm-up. (Writing the plan after those loads
+    //    instead of before measured slower: Qwen3 18.58 -> 18.97 us per layer,
+    //    OLMoE Q8_0 24.08 -> 26.64.)
     ps.after(2, e_j);
     const uint8_t *G = table_entry<TPL>(tab, 3 * e_j);
     const uint8_t *U = table_entry<TPL>(tab, 3 * e_j + 1);
-    const bool gu_ok = G && U;
     const int o0 = (blockIdx.x * kGuWaves + wv) * RPW;
-    typename F::Raw rg[RPW], ru[RPW];
-    if (gu_ok) {
+    if (!G || !U) {  // unregistered expert: contributes nothing (src/gguf_run.c:201)
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const int64_t o = min(o0 + r, fe - 1);
-            rg[r] = F::fetch(gmem(G), o * row_bytes, lane);
-            ru[r] = F::fetch(gmem(U), o * row_bytes, lane);
-        }
+        for (int r = 0; r < RPW; r++)
+            if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = 0.0f;
+        return;
+    }
+    typename F::Raw rg[RPW], ru[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const int64_t o = min(o0 + r, fe - 1);
+        rg[r] = F::fetch(gmem(G), o * row_bytes, lane);
+        ru[r] = F::fetch(gmem(U), o * row_bytes, lane);
     }
     // the down rows' warm-up, issued after this workgroup's own loads.
     // Unconditional loads (threads past the last line repeat it) whose values
@@ -150,7 +164,7 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     // for the weights issued before them, comes earlier.
     uint32_t pf[kPfPerThread] = {};
     const uint8_t *D = table_entry<TPL>(tab, 3 * e_j + 2);
-    if (gu_ok && pf_rows > 0 && D) {
+    if (pf_rows > 0 && D) {
         const int gq = gridDim.x >> 3, x8 = (blockIdx.y * gridDim.x + blockIdx.x) & 7, q = blockIdx.x >> 3;
         const int64_t span = int64_t(pf_rows) * pf_rb;           // bytes of one down workgroup's rows
         const int lines = int((span + 63) >> 6), per = (pf_nbd >> 3) / gq;  // down workgroups per gate/up one
@@ -161,26 +175,6 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
             const int64_t off = (int64_t(b) * span + int64_t(t % lines) * 64) & ~int64_t(3);
             pf[u] = ld_u32(gmem(D) + off);
         }
-    }
-    if (ok && writer && wv == 0) {
-        int e;
-        float w;
-        route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
-        if (lane < k) {
-            idx_out[lane] = e;
-            w_out[lane] = w;
-            plan->w[lane] = w;
-        }
-        // every lane takes part in the cross-lane reads
-        const void *dn = table_entry_of_lane<TPL>(tab, 3 * (lane < k ? e : 0) + 2);
-        if (lane < k) plan->down[lane] = dn;
-        if (lane == 0 && flags_out) flags_out[0] = 0u;
-    }
-    if (!gu_ok) {  // unregistered expert: contributes nothing (src/gguf_run.c:201)
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
-            if (lane == 63 && o0 + r < fe) h[size_t(j) * fe + o0 + r] = 0.0f;
-        return;
     }
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
@@ -214,8 +208,12 @@ int launch_decode_gateup(const RoutePart *parts, const float *R, const float *hb
         const int64_t lines = (int64_t(pf.rows) * pf.rb + 63) / 64, per = (pf.nbd / 8) / (g.x / 8);
         warm = per * lines <= 512 * kPfPerThread;
     }
-    VH_LAUNCH((decode_gateup_kernel<T, Q, RPW>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe, d, renorm,
-              rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref, vh_stamps_for(1));
+    if (uint64_t *st = vh_stamps_for(1))
+        VH_LAUNCH((decode_gateup_kernel<T, Q, RPW, true>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe,
+                  d, renorm, rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref, st);
+    else
+        VH_LAUNCH((decode_gateup_kernel<T, Q, RPW, false>), g, dim3(64 * kGuWaves), 0, s, parts, hb, table, E, k, fe,
+                  d, renorm, rb, R, bias, h, idx, w, flags, plan, warm ? pf.rows : 0, pf.nbd, pf.rb, nref, nullptr);
     return vh_check(hipGetLastError());
 }
 
@@ -259,7 +257,7 @@ constexpr int kDnRpg = 2;  // rows per lane group
 // grid (d / R), 256 threads, R = kDnRpg * (256 / L) / k. Lane group g (L
 // lanes) takes expert g % k and rows g / k + i * (256 / L / k), i < kDnRpg;
 // lane li of the group owns items li, li + L, ... (at most IPL) of those rows.
-template <int T, int L, int IPL>
+template <int T, int L, int IPL, bool ST>
 __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__restrict__ plan,
                                                            const float *__restrict__ h, int d, int fe, int k, int R,
                                                            int64_t row_bytes, float *__restrict__ x,
@@ -267,7 +265,7 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     using F = Reg<T>;
     // stamps: 0 start, 1 plan loaded, 2 first row computed, 3 every row
     // computed (after the barrier), 4 outputs written
-    PhaseStamps ps(stamps);
+    PhaseStamps<ST> ps(stamps);
     ps.now(0);
     constexpr int NS = F::NS, NG = 256 / L;
     extern __shared__ float ys[];  // [k][R]
@@ -347,8 +345,12 @@ template <int T, int L, int IPL>
 int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, hipStream_t s) {
     const int R = kDnRpg * (256 / L) / k;
     const int64_t rb = row_bytes_of(T, fe);
-    VH_LAUNCH((down_combine_kernel<T, L, IPL>), dim3(d / R), dim3(256), uint32_t(size_t(k) * R * 4), s, plan, h, d,
-              fe, k, R, rb, x, vh_stamps_for(2));
+    const dim3 g(d / R);
+    const uint32_t lds = uint32_t(size_t(k) * R * 4);
+    if (uint64_t *st = vh_stamps_for(2))
+        VH_LAUNCH((down_combine_kernel<T, L, IPL, true>), g, dim3(256), lds, s, plan, h, d, fe, k, R, rb, x, st);
+    else
+        VH_LAUNCH((down_combine_kernel<T, L, IPL, false>), g, dim3(256), lds, s, plan, h, d, fe, k, R, rb, x, nullptr);
     return vh_check(hipGetLastError());
 }
 

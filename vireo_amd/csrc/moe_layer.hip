@@ -56,7 +56,7 @@ VH_DEV void put_part(uint64_t *rec, double c, double beta, uint32_t epoch) {
     st_agent64(rec + 1, (uint64_t(epoch) << 32) | __float_as_uint(__double2float_ru(b)));
 }
 
-template <int TG, int TD, int Q, int RPW, int L, int IPL, int UPG, bool NORM>
+template <int TG, int TD, int Q, int RPW, int L, int IPL, int UPG, bool NORM, bool ST>
 __global__ void __launch_bounds__(512) moe_layer_kernel(
     const float *__restrict__ R, const float *xin, const void *const *__restrict__ table,
     LayerXchg *__restrict__ xg, int E, int k, int fe, int d, int renorm, int64_t rb_gu, int64_t rb_dn,
@@ -66,7 +66,7 @@ __global__ void __launch_bounds__(512) moe_layer_kernel(
     // stamps: 0 start, 1 router part computed, 2 every part received, 3 top-k
     // chosen, 4 first gate/up row computed, 5 activations published, 6 the
     // down expert's activations received, 7 end
-    PhaseStamps ps(stamps);
+    PhaseStamps<ST> ps(stamps);
     ps.now(0);
     using FG = Reg<TG>;
     using FD = Reg<TD>;
@@ -382,14 +382,16 @@ int launch_layer(const LayerArgs &a, hipStream_t s) {
     uint32_t *status = nullptr;
     if (int rc = vh_status_word(&status)) return rc;
     const int64_t rb_gu = vh_row_bytes(TG, a.d), rb_dn = vh_row_bytes(TD, a.fe);
-    if (a.norm)
-        VH_LAUNCH((moe_layer_kernel<TG, TD, Q, RPW, L, IPL, UPG, true>), dim3(kLB), dim3(64 * kWaves), 0, s, a.R,
-                  a.xin, a.table, a.xg, a.E, a.k, a.fe, a.d, a.renorm, rb_gu, rb_dn, a.bias, a.x, a.idx, a.w, a.flags,
-                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out, vh_stamps_for(0));
-    else
-        VH_LAUNCH((moe_layer_kernel<TG, TD, Q, RPW, L, IPL, UPG, false>), dim3(kLB), dim3(64 * kWaves), 0, s, a.R,
-                  a.xin, a.table, a.xg, a.E, a.k, a.fe, a.d, a.renorm, rb_gu, rb_dn, a.bias, a.x, a.idx, a.w, a.flags,
-                  status, vh_spin_limit(), a.nw, a.eps, a.hb_out, vh_stamps_for(0));
+    uint64_t *st = vh_stamps_for(0);
+#define VH_LAYER(NORM, ST)                                                                                           \
+    VH_LAUNCH((moe_layer_kernel<TG, TD, Q, RPW, L, IPL, UPG, NORM, ST>), dim3(kLB), dim3(64 * kWaves), 0, s, a.R,  \
+              a.xin, a.table, a.xg, a.E, a.k, a.fe, a.d, a.renorm, rb_gu, rb_dn, a.bias, a.x, a.idx, a.w, a.flags,    \
+              status, vh_spin_limit(), a.nw, a.eps, a.hb_out, st)
+    if (a.norm && st) VH_LAYER(true, true);
+    else if (a.norm) VH_LAYER(true, false);
+    else if (st) VH_LAYER(false, true);
+    else VH_LAYER(false, false);
+#undef VH_LAYER
     return vh_check(hipGetLastError());
 }
 

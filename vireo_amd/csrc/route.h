@@ -837,20 +837,3 @@ VH_DEV const uint8_t *table_entry(const void *const (&tab)[TPL], int idx) {
     return reinterpret_cast<const uint8_t *>((uint64_t(hi) << 32) | lo);
 }
 
-// Entry idx of the same distributed table, idx per lane (all 64 lanes
-// active): cross-lane reads (ds_bpermute) of the TPL slots of lane idx / TPL,
-// so no global load is involved (a kernel whose vector loads are in flight
-// does not wait for them here).
-template <int TPL>
-VH_DEV const void *table_entry_of_lane(const void *const (&tab)[TPL], int idx) {
-    const int src = idx / TPL, slot = idx - src * TPL;
-    uint64_t v = 0;
-#pragma unroll
-    for (int s = 0; s < TPL; s++) {
-        const uint64_t t = reinterpret_cast<uint64_t>(tab[s]);
-        const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(src * 4, int(uint32_t(t))));
-        const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(src * 4, int(uint32_t(t >> 32))));
-        if (s == slot) v = (uint64_t(hi) << 32) | lo;
-    }
-    return reinterpret_cast<const void *>(v);
-}

@@ -20,12 +20,12 @@
 
 namespace {
 
-template <int C>
+template <int C, bool ST>
 __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict__ R, const float *__restrict__ hb,
                                                          const float *__restrict__ bias, int d, int E,
                                                          RoutePart *__restrict__ parts, uint32_t *__restrict__ zero,
                                                          int nzero, uint64_t *__restrict__ stamps) {
-    PhaseStamps ps(stamps);
+    PhaseStamps<ST> ps(stamps);
     ps.now(0);
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
@@ -44,14 +44,14 @@ __global__ void __launch_bounds__(64) route_parts_kernel(const float *__restrict
 // (the same operations in every wave, so the same r), forms
 // hb = (x * r) * w in registers and uses it for its row's part; the wave of
 // expert 0 also writes hb for the later stages. d == 64 * C.
-template <int C>
+template <int C, bool ST>
 __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__restrict__ R, const float *__restrict__ x,
                                                               const float *__restrict__ nw, float eps,
                                                               float *__restrict__ hb_out, const float *__restrict__ bias,
                                                               int d, int E, RoutePart *__restrict__ parts,
                                                               uint32_t *__restrict__ zero, int nzero,
                                                               uint64_t *__restrict__ stamps) {
-    PhaseStamps ps(stamps);
+    PhaseStamps<ST> ps(stamps);
     ps.now(0);
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
@@ -278,8 +278,12 @@ int vh_route_parts_norm(const float *R, const float *x, const float *nw, float e
     if (d != 2048 || (reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(hb_out) & 15u) ||
         (reinterpret_cast<uintptr_t>(R) & 15u) || nzero > E * T * 64)
         return -EINVAL;
-    VH_LAUNCH(route_parts_norm_kernel<32>, dim3(E, T), dim3(64), 0, s, R, x, nw, eps, hb_out, bias, d, E, parts, zero,
-              nzero, vh_stamps_for(0));
+    if (uint64_t *st = vh_stamps_for(0))
+        VH_LAUNCH((route_parts_norm_kernel<32, true>), dim3(E, T), dim3(64), 0, s, R, x, nw, eps, hb_out, bias, d, E,
+                  parts, zero, nzero, st);
+    else
+        VH_LAUNCH((route_parts_norm_kernel<32, false>), dim3(E, T), dim3(64), 0, s, R, x, nw, eps, hb_out, bias, d, E,
+                  parts, zero, nzero, nullptr);
     return vh_check(hipGetLastError());
 }
 
@@ -304,8 +308,12 @@ int vh_route_parts(const float *R, const float *hb, const float *bias, int d, in
                           (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
         dim3 g(E, T);
         uint64_t *st = vh_stamps_for(0);
-        if (fast) VH_LAUNCH(route_parts_kernel<32>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
-        else VH_LAUNCH(route_parts_kernel<0>, g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
+        if (fast && st)  // the stamped build only where the phases are recorded (d == 2048)
+            VH_LAUNCH((route_parts_kernel<32, true>), g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
+        else if (fast)
+            VH_LAUNCH((route_parts_kernel<32, false>), g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
+        else
+            VH_LAUNCH((route_parts_kernel<0, false>), g, dim3(64), 0, s, R, hb, bias, d, E, parts, zero, nzero, st);
     }
     return vh_check(hipGetLastError());
 }
