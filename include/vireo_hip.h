@@ -66,6 +66,12 @@ int qdequant_rows(uint32_t ggml_type, const void *src, float *dst, int n, int ro
  * o = x * (1/sqrt(mean(x^2) + eps)) * w. w: device [n] F32 weight, or NULL
  * for a unit weight. o may equal x. */
 int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream);
+/* The same for one row, bit for bit the reference's: its in-order fp32 sum of
+ * squares (src/gguf_run.c:162), then the scale and the products in its order
+ * (vireo_rmsnorm sums the squares in fp64 and rounds once: within 2e-5 of
+ * this, and parallel). One workgroup adds the n squares in order, about 7 us
+ * for n = 2048. o must not alias x. */
+int vireo_rmsnorm_exact(float *o, const float *x, const float *w, int n, float eps, void *stream);
 /* The router logits exactly as the reference forms them (the F32 gguf_matmul,
  * src/gguf_compute.c:202-207: per expert an in-order fp32 sum of fp32
  * products, no contraction): out[t*E + e] = row e of R . hb[t], for T

@@ -1,5 +1,7 @@
 """qmatvec / qdequant_rows / rmsnorm / argmax on the GPU against the oracle,
 the golden vectors and the rigorous error bound of an fp32 dot product."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -70,6 +72,26 @@ def test_rmsnorm(cuda, oracle):
     out = M.rmsnorm(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), 1e-6).cpu().numpy()
     for r in range(4):
         np.testing.assert_allclose(out[r], oracle.rmsnorm(x[r], w, 1e-6), rtol=2e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [2048, 768, 5, 20000])
+def test_rmsnorm_exact(cuda, oracle, n):
+    """vireo_rmsnorm_exact equals the reference's rmsnorm bit for bit (its
+    in-order fp32 sum of squares), with an F32 weight row and with none; rows
+    longer than its LDS buffer (20000) sum from the output row."""
+    from vireo_amd import _lib
+    lib = _lib.load()
+    x = W.host_normal(n, 3, 3) * np.float32(7)
+    x[::97] *= np.float32(1e-3)  # magnitudes that make the order of the sum matter
+    for w in (W.host_normal(n, 4, 4), None):
+        xt = torch.from_numpy(x).to(cuda)
+        o = torch.empty_like(xt)
+        wt = torch.from_numpy(w).to(cuda) if w is not None else None
+        _lib.check(lib.vireo_rmsnorm_exact(C.c_void_p(o.data_ptr()), C.c_void_p(xt.data_ptr()),
+                                           C.c_void_p(wt.data_ptr()) if wt is not None else None, n,
+                                           C.c_float(1e-6), None), "vireo_rmsnorm_exact")
+        want = oracle.rmsnorm(x, w if w is not None else np.ones(n, np.float32), 1e-6)
+        np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("n,ties", [(151936, (7, 100000)), (151936, (4096 * 3 - 1, 4096 * 3, 151935)),

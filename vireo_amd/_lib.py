@@ -207,6 +207,7 @@ SIGNATURES = {
     "expert_store_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
     "expert_store_hbm_stats": (None, [c_vp, C.POINTER(ExpertStats)]),
     "expert_store_packed_bytes": (C.c_uint64, [c_vp]),
+    "vireo_rmsnorm_exact": (C.c_int, [c_vp, c_vp, c_vp, C.c_int, C.c_float, c_vp]),
     "expert_store_set_prefetch": (C.c_int, [c_vp, C.c_int]),
     "expert_store_prefetch_stats": (None, [c_vp, C.POINTER(C.c_uint64)]),
     "vireo_hip_status": (C.c_int, [c_vp]),

@@ -183,6 +183,11 @@ int vh_rmsnorm_ref(float *o, const float *x, const float *w, int n, float eps, h
     return vh_check(hipGetLastError());
 }
 
+extern "C" int vireo_rmsnorm_exact(float *o, const float *x, const float *w, int n, float eps, void *stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return vh_finish(s, vh_rmsnorm_ref(o, x, w, n, eps, s));
+}
+
 extern "C" int vireo_rmsnorm(float *o, const float *x, const float *w, int n, int rows, float eps, void *stream) {
     if (n <= 0 || rows < 0 || (rows && (!o || !x))) return -EINVAL;
     if (rows == 0) return 0;
