@@ -20,9 +20,11 @@
  *     reference is synchronous); with a stream the call only enqueues.
  *   - Tensor data must be 4-byte aligned at its start (hipMalloc gives 256);
  *     every row in these formats is a whole number of 2-byte units.
- *   - Calls on one device are not thread-safe with respect to each other: the
- *     library keeps one workspace per device, like the reference's single
- *     Model buffers (src/gguf_run.c:346-350).
+ *   - Calls on one device must not overlap: the library keeps one workspace
+ *     per device, like the reference's single Model buffers
+ *     (src/gguf_run.c:346-350), so calls from other threads, or on other
+ *     streams whose work may run at the same time, race. Calls enqueued on
+ *     one stream are ordered and safe.
  */
 #ifndef VIREO_HIP_H
 #define VIREO_HIP_H
