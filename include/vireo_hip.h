@@ -207,7 +207,11 @@ int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const
 
 /* Execution plan for moe_ffn_forward (a tuning and testing knob; no
  * counterpart in the reference): 0 = automatic (default), 1 = the one-token
- * decode plan whenever it applies, 2 = always the grouped plan, 3 = the
+ * decode plan whenever it applies (also to calls of 2 to 8 tokens, at most 64
+ * (token, routed expert) pairs: every token then gets the bits of a one-token
+ * call; plan 0 does this up to 4 tokens on Q4_K gate/up + Q6_K down layers,
+ * whose larger calls take the matrix cores, and up to 8 on the other types
+ * the one-token kernels take), 2 = always the grouped plan, 3 = the
  * one-token decode plan with its experts fused into one kernel where that
  * kernel is built for the shapes (see moe_decode_stage), 4 = always the
  * grouped plan, with every group on the fp32 kernels, 5 = one token through
@@ -223,7 +227,7 @@ int moe_ffn_forward_noalloc(const vireo_moe_model *m, int layer, float *x, const
  * routing is unaffected. */
 int vireo_hip_set_path(int path);
 
-/* Decode-batch calls (3 to 63 tokens) on a pinned layer with Q4_K gate/up and
+/* Decode-batch calls (5 to 63 tokens, or 3 and 4 under plan 2) on a pinned layer with Q4_K gate/up and
  * Q6_K down run on the matrix cores, whose loads read 16 rows of a matrix at
  * a time. With packing on (the default), the first such call on a layer that
  * may allocate (not moe_ffn_forward_noalloc, not under graph capture) copies

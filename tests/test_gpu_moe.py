@@ -119,6 +119,37 @@ def test_decode_batch_every_type(cuda, oracle, types, T):
     m.close()
 
 
+@pytest.mark.parametrize("name", ["qwen3-30b-a3b-q4_k_m", "olmoe-q4_k_m", "olmoe-q8_0"])
+@pytest.mark.parametrize("T", [2, 3, 5, 8])
+def test_decode_batch_equals_one_token_calls(cuda, oracle, path, name, T):
+    """Calls of 2 to 8 tokens on the decode plan (plan 1) give every token the
+    bits of a one-token call - its routed experts, their weights and its x -
+    also for a token whose order the fp64 bounds leave open (its inputs scaled
+    so that most probabilities underflow: ranked again on exact logits) and,
+    on the OLMoE Q4_K_M layer, with two experts unregistered; and they match
+    the oracle."""
+    path(1)
+    shape = W.SHAPES[name]
+    unreg = {(0, 3), (0, 17)} if name == "olmoe-q4_k_m" else set()
+    m = M.DeviceMoE(shape, 1, seed=71 + T, unregistered=unreg)
+    x, hb = W.host_hidden(shape.d, T, 71 + T)
+    hb[T // 2] *= np.float32(3.0e5)
+    xt = torch.from_numpy(x).to(cuda)
+    hbt = torch.from_numpy(hb).to(cuda)
+    idx, w = m.forward(0, xt, hbt, return_routing=True)
+    xb, ib, wb = xt.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        x1 = torch.from_numpy(x[t:t + 1].copy()).to(cuda)
+        i1, w1 = m.forward(0, x1, hbt[t:t + 1], return_routing=True)
+        np.testing.assert_array_equal(ib[t:t + 1], i1.cpu().numpy())
+        np.testing.assert_array_equal(wb[t:t + 1].view(np.uint32), w1.cpu().numpy().view(np.uint32))
+        np.testing.assert_array_equal(xb[t:t + 1].view(np.uint32), x1.cpu().numpy().view(np.uint32))
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"decode batch {name} T={T}", x, xb, xo, ib, io)
+    np.testing.assert_allclose(wb, wo, rtol=1e-5, atol=1e-30)
+    m.close()
+
+
 @pytest.mark.parametrize("plan", [0, 1, 3, 5])
 def test_decode_probability_ties(cuda, oracle, path, plan):
     """A token whose inputs are so large that all but a few probabilities
@@ -139,12 +170,13 @@ def test_decode_probability_ties(cuda, oracle, path, plan):
 
 
 @pytest.mark.parametrize("T", [1, 2, 3, 8, 40])
-@pytest.mark.parametrize("plan", [0, 4])
+@pytest.mark.parametrize("plan", [0, 2, 4])
 def test_decode_batch_matrix_cores(cuda, oracle, path, T, plan):
-    """Q4_K_M calls of 3 to 63 tokens run on the matrix cores (plan 0), smaller
-    calls and plan 4 on the fp32 decode-batch kernels (T=2 and T=3 sit on
-    either side of the switch). With 40 tokens over 8 experts (top 4) every
-    group holds more than one 16-token tile. Token 0's
+    """Q4_K_M calls of 3 to 63 tokens run on the matrix cores under plan 2
+    (under plan 0 from 5 tokens; 2 to 4 take the decode plan), smaller calls
+    and plan 4 on the fp32 decode-batch kernels (T=2 and T=3 sit on either
+    side of the switch under plan 2). With 40 tokens over 8 experts (top 4)
+    every group holds more than one 16-token tile. Token 0's
     inputs are scaled past the fp16 range (their split takes a power of two
     per token) and token 1's far below it."""
     path(plan)

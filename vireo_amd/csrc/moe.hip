@@ -3,7 +3,8 @@
 //
 // Reference: moe_ffn, src/gguf_run.c:185-214. Two execution plans produce its
 // result for a batch of independent tokens:
-//   decode (one token):  router parts -> fused top-k + gate/up SwiGLU ->
+//   decode (one token, or a decode batch of up to kDecodeBatchMax tokens):
+//                        router parts -> fused top-k + gate/up SwiGLU ->
 //                        down + combine + residual               (3 kernels)
 //   grouped (any count): router -> top-k -> dispatch -> grouped gate/up ->
 //                        grouped down -> combine + residual      (6 kernels)
@@ -45,6 +46,19 @@ constexpr int kExactRouteTokens = 64;
 // B=4 54.0 / 67.4, B=6 65.1 / 91.5; Qwen3 Q4_K_M B=2 43.0 / 40.6, B=3
 // 48.8 / 49.5, B=4 52.8 / 59.7, B=6 59.6 / 78.9.
 constexpr int kMdecMinTokens = 3;
+// Calls of 2 to kDecodeBatchMax tokens whose shapes the one-token kernels
+// take run the decode plan for every token at once: router parts -> top-k
+// and gate/up of the distinct chosen experts -> down + combine per token,
+// each token's bits those of a one-token call. Its fp32 arithmetic grows with
+// the tokens (a weight is converted again for every token that reads it), so
+// on layers whose groups the matrix cores take (moe_mdec.hip) plan 0 uses it
+// only up to kDecodeBatchAuto tokens. Measured per layer (decode batch /
+// matrix cores, or / fp32 grouped kernels for Q8_0): OLMoE Q4_K_M B=2 32.2 /
+// 42.5 us, B=3 42.8 / 48.2, B=4 51.2 / 53.2, B=5 61.3 / 57.8, B=8 96.1 /
+// 68.6; Qwen3 Q4_K_M B=2 30.4 / 40.3, B=4 46.3 / 57.2, B=5 55.0 / 59.6, B=6
+// 64.2 / 63.3, B=8 84.7 / 69.6; OLMoE Q8_0 B=2 39.9 / 49.2, B=4 62.8 / 74.2,
+// B=8 108.4 / 131.1.
+constexpr int kDecodeBatchAuto = 4;
 
 bool type_ok(uint32_t t, int n) {
     // the expert formats of the MoE models (Q8_0, Q4_K gate/up, Q6_K down), and
@@ -720,10 +734,15 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
 
     const bool decode = n_tokens == 1 && g_path != 2 && g_path != 4 && decode_supported(m, layer) &&
                         (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
-    const bool mfma = !decode && g_path != 4 && n_tokens >= kMfmaMinCall && vh_mfma_supported(tg, td, d, fe, E) &&
-                      (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
+    const int batch_max = g_path == 1   ? kDecodeBatchMax
+                          : g_path == 0 ? (vh_mdec_supported(tg, td, d, fe) ? kDecodeBatchAuto : kDecodeBatchMax)
+                                        : 0;
+    const bool dbatch = n_tokens >= 2 && n_tokens <= batch_max && n_tokens * k <= 64 && decode_supported(m, layer) &&
+                        (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
+    const bool mfma = !decode && !dbatch && g_path != 4 && n_tokens >= kMfmaMinCall &&
+                      vh_mfma_supported(tg, td, d, fe, E) && (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
     Ws ws;
-    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode, &ws, mfma, false, src)) return rc;
+    if (int rc = get_ws(n_tokens, E, k, d, fe, true, !decode && !dbatch, &ws, mfma, false, src)) return rc;
     int32_t *idx = idx_out ? idx_out : ws.idx;
     float *w = w_out ? w_out : ws.w;
     int rc;
@@ -744,6 +763,15 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
         rc = vh_finish(s, rc);
         if (!rc && !s && !src && fused(m, layer)) rc = vh_take_status(s);  // a grid-wide wait that gave up
         return rc;
+    }
+    if (dbatch) {  // the decode plan for every token at once
+        rc = vh_route_parts(R, hb, L.logit_bias, d, E, n_tokens, false, ws.parts, s);
+        if (!rc)
+            rc = vh_decode_batch_gateup(tg, ws.parts, R, hb, L.logit_bias, d, E, k, fe, m->topk_renorm, table, ws.h,
+                                        idx, w, flags_out ? flags_out : ws.flags, ws.plan, n_tokens, s);
+        if (!rc) rc = vh_down_combine(td, ws.plan, ws.h, d, fe, k, x, s, n_tokens);
+        if (!rc && !src) rc = vh_store_note_routing(m->es, layer, idx, n_tokens, k, s);
+        return vh_finish(s, rc);
     }
     const bool exact = n_tokens >= kExactRouteTokens;
     const int P = n_tokens * k, slots = P < E ? P : E;

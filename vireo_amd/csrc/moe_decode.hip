@@ -17,6 +17,7 @@
 // results meet in LDS and x[o] += sum_j w_j * y_j is formed in selection order
 // (src/gguf_run.c:208-213). Every output element has one writer: no atomics.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include "common.h"
 #include "qdecode.h"
 #include "route.h"
@@ -191,6 +192,254 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     ps.store();
 }
 
+// ------------------------------------------------------------------ decode batch: top-k + gate/up
+// decode_batch_gateup_kernel (512 threads, one workgroup per CU): the
+// one-token kernel's work for nt tokens in one launch. Wave w < nt ranks
+// token w with route_select_wave on the same parts and with the same
+// certification as decode_gateup_kernel; a token whose order is not certified
+// is ranked again by the whole workgroup on exact logits (route_topk_block).
+// The tokens' chosen experts are merged into the ascending list of distinct
+// experts, and the (distinct expert, gate/up row) items are cut into equal
+// contiguous ranges, one per wave of the grid. A wave keeps kBgDepth items'
+// gate and up rows in flight and multiplies each row with every token that
+// chose its expert, their inputs and run sums held in LDS in each lane's item
+// order. h[t k + j][o] is formed with the operations of decode_gateup_kernel,
+// so each token's activations - and, through down_combine_kernel, its output -
+// are the bits of a one-token call. The outputs of a wave's items gather in
+// LDS and are written after its last row (a store between the rows' loads
+// would make the waits for them count a data-dependent number of stores),
+// where the SwiGLU of each is formed by the wave's lanes side by side.
+constexpr int kBgDepth = 4;
+constexpr int kBgXPad = 36;  // a lane's 32 inputs, then their run sums (at most 4)
+constexpr size_t kBgOutBytes = 60 * 1024;  // the outputs' LDS (with the kernel's 96.5 KB of static LDS)
+
+template <int T, int Q>
+__global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
+    const RoutePart *__restrict__ parts, const float *__restrict__ hb, const void *const *__restrict__ table, int E,
+    int k, int fe, int nt, int renorm, int64_t row_bytes, const float *__restrict__ R, const float *__restrict__ bias,
+    float *__restrict__ h, int32_t *__restrict__ idx_out, float *__restrict__ w_out, uint32_t *__restrict__ flags_out,
+    DecodePlan *__restrict__ plan, int cap) {
+    using F = Reg<T>;
+    constexpr int NS = F::NS, TPL = 3 * Q, NB = kDecodeBatchMax, D = kBgDepth, d = 2048;
+    static_assert(NS <= kBgXPad - 32, "the run sums fit in the lane's pad");
+    __shared__ TopKSmem sm;                               // the exact ranking of an uncertified token
+    __shared__ __align__(16) float xl[NB][64 * kBgXPad];  // token t, lane l: the inputs of item l, then their sums
+    __shared__ double2 cert[kGuWaves][64];
+    __shared__ float2 stage[kGuWaves][64];
+    __shared__ int sel[NB][64];           // token t's experts in selection order
+    __shared__ float wsel[NB][64];        // and their weights (the plan writer's)
+    __shared__ uint64_t chosen[NB][Q];    // token t: bit e % 64 of word e / 64 when it chose e
+    __shared__ uint64_t uni[Q];           // their union
+    __shared__ uint32_t okv[NB], flagv[NB];
+    __shared__ int dlist[64];             // the distinct experts, ascending
+    __shared__ uint64_t pmask[64];        // entry n: bit t k + j when token t's round j chose dlist[n]
+    __shared__ int ndist;
+    extern __shared__ float4 outbuf[];    // per wave: cap outputs
+    // the wave index through readfirstlane: the compiler then keeps everything
+    // derived from it (the item cursor, the pair masks) in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tw = min(wv, nt - 1);  // the token this wave ranks (waves past the last repeat it, writing nothing)
+    const bool writer = blockIdx.x == 0;
+
+    // 1. the prologue's loads, unconditional so that each wait counts exactly
+    //    the loads issued after it: the router parts of token tw, the layer's
+    //    expert table spread over the lanes (entries past 3 E repeat the last
+    //    one and are never read) and this lane's item of token tw's input
+    RoutePart p[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) p[q] = parts[size_t(tw) * E + min(lane + 64 * q, E - 1)];
+    const void *tab[TPL];
+#pragma unroll
+    for (int s = 0; s < TPL; s++) tab[s] = table[min(TPL * lane + s, 3 * E - 1)];
+    float xr[32];
+    F::load_x(hb + size_t(tw) * d, lane, xr);
+
+    // 2. token tw ranked and certified by this wave alone
+    int e_unused0, e_unused1, rank[Q];
+    const bool ok = route_select_wave<Q>(p, E, k, 0, e_unused0, 0, e_unused1, rank, cert[wv]);
+    if (wv < nt) {
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            if (rank[q] >= 0) sel[wv][rank[q]] = lane + 64 * q;
+            const uint64_t m = __ballot(rank[q] >= 0);
+            if (lane == 0) chosen[wv][q] = m;
+        }
+        if (lane == 0) {
+            okv[wv] = ok ? 1u : 0u;
+            flagv[wv] = 0u;
+        }
+        if (ok && writer) {
+            int e;
+            float w;
+            route_weights_wave<Q>(p, rank, E, k, renorm, stage[wv], e, w);
+            if (lane < k) wsel[wv][lane] = w;
+        }
+        float xs[NS];
+        F::sums(xr, xs);
+        float4 *dst = reinterpret_cast<float4 *>(&xl[wv][lane * kBgXPad]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) dst[i] = make_float4(xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]);
+        float sp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < NS; i++) sp[i] = xs[i];
+        dst[8] = make_float4(sp[0], sp[1], sp[2], sp[3]);
+    }
+    __syncthreads();
+
+    // 3. the tokens whose order the bounds leave open, ranked again on exact
+    //    logits by the whole workgroup (the same verdict in every workgroup)
+    for (int t = 0; t < nt; t++) {
+        if (okv[t]) continue;
+        route_topk_block(sm, parts + size_t(t) * E, R, hb + size_t(t) * d, bias, d, E, k, renorm, false, nullptr);
+        if (tid < k) {
+            sel[t][tid] = sm.sel[tid];
+            wsel[t][tid] = sm.sel_w[tid];
+        }
+        if (tid == 0) flagv[t] = sm.flag;
+        if (tid < 64 * Q) {  // wave q: word q of token t's chosen set
+            bool c = false;
+            for (int j = 0; j < k; j++) c = c || sm.sel[j] == tid;
+            const uint64_t m = __ballot(c);
+            if (lane == 0) chosen[t][wv] = m;
+        }
+        __syncthreads();
+    }
+
+    // 4. the distinct experts in ascending order, the pairs that chose each,
+    //    and (workgroup 0) the routing and the down kernel's plan
+    if (tid < Q) {
+        uint64_t u = 0;
+        for (int t = 0; t < nt; t++) u |= chosen[t][tid];
+        uni[tid] = u;
+    }
+    __syncthreads();
+    if (tid < 64 * Q) {  // thread e: expert e
+        const uint64_t u = uni[wv];
+        int before = __popcll(u & ((uint64_t(1) << lane) - 1));
+        for (int q = 0; q < wv; q++) before += __popcll(uni[q]);
+        const bool in = (u >> lane) & 1u;
+        if (in) {
+            dlist[before] = tid;
+            pmask[before] = 0;
+        }
+        if (tid == 64 * Q - 1) ndist = before + (in ? 1 : 0);
+    }
+    __syncthreads();
+    const int P = nt * k;
+    if (tid < P) {
+        const int t = tid / k, j = tid - t * k, e = sel[t][j];
+        int pos = __popcll(uni[e >> 6] & ((uint64_t(1) << (e & 63)) - 1));
+        for (int q = 0; q < (e >> 6); q++) pos += __popcll(uni[q]);
+        atomicOr(reinterpret_cast<unsigned long long *>(&pmask[pos]), 1ull << tid);
+        if (writer) {
+            idx_out[tid] = e;
+            w_out[tid] = wsel[t][j];
+            plan->w[tid] = wsel[t][j];
+            plan->down[tid] = table[3 * e + 2];
+        }
+    }
+    if (writer && tid < nt && flags_out) flags_out[tid] = flagv[tid];
+    __syncthreads();
+
+    // 5. this wave's items i in [i0, i1): distinct expert n = i / fe, row o = i % fe
+    const int total = ndist * fe, W = int(gridDim.x) * kGuWaves;
+    const int per = (total + W - 1) / W, gw = int(blockIdx.x) * kGuWaves + wv;
+    const int i0 = min(gw * per, total), i1 = min(i0 + per, total);
+    if (i0 >= i1) return;
+    float4 *ob = outbuf + size_t(wv) * cap;  // (g, u, index in h) of each output, SwiGLU at the end
+    int nout = 0;
+    // an unregistered expert's items load from hb (any readable row bytes) and write zeros (src/gguf_run.c:201)
+    const uint8_t *spare = reinterpret_cast<const uint8_t *>(hb);
+    // the fetch cursor (uniform): item ic = (distinct expert nc, row oc), that expert's rows and pairs
+    int ic = i0, nc = i0 / fe, oc = i0 - nc * fe;
+    const uint8_t *Gc = nullptr, *Uc = nullptr;
+    uint64_t pmc = 0;
+    auto expert = [&]() {
+        const int e = __builtin_amdgcn_readfirstlane(dlist[nc]);
+        Gc = table_entry<TPL>(tab, 3 * e);
+        Uc = table_entry<TPL>(tab, 3 * e + 1);
+        const uint64_t v = pmask[nc];
+        pmc = (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))))) << 32) |
+              uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
+    };
+    expert();
+    typename F::Raw rg[D], ru[D];
+    uint64_t spm[D];
+    int so[D];
+    bool slive[D];
+    // slot u: the cursor's item, then the cursor moves on (past the range it stays on the last item, fetched
+    // again: every slot issues the same loads, so the waits stay exact)
+    auto fetch = [&](int u) {
+        const bool live = Gc && Uc;
+        const int64_t off = int64_t(oc) * row_bytes;
+        rg[u] = F::fetch(gmem(live ? Gc + off : spare), 0, lane);
+        ru[u] = F::fetch(gmem(live ? Uc + off : spare), 0, lane);
+        spm[u] = pmc;
+        so[u] = oc;
+        slive[u] = live;
+        if (ic + 1 < i1) {
+            ic++;
+            if (++oc == fe) {
+                oc = 0;
+                nc++;
+                expert();
+            }
+        }
+    };
+    int xt = -1;  // the token whose inputs xv / xs hold
+    float xv[32], xs[NS];
+    const int mk = (65536 + k - 1) / k;  // t = p / k as (p * mk) >> 16, exact for p < 64 and k <= 64
+    auto compute = [&](int u) {
+        uint64_t pm = spm[u];
+        while (pm) {
+            const int pr = __builtin_ctzll(pm);
+            pm &= pm - 1;
+            const int t = (pr * mk) >> 16;
+            if (t != xt) {
+                xt = t;
+                const float4 *src = reinterpret_cast<const float4 *>(&xl[t][lane * kBgXPad]);
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 v = src[q];
+                    xv[4 * q] = v.x;
+                    xv[4 * q + 1] = v.y;
+                    xv[4 * q + 2] = v.z;
+                    xv[4 * q + 3] = v.w;
+                }
+                const float4 sv = src[8];
+                const float sa[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                for (int q = 0; q < NS; q++) xs[q] = sa[q];
+            }
+            float g = F::compute(rg[u], lane, xv, xs);
+            float v = F::compute(ru[u], lane, xv, xs);
+            g = group_sum<64>(g);
+            v = group_sum<64>(v);
+            if (lane == 63)
+                ob[nout] = slive[u] ? make_float4(g, v, __int_as_float(pr * fe + so[u]), 0.0f)
+                                    : make_float4(0.0f, 0.0f, __int_as_float(pr * fe + so[u]), 0.0f);
+            nout++;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < D; u++) fetch(u);
+    for (int c = i0; c < i1; c += D) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            if (c + u < i1) compute(u);
+            fetch(u);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // swiglu(0, 0) = +0: an unregistered expert's rows (src/gguf_run.c:201)
+    for (int q = lane; q < nout; q += 64) {
+        const float4 v = ob[q];
+        h[__float_as_int(v.z)] = swiglu(v.x, v.y);
+    }
+}
+
 // The down kernel's row blocks, for the warm-up (0 rows: none).
 struct DownPrefetch {
     int rows, nbd;
@@ -251,13 +500,43 @@ int launch_gateup_t(int rpw, const RoutePart *parts, const float *R, const float
                                    pf, nref, s);
 }
 
+template <int T, int Q>
+int launch_batch_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int E, int k,
+                        int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
+                        uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
+    const int g = vh_num_cus();
+    // a wave's outputs: its items (of at most min(nt k, E) experts' fe rows over the grid's waves) times the
+    // tokens that chose an item's expert
+    const int64_t items = (int64_t(std::min(nt * k, E)) * fe + int64_t(g) * kGuWaves - 1) / (int64_t(g) * kGuWaves);
+    const int cap = int(items * nt);
+    const size_t lds = size_t(kGuWaves) * cap * sizeof(float4);
+    if (lds > kBgOutBytes) return -EINVAL;
+    VH_LAUNCH((decode_batch_gateup_kernel<T, Q>), dim3(g), dim3(64 * kGuWaves), lds, s, parts, hb, table, E, k, fe,
+              nt, renorm, rb, R, bias, h, idx, w, flags, plan, cap);
+    return vh_check(hipGetLastError());
+}
+
+template <int T>
+int launch_batch_gateup_t(const RoutePart *parts, const float *R, const float *hb, const float *bias, int E, int k,
+                          int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
+                          uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
+    if (E <= 64)
+        return launch_batch_gateup<T, 1>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+    if (E <= 128)
+        return launch_batch_gateup<T, 2>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+    return launch_batch_gateup<T, 4>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+}
+
 // ------------------------------------------------------------------ down + combine
 constexpr int kDnRpg = 2;  // rows per lane group
 
-// grid (d / R), 256 threads, R = kDnRpg * (256 / L) / k. Lane group g (L
-// lanes) takes expert g % k and rows g / k + i * (256 / L / k), i < kDnRpg;
-// lane li of the group owns items li, li + L, ... (at most IPL) of those rows.
-template <int T, int L, int IPL, bool ST>
+// grid (d / R, tokens), 256 threads, R = kDnRpg * (256 / L) / k. Lane group
+// g (L lanes) takes expert g % k and rows g / k + i * (256 / L / k), i <
+// kDnRpg; lane li of the group owns items li, li + L, ... (at most IPL) of
+// those rows. MT (a decode batch): workgroup row y takes token y - its
+// selection's plan entries y k .. y k + k - 1, activations h[y k + j] and
+// output row x[y] - with the same operations as a one-token call.
+template <int T, int L, int IPL, bool ST, bool MT = false>
 __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__restrict__ plan,
                                                            const float *__restrict__ h, int d, int fe, int k, int R,
                                                            int64_t row_bytes, float *__restrict__ x,
@@ -274,14 +553,25 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     const int o0 = blockIdx.x * R;
     const int items = F::items(fe);
     const int lane = tid & 63;
-    const uint8_t *D = static_cast<const uint8_t *>(plan->down[j]);
+    const void *const *pdown = plan->down;
+    const float *pw = plan->w;
+    int l2 = lane;
+    if constexpr (MT) {
+        const int y = blockIdx.y;
+        pdown += y * k;
+        pw += y * k;
+        h += size_t(y) * k * fe;
+        x += size_t(y) * d;
+        l2 = lane < k ? lane : 0;  // within this token's k entries
+    }
+    const uint8_t *D = static_cast<const uint8_t *>(pdown[j]);
     // what the combine needs, loaded now: lane j2 < k of wave 0 holds expert
     // j2's weight and whether its lookup succeeded, thread tid < R its output
     // (unconditional loads: DecodePlan has 64 entries and lanes past k are not
     // read; the pointer is tested only in the combine, so nothing waits for it
     // earlier)
-    const void *dj2 = plan->down[lane];
-    const float wj2 = plan->w[lane];
+    const void *dj2 = pdown[l2];
+    const float wj2 = pw[l2];
     const float xo = x[o0 + min(tid, R - 1)];
     // activations of expert j for this lane's items (independent of the plan;
     // items past the row repeat its last one, and their products are skipped)
@@ -342,12 +632,15 @@ int down_lanes(int items, int k) {
 }
 
 template <int T, int L, int IPL>
-int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, hipStream_t s) {
+int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, int nt, hipStream_t s) {
     const int R = kDnRpg * (256 / L) / k;
     const int64_t rb = row_bytes_of(T, fe);
-    const dim3 g(d / R);
+    const dim3 g(d / R, nt);
     const uint32_t lds = uint32_t(size_t(k) * R * 4);
-    if (uint64_t *st = vh_stamps_for(2))
+    if (nt > 1)
+        VH_LAUNCH((down_combine_kernel<T, L, IPL, false, true>), g, dim3(256), lds, s, plan, h, d, fe, k, R, rb, x,
+                  nullptr);
+    else if (uint64_t *st = vh_stamps_for(2))
         VH_LAUNCH((down_combine_kernel<T, L, IPL, true>), g, dim3(256), lds, s, plan, h, d, fe, k, R, rb, x, st);
     else
         VH_LAUNCH((down_combine_kernel<T, L, IPL, false>), g, dim3(256), lds, s, plan, h, d, fe, k, R, rb, x, nullptr);
@@ -355,16 +648,18 @@ int launch_down(const DecodePlan *plan, const float *h, int d, int fe, int k, fl
 }
 
 template <int T>
-int launch_down_t(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, hipStream_t s) {
+int launch_down_t(const DecodePlan *plan, const float *h, int d, int fe, int k, float *x, int nt, hipStream_t s) {
     const int items = Reg<T>::items(fe), L = down_lanes(items, k);
     if (!L) return -EINVAL;
     const int ipl = (items + L - 1) / L;
     if (L == 8)
-        return ipl <= 2 ? launch_down<T, 8, 2>(plan, h, d, fe, k, x, s) : launch_down<T, 8, 3>(plan, h, d, fe, k, x, s);
+        return ipl <= 2 ? launch_down<T, 8, 2>(plan, h, d, fe, k, x, nt, s)
+                        : launch_down<T, 8, 3>(plan, h, d, fe, k, x, nt, s);
     if (L == 16)
-        return ipl <= 2 ? launch_down<T, 16, 2>(plan, h, d, fe, k, x, s)
-                        : launch_down<T, 16, 3>(plan, h, d, fe, k, x, s);
-    return ipl <= 2 ? launch_down<T, 32, 2>(plan, h, d, fe, k, x, s) : launch_down<T, 32, 3>(plan, h, d, fe, k, x, s);
+        return ipl <= 2 ? launch_down<T, 16, 2>(plan, h, d, fe, k, x, nt, s)
+                        : launch_down<T, 16, 3>(plan, h, d, fe, k, x, nt, s);
+    return ipl <= 2 ? launch_down<T, 32, 2>(plan, h, d, fe, k, x, nt, s)
+                    : launch_down<T, 32, 3>(plan, h, d, fe, k, x, nt, s);
 }
 
 }  // namespace
@@ -398,6 +693,21 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
     }
 }
 
+int vh_decode_batch_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias,
+                           int d, int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx,
+                           float *w, uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
+    if (!vh_decode_gateup_supported(type, d, fe) || E > kMaxExperts || k < 1 || nt < 2 || nt > kDecodeBatchMax ||
+        nt * k > 64)
+        return -EINVAL;
+    const int64_t rb = row_bytes_of(type, d);
+    switch (type) {
+    case VT_Q4_K: return launch_batch_gateup_t<VT_Q4_K>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+    case VT_Q8_0: return launch_batch_gateup_t<VT_Q8_0>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+    case VT_Q6_K: return launch_batch_gateup_t<VT_Q6_K>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);
+    default: return -EINVAL;
+    }
+}
+
 bool vh_down_combine_supported(uint32_t type, int d, int fe, int k) {
     if (!(type == VT_Q4_K || type == VT_Q8_0 || type == VT_Q6_K)) return false;
     if (fe % (type == VT_Q8_0 ? 32 : 256) || k < 1 || k > 64) return false;
@@ -408,12 +718,12 @@ bool vh_down_combine_supported(uint32_t type, int d, int fe, int k) {
 }
 
 int vh_down_combine(uint32_t type, const DecodePlan *plan, const float *h, int d, int fe, int k, float *x,
-                    hipStream_t s) {
-    if (!vh_down_combine_supported(type, d, fe, k)) return -EINVAL;
+                    hipStream_t s, int nt) {
+    if (!vh_down_combine_supported(type, d, fe, k) || nt < 1 || nt * k > 64) return -EINVAL;
     switch (type) {
-    case VT_Q4_K: return launch_down_t<VT_Q4_K>(plan, h, d, fe, k, x, s);
-    case VT_Q8_0: return launch_down_t<VT_Q8_0>(plan, h, d, fe, k, x, s);
-    case VT_Q6_K: return launch_down_t<VT_Q6_K>(plan, h, d, fe, k, x, s);
+    case VT_Q4_K: return launch_down_t<VT_Q4_K>(plan, h, d, fe, k, x, nt, s);
+    case VT_Q8_0: return launch_down_t<VT_Q8_0>(plan, h, d, fe, k, x, nt, s);
+    case VT_Q6_K: return launch_down_t<VT_Q6_K>(plan, h, d, fe, k, x, nt, s);
     default: return -EINVAL;
     }
 }

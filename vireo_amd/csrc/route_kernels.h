@@ -90,10 +90,17 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
                      int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx, float *w,
                      uint32_t *flags, DecodePlan *plan, uint32_t down_type, NormRef nref, hipStream_t s);
 bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
-// Down projection + weighted combine + residual for one token:
-// x += sum_j plan.w[j] * down_j h[j], in selection order.
+// The same for a decode batch of 2 <= nt <= kDecodeBatchMax tokens (nt k <=
+// 64): parts [nt x E], hb [nt x d]; h [nt k x fe], idx / w [nt k], flags [nt]
+// and plan entries t k + j as the one-token kernel writes them for each token.
+constexpr int kDecodeBatchMax = 8;
+int vh_decode_batch_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias,
+                           int d, int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx,
+                           float *w, uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s);
+// Down projection + weighted combine + residual, for nt tokens (nt k <= 64):
+// x[t] += sum_j plan.w[t k + j] * down_j h[t k + j], in selection order.
 int vh_down_combine(uint32_t type, const DecodePlan *plan, const float *h, int d, int fe, int k, float *x,
-                    hipStream_t s);
+                    hipStream_t s, int nt = 1);
 bool vh_down_combine_supported(uint32_t type, int d, int fe, int k);
 
 // Grouped path (any number of tokens): dispatch, grouped gate/up, grouped
