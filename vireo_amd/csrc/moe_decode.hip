@@ -83,19 +83,15 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
     // 1. every load of the prologue, issued before any of them is used: the
     //    router parts, the layer's expert table (spread over the lanes) and
     //    this lane's item of the input
+    // (unconditional: entries past E and 3 E repeat the last one; their keys
+    // are masked in the selection and table_entry never reads them, so the
+    // selection waits only for the parts)
     RoutePart p[Q];
 #pragma unroll
-    for (int q = 0; q < Q; q++) {
-        const int e = lane + 64 * q;
-        if (e < E) p[q] = parts[e];
-        else p[q] = RoutePart{0.0, 0.0};
-    }
+    for (int q = 0; q < Q; q++) p[q] = parts[min(lane + 64 * q, E - 1)];
     const void *tab[TPL];
 #pragma unroll
-    for (int s = 0; s < TPL; s++) {
-        const int i = TPL * lane + s;
-        tab[s] = i < 3 * E ? table[i] : nullptr;
-    }
+    for (int s = 0; s < TPL; s++) tab[s] = table[min(TPL * lane + s, 3 * E - 1)];
     float xr[32], xs[NS];
     F::load_x(hb, lane, xr);
     F::sums(xr, xs);
