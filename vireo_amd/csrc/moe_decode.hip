@@ -576,15 +576,18 @@ __global__ void __launch_bounds__(256) down_combine_kernel(const DecodePlan *__r
     for (int m = 0; m < IPL; m++) F::load_x(h + size_t(j) * fe, min(li + L * m, items - 1), xv[m]);
     // every lane loads (items past the row repeat its last one and are not
     // used), through a global-address-space pointer, with no branch: all the
-    // loads are in flight before the first is used
+    // loads are in flight before the first is used. A failed lookup's lanes
+    // load the first row bytes of h instead (readable; their values are not
+    // used): inside a branch the compiler waits for nearly every load before
+    // leaving it.
     typename F::Raw raw[kDnRpg][IPL];
-    if (D) {
+    gbyte *Dg = D ? gmem(D) : gmem(h);
+    const int64_t rsel = D ? row_bytes : 0;
 #pragma unroll
-        for (int rr = 0; rr < kDnRpg; rr++)
+    for (int rr = 0; rr < kDnRpg; rr++)
 #pragma unroll
-            for (int m = 0; m < IPL; m++)
-                raw[rr][m] = F::fetch(gmem(D), int64_t(o0 + rf + rr * rstep) * row_bytes, min(li + L * m, items - 1));
-    }
+        for (int m = 0; m < IPL; m++)
+            raw[rr][m] = F::fetch(Dg, int64_t(o0 + rf + rr * rstep) * rsel, min(li + L * m, items - 1));
 #pragma unroll
     for (int m = 0; m < IPL; m++) F::sums(xv[m], xs[m]);
     ps.after(1, wj2);
