@@ -3,8 +3,8 @@
 moe_ffn_forward's bit for bit on the same inputs (the same kernels run), on
 consecutive calls whose second is smaller than the first, on every plan it
 takes (matrix-core GEMMs on GGUF rows and on packed Q8_0 fragments, the
-matrix-core decode batch on packed tiles, register-input groups, the
-one-token decode plan);
+matrix-core decode batch on packed tiles, register-input groups, the decode
+plan for a batch of tokens and for one token);
 it refuses calls whose intermediates exceed the region (-E2BIG) and layers
 that are not pinned yet (-EINVAL), and it allocates no device memory."""
 import ctypes as C
@@ -78,22 +78,23 @@ def _check_noalloc(cuda, lib, m, shape, sizes, seed, unpinned, too_big):
 
 def test_noalloc_matches_moe_ffn_forward(cuda, lib):
     """Q4_K_M experts: the matrix-core GEMMs (96 tokens), the matrix-core
-    decode batch on its packed 16-row tiles (40), the register-input groups
-    (5) and the one-token plan."""
+    decode batch on its packed 16-row tiles (40 and 5), the decode plan for
+    a batch of 3 tokens and the one-token plan."""
     shape = W.SHAPES["qwen3-30b-a3b-q4_k_m"]
     m = M.DeviceMoE(shape, 2, seed=91)
     try:
-        _check_noalloc(cuda, lib, m, shape, [(0, 96), (1, 40), (1, 5), (0, 1), (1, 1)], 91, (1, 5), 2048)
+        _check_noalloc(cuda, lib, m, shape, [(0, 96), (1, 40), (1, 5), (1, 3), (0, 1), (1, 1)], 91, (1, 5), 2048)
     finally:
         m.close()
 
 
 def test_noalloc_q8_fragments(cuda, lib):
-    """Q8_0 experts of 64+ tokens: the matrix-core GEMMs reading the packed
-    operand fragments the first moe_ffn_forward made."""
+    """Q8_0 experts: calls of 64+ tokens on the matrix-core GEMMs reading the
+    packed operand fragments the first moe_ffn_forward made, 20 tokens on the
+    register-input groups and 6 on the decode plan for a batch."""
     shape = W.SHAPES["olmoe-q8_0"]
     m = M.DeviceMoE(shape, 1, seed=93)
     try:
-        _check_noalloc(cuda, lib, m, shape, [(0, 130), (0, 70)], 93, (0, 70), 2048)
+        _check_noalloc(cuda, lib, m, shape, [(0, 130), (0, 70), (0, 20), (0, 6)], 93, (0, 70), 2048)
     finally:
         m.close()
