@@ -150,6 +150,56 @@ def test_decode_batch_equals_one_token_calls(cuda, oracle, path, name, T):
     m.close()
 
 
+# shapes beyond the models': more than 128 experts (four router parts per
+# lane), a count that is no multiple of 64 with unregistered experts, top-16
+# and top-1, a wider expert; every one at up to the 64 (token, expert) pairs
+BATCH_SHAPES = [
+    (W.MoEShape("batch-e256", 2048, 256, 8, 512, True, W.Q4_K, W.Q4_K, W.Q6_K), 8, ()),
+    (W.MoEShape("batch-e40-k4", 2048, 40, 4, 768, False, W.Q8_0, W.Q8_0, W.Q8_0), 8, ((0, 5), (0, 39))),
+    (W.MoEShape("batch-k16", 2048, 128, 16, 768, True, W.Q4_K, W.Q4_K, W.Q6_K), 4, ()),
+    (W.MoEShape("batch-k1", 2048, 16, 1, 1024, False, W.Q6_K, W.Q6_K, W.Q8_0), 7, ()),
+    (W.MoEShape("batch-fe1536", 2048, 64, 8, 1536, False, W.Q4_K, W.Q4_K, W.Q6_K), 8, ()),
+]
+
+
+@pytest.mark.parametrize("shape,T,unreg", BATCH_SHAPES, ids=[s[0].name for s in BATCH_SHAPES])
+def test_decode_batch_shapes(cuda, oracle, path, shape, T, unreg):
+    """The decode plan for a batch (plan 1) on shapes beyond the models':
+    every token gets the bits of a one-token call, one of them through the
+    exact ranking, and the batch matches the oracle."""
+    path(1)
+    m = M.DeviceMoE(shape, 1, seed=81 + T, unregistered=set(unreg))
+    x, hb = W.host_hidden(shape.d, T, 81 + T)
+    hb[T // 2] *= np.float32(3.0e5)
+    xt = torch.from_numpy(x).to(cuda)
+    hbt = torch.from_numpy(hb).to(cuda)
+    idx, w = m.forward(0, xt, hbt, return_routing=True)
+    xb, ib, wb = xt.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        x1 = torch.from_numpy(x[t:t + 1].copy()).to(cuda)
+        i1, w1 = m.forward(0, x1, hbt[t:t + 1], return_routing=True)
+        np.testing.assert_array_equal(ib[t:t + 1], i1.cpu().numpy())
+        np.testing.assert_array_equal(wb[t:t + 1].view(np.uint32), w1.cpu().numpy().view(np.uint32))
+        np.testing.assert_array_equal(xb[t:t + 1].view(np.uint32), x1.cpu().numpy().view(np.uint32))
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"decode batch {shape.name} T={T}", x, xb, xo, ib, io)
+    m.close()
+
+
+def test_decode_batch_falls_back_past_its_lds(cuda, oracle, path):
+    """A batch whose outputs would not fit the gate/up kernel's LDS (8 tokens,
+    64 experts of width 2048) takes the grouped plan, also under plan 1."""
+    path(1)
+    shape = W.MoEShape("batch-fe2048", 2048, 64, 8, 2048, False, W.Q8_0, W.Q8_0, W.Q8_0)
+    m = M.DeviceMoE(shape, 1, seed=89)
+    x, hb = W.host_hidden(shape.d, 8, 89)
+    xt = torch.from_numpy(x).to(cuda)
+    idx, w = m.forward(0, xt, torch.from_numpy(hb).to(cuda), return_routing=True)
+    xo, io, wo, _ = oracle_layer(oracle, m, 0, x, hb)
+    check(f"decode batch fallback {shape.name}", x, xt.cpu().numpy(), xo, idx.cpu().numpy(), io)
+    m.close()
+
+
 @pytest.mark.parametrize("plan", [0, 1, 3, 5])
 def test_decode_probability_ties(cuda, oracle, path, plan):
     """A token whose inputs are so large that all but a few probabilities

@@ -737,7 +737,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     const int batch_max = g_path == 1   ? kDecodeBatchMax
                           : g_path == 0 ? (vh_mdec_supported(tg, td, d, fe) ? kDecodeBatchAuto : kDecodeBatchMax)
                                         : 0;
-    const bool dbatch = n_tokens >= 2 && n_tokens <= batch_max && n_tokens * k <= 64 && decode_supported(m, layer) &&
+    const bool dbatch = n_tokens >= 2 && n_tokens <= batch_max && decode_supported(m, layer) &&
+                        vh_decode_batch_supported(tg, d, fe, E, k, n_tokens) &&
                         (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;
     const bool mfma = !decode && !dbatch && g_path != 4 && n_tokens >= kMfmaMinCall &&
                       vh_mfma_supported(tg, td, d, fe, E) && (reinterpret_cast<uintptr_t>(hb) & 15u) == 0;

@@ -496,15 +496,20 @@ int launch_gateup_t(int rpw, const RoutePart *parts, const float *R, const float
                                    pf, nref, s);
 }
 
+// A wave's outputs in decode_batch_gateup_kernel on a grid of g workgroups:
+// its items (at most min(nt k, E) experts' fe rows over the grid's waves) times
+// the tokens that chose an item's expert.
+int batch_out_cap(int E, int k, int fe, int nt, int g) {
+    const int64_t items = (int64_t(std::min(nt * k, E)) * fe + int64_t(g) * kGuWaves - 1) / (int64_t(g) * kGuWaves);
+    return int(items * nt);
+}
+
 template <int T, int Q>
 int launch_batch_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int E, int k,
                         int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
                         uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
     const int g = vh_num_cus();
-    // a wave's outputs: its items (of at most min(nt k, E) experts' fe rows over the grid's waves) times the
-    // tokens that chose an item's expert
-    const int64_t items = (int64_t(std::min(nt * k, E)) * fe + int64_t(g) * kGuWaves - 1) / (int64_t(g) * kGuWaves);
-    const int cap = int(items * nt);
+    const int cap = batch_out_cap(E, k, fe, nt, g);
     const size_t lds = size_t(kGuWaves) * cap * sizeof(float4);
     if (lds > kBgOutBytes) return -EINVAL;
     VH_LAUNCH((decode_batch_gateup_kernel<T, Q>), dim3(g), dim3(64 * kGuWaves), lds, s, parts, hb, table, E, k, fe,
@@ -692,12 +697,16 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
     }
 }
 
+bool vh_decode_batch_supported(uint32_t type, int d, int fe, int E, int k, int nt) {
+    return vh_decode_gateup_supported(type, d, fe) && E >= 1 && E <= kMaxExperts && k >= 1 && nt >= 2 &&
+           nt <= kDecodeBatchMax && nt * k <= 64 &&
+           size_t(kGuWaves) * batch_out_cap(E, k, fe, nt, vh_num_cus()) * sizeof(float4) <= kBgOutBytes;
+}
+
 int vh_decode_batch_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias,
                            int d, int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx,
                            float *w, uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
-    if (!vh_decode_gateup_supported(type, d, fe) || E > kMaxExperts || k < 1 || nt < 2 || nt > kDecodeBatchMax ||
-        nt * k > 64)
-        return -EINVAL;
+    if (!vh_decode_batch_supported(type, d, fe, E, k, nt)) return -EINVAL;
     const int64_t rb = row_bytes_of(type, d);
     switch (type) {
     case VT_Q4_K: return launch_batch_gateup_t<VT_Q4_K>(parts, R, hb, bias, E, k, fe, renorm, table, rb, h, idx, w, flags, plan, nt, s);

@@ -94,6 +94,8 @@ bool vh_decode_gateup_supported(uint32_t type, int d, int fe);
 // 64): parts [nt x E], hb [nt x d]; h [nt k x fe], idx / w [nt k], flags [nt]
 // and plan entries t k + j as the one-token kernel writes them for each token.
 constexpr int kDecodeBatchMax = 8;
+// Whether vh_decode_batch_gateup takes the shape (its outputs' LDS included).
+bool vh_decode_batch_supported(uint32_t type, int d, int fe, int E, int k, int nt);
 int vh_decode_batch_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias,
                            int d, int E, int k, int fe, int renorm, const void *const *table, float *h, int32_t *idx,
                            float *w, uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s);
