@@ -528,17 +528,26 @@ struct Reg<VT_Q8_0> {
     struct Words { uint32_t w[9], s; };
     static __host__ __device__ int items(int n) { return n / 32; }
     // block it of the row at byte offset row (even): the aligned window from
-    // the dword holding its first byte. Its last word is two 16-bit loads, at
-    // a + 32 and at a + 32 + s (the same halfword when the block starts 4-aligned),
-    // so nothing past the block is read and no load depends on another.
+    // the dword holding its first byte, its first 32 bytes as two 16-byte
+    // loads (4-aligned: the Q6_K windows' 12-byte loads take the same). Its
+    // last word is two 16-bit loads, at a + 32 and at a + 32 + s (the same
+    // halfword when the block starts 4-aligned), so nothing past the block is
+    // read and no load depends on another: four load instructions per block.
     template <class P>
     static VH_DEV Raw fetch(P base, int64_t row, int it) {
         const int64_t b = row + 34 * int64_t(it);
         Raw r;
         r.s = uint32_t(b) & 3u;
         P a = base + (b - int64_t(r.s));
-#pragma unroll
-        for (int i = 0; i < 8; i++) r.w[i] = ld_u32(a + 4 * i);
+        const uint4 v0 = ld_u128(a), v1 = ld_u128(a + 16);
+        r.w[0] = v0.x;
+        r.w[1] = v0.y;
+        r.w[2] = v0.z;
+        r.w[3] = v0.w;
+        r.w[4] = v1.x;
+        r.w[5] = v1.y;
+        r.w[6] = v1.z;
+        r.w[7] = v1.w;
         r.lo = ld_u16(a + 32);
         r.hi = ld_u16(a + 32 + r.s);
         return r;

@@ -147,14 +147,16 @@ __global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y,
     const int64_t nw = int64_t(gridDim.x) * 4;
     for (int64_t r0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RB; r0 < d; r0 += nw * RB) {
         typename F::Raw raw[RB][IPL];
+        // unconditional (items past the row repeat its last one and are not
+        // used): under a condition the compiler waits for a row's loads before
+        // the next row's are issued
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) {
             const int64_t row = r0 + rr < d ? r0 + rr : d - 1;
 #pragma unroll
-            for (int m = 0; m < IPL; m++) {
-                const int it = lane + 64 * m;
-                if (it < items) raw[rr][m] = F::fetch(w, row * row_bytes, it);
-            }
+            for (int m = 0; m < IPL; m++) raw[rr][m] = F::fetch(w, row * row_bytes, min(lane + 64 * m, items - 1));
+            // rows issued in order: the first row's arithmetic then waits for its own loads only
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) {
