@@ -224,9 +224,9 @@ VH_DEV bf16x8 to_bf16(const float (&v)[8]) {
 // per K step. A tile of fewer rows stages fewer input bytes per step for the
 // same weight bytes: small groups cost less than a full tile.
 template <int T, bool GATEUP, int BM>
-VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kBRows], gbyte *M0, gbyte *M1,
-                      const int32_t *__restrict__ perm, const __bf16 *__restrict__ src, int K, int rows, int k,
-                      int64_t row_bytes, void *__restrict__ out, int base, int m0, int mcnt, int n0) {
+VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kBRows], int (&prow)[kBM], gbyte *M0,
+                      gbyte *M1, const int32_t *__restrict__ perm, const __bf16 *__restrict__ src, int K, int rows,
+                      int k, int64_t row_bytes, void *__restrict__ out, int base, int m0, int mcnt, int n0) {
     static_assert(BM == 32 || BM == 64 || BM == 128, "token tiles of 32, 64 or 128 rows");
     constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;  // output columns per workgroup
     constexpr int WM = BM >= 64 ? 2 : 1, WN = 4 / WM;    // multiplying waves along rows, columns
@@ -234,6 +234,11 @@ VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kB
     constexpr int AQ = BM / 32;                          // input rows staged per staging thread
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nk = K / kBK;
+    // down: the y row of each tile row (the dispatch permutation) in LDS for
+    // the epilogue, read once here (threads of the multiplying waves; the
+    // first barrier below publishes it): loaded under the epilogue's row
+    // condition, each store waited for its own load
+    if (!GATEUP && tid < BM) prow[tid] = perm[base + m0 + min(tid, mcnt - 1)];
 
     if (wv >= 4) {
         // ---- staging waves: thread p stages K chunk kc = p & 7 of A rows
@@ -352,7 +357,7 @@ VH_DEV void mfma_tile(bf16x8 (&As)[2][kChunks][kBM], bf16x8 (&Bs)[2][kChunks][kB
                 for (int jj = 0; jj < FJ / 2; jj++)
                     hs[n0 + (NCOL / WN) * wn + 32 * jj + (lane & 31)] = __bf16(swiglu(acc[i][jj][r], acc[i][FJ / 2 + jj][r]));
             } else {
-                float *y = static_cast<float *>(out) + size_t(perm[pos]) * rows;
+                float *y = static_cast<float *>(out) + size_t(prow[row]) * rows;
 #pragma unroll
                 for (int j = 0; j < FJ; j++) y[n0 + (kBRows / WN) * wn + 32 * j + (lane & 31)] = acc[i][j][r];
             }
@@ -378,6 +383,7 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
     constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;  // output columns per workgroup
     __shared__ bf16x8 As[2][kChunks][kBM];
     __shared__ bf16x8 Bs[2][kChunks][kBRows];
+    __shared__ int prow[kBM];
     const int nct = rows / NCOL, xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
     const int32_t *run = tiles + (GATEUP ? kPlanRunsGU : kPlanRunsDN);
     const int L = run[xcd] + slot;
@@ -399,11 +405,11 @@ __global__ void __launch_bounds__(kThreads) mfma_proj_kernel(const int32_t *__re
         return;
     }
     if (bmt == 32)
-        mfma_tile<T, GATEUP, 32>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+        mfma_tile<T, GATEUP, 32>(As, Bs, prow, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
     else if (bmt == 64)
-        mfma_tile<T, GATEUP, 64>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+        mfma_tile<T, GATEUP, 64>(As, Bs, prow, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
     else
-        mfma_tile<T, GATEUP, 128>(As, Bs, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
+        mfma_tile<T, GATEUP, 128>(As, Bs, prow, M0, M1, perm, src, K, rows, k, row_bytes, out, base, m0, mcnt, n0);
 }
 
 // ---- Q8_0 experts packed in the matrix cores' operand order (kQ8Frag) ----
@@ -429,11 +435,14 @@ constexpr int kFragBytes = 2176;
 // inputs of the next step into the other LDS buffer. The barrier is LDS-only:
 // global loads stay in flight across it.
 template <bool GATEUP, int BM>
-VH_DEV void frag_tile(bf16x8 (&As)[2][kChunks][kBM], gbyte *F, const int32_t *__restrict__ perm,
+VH_DEV void frag_tile(bf16x8 (&As)[2][kChunks][kBM], int (&prow)[kBM], gbyte *F, const int32_t *__restrict__ perm,
                       const __bf16 *__restrict__ src, int K, int rows, int k, void *__restrict__ out, int base, int m0,
                       int mcnt, int n0) {
     constexpr int FI = BM / 32, AQ = (BM * kChunks + kThreads - 1) / kThreads;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nk = K / kBK;
+    // down: the y row of each tile row in LDS for the epilogue (as mfma_tile;
+    // the first barrier below publishes it)
+    if (!GATEUP && tid < BM) prow[tid] = perm[base + m0 + min(tid, mcnt - 1)];
     // this wave's fragments: g = n0 / 16 + wv (gate/up) or n0 / 32 + wv (down)
     gbyte *fb = F + size_t((GATEUP ? n0 / 16 : n0 / 32) + wv) * nk * kFragBytes;
     gbyte *fq = fb + 32 * lane, *fs = fb + 2048 + 4 * (lane & 31);
@@ -532,7 +541,7 @@ VH_DEV void frag_tile(bf16x8 (&As)[2][kChunks][kBM], gbyte *F, const int32_t *__
                     static_cast<__bf16 *>(out)[size_t(base + m0 + row) * rows + n0 + 16 * wv + (lane & 15)] =
                         __bf16(swiglu(g, u));
             } else if (row < mcnt) {
-                static_cast<float *>(out)[size_t(perm[base + m0 + row]) * rows + n0 + 32 * wv + (lane & 31)] = acc[i][r];
+                static_cast<float *>(out)[size_t(prow[row]) * rows + n0 + 32 * wv + (lane & 31)] = acc[i][r];
             }
         }
 }
@@ -551,6 +560,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                                                              void *__restrict__ out) {
     constexpr int NCOL = GATEUP ? kBRows / 2 : kBRows;
     __shared__ bf16x8 As[2][kChunks][kBM];
+    __shared__ int prow[kBM];
     const int nct = rows / NCOL, xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
     const int32_t *run = tiles + (GATEUP ? kPlanRunsGU : kPlanRunsDN);
     const int L = run[xcd] + slot;
@@ -568,11 +578,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         return;
     }
     if (bmt == 32)
-        frag_tile<GATEUP, 32>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
+        frag_tile<GATEUP, 32>(As, prow, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
     else if (bmt == 64)
-        frag_tile<GATEUP, 64>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
+        frag_tile<GATEUP, 64>(As, prow, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
     else
-        frag_tile<GATEUP, 128>(As, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
+        frag_tile<GATEUP, 128>(As, prow, F, perm, src, K, rows, k, out, base, m0, mcnt, n0);
 }
 
 // bf16 copy of n4 x 4 fp32 values (both 16-byte aligned) by workgroup blk of nblk
