@@ -125,11 +125,14 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
         int e;
         float w;
         route_weights_wave<Q>(p, rank, E, k, renorm, stage, e, w);
+        // the down matrix from the table this wave already holds (a reload
+        // from memory would hold the wave's own rows back by a round trip)
+        const void *dn = table_gather<TPL>(tab, 3 * e + 2);
         if (lane < k) {
             idx_out[lane] = e;
             w_out[lane] = w;
             plan->w[lane] = w;
-            plan->down[lane] = table[3 * e + 2];
+            plan->down[lane] = dn;
         }
         if (lane == 0 && flags_out) flags_out[0] = 0u;
     }
@@ -321,17 +324,21 @@ __global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
         if (tid == 64 * Q - 1) ndist = before + (in ? 1 : 0);
     }
     __syncthreads();
-    const int P = nt * k;
-    if (tid < P) {
-        const int t = tid / k, j = tid - t * k, e = sel[t][j];
-        int pos = __popcll(uni[e >> 6] & ((uint64_t(1) << (e & 63)) - 1));
-        for (int q = 0; q < (e >> 6); q++) pos += __popcll(uni[q]);
-        atomicOr(reinterpret_cast<unsigned long long *>(&pmask[pos]), 1ull << tid);
-        if (writer) {
-            idx_out[tid] = e;
-            w_out[tid] = wsel[t][j];
-            plan->w[tid] = wsel[t][j];
-            plan->down[tid] = table[3 * e + 2];
+    const int P = nt * k;  // at most 64: the pairs are wave 0's lanes
+    if (wv == 0) {
+        const int pp = min(tid, P - 1);  // lanes past the last pair repeat it (the gather needs every lane)
+        const int t = pp / k, j = pp - t * k, e = sel[t][j];
+        const void *dn = table_gather<TPL>(tab, 3 * e + 2);  // the down matrix without a memory round trip
+        if (tid < P) {
+            int pos = __popcll(uni[e >> 6] & ((uint64_t(1) << (e & 63)) - 1));
+            for (int q = 0; q < (e >> 6); q++) pos += __popcll(uni[q]);
+            atomicOr(reinterpret_cast<unsigned long long *>(&pmask[pos]), 1ull << tid);
+            if (writer) {
+                idx_out[tid] = e;
+                w_out[tid] = wsel[t][j];
+                plan->w[tid] = wsel[t][j];
+                plan->down[tid] = dn;
+            }
         }
     }
     if (writer && tid < nt && flags_out) flags_out[tid] = flagv[tid];

@@ -823,6 +823,25 @@ VH_DEV void route_weights_wave(const RoutePart (&p)[Q], const int (&rank)[Q], in
     w_out = w;
 }
 
+// Entry idx of a table spread over a wave's registers as table_entry holds
+// it, where idx may differ from lane to lane: every lane reads all TPL slots of
+// lane idx / TPL across the wave (ds_bpermute; call it with every lane of the
+// wave active) and keeps slot idx % TPL. No memory round trip, unlike a
+// reload of the entry from the table.
+template <int TPL>
+VH_DEV const void *table_gather(const void *const (&tab)[TPL], int idx) {
+    const int src = idx / TPL, slot = idx - src * TPL;
+    uint64_t v = 0;
+#pragma unroll
+    for (int s = 0; s < TPL; s++) {
+        const uint64_t t = reinterpret_cast<uint64_t>(tab[s]);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(src << 2, int(uint32_t(t))));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(src << 2, int(uint32_t(t >> 32))));
+        if (s == slot) v = (uint64_t(hi) << 32) | lo;
+    }
+    return reinterpret_cast<const void *>(v);
+}
+
 // Entry idx of a table spread over a wave's registers (lane l holds entries
 // [TPL*l, TPL*l + TPL)); idx must be the same on every lane.
 template <int TPL>

@@ -161,21 +161,44 @@ __global__ void __launch_bounds__(256) route_exact_kernel(const float *__restric
         lds_barrier();  // LDS only: the loads in flight stay in flight
         load(SET, c0 + 2 * CH);
         if (d - c0 >= CH) {
+            // operands of four columns, read one group ahead of their use
+            float4 rn[kExCpl], xn;
+#pragma unroll
+            for (int q = 0; q < kExCpl; q++) rn[q] = rs[kExCpl * g + q][0];
+            xn = *reinterpret_cast<const float4 *>(&xs[tl][0]);
 #pragma unroll
             for (int i4 = 0; i4 < CH / 4; i4++) {
                 float4 r[kExCpl];
 #pragma unroll
-                for (int q = 0; q < kExCpl; q++) r[q] = rs[kExCpl * g + q][i4];
-                const float4 x4 = *reinterpret_cast<const float4 *>(&xs[tl][4 * i4]);
+                for (int q = 0; q < kExCpl; q++) r[q] = rn[q];
+                const float4 x4 = xn;
+                if (i4 + 1 < CH / 4) {
+#pragma unroll
+                    for (int q = 0; q < kExCpl; q++) rn[q] = rs[kExCpl * g + q][i4 + 1];
+                    xn = *reinterpret_cast<const float4 *>(&xs[tl][4 * i4 + 4]);
+                }
+                // the four columns' products first, then the chains' adds in
+                // column order: an add never waits for a product issued just
+                // before it (the asm statement keeps the products ahead)
+                float pr[4][kExCpl];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     const float xv = u == 0 ? x4.x : u == 1 ? x4.y : u == 2 ? x4.z : x4.w;
 #pragma unroll
                     for (int q = 0; q < kExCpl; q++) {
                         const float rv = u == 0 ? r[q].x : u == 1 ? r[q].y : u == 2 ? r[q].z : r[q].w;
-                        acc[q] = add_rn(acc[q], mul_rn(rv, xv));
+                        pr[u][q] = mul_rn(rv, xv);
                     }
                 }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int q = 0; q < kExCpl; q++) asm volatile("" : "+v"(pr[u][q]));
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int q = 0; q < kExCpl; q++) acc[q] = add_rn(acc[q], pr[u][q]);
+                __builtin_amdgcn_sched_barrier(0);  // the next group's products stay behind these adds
             }
         } else {  // the last, partial chunk: only its d - c0 columns
             for (int i = 0; i < d - c0; i++) {
