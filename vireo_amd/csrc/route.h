@@ -24,23 +24,16 @@ constexpr double kRouteMargin = 2e-6;  // separation required beyond the bounds
 constexpr float kNearTie = 1e-6f;      // exact-logit gap reported as an exception
 constexpr int kMaxExperts = 256;
 
-// One wave: router row r (d floats) against x. Lane l owns elements
-// [l*C, l*C + C) so prefix sums follow element order. Returns the part on all lanes.
-// The same part from the lane's C inputs already in registers (columns
-// lane*C .. lane*C + C - 1; d == 64*C).
+// One wave: the part of a router row against x from the lane's C router
+// values rv and inputs xv in registers (columns lane*C .. lane*C + C - 1;
+// d == 64*C): lane l owns elements [l*C, l*C + C), so prefix sums follow
+// element order. Returns the part on all lanes.
 template <int C>
-VH_DEV RoutePart route_row_part_regs(const float *__restrict__ r, const float (&xv)[C], int lane,
+VH_DEV RoutePart route_row_part_vals(const float (&rv)[C], const float (&xv)[C], int lane,
                                      double *abs_products = nullptr) {
     float p[C];
-    const float4 *r4 = reinterpret_cast<const float4 *>(r + lane * C);
 #pragma unroll
-    for (int i = 0; i < C / 4; i++) {
-        const float4 a = r4[i];
-        p[4 * i + 0] = mul_rn(a.x, xv[4 * i + 0]);
-        p[4 * i + 1] = mul_rn(a.y, xv[4 * i + 1]);
-        p[4 * i + 2] = mul_rn(a.z, xv[4 * i + 2]);
-        p[4 * i + 3] = mul_rn(a.w, xv[4 * i + 3]);
-    }
+    for (int i = 0; i < C; i++) p[i] = mul_rn(rv[i], xv[i]);
     double tot = 0.0, absum = 0.0, pabs = 0.0;
 #pragma unroll
     for (int i = 0; i < C; i++) {

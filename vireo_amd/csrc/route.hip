@@ -56,33 +56,46 @@ __global__ void __launch_bounds__(64) route_parts_norm_kernel(const float *__res
     const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane;
     if (gid < nzero) zero[gid] = 0u;
-    float xv[C];
+    // every load first, together: this lane's x, its norm weights (without
+    // them, x again, unused) and its router row piece; then the arithmetic
+    float xv[C], wv[C], rv[C];
     const float4 *x4 = reinterpret_cast<const float4 *>(x + size_t(t) * d + lane * C);
+    const float4 *w4 = reinterpret_cast<const float4 *>((nw ? nw : x + size_t(t) * d) + lane * C);
+    const float4 *r4 = reinterpret_cast<const float4 *>(R + size_t(e) * d + lane * C);
 #pragma unroll
     for (int i = 0; i < C / 4; i++) {
-        const float4 v = x4[i];
+        const float4 v = x4[i], w = w4[i], a = r4[i];
         xv[4 * i + 0] = v.x;
         xv[4 * i + 1] = v.y;
         xv[4 * i + 2] = v.z;
         xv[4 * i + 3] = v.w;
+        wv[4 * i + 0] = w.x;
+        wv[4 * i + 1] = w.y;
+        wv[4 * i + 2] = w.z;
+        wv[4 * i + 3] = w.w;
+        rv[4 * i + 0] = a.x;
+        rv[4 * i + 1] = a.y;
+        rv[4 * i + 2] = a.z;
+        rv[4 * i + 3] = a.w;
     }
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the arithmetic
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < C; i++) ss += double(mul_rn(xv[i], xv[i]));
     ss = wave_sum_d(ss);
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(float(ss), float(d)), eps)));
 #pragma unroll
-    for (int i = 0; i < C; i++) xv[i] = nw ? mul_rn(mul_rn(xv[i], r), nw[lane * C + i]) : mul_rn(xv[i], r);
-    if (e == 0) {
+    for (int i = 0; i < C; i++) xv[i] = nw ? mul_rn(mul_rn(xv[i], r), wv[i]) : mul_rn(xv[i], r);
+    double abs_products;
+    RoutePart p = route_row_part_vals<C>(rv, xv, lane, &abs_products);
+    p = route_part_on_own_norm(p, abs_products, d, bias, e);  // certified against the reference's xb
+    ps.after(1, p.c);
+    if (lane == 0) parts[size_t(t) * E + e] = p;
+    if (e == 0) {  // after the part: no wait in this wave counts these stores
         float4 *h4 = reinterpret_cast<float4 *>(hb_out + size_t(t) * d + lane * C);
 #pragma unroll
         for (int i = 0; i < C / 4; i++) h4[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
     }
-    double abs_products;
-    RoutePart p = route_row_part_regs<C>(R + size_t(e) * d, xv, lane, &abs_products);
-    p = route_part_on_own_norm(p, abs_products, d, bias, e);  // certified against the reference's xb
-    ps.after(1, p.c);
-    if (lane == 0) parts[size_t(t) * E + e] = p;
     ps.store();
 }
 
