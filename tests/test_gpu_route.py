@@ -109,10 +109,13 @@ def test_route_zipf_bias(cuda, oracle):
 
 @pytest.mark.parametrize("T,k,E,skew", [(1, 8, 128, 0), (7, 8, 64, 0), (2048, 8, 128, 0), (300, 1, 256, 0),
                                          (33, 4, 8, 0), (256, 8, 64, 0), (257, 8, 64, 0), (4096, 8, 128, 1.1),
-                                         (1000, 3, 256, 1.1)])
+                                         (1000, 3, 256, 1.1), (1001, 3, 256, 0), (16500, 8, 128, 1.1)])
 def test_dispatch_is_a_stable_sort(cuda, T, k, E, skew):
-    """One-workgroup form up to 2048 pairs, per-expert form above (256 x 8 and
-    257 x 8 straddle the switch); skew draws experts with Zipf weights."""
+    """One-workgroup form up to 2048 pairs (256 x 8 and 257 x 8 straddle the
+    switch); above, one launch with a workgroup per expert when the pair
+    count is a multiple of 4 and at most 131072 (2048 x 8, 4096 x 8,
+    1000 x 3), else the two-kernel form (1001 x 3, 16500 x 8); skew draws
+    experts with Zipf weights."""
     rng = np.random.default_rng(T * k + E)
     p = None
     if skew:

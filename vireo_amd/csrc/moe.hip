@@ -785,7 +785,8 @@ int ffn_forward(const vireo_moe_model *m, int layer, float *x, const float *hb, 
     if (!rc) rc = vh_route_finish(ws.parts, R, hb, L.logit_bias, d, E, k, m->topk_renorm, exact, n_tokens, idx, w,
                                   ws.flags, nullptr, s);
     // the matrix-core decode batch finds each expert's tokens itself
-    if (!rc && !mdec) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, ws.active, s);
+    // (the matrix-core plan lists its groups itself: no active list)
+    if (!rc && !mdec) rc = vh_dispatch(idx, P, E, ws.counts, ws.offs, ws.perm, mfma ? nullptr : ws.active, s);
     if (!rc && flags_out)
         rc = vh_check(hipMemcpyAsync(flags_out, ws.flags, size_t(n_tokens) * 4, hipMemcpyDeviceToDevice, s));
     if (mfma) {  // every group on the matrix cores (its small list stays empty)

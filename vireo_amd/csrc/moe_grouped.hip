@@ -192,6 +192,137 @@ __global__ void __launch_bounds__(256) dispatch_place_kernel(const int32_t *__re
     }
 }
 
+// One launch for large calls (P % 4 == 0, idx 16-byte aligned, P at most
+// kFusedChunks * kFusedChunk pairs): workgroup e reads every pair's expert
+// once - a group of four 4096-pair chunks' loads issued before any is used -
+// and counts the pairs of experts below e (its bucket offset) and its own
+// (its count, and which of its 16 consecutive pairs per thread match, kept in
+// LDS); with `active`, it also marks in LDS the experts seen (its rank among
+// the non-empty experts). Then it writes its pairs in pair order as
+// dispatch_place_kernel does, four chunks per block scan. The same counts,
+// offsets, order and list as the two-kernel form.
+constexpr int kFusedThreads = 256, kFusedChunk = kFusedThreads * kPlacePer, kFusedChunks = 32;
+
+// Exclusive block scan (kFusedThreads threads) of N values at once: before[i]
+// = the sum of v[i] over the threads below, total[i] = over all. Two barriers.
+template <int N>
+VH_DEV void block_excl_scan_n(const int (&v)[N], int (&before)[N], int (&total)[N],
+                              int (&wsum)[kFusedThreads / 64][N]) {
+    constexpr int W = kFusedThreads / 64;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int inc[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) inc[i] = v[i];
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1)
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const int o = __shfl_up(inc[i], sh, 64);
+            if (lane >= sh) inc[i] += o;
+        }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < N; i++) wsum[wv][i] = inc[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        int b = 0, t = 0;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            b += w < wv ? wsum[w][i] : 0;
+            t += wsum[w][i];
+        }
+        before[i] = b + inc[i] - v[i];
+        total[i] = t;
+    }
+    __syncthreads();  // wsum is reused by the next call
+}
+
+__global__ void __launch_bounds__(kFusedThreads) dispatch_fused_kernel(const int32_t *__restrict__ idx, int P, int E,
+                                                                       int32_t *__restrict__ counts,
+                                                                       int32_t *__restrict__ offs,
+                                                                       int32_t *__restrict__ perm,
+                                                                       int32_t *__restrict__ active) {
+    constexpr int W = kFusedThreads / 64;
+    static_assert(kFusedThreads == kMaxExperts, "one thread per expert clears seen[]");
+    __shared__ uint32_t hits[kFusedChunks][kFusedThreads];
+    __shared__ int seen[kMaxExperts];
+    __shared__ int wsum3[W][3], wsum[W][4];
+    const int e = blockIdx.x, tid = threadIdx.x;
+    const bool list = active != nullptr;
+    if (list) seen[tid] = 0;  // kFusedThreads == kMaxExperts
+    __syncthreads();
+    const int nch = (P + kFusedChunk - 1) / kFusedChunk, P4 = P / 4;
+    const int4 *idx4 = reinterpret_cast<const int4 *>(idx);
+    int below = 0, mine = 0;
+    for (int c0 = 0; c0 < nch; c0 += 4) {
+        // four chunks' loads first (unconditional: past the end the last
+        // pairs again, masked below)
+        int4 v[4][kPlacePer / 4];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+            for (int j = 0; j < kPlacePer / 4; j++)
+                v[cc][j] = idx4[min(((c0 + cc) * kFusedChunk + kPlacePer * tid) / 4 + j, P4 - 1)];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const int q0 = (c0 + cc) * kFusedChunk + kPlacePer * tid;
+            const bool whole = q0 + kPlacePer <= P;  // every pair of the thread's 16 exists
+            uint32_t hit = 0;
+#pragma unroll
+            for (int j = 0; j < kPlacePer; j++) {
+                const int4 w4 = v[cc][j / 4];
+                const int x = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
+                const bool in = whole || q0 + j < P;
+                // an expert id outside [0, E) belongs to no bucket: as unsigned it
+                // is at least E, so neither below e nor e
+                below += in && uint32_t(x) < uint32_t(e) ? 1 : 0;
+                hit |= uint32_t(in && x == e) << j;
+                if (list && in && uint32_t(x) < uint32_t(E)) seen[x] = 1;
+            }
+            mine += __popc(hit);
+            if (c0 + cc < nch) hits[c0 + cc][tid] = hit;
+        }
+    }
+    __syncthreads();  // seen[] and hits[] complete
+    const int v3[3] = {below, mine, list && tid < e ? seen[tid] : 0};
+    int b3[3], t3[3];
+    block_excl_scan_n<3>(v3, b3, t3, wsum3);
+    const int base = t3[0], count = t3[1], rank = t3[2];
+    if (tid == 0) {
+        counts[e] = count;
+        offs[e] = base;
+        if (list && count > 0) active[rank] = e;
+        if (e == E - 1) {
+            offs[E] = base + count;
+            if (list) active[E] = rank + (count > 0 ? 1 : 0);
+        }
+    }
+    int run = base;
+    for (int c0 = 0; c0 < nch; c0 += 4) {
+        uint32_t hit[4];
+        int pc[4], before[4], total[4];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            hit[cc] = c0 + cc < nch ? hits[c0 + cc][tid] : 0u;
+            pc[cc] = __popc(hit[cc]);
+        }
+        block_excl_scan_n<4>(pc, before, total, wsum);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            int pos = run + before[cc];
+            const int q0 = (c0 + cc) * kFusedChunk + kPlacePer * tid;
+            uint32_t h = hit[cc];
+            while (h) {
+                const int j = __ffs(h) - 1;
+                perm[pos++] = q0 + j;
+                h &= h - 1u;
+            }
+            run += total[cc];
+        }
+    }
+}
+
 // ------------------------------------------------------------ grouped projections
 // An item's 32 weights dequantized from the resolved words of Reg<T>::fetch, in the
 // item's own order (the order Reg<T>::load_x gives the inputs): every value is
@@ -529,6 +660,10 @@ int vh_dispatch(const int32_t *idx, int P, int E, int32_t *counts, int32_t *offs
                 hipStream_t s) {
     if (P <= kDispatchOneBlock) {
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, idx, P, E, counts, offs, perm, active);
+    } else if (P % 4 == 0 && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0 && P <= kFusedChunks * kFusedChunk &&
+               E <= kMaxExperts) {
+        hipLaunchKernelGGL(dispatch_fused_kernel, dim3(E), dim3(kFusedThreads), 0, s, idx, P, E, counts, offs, perm,
+                           active);
     } else {
         hipLaunchKernelGGL(dispatch_count_kernel, dim3(E), dim3(256), 0, s, idx, P, counts);
         hipLaunchKernelGGL(dispatch_place_kernel, dim3(E), dim3(256), 0, s, idx, P, E, counts, offs, perm, active);
