@@ -18,7 +18,8 @@ token, and the case is counted). Cases cover:
   dim / heads, F16 norm weights (dequantized at load), Q5_0 attention and
   F16 / Q8_0 / Q6_K FFN matrices, an untied head;
 * a tied head (the LM head is the token embedding) with F32 attention and
-  Q4_K FFN matrices.
+  Q4_K FFN matrices;
+* Q4_K and Q6_K attention matrices.
 """
 import numpy as np
 import pytest
@@ -45,6 +46,13 @@ CASES = {
                         ffn_types=(W.F16, W.Q8_0, W.Q6_K), norm_type=W.F16, untied=True),
     "llama-tied": dict(arch="llama", n_layers=2, d=256, n_heads=4, n_kv_heads=1, head_size=64, vocab=256, ffn=256,
                        qk_norm=None, explicit_head=False, attn_type=W.F32, ffn_types=(W.Q4_K, W.Q4_K, W.Q4_K)),
+    # K-quant attention matrices (q, k and v on the register-resident decoders)
+    "llama-q4k-attn": dict(arch="llama", n_layers=2, d=256, n_heads=4, n_kv_heads=2, head_size=64, vocab=256,
+                           ffn=256, qk_norm=None, explicit_head=False, attn_type=W.Q4_K,
+                           ffn_types=(W.Q8_0, W.Q8_0, W.Q8_0)),
+    "olmoe-q6k-attn": dict(arch="olmoe", n_layers=2, d=256, n_heads=4, n_kv_heads=4, head_size=64, vocab=384,
+                           moe=W.MoEShape("o", 256, 8, 3, 256, False, W.Q4_K, W.Q4_K, W.Q6_K), qk_norm="full",
+                           untied=True, explicit_head=False, attn_type=W.Q6_K),
 }
 
 

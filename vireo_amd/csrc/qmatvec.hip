@@ -111,6 +111,73 @@ __global__ void __launch_bounds__(256) qmatvec3_kernel(MvJob j0, MvJob j1, MvJob
     }
 }
 
+// q, k and v on the register-resident decoders (Q4_K, Q6_K and Q8_0 rows of
+// n = 64 IPL items or fewer, x 16-byte aligned): wave w takes kQ3Rows
+// consecutive rows of one matrix - each matrix's row blocks numbered after
+// the previous one's - and issues its inputs' loads and all its rows' raw
+// words before using any (one memory round trip per wave), then reduces each
+// row over the wave as qmatvec_reg_kernel does.
+constexpr int kQ3Rows = 4;
+
+template <int T, int IPL>
+VH_DEV void q3_rows(const MvJob &j, int64_t r0, const float *__restrict__ x, int n, int lane) {
+    using F = Reg<T>;
+    constexpr int NS = F::NS;
+    const int items = F::items(n);
+    float xr[IPL][32], xs[IPL][NS];
+    typename F::Raw raw[kQ3Rows][IPL];
+#pragma unroll
+    for (int m = 0; m < IPL; m++) F::load_x(x, min(lane + 64 * m, items - 1), xr[m]);
+#pragma unroll
+    for (int rr = 0; rr < kQ3Rows; rr++) {
+        const int64_t row = min(r0 + rr, int64_t(j.d) - 1);  // unconditional: rows past the end repeat the last
+#pragma unroll
+        for (int m = 0; m < IPL; m++) raw[rr][m] = F::fetch(j.w, row * j.row_bytes, min(lane + 64 * m, items - 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the arithmetic
+#pragma unroll
+    for (int m = 0; m < IPL; m++) F::sums(xr[m], xs[m]);
+#pragma unroll
+    for (int rr = 0; rr < kQ3Rows; rr++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < IPL; m++) {
+            const int it = lane + 64 * m;
+            if (it < items) acc += F::compute(raw[rr][m], it, xr[m], xs[m]);
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 63 && r0 + rr < j.d) j.y[r0 + rr] = acc;
+    }
+}
+
+template <int IPL>
+__global__ void __launch_bounds__(256) qmatvec3_reg_kernel(MvJob j0, MvJob j1, MvJob j2, const float *__restrict__ x,
+                                                           int n) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t b0 = (j0.d + kQ3Rows - 1) / kQ3Rows, b1 = (j1.d + kQ3Rows - 1) / kQ3Rows,
+                  b2 = (j2.d + kQ3Rows - 1) / kQ3Rows;
+    MvJob j;
+    int64_t r0;
+    if (w < b0) {
+        j = j0;
+        r0 = w * kQ3Rows;
+    } else if (w < b0 + b1) {
+        j = j1;
+        r0 = (w - b0) * kQ3Rows;
+    } else if (w < b0 + b1 + b2) {
+        j = j2;
+        r0 = (w - b0 - b1) * kQ3Rows;
+    } else {
+        return;
+    }
+    switch (j.type) {
+    case VT_Q4_K: q3_rows<VT_Q4_K, IPL>(j, r0, x, n, lane); break;
+    case VT_Q6_K: q3_rows<VT_Q6_K, IPL>(j, r0, x, n, lane); break;
+    default: q3_rows<VT_Q8_0, IPL>(j, r0, x, n, lane); break;
+    }
+}
+
 // Lanes per row: the power of two (<= 64) that leaves the fewest idle item
 // slots, preferring more lanes on a tie.
 int pick_lanes(int items) {
@@ -329,6 +396,18 @@ int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0,
         int64_t rb;
         if (int rc = check_weights(t, w[i]->data, n, d[i], &rb)) return rc;
         j[i] = MvJob{y[i], static_cast<const uint8_t *>(w[i]->data), rb, d[i], t};
+    }
+    auto reg_type = [](uint32_t t) { return t == VT_Q4_K || t == VT_Q6_K || t == VT_Q8_0; };
+    if (reg_type(j[0].type) && reg_type(j[1].type) && reg_type(j[2].type) && n % 256 == 0 && n <= 64 * 32 * 2 &&
+        (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        int64_t waves = 0;
+        for (int i = 0; i < 3; i++) waves += (d[i] + kQ3Rows - 1) / kQ3Rows;
+        const dim3 g(static_cast<unsigned>((waves + 3) / 4)), b(256);
+        if (n <= 64 * 32)
+            hipLaunchKernelGGL(qmatvec3_reg_kernel<1>, g, b, 0, s, j[0], j[1], j[2], x, n);
+        else
+            hipLaunchKernelGGL(qmatvec3_reg_kernel<2>, g, b, 0, s, j[0], j[1], j[2], x, n);
+        return vh_check(hipGetLastError());
     }
     const int L = pick_lanes(n / 32), rpw = 64 / L;
     const int64_t total = int64_t(d0) + d1 + d2;
