@@ -15,7 +15,9 @@ pytestmark = pytest.mark.gpu
 U24 = 2.0 ** -24
 
 CASES = [(W.Q8_0, 2048, 768), (W.Q8_0, 96, 33), (W.Q4_K, 2048, 768), (W.Q6_K, 768, 2048), (W.Q6_K, 1024, 37),
-         (W.Q5_0, 1024, 64), (W.F16, 300, 16), (W.F32, 2048, 128), (W.Q4_K, 256, 1)]
+         (W.Q5_0, 1024, 64), (W.F16, 300, 16), (W.F32, 2048, 128), (W.Q4_K, 256, 1),
+         # register-input kernel, two rows per wave (1024 to 8191 rows of 32 to 128 items)
+         (W.Q4_K, 4096, 2048), (W.Q6_K, 2048, 1536), (W.Q8_0, 2048, 1025)]
 
 
 def _weights(typ, n, d, seed):

@@ -203,14 +203,11 @@ __global__ void __launch_bounds__(256) qmatvec_reg_kernel(float *__restrict__ y,
     const int lane = threadIdx.x & 63;
     const int items = F::items(n);
     float xr[IPL][32], xs[IPL][NS];
+    // unconditional (lanes past the last item load it again, unused)
 #pragma unroll
-    for (int m = 0; m < IPL; m++) {
-        const int it = lane + 64 * m;
-        if (it < items) {
-            F::load_x(x, it, xr[m]);
-            F::sums(xr[m], xs[m]);
-        }
-    }
+    for (int m = 0; m < IPL; m++) F::load_x(x, min(lane + 64 * m, items - 1), xr[m]);
+#pragma unroll
+    for (int m = 0; m < IPL; m++) F::sums(xr[m], xs[m]);
     const int64_t nw = int64_t(gridDim.x) * 4;
     for (int64_t r0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RB; r0 < d; r0 += nw * RB) {
         typename F::Raw raw[RB][IPL];
@@ -267,7 +264,7 @@ int launch_reg(float *y, const float *x, const uint8_t *w, int n, int d, int64_t
 bool reg_path(uint32_t type, const float *x, int n, int d) {
     if (type != VT_Q8_0 && type != VT_Q4_K && type != VT_Q6_K) return false;
     const int items = n / 32;
-    return n % 32 == 0 && items >= 32 && items <= 128 && d >= 4096 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    return n % 32 == 0 && items >= 32 && items <= 128 && d >= 1024 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 // ---- dequant ----
