@@ -223,10 +223,13 @@ int model_step(const vireo_model *m, VireoKV *kv, int32_t *token, int pos, int32
     for (int l = 0; l < m->n_layers && !rc; l++) {
         const vireo_block &B = m->blocks[l];
         bool appended = false;
-        // attention (src/gguf_run.c:221-237)
-        rc = vireo_rmsnorm(b.xb, x, B.attn_norm, d, 1, eps, s);
-        if (!rc) {  // q, k and v in one launch where the types allow
-            rc = vh_qmatvec3(b.xb, d, b.q, B.wq, nq, b.k, B.wk, nk, b.v, B.wv, nk, s);
+        // attention (src/gguf_run.c:221-237): the RMSNorm and q, k and v in
+        // one launch where the types allow, else the norm, then q, k and v in
+        // one launch, else one per matrix
+        rc = vh_qmatvec3_normed(x, B.attn_norm, eps, d, b.q, B.wq, nq, b.k, B.wk, nk, b.v, B.wv, nk, s);
+        if (rc == -ENOTSUP) {
+            rc = vireo_rmsnorm(b.xb, x, B.attn_norm, d, 1, eps, s);
+            if (!rc) rc = vh_qmatvec3(b.xb, d, b.q, B.wq, nq, b.k, B.wk, nk, b.v, B.wv, nk, s);
             if (rc == -ENOTSUP) {
                 rc = qmatvec_async(b.q, b.xb, B.wq, d, nq, s);
                 if (!rc) rc = qmatvec_async(b.k, b.xb, B.wk, d, nk, s);

@@ -116,18 +116,27 @@ __global__ void __launch_bounds__(256) qmatvec3_kernel(MvJob j0, MvJob j1, MvJob
 // consecutive rows of one matrix - each matrix's row blocks numbered after
 // the previous one's - and issues its inputs' loads and all its rows' raw
 // words before using any (one memory round trip per wave), then reduces each
-// row over the wave as qmatvec_reg_kernel does.
+// row over the wave as qmatvec_reg_kernel does. NORM: the inputs are the
+// RMSNorm of x with weights nw (null: unit weights), formed by every wave
+// from the whole vector it holds, with rmsnorm_kernel's arithmetic (the
+// squares summed in fp64 and rounded once, r = 1 / sqrtf(ss / n + eps),
+// then (x r) w).
 constexpr int kQ3Rows = 4;
 
-template <int T, int IPL>
-VH_DEV void q3_rows(const MvJob &j, int64_t r0, const float *__restrict__ x, int n, int lane) {
+template <int T, int IPL, bool NORM>
+VH_DEV void q3_rows(const MvJob &j, int64_t r0, const float *__restrict__ x, const float *__restrict__ nw, float eps,
+                    int n, int lane) {
     using F = Reg<T>;
     constexpr int NS = F::NS;
     const int items = F::items(n);
-    float xr[IPL][32], xs[IPL][NS];
+    float xr[IPL][32], xs[IPL][NS], wr[NORM ? IPL : 1][32];
     typename F::Raw raw[kQ3Rows][IPL];
 #pragma unroll
     for (int m = 0; m < IPL; m++) F::load_x(x, min(lane + 64 * m, items - 1), xr[m]);
+    if constexpr (NORM) {
+#pragma unroll
+        for (int m = 0; m < IPL; m++) F::load_x(nw ? nw : x, min(lane + 64 * m, items - 1), wr[m]);
+    }
 #pragma unroll
     for (int rr = 0; rr < kQ3Rows; rr++) {
         const int64_t row = min(r0 + rr, int64_t(j.d) - 1);  // unconditional: rows past the end repeat the last
@@ -135,6 +144,20 @@ VH_DEV void q3_rows(const MvJob &j, int64_t r0, const float *__restrict__ x, int
         for (int m = 0; m < IPL; m++) raw[rr][m] = F::fetch(j.w, row * j.row_bytes, min(lane + 64 * m, items - 1));
     }
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the arithmetic
+    if constexpr (NORM) {
+        double ss = 0.0;
+#pragma unroll
+        for (int m = 0; m < IPL; m++)
+            if (lane + 64 * m < items)  // each item once
+#pragma unroll
+                for (int i = 0; i < 32; i++) ss += double(mul_rn(xr[m][i], xr[m][i]));
+        ss = wave_sum_d(ss);
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(float(ss), float(n)), eps)));
+#pragma unroll
+        for (int m = 0; m < IPL; m++)
+#pragma unroll
+            for (int i = 0; i < 32; i++) xr[m][i] = nw ? mul_rn(mul_rn(xr[m][i], r), wr[m][i]) : mul_rn(xr[m][i], r);
+    }
 #pragma unroll
     for (int m = 0; m < IPL; m++) F::sums(xr[m], xs[m]);
 #pragma unroll
@@ -150,9 +173,9 @@ VH_DEV void q3_rows(const MvJob &j, int64_t r0, const float *__restrict__ x, int
     }
 }
 
-template <int IPL>
+template <int IPL, bool NORM>
 __global__ void __launch_bounds__(256) qmatvec3_reg_kernel(MvJob j0, MvJob j1, MvJob j2, const float *__restrict__ x,
-                                                           int n) {
+                                                           const float *__restrict__ nw, float eps, int n) {
     const int lane = threadIdx.x & 63;
     const int64_t w = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t b0 = (j0.d + kQ3Rows - 1) / kQ3Rows, b1 = (j1.d + kQ3Rows - 1) / kQ3Rows,
@@ -172,9 +195,9 @@ __global__ void __launch_bounds__(256) qmatvec3_reg_kernel(MvJob j0, MvJob j1, M
         return;
     }
     switch (j.type) {
-    case VT_Q4_K: q3_rows<VT_Q4_K, IPL>(j, r0, x, n, lane); break;
-    case VT_Q6_K: q3_rows<VT_Q6_K, IPL>(j, r0, x, n, lane); break;
-    default: q3_rows<VT_Q8_0, IPL>(j, r0, x, n, lane); break;
+    case VT_Q4_K: q3_rows<VT_Q4_K, IPL, NORM>(j, r0, x, nw, eps, n, lane); break;
+    case VT_Q6_K: q3_rows<VT_Q6_K, IPL, NORM>(j, r0, x, nw, eps, n, lane); break;
+    default: q3_rows<VT_Q8_0, IPL, NORM>(j, r0, x, nw, eps, n, lane); break;
     }
 }
 
@@ -379,13 +402,13 @@ int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d,
     return qmv(y, x, w, n, d, 1, s);
 }
 
-int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1,
-                int d1, float *y2, const gguf_tensor *w2, int d2, hipStream_t s) {
-    if (!x || n <= 0 || n % 32) return -ENOTSUP;
+namespace {
+// the three jobs of vh_qmatvec3 / vh_qmatvec3_normed, checked
+int q3_jobs(int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1, int d1, float *y2,
+            const gguf_tensor *w2, int d2, MvJob (&j)[3]) {
     const gguf_tensor *w[3] = {w0, w1, w2};
     float *y[3] = {y0, y1, y2};
     const int d[3] = {d0, d1, d2};
-    MvJob j[3];
     for (int i = 0; i < 3; i++) {
         if (!w[i] || !y[i] || d[i] <= 0) return -EINVAL;
         const uint32_t t = w[i]->ggml_type;
@@ -394,18 +417,35 @@ int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0,
         if (int rc = check_weights(t, w[i]->data, n, d[i], &rb)) return rc;
         j[i] = MvJob{y[i], static_cast<const uint8_t *>(w[i]->data), rb, d[i], t};
     }
+    return 0;
+}
+
+// the register-resident launch, where the types and sizes allow it
+bool q3_reg_ok(const MvJob (&j)[3], const float *x, int n) {
     auto reg_type = [](uint32_t t) { return t == VT_Q4_K || t == VT_Q6_K || t == VT_Q8_0; };
-    if (reg_type(j[0].type) && reg_type(j[1].type) && reg_type(j[2].type) && n % 256 == 0 && n <= 64 * 32 * 2 &&
-        (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
-        int64_t waves = 0;
-        for (int i = 0; i < 3; i++) waves += (d[i] + kQ3Rows - 1) / kQ3Rows;
-        const dim3 g(static_cast<unsigned>((waves + 3) / 4)), b(256);
-        if (n <= 64 * 32)
-            hipLaunchKernelGGL(qmatvec3_reg_kernel<1>, g, b, 0, s, j[0], j[1], j[2], x, n);
-        else
-            hipLaunchKernelGGL(qmatvec3_reg_kernel<2>, g, b, 0, s, j[0], j[1], j[2], x, n);
-        return vh_check(hipGetLastError());
-    }
+    return reg_type(j[0].type) && reg_type(j[1].type) && reg_type(j[2].type) && n % 256 == 0 && n <= 64 * 32 * 2 &&
+           (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+template <bool NORM>
+int q3_reg_launch(const MvJob (&j)[3], const float *x, const float *nw, float eps, int n, hipStream_t s) {
+    int64_t waves = 0;
+    for (int i = 0; i < 3; i++) waves += (j[i].d + kQ3Rows - 1) / kQ3Rows;
+    const dim3 g(static_cast<unsigned>((waves + 3) / 4)), b(256);
+    if (n <= 64 * 32)
+        hipLaunchKernelGGL((qmatvec3_reg_kernel<1, NORM>), g, b, 0, s, j[0], j[1], j[2], x, nw, eps, n);
+    else
+        hipLaunchKernelGGL((qmatvec3_reg_kernel<2, NORM>), g, b, 0, s, j[0], j[1], j[2], x, nw, eps, n);
+    return vh_check(hipGetLastError());
+}
+}  // namespace
+
+int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1,
+                int d1, float *y2, const gguf_tensor *w2, int d2, hipStream_t s) {
+    if (!x || n <= 0 || n % 32) return -ENOTSUP;
+    MvJob j[3];
+    if (int rc = q3_jobs(n, y0, w0, d0, y1, w1, d1, y2, w2, d2, j)) return rc;
+    if (q3_reg_ok(j, x, n)) return q3_reg_launch<false>(j, x, nullptr, 0.0f, n, s);
     const int L = pick_lanes(n / 32), rpw = 64 / L;
     const int64_t total = int64_t(d0) + d1 + d2;
     int64_t blocks = ((total + rpw - 1) / rpw + 3) / 4;
@@ -422,6 +462,16 @@ int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0,
     default: hipLaunchKernelGGL(qmatvec3_kernel<1>, g, b, 0, s, j[0], j[1], j[2], x, n); break;
     }
     return vh_check(hipGetLastError());
+}
+
+int vh_qmatvec3_normed(const float *x, const float *nw, float eps, int n, float *y0, const gguf_tensor *w0, int d0,
+                       float *y1, const gguf_tensor *w1, int d1, float *y2, const gguf_tensor *w2, int d2,
+                       hipStream_t s) {
+    if (!x || n <= 0 || n % 32 || (reinterpret_cast<uintptr_t>(nw) & 15u)) return -ENOTSUP;
+    MvJob j[3];
+    if (int rc = q3_jobs(n, y0, w0, d0, y1, w1, d1, y2, w2, d2, j)) return rc;
+    if (!q3_reg_ok(j, x, n)) return -ENOTSUP;
+    return q3_reg_launch<true>(j, x, nw, eps, n, s);
 }
 
 extern "C" int qmatvec(float *y, const float *x, const gguf_tensor *w, int n, int d) {

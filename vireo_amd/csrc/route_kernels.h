@@ -60,6 +60,12 @@ int vh_qmatvec_acc(float *y, const float *x, const gguf_tensor *w, int n, int d,
 // type or n has no such launch (then one qmatvec_async per matrix)
 int vh_qmatvec3(const float *x, int n, float *y0, const gguf_tensor *w0, int d0, float *y1, const gguf_tensor *w1,
                 int d1, float *y2, const gguf_tensor *w2, int d2, hipStream_t s);
+// The same on the RMSNorm of x with weights nw (null: unit weights), formed
+// in the launch as vireo_rmsnorm forms it; -ENOTSUP when a type or n has no
+// such launch (then vireo_rmsnorm and vh_qmatvec3)
+int vh_qmatvec3_normed(const float *x, const float *nw, float eps, int n, float *y0, const gguf_tensor *w0, int d0,
+                       float *y1, const gguf_tensor *w1, int d1, float *y2, const gguf_tensor *w2, int d2,
+                       hipStream_t s);
 // Per-token top-k from parts: idx/w [T x k], flags [T], probs [T x E] optional.
 int vh_route_finish(const RoutePart *parts, const float *R, const float *hb, const float *bias, int d, int E, int k,
                     int renorm, bool exact, int T, int32_t *idx, float *w, uint32_t *flags, float *probs,
