@@ -67,9 +67,25 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         h -= q.heads, j = k, kind = 1;
         if (h >= k.heads) h -= k.heads, j = v, kind = 2;
     }
+    const int l = threadIdx.x, ng = hs >> 6, half = hs / 2;
+    float *p = j.p + size_t(h) * hs;
+    // 1. every load that needs no position, issued with the position's:
+    //    the head's values, its bias and the norm weights (unconditional:
+    //    slots past the head and absent operands read the head's values
+    //    again, unused)
     if (pos_dev) pos = *pos_dev;
-    const bool rotate = kind < 2;
-    // the store's row for this key / value head, and the key's mean row
+    const float *bp = j.bias ? j.bias + size_t(h) * hs : p, *np = j.norm ? j.norm : p;
+    float val[4], bia[4], nrm[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int i = min(64 * c + l, hs - 1);
+        val[c] = p[i];
+        bia[c] = bp[i];
+        nrm[c] = np[i];
+    }
+    // 2. the position's loads: the rotation's table entries and, for a key
+    //    appended to the store, the block's mean-key entries this lane updates
+    const bool rotate = kind < 2 && pos >= 0 && pos < max_pos;
     float *srow = nullptr, *ks = nullptr;
     float inv = 0.0f;
     int slot = 0;
@@ -81,26 +97,36 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         if (kind == 1) ks = kv.ksum + li * size_t(hs);
         inv = 1.0f / float(slot + 1);
     }
-    const int l = threadIdx.x, ng = hs >> 6;
-    float *p = j.p + size_t(h) * hs;
-    // the head's final value at index i: to its buffer, and to the store
-    auto emit = [&](int i, float x) {
-        p[i] = x;
-        if (srow) {
-            srow[i] = x;
-            if (ks) {
-                const float old = slot == 0 ? 0.0f : ks[i];  // a new block's mean starts at zero
-                ks[i] = add_rn(old, mul_rn(sub_rn(x, old), inv));
-            }
+    // the indices this lane emits: rotated, i and i + half for i = l, l + 64
+    // (below half); else l + 64 c (below hs)
+    int ei[4];
+    bool eon[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        if (rotate) {
+            const int i = l + 64 * (u & 1);
+            ei[u] = u < 2 ? i : i + half;
+            eon[u] = i < half;
+        } else {
+            ei[u] = l + 64 * u;
+            eon[u] = ei[u] < hs;
         }
-    };
-    float val[4];
+    }
+    const float *tab = rope + size_t(rotate ? pos : 0) * hs;
+    float cs[2], sn[2], kold[4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int i = min(l + 64 * u, half - 1);
+        cs[u] = tab[i];
+        sn[u] = tab[half + i];
+    }
+    const float *kp = ks ? ks : p;
+#pragma unroll
+    for (int u = 0; u < 4; u++) kold[u] = kp[min(ei[u], hs - 1)];
+    // 3. the arithmetic
 #pragma unroll
     for (int c = 0; c < 4; c++)
-        if (c < ng) {
-            val[c] = p[64 * c + l];
-            if (j.bias) val[c] = add_rn(val[c], j.bias[size_t(h) * hs + 64 * c + l]);
-        }
+        if (j.bias) val[c] = add_rn(val[c], bia[c]);
     if (j.norm) {
         double part[4];
 #pragma unroll
@@ -108,26 +134,40 @@ __global__ void __launch_bounds__(64) head_prologue_kernel(HeadJob q, HeadJob k,
         const float ss = float((part[0] + part[1]) + (part[2] + part[3]));
         const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, float(hs)), eps)));
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            if (c < ng) val[c] = mul_rn(mul_rn(val[c], r), j.norm[64 * c + l]);
+        for (int c = 0; c < 4; c++) val[c] = mul_rn(mul_rn(val[c], r), nrm[c]);
     }
-    if (rotate && pos >= 0 && pos < max_pos) {
+    // the head's final value u at index ei[u]: to its buffer, and to the store
+    float outv[4];
+    if (rotate) {
 #pragma unroll
         for (int c = 0; c < 4; c++)
             if (c < ng) row[64 * c + l] = val[c];
         __syncthreads();
-        const int half = hs / 2;
-        const float *tab = rope + size_t(pos) * hs;
-        for (int i = l; i < half; i += 64) {
-            const float cs = tab[i], sn = tab[half + i], x0 = row[i], x1 = row[i + half];
-            emit(i, sub_rn(mul_rn(x0, cs), mul_rn(x1, sn)));
-            emit(i + half, add_rn(mul_rn(x0, sn), mul_rn(x1, cs)));
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int i = min(l + 64 * u, half - 1);
+            const float x0 = row[i], x1 = row[i + half];
+            outv[u] = sub_rn(mul_rn(x0, cs[u]), mul_rn(x1, sn[u]));
+            outv[u + 2] = add_rn(mul_rn(x0, sn[u]), mul_rn(x1, cs[u]));
         }
-        return;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++) outv[u] = val[u];
     }
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        if (c < ng) emit(64 * c + l, val[c]);
+    for (int u = 0; u < 4; u++) {
+        if (!eon[u]) continue;
+        const int i = ei[u];
+        const float x = outv[u];
+        p[i] = x;
+        if (srow) {
+            srow[i] = x;
+            if (ks) {
+                const float old = slot == 0 ? 0.0f : kold[u];  // a new block's mean starts at zero
+                ks[i] = add_rn(old, mul_rn(sub_rn(x, old), inv));
+            }
+        }
+    }
 }
 
 // y_i += b_i for up to three (y, b, n) vectors (add_bias, src/gguf_run.c:166,
