@@ -142,6 +142,38 @@ def test_gqa_matches_reference(cuda, ref, strategy):
     r.close()
 
 
+@pytest.mark.parametrize("strategy", ["all", "topk"])
+def test_gqa_long_context(cuda, ref, strategy):
+    """A context long enough that the chunks' partials of one head number
+    more than 64 (600 tokens in blocks of 4: 75 chunks of 2 blocks for the
+    grouped kernel; top-k keeps 100 blocks for the per-head one), so the
+    merge takes more than one pass over 64 chunks, against the reference's
+    kv_attend per head."""
+    from oracle.oracle import RefKV
+    n_kv, n_heads, d, G, T = 1, 4, 64, 4, 600
+    code = {"all": KV.ALL, "topk": KV.TOPK}[strategy]
+    r = RefKV(ref, n_kv, d, G, 16, 32, 0, strategy=strategy, budget=100)
+    g = KV.DeviceKV(n_kv, d, G, 16, 32, 0, strategy=code, topk_budget=100)
+    rng = np.random.default_rng(12)
+    out = torch.empty((n_heads, d), dtype=torch.float32, device=cuda)
+    worst = 0.0
+    for t in range(T):
+        K = rng.standard_normal((n_kv, d)).astype(np.float32)
+        V = rng.standard_normal((n_kv, d)).astype(np.float32)
+        r.append(0, t, K[0], V[0])
+        g.append(0, t, torch.from_numpy(K).to(cuda), torch.from_numpy(V).to(cuda))
+        if t in (255, 520, T - 1):
+            q = rng.standard_normal((n_heads, d)).astype(np.float32)
+            o_ref = np.stack([r.attend(0, q[h]) for h in range(n_heads)])
+            g.attend_gqa(0, n_heads, n_kv, torch.from_numpy(q).to(cuda), out)
+            worst = max(worst, rel(out.cpu().numpy(), o_ref))
+            assert g.stats() == r.stats()
+    print(f"gqa long {strategy}: max rel {worst:.2e}; {g.stats()}")
+    assert worst <= TOL
+    g.close()
+    r.close()
+
+
 def test_empty_layer_attends_to_zero(cuda, ref):
     g = KV.DeviceKV(2, 64, 16, dense=True)
     q = torch.ones(64, dtype=torch.float32, device=cuda)
