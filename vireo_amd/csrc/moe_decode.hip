@@ -192,15 +192,16 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
 }
 
 // ------------------------------------------------------------------ decode batch: top-k + gate/up
-// decode_batch_gateup_kernel (512 threads, one workgroup per CU): the
+// decode_batch_gateup_kernel (512 threads, one or two workgroups per CU): the
 // one-token kernel's work for nt tokens in one launch. Wave w < nt ranks
 // token w with route_select_wave on the same parts and with the same
 // certification as decode_gateup_kernel; a token whose order is not certified
 // is ranked again by the whole workgroup on exact logits (route_topk_block).
 // The tokens' chosen experts are merged into the ascending list of distinct
 // experts, and the (distinct expert, gate/up row) items are cut into equal
-// contiguous ranges, one per wave of the grid. A wave keeps kBgDepth items'
-// gate and up rows in flight and multiplies each row with every token that
+// contiguous ranges, one per wave of the grid. A wave keeps D items' gate
+// and up rows in flight (4, or 2 where two workgroups share a CU) and
+// multiplies each row with every token that
 // chose its expert, their inputs and run sums held in LDS in each lane's item
 // order. h[t k + j][o] is formed with the operations of decode_gateup_kernel,
 // so each token's activations - and, through down_combine_kernel, its output -
@@ -208,21 +209,23 @@ __global__ void __launch_bounds__(512) decode_gateup_kernel(const RoutePart *__r
 // LDS and are written after its last row (a store between the rows' loads
 // would make the waits for them count a data-dependent number of stores),
 // where the SwiGLU of each is formed by the wave's lanes side by side.
-constexpr int kBgDepth = 4;
 constexpr int kBgXPad = 36;  // a lane's 32 inputs, then their run sums (at most 4)
-constexpr size_t kBgOutBytes = 60 * 1024;  // the outputs' LDS (with the kernel's 96.5 KB of static LDS)
+// the inputs' and outputs' LDS (dynamic; with the kernel's 23 KB of static LDS)
+constexpr size_t kBgDynBytes = 128 * 1024;
+__host__ __device__ inline size_t batch_xl_bytes(int nt) { return size_t(nt) * 64 * kBgXPad * sizeof(float); }
 
-template <int T, int Q>
-__global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
+// D: items in flight per wave. D = 2 holds the kernel to 128 registers, so
+// that two workgroups share a CU where their LDS fits.
+template <int T, int Q, int D>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 2 ? 4 : 1))) decode_batch_gateup_kernel(
     const RoutePart *__restrict__ parts, const float *__restrict__ hb, const void *const *__restrict__ table, int E,
     int k, int fe, int nt, int renorm, int64_t row_bytes, const float *__restrict__ R, const float *__restrict__ bias,
     float *__restrict__ h, int32_t *__restrict__ idx_out, float *__restrict__ w_out, uint32_t *__restrict__ flags_out,
     DecodePlan *__restrict__ plan, int cap) {
     using F = Reg<T>;
-    constexpr int NS = F::NS, TPL = 3 * Q, NB = kDecodeBatchMax, D = kBgDepth, d = 2048;
+    constexpr int NS = F::NS, TPL = 3 * Q, NB = kDecodeBatchMax, d = 2048;
     static_assert(NS <= kBgXPad - 32, "the run sums fit in the lane's pad");
     __shared__ TopKSmem sm;                               // the exact ranking of an uncertified token
-    __shared__ __align__(16) float xl[NB][64 * kBgXPad];  // token t, lane l: the inputs of item l, then their sums
     __shared__ double2 cert[kGuWaves][64];
     __shared__ float2 stage[kGuWaves][64];
     __shared__ int sel[NB][64];           // token t's experts in selection order
@@ -233,7 +236,11 @@ __global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
     __shared__ int dlist[64];             // the distinct experts, ascending
     __shared__ uint64_t pmask[64];        // entry n: bit t k + j when token t's round j chose dlist[n]
     __shared__ int ndist;
-    extern __shared__ float4 outbuf[];    // per wave: cap outputs
+    // dynamic LDS: token t, lane l: the inputs of item l, then their sums (at
+    // xl + (64 t + l) kBgXPad); then per wave cap outputs
+    extern __shared__ float4 dynl[];
+    float *xl = reinterpret_cast<float *>(dynl);
+    float4 *outbuf = dynl + batch_xl_bytes(nt) / sizeof(float4);
     // the wave index through readfirstlane: the compiler then keeps everything
     // derived from it (the item cursor, the pair masks) in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -275,7 +282,7 @@ __global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
         }
         float xs[NS];
         F::sums(xr, xs);
-        float4 *dst = reinterpret_cast<float4 *>(&xl[wv][lane * kBgXPad]);
+        float4 *dst = reinterpret_cast<float4 *>(xl + (size_t(wv) * 64 + lane) * kBgXPad);
 #pragma unroll
         for (int i = 0; i < 8; i++) dst[i] = make_float4(xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]);
         float sp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -400,7 +407,7 @@ __global__ void __launch_bounds__(512) decode_batch_gateup_kernel(
             const int t = (pr * mk) >> 16;
             if (t != xt) {
                 xt = t;
-                const float4 *src = reinterpret_cast<const float4 *>(&xl[t][lane * kBgXPad]);
+                const float4 *src = reinterpret_cast<const float4 *>(xl + (size_t(t) * 64 + lane) * kBgXPad);
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
                     const float4 v = src[q];
@@ -511,16 +518,45 @@ int batch_out_cap(int E, int k, int fe, int nt, int g) {
     return int(items * nt);
 }
 
+// The dynamic LDS of a grid of g workgroups: the inputs, then every wave's outputs.
+size_t batch_lds(int E, int k, int fe, int nt, int g) {
+    return batch_xl_bytes(nt) + size_t(kGuWaves) * batch_out_cap(E, k, fe, nt, g) * sizeof(float4);
+}
+
+// The kernel's static LDS, and its dynamic LDS limit raised to kBgDynBytes
+// (once per process and instantiation); 0 on failure.
+template <int T, int Q, int D>
+size_t batch_static_lds() {
+    static size_t bytes = 0;
+    if (bytes == 0) {
+        const void *f = reinterpret_cast<const void *>(&decode_batch_gateup_kernel<T, Q, D>);
+        hipFuncAttributes a{};
+        if (hipFuncGetAttributes(&a, f) != hipSuccess ||
+            hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(kBgDynBytes)) != hipSuccess)
+            return 0;
+        bytes = a.sharedSizeBytes;
+    }
+    return bytes;
+}
+
 template <int T, int Q>
 int launch_batch_gateup(const RoutePart *parts, const float *R, const float *hb, const float *bias, int E, int k,
                         int fe, int renorm, const void *const *table, int64_t rb, float *h, int32_t *idx, float *w,
                         uint32_t *flags, DecodePlan *plan, int nt, hipStream_t s) {
-    const int g = vh_num_cus();
-    const int cap = batch_out_cap(E, k, fe, nt, g);
-    const size_t lds = size_t(kGuWaves) * cap * sizeof(float4);
-    if (lds > kBgOutBytes) return -EINVAL;
-    VH_LAUNCH((decode_batch_gateup_kernel<T, Q>), dim3(g), dim3(64 * kGuWaves), lds, s, parts, hb, table, E, k, fe,
-              nt, renorm, rb, R, bias, h, idx, w, flags, plan, cap);
+    constexpr size_t kCuLds = 160 * 1024;
+    const int cus = vh_num_cus();
+    // two workgroups per CU (two items in flight per wave, 128 registers)
+    // where both workgroups' LDS fits in the CU's, else one (four in flight)
+    const size_t lds2 = batch_lds(E, k, fe, nt, 2 * cus), st2 = batch_static_lds<T, Q, 2>();
+    if (st2 && 2 * (st2 + lds2) <= kCuLds) {
+        VH_LAUNCH((decode_batch_gateup_kernel<T, Q, 2>), dim3(2 * cus), dim3(64 * kGuWaves), lds2, s, parts, hb, table,
+                  E, k, fe, nt, renorm, rb, R, bias, h, idx, w, flags, plan, batch_out_cap(E, k, fe, nt, 2 * cus));
+        return vh_check(hipGetLastError());
+    }
+    const size_t lds = batch_lds(E, k, fe, nt, cus), st4 = batch_static_lds<T, Q, 4>();
+    if (!st4 || lds > kBgDynBytes) return -EINVAL;
+    VH_LAUNCH((decode_batch_gateup_kernel<T, Q, 4>), dim3(cus), dim3(64 * kGuWaves), lds, s, parts, hb, table, E, k,
+              fe, nt, renorm, rb, R, bias, h, idx, w, flags, plan, batch_out_cap(E, k, fe, nt, cus));
     return vh_check(hipGetLastError());
 }
 
@@ -706,8 +742,7 @@ int vh_decode_gateup(uint32_t type, const RoutePart *parts, const float *R, cons
 
 bool vh_decode_batch_supported(uint32_t type, int d, int fe, int E, int k, int nt) {
     return vh_decode_gateup_supported(type, d, fe) && E >= 1 && E <= kMaxExperts && k >= 1 && nt >= 2 &&
-           nt <= kDecodeBatchMax && nt * k <= 64 &&
-           size_t(kGuWaves) * batch_out_cap(E, k, fe, nt, vh_num_cus()) * sizeof(float4) <= kBgOutBytes;
+           nt <= kDecodeBatchMax && nt * k <= 64 && batch_lds(E, k, fe, nt, vh_num_cus()) <= kBgDynBytes;
 }
 
 int vh_decode_batch_gateup(uint32_t type, const RoutePart *parts, const float *R, const float *hb, const float *bias,
