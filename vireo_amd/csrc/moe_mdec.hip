@@ -702,7 +702,10 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         }
         __syncthreads();  // the activations are in LDS (and the weights have arrived)
         const uint4 *xr = reinterpret_cast<const uint4 *>(&hs[min(r, tn - 1) * hstride]) + g;
-        constexpr uint32_t kB = 0x43004300u;  // bf16 128 in both halves
+        // bf16 q + 128 is the byte q under the byte 0x43: v_perm_b32 takes
+        // bytes 0 and 2 (w0) or 1 and 3 (w1) of q (selectors 4-7: its bytes)
+        // with a 0x43 byte of the constant (selector 0) above each
+        constexpr uint32_t kB = 0x43434343u, kSel0 = 0x00060004u, kSel1 = 0x00070005u;
         const bf16x8 k160 = __builtin_bit_cast(bf16x8, make_uint4(0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u));  // bf16 -160
         uint32_t *wl = PK ? &wq[0][0] : &wq[wv][r * kDnRowStride];
 #pragma unroll
@@ -736,7 +739,7 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                         const uint32_t lw = PK ? u4_at(la, ql_c & 3) : wl[4 * ql_c + g];
                         const uint32_t hw = PK ? u4_at(qq[b], qh_c) : wl[32 + 4 * qh_c + g];
                         const uint32_t q = ((lw >> (j >= 2 ? 4 : 0)) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4);
-                        const uint32_t w0 = (q & 0x00ff00ffu) | kB, w1 = ((q >> 8) & 0x00ff00ffu) | kB;
+                        const uint32_t w0 = __builtin_amdgcn_perm(q, kB, kSel0), w1 = __builtin_amdgcn_perm(q, kB, kSel1);
                         const bf16x8 wb = __builtin_bit_cast(bf16x8, make_uint4(w0, w1, w0, w1));
                         f32x4 c = {0.f, 0.f, 0.f, 0.f};
                         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wb, c, 0, 0, 0);
