@@ -67,6 +67,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTok = 16;  // tokens per tile (the A operand's rows)
+constexpr int kDnTok = 8;  // tokens per down tile: its LDS holds their activations, and few experts of a
+                           // decode call serve more (the MFMA rows past them are idle either way)
 constexpr int kGroupMax = 64;     // a call's tokens per expert (at most one pair per token; calls < 64 tokens)
 constexpr int kCombRows = 128;    // output rows of one down workgroup (the combine's unit)
 
@@ -643,10 +645,9 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                                                                   const void *const *__restrict__ table,
                                                                   const uint4 *__restrict__ hp, int fe, int d, int E,
                                                                   int64_t row_bytes, float *__restrict__ y, MdecSelf sf) {
-    extern __shared__ __align__(16) uint32_t hs[];  // [kTok][fe + 4]
+    extern __shared__ __align__(16) uint32_t hs[];  // [kDnTok][fe + 4]
     __shared__ __align__(16) uint32_t wq[PK ? 1 : kDnWaves][PK ? 4 : 16 * kDnRowStride];  // GGUF rows only
-    __shared__ int glist[SELF ? kGroupMax : 1], gwc[SELF ? kDnWaves : 1], last[SELF ? kTok + 1 : 1];
-    const int t0 = blockIdx.z * kTok;
+    __shared__ int glist[SELF ? kGroupMax : 1], gwc[SELF ? kDnWaves : 1], last[SELF ? kGroupMax + 1 : 1];
     int e, cnt, base = 0;
     if constexpr (SELF) {
         e = blockIdx.y;
@@ -658,23 +659,21 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         cnt = counts[e];
         base = offs[e];
     }
-    if (t0 >= cnt) return;
+    if (int(blockIdx.z) * kDnTok >= cnt) return;
     auto pair_of = [&](int i) { return SELF ? glist[i] : perm[base + i]; };
     gbyte *D = gmem(table[3 * e + 2]);
     // an unregistered expert: skipped by the combine kernel, or (SELF) its rows
     // of y are zeros, which the combine below adds without changing a bit
     // (src/gguf_run.c:201)
     if (!SELF && !D) return;
-    const int tn = min(kTok, cnt - t0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
     const int o0 = min((blockIdx.x * kDnWaves + wv) * 16, d - 16);  // d % 16 == 0: a wave past d repeats rows
     const bool live = (blockIdx.x * kDnWaves + wv) * 16 < d;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (D) {
-        gbyte *row = D + int64_t(o0 + r) * row_bytes;
-        const int nb = fe / 256;
-        uint4 a0[kDnMaxBlocks], a1[kDnMaxBlocks], qq[kDnMaxBlocks], scb[kDnMaxBlocks];
-        uint32_t ddb[kDnMaxBlocks];
+    gbyte *row = D + int64_t(o0 + r) * row_bytes;
+    const int nb = fe / 256;
+    uint4 a0[kDnMaxBlocks], a1[kDnMaxBlocks], qq[kDnMaxBlocks], scb[kDnMaxBlocks];
+    uint32_t ddb[kDnMaxBlocks];
+    if (D) {  // the rows' weights, held in registers for every token tile of the expert
 #pragma unroll
         for (int b = 0; b < kDnMaxBlocks; b++) {
             if (b >= nb) break;
@@ -694,8 +693,16 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                 ddb[b] = ld_u16(p + 208);
             }
         }
+    }
+    // the expert's tokens in tiles of kDnTok (with one workgroup on the z
+    // axis: every tile; the weights are read once)
+    for (int t0 = blockIdx.z * kDnTok; t0 < cnt; t0 += gridDim.z * kDnTok) {
+    const int tn = min(kDnTok, cnt - t0);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (D) {
         // the tile's activations: token i's fe / 4 pieces of 16 bytes
         const int hstride = fe + 4, npc = fe / 4;
+        if (t0 != int(blockIdx.z) * kDnTok) __syncthreads();  // every wave is done with the previous tile
         for (int i = tid; i < tn * npc; i += 64 * kDnWaves) {
             const int tt = i / npc, c = i - tt * npc;
             *reinterpret_cast<uint4 *>(&hs[tt * hstride + 4 * c]) = hp[size_t(pair_of(t0 + tt)) * npc + c];
@@ -711,6 +718,16 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
 #pragma unroll
         for (int b = 0; b < kDnMaxBlocks; b++) {
             if (b >= nb) break;
+            {  // the super-block's words pass an empty asm statement in every tile: nothing
+               // derived from them is hoisted out of the token loop (into registers for all tiles)
+                u32x4 v0 = __builtin_bit_cast(u32x4, a0[b]), v1 = __builtin_bit_cast(u32x4, a1[b]);
+                u32x4 v2 = __builtin_bit_cast(u32x4, qq[b]), v3 = __builtin_bit_cast(u32x4, scb[b]);
+                asm volatile("" : "+v"(v0), "+v"(v1), "+v"(v2), "+v"(v3), "+v"(ddb[b]));
+                a0[b] = __builtin_bit_cast(uint4, v0);
+                a1[b] = __builtin_bit_cast(uint4, v1);
+                qq[b] = __builtin_bit_cast(uint4, v2);
+                scb[b] = __builtin_bit_cast(uint4, v3);
+            }
             // ql chunks g and g + 4, qh chunk g of the row into the wave's LDS;
             // lane group g then reads word g of the chunk each step needs
             if constexpr (!PK) {
@@ -755,14 +772,19 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
             }
         }
     }  // D
-    if constexpr (!SELF) {
-        if (!live) return;
+    // y (SELF: agent-scope stores, for the combine below)
+    if (live) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int tt = 4 * g + i;
-            if (tt < tn) y[size_t(pair_of(t0 + tt)) * d + o0 + r] = acc[i];
+            if (tt >= tn) continue;
+            float *dst = &y[size_t(pair_of(t0 + tt)) * d + o0 + r];
+            if constexpr (SELF) __hip_atomic_store(dst, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *dst = acc[i];
         }
-    } else {
+    }
+    }  // token tiles
+    if constexpr (SELF) {
         // The combine (src/gguf_run.c:208-212) of output rows [kCombRows c,
         // + kCombRows) of a token is done by the last of its k experts'
         // workgroups to write them: y goes out as agent-scope stores, each
@@ -770,33 +792,25 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         // per token at ctr[c][t] (agent-scope atomics); the workgroup that
         // brings a count to k reads the k rows with agent-scope loads (they
         // bypass this XCD's L2, which need not hold the other XCDs' writes).
-        if (live) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tt = 4 * g + i;
-                if (tt < tn)
-                    __hip_atomic_store(&y[size_t(pair_of(t0 + tt)) * d + o0 + r], acc[i], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (tid == 0) last[kTok] = 0;
+        if (tid == 0) last[kGroupMax] = 0;
         VH_WAIT_VMCNT(0);
         __syncthreads();
         const int c = blockIdx.x, k = sf.k;
-        if (tid < tn) {
-            const int t = pair_of(t0 + tid) / k;
+        // the tokens of this workgroup's tiles (cnt <= kGroupMax < 64 kDnWaves)
+        if (tid < cnt && (tid / kDnTok) % int(gridDim.z) == int(blockIdx.z)) {
+            const int t = pair_of(tid) / k;
             const uint32_t n = __hip_atomic_fetch_add(&sf.ctr[c * kGroupMax + t], 1u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT);
-            if (n == uint32_t(k - 1)) last[atomicAdd(&last[kTok], 1)] = t;  // this workgroup combines token t
+            if (n == uint32_t(k - 1)) last[atomicAdd(&last[kGroupMax], 1)] = t;  // this workgroup combines token t
         }
         __syncthreads();
         // the (token, row) items of the combines, kItems per thread with every
         // load of a thread issued before the first sum (the combine kernel's
         // arithmetic, in selection order)
-        constexpr int kItems = kTok * kCombRows / (64 * kDnWaves);
-        const int nl = last[kTok];
-        if (nl == 0 || k > 8) {
-            for (int it = tid; it < nl * kCombRows; it += 64 * kDnWaves) {  // k > 8: one item at a time
+        constexpr int kItems = kDnTok * kCombRows / (64 * kDnWaves);
+        const int nl = last[kGroupMax];
+        if (nl == 0 || nl > kDnTok || k > 8) {
+            for (int it = tid; it < nl * kCombRows; it += 64 * kDnWaves) {  // k > 8 or tokens of several tiles: one item at a time
                 const int t = last[it / kCombRows], o = c * kCombRows + it % kCombRows;
                 if (o >= d) continue;
                 float a = 0.0f;
@@ -908,8 +922,11 @@ int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm
         return -EINVAL;
     static_assert(kCombRows == 16 * kDnWaves, "a down workgroup's rows are the combine's unit");
     const MdecSelf sf = self ? *self : MdecSelf{};
-    const dim3 g((d + 16 * kDnWaves - 1) / (16 * kDnWaves), self ? E : max_slots, (max_count + kTok - 1) / kTok);
-    const size_t lds = size_t(kTok) * (fe + 4) * 4;
+    // one workgroup per (row chunk, expert) takes all of the expert's tokens
+    // where it finds them itself; else the token tiles spread over z
+    const dim3 g((d + 16 * kDnWaves - 1) / (16 * kDnWaves), self ? E : max_slots,
+                 self ? 1 : (max_count + kDnTok - 1) / kDnTok);
+    const size_t lds = size_t(kDnTok) * (fe + 4) * 4;
     static bool attr = false;  // dynamic LDS above the default limit: raised once per process
     if (!attr) {
         for (const void *f : {reinterpret_cast<const void *>(&mdec_down_kernel<true, false>),
