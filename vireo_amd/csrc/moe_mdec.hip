@@ -41,13 +41,13 @@
 // and the inputs are laid out to match.
 //
 // Grids: (row chunk, active expert slot, 16-token tile); gate/up: 256
-// threads, waves of 16 rows of gate and the same 16 of up; down: 512
-// threads, waves of 16 rows. A call of moe_ffn_forward (MdecSelf) launches no
+// threads, waves of 16 rows of gate and the same 16 of up; down: 4 or 8
+// waves of 16 rows. A call of moe_ffn_forward (MdecSelf) launches no
 // dispatch and no combine kernel: the grids' second dimension is the expert
 // id, each workgroup lists its expert's pairs from the routing itself
 // (expert_group: one load of idx and two barriers, where a dispatch kernel
 // cost about 7 us), and the down kernel's workgroups combine: the last of a
-// token's k experts to write a 128-row chunk of y adds the chunk's k rows
+// token's k experts to write a workgroup's chunk of y adds the chunk's k rows
 // into x (agent-scope stores, counters and loads). Qwen3 Q4_K_M, 32 tokens:
 // 113.3 -> 110.3 us per layer; OLMoE Q4_K_M 16 tokens: 85.5 -> 79.0. Q6_K rows (210 bytes per super-block) start at
 // any even address; their 16-byte loads rely on global memory accepting any
@@ -70,7 +70,6 @@ constexpr int kTok = 16;  // tokens per tile (the A operand's rows)
 constexpr int kDnTok = 8;  // tokens per down tile: its LDS holds their activations, and few experts of a
                            // decode call serve more (the MFMA rows past them are idle either way)
 constexpr int kGroupMax = 64;     // a call's tokens per expert (at most one pair per token; calls < 64 tokens)
-constexpr int kCombRows = 128;    // output rows of one down workgroup (the combine's unit)
 
 // The pairs p < P routed to expert e (idx[p] == e) in ascending order into
 // list (at most kGroupMax kept); returns their number. Called by every thread
@@ -625,20 +624,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PK ? 4
     }
 }
 
-// down: wave w of workgroup (c, s, z) owns rows 128 c + 16 w .. + 15 of down
-// of expert active[s] (one 16-row tile) for tokens 16 z .. of its group, and
-// writes y[pair][row] = down_row . h[pair] (src/gguf_run.c:208), combined
-// afterwards in selection order by the combine kernel. Every super-block of
-// the lane's row is requested first; then the tile's activations (all of fe)
-// are copied to LDS for the workgroup's eight waves; each wave passes its
+// down: wave w of workgroup (c, s, z) of NW waves owns rows 16 NW c + 16 w ..
+// + 15 of down of expert active[s] (one 16-row tile) for its group's tokens
+// in tiles of kDnTok, and writes y[pair][row] = down_row . h[pair]
+// (src/gguf_run.c:208), combined in selection order by the combine kernel or
+// (SELF) by the kernel itself. Every super-block of the lane's row is
+// requested first; then each tile's activations (all of fe) are copied to LDS
+// for the workgroup's waves; each wave passes its
 // rows' ql and qh bytes through its own LDS (coalesced 16-byte loads in, the
 // words its lanes need out).
 constexpr int kDnRowStride = 52;  // dwords per weight row in LDS: 32 ql + 16 qh + 4 (no bank conflicts)
 constexpr int kDnMaxBlocks = 4;   // fe <= 1024
-constexpr int kDnWaves = 8;
-
-template <bool PK, bool SELF>
-__global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t *__restrict__ counts,
+template <bool PK, bool SELF, int NW>
+__global__ void __launch_bounds__(64 * NW) mdec_down_kernel(const int32_t *__restrict__ counts,
                                                                   const int32_t *__restrict__ offs,
                                                                   const int32_t *__restrict__ perm,
                                                                   const int32_t *__restrict__ active,
@@ -646,12 +644,13 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
                                                                   const uint4 *__restrict__ hp, int fe, int d, int E,
                                                                   int64_t row_bytes, float *__restrict__ y, MdecSelf sf) {
     extern __shared__ __align__(16) uint32_t hs[];  // [kDnTok][fe + 4]
-    __shared__ __align__(16) uint32_t wq[PK ? 1 : kDnWaves][PK ? 4 : 16 * kDnRowStride];  // GGUF rows only
-    __shared__ int glist[SELF ? kGroupMax : 1], gwc[SELF ? kDnWaves : 1], last[SELF ? kGroupMax + 1 : 1];
+    constexpr int CR = 16 * NW;  // output rows of one workgroup (the combine's unit)
+    __shared__ __align__(16) uint32_t wq[PK ? 1 : NW][PK ? 4 : 16 * kDnRowStride];  // GGUF rows only
+    __shared__ int glist[SELF ? kGroupMax : 1], gwc[SELF ? NW : 1], last[SELF ? kGroupMax + 1 : 1];
     int e, cnt, base = 0;
     if constexpr (SELF) {
         e = blockIdx.y;
-        cnt = expert_group<64 * kDnWaves>(sf.idx, sf.T * sf.k, e, glist, gwc);
+        cnt = expert_group<64 * NW>(sf.idx, sf.T * sf.k, e, glist, gwc);
     } else {
         const int s = blockIdx.y;
         if (s >= active[E]) return;
@@ -667,8 +666,8 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
     // (src/gguf_run.c:201)
     if (!SELF && !D) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int o0 = min((blockIdx.x * kDnWaves + wv) * 16, d - 16);  // d % 16 == 0: a wave past d repeats rows
-    const bool live = (blockIdx.x * kDnWaves + wv) * 16 < d;
+    const int o0 = min((blockIdx.x * NW + wv) * 16, d - 16);  // d % 16 == 0: a wave past d repeats rows
+    const bool live = (blockIdx.x * NW + wv) * 16 < d;
     gbyte *row = D + int64_t(o0 + r) * row_bytes;
     const int nb = fe / 256;
     uint4 a0[kDnMaxBlocks], a1[kDnMaxBlocks], qq[kDnMaxBlocks], scb[kDnMaxBlocks];
@@ -703,7 +702,7 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         // the tile's activations: token i's fe / 4 pieces of 16 bytes
         const int hstride = fe + 4, npc = fe / 4;
         if (t0 != int(blockIdx.z) * kDnTok) __syncthreads();  // every wave is done with the previous tile
-        for (int i = tid; i < tn * npc; i += 64 * kDnWaves) {
+        for (int i = tid; i < tn * npc; i += 64 * NW) {
             const int tt = i / npc, c = i - tt * npc;
             *reinterpret_cast<uint4 *>(&hs[tt * hstride + 4 * c]) = hp[size_t(pair_of(t0 + tt)) * npc + c];
         }
@@ -785,8 +784,8 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
     }
     }  // token tiles
     if constexpr (SELF) {
-        // The combine (src/gguf_run.c:208-212) of output rows [kCombRows c,
-        // + kCombRows) of a token is done by the last of its k experts'
+        // The combine (src/gguf_run.c:208-212) of output rows [CR c,
+        // + CR) of a token is done by the last of its k experts'
         // workgroups to write them: y goes out as agent-scope stores, each
         // workgroup waits until its stores are done, then counts one arrival
         // per token at ctr[c][t] (agent-scope atomics); the workgroup that
@@ -796,7 +795,7 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         VH_WAIT_VMCNT(0);
         __syncthreads();
         const int c = blockIdx.x, k = sf.k;
-        // the tokens of this workgroup's tiles (cnt <= kGroupMax < 64 kDnWaves)
+        // the tokens of this workgroup's tiles (cnt <= kGroupMax < 64 NW)
         if (tid < cnt && (tid / kDnTok) % int(gridDim.z) == int(blockIdx.z)) {
             const int t = pair_of(tid) / k;
             const uint32_t n = __hip_atomic_fetch_add(&sf.ctr[c * kGroupMax + t], 1u, __ATOMIC_RELAXED,
@@ -807,11 +806,11 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         // the (token, row) items of the combines, kItems per thread with every
         // load of a thread issued before the first sum (the combine kernel's
         // arithmetic, in selection order)
-        constexpr int kItems = kDnTok * kCombRows / (64 * kDnWaves);
+        constexpr int kItems = kDnTok * CR / (64 * NW);
         const int nl = last[kGroupMax];
         if (nl == 0 || nl > kDnTok || k > 8) {
-            for (int it = tid; it < nl * kCombRows; it += 64 * kDnWaves) {  // k > 8 or tokens of several tiles: one item at a time
-                const int t = last[it / kCombRows], o = c * kCombRows + it % kCombRows;
+            for (int it = tid; it < nl * CR; it += 64 * NW) {  // k > 8 or tokens of several tiles: one item at a time
+                const int t = last[it / CR], o = c * CR + it % CR;
                 if (o >= d) continue;
                 float a = 0.0f;
                 for (int j = 0; j < k; j++)
@@ -825,8 +824,8 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         float yv[kItems][8], wt[kItems][8], xo[kItems];
 #pragma unroll
         for (int q = 0; q < kItems; q++) {
-            const int it = min(tid + 64 * kDnWaves * q, nl * kCombRows - 1);
-            const int t = last[it / kCombRows], o = min(c * kCombRows + it % kCombRows, d - 1);
+            const int it = min(tid + 64 * NW * q, nl * CR - 1);
+            const int t = last[it / CR], o = min(c * CR + it % CR, d - 1);
             xo[q] = sf.x[size_t(t) * d + o];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
@@ -838,10 +837,10 @@ __global__ void __launch_bounds__(64 * kDnWaves) mdec_down_kernel(const int32_t 
         }
 #pragma unroll
         for (int q = 0; q < kItems; q++) {
-            const int it = tid + 64 * kDnWaves * q;
-            const int o = c * kCombRows + it % kCombRows;
-            if (it >= nl * kCombRows || o >= d) continue;
-            const int t = last[it / kCombRows];
+            const int it = tid + 64 * NW * q;
+            const int o = c * CR + it % CR;
+            if (it >= nl * CR || o >= d) continue;
+            const int t = last[it / CR];
             float a = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++)
@@ -913,6 +912,45 @@ int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *pe
     return vh_check(hipGetLastError());
 }
 
+namespace {
+// The down kernel's launch with NW waves (16 NW rows of d) per workgroup.
+template <int NW>
+int mdec_down_launch(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
+                     const void *const *table, bool packed, const uint4 *h4, int d, int fe, int E, int max_slots,
+                     int max_count, float *ybuf, hipStream_t s, const MdecSelf *self) {
+    const MdecSelf sf = self ? *self : MdecSelf{};
+    // one workgroup per (row chunk, expert) takes all of the expert's tokens
+    // where it finds them itself; else the token tiles spread over z
+    const dim3 g((d + 16 * NW - 1) / (16 * NW), self ? E : max_slots, self ? 1 : (max_count + kDnTok - 1) / kDnTok);
+    const size_t lds = size_t(kDnTok) * (fe + 4) * 4;
+    static bool attr = false;  // dynamic LDS above the default limit: raised once per process
+    if (!attr) {
+        for (const void *f : {reinterpret_cast<const void *>(&mdec_down_kernel<true, false, NW>),
+                              reinterpret_cast<const void *>(&mdec_down_kernel<false, false, NW>),
+                              reinterpret_cast<const void *>(&mdec_down_kernel<true, true, NW>),
+                              reinterpret_cast<const void *>(&mdec_down_kernel<false, true, NW>)})
+            if (int rc = vh_check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024)))
+                return rc;
+        attr = true;
+    }
+    const int64_t rb = vh_row_bytes(VT_Q6_K, fe);
+    const dim3 b(64 * NW);
+    if (packed && self)
+        hipLaunchKernelGGL((mdec_down_kernel<true, true, NW>), g, b, lds, s, counts, offs, perm, active, table, h4, fe,
+                           d, E, rb, ybuf, sf);
+    else if (packed)
+        hipLaunchKernelGGL((mdec_down_kernel<true, false, NW>), g, b, lds, s, counts, offs, perm, active, table, h4,
+                           fe, d, E, rb, ybuf, sf);
+    else if (self)
+        hipLaunchKernelGGL((mdec_down_kernel<false, true, NW>), g, b, lds, s, counts, offs, perm, active, table, h4,
+                           fe, d, E, rb, ybuf, sf);
+    else
+        hipLaunchKernelGGL((mdec_down_kernel<false, false, NW>), g, b, lds, s, counts, offs, perm, active, table, h4,
+                           fe, d, E, rb, ybuf, sf);
+    return vh_check(hipGetLastError());
+}
+}  // namespace
+
 int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
                  const void *const *table, bool packed, const void *hp, int d, int fe, int E, int max_slots,
                  int max_count, float *ybuf, hipStream_t s, const MdecSelf *self) {
@@ -920,40 +958,16 @@ int vh_mdec_down(const int32_t *counts, const int32_t *offs, const int32_t *perm
     if (self && (self->T > kGroupMax || self->T < max_count || !self->x || !self->w || self->k < 1 ||
                  self->nctr < vh_mdec_ctr_words(d)))
         return -EINVAL;
-    static_assert(kCombRows == 16 * kDnWaves, "a down workgroup's rows are the combine's unit");
-    const MdecSelf sf = self ? *self : MdecSelf{};
-    // one workgroup per (row chunk, expert) takes all of the expert's tokens
-    // where it finds them itself; else the token tiles spread over z
-    const dim3 g((d + 16 * kDnWaves - 1) / (16 * kDnWaves), self ? E : max_slots,
-                 self ? 1 : (max_count + kDnTok - 1) / kDnTok);
-    const size_t lds = size_t(kDnTok) * (fe + 4) * 4;
-    static bool attr = false;  // dynamic LDS above the default limit: raised once per process
-    if (!attr) {
-        for (const void *f : {reinterpret_cast<const void *>(&mdec_down_kernel<true, false>),
-                              reinterpret_cast<const void *>(&mdec_down_kernel<false, false>),
-                              reinterpret_cast<const void *>(&mdec_down_kernel<true, true>),
-                              reinterpret_cast<const void *>(&mdec_down_kernel<false, true>)})
-            if (int rc = vh_check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024)))
-                return rc;
-        attr = true;
-    }
-    if (lds > 96 * 1024) return -EINVAL;
+    if (size_t(kDnTok) * (fe + 4) * 4 > 96 * 1024) return -EINVAL;
     const uint4 *h4 = static_cast<const uint4 *>(hp);
-    const int64_t rb = vh_row_bytes(VT_Q6_K, fe);
-    const dim3 b(64 * kDnWaves);
-    if (packed && self)
-        hipLaunchKernelGGL((mdec_down_kernel<true, true>), g, b, lds, s, counts, offs, perm, active, table, h4, fe, d,
-                           E, rb, ybuf, sf);
-    else if (packed)
-        hipLaunchKernelGGL((mdec_down_kernel<true, false>), g, b, lds, s, counts, offs, perm, active, table, h4, fe,
-                           d, E, rb, ybuf, sf);
-    else if (self)
-        hipLaunchKernelGGL((mdec_down_kernel<false, true>), g, b, lds, s, counts, offs, perm, active, table, h4, fe,
-                           d, E, rb, ybuf, sf);
-    else
-        hipLaunchKernelGGL((mdec_down_kernel<false, false>), g, b, lds, s, counts, offs, perm, active, table, h4, fe,
-                           d, E, rb, ybuf, sf);
-    return vh_check(hipGetLastError());
+    // four-wave workgroups for rows of up to three super-blocks (a 768-wide
+    // down: 108.3 -> 106.9 us per 32-token layer call), eight for four (a
+    // 1024-wide down: 79.2 us per 16-token call with four, 77.8 with eight)
+    if (fe <= 768)
+        return mdec_down_launch<4>(counts, offs, perm, active, table, packed, h4, d, fe, E, max_slots, max_count, ybuf,
+                                   s, self);
+    return mdec_down_launch<8>(counts, offs, perm, active, table, packed, h4, d, fe, E, max_slots, max_count, ybuf, s,
+                               self);
 }
 
 namespace {

@@ -162,7 +162,8 @@ struct MdecSelf {
     uint32_t *ctr;
     int nctr, T, k;
 };
-inline int vh_mdec_ctr_words(int d) { return (d + 127) / 128 * 64; }
+// the down kernel's arrival counters: 64 tokens per chunk of 64 or 128 rows of d
+inline int vh_mdec_ctr_words(int d) { return (d + 63) / 64 * 64; }
 // `packed`: table points at vh_mdec_pack_layer's tiles instead of GGUF rows;
 // `self` (optional): the call's routing (counts, offs, perm and active unused).
 int vh_mdec_gateup(const int32_t *counts, const int32_t *offs, const int32_t *perm, const int32_t *active,
